@@ -1,0 +1,146 @@
+"""Host-side weight codecs: the reference's `compress=` encodings (aneforge/_blob.py:20-56)
+plus GGUF Q4_0, and the packing into the layouts the HIP kernels stream.
+
+  quantize_per_row   int8 codes + fp16 per-output-row scale      (aneforge/_blob.py:20-25)
+  quantize_blockwise int8 codes + fp16 scale per 32-column block (aneforge/_blob.py:46-56)
+  palettize_lut4     16-entry per-tensor LUT, 4-bit indices      (aneforge/_blob.py:28-43)
+  quantize_q4_0      ggml Q4_0 blocks (18 B / 32 weights) from fp weights
+  q4_0_to_superblock GGUF Q4_0 bytes -> (qs, d) superblock layout (host twin of afx_q4_0_repack)
+
+The encodings must produce the reference's bytes, so their steps match the reference's; the
+code is this package's own.  The BLOBFILE container is ANE-specific and is not rebuilt."""
+from __future__ import annotations
+
+import numpy as np
+
+F16 = np.float16
+
+
+def quantize_per_row(W: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """[OUT, IN] -> (int8 [OUT, IN], fp16 scale [OUT]).  Scale = max|row|/127 floored at 1e-8,
+    computed in fp32; codes use that fp32 scale with round-half-to-even; the scale is stored fp16."""
+    W32 = np.asarray(W, dtype=np.float32)
+    amax = np.max(np.abs(W32), axis=1)
+    scale = np.maximum(amax / np.float32(127.0), np.float32(1e-8)).astype(np.float32)
+    codes = np.rint(W32 / scale[:, None])
+    return np.clip(codes, -127, 127).astype(np.int8), scale.astype(F16)
+
+
+def quantize_per_tensor_rows(W: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's bmm_weight quirk (aneforge/_compile.py:117 reshapes [B, K, N] to
+    [B, K*N] before quantize_per_row): ONE scale per leading index.  W [B, ...] -> (codes
+    with W's shape, fp16 scale [B])."""
+    B = W.shape[0]
+    q, s = quantize_per_row(np.asarray(W).reshape(B, -1))
+    return q.reshape(W.shape), s
+
+
+def quantize_blockwise(W: np.ndarray, block_size: int = 32) -> tuple[np.ndarray, np.ndarray, int]:
+    """[OUT, IN] -> (int8 [OUT, IN], fp16 scale [OUT, IN/bs], bs); bs clamps down to a divisor of IN."""
+    W32 = np.asarray(W, dtype=np.float32)
+    OUT, IN = W32.shape
+    bs = int(block_size)
+    while bs > 1 and IN % bs:
+        bs -= 1
+    blocks = W32.reshape(OUT, IN // bs, bs)
+    scale = np.maximum(np.max(np.abs(blocks), axis=2) / np.float32(127.0), np.float32(1e-8))
+    codes = np.clip(np.rint(blocks / scale[:, :, None]), -127, 127).astype(np.int8)
+    return codes.reshape(OUT, IN), scale.astype(F16), bs
+
+
+def palettize_lut4(W: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-tensor 16-entry codebook by 20 deterministic Lloyd iterations from quantile edges;
+    indices packed two per byte, low nibble = even column.  -> (packed uint8 [OUT, ceil(IN/2)],
+    fp16 codebook [16])."""
+    flat = np.asarray(W, dtype=np.float32).reshape(-1)
+    edges = np.quantile(flat, np.linspace(0.0, 1.0, 17))
+    cb = ((edges[:-1] + edges[1:]) / 2.0).astype(np.float32)
+    for _ in range(20):
+        idx = np.abs(flat[:, None] - cb[None, :]).argmin(axis=1)
+        for j in range(16):
+            members = flat[idx == j]
+            if members.size:
+                cb[j] = members.mean()
+    idx = np.abs(flat[:, None] - cb[None, :]).argmin(axis=1).astype(np.uint8).reshape(W.shape[0], -1)
+    if idx.shape[1] % 2:
+        idx = np.pad(idx, ((0, 0), (0, 1)))
+    return (idx[:, 0::2] | (idx[:, 1::2] << 4)).astype(np.uint8), cb.astype(F16)
+
+
+# ----------------------------------------------------------------------------- Q4_0
+Q4_BLOCK, Q4_BYTES = 32, 18
+
+
+def quantize_q4_0(W: np.ndarray) -> np.ndarray:
+    """ggml Q4_0: per 32-block, d = (signed element of largest magnitude) / -8, code =
+    min(15, trunc(x/d + 8.5)).  Returns GGUF block bytes [OUT, IN/32*18]."""
+    W32 = np.asarray(W, dtype=np.float32)
+    OUT, IN = W32.shape
+    if IN % Q4_BLOCK:
+        raise ValueError(f"Q4_0 needs IN % 32 == 0 (got {IN})")
+    b = W32.reshape(OUT, IN // Q4_BLOCK, Q4_BLOCK)
+    pick = np.take_along_axis(b, np.abs(b).argmax(axis=2)[:, :, None], axis=2)[:, :, 0]
+    d = pick / np.float32(-8.0)
+    safe = np.where(d == 0, np.float32(1.0), d)
+    inv = np.where(d == 0, np.float32(0.0), np.float32(1.0) / safe).astype(np.float32)
+    codes = np.clip(np.minimum(15, np.trunc(b * inv[:, :, None] + np.float32(8.5))), 0, 15).astype(np.uint8)
+    out = np.empty((OUT, IN // Q4_BLOCK, Q4_BYTES), np.uint8)
+    out[:, :, 0:2] = d.astype(F16)[:, :, None].view(np.uint8)
+    out[:, :, 2:] = (codes[:, :, :16] & 15) | ((codes[:, :, 16:] & 15) << 4)
+    return out.reshape(OUT, -1)
+
+
+def q4_0_codes(blocks: np.ndarray, N: int, K: int) -> tuple[np.ndarray, np.ndarray]:
+    """GGUF Q4_0 bytes -> (codes uint8 [N, K] in 0..15, d fp16 [N, K/32])."""
+    b = np.asarray(blocks, np.uint8).reshape(N, K // Q4_BLOCK, Q4_BYTES)
+    d = np.ascontiguousarray(b[:, :, 0:2]).view(F16).reshape(N, K // Q4_BLOCK)
+    lo, hi = b[:, :, 2:] & 15, b[:, :, 2:] >> 4
+    return np.concatenate([lo, hi], axis=2).reshape(N, K), d
+
+
+def q4_0_to_superblock(blocks: np.ndarray, N: int, K: int) -> tuple[np.ndarray, np.ndarray]:
+    """Host twin of afx_q4_0_repack: -> (qs uint8 [N, K/2], d fp16 [N, K/32]).  Word
+    (row, sb, g, j) holds elements 8g..8g+7 of block 4sb+j: even elements' nibbles in bits
+    0/4/8/12, odd elements' in bits 16/20/24/28."""
+    if K % 128:
+        raise ValueError(f"superblock layout needs K % 128 == 0 (got {K})")
+    codes, d = q4_0_codes(blocks, N, K)
+    c = codes.reshape(N, K // 128, 4, 4, 8).astype(np.uint32)        # [N, sb, j, g, e]
+    ev, od = c[..., 0::2], c[..., 1::2]                              # [N, sb, j, g, 4]
+    sh = (4 * np.arange(4, dtype=np.uint32))
+    words = ((ev << sh).sum(-1) | ((od << (sh + 16)).sum(-1))).astype(np.uint32)   # [N, sb, j, g]
+    words = np.ascontiguousarray(words.transpose(0, 1, 3, 2))       # [N, sb, g, j]
+    return words.reshape(N, -1).view(np.uint8).reshape(N, K // 2), d
+
+
+def superblock_to_q4_0(qs: np.ndarray, d: np.ndarray, N: int, K: int) -> np.ndarray:
+    """Inverse of q4_0_to_superblock -> GGUF bytes [N, K/32*18]."""
+    words = np.ascontiguousarray(qs).view(np.uint32).reshape(N, K // 128, 4, 4)   # [N, sb, g, j]
+    words = words.transpose(0, 1, 3, 2)                                          # [N, sb, j, g]
+    sh = (4 * np.arange(4, dtype=np.uint32))
+    ev = (words[..., None] >> sh) & 15
+    od = (words[..., None] >> (sh + 16)) & 15
+    e = np.empty(words.shape + (8,), np.uint8)
+    e[..., 0::2], e[..., 1::2] = ev, od
+    codes = e.reshape(N, K // 32, 32)
+    out = np.empty((N, K // 32, Q4_BYTES), np.uint8)
+    out[:, :, 0:2] = np.asarray(d, F16).reshape(N, K // 32, 1).view(np.uint8)
+    out[:, :, 2:] = (codes[:, :, :16] & 15) | ((codes[:, :, 16:] & 15) << 4)
+    return out.reshape(N, -1)
+
+
+# ----------------------------------------------------------------------------- row layouts
+def rope_pair_order(n_heads: int, dh: int) -> np.ndarray:
+    """Row permutation putting dims (i, i+dh/2) of every head next to each other, so the fused
+    QKV kernel can rotate pairs held by one wavefront.  Per-row quantization is unaffected."""
+    half = dh // 2
+    per = np.empty(dh, np.int64)
+    per[0::2], per[1::2] = np.arange(half), np.arange(half) + half
+    return (np.arange(n_heads)[:, None] * dh + per[None, :]).reshape(-1)
+
+
+def interleave_rows(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Rows a0, b0, a1, b1, ... (gate/up pairs for the fused SwiGLU epilogue)."""
+    out = np.empty((a.shape[0] * 2,) + a.shape[1:], a.dtype)
+    out[0::2], out[1::2] = a, b
+    return out

@@ -1,0 +1,300 @@
+// Decode attention over a resident fp16 KV cache (flash-decoding / split-KV).
+//
+//   o[b, h, :] = softmax(q[b, h, :] . K[b, h/G, :L, :]^T * scale) @ V[b, h/G, :L, :]
+//
+// Semantics follow the reference's decode attention (aneforge/llm.py:214-237: GQA head h
+// reads kv head h // G as in _repeat_kv3, llm.py:205-211; positions > pos masked) and the
+// af.sdpa oracle (aneforge/_bridges/ane_sdpa_fused.py:57-68: fp32 scores with max
+// subtraction, fp32 softmax, fp16 output).  Optional additive mask [B][Skv] and causal
+// alignment for the af.sdpa entry (aneforge/graph.py:993-1040).
+//
+// Kernel 1 (partial): grid (splits, KVH, B); one 256-thread workgroup handles `chunk`
+// positions of one kv head for all G query heads that share it, so each K/V byte is read
+// from HBM once per GQA group.  D/8 lanes cover one 16-byte row slice each; every lane
+// issues all its K and V loads before any math.  Scores stay in registers (two-pass
+// softmax inside the chunk), P@V accumulates in fp32.  Output: (m, l, o[D]) per
+// (b, h, split) in a caller-provided fp32 workspace.
+// Kernel 2 (combine): rescales and sums the split partials, writes fp16.
+#include "afx_common.h"
+
+namespace afx {
+
+struct AttnArgs {
+  const half_t* q;   // [B][Hq][D] via strides
+  const half_t* k;   // cache: b*kv_bs + kvh*kv_hs + pos*D
+  const half_t* v;
+  half_t* o;         // same strides as q
+  const half_t* mask;  // optional additive mask [B][mask_bs] over positions
+  const int* pos;      // optional: ctx length of sequence b = pos[b] + 1 (device)
+  float* ws;           // [B][Hq][nsplit][D+2]
+  long long q_bs, q_hs, kv_bs, kv_hs;
+  long long mask_bs;
+  int B, Hq, Hkv, L, Mmax, chunk, nsplit, causal_off;  // causal_off < 0: no causal masking
+  float scale_log2;    // scale * log2(e)
+};
+
+__device__ __forceinline__ int seq_len(const AttnArgs& a, int b) {
+  int L = a.pos ? a.pos[b] + 1 : a.L;
+  if (L > a.Mmax) L = a.Mmax;
+  if (a.causal_off >= 0) {
+    const int lc = a.causal_off + b + 1;   // query b attends keys [0, causal_off + b]
+    L = lc < L ? lc : L;
+  }
+  return L < 1 ? 1 : L;
+}
+
+template <int D, int G, int NSTEP>
+__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+  constexpr int LPP = D / 8;        // lanes per position (16 B each)
+  constexpr int PPS = 64 / LPP;     // positions per wavefront step
+  constexpr int C = NSTEP * 4 * PPS;
+  __shared__ float red_m[4][G], red_l[4][G];
+  __shared__ float red_o[4][G][D];
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int L = seq_len(a, b);
+  const int p0 = split * C;
+  if (p0 >= L) return;   // whole workgroup: the combine ignores splits past L
+
+  const int dl = lane % LPP;       // which 8-dim slice
+  const int pl = lane / LPP;       // which position within the step
+
+  h2 qh[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const half_t* qp = a.q + (size_t)b * a.q_bs + (size_t)(kvh * G + g) * a.q_hs + dl * 8;
+    u4 t = *(const u4*)qp;
+    qh[g][0] = as_h2(t.x); qh[g][1] = as_h2(t.y); qh[g][2] = as_h2(t.z); qh[g][3] = as_h2(t.w);
+  }
+
+  const half_t* kb = a.k + (size_t)b * a.kv_bs + (size_t)kvh * a.kv_hs + dl * 8;
+  const half_t* vb = a.v + (size_t)b * a.kv_bs + (size_t)kvh * a.kv_hs + dl * 8;
+  u4 kv[NSTEP], vv[NSTEP];
+  int posn[NSTEP];
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const int p = p0 + (wave + 4 * s) * PPS + pl;
+    posn[s] = p;
+    const int pc = p < L ? p : L - 1;
+    kv[s] = __builtin_nontemporal_load((const u4*)(kb + (size_t)pc * D));
+  }
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const int pc = posn[s] < L ? posn[s] : L - 1;
+    vv[s] = __builtin_nontemporal_load((const u4*)(vb + (size_t)pc * D));
+  }
+
+  // scores (log2 domain), identical in all LPP lanes of a position
+  float sc[NSTEP][G];
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const h2 k0 = as_h2(kv[s].x), k1 = as_h2(kv[s].y), k2 = as_h2(kv[s].z), k3 = as_h2(kv[s].w);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float t = dot2(qh[g][0], k0, 0.0f);
+      t = dot2(qh[g][1], k1, t);
+      t = dot2(qh[g][2], k2, t);
+      t = dot2(qh[g][3], k3, t);
+#pragma unroll
+      for (int m = LPP / 2; m >= 1; m >>= 1) t += shfl_xor(t, m);
+      float x = t * a.scale_log2;
+      if (a.mask) x += (float)a.mask[(size_t)b * a.mask_bs + (posn[s] < L ? posn[s] : 0)] * 1.4426950408889634f;
+      sc[s][g] = posn[s] < L ? x : -INFINITY;
+    }
+  }
+
+  // chunk max per head
+  float mx[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) m = fmaxf(m, sc[s][g]);
+#pragma unroll
+    for (int sh = LPP; sh < 64; sh <<= 1) m = fmaxf(m, shfl_xor(m, sh));
+    mx[g] = m;
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int g = 0; g < G; ++g) red_m[wave][g] = mx[g];
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    mx[g] = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
+
+  // probabilities, row sums and P@V
+  float o[G][8];
+  float l[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[g][i] = 0.0f;
+  }
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const h2 v0 = as_h2(vv[s].x), v1 = as_h2(vv[s].y), v2 = as_h2(vv[s].z), v3 = as_h2(vv[s].w);
+    const float vf[8] = {(float)v0.x, (float)v0.y, (float)v1.x, (float)v1.y,
+                         (float)v2.x, (float)v2.y, (float)v3.x, (float)v3.y};
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float p = exp2f(sc[s][g] - mx[g]);   // 0 for masked positions
+      l[g] += p;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[g][i] = __builtin_fmaf(p, vf[i], o[g][i]);
+    }
+  }
+  // reduce across the position groups of the wavefront
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int sh = LPP; sh < 64; sh <<= 1) {
+      l[g] += shfl_xor(l[g], sh);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[g][i] += shfl_xor(o[g][i], sh);
+    }
+  }
+  if (lane < LPP) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) red_o[wave][g][dl * 8 + i] = o[g][i];
+    }
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int g = 0; g < G; ++g) red_l[wave][g] = l[g];
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx - g * D;
+    const float acc = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
+    float* w = a.ws + (((size_t)b * a.Hq + kvh * G + g) * a.nsplit + split) * (D + 2);
+    w[2 + d] = acc;
+    if (d == 0) {
+      w[0] = mx[g];
+      w[1] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int L = seq_len(a, b);
+  const int ns = (L + a.chunk - 1) / a.chunk;
+  const float* w = a.ws + ((size_t)b * a.Hq + h) * a.nsplit * (D + 2);
+  float m = -INFINITY;
+  for (int s = 0; s < ns; ++s) m = fmaxf(m, w[s * (D + 2)]);
+  float num = 0.0f, den = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const float* ws = w + s * (D + 2);
+    const float f = exp2f(ws[0] - m);
+    den = __builtin_fmaf(f, ws[1], den);
+    num = __builtin_fmaf(f, ws[2 + d], num);
+  }
+  a.o[(size_t)b * a.q_bs + (size_t)h * a.q_hs + d] = (half_t)(num / den);
+}
+
+typedef void (*attn_fn)(AttnArgs);
+
+template <int D, int G>
+static attn_fn pick_steps(int nstep) {
+  switch (nstep) {
+    case 1: return attn_partial_kernel<D, G, 1>;
+    case 2: return attn_partial_kernel<D, G, 2>;
+    case 4: return attn_partial_kernel<D, G, 4>;
+    default: return attn_partial_kernel<D, G, 8>;
+  }
+}
+template <int D>
+static attn_fn pick_g(int G, int nstep) {
+  switch (G) {
+    case 1: return pick_steps<D, 1>(nstep);
+    case 2: return pick_steps<D, 2>(nstep);
+    case 4: return pick_steps<D, 4>(nstep);
+    default: return pick_steps<D, 8>(nstep);
+  }
+}
+
+static int attn_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    hipGetDevice(&dev);
+    hipDeviceProp_t p;
+    cus = hipGetDeviceProperties(&p, dev) == hipSuccess ? p.multiProcessorCount : 256;
+  }
+  return cus;
+}
+
+// Steps per wavefront (chunk = nstep * 4 * (512 / D) positions): the largest chunk that
+// still gives about two workgroups per CU.
+static int choose_nstep(int D, int B, int Hkv, int L, int want) {
+  if (want == 1 || want == 2 || want == 4 || want == 8) return want;
+  const int pps = 512 / D;
+  const int target = 2 * attn_cus();
+  for (int ns = 8; ns >= 1; ns >>= 1) {
+    const int c = ns * 4 * pps;
+    const long long wgs = (long long)B * Hkv * ((L + c - 1) / c);
+    if (wgs >= target) return ns;
+  }
+  return 1;
+}
+
+}  // namespace afx
+
+using namespace afx;
+
+extern "C" {
+
+// Workspace bytes needed by afx_decode_attn for a given shape (max_len = the longest ctx).
+long long afx_decode_attn_ws_bytes(int B, int Hq, int Hkv, int D, int max_len, int nstep_hint) {
+  if (D != 64 && D != 128) return -1;
+  const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
+  const int chunk = ns * 4 * (512 / D);
+  const long long nsplit = (max_len + chunk - 1) / chunk;
+  return (long long)B * Hq * nsplit * (D + 2) * 4;
+}
+
+// q/o: element (b, h, d) at b*q_bs + h*q_hs + d.  K/V: (b, kvh, p, d) at b*kv_bs + kvh*kv_hs + p*D + d.
+// Context length: pos ? pos[b]+1 : ctx_len (clamped to max_len).  causal_off >= 0 additionally
+// limits query b to keys [0, causal_off + b] (af.sdpa is_causal with Sq == Skv: causal_off = 0).
+// mask: optional fp16 additive mask, element (b, p) at b*mask_bs + p.
+int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long long q_bs, long long q_hs,
+                    long long kv_bs, long long kv_hs, int B, int Hq, int Hkv, int D, int ctx_len,
+                    const int* pos, int max_len, const void* mask, long long mask_bs, int causal_off,
+                    float scale, void* ws, long long ws_bytes, int nstep_hint, void* stream) {
+  AFX_REQUIRE(q && k && v && o && ws, "afx_decode_attn: null pointer");
+  AFX_REQUIRE(D == 64 || D == 128, "afx_decode_attn: head dim %d not supported (64, 128)", D);
+  AFX_REQUIRE(B >= 1 && Hkv >= 1 && Hq % Hkv == 0, "afx_decode_attn: bad heads Hq=%d Hkv=%d", Hq, Hkv);
+  const int G = Hq / Hkv;
+  AFX_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "afx_decode_attn: GQA group %d not in {1,2,4,8}", G);
+  AFX_REQUIRE(max_len >= 1 && (pos || (ctx_len >= 1 && ctx_len <= max_len)),
+              "afx_decode_attn: ctx_len=%d outside [1, max_len=%d]", ctx_len, max_len);
+  AFX_REQUIRE((q_hs % 8) == 0 && (q_bs % 8) == 0 && (kv_hs % 8) == 0 && (kv_bs % 8) == 0,
+              "afx_decode_attn: strides must be multiples of 8 elements");
+  const long long need = afx_decode_attn_ws_bytes(B, Hq, Hkv, D, max_len, nstep_hint);
+  AFX_REQUIRE(ws_bytes >= need, "afx_decode_attn: workspace %lld B < %lld B", ws_bytes, need);
+  AttnArgs a = {};
+  a.q = (const half_t*)q; a.k = (const half_t*)k; a.v = (const half_t*)v; a.o = (half_t*)o;
+  a.mask = (const half_t*)mask; a.pos = pos; a.ws = (float*)ws;
+  a.q_bs = q_bs; a.q_hs = q_hs; a.kv_bs = kv_bs; a.kv_hs = kv_hs; a.mask_bs = mask_bs;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.L = ctx_len; a.Mmax = max_len; a.causal_off = causal_off;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
+  a.chunk = ns * 4 * (512 / D);
+  a.nsplit = (max_len + a.chunk - 1) / a.chunk;
+  attn_fn fn = D == 64 ? pick_g<64>(G, ns) : pick_g<128>(G, ns);
+  hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
+  int rc = check_launch("afx_decode_attn(partial)");
+  if (rc) return rc;
+  if (D == 64)
+    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(Hq, B), dim3(64), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(Hq, B), dim3(128), 0, (hipStream_t)stream, a);
+  return check_launch("afx_decode_attn(combine)");
+}
+
+}  // extern "C"

@@ -1,0 +1,153 @@
+// Weight codecs on the device: GGUF Q4_0 <-> the superblock layout the GEMV streams, and
+// "debug" dequantisers that run the exact same in-register unpack as the GEMV kernels and
+// write the dequantised weights as fp32, so the host can check them bit-for-bit.
+//
+// GGUF Q4_0 block (ggml block_q4_0; decoded on the host by the reference through the
+// third-party `gguf` package, aneforge/_gguf.py:34-39): 18 bytes = fp16 d + 16 bytes qs;
+// element i (i < 16) is (qs[i] & 15) - 8, element i+16 is (qs[i] >> 4) - 8, value = elem * d.
+//
+// Superblock layout (this library): per row, K/128 superblocks of 64 bytes.  The 32-bit word
+// at index (row*(K/128) + sb)*16 + g*4 + j holds elements 8g..8g+7 of block 4*sb+j, with
+// the even elements' nibbles in bits 0,4,8,12 and the odd elements' in bits 16,20,24,28
+// (see q4_word_to_h2).  A 16-byte load at offset 16g of a superblock therefore yields word g
+// of four consecutive blocks - exactly one MFMA B-operand slot per block, and 32 weights for
+// the dot2 GEMV.  Block scales stay row-major: d[row][K/32].
+#include "afx_common.h"
+
+namespace afx {
+
+__global__ void q4_repack_kernel(const uint8_t* __restrict__ blocks, uint32_t* __restrict__ qs,
+                                 half_t* __restrict__ d, int N, int K) {
+  const int nb = K >> 5;
+  const long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= (long long)N * nb) return;
+  const int row = (int)(b / nb), blk = (int)(b - (long long)row * nb);
+  const uint8_t* src = blocks + b * 18;
+  uint16_t dbits = (uint16_t)src[0] | ((uint16_t)src[1] << 8);
+  d[(size_t)row * nb + blk] = __builtin_bit_cast(half_t, dbits);
+  uint8_t e[32];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    e[i] = src[2 + i] & 15;
+    e[i + 16] = src[2 + i] >> 4;
+  }
+  const int sb = blk >> 2, j = blk & 3;
+  uint32_t* dst = qs + ((size_t)row * (K >> 7) + sb) * 16;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      w |= (uint32_t)e[8 * g + 2 * t] << (4 * t);
+      w |= (uint32_t)e[8 * g + 2 * t + 1] << (16 + 4 * t);
+    }
+    dst[g * 4 + j] = w;
+  }
+}
+
+__global__ void q4_unpack_kernel(const uint32_t* __restrict__ qs, const half_t* __restrict__ d,
+                                 uint8_t* __restrict__ blocks, int N, int K) {
+  const int nb = K >> 5;
+  const long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= (long long)N * nb) return;
+  const int row = (int)(b / nb), blk = (int)(b - (long long)row * nb);
+  const int sb = blk >> 2, j = blk & 3;
+  const uint32_t* src = qs + ((size_t)row * (K >> 7) + sb) * 16;
+  uint8_t e[32];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w = src[g * 4 + j];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      e[8 * g + 2 * t] = (w >> (4 * t)) & 15;
+      e[8 * g + 2 * t + 1] = (w >> (16 + 4 * t)) & 15;
+    }
+  }
+  uint8_t* dst = blocks + b * 18;
+  const uint16_t dbits = __builtin_bit_cast(uint16_t, d[(size_t)row * nb + blk]);
+  dst[0] = dbits & 255;
+  dst[1] = dbits >> 8;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dst[2 + i] = (uint8_t)(e[i] | (e[i + 16] << 4));
+}
+
+// out[n][k] = code * scale as fp32, through the GEMV's own unpack helpers.
+__global__ void dequant_i8_kernel(const uint32_t* __restrict__ q, const half_t* __restrict__ s,
+                                  float* __restrict__ out, int N, int K) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;   // one dword = 4 codes
+  const long long nw = (long long)N * (K >> 2);
+  if (i >= nw) return;
+  const int row = (int)(i / (K >> 2));
+  h2 lo, hi;
+  i8x4_to_h2(q[i], lo, hi);
+  const float sc = (float)s[row];
+  float4 o = {(float)lo.x * sc, (float)lo.y * sc, (float)hi.x * sc, (float)hi.y * sc};
+  *(float4*)(out + 4 * i) = o;
+}
+
+__global__ void dequant_q4_kernel(const uint32_t* __restrict__ qs, const half_t* __restrict__ d,
+                                  float* __restrict__ out, int N, int K) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;   // one word = 8 elements
+  const long long nw = (long long)N * (K >> 3);
+  if (i >= nw) return;
+  const int wpr = K >> 3;
+  const int row = (int)(i / wpr), w = (int)(i - (long long)row * wpr);
+  const int sb = w >> 4, g = (w >> 2) & 3, j = w & 3;
+  const int blk = 4 * sb + j;
+  h2 v[4];
+  q4_word_to_h2(qs[i], v);
+  const float sc = (float)d[(size_t)row * (K >> 5) + blk];
+  float* o = out + (size_t)row * K + 32 * blk + 8 * g;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    o[2 * t] = (float)v[t].x * sc;
+    o[2 * t + 1] = (float)v[t].y * sc;
+  }
+}
+
+}  // namespace afx
+
+using namespace afx;
+
+extern "C" {
+
+// GGUF Q4_0 blocks [N][K/32] (18 B each) -> superblock codes qs [N][K/2] + scales d [N][K/32].
+int afx_q4_0_repack(const void* blocks, void* qs, void* d, int N, int K, void* stream) {
+  AFX_REQUIRE(blocks && qs && d, "afx_q4_0_repack: null pointer");
+  AFX_REQUIRE(N >= 1 && K >= 128 && K % 128 == 0, "afx_q4_0_repack: K=%d must be a positive multiple of 128", K);
+  const long long nblk = (long long)N * (K / 32);
+  hipLaunchKernelGGL(q4_repack_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)blocks, (uint32_t*)qs, (half_t*)d, N, K);
+  return check_launch("afx_q4_0_repack");
+}
+
+// Inverse of afx_q4_0_repack (round-trip check back to GGUF bytes).
+int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, void* stream) {
+  AFX_REQUIRE(blocks && qs && d, "afx_q4_0_unpack: null pointer");
+  AFX_REQUIRE(N >= 1 && K >= 128 && K % 128 == 0, "afx_q4_0_unpack: K=%d must be a positive multiple of 128", K);
+  const long long nblk = (long long)N * (K / 32);
+  hipLaunchKernelGGL(q4_unpack_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint32_t*)qs, (const half_t*)d, (uint8_t*)blocks, N, K);
+  return check_launch("afx_q4_0_unpack");
+}
+
+// Dequantise through the GEMV unpack path: fmt 0 = int8 [N][K] + s[N]; fmt 1 = Q4_0 superblock.
+int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream) {
+  AFX_REQUIRE(w && scale && out, "afx_dequant: null pointer");
+  if (fmt == 0) {
+    AFX_REQUIRE(K % 4 == 0 && ((uintptr_t)w & 3) == 0, "afx_dequant: int8 K must be a multiple of 4");
+    const long long nw = (long long)N * (K / 4);
+    hipLaunchKernelGGL(dequant_i8_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint32_t*)w, (const half_t*)scale, out, N, K);
+  } else if (fmt == 1) {
+    AFX_REQUIRE(K % 128 == 0, "afx_dequant: Q4_0 K must be a multiple of 128");
+    const long long nw = (long long)N * (K / 8);
+    hipLaunchKernelGGL(dequant_q4_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint32_t*)w, (const half_t*)scale, out, N, K);
+  } else {
+    return set_error("afx_dequant: unknown format %d", fmt);
+  }
+  return check_launch("afx_dequant");
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+// Shared device helpers for the aneforge_amd HIP kernels (gfx950 / CDNA4 only).
+//
+// Conventions used by every kernel in this library:
+//  * fp16 tensors travel as raw IEEE half bits; on the device they are `_Float16`.
+//  * All accumulation is fp32.  Integer codes are turned into fp16 values EXACTLY
+//    (magic-number construction, see i8x4_to_h2 / q4_word_to_h2), so a dequantised
+//    weight q*s is bit-identical to the fp32 product of the code and the fp32 scale.
+//  * Wavefronts are 64 lanes; every reduction below is written for wave64.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace afx {
+
+typedef _Float16 half_t;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// c + a.x*b.x + a.y*b.y in fp32 (v_dot2_f32_f16).
+__device__ __forceinline__ float dot2(h2 a, h2 b, float c) {
+  return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+// Four signed int8 codes (one dword, byte i = code i) -> two exact fp16 pairs.
+// (b ^ 0x80) = b + 128 is placed in the low mantissa byte of 0x64xx (= 1024 + byte),
+// then 1152 = 1024 + 128 is subtracted; every step is exact in fp16.
+__device__ __forceinline__ void i8x4_to_h2(uint32_t w, h2& lo, h2& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const h2 off = {(half_t)1152.0f, (half_t)1152.0f};
+  lo = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - off;   // codes 0,1
+  hi = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - off;   // codes 2,3
+}
+
+// One 32-bit word of the repacked Q4_0 layout holds 8 consecutive elements e0..e7 of a
+// 32-element block: low half-word = e0,e2,e4,e6 (bits 0,4,8,12), high half-word =
+// e1,e3,e5,e7 (bits 16,20,24,28).  Output: exact fp16 pairs (e0-8,e1-8) .. (e6-8,e7-8).
+// Nibble n in bits 0..3 of a half gives 0x6400|n = 1024+n; in bits 4..7 it gives
+// 1024+16n, and (1024+16n)/16 - 72 = n-8 exactly.
+__device__ __forceinline__ void q4_word_to_h2(uint32_t w, h2 out[4]) {
+  const h2 off_lo = {(half_t)-1032.0f, (half_t)-1032.0f};
+  const h2 sc_hi = {(half_t)0.0625f, (half_t)0.0625f};
+  const h2 off_hi = {(half_t)-72.0f, (half_t)-72.0f};
+  const uint32_t w8 = w >> 8;
+  out[0] = as_h2((w & 0x000F000Fu) | 0x64006400u) + off_lo;
+  out[1] = as_h2((w & 0x00F000F0u) | 0x64006400u) * sc_hi + off_hi;
+  out[2] = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + off_lo;
+  out[3] = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sc_hi + off_hi;
+}
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+  return v;
+}
+
+// Transposed butterfly: each lane holds v[R] (R row partials); afterwards lane l holds the
+// full 64-lane sum of row (l >> (6 - log2 R)) in v[0].  Costs R-1 + log2(64/R) shuffles
+// instead of R*6.
+template <int R>
+__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
+  static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "R must be a power of two <= 16");
+  if constexpr (R >= 16) {
+    const bool hi = lane & 32;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float keep = hi ? v[i + 8] : v[i], send = hi ? v[i] : v[i + 8];
+      v[i] = keep + shfl_xor(send, 32);
+    }
+  }
+  if constexpr (R >= 8) {
+    constexpr int B = (R >= 16) ? 16 : 32;
+    const bool hi = lane & B;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float keep = hi ? v[i + 4] : v[i], send = hi ? v[i] : v[i + 4];
+      v[i] = keep + shfl_xor(send, B);
+    }
+  }
+  if constexpr (R >= 4) {
+    constexpr int B = (R >= 16) ? 8 : (R >= 8) ? 16 : 32;
+    const bool hi = lane & B;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float keep = hi ? v[i + 2] : v[i], send = hi ? v[i] : v[i + 2];
+      v[i] = keep + shfl_xor(send, B);
+    }
+  }
+  if constexpr (R >= 2) {
+    constexpr int B = (R >= 16) ? 4 : (R >= 8) ? 8 : (R >= 4) ? 16 : 32;
+    const bool hi = lane & B;
+    float keep = hi ? v[1] : v[0], send = hi ? v[0] : v[1];
+    v[0] = keep + shfl_xor(send, B);
+  }
+  constexpr int start = 32 / R;  // remaining butterfly over the low bits
+  float s = v[0];
+#pragma unroll
+  for (int m = start; m >= 1; m >>= 1) s += shfl_xor(s, m);
+  return s;
+}
+
+// Row owned by `lane` after wave_reduce_rows<R>.
+template <int R>
+__device__ __forceinline__ int reduced_row_of_lane(int lane) {
+  if constexpr (R == 1) return 0;
+  else if constexpr (R == 2) return lane >> 5;
+  else if constexpr (R == 4) return ((lane >> 5) << 1) | ((lane >> 4) & 1);
+  else if constexpr (R == 8) return ((lane >> 5) << 2) | (((lane >> 4) & 1) << 1) | ((lane >> 3) & 1);
+  else return ((lane >> 5) << 3) | (((lane >> 4) & 1) << 2) | (((lane >> 3) & 1) << 1) | ((lane >> 2) & 1);
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+}  // namespace afx
+
+// ---- host-side error plumbing shared by all entry points (defined in afx_capi.hip) ----
+extern "C" const char* afx_last_error(void);
+namespace afx {
+int set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace afx
+
+#define AFX_REQUIRE(cond, ...) \
+  do { if (!(cond)) return ::afx::set_error(__VA_ARGS__); } while (0)

@@ -1,0 +1,255 @@
+// Sparse MoE dispatch for decode (replaces the reference's dense all-expert compute,
+// aneforge/moe.py:40-63, with identical math: unselected experts have gate weight 0).
+//
+//  afx_moe_topk     softmax over E router logits (fp32), probabilities rounded to fp16, k
+//                   rounds of "row max, lowest index among exact fp16 ties" (moe.py:21-37),
+//                   optional renormalisation (moe.py:55-56); then device-side bucketing:
+//                   cnt[e] and list[e][i] = t*k + slot, in token order (deterministic).
+//  afx_moe_gateup   per active expert e: act[t*k+slot] = silu(g) * u over the tokens routed to e,
+//                   weights [E][2F][D] with gate/up rows interleaved (2i, 2i+1).
+//  afx_moe_down     per active expert e: y[t*k+slot] = act[t*k+slot] @ Wd_e^T, Wd [E][D][F] (fp32 out).
+//  afx_moe_combine  out[t] = fp16(h[t] + fp16(sum_slot g[t,slot] * fp16(y[t*k+slot]))) (+ shared).
+// The grid covers all E experts; workgroups of experts with no tokens exit at once, so the
+// launch shape is fixed and the whole layer is graph-capturable (no host round trip).
+#include "afx_gemv_core.h"
+
+namespace afx {
+
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                       int renorm, float* __restrict__ gate,
+                                                       int* __restrict__ sel, int* __restrict__ cnt,
+                                                       int* __restrict__ list) {
+  extern __shared__ int s_sel[];   // [T][k]
+  const int t = threadIdx.x;
+  for (int tt = t; tt < T; tt += blockDim.x) {
+    const float* lr = logits + (size_t)tt * E;
+    float m = -INFINITY;
+    for (int e = 0; e < E; ++e) m = fmaxf(m, lr[e]);
+    float s = 0.0f;
+    for (int e = 0; e < E; ++e) s += expf(lr[e] - m);
+    const float inv = 1.0f / s;
+    // k rounds: max of the fp16 probabilities, lowest index on exact ties
+    float picked[64];
+    int chosen[64];
+    float tot = 0.0f;
+    for (int r = 0; r < k; ++r) {
+      float best = -1.0f;
+      int bi = -1;
+      for (int e = 0; e < E; ++e) {
+        bool used = false;
+        for (int q = 0; q < r; ++q) used |= chosen[q] == e;
+        if (used) continue;
+        const float p = (float)(half_t)(expf(lr[e] - m) * inv);
+        if (p > best) { best = p; bi = e; }
+      }
+      chosen[r] = bi;
+      picked[r] = best;
+      tot += best;
+    }
+    for (int r = 0; r < k; ++r) {
+      gate[(size_t)tt * k + r] = renorm ? picked[r] / tot : picked[r];
+      sel[(size_t)tt * k + r] = chosen[r];
+      s_sel[tt * k + r] = chosen[r];
+    }
+  }
+  __syncthreads();
+  for (int e = t; e < E; e += blockDim.x) {
+    int c = 0;
+    for (int i = 0; i < T * k; ++i)
+      if (s_sel[i] == e) list[(size_t)e * T + c++] = i;
+    cnt[e] = c;
+  }
+}
+
+struct MoeArgs {
+  const void* w;          // expert weights, expert stride w_es bytes
+  const half_t* scale;    // I8: [E][N]; Q4: [E][N][K/32]
+  long long w_es, s_es;   // per-expert strides (bytes for w, elements for scale)
+  const half_t* x;        // activation rows, row r at x + r_src * ldx
+  int ldx;
+  void* y;
+  int ldy;
+  const int* cnt;
+  const int* list;
+  int T, k, N, K, epi;    // epi: 0 = fp32 store (down), 1 = SwiGLU fp16 (gate/up)
+  int x_by_token;         // 1: x row = list/k (token), 0: x row = list entry (token*k+slot)
+};
+
+template <int FMT, int MG, int R>
+__global__ __launch_bounds__(256) void moe_group_kernel(MoeArgs a) {
+  const int e = blockIdx.y;
+  const int n_e = a.cnt[e];
+  if (n_e == 0) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  if (row0 >= a.N) return;
+  const int K = a.K, N = a.N;
+  const int* lst = a.list + (size_t)e * a.T;
+  const size_t rb = Fmt<FMT>::row_bytes(K);
+  const unsigned char* wbase = (const unsigned char*)a.w + (size_t)e * a.w_es;
+  const half_t* sbase = a.scale ? a.scale + (size_t)e * a.s_es : nullptr;
+  const unsigned char* wrow[R];
+  const half_t* drow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r < N ? row0 + r : N - 1;
+    wrow[r] = wbase + (size_t)row * rb;
+    drow[r] = (FMT == FMT_Q4) ? sbase + (size_t)row * (K >> 5) : nullptr;
+  }
+  const int nchunks = K / Fmt<FMT>::kWeightsPerChunk;
+  const int rr = reduced_row_of_lane<R>(lane);
+  const int row = row0 + rr;
+  constexpr int GROUP = 64 / R;
+  const bool writer = (lane & (GROUP - 1)) == 0;
+
+  for (int mb = 0; mb < n_e; mb += MG) {
+    const half_t* xp[MG];
+    int ent[MG];
+#pragma unroll
+    for (int m = 0; m < MG; ++m) {
+      const int i = mb + m < n_e ? mb + m : n_e - 1;
+      ent[m] = lst[i];
+      const int src = a.x_by_token ? ent[m] / a.k : ent[m];
+      xp[m] = a.x + (size_t)src * a.ldx;
+    }
+    float acc[MG][R];
+#pragma unroll
+    for (int m = 0; m < MG; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+    constexpr int U = 2;
+    for (int cb = lane; cb < nchunks; cb += 64 * U) {
+      u4 wv[U][R];
+      u2 dv[U][R];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = cb + 64 * u;
+        const int cc = c < nchunks ? c : nchunks - 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          wv[u][r] = *(const u4*)(wrow[r] + (size_t)cc * 16);
+          if constexpr (FMT == FMT_Q4) dv[u][r] = *(const u2*)(drow[r] + 4 * (cc >> 2));
+          else dv[u][r] = (u2){0u, 0u};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = cb + 64 * u;
+        if (c < nchunks) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float part[MG];
+#pragma unroll
+            for (int m = 0; m < MG; ++m) part[m] = acc[m][r];
+            Fmt<FMT>::template dot<MG>(wv[u][r], xp, c, K, dv[u][r], part);
+#pragma unroll
+            for (int m = 0; m < MG; ++m) acc[m][r] = part[m];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MG; ++m) {
+      const float sum = wave_reduce_rows<R>(acc[m], lane);
+      const bool live = mb + m < n_e;
+      const float sc = (FMT == FMT_I8 && row < N) ? (float)sbase[row] : 1.0f;
+      const float v = sum * sc;
+      if (a.epi == 1) {
+        const float other = shfl_xor(v, GROUP);
+        if (writer && live && row < N && (row & 1) == 0) {
+          const float g16 = (float)(half_t)v, u16 = (float)(half_t)other;
+          ((half_t*)a.y)[(size_t)ent[m] * a.ldy + (row >> 1)] = (half_t)(silu(g16) * u16);
+        }
+      } else {
+        if (writer && live && row < N) ((float*)a.y)[(size_t)ent[m] * a.ldy + row] = v;
+      }
+    }
+  }
+}
+
+__global__ void moe_combine_kernel(const half_t* __restrict__ h, const float* __restrict__ y,
+                                   const float* __restrict__ gate, const half_t* __restrict__ shared,
+                                   half_t* __restrict__ out, int T, int k, int D) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)T * D) return;
+  const int t = (int)(i / D), d = (int)(i - (long long)t * D);
+  float acc = 0.0f;
+  for (int s = 0; s < k; ++s) {
+    const float ys = (float)(half_t)y[((size_t)t * k + s) * D + d];
+    acc = __builtin_fmaf(gate[(size_t)t * k + s], ys, acc);
+  }
+  float c = (float)(half_t)acc;
+  if (shared) c = (float)(half_t)(c + (float)shared[i]);
+  out[i] = (half_t)((float)h[i] + c);
+}
+
+typedef void (*moe_fn)(MoeArgs);
+template <int FMT>
+static moe_fn pick_moe(int R) {
+  return R >= 4 ? moe_group_kernel<FMT, 4, 4> : R >= 2 ? moe_group_kernel<FMT, 4, 2> : moe_group_kernel<FMT, 4, 1>;
+}
+
+static int moe_launch(int fmt, MoeArgs& a, int E, int R, hipStream_t stream, const char* what) {
+  AFX_REQUIRE(fmt >= 0 && fmt <= 2, "%s: unknown weight format %d", what, fmt);
+  const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : 8;
+  AFX_REQUIRE(a.K % kq == 0, "%s: K=%d must be a multiple of %d", what, a.K, kq);
+  AFX_REQUIRE(a.w && a.x && a.y && a.cnt && a.list, "%s: null pointer", what);
+  AFX_REQUIRE(fmt == FMT_F16 || a.scale, "%s: quantized weights need scales", what);
+  moe_fn fn = fmt == FMT_I8 ? pick_moe<FMT_I8>(R) : fmt == FMT_Q4 ? pick_moe<FMT_Q4>(R) : pick_moe<FMT_F16>(R);
+  const int gx = (a.N + 4 * R - 1) / (4 * R);
+  hipLaunchKernelGGL(fn, dim3(gx, E), dim3(256), 0, stream, a);
+  return check_launch(what);
+}
+
+static long long fmt_row_bytes(int fmt, int K) { return fmt == FMT_I8 ? K : fmt == FMT_Q4 ? K / 2 : 2LL * K; }
+
+}  // namespace afx
+
+using namespace afx;
+
+extern "C" {
+
+int afx_moe_topk(const float* logits, int T, int E, int k, int renorm, float* gate, int* sel, int* cnt,
+                 int* list, void* stream) {
+  AFX_REQUIRE(logits && gate && sel && cnt && list, "afx_moe_topk: null pointer");
+  AFX_REQUIRE(k >= 1 && k <= E && E <= 2049 && k <= 64, "afx_moe_topk: need 1 <= k <= E <= 2049 (k <= 64); got k=%d E=%d", k, E);
+  AFX_REQUIRE(T >= 1 && T * k <= 16384, "afx_moe_topk: T=%d out of range", T);
+  hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(256), (size_t)T * k * sizeof(int), (hipStream_t)stream,
+                     logits, T, E, k, renorm, gate, sel, cnt, list);
+  return check_launch("afx_moe_topk");
+}
+
+// W: [E][2F][D] gate/up interleaved rows (format fmt), x: normed hidden [T][D].
+int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int T, int k, int E, int F, int D,
+                   const int* cnt, const int* list, void* act, int rows_hint, void* stream) {
+  MoeArgs a = {};
+  a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)x; a.ldx = D; a.y = act; a.ldy = F;
+  a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = 2 * F; a.K = D; a.epi = 1; a.x_by_token = 1;
+  a.w_es = fmt_row_bytes(fmt, D) * 2 * F;
+  a.s_es = fmt == FMT_Q4 ? 2LL * F * (D / 32) : 2LL * F;
+  const int R = rows_hint == 1 || rows_hint == 2 || rows_hint == 4 ? (rows_hint < 2 ? 2 : rows_hint) : 4;
+  return moe_launch(fmt, a, E, R, (hipStream_t)stream, "afx_moe_gateup");
+}
+
+// W: [E][D][F], act: [T*k][F] -> y: [T*k][D] fp32.
+int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F, int D,
+                 const int* cnt, const int* list, float* y, int rows_hint, void* stream) {
+  MoeArgs a = {};
+  a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)act; a.ldx = F; a.y = y; a.ldy = D;
+  a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = D; a.K = F; a.epi = 0; a.x_by_token = 0;
+  a.w_es = fmt_row_bytes(fmt, F) * D;
+  a.s_es = fmt == FMT_Q4 ? (long long)D * (F / 32) : (long long)D;
+  const int R = rows_hint == 1 || rows_hint == 2 || rows_hint == 4 ? rows_hint : 4;
+  return moe_launch(fmt, a, E, R, (hipStream_t)stream, "afx_moe_down");
+}
+
+int afx_moe_combine(const void* h, const float* y, const float* gate, const void* shared, void* out, int T, int k,
+                    int D, void* stream) {
+  AFX_REQUIRE(h && y && gate && out, "afx_moe_combine: null pointer");
+  const long long n = (long long)T * D;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const half_t*)h, y, gate, (const half_t*)shared, (half_t*)out, T, k, D);
+  return check_launch("afx_moe_combine");
+}
+
+}  // extern "C"

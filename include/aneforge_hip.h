@@ -1,0 +1,156 @@
+/* libaneforge_hip: the C ABI of the MI355X (gfx950) quantized-decode path.
+ *
+ * This library replaces the native layer the reference binds through ctypes
+ * (aneforge/_runtime.py:60-92 over aneforge/_lib/ane_e5rt_dispatch.mm:528-713).  The
+ * reference hands a whole compiled ANE program to Espresso; here the same work is exposed as
+ * kernel-level entry points that the Python host (aneforge_amd) sequences and captures into
+ * HIP graphs.
+ *
+ * Conventions (all entry points):
+ *   - return 0 on success, a negative code on failure; afx_last_error() gives the calling
+ *     thread's message (reference: int rc / NULL handle + stderr, ane_e5rt_dispatch.mm:528).
+ *   - every buffer is caller-owned DEVICE memory; nothing here allocates in the hot path.
+ *   - fp16 buffers are raw IEEE-754 half bits; int8/Q4 codes are raw bytes.
+ *   - `stream` is a hipStream_t (NULL = default stream); calls enqueue and return at once.
+ *     The Python Program.execute() synchronises, preserving the reference's synchronous
+ *     execute (ane_e5rt_dispatch.mm:667-673).
+ *   - weight formats: 0 = int8 codes [N][K] + fp16 row scale [N]
+ *                     1 = Q4_0 superblock codes [N][K/2] + fp16 block scales [N][K/32]
+ *                     2 = fp16 [N][K]
+ */
+#ifndef ANEFORGE_HIP_H
+#define ANEFORGE_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime plumbing --------------------------------------------------------------- */
+
+/* Error text of the last failing call on this thread (reference: stderr text after rc -1,
+ * aneforge/_lib/ane_e5rt_dispatch.mm:528-608). */
+const char* afx_last_error(void);
+int afx_abi_version(void);
+/* CU count, LDS and L2 bytes, gfx arch number (reference: per-family limits tables,
+ * aneforge/_targets.py:106-116, consulted before compiling). */
+int afx_device_info(int device, int* cu_count, int* lds_bytes, int* l2_bytes, int* gcn_arch);
+/* Block until `stream` drains (reference: synchronous execute, ane_e5rt_dispatch.mm:667-673). */
+int afx_stream_sync(void* stream);
+/* Capture a kernel sequence on `stream` into a replayable graph (reference: a compiled program
+ * executed repeatedly, ane_e5rt_program_compile :528 / _execute :667). */
+int afx_graph_begin(void* stream);
+int afx_graph_end(void* stream, void** exec_out);
+int afx_graph_launch(void* exec, void* stream);
+/* (reference: ane_e5rt_program_release, ane_e5rt_dispatch.mm:675-677) */
+int afx_graph_destroy(void* exec);
+/* Events on the caller's stream, for timing the stream the kernels run on. */
+int afx_event_create(void** ev);
+int afx_event_record(void* ev, void* stream);
+int afx_event_elapsed_ms(void* start, void* stop, float* ms);
+int afx_event_destroy(void* ev);
+
+/* ---- weight-streaming linear layers --------------------------------------------------- */
+
+/* y[M][N] = x[M][K] @ W^T (+bias) (+residual, may alias y); M <= 8; out_f32 selects fp32 y.
+ * Replaces the compress="int8" linear: constexpr_affine_dequantize(axis=0) + matmul
+ * (aneforge/_compile.py:171-179, 375-385; aneforge/graph.py:187-195), the fp16 weight path,
+ * and the GGUF Q4_0 weights the reference dequantises on the host (aneforge/_gguf.py:34-39). */
+int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
+               int M, int N, int K, const void* bias, const void* residual, int out_f32,
+               int rows_hint, void* stream);
+/* y = rms_norm(x, gamma, eps) @ W^T (+bias): RMSNorm (aneforge/graph.py:293-301,
+ * aneforge/_compile.py:738-755) fused as the GEMV prologue. */
+int afx_linear_rms(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
+                   float eps, void* y, int ldy, int M, int N, int K, const void* bias, int out_f32,
+                   int rows_hint, void* stream);
+/* act[M][N/2] = silu(g) * u, rows of W interleaved (gate_i, up_i), optional RMSNorm first:
+ * the front half of _swiglu (aneforge/llm.py:171-175). */
+int afx_linear_swiglu(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
+                      float eps, int norm, void* act, int ld_act, int M, int N, int K, int rows_hint,
+                      void* stream);
+/* [q|k|v] = rms_norm(h) @ Wqkv^T (+bias), RoPE on q and k, k/v written into the resident cache
+ * at row pos[m]: the projection half of _attn_decode (aneforge/llm.py:214-233) including the
+ * masked positional cache write Kin*inv + k*oh, done here as one O(1) row store. */
+int afx_qkv_rope_kv(int fmt, const void* w, const void* scale, const void* h, int ldh, const void* gamma,
+                    float eps, int norm, const void* bias, int nq, int nk, int nv, int dh,
+                    const void* cos_tab, const void* sin_tab, int rope, const int* pos, void* qout,
+                    int ldq, void* kcache, void* vcache, long long kv_seq_stride,
+                    long long kv_head_stride, int kv_len, int M, int K, int rows_hint, void* stream);
+
+/* ---- codecs ----------------------------------------------------------------------------- */
+
+/* GGUF Q4_0 blocks [N][K/32] (18 B) -> superblock layout (reference: GGUFView.get ->
+ * gguf.quants.dequantize, aneforge/_gguf.py:34-39, which this keeps in 4-bit form). */
+int afx_q4_0_repack(const void* blocks, void* qs, void* d, int N, int K, void* stream);
+int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, void* stream);
+/* Dequantise through the GEMV's own unpack path into fp32 (bit-exact check of
+ * quantize_per_row / Q4_0 reconstruction, aneforge/_blob.py:20-25). */
+int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream);
+
+/* ---- attention -------------------------------------------------------------------------- */
+
+long long afx_decode_attn_ws_bytes(int B, int Hq, int Hkv, int D, int max_len, int nstep_hint);
+/* Split-KV decode attention over an fp16 GQA cache: softmax(q K^T * scale (+mask)) V with
+ * query head h reading kv head h / (Hq/Hkv).  Replaces af.sdpa at decode shape
+ * (aneforge/graph.py:993-1040 -> aneforge/_compile.py:1442-1452 -> sdpa_fused,
+ * aneforge/_bridges/ane_sdpa_fused.py:71-164) and the decomposed decode attention of
+ * _attn_decode (aneforge/llm.py:234-236). */
+int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long long q_bs, long long q_hs,
+                    long long kv_bs, long long kv_hs, int B, int Hq, int Hkv, int D, int ctx_len,
+                    const int* pos, int max_len, const void* mask, long long mask_bs, int causal_off,
+                    float scale, void* ws, long long ws_bytes, int nstep_hint, void* stream);
+
+/* ---- norms, rope, sampling -------------------------------------------------------------- */
+
+/* (aneforge/graph.py:293-301) */
+int afx_rmsnorm(const void* x, int ldx, const void* gamma, float eps, void* y, int ldy, int M, int D,
+                void* stream);
+/* x*cos + rotate_half(x)*sin (aneforge/llm.py:96-105) */
+int afx_rope(const void* x, void* y, int rows, int dh, const void* cos_tab, const void* sin_tab,
+             const int* pos_dev, int pos0, int rows_per_pos, void* stream);
+/* host embedding gather of LlamaPrefill.step (aneforge/llm.py:593-594), on the device */
+int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vocab, void* stream);
+/* greedy _sample (aneforge/llm.py:406-409) + the decode loop's bookkeeping (:619-627) on the
+ * device: token = argmax, hist[*step] = token, ++*step, ++*pos, h = embed[token]. */
+int afx_greedy_advance(const float* logits, int V, int* tok, int* pos, int* hist, int hist_cap, int* step,
+                       const void* embed, void* h, int D, void* stream);
+/* np.argmax per row (lowest index on ties) */
+int afx_argmax(const float* x, int M, int V, int* out, void* stream);
+/* graph-capturable fills (zeroing resident state, aneforge/llm.py:581-583) */
+int afx_fill_i32(int* p, int n, int v, void* stream);
+int afx_fill_f16(void* p, long long n, float v, void* stream);
+
+/* ---- generic tensor ops for the af.compile executor (aneforge/graph.py op set) ---------- */
+
+int afx_ew_binary(int op, const void* a, const long long* sa, const void* b, const long long* sb, void* y,
+                  int rank, const int* dim, void* stream);
+int afx_ew_select(const void* c, const long long* sc, const void* a, const long long* sa, const void* b,
+                  const long long* sb, void* y, int rank, const int* dim, void* stream);
+int afx_ew_unary(int op, const void* x, void* y, long long n, float alpha, float beta, void* stream);
+int afx_copy_strided(const void* src, const long long* ss, void* dst, const long long* sd, int rank,
+                     const int* dim, void* stream);
+int afx_softmax(const void* x, void* y, int rows, int cols, void* stream);
+int afx_reduce(int op, const void* x, void* y, int rows, int cols, void* stream);
+int afx_bmm_f16(const void* A, const void* B, void* C, int batch, int M, int N, int K, long long sa,
+                long long sb, long long sc, void* stream);
+
+/* ---- mixture of experts (aneforge/moe.py:21-63) ----------------------------------------- */
+
+/* softmax router -> top-k with the lowest-index fp16 tie rule (_topk_gate, moe.py:21-37) ->
+ * optional renorm (moe.py:55-56) -> device bucketing of tokens per expert */
+int afx_moe_topk(const float* logits, int T, int E, int k, int renorm, float* gate, int* sel, int* cnt,
+                 int* list, void* stream);
+/* active experts only: silu(x Wg_e^T) * (x Wu_e^T) (_experts_gate, moe.py:40-45, :57) */
+int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int T, int k, int E, int F, int D,
+                   const int* cnt, const int* list, void* act, int rows_hint, void* stream);
+/* active experts only: act @ Wd_e (bmm_weight, moe.py:58) */
+int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F, int D,
+                 const int* cnt, const int* list, float* y, int rows_hint, void* stream);
+/* h + sum_e gate * y_e (+ shared expert) (moe.py:59-63) */
+int afx_moe_combine(const void* h, const float* y, const float* gate, const void* shared, void* out, int T,
+                    int k, int D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ANEFORGE_HIP_H */

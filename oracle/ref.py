@@ -1,0 +1,333 @@
+"""CPU oracle for the quantized-decode path — TEST INFRASTRUCTURE ONLY.
+
+This module is a numpy restatement of the reference's algorithms, used solely as the checker
+by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.  The product
+(aneforge_amd) never imports it, and nothing here runs on the GPU.
+
+Every function cites the reference file:line it restates (paths relative to the
+sbryngelson/ANEForge tree).  Where the reference computes in fp16 on the ANE, the oracle
+computes in float64 and rounds to fp16 at the same op boundaries as the HIP kernels
+(`r16`), so kernel-vs-oracle differences are accumulation-order noise only.  Passing
+`exact=True` to the model-level functions disables the fp16 rounding entirely; that mode is
+what the pinning tests compare against Hugging Face transformers and torch.
+
+Pinning status (see tests/test_oracle.py):
+  quantize_per_row, dequant_w8          pinned: closed form + KATs (half-even rounding)
+  q4_0 pack/unpack/dequant, quantize     pinned: ggml spec KATs + brute-force loop
+  quantize_blockwise                    pinned: closed form + reference property tests
+  rms_norm                              pinned: torch + invariants
+  rope_tables / rope / llama3 scaling    pinned: transformers' rope utilities + HF formula
+  attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
+  topk_gate / moe_layer                 pinned: reference tie KAT + HF Qwen3-MoE block
+  decoder step / generate               pinned: HF LlamaForCausalLM (tiny, fp32)
+  palettize_lut4                        parity unpinned (loose properties only)
+"""
+from __future__ import annotations
+
+import numpy as np
+
+f16 = np.float16
+
+
+def r16(a, exact=False):
+    """Round to fp16 (the kernels' output rounding) unless `exact`."""
+    return np.asarray(a, np.float64) if exact else np.asarray(a).astype(f16).astype(np.float64)
+
+
+# ----------------------------------------------------------------------------- int8 codec
+def quantize_per_row(W):
+    """Per-output-channel symmetric int8 (aneforge/_blob.py:20-25): scale = clip(max|W|/127,
+    1e-8) in fp32, q = clip(round-half-even(W/scale), -127, 127); the scale is stored fp16
+    while q used the fp32 scale.  Returns (q int8 [OUT,IN], s fp16 [OUT])."""
+    W = np.asarray(W, np.float32)
+    s32 = np.maximum(np.abs(W).max(axis=1, keepdims=True) / np.float32(127.0), np.float32(1e-8))
+    q = np.clip(np.round(W / s32), -127, 127).astype(np.int8)
+    return q, s32[:, 0].astype(f16)
+
+
+def dequant_w8(q, s):
+    """constexpr_affine_dequantize(axis=0, zero_point=0) (aneforge/_compile.py:171-179) taken
+    in fp32: every int8 x fp16 product is exact in fp32 (<= 19 significant bits)."""
+    return np.asarray(q, np.int8).astype(np.float32) * np.asarray(s, f16).astype(np.float32)[:, None]
+
+
+def quantize_blockwise(W, block_size=32):
+    """aneforge/_blob.py:46-56: int8 codes with one fp32->fp16 scale per [row, block]; the
+    block size clamps down to a divisor of IN.  Returns (q int8 [OUT,IN], s fp16 [OUT,nb], bs)."""
+    W = np.asarray(W, np.float32)
+    OUT, IN = W.shape
+    bs = int(block_size)
+    while bs > 1 and IN % bs:
+        bs -= 1
+    Wb = W.reshape(OUT, IN // bs, bs)
+    s = np.maximum(np.abs(Wb).max(axis=2) / np.float32(127.0), np.float32(1e-8))
+    q = np.clip(np.round(Wb / s[:, :, None]), -127, 127).astype(np.int8).reshape(OUT, IN)
+    return q, s.astype(f16), bs
+
+
+# ----------------------------------------------------------------------------- Q4_0 codec
+# ggml block_q4_0 (the format aneforge/_gguf.py:34-39 hands to gguf.quants.dequantize):
+# 18 bytes = fp16 d, then 16 bytes qs; element i<16 = (qs[i] & 15) - 8, element i+16 =
+# (qs[i] >> 4) - 8; value = element * d.
+Q4_BLOCK = 32
+Q4_BYTES = 18
+
+
+def pack_q4_0(codes, d):
+    """codes uint8 [N, K] in 0..15 (value = code - 8), d fp16 [N, K/32] -> bytes [N, K/32*18]."""
+    codes = np.asarray(codes, np.uint8)
+    N, K = codes.shape
+    nb = K // Q4_BLOCK
+    c = codes.reshape(N, nb, Q4_BLOCK)
+    qs = (c[:, :, :16] & 15) | ((c[:, :, 16:] & 15) << 4)
+    out = np.empty((N, nb, Q4_BYTES), np.uint8)
+    out[:, :, :2] = np.asarray(d, f16).reshape(N, nb, 1).view(np.uint8).reshape(N, nb, 2)
+    out[:, :, 2:] = qs
+    return out.reshape(N, nb * Q4_BYTES)
+
+
+def unpack_q4_0(blocks, N, K):
+    """bytes [N, K/32*18] -> (codes uint8 [N, K], d fp16 [N, K/32])."""
+    b = np.asarray(blocks, np.uint8).reshape(N, K // Q4_BLOCK, Q4_BYTES)
+    d = b[:, :, :2].copy().view(f16).reshape(N, K // Q4_BLOCK)
+    qs = b[:, :, 2:]
+    codes = np.concatenate([qs & 15, qs >> 4], axis=2).reshape(N, K)
+    return codes, d
+
+
+def dequant_q4_0(blocks, N, K):
+    """Q4_0 bytes -> fp32 weights [N, K]; (code-8)*d is exact in fp32."""
+    codes, d = unpack_q4_0(blocks, N, K)
+    vals = codes.astype(np.float32) - 8.0
+    return (vals.reshape(N, K // Q4_BLOCK, Q4_BLOCK) * d.astype(np.float32)[:, :, None]).reshape(N, K)
+
+
+def quantize_q4_0(W):
+    """ggml's reference Q4_0 quantizer (quantize_row_q4_0_ref): per block, m = the element of
+    largest magnitude (signed), d = m / -8, code = min(15, trunc(x/d + 8.5)).  -> bytes."""
+    W = np.asarray(W, np.float32)
+    N, K = W.shape
+    Wb = W.reshape(N, K // Q4_BLOCK, Q4_BLOCK)
+    idx = np.abs(Wb).argmax(axis=2)
+    m = np.take_along_axis(Wb, idx[:, :, None], axis=2)[:, :, 0]
+    d = m / np.float32(-8.0)
+    inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, 1), np.float32(0.0)).astype(np.float32)
+    codes = np.minimum(15, np.trunc(Wb * inv[:, :, None] + np.float32(8.5))).astype(np.int32)
+    codes = np.clip(codes, 0, 15).astype(np.uint8).reshape(N, K)
+    return pack_q4_0(codes, d.astype(f16))
+
+
+# ----------------------------------------------------------------------------- linear layers
+def linear(x16, Wf32, bias=None, exact=False):
+    """y = x @ W^T (+ bias) in float64 from fp16 x, rounded to fp16 (aneforge/graph.py:187-195,
+    aneforge/_compile.py:375-385; the kernel accumulates in fp32)."""
+    y = np.asarray(x16, np.float64) @ np.asarray(Wf32, np.float64).T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    return r16(y, exact)
+
+
+# ----------------------------------------------------------------------------- norms / rope
+def rms_norm(x, g, eps=1e-5, exact=False):
+    """Textbook RMSNorm x / sqrt(mean(x^2) + eps) * g, as in the reference's numpy oracles
+    (tests/test_moe.py:26, bench/decode_measurement.py:92-94); the device lowering
+    (aneforge/_compile.py:738-755) agrees to within eps/mean(x^2)."""
+    x = np.asarray(x, np.float64)
+    ms = (x * x).mean(-1, keepdims=True)
+    return r16(x / np.sqrt(ms + eps) * np.asarray(g, np.float64), exact)
+
+
+def llama3_rope_scale(inv, s):
+    """Llama-3.1 inv_freq rescaling (aneforge/llm.py:62-73)."""
+    factor, lo, hi = float(s["factor"]), float(s["low_freq_factor"]), float(s["high_freq_factor"])
+    old = float(s["original_max_position_embeddings"])
+    low_wl, high_wl = old / lo, old / hi
+    wl = 2.0 * np.pi / inv
+    scaled = np.where(wl > low_wl, inv / factor, inv)
+    smooth = (old / wl - lo) / (hi - lo)
+    blended = (1.0 - smooth) * scaled / factor + smooth * scaled
+    return np.where((wl >= high_wl) & (wl <= low_wl), blended, scaled)
+
+
+def rope_tables(seq, dh, base=10000.0, rotary_dim=0, interleaved=False, scaling=None):
+    """[seq, dh] cos/sin tables in float64, cast to fp16 (aneforge/llm.py:76-93)."""
+    rd = rotary_dim or dh
+    inv = 1.0 / (base ** (np.arange(0, rd, 2) / rd))
+    if scaling and scaling.get("rope_type") == "llama3":
+        inv = llama3_rope_scale(inv, scaling)
+    ang = np.arange(seq)[:, None] * inv[None, :]
+    if interleaved:
+        c, s = np.repeat(np.cos(ang), 2, axis=1), np.repeat(np.sin(ang), 2, axis=1)
+    else:
+        c, s = np.cos(np.concatenate([ang, ang], -1)), np.sin(np.concatenate([ang, ang], -1))
+    if rd < dh:
+        c = np.concatenate([c, np.ones((seq, dh - rd))], 1)
+        s = np.concatenate([s, np.zeros((seq, dh - rd))], 1)
+    return c.astype(f16), s.astype(f16)
+
+
+def rope(x, cos, sin, exact=False):
+    """x*cos + rotate_half(x)*sin over the last axis (aneforge/llm.py:96-105, neox layout)."""
+    x = np.asarray(x, np.float64)
+    h = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., h:], x[..., :h]], -1)
+    return r16(x * np.asarray(cos, np.float64) + rot * np.asarray(sin, np.float64), exact)
+
+
+# ----------------------------------------------------------------------------- attention
+def attention(q, K, V, scale=None, lengths=None, mask=None, exact=False):
+    """softmax(q K^T * scale (+ mask)) V with fp32-or-better softmax and an fp16 result
+    (aneforge/_bridges/ane_sdpa_fused.py:57-68).  GQA: query head h reads kv head h // G
+    (aneforge/llm.py:205-211).  q [B, Hq, Sq, D]; K/V [B, Hkv, L, D]; `lengths[b]` limits the
+    keys of batch b to [0, lengths[b]) (the -1e4 position mask of aneforge/llm.py:584-588)."""
+    q = np.asarray(q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    B, Hq, Sq, D = q.shape
+    Hkv = K.shape[1]
+    G = Hq // Hkv
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    out = np.zeros((B, Hq, Sq, D))
+    for b in range(B):
+        L = K.shape[2] if lengths is None else int(lengths[b])
+        for h in range(Hq):
+            s = q[b, h] @ K[b, h // G, :L].T * scale           # [Sq, L]
+            if mask is not None:
+                s = s + np.asarray(mask, np.float64)[..., :L].reshape(-1, L)[: Sq]
+            s = s - s.max(-1, keepdims=True)
+            p = np.exp(s)
+            p = p / p.sum(-1, keepdims=True)
+            out[b, h] = p @ V[b, h // G, :L]
+    return r16(out, exact)
+
+
+def silu(x):
+    x = np.asarray(x, np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+# ----------------------------------------------------------------------------- MoE
+def topk_gate(probs16, k):
+    """aneforge/moe.py:21-37: k rounds of row max with the LOWEST index among exact ties;
+    exactly k experts per row; returns probs masked to the chosen experts.  Bounds
+    1 <= k <= E <= 2049 else ValueError (moe.py:27-28)."""
+    p = np.asarray(probs16, np.float64)
+    T, E = p.shape
+    if not 1 <= k <= E <= 2049:
+        raise ValueError(f"moe top-k: need 1 <= k <= E <= 2049; got k={k}, E={E}")
+    out = np.zeros_like(p)
+    for t in range(T):
+        rem = p[t].copy()
+        for _ in range(k):
+            j = int(np.flatnonzero(rem == rem.max())[0])
+            out[t, j] = p[t, j]
+            rem[j] = -np.inf
+    return out
+
+
+def moe_route(hn16, router, k, renorm=True):
+    """Router: softmax(hn R^T) over experts (fp32+), probabilities taken at fp16 (the
+    reference's fp16 tie semantics), top-k, optional renorm (aneforge/moe.py:53-56).
+    Returns (gate [T, E] with zeros off the top-k, chosen index sets)."""
+    lg = np.asarray(hn16, np.float64) @ np.asarray(router, np.float64).T
+    p = np.exp(lg - lg.max(-1, keepdims=True))
+    p = (p / p.sum(-1, keepdims=True)).astype(f16).astype(np.float64)
+    g = topk_gate(p, k)
+    if renorm:
+        g = g / g.sum(1, keepdims=True)
+    chosen = [sorted(np.flatnonzero(g[t]).tolist()) for t in range(g.shape[0])]
+    return g, chosen
+
+
+def moe_layer(h16, mlp_norm, router, Wg, Wu, Wd, k, renorm=True, eps=1e-5, exact=False):
+    """MoE SwiGLU MLP with residual (aneforge/moe.py:48-63), active experts only (identical to
+    the dense all-expert sum because unselected experts carry weight 0).  Wg/Wu [E, F, D] and
+    Wd [E, D, F] as dequantised fp32; rounding points follow the HIP kernels:
+    act = fp16(silu(fp16 g) * fp16 u), y_e = fp16(act Wd_e^T), out = fp16(h + fp16(sum g*y))."""
+    h = np.asarray(h16, np.float64)
+    hn = rms_norm(h, mlp_norm, eps, exact)
+    gate, chosen = moe_route(hn, router, k, renorm)
+    T, D = h.shape
+    comb = np.zeros((T, D))
+    for t in range(T):
+        for e in chosen[t]:
+            g = r16(hn[t] @ np.asarray(Wg[e], np.float64).T, exact)
+            u = r16(hn[t] @ np.asarray(Wu[e], np.float64).T, exact)
+            a = r16(silu(g) * u, exact)
+            y = r16(a @ np.asarray(Wd[e], np.float64).T, exact)
+            comb[t] += gate[t, e] * y
+    return r16(h + r16(comb, exact), exact), gate, chosen
+
+
+# ----------------------------------------------------------------------------- decoder
+def decode_layer(h16, w, cfg, K, V, pos, cos_row, sin_row, exact=False, trace=None):
+    """One pre-norm decoder layer for one token at position `pos` against a resident cache
+    (aneforge/llm.py:214-237 `_attn_decode` + :171-175 `_swiglu`).  w holds dequantised
+    fp32 weights: wq [H*dh, D], wk/wv [KV*dh, D], wo [D, H*dh], wgate/wup [F, D], wdown [D, F],
+    attn_norm/mlp_norm [D], optional q_bias/k_bias/v_bias/o_bias.  K/V [KV, M, dh] are
+    updated in place at row pos.  Returns the new hidden [1, D]."""
+    H, KV, dh, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg["dh"], cfg["norm_eps"]
+    h = np.asarray(h16, np.float64).reshape(1, -1)
+    xn = rms_norm(h, w["attn_norm"], eps, exact)
+    q = linear(xn, w["wq"], w.get("q_bias"), exact).reshape(H, dh)
+    k = linear(xn, w["wk"], w.get("k_bias"), exact).reshape(KV, dh)
+    v = linear(xn, w["wv"], w.get("v_bias"), exact).reshape(KV, dh)
+    if "q_norm" in w:
+        q = rms_norm(q, w["q_norm"], eps, exact)
+        k = rms_norm(k, w["k_norm"], eps, exact)
+    if cfg.get("rope", True):
+        q = rope(q, cos_row, sin_row, exact)
+        k = rope(k, cos_row, sin_row, exact)
+    K[:, pos] = k
+    V[:, pos] = v
+    a = attention(q[None, :, None, :], K[None], V[None], 1.0 / np.sqrt(dh), [pos + 1], exact=exact)
+    a = a.reshape(1, H * dh)
+    h1 = r16(h + linear(a, w["wo"], w.get("o_bias"), exact), exact)
+    hn = rms_norm(h1, w["mlp_norm"], eps, exact)
+    g = linear(hn, w["wgate"], None, exact)
+    u = linear(hn, w["wup"], None, exact)
+    act = r16(silu(g) * u, exact)
+    out = r16(h1 + linear(act, w["wdown"], None, exact), exact)
+    if trace is not None:
+        trace.append(out.copy())
+    return out
+
+
+def logits(h16, final_norm, lm_head, eps=1e-5, exact=False):
+    """Final RMSNorm then the fp16 lm_head, logits kept in float64 (aneforge/llm.py:395-404)."""
+    hn = rms_norm(h16, final_norm, eps, exact)
+    return np.asarray(hn, np.float64).reshape(1, -1) @ np.asarray(lm_head, np.float64).T
+
+
+def decode_step(tok, pos, W, cfg, caches, tables, exact=False, trace=None):
+    """Embedding gather -> all layers -> final norm -> lm_head logits [vocab]."""
+    cos, sin = tables
+    h = np.asarray(W["embed"][tok], np.float64).reshape(1, -1)
+    h = r16(h, exact)
+    for li, lw in enumerate(W["layers"]):
+        K, V = caches[li]
+        h = decode_layer(h, lw, cfg, K, V, pos, cos[pos], sin[pos], exact, trace)
+    return logits(h, W["final_norm"], W["lm_head"], cfg["norm_eps"], exact)[0]
+
+
+def generate(prompt, n_new, W, cfg, M, exact=False, caches=None, start_pos=None):
+    """Greedy token-by-token generation with a resident cache (restates the decode loop of
+    aneforge/llm.py:560-633 with batched_prefill=False, and examples/gpt_multilayer_resident.py:75-101).
+    Returns (tokens, list of logits per generated token)."""
+    dh = cfg["dh"]
+    tables = rope_tables(M, dh, cfg.get("rope_base", 10000.0), scaling=cfg.get("rope_scaling"))
+    if caches is None:
+        caches = [(np.zeros((cfg["n_kv_heads"], M, dh)), np.zeros((cfg["n_kv_heads"], M, dh)))
+                  for _ in W["layers"]]
+    p0 = 0 if start_pos is None else start_pos
+    for i, tok in enumerate(prompt[:-1]):
+        decode_step(tok, p0 + i, W, cfg, caches, tables, exact)
+    cur, pos = prompt[-1], p0 + len(prompt) - 1
+    out, all_logits = [], []
+    for _ in range(n_new):
+        lg = decode_step(cur, pos, W, cfg, caches, tables, exact)
+        nxt = int(np.argmax(lg))
+        out.append(nxt)
+        all_logits.append(lg)
+        cur, pos = nxt, pos + 1
+    return out, all_logits

@@ -1,0 +1,42 @@
+"""Shared helpers for the parity tests (plain module, not a test file)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+RTOL, ATOL, MIN_COS = 1e-2, 1e-3, 0.9999     # the fp16 parity bar of the path
+
+
+def say(msg: str) -> None:
+    """Name the case before a GPU step, so a failure log identifies it."""
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def cosine(a, b) -> float:
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-30))
+
+
+def check_f16(got, want, rtol=RTOL, atol=ATOL, min_cos=MIN_COS, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    bad = ~np.isclose(got, want, rtol=rtol, atol=atol)
+    c = cosine(got, want)
+    assert not bad.any(), (f"{what}: {int(bad.sum())}/{bad.size} outside rtol={rtol} atol={atol}; "
+                           f"max abs err {np.abs(got - want).max():.3e}; cos {c:.6f}")
+    assert c >= min_cos, f"{what}: cosine {c:.6f} < {min_cos}"
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()

@@ -1,0 +1,345 @@
+"""Parity of each HIP kernel against the CPU oracle (oracle/ref.py), through the C ABI.
+
+Integer unpack/dequant is checked bit-for-bit; fp16 outputs within rtol 1e-2 / atol 1e-3
+with cosine >= 0.9999.  Shapes cover the benchmark configurations (full size) plus ragged
+sizes that exercise the tails (rows not a multiple of the tile, K not a multiple of the
+wavefront's slab, partial attention splits)."""
+import numpy as np
+import pytest
+
+from _util import check_f16, cosine, dev, host, say
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def K():
+    from aneforge_amd import _kernels
+    return _kernels
+
+
+# ----------------------------------------------------------------------------- codecs
+def test_dequant_int8_bit_exact(K):
+    say("dequant int8 [300, 4096]")
+    rng = np.random.default_rng(10)
+    q = rng.integers(-128, 128, (300, 4096), dtype=np.int8)          # includes -128 (beyond the codec)
+    s = (np.abs(rng.normal(0, 0.02, 300)) / 127).astype(np.float16)
+    got = host(K.dequant("int8", dev(q), dev(s), 300, 4096))
+    want = ref.dequant_w8(q, s)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,Kd", [(1, 128), (37, 384), (4096, 11008)])
+def test_q4_0_repack_roundtrip_and_dequant_bit_exact(K, N, Kd):
+    say(f"q4_0 repack/unpack/dequant N={N} K={Kd}")
+    from aneforge_amd import _blob, workloads
+    rng = np.random.default_rng(11)
+    codes = rng.integers(0, 16, (N, Kd), dtype=np.uint8)
+    d = (np.abs(rng.normal(0, 0.02, (N, Kd // 32))) / 8).astype(np.float16)
+    blocks = workloads.q4_blocks_from_codes(codes, d)
+    qs, dd = K.q4_repack(dev(blocks), N, Kd)
+    hq, hd = _blob.q4_0_to_superblock(blocks, N, Kd)
+    assert np.array_equal(host(qs), hq) and np.array_equal(host(dd).view(np.uint16), hd.view(np.uint16))
+    back = host(K.q4_unpack(qs, dd, N, Kd))
+    assert np.array_equal(back, blocks)
+    got = host(K.dequant("q4_0", qs, dd, N, Kd))
+    want = ref.dequant_q4_0(blocks, N, Kd)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ----------------------------------------------------------------------------- linear layers
+def _w8(N, Kd, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-127, 128, (N, Kd), dtype=np.int8)
+    s = (np.abs(rng.normal(0, 0.02, N)) / 127).astype(np.float16)
+    return q, s
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 4096, 4096), (1, 1000, 1024), (3, 777, 4112), (8, 256, 11008),
+                                    (5, 6144, 4096), (2, 22016, 4096), (1, 4096, 11008)])
+def test_linear_int8(K, M, N, Kd):
+    say(f"linear int8 M={M} N={N} K={Kd}")
+    q, s = _w8(N, Kd, 20 + M)
+    x = np.random.default_rng(21).standard_normal((M, Kd)).astype(np.float16)
+    got = host(K.linear("int8", dev(q), dev(s), dev(x)))
+    want = ref.linear(x, ref.dequant_w8(q, s))
+    check_f16(got, want, what="int8 linear")
+
+
+def test_linear_int8_cfg0_seeded(K):
+    say("linear int8 cfg0 (seeded 4096x4096)")
+    from aneforge_amd import workloads
+    c = workloads.cfg0_gemv_w8()
+    got = host(K.linear("int8", dev(c["q"]), dev(c["s"]), dev(c["x"])))
+    check_f16(got, ref.linear(c["x"], ref.dequant_w8(c["q"], c["s"])), what="cfg0")
+
+
+def test_linear_int8_bias_residual_inplace(K):
+    say("linear int8 + bias + residual in place")
+    q, s = _w8(512, 1024, 22)
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((2, 1024)).astype(np.float16)
+    b = rng.standard_normal(512).astype(np.float16)
+    r = rng.standard_normal((2, 512)).astype(np.float16)
+    rd = dev(r)
+    K.linear("int8", dev(q), dev(s), dev(x), y=rd, bias=dev(b), residual=rd)
+    want = ref.r16(r.astype(np.float64) + ref.linear(x, ref.dequant_w8(q, s), b))
+    check_f16(host(rd), want, what="bias+residual")
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 11008, 4096), (1, 4096, 11008), (4, 11008, 4096), (4, 4096, 11008),
+                                    (8, 11008, 4096), (8, 4096, 11008), (3, 100, 384)])
+def test_linear_q4_0_cfg1(K, M, N, Kd):
+    say(f"linear q4_0 M={M} N={N} K={Kd}")
+    from aneforge_amd import workloads
+    c = workloads.cfg1_gemv_q4(N, Kd, M)
+    qs, d = K.q4_repack(dev(c["blocks"]), N, Kd)
+    got = host(K.linear("q4_0", qs, d, dev(c["x"])))
+    want = ref.linear(c["x"], ref.dequant_q4_0(c["blocks"], N, Kd))
+    check_f16(got, want, what="q4_0 linear")
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 32000, 4096), (2, 1000, 520)])
+def test_linear_f16_logits(K, M, N, Kd):
+    say(f"linear fp16 -> fp32 M={M} N={N} K={Kd}")
+    rng = np.random.default_rng(24)
+    w = rng.normal(0, 0.02, (N, Kd)).astype(np.float16)
+    x = rng.standard_normal((M, Kd)).astype(np.float16)
+    got = host(K.linear("fp16", dev(w), None, dev(x), out_f32=True))
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.abs(got - want).max() < 1e-4 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4_0", "fp16"])
+def test_linear_rms_prologue(K, fmt):
+    say(f"linear + rmsnorm prologue fmt={fmt}")
+    rng = np.random.default_rng(25)
+    M, N, Kd = 3, 1536, 4096
+    h = (rng.standard_normal((M, Kd)) * 2).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, Kd).astype(np.float16)
+    if fmt == "int8":
+        q, s = _w8(N, Kd, 26)
+        wd, sd, Wf = dev(q), dev(s), ref.dequant_w8(q, s)
+    elif fmt == "q4_0":
+        from aneforge_amd import workloads
+        c = workloads.cfg1_gemv_q4(N, Kd, 1, seed=26)
+        wd, sd = K.q4_repack(dev(c["blocks"]), N, Kd)
+        Wf = ref.dequant_q4_0(c["blocks"], N, Kd)
+    else:
+        Wf16 = rng.normal(0, 0.02, (N, Kd)).astype(np.float16)
+        wd, sd, Wf = dev(Wf16), None, Wf16.astype(np.float32)
+    got = host(K.linear_rms(fmt, wd, sd, dev(h), dev(g), 1e-5))
+    want = ref.linear(ref.rms_norm(h, g, 1e-5), Wf)
+    check_f16(got, want, what=f"rms+{fmt}")
+
+
+def test_linear_swiglu(K):
+    say("linear swiglu (gate/up interleaved) with norm")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(27)
+    M, F, Kd = 2, 1376, 4096
+    qg, sg = _w8(F, Kd, 28)
+    qu, su = _w8(F, Kd, 29)
+    h = rng.standard_normal((M, Kd)).astype(np.float16)
+    g = np.ones(Kd, np.float16)
+    w = _blob.interleave_rows(qg, qu)
+    s = _blob.interleave_rows(sg, su)
+    got = host(K.linear_swiglu("int8", dev(w), dev(s), dev(h), dev(g), 1e-5))
+    hn = ref.rms_norm(h, g, 1e-5)
+    gg = ref.linear(hn, ref.dequant_w8(qg, sg))
+    uu = ref.linear(hn, ref.dequant_w8(qu, su))
+    check_f16(got, ref.r16(ref.silu(gg) * uu), what="swiglu")
+
+
+@pytest.mark.parametrize("M,H,KV,dh,pos", [(1, 32, 8, 128, 2048), (2, 4, 2, 64, 5)])
+def test_qkv_rope_kv_fused(K, M, H, KV, dh, pos):
+    say(f"fused qkv+rope+kv write M={M} H={H} KV={KV} dh={dh} pos={pos}")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(30)
+    D = H * dh if H * dh >= 1024 else 1024
+    Mmax = pos + 4
+    qq, sq = _w8(H * dh, D, 31)
+    qk, sk = _w8(KV * dh, D, 32)
+    qv, sv = _w8(KV * dh, D, 33)
+    bias = rng.standard_normal(H * dh + 2 * KV * dh).astype(np.float16) * 0.1
+    permq, permk = _blob.rope_pair_order(H, dh), _blob.rope_pair_order(KV, dh)
+    w = np.concatenate([qq[permq], qk[permk], qv])
+    s = np.concatenate([sq[permq], sk[permk], sv])
+    bb = np.concatenate([bias[:H * dh][permq], bias[H * dh:H * dh + KV * dh][permk], bias[H * dh + KV * dh:]])
+    h = rng.standard_normal((M, D)).astype(np.float16)
+    g = rng.uniform(0.8, 1.2, D).astype(np.float16)
+    cos, sin = ref.rope_tables(Mmax, dh)
+    kc = torch.zeros((M, KV, Mmax, dh), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    posd = torch.tensor([pos + m for m in range(M)], dtype=torch.int32, device="cuda")
+    qout = torch.empty((M, H * dh), dtype=torch.float16, device="cuda")
+    K.qkv_rope_kv("int8", dev(w), dev(s), dev(h), dev(g), 1e-5, dev(bb), H * dh, KV * dh, dh, dev(cos), dev(sin),
+                  posd, qout, kc, vc)
+    hq, hk, hv = host(qout), host(kc), host(vc)
+    for m in range(M):
+        p = pos + m
+        xn = ref.rms_norm(h[m:m + 1], g, 1e-5)
+        qr = ref.rope(ref.linear(xn, ref.dequant_w8(qq, sq), bias[:H * dh]).reshape(H, dh), cos[p], sin[p])
+        kr = ref.rope(ref.linear(xn, ref.dequant_w8(qk, sk), bias[H * dh:H * dh + KV * dh]).reshape(KV, dh),
+                      cos[p], sin[p])
+        vr = ref.linear(xn, ref.dequant_w8(qv, sv), bias[H * dh + KV * dh:]).reshape(KV, dh)
+        check_f16(hq[m].reshape(H, dh), qr, what="q")
+        check_f16(hk[m, :, p], kr, what="k cache row")
+        check_f16(hv[m, :, p], vr, what="v cache row")
+        assert not hk[m, :, :p].any() and not hk[m, :, p + 1:].any()    # nothing else written
+
+
+# ----------------------------------------------------------------------------- attention
+@pytest.mark.parametrize("B,ctx", [(1, 512), (1, 2048), (1, 8192), (16, 512), (16, 2048), (16, 8192)])
+def test_decode_attn_cfg2(K, B, ctx):
+    say(f"decode attention cfg2 B={B} ctx={ctx}")
+    from aneforge_amd import workloads
+    c = workloads.cfg2_attn(ctx, B)
+    got = host(K.decode_attn(dev(c["q"]), dev(c["K"]), dev(c["V"]), ctx_len=ctx))
+    check_b = [0, B - 1] if B > 2 else list(range(B))
+    for b in check_b:
+        want = ref.attention(c["q"][b:b + 1, :, None, :], c["K"][b:b + 1], c["V"][b:b + 1])[0, :, 0]
+        check_f16(got[b], want, what=f"attn b={b}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,Mmax", [(4, 4, 64, 37), (8, 2, 128, 300), (16, 2, 64, 1000), (8, 1, 128, 5)])
+def test_decode_attn_device_positions(K, Hq, Hkv, D, Mmax):
+    say(f"decode attention pos-driven Hq={Hq} Hkv={Hkv} D={D} Mmax={Mmax}")
+    rng = np.random.default_rng(40)
+    B = 3
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    Kc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
+    Vc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
+    pos = np.array([0, Mmax // 2, Mmax - 1], np.int32)
+    got = host(K.decode_attn(dev(q), dev(Kc), dev(Vc), pos=dev(pos)))
+    want = ref.attention(q[:, :, None, :], Kc, Vc, lengths=pos + 1)[:, :, 0]
+    check_f16(got, want, what="attn pos")
+
+
+def test_decode_attn_mask_and_causal(K):
+    say("decode attention additive mask + causal alignment")
+    rng = np.random.default_rng(41)
+    Sq, Skv, H, D = 6, 6, 2, 64
+    q = rng.standard_normal((1, H, Sq, D)).astype(np.float16)
+    k = rng.standard_normal((1, H, Skv, D)).astype(np.float16)
+    v = rng.standard_normal((1, H, Skv, D)).astype(np.float16)
+    qd = dev(q)
+    # queries as the batch axis sharing one KV (af.sdpa layout [1, H, S, D])
+    o = torch.empty_like(qd)
+    K.decode_attn(qd, dev(k), dev(v), o=o, ctx_len=Skv, causal_off=0, q_strides=(D, Sq * D),
+                  kv_strides=(0, Skv * D), B=Sq, Hq=H)
+    mask = np.triu(np.full((Sq, Skv), -1e4), 1)
+    want = ref.attention(q, k, v, mask=None, exact=False) if False else None
+    want = np.stack([ref.attention(q[:, :, s:s + 1], k, v, lengths=[s + 1])[0, :, 0] for s in range(Sq)], 1)
+    check_f16(host(o)[0], want, what="causal")
+    m = rng.standard_normal((Sq, Skv)).astype(np.float16)
+    o2 = torch.empty_like(qd)
+    K.decode_attn(qd, dev(k), dev(v), o=o2, ctx_len=Skv, mask=dev(m), q_strides=(D, Sq * D),
+                  kv_strides=(0, Skv * D), B=Sq, Hq=H)
+    want2 = np.stack([ref.attention(q[:, :, s:s + 1], k, v, mask=m[s:s + 1])[0, :, 0] for s in range(Sq)], 1)
+    check_f16(host(o2)[0], want2, what="mask")
+    del mask
+
+
+# ----------------------------------------------------------------------------- small ops
+def test_rmsnorm_rope_embed_argmax(K):
+    say("rmsnorm / rope / embed / argmax")
+    rng = np.random.default_rng(50)
+    x = rng.standard_normal((3, 4096)).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, 4096).astype(np.float16)
+    check_f16(host(K.rmsnorm(dev(x), dev(g), 1e-5)), ref.rms_norm(x, g, 1e-5), what="rmsnorm")
+    cos, sin = ref.rope_tables(40, 128)
+    xr = rng.standard_normal((8, 128)).astype(np.float16)
+    got = host(K.rope(dev(xr), dev(cos), dev(sin), pos0=30, rows_per_pos=4))
+    want = np.concatenate([ref.rope(xr[:4], cos[30], sin[30]), ref.rope(xr[4:], cos[31], sin[31])])
+    check_f16(got, want, what="rope")
+    table = rng.standard_normal((100, 64)).astype(np.float16)
+    ids = np.array([5, 99, 0], np.int32)
+    assert np.array_equal(host(K.embed(dev(table), dev(ids))), table[ids])
+    lg = rng.standard_normal((2, 32000)).astype(np.float32)
+    lg[1, 7] = lg[1, 9] = 100.0                                   # tie -> lowest index
+    assert host(K.argmax(dev(lg))).tolist() == [int(np.argmax(lg[0])), 7]
+
+
+def test_greedy_advance(K):
+    say("greedy advance (argmax + hist + pos + embed)")
+    rng = np.random.default_rng(51)
+    V, D = 32000, 4096
+    lg = rng.standard_normal(V).astype(np.float32)
+    table = rng.standard_normal((V, D)).astype(np.float16)
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos = torch.tensor([10], dtype=torch.int32, device="cuda")
+    step = torch.tensor([2], dtype=torch.int32, device="cuda")
+    hist = torch.full((8,), -1, dtype=torch.int32, device="cuda")
+    h = torch.zeros((1, D), dtype=torch.float16, device="cuda")
+    K.greedy_advance(dev(lg), tok, pos, hist, step, dev(table), h)
+    t = int(np.argmax(lg))
+    assert host(tok)[0] == t and host(pos)[0] == 11 and host(step)[0] == 3 and host(hist)[2] == t
+    assert np.array_equal(host(h)[0], table[t])
+
+
+# ----------------------------------------------------------------------------- MoE
+def test_moe_topk_reference_ties(K):
+    say("moe top-k tie vectors")
+    rows = np.array([[0.2, 0.2, 0.2, 0.1, 0.1, 0.1, 0.05, 0.05],
+                     [0.3, 0.2, 0.2, 0.2, 0.05, 0.03, 0.01, 0.01],
+                     [0.1, 0.1, 0.1, 0.1, 0.1, 0.1, 0.2, 0.2],
+                     [0.4, 0.3, 0.1, 0.1, 0.05, 0.03, 0.01, 0.01]], np.float16)
+    # logits whose softmax reproduces the rows exactly up to fp16 rounding: log(p)
+    lg = np.log(rows.astype(np.float64)).astype(np.float32)
+    gate, sel, cnt, lst = K.moe_topk(dev(lg), 2, renorm=False)
+    sel = host(sel)
+    want = [[0, 1], [0, 1], [6, 7], [0, 1]]
+    assert [sorted(r) for r in sel.tolist()] == want
+    cnt = host(cnt)
+    assert cnt.tolist() == [3, 3, 0, 0, 0, 0, 1, 1]
+    lst = host(lst)
+    assert lst[0, :3].tolist() == [0, 2, 6] and lst[6, 0] == 4 and lst[7, 0] == 5
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "int8"])
+def test_moe_layer_sparse_dispatch(K, fmt):
+    say(f"moe layer E=8 k=2 T=16 D=512 F=768 fmt={fmt}")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(60)
+    E, k, T, D, F = 8, 2, 16, 512, 768
+    router = rng.normal(0, 0.2, (E, D)).astype(np.float16)
+    h = rng.standard_normal((T, D)).astype(np.float16)
+    g = np.ones(D, np.float16)
+    Wg = rng.normal(0, 0.05, (E, F, D)).astype(np.float32)
+    Wu = rng.normal(0, 0.05, (E, F, D)).astype(np.float32)
+    Wd = rng.normal(0, 0.05, (E, D, F)).astype(np.float32)
+    if fmt == "q4_0":
+        gu, dn, Gf, Uf, Df = [], [], [], [], []
+        for e in range(E):
+            bg, bu, bd = _blob.quantize_q4_0(Wg[e]), _blob.quantize_q4_0(Wu[e]), _blob.quantize_q4_0(Wd[e])
+            Gf.append(ref.dequant_q4_0(bg, F, D)); Uf.append(ref.dequant_q4_0(bu, F, D)); Df.append(ref.dequant_q4_0(bd, D, F))
+            qg, dg = _blob.q4_0_to_superblock(bg, F, D)
+            qu, du = _blob.q4_0_to_superblock(bu, F, D)
+            gu.append((_blob.interleave_rows(qg, qu), _blob.interleave_rows(dg, du)))
+            dn.append(_blob.q4_0_to_superblock(bd, D, F))
+        wgu = np.stack([a for a, _ in gu]); sgu = np.stack([b for _, b in gu])
+        wdn = np.stack([a for a, _ in dn]); sdn = np.stack([b for _, b in dn])
+    else:
+        gu, dn, Gf, Uf, Df = [], [], [], [], []
+        for e in range(E):
+            qg, sg = _blob.quantize_per_row(Wg[e]); qu, su = _blob.quantize_per_row(Wu[e]); qd, sd = _blob.quantize_per_row(Wd[e])
+            Gf.append(ref.dequant_w8(qg, sg)); Uf.append(ref.dequant_w8(qu, su)); Df.append(ref.dequant_w8(qd, sd))
+            gu.append((_blob.interleave_rows(qg, qu), _blob.interleave_rows(sg, su)))
+            dn.append((qd, sd))
+        wgu = np.stack([a for a, _ in gu]); sgu = np.stack([b for _, b in gu])
+        wdn = np.stack([a for a, _ in dn]); sdn = np.stack([b for _, b in dn])
+    hd = dev(h)
+    hn = K.rmsnorm(hd, dev(g), 1e-5)
+    logits = K.linear("fp16", dev(router), None, hn, out_f32=True) if T <= 8 else torch.cat(
+        [K.linear("fp16", dev(router), None, hn[i:i + 8], out_f32=True) for i in range(0, T, 8)])
+    gate, sel, cnt, lst = K.moe_topk(logits, k, renorm=True)
+    act = K.moe_gateup(fmt, dev(wgu), dev(sgu), hn, k, E, F, cnt, lst)
+    y = K.moe_down(fmt, dev(wdn), dev(sdn), act, T, k, E, F, D, cnt, lst)
+    out = host(K.moe_combine(hd, y, gate))
+    want, wgate, chosen = ref.moe_layer(h, g, router, Gf, Uf, Df, k, True, 1e-5)
+    assert [sorted(r) for r in host(sel).tolist()] == chosen
+    check_f16(out, want, what="moe")

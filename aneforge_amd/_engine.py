@@ -1,0 +1,418 @@
+"""Device-resident decode engine: packed weights, per-layer executors, and the step graphs.
+
+The reference builds a per-chunk ANE program per decode length and round-trips the hidden
+state through the host for every chunk of every token (aneforge/llm.py:435-478, :584-606).
+Here the whole step runs on the GPU:
+
+  per layer:  afx_qkv_rope_kv   RMSNorm + fused [q|k|v] GEMV + RoPE + KV-cache row write
+              afx_decode_attn   split-KV GQA attention over the resident cache (pos from device)
+              afx_linear        o-proj GEMV + residual add (in place on h)
+              afx_linear_swiglu RMSNorm + gate/up GEMV + SwiGLU
+              afx_linear        down GEMV + residual add
+  head:       afx_linear_rms    final RMSNorm + fp16 lm_head -> fp32 logits
+  advance:    afx_decode_advance next token (prompt token or greedy argmax), pos/step, embedding
+
+Position, step counter, prompt tokens and the generated-token history live in device memory,
+so one step is captured once as a HIP graph and replayed for every token with no host sync.
+
+Weights are packed once (compress=None -> fp16, "int8" -> per-row int8, "q4_0" -> GGUF Q4_0
+in the superblock layout); the reference's other encodings ("blockwise", "int4" LUT) are
+reconstructed exactly as the reference's constexpr ops would and streamed as fp16."""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _blob, _hip
+from . import _kernels as K
+
+F16 = np.float16
+
+
+# ----------------------------------------------------------------------------- packed weights
+@dataclass
+class Linear:
+    """A weight [N, K] resident on the device in one of the kernel formats."""
+    fmt: str                          # "int8" | "q4_0" | "fp16"
+    w: torch.Tensor
+    scale: torch.Tensor | None
+    N: int
+    K: int
+    bias: torch.Tensor | None = None
+
+    @property
+    def nbytes(self) -> int:
+        n = self.w.numel() * self.w.element_size()
+        if self.scale is not None:
+            n += self.scale.numel() * self.scale.element_size()
+        return n
+
+    def __call__(self, x, y=None, residual=None, out_f32=False):
+        return K.linear(self.fmt, self.w, self.scale, x, y=y, bias=self.bias, residual=residual, out_f32=out_f32)
+
+
+@dataclass
+class QuantizedWeight:
+    """Weights that arrive already encoded (GGUF Q4_0 bytes, int8 codes + row scales): packing
+    keeps the codes bit-for-bit instead of round-tripping through float.
+      fmt "int8":      codes int8 [N, K], scale fp16 [N]
+      fmt "q4_0":      codes uint8 [N, K/2] superblock layout, scale fp16 [N, K/32]
+      fmt "q4_0_gguf": codes uint8 [N, K/32*18] GGUF block bytes, scale None"""
+    fmt: str
+    codes: np.ndarray
+    scale: np.ndarray | None
+    shape: tuple
+
+    def rows(self, idx) -> "QuantizedWeight":
+        idx = np.asarray(idx)
+        return QuantizedWeight(self.fmt, self.codes[idx], None if self.scale is None else self.scale[idx],
+                               (len(idx), self.shape[1]))
+
+    def to_superblock(self) -> "QuantizedWeight":
+        if self.fmt != "q4_0_gguf":
+            return self
+        qs, d = _blob.q4_0_to_superblock(self.codes, *self.shape)
+        return QuantizedWeight("q4_0", qs, d, self.shape)
+
+    def dequant(self) -> np.ndarray:
+        """Host fp32 reconstruction (exact: code * scale in fp32)."""
+        N, Kd = self.shape
+        if self.fmt == "int8":
+            return self.codes.astype(np.float32) * self.scale.astype(np.float32)[:, None]
+        q = self if self.fmt == "q4_0" else self.to_superblock()
+        blocks = _blob.superblock_to_q4_0(q.codes, q.scale, N, Kd)
+        codes, d = _blob.q4_0_codes(blocks, N, Kd)
+        vals = codes.astype(np.float32) - 8.0
+        return (vals.reshape(N, Kd // 32, 32) * d.astype(np.float32)[:, :, None]).reshape(N, Kd)
+
+
+def _rows(W, idx):
+    return W.rows(idx) if isinstance(W, QuantizedWeight) else np.asarray(W, np.float32)[np.asarray(idx)]
+
+
+def _cat(parts):
+    if all(isinstance(p, QuantizedWeight) for p in parts):
+        ps = [p.to_superblock() for p in parts]
+        if len({p.fmt for p in ps}) != 1:
+            raise ValueError("cannot fuse weights of different encodings")
+        sc = None if ps[0].scale is None else np.concatenate([p.scale for p in ps])
+        return QuantizedWeight(ps[0].fmt, np.concatenate([p.codes for p in ps]), sc,
+                               (sum(p.shape[0] for p in ps), ps[0].shape[1]))
+    if any(isinstance(p, QuantizedWeight) for p in parts):
+        raise ValueError("cannot fuse quantized and float weights")
+    return np.concatenate([np.asarray(p, np.float32) for p in parts])
+
+
+def _interleave(a, b):
+    if isinstance(a, QuantizedWeight):
+        a, b = a.to_superblock(), b.to_superblock()
+        sc = None if a.scale is None else _blob.interleave_rows(a.scale, b.scale)
+        return QuantizedWeight(a.fmt, _blob.interleave_rows(a.codes, b.codes), sc, (2 * a.shape[0], a.shape[1]))
+    return _blob.interleave_rows(np.asarray(a, np.float32), np.asarray(b, np.float32))
+
+
+def _shape(W):
+    return W.shape if isinstance(W, QuantizedWeight) else np.asarray(W).shape
+
+
+def _to_dev(a, dtype=None) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def encode(W: np.ndarray, compress: str | None):
+    """Host encoding of a float weight [N, K] -> (fmt, codes, scale) following `compress=`
+    (aneforge/_compile.py:112-188: per-row int8; blockwise and LUT4 are reconstructed to fp16).
+    Already-encoded weights keep their codes."""
+    if isinstance(W, QuantizedWeight):
+        q = W.to_superblock()
+        return q.fmt, q.codes, q.scale
+    W = np.asarray(W, np.float32)
+    if W.ndim != 2:
+        raise ValueError(f"weights must be 2-D [out, in], got {W.shape}")
+    if compress in (None, "fp16", "sparse"):
+        return "fp16", W.astype(F16), None
+    if compress in ("int8", "auto"):
+        q, s = _blob.quantize_per_row(W)
+        return "int8", q, s
+    if compress in ("q4_0", "gguf_q4_0"):
+        N, Kd = W.shape
+        if Kd % 128:
+            raise ValueError(f"q4_0 needs in_features % 128 == 0 (got {Kd})")
+        qs, d = _blob.q4_0_to_superblock(_blob.quantize_q4_0(W), N, Kd)
+        return "q4_0", qs, d
+    if compress == "blockwise":
+        q, s, bs = _blob.quantize_blockwise(W, 32)
+        N, Kd = W.shape
+        rec = (q.reshape(N, Kd // bs, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(N, Kd)
+        return "fp16", rec.astype(F16), None
+    if compress == "int4":
+        packed, cb = _blob.palettize_lut4(W)
+        idx = np.empty((W.shape[0], packed.shape[1] * 2), np.uint8)
+        idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
+        rec = cb.astype(np.float32)[idx[:, :W.shape[1]]]
+        return "fp16", rec.astype(F16), None
+    raise ValueError(f"unknown compress={compress!r}")
+
+
+def pack_linear(W, compress, bias=None) -> Linear:
+    fmt, w, s = encode(W, compress)
+    N, Kd = _shape(W)
+    return Linear(fmt, _to_dev(w), None if s is None else _to_dev(s), N, Kd,
+                  None if bias is None else _to_dev(np.asarray(bias, np.float32).astype(F16)))
+
+
+def linear_from_q4_0_blocks(blocks, N: int, Kd: int, bias=None) -> Linear:
+    """Device repack of GGUF Q4_0 bytes (kept 4-bit; the reference dequantised them on the host)."""
+    b = _to_dev(np.asarray(blocks, np.uint8).reshape(N, -1))
+    qs, d = K.q4_repack(b, N, Kd)
+    return Linear("q4_0", qs, d, N, Kd, None if bias is None else _to_dev(np.asarray(bias, F16)))
+
+
+def _gamma(g, D) -> torch.Tensor:
+    g = np.asarray(g, np.float32).reshape(-1)
+    if g.shape[0] != D:
+        raise ValueError(f"norm weight has {g.shape[0]} entries, expected {D}")
+    return _to_dev(g.astype(F16))
+
+
+# ----------------------------------------------------------------------------- layer executors
+class AttentionDecode:
+    """Decode token mixer (aneforge/llm.py:214-237): RMSNorm -> QKV -> RoPE -> cache write ->
+    GQA attention over positions [0, pos] -> o-proj + residual."""
+
+    def __init__(self, lw: dict, cfg, ls, compress):
+        if cfg.norm_type != "rms":
+            raise NotImplementedError("the device decode engine implements RMSNorm decoders (norm_type='rms')")
+        if ls.qk_norm:
+            raise NotImplementedError("QK-norm (Qwen3) is not fused on the device decode path yet")
+        if cfg.rope and (cfg.rotary_dim not in (0, cfg.dh) or cfg.rope_interleaved):
+            raise NotImplementedError("partial / interleaved RoPE is not fused on the device decode path yet")
+        H, KV, dh, D = cfg.n_heads, cfg.n_kv_heads, cfg.dh, cfg.dim
+        self.H, self.KV, self.dh, self.eps, self.rope = H, KV, dh, float(cfg.norm_eps), bool(cfg.rope)
+        pq = _blob.rope_pair_order(H, dh) if self.rope else np.arange(H * dh)
+        pk = _blob.rope_pair_order(KV, dh) if self.rope else np.arange(KV * dh)
+        W = _cat([_rows(lw["wq"], pq), _rows(lw["wk"], pk), lw["wv"]])
+        bias = None
+        if any(k in lw for k in ("q_bias", "k_bias", "v_bias")):
+            bq = np.asarray(lw.get("q_bias", np.zeros(H * dh)), np.float32)
+            bk = np.asarray(lw.get("k_bias", np.zeros(KV * dh)), np.float32)
+            bv = np.asarray(lw.get("v_bias", np.zeros(KV * dh)), np.float32)
+            bias = np.concatenate([bq[pq], bk[pk], bv])
+        self.qkv = pack_linear(W, compress, bias)
+        self.wo = pack_linear(lw["wo"], compress, lw.get("o_bias"))
+        self.norm = _gamma(lw["attn_norm"], D)
+        self.kc = self.vc = None
+
+    @classmethod
+    def from_linears(cls, cfg, qkv: "Linear", wo: "Linear", norm: torch.Tensor, rope: bool = True):
+        """Build from already-packed device weights (qkv rows in rope-pair order for q and k)."""
+        self = cls.__new__(cls)
+        self.H, self.KV, self.dh, self.eps, self.rope = cfg.n_heads, cfg.n_kv_heads, cfg.dh, float(cfg.norm_eps), rope
+        self.qkv, self.wo, self.norm = qkv, wo, norm
+        self.kc = self.vc = None
+        return self
+
+    def bind(self, eng):
+        shape = (eng.B, self.KV, eng.M, self.dh)
+        self.kc = torch.zeros(shape, dtype=torch.float16, device="cuda")
+        self.vc = torch.zeros(shape, dtype=torch.float16, device="cuda")
+
+    def reset(self, eng):
+        self.kc.zero_()
+        self.vc.zero_()
+
+    def state(self):
+        return [self.kc, self.vc]
+
+    def enqueue(self, eng):
+        B, H, dh = eng.B, self.H, self.dh
+        q = eng.q[:, :H * dh]
+        K.qkv_rope_kv(self.qkv.fmt, self.qkv.w, self.qkv.scale, eng.h, self.norm, self.eps, self.qkv.bias,
+                      H * dh, self.KV * dh, dh, eng.cos, eng.sin, eng.pos, q, self.kc, self.vc, rope=self.rope)
+        K.decode_attn(q.view(B, H, dh), self.kc, self.vc, o=eng.a[:, :H * dh].view(B, H, dh), pos=eng.pos,
+                      ws=eng.attn_ws)
+        K.linear(self.wo.fmt, self.wo.w, self.wo.scale, eng.a[:, :H * dh], y=eng.h, bias=self.wo.bias,
+                 residual=eng.h)
+
+    @property
+    def nbytes(self):
+        return self.qkv.nbytes + self.wo.nbytes + self.norm.numel() * 2
+
+
+class SwiGLUDecode:
+    """SwiGLU MLP with residual (aneforge/llm.py:171-175): h + down(silu(gate(n)) * up(n)), n = rms(h)."""
+
+    def __init__(self, lw: dict, cfg, ls, compress):
+        D = cfg.dim
+        self.F = _shape(lw["wgate"])[0]
+        self.eps = float(cfg.norm_eps)
+        self.gu = pack_linear(_interleave(lw["wgate"], lw["wup"]), compress)
+        self.down = pack_linear(lw["wdown"], compress)
+        self.norm = _gamma(lw["mlp_norm"], D)
+
+    @classmethod
+    def from_linears(cls, cfg, gu: "Linear", down: "Linear", norm: torch.Tensor):
+        """Build from already-packed device weights (gate/up rows interleaved)."""
+        self = cls.__new__(cls)
+        self.F, self.eps, self.gu, self.down, self.norm = gu.N // 2, float(cfg.norm_eps), gu, down, norm
+        return self
+
+    def bind(self, eng):
+        pass
+
+    def reset(self, eng):
+        pass
+
+    def state(self):
+        return []
+
+    def enqueue(self, eng):
+        act = eng.act[:, :self.F]
+        K.linear_swiglu(self.gu.fmt, self.gu.w, self.gu.scale, eng.h, self.norm, self.eps, act=act)
+        K.linear(self.down.fmt, self.down.w, self.down.scale, act, y=eng.h, residual=eng.h)
+
+    @property
+    def nbytes(self):
+        return self.gu.nbytes + self.down.nbytes + self.norm.numel() * 2
+
+
+# ----------------------------------------------------------------------------- the engine
+class _Graph:
+    def __init__(self, stream, fn):
+        self.stream = stream
+        self.exec = ctypes.c_void_p()
+        with torch.cuda.stream(stream):
+            _hip.call("afx_graph_begin", stream.cuda_stream)
+            try:
+                fn()
+            finally:
+                _hip.call("afx_graph_end", stream.cuda_stream, ctypes.byref(self.exec))
+
+    def launch(self):
+        _hip.call("afx_graph_launch", self.exec, self.stream.cuda_stream)
+
+    def close(self):
+        if self.exec:
+            _hip.call("afx_graph_destroy", self.exec)
+            self.exec = ctypes.c_void_p()
+
+
+class DecodeEngine:
+    """All layers + head + advance for one sequence (B=1) with a resident cache of M rows."""
+
+    def __init__(self, cfg, layers, embed: torch.Tensor, head: Linear, final_norm: torch.Tensor, M: int,
+                 rope_tables=None):
+        self.cfg, self.layers, self.embed, self.head, self.final_norm = cfg, layers, embed, head, final_norm
+        self.M, self.B = int(M), 1
+        D, H, dh = cfg.dim, cfg.n_heads, cfg.dh
+        self.V = head.N
+        dev = "cuda"
+        self.h = torch.zeros((1, D), dtype=torch.float16, device=dev)
+        self.q = torch.zeros((1, H * dh), dtype=torch.float16, device=dev)
+        self.a = torch.zeros((1, H * dh), dtype=torch.float16, device=dev)
+        fmax = max([getattr(m, "F", 0) for _, m in layers] + [8])
+        self.act = torch.zeros((1, fmax), dtype=torch.float16, device=dev)
+        self.logits = torch.zeros((1, self.V), dtype=torch.float32, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.tok = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.step = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.n_forced = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.hist = torch.zeros(self.M + 8, dtype=torch.int32, device=dev)
+        self.forced = torch.zeros(self.M + 8, dtype=torch.int32, device=dev)
+        if rope_tables is None:
+            from .llm import rope_tables as _rt
+            rope_tables = _rt(self.M, dh, cfg.rope_base, cfg.rotary_dim, cfg.rope_interleaved, cfg.rope_scaling)
+        self.cos, self.sin = _to_dev(rope_tables[0]), _to_dev(rope_tables[1])
+        self.attn_ws = torch.zeros(K.attn_ws_bytes(1, H, cfg.n_kv_heads, dh, self.M) // 4 + 1,
+                                   dtype=torch.float32, device=dev)
+        for mixer, mlp in layers:
+            mixer.bind(self)
+            mlp.bind(self)
+        self.stream = torch.cuda.Stream()
+        self._g_fwd = self._g_dec = None
+
+    # -- enqueue helpers (on the current stream) --
+    def enqueue_layers(self):
+        for mixer, mlp in self.layers:
+            mixer.enqueue(self)
+            mlp.enqueue(self)
+
+    def enqueue_head(self):
+        K.linear_rms(self.head.fmt, self.head.w, self.head.scale, self.h, self.final_norm, self.cfg.norm_eps,
+                     y=self.logits, out_f32=True)
+
+    def enqueue_advance(self, with_logits: bool):
+        K.decode_advance(self.logits if with_logits else None, self.tok, self.pos, self.hist, self.step,
+                         self.embed, self.h, self.forced, self.n_forced)
+
+    def _graphs(self):
+        if self._g_dec is None:
+            self._g_fwd = _Graph(self.stream, lambda: (self.enqueue_layers(), self.enqueue_advance(False)))
+            self._g_dec = _Graph(self.stream, lambda: (self.enqueue_layers(), self.enqueue_head(),
+                                                      self.enqueue_advance(True)))
+        return self._g_fwd, self._g_dec
+
+    # -- host control --
+    def reset(self, prompt, pos0: int = 0, zero_state: bool = True):
+        """Start a sequence: zero the resident state, queue prompt[1:] as forced tokens, h = embed[prompt[0]]."""
+        prompt = [int(t) for t in prompt]
+        if not prompt:
+            raise ValueError("empty prompt")
+        if len(prompt) + pos0 > self.M:
+            raise ValueError(f"prompt of {len(prompt)} tokens does not fit the {self.M}-row cache")
+        with torch.cuda.stream(self.stream):
+            if zero_state:
+                for mixer, mlp in self.layers:
+                    mixer.reset(self)
+                    mlp.reset(self)
+            f = torch.tensor(prompt[1:] + [0], dtype=torch.int32)
+            self.forced[:len(f)].copy_(f, non_blocking=False)
+            self.n_forced.fill_(len(prompt) - 1)
+            self.step.zero_()
+            self.pos.fill_(pos0)
+            K.embed(self.embed, torch.tensor(prompt[:1], dtype=torch.int32, device="cuda"), out=self.h)
+
+    def run(self, n_prefill: int, n_decode: int, graph: bool = True):
+        """Enqueue n_prefill forced steps then n_decode greedy steps (no host sync)."""
+        if graph:
+            g_fwd, g_dec = self._graphs()
+            for _ in range(n_prefill):
+                g_fwd.launch()
+            for _ in range(n_decode):
+                g_dec.launch()
+        else:
+            with torch.cuda.stream(self.stream):
+                for _ in range(n_prefill):
+                    self.enqueue_layers()
+                    self.enqueue_advance(False)
+                for _ in range(n_decode):
+                    self.enqueue_layers()
+                    self.enqueue_head()
+                    self.enqueue_advance(True)
+
+    def sync(self):
+        self.stream.synchronize()
+
+    def history(self, start: int, count: int) -> list[int]:
+        self.sync()
+        return self.hist[start:start + count].cpu().tolist()
+
+    def logits_host(self) -> np.ndarray:
+        self.sync()
+        return self.logits[0].cpu().numpy()
+
+    def close(self):
+        for g in (self._g_fwd, self._g_dec):
+            if g is not None:
+                g.close()
+        self._g_fwd = self._g_dec = None
+
+    @property
+    def weight_bytes(self) -> int:
+        return sum(m.nbytes + p.nbytes for m, p in self.layers) + self.head.nbytes

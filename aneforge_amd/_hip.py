@@ -52,7 +52,7 @@ SIGNATURES: dict[str, tuple] = {
     "afx_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _i, _i, _i, _vp]),
     "afx_rope": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp]),
     "afx_embed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
-    "afx_greedy_advance": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp]),
+    "afx_decode_advance": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp]),
     "afx_argmax": (_i, [_vp, _i, _i, _vp, _vp]),
     "afx_fill_i32": (_i, [_vp, _i, _i, _vp]),
     "afx_fill_f16": (_i, [_vp, _ll, _f, _vp]),

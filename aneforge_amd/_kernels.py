@@ -143,12 +143,12 @@ def decode_attn(q, k, v, o=None, ctx_len=None, pos=None, scale=None, mask=None, 
     kbs, khs = kv_strides if kv_strides else (k.stride(0), k.stride(1))
     need = attn_ws_bytes(B, Hq, Hkv, D, Mmax, nstep_hint)
     if ws is None or ws.numel() * ws.element_size() < need:
-        ws = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
+        ws = torch.zeros(need // 4 + 1, dtype=torch.float32, device=q.device)   # counters start at 0
     scale = (1.0 / D ** 0.5) if scale is None else float(scale)
     _hip.call("afx_decode_attn", P(q), P(k), P(v), P(o), qbs, qhs, kbs, khs, B, Hq, Hkv, D,
               int(ctx_len if ctx_len is not None else Mmax), P(pos), Mmax, P(mask),
               mask.stride(0) if mask is not None else 0, int(causal_off), scale, P(ws),
-              ws.numel() * ws.element_size(), nstep_hint, stream())
+              need, nstep_hint, stream())
     return o
 
 
@@ -181,11 +181,12 @@ def embed(table, ids, out=None):
     return out
 
 
-def greedy_advance(logits, tok, pos, hist, step, embed_table=None, h=None):
-    V = logits.shape[-1]
-    D = embed_table.shape[1] if embed_table is not None else 0
-    _hip.call("afx_greedy_advance", P(logits), V, P(tok), P(pos), P(hist), hist.numel() if hist is not None else 0,
-              P(step), P(embed_table), P(h), D, stream())
+def decode_advance(logits, tok, pos, hist, step, embed_table=None, h=None, forced=None, n_forced=None):
+    """Next token (forced prompt token or greedy argmax) + bookkeeping + embedding gather."""
+    V = logits.shape[-1] if logits is not None else 0
+    vocab, D = (embed_table.shape if embed_table is not None else (V, 0))
+    _hip.call("afx_decode_advance", P(logits), V, P(forced), P(n_forced), P(tok), P(pos), P(hist),
+              hist.numel() if hist is not None else 0, P(step), P(embed_table), P(h), D, vocab, stream())
 
 
 def argmax(x, out=None):

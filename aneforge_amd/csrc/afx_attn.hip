@@ -14,7 +14,10 @@
 // issues all its K and V loads before any math.  Scores stay in registers (two-pass
 // softmax inside the chunk), P@V accumulates in fp32.  Output: (m, l, o[D]) per
 // (b, h, split) in a caller-provided fp32 workspace.
-// Kernel 2 (combine): rescales and sums the split partials, writes fp16.
+// The last workgroup to finish a (b, kvh) group (agent-scope fence + arrival counter, which it
+// resets, so graph replays need no memset) rescales and sums the split partials and writes
+// the fp16 output: one launch per call.  The workspace's counter tail must be zero before the
+// first call.
 #include "afx_common.h"
 
 namespace afx {
@@ -26,7 +29,8 @@ struct AttnArgs {
   half_t* o;         // same strides as q
   const half_t* mask;  // optional additive mask [B][mask_bs] over positions
   const int* pos;      // optional: ctx length of sequence b = pos[b] + 1 (device)
-  float* ws;           // [B][Hq][nsplit][D+2]
+  float* ws;           // [B][Hq][nsplit][D+2] split partials
+  int* counters;       // [B][Hkv] arrival counters (zero before first use; reset by the last arrival)
   long long q_bs, q_hs, kv_bs, kv_hs;
   long long mask_bs;
   int B, Hq, Hkv, L, Mmax, chunk, nsplit, causal_off;  // causal_off < 0: no causal masking
@@ -177,24 +181,75 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       w[1] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
     }
   }
-}
 
-template <int D>
-__global__ __launch_bounds__(D) void attn_combine_kernel(AttnArgs a) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int L = seq_len(a, b);
-  const int ns = (L + a.chunk - 1) / a.chunk;
-  const float* w = a.ws + ((size_t)b * a.Hq + h) * a.nsplit * (D + 2);
-  float m = -INFINITY;
-  for (int s = 0; s < ns; ++s) m = fmaxf(m, w[s * (D + 2)]);
-  float num = 0.0f, den = 0.0f;
-  for (int s = 0; s < ns; ++s) {
-    const float* ws = w + s * (D + 2);
-    const float f = exp2f(ws[0] - m);
-    den = __builtin_fmaf(f, ws[1], den);
-    num = __builtin_fmaf(f, ws[2 + d], num);
+  // ---- the last workgroup of this (b, kvh) merges all split partials (no second launch) ----
+  const int ns = (L + C - 1) / C;            // splits that ran for this sequence
+  __shared__ int s_last;
+  __threadfence();                           // release this workgroup's partials (agent scope)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* ctr = a.counters + (size_t)b * a.Hkv + kvh;
+    const int prev = atomicAdd(ctr, 1);
+    s_last = prev == ns - 1;
+    if (s_last) atomicExch(ctr, 0);          // every split has arrived: reset for the next launch
   }
-  a.o[(size_t)b * a.q_bs + (size_t)h * a.q_hs + d] = (half_t)(num / den);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();                           // acquire the other workgroups' partials
+  __shared__ float s_scale[G][64];
+  __shared__ float s_den[G];
+  // per head: global max over splits, then per-split weights exp2(m_s - M) (up to 64 per pass)
+  for (int g = 0; g < G; ++g) {
+    const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2);
+    float m = -INFINITY;
+    for (int s2 = threadIdx.x; s2 < ns; s2 += 256) m = fmaxf(m, __builtin_nontemporal_load(base + (size_t)s2 * (D + 2)));
+    m = wave_max(m);
+    if (lane == 0) red_m[wave][g] = m;
+  }
+  __syncthreads();
+  float den_part[G];
+  for (int g = 0; g < G; ++g) {
+    const float M = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
+    const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2);
+    float den = 0.0f;
+    for (int s2 = threadIdx.x; s2 < ns; s2 += 256) {
+      const float* ws = base + (size_t)s2 * (D + 2);
+      den += exp2f(__builtin_nontemporal_load(ws) - M) * __builtin_nontemporal_load(ws + 1);
+    }
+    den_part[g] = wave_sum(den);
+  }
+  __syncthreads();
+  if (lane == 0)
+    for (int g = 0; g < G; ++g) red_l[wave][g] = den_part[g];
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    s_den[g] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
+  }
+  __syncthreads();
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    const int nc = ns - s0 < 64 ? ns - s0 : 64;
+    for (int idx = threadIdx.x; idx < G * 64; idx += 256) {
+      const int g = idx >> 6, j = idx & 63;
+      const float M = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
+      const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2);
+      s_scale[g][j] = j < nc ? exp2f(__builtin_nontemporal_load(base + (size_t)(s0 + j) * (D + 2)) - M) : 0.0f;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+      const int g = idx / D, d = idx - g * D;
+      const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2) + 2 + d;
+      float num = s0 == 0 ? 0.0f : red_o[0][g][d];
+#pragma unroll 8
+      for (int j = 0; j < nc; ++j) num = __builtin_fmaf(s_scale[g][j], __builtin_nontemporal_load(base + (size_t)(s0 + j) * (D + 2)), num);
+      red_o[0][g][d] = num;
+    }
+    __syncthreads();
+  }
+  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx - g * D;
+    a.o[(size_t)b * a.q_bs + (size_t)(kvh * G + g) * a.q_hs + d] = (half_t)(red_o[0][g][d] / s_den[g]);
+  }
 }
 
 typedef void (*attn_fn)(AttnArgs);
@@ -255,7 +310,7 @@ long long afx_decode_attn_ws_bytes(int B, int Hq, int Hkv, int D, int max_len, i
   const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
   const int chunk = ns * 4 * (512 / D);
   const long long nsplit = (max_len + chunk - 1) / chunk;
-  return (long long)B * Hq * nsplit * (D + 2) * 4;
+  return (long long)B * Hq * nsplit * (D + 2) * 4 + (long long)B * Hkv * 4;
 }
 
 // q/o: element (b, h, d) at b*q_bs + h*q_hs + d.  K/V: (b, kvh, p, d) at b*kv_bs + kvh*kv_hs + p*D + d.
@@ -286,15 +341,10 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
   a.chunk = ns * 4 * (512 / D);
   a.nsplit = (max_len + a.chunk - 1) / a.chunk;
+  a.counters = (int*)((char*)ws + need - (long long)B * Hkv * 4);
   attn_fn fn = D == 64 ? pick_g<64>(G, ns) : pick_g<128>(G, ns);
   hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
-  int rc = check_launch("afx_decode_attn(partial)");
-  if (rc) return rc;
-  if (D == 64)
-    hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(Hq, B), dim3(64), 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(Hq, B), dim3(128), 0, (hipStream_t)stream, a);
-  return check_launch("afx_decode_attn(combine)");
+  return check_launch("afx_decode_attn");
 }
 
 }  // extern "C"

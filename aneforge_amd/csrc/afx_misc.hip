@@ -52,41 +52,54 @@ __global__ void embed_kernel(const half_t* __restrict__ table, const int* __rest
   for (int i = threadIdx.x; i < D / 8; i += blockDim.x) dst[i] = src[i];
 }
 
-// ---- greedy advance for a device-resident decode loop ----
-// token = argmax(logits) (lowest index on ties, like np.argmax), then
-// hist[*step] = token, ++*step, ++*pos, h = embed[token].  One workgroup.
-__global__ __launch_bounds__(1024) void greedy_advance_kernel(
-    const float* __restrict__ logits, int V, int* __restrict__ tok, int* __restrict__ pos,
-    int* __restrict__ hist, int hist_cap, int* __restrict__ step, const half_t* __restrict__ embed,
-    half_t* __restrict__ h, int D) {
+// ---- one step of the device-resident decode loop ----
+// The next token is forced[*step] while *step < *n_forced (prompt tokens, token-by-token
+// prefill), else argmax(logits) (lowest index on ties, like np.argmax; greedy _sample).  Then
+// hist[*step] = token, ++*step, ++*pos, h = embed[token].  One workgroup; every input that
+// changes between steps lives in device memory, so the step replays as a captured graph.
+__global__ __launch_bounds__(1024) void decode_advance_kernel(
+    const float* __restrict__ logits, int V, const int* __restrict__ forced, const int* __restrict__ n_forced,
+    int* __restrict__ tok, int* __restrict__ pos, int* __restrict__ hist, int hist_cap, int* __restrict__ step,
+    const half_t* __restrict__ embed, half_t* __restrict__ h, int D, int vocab) {
   __shared__ float bv[16];
   __shared__ int bi[16];
   __shared__ int chosen;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  float best = -INFINITY;
-  int besti = 0x7fffffff;
-  for (int i = t; i < V; i += blockDim.x) {
-    const float v = logits[i];
-    if (v > best || (v == best && i < besti)) { best = v; besti = i; }
-  }
+  const int s = step[0];
+  const bool use_forced = forced && n_forced && s < n_forced[0];
+  if (!use_forced && logits) {
+    float best = -INFINITY;
+    int besti = 0x7fffffff;
+    for (int i = t; i < V; i += blockDim.x) {
+      const float v = logits[i];
+      if (v > best || (v == best && i < besti)) { best = v; besti = i; }
+    }
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(best, m, 64);
-    const int oi = __shfl_xor(besti, m, 64);
-    if (ov > best || (ov == best && oi < besti)) { best = ov; besti = oi; }
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(best, m, 64);
+      const int oi = __shfl_xor(besti, m, 64);
+      if (ov > best || (ov == best && oi < besti)) { best = ov; besti = oi; }
+    }
+    if (lane == 0) { bv[wave] = best; bi[wave] = besti; }
   }
-  if (lane == 0) { bv[wave] = best; bi[wave] = besti; }
   __syncthreads();
   if (t == 0) {
-    const int nw = blockDim.x >> 6;
-    float b = bv[0];
-    int bidx = bi[0];
-    for (int w = 1; w < nw; ++w)
-      if (bv[w] > b || (bv[w] == b && bi[w] < bidx)) { b = bv[w]; bidx = bi[w]; }
-    if (bidx >= V) bidx = 0;   // all-NaN logits: deterministic fallback
+    int bidx;
+    if (use_forced) {
+      bidx = forced[s];
+    } else if (!logits) {
+      bidx = 0;                  // a forced-only step run past its prompt: inert token
+    } else {
+      const int nw = blockDim.x >> 6;
+      float b = bv[0];
+      bidx = bi[0];
+      for (int w = 1; w < nw; ++w)
+        if (bv[w] > b || (bv[w] == b && bi[w] < bidx)) { b = bv[w]; bidx = bi[w]; }
+      if (bidx >= V) bidx = 0;   // all-NaN logits: deterministic fallback
+    }
+    bidx = bidx < 0 ? 0 : (bidx >= vocab ? vocab - 1 : bidx);
     chosen = bidx;
     tok[0] = bidx;
-    const int s = step[0];
     if (s < hist_cap) hist[s] = bidx;
     step[0] = s + 1;
     pos[0] = pos[0] + 1;
@@ -350,13 +363,17 @@ int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vo
   return check_launch("afx_embed");
 }
 
-int afx_greedy_advance(const float* logits, int V, int* tok, int* pos, int* hist, int hist_cap, int* step,
-                       const void* embed, void* h, int D, void* stream) {
-  AFX_REQUIRE(logits && tok && pos && step && V >= 1, "afx_greedy_advance: bad arguments");
-  AFX_REQUIRE(!embed || (h && D % 8 == 0), "afx_greedy_advance: embed gather needs h and D % 8 == 0");
-  hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, V, tok, pos,
-                     hist, hist_cap, step, (const half_t*)embed, (half_t*)h, D);
-  return check_launch("afx_greedy_advance");
+int afx_decode_advance(const float* logits, int V, const int* forced, const int* n_forced, int* tok, int* pos,
+                       int* hist, int hist_cap, int* step, const void* embed, void* h, int D, int vocab,
+                       void* stream) {
+  AFX_REQUIRE(tok && pos && step && (logits || forced), "afx_decode_advance: bad arguments");
+  AFX_REQUIRE(!logits || V >= 1, "afx_decode_advance: V must be positive");
+  AFX_REQUIRE(!embed || (h && D % 8 == 0 && vocab >= 1), "afx_decode_advance: embed gather needs h, D % 8 == 0");
+  AFX_REQUIRE(logits || n_forced, "afx_decode_advance: a forced-only step needs n_forced");
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, V, forced,
+                     n_forced, tok, pos, hist, hist_cap, step, (const half_t*)embed, (half_t*)h, D,
+                     vocab > 0 ? vocab : V);
+  return check_launch("afx_decode_advance");
 }
 
 int afx_argmax(const float* x, int M, int V, int* out, void* stream) {

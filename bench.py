@@ -147,7 +147,7 @@ def bench_attn(args, ctx=None, B=None):
     vs = [torch.randn((B, Hkv, ctx, D), device="cuda", generator=g).half() for _ in range(copies)]
     q = torch.randn((B, Hq, D), device="cuda", generator=g).half()
     o = torch.empty_like(q)
-    ws = torch.empty(K.attn_ws_bytes(B, Hq, Hkv, D, ctx) // 4 + 1, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(K.attn_ws_bytes(B, Hq, Hkv, D, ctx) // 4 + 1, dtype=torch.float32, device="cuda")
     gr = Graph(lambda: [K.decode_attn(q, ks[i], vs[i], o=o, ctx_len=ctx, ws=ws) for i in range(copies)])
     for _ in range(3):
         gr.launch()
@@ -169,6 +169,176 @@ def bench_kernels(args):
     for B in (1, 16):
         for ctx in (512, 2048, 8192):
             out.append(bench_attn(a, ctx, B))
+    return out
+
+
+# ----------------------------------------------------------------------------- cfg3 decode
+CFG3 = dict(dim=4096, n_layers=32, n_heads=32, n_kv_heads=8, ffn_dim=11008, vocab=32000, prefill=2048)
+
+
+def cfg3_token_bytes(pos: int) -> int:
+    """Algorithmic (compulsory) HBM bytes of one decode token at position `pos`: every layer's
+    int8 weights + fp16 scales + fp16 norm gammas, the fp16 lm_head + final gamma, KV read of
+    rows [0, pos] and the KV row write."""
+    D, L, F, V, KV, dh = 4096, 32, 11008, 32000, 8, 128
+    per_layer_w = (D * D + 2 * KV * dh * D + D * D + 2 * F * D + D * F)            # int8 codes
+    per_layer_s = 2 * (D + 2 * KV * dh + D + 2 * F + D)                           # fp16 row scales
+    per_layer_g = 2 * 2 * D                                                       # two gammas
+    kv = L * 2 * KV * (pos + 1) * dh * 2 + L * 2 * KV * dh * 2                     # read + write
+    return L * (per_layer_w + per_layer_s + per_layer_g) + V * D * 2 + 2 * D + kv
+
+
+def build_cfg3_engine(steps: int, warmup: int):
+    import torch
+    from aneforge_amd import _engine as E
+    from aneforge_amd.llm import LlamaConfig
+    c = CFG3
+    cfg = LlamaConfig(dim=c["dim"], n_layers=c["n_layers"], n_heads=c["n_heads"], n_kv_heads=c["n_kv_heads"],
+                      ffn_dim=c["ffn_dim"], vocab=c["vocab"])
+    D, F, V = c["dim"], c["ffn_dim"], c["vocab"]
+    nkv = c["n_kv_heads"] * cfg.dh
+    g = torch.Generator(device="cuda").manual_seed(3)
+
+    def i8(N, Kd):
+        q = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
+        s = (torch.randn(N, device="cuda", generator=g).abs() * (0.02 / 127)).half()
+        return E.Linear("int8", q, s, N, Kd)
+
+    ones = torch.ones(D, dtype=torch.float16, device="cuda")
+    layers = []
+    for _ in range(c["n_layers"]):
+        layers.append((E.AttentionDecode.from_linears(cfg, i8(D + 2 * nkv, D), i8(D, D), ones),
+                       E.SwiGLUDecode.from_linears(cfg, i8(2 * F, D), i8(D, F), ones)))
+    embed = (torch.randn((V, D), device="cuda", generator=g) * 0.02).half()
+    head = E.Linear("fp16", (torch.randn((V, D), device="cuda", generator=g) * 0.02).half(), None, V, D)
+    M = c["prefill"] + max(steps, warmup) + 8
+    eng = E.DecodeEngine(cfg, layers, embed, head, ones, M)
+    P = c["prefill"]
+    for mixer, _ in layers:                     # resident cache prefilled with N(0, 1) rows [0, 2048)
+        mixer.kc[:, :, :P].normal_(generator=g)
+        mixer.vc[:, :, :P].normal_(generator=g)
+    torch.cuda.synchronize()
+    return cfg, eng, layers
+
+
+def time_dominant_kernel(eng, layers, reps: int = 10):
+    """Average duration of the fused RMSNorm + gate/up + SwiGLU int8 GEMV, one launch per layer
+    (32 distinct weight sets, 2.9 GB: no cache reuse), HIP events on the launching stream."""
+    from aneforge_amd import _kernels as K
+
+    def body():
+        for _, mlp in layers:
+            K.linear_swiglu(mlp.gu.fmt, mlp.gu.w, mlp.gu.scale, eng.h, mlp.norm, mlp.eps, act=eng.act[:, :mlp.F])
+
+    gr = Graph(body)
+    gr.launch()
+    ms = gr.time_ms(reps) / len(layers)
+    gr.close()
+    mlp = layers[0][1]
+    N, Kd = mlp.gu.N, mlp.gu.K
+    byts = N * Kd + 2 * N + 2 * Kd + 2 * Kd + 2 * (N // 2)
+    return ms, byts
+
+
+def cpu_baseline_decode(seconds: float = 12.0):
+    """The reference CPU path (numpy fp32, oracle.ref.cpu_decode_layer_f32) on one 7B-shape
+    layer + the lm_head, dequantised weights prepared outside the timed region; tokens/s is
+    extrapolated to 32 layers.  Threads = what the BLAS pool actually uses."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import ref
+    rng = np.random.default_rng(3)
+    D, F, KV, dh, H, V, P = 4096, 11008, 8, 128, 32, 32000, 2048
+    w = {}
+    for name, (n, k) in {"wq": (D, D), "wk": (KV * dh, D), "wv": (KV * dh, D), "wo": (D, D),
+                         "wgate": (F, D), "wup": (F, D), "wdown": (D, F)}.items():
+        q = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        s = (np.abs(rng.normal(0, 0.02, n)) / 127).astype(np.float16)
+        w[name] = ref.dequant_w8(q, s)
+    w["attn_norm"] = np.ones(D, np.float32)
+    w["mlp_norm"] = np.ones(D, np.float32)
+    lm = (rng.standard_normal((V, D)).astype(np.float32) * np.float32(0.02))
+    Kc = rng.standard_normal((KV, P + 64, dh)).astype(np.float32)
+    Vc = rng.standard_normal((KV, P + 64, dh)).astype(np.float32)
+    cos, sin = ref.rope_tables(P + 64, dh)
+    cfg = {"n_heads": H, "n_kv_heads": KV, "dh": dh, "norm_eps": 1e-5}
+    h = rng.standard_normal((1, D)).astype(np.float32)
+    t_layer, t_head, n, t_end = [], [], 0, time.perf_counter() + seconds
+    while time.perf_counter() < t_end or n < 2:
+        t0 = time.perf_counter()
+        ref.cpu_decode_layer_f32(h, w, cfg, Kc, Vc, P + n, cos[P + n].astype(np.float32), sin[P + n].astype(np.float32))
+        t1 = time.perf_counter()
+        _ = h @ lm.T
+        t2 = time.perf_counter()
+        t_layer.append(t1 - t0)
+        t_head.append(t2 - t1)
+        n += 1
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = len(os.sched_getaffinity(0))
+    per_tok = 32 * min(t_layer) + min(t_head)
+    return {"value": 1.0 / per_tok, "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "sample": f"numpy fp32 restatement of the reference CPU decode (bench/decode_measurement.py:86-132 + "
+                      f"GQA/RoPE) on one 4096/11008/32-head layer at pos {P} + the 32000x4096 lm_head, min of "
+                      f"{n} reps, extrapolated to 32 layers; host cores available {len(os.sched_getaffinity(0))}"}
+
+
+def bench_decode(args):
+    import ctypes
+    import torch
+    from aneforge_amd import _hip
+    K_steps, W_steps = args.steps, args.warmup
+    log(f"building cfg3 engine (32 layers int8, KV prefilled to {CFG3['prefill']})")
+    cfg, eng, layers = build_cfg3_engine(K_steps, W_steps)
+    log(f"weights resident: {eng.weight_bytes / 1e9:.3f} GB; capturing step graphs")
+    P = CFG3["prefill"]
+    eng.reset([1], pos0=P, zero_state=False)
+    eng.run(0, W_steps)
+    eng.sync()
+    eng.reset([1], pos0=P, zero_state=False)     # timed steps cover positions P .. P+K-1
+    eng.sync()
+    torch.cuda.synchronize()
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    _hip.call("afx_event_create", ctypes.byref(e0))
+    _hip.call("afx_event_create", ctypes.byref(e1))
+    t0 = time.perf_counter()
+    _hip.call("afx_event_record", e0, eng.stream.cuda_stream)
+    eng.run(0, K_steps)
+    _hip.call("afx_event_record", e1, eng.stream.cuda_stream)
+    ms = ctypes.c_float()
+    _hip.call("afx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = ms.value / 1e3
+    toks = eng.history(0, K_steps)
+    log(f"decoded {K_steps} tokens in {gpu_s * 1e3:.2f} ms (events), wall {wall * 1e3:.2f} ms; first tokens {toks[:8]}")
+    per_tok_bytes = np.mean([cfg3_token_bytes(P + i) for i in range(K_steps)])
+    tok_s = K_steps / gpu_s
+    roof_tok_s = HBM_PEAK / per_tok_bytes
+    k_ms, k_bytes = time_dominant_kernel(eng, layers)
+    achieved = k_bytes / (k_ms * 1e-3)
+    out = {
+        "metric": "quantized decode GEMV GB/s (% HBM peak) + tokens/s, 7B-shape int8 decode, bs=1",
+        "value": tok_s, "unit": "tokens/s", "n_gpus": 1, "steps": K_steps, "warmup": W_steps,
+        "ms_per_step": gpu_s * 1e3 / K_steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 weights / fp16 activations / fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "cfg3: 32-layer Llama-style decode, d4096, 32/8 heads, SwiGLU 11008, vocab 32000, "
+                               "int8 per-channel linears, fp16 lm_head, fp16 KV prefilled to 2048, greedy bs=1",
+                   "global_batch": 1, "seq_len": P + K_steps, "parallelism": "none (1 GPU)"},
+        "decode": {"bytes_per_token": per_tok_bytes, "effective_GBps": per_tok_bytes * tok_s / 1e9,
+                   "roofline_tokens_per_s": roof_tok_s, "frac_of_roofline": tok_s / roof_tok_s,
+                   "kernels_per_token": 5 * CFG3["n_layers"] + 2},
+        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<int8> fused RMSNorm + gate/up + SwiGLU (22016x4096)",
+                     "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK, "avg_launch_us": k_ms * 1e3, "bytes_per_launch": k_bytes,
+                     "traffic": None},
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline (bounded sample)")
+        out["cpu_baseline"] = cpu_baseline_decode()
+    else:
+        out["cpu_baseline"] = None
     return out
 
 
@@ -194,6 +364,14 @@ def main():
         return
     if args.workload == "attn":
         print(json.dumps(bench_attn(args)))
+        return
+    if args.workload == "decode":
+        res = bench_decode(args)
+        line = json.dumps(res)
+        print(line, flush=True)
+        if args.out:
+            with open(args.out, "a") as f:
+                f.write(line + "\n")
         return
     raise SystemExit(f"workload {args.workload} not built yet")
 

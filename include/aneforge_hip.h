@@ -110,10 +110,12 @@ int afx_rope(const void* x, void* y, int rows, int dh, const void* cos_tab, cons
              const int* pos_dev, int pos0, int rows_per_pos, void* stream);
 /* host embedding gather of LlamaPrefill.step (aneforge/llm.py:593-594), on the device */
 int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vocab, void* stream);
-/* greedy _sample (aneforge/llm.py:406-409) + the decode loop's bookkeeping (:619-627) on the
- * device: token = argmax, hist[*step] = token, ++*step, ++*pos, h = embed[token]. */
-int afx_greedy_advance(const float* logits, int V, int* tok, int* pos, int* hist, int hist_cap, int* step,
-                       const void* embed, void* h, int D, void* stream);
+/* One step of the device-resident decode loop (aneforge/llm.py:584-627 step/_sample/generate):
+ * token = forced[*step] while *step < *n_forced (prompt), else greedy argmax of logits; then
+ * hist[*step] = token, ++*step, ++*pos, h = embed[token] (the host gather of :593-594). */
+int afx_decode_advance(const float* logits, int V, const int* forced, const int* n_forced, int* tok, int* pos,
+                       int* hist, int hist_cap, int* step, const void* embed, void* h, int D, int vocab,
+                       void* stream);
 /* np.argmax per row (lowest index on ties) */
 int afx_argmax(const float* x, int M, int V, int* out, void* stream);
 /* graph-capturable fills (zeroing resident state, aneforge/llm.py:581-583) */

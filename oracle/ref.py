@@ -331,3 +331,37 @@ def generate(prompt, n_new, W, cfg, M, exact=False, caches=None, start_pos=None)
         all_logits.append(lg)
         cur, pos = nxt, pos + 1
     return out, all_logits
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+def cpu_decode_layer_f32(h, w, cfg, K, V, pos, cos_row, sin_row):
+    """The reference's CPU decode path in fp32 (bench/decode_measurement.py:86-132 `ref_decode`,
+    extended with GQA and RoPE as in aneforge/llm.py:214-237): numpy matmuls on weights already
+    dequantised to fp32, attention over the cache plus the new row, SwiGLU, residuals.  Used
+    only as the timed CPU baseline; parity checks use decode_layer."""
+    H, KV, dh, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg["dh"], cfg["norm_eps"]
+    f32 = np.float32
+
+    def rms(x, g):
+        return (x / np.sqrt((x * x).mean(-1, keepdims=True) + f32(eps))) * g
+
+    def rot(x):
+        half = x.shape[-1] // 2
+        return x * cos_row + np.concatenate([-x[..., half:], x[..., :half]], -1) * sin_row
+
+    xn = rms(h, w["attn_norm"])
+    q = rot((xn @ w["wq"].T).reshape(H, dh))
+    k = rot((xn @ w["wk"].T).reshape(KV, dh))
+    v = (xn @ w["wv"].T).reshape(KV, dh)
+    K[:, pos] = k
+    V[:, pos] = v
+    G = H // KV
+    out = np.empty((H, dh), f32)
+    for g in range(KV):
+        s = (q[g * G:(g + 1) * G] @ K[g, :pos + 1].T) * f32(1.0 / np.sqrt(dh))
+        s = np.exp(s - s.max(-1, keepdims=True))
+        out[g * G:(g + 1) * G] = (s / s.sum(-1, keepdims=True)) @ V[g, :pos + 1]
+    h = h + out.reshape(1, H * dh) @ w["wo"].T
+    fn = rms(h, w["mlp_norm"])
+    gg = fn @ w["wgate"].T
+    return h + ((gg / (1 + np.exp(-gg))) * (fn @ w["wup"].T)) @ w["wdown"].T

@@ -219,6 +219,28 @@ def test_decode_attn_device_positions(K, Hq, Hkv, D, Mmax):
     check_f16(got, want, what="attn pos")
 
 
+def test_decode_attn_workspace_reuse_and_graph_replay(K):
+    say("decode attention: one workspace reused across calls and graph replays")
+    import bench
+    from aneforge_amd import workloads
+    outs = []
+    for ctx in (300, 2048):
+        c = workloads.cfg2_attn(ctx, 2, seed=ctx)
+        q, k, v = dev(c["q"]), dev(c["K"]), dev(c["V"])
+        ws = torch.zeros(K.attn_ws_bytes(2, 32, 8, 128, ctx) // 4 + 1, dtype=torch.float32, device="cuda")
+        want = ref.attention(c["q"][:, :, None, :], c["K"], c["V"])[:, :, 0]
+        for _ in range(3):                                   # eager reuse: the counters reset themselves
+            check_f16(host(K.decode_attn(q, k, v, ctx_len=ctx, ws=ws)), want, what=f"eager ctx={ctx}")
+        o = torch.empty_like(q)
+        g = bench.Graph(lambda: K.decode_attn(q, k, v, o=o, ctx_len=ctx, ws=ws))
+        for _ in range(3):
+            o.zero_()
+            g.launch()
+            g.stream.synchronize()
+            check_f16(host(o), want, what=f"replay ctx={ctx}")
+        g.close()
+
+
 def test_decode_attn_mask_and_causal(K):
     say("decode attention additive mask + causal alignment")
     rng = np.random.default_rng(41)
@@ -264,8 +286,8 @@ def test_rmsnorm_rope_embed_argmax(K):
     assert host(K.argmax(dev(lg))).tolist() == [int(np.argmax(lg[0])), 7]
 
 
-def test_greedy_advance(K):
-    say("greedy advance (argmax + hist + pos + embed)")
+def test_decode_advance_greedy_and_forced(K):
+    say("decode advance (argmax / forced + hist + pos + embed)")
     rng = np.random.default_rng(51)
     V, D = 32000, 4096
     lg = rng.standard_normal(V).astype(np.float32)
@@ -275,9 +297,15 @@ def test_greedy_advance(K):
     step = torch.tensor([2], dtype=torch.int32, device="cuda")
     hist = torch.full((8,), -1, dtype=torch.int32, device="cuda")
     h = torch.zeros((1, D), dtype=torch.float16, device="cuda")
-    K.greedy_advance(dev(lg), tok, pos, hist, step, dev(table), h)
+    forced = torch.tensor([7, 8, 9], dtype=torch.int32, device="cuda")
+    nf = torch.tensor([3], dtype=torch.int32, device="cuda")
+    tb = dev(table)
+    K.decode_advance(dev(lg), tok, pos, hist, step, tb, h, forced, nf)     # step 2 < 3: forced[2]
+    assert host(tok)[0] == 9 and host(pos)[0] == 11 and host(step)[0] == 3 and host(hist)[2] == 9
+    assert np.array_equal(host(h)[0], table[9])
+    K.decode_advance(dev(lg), tok, pos, hist, step, tb, h, forced, nf)     # step 3: greedy
     t = int(np.argmax(lg))
-    assert host(tok)[0] == t and host(pos)[0] == 11 and host(step)[0] == 3 and host(hist)[2] == t
+    assert host(tok)[0] == t and host(pos)[0] == 12 and host(step)[0] == 4 and host(hist)[3] == t
     assert np.array_equal(host(h)[0], table[t])
 
 

@@ -18,9 +18,12 @@
 // resets, so graph replays need no memset) rescales and sums the split partials and writes
 // the fp16 output: one launch per call.  The workspace's counter tail must be zero before the
 // first call.
+#include <stdlib.h>
 #include "afx_common.h"
 
 namespace afx {
+
+constexpr int kMaxSplits = 128;   // partials per (b, head); the chunk grows so ctx/chunk <= this
 
 struct AttnArgs {
   const half_t* q;   // [B][Hq][D] via strides
@@ -29,11 +32,12 @@ struct AttnArgs {
   half_t* o;         // same strides as q
   const half_t* mask;  // optional additive mask [B][mask_bs] over positions
   const int* pos;      // optional: ctx length of sequence b = pos[b] + 1 (device)
-  float* ws;           // [B][Hq][nsplit][D+2] split partials
+  float* ws_o;         // [B][Hq][D][nsp] split partial outputs (a (head, dim) row is contiguous)
+  float* ws_ml;        // [B][Hq][2][nsp] split max (log2 domain) and row sum
   int* counters;       // [B][Hkv] arrival counters (zero before first use; reset by the last arrival)
   long long q_bs, q_hs, kv_bs, kv_hs;
   long long mask_bs;
-  int B, Hq, Hkv, L, Mmax, chunk, nsplit, causal_off;  // causal_off < 0: no causal masking
+  int B, Hq, Hkv, L, Mmax, chunk, nsplit, nsp, causal_off;  // causal_off < 0: no causal masking
   float scale_log2;    // scale * log2(e)
 };
 
@@ -47,7 +51,10 @@ __device__ __forceinline__ int seq_len(const AttnArgs& a, int b) {
   return L < 1 ? 1 : L;
 }
 
-template <int D, int G, int NSTEP>
+template <int D, int G>
+__device__ void combine_group(const AttnArgs& a, int b, int kvh, int ns);
+
+template <int D, int G, int NSTEP, bool FUSED>
 __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   constexpr int LPP = D / 8;        // lanes per position (16 B each)
   constexpr int PPS = 64 / LPP;     // positions per wavefront step
@@ -171,21 +178,23 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     for (int g = 0; g < G; ++g) red_l[wave][g] = l[g];
   __syncthreads();
 
+  const int NSP = a.nsp;
   for (int idx = threadIdx.x; idx < G * D; idx += 256) {
     const int g = idx / D, d = idx - g * D;
     const float acc = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
-    float* w = a.ws + (((size_t)b * a.Hq + kvh * G + g) * a.nsplit + split) * (D + 2);
-    w[2 + d] = acc;
+    const size_t bh = (size_t)b * a.Hq + kvh * G + g;
+    a.ws_o[(bh * D + d) * NSP + split] = acc;
     if (d == 0) {
-      w[0] = mx[g];
-      w[1] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
+      a.ws_ml[(bh * 2 + 0) * NSP + split] = mx[g];
+      a.ws_ml[(bh * 2 + 1) * NSP + split] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
     }
   }
 
+  if constexpr (!FUSED) return;            // a separate combine launch merges the splits
   // ---- the last workgroup of this (b, kvh) merges all split partials (no second launch) ----
   const int ns = (L + C - 1) / C;            // splits that ran for this sequence
   __shared__ int s_last;
-  __threadfence();                           // release this workgroup's partials (agent scope)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // write back this workgroup's partials
   __syncthreads();
   if (threadIdx.x == 0) {
     int* ctr = a.counters + (size_t)b * a.Hkv + kvh;
@@ -195,105 +204,128 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();                           // acquire the other workgroups' partials
-  __shared__ float s_scale[G][64];
-  __shared__ float s_den[G];
-  // per head: global max over splits, then per-split weights exp2(m_s - M) (up to 64 per pass)
-  for (int g = 0; g < G; ++g) {
-    const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // see the other workgroups' partials
+  combine_group<D, G>(a, b, kvh, ns);
+}
+
+// Merge the ns split partials of one (b, kvh) group: per head the global max and denominator,
+// then every output (head, dim) sums its contiguous row of partials with float4 loads.
+template <int D, int G>
+__device__ void combine_group(const AttnArgs& a, int b, int kvh, int ns) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int NSP = a.nsp;
+  __shared__ float s_w[G][kMaxSplits];       // exp2(m_s - M) / den per (head, split)
+  __shared__ float s_l[G][kMaxSplits];
+  for (int i = threadIdx.x; i < G * ns; i += 256) {
+    const int g = i / ns, sp = i - g * ns;
+    const size_t bh = (size_t)b * a.Hq + kvh * G + g;
+    s_w[g][sp] = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 0) * NSP + sp);
+    s_l[g][sp] = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 1) * NSP + sp);
+  }
+  __syncthreads();
+  for (int g = wave; g < G; g += 4) {
     float m = -INFINITY;
-    for (int s2 = threadIdx.x; s2 < ns; s2 += 256) m = fmaxf(m, __builtin_nontemporal_load(base + (size_t)s2 * (D + 2)));
+    for (int sp = lane; sp < ns; sp += 64) m = fmaxf(m, s_w[g][sp]);
     m = wave_max(m);
-    if (lane == 0) red_m[wave][g] = m;
-  }
-  __syncthreads();
-  float den_part[G];
-  for (int g = 0; g < G; ++g) {
-    const float M = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
-    const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2);
     float den = 0.0f;
-    for (int s2 = threadIdx.x; s2 < ns; s2 += 256) {
-      const float* ws = base + (size_t)s2 * (D + 2);
-      den += exp2f(__builtin_nontemporal_load(ws) - M) * __builtin_nontemporal_load(ws + 1);
-    }
-    den_part[g] = wave_sum(den);
+    for (int sp = lane; sp < ns; sp += 64) den += exp2f(s_w[g][sp] - m) * s_l[g][sp];
+    den = wave_sum(den);
+    const float inv = 1.0f / den;
+    for (int sp = lane; sp < ns; sp += 64) s_w[g][sp] = exp2f(s_w[g][sp] - m) * inv;
   }
   __syncthreads();
-  if (lane == 0)
-    for (int g = 0; g < G; ++g) red_l[wave][g] = den_part[g];
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int g = threadIdx.x;
-    s_den[g] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
-  }
-  __syncthreads();
-  for (int s0 = 0; s0 < ns; s0 += 64) {
-    const int nc = ns - s0 < 64 ? ns - s0 : 64;
-    for (int idx = threadIdx.x; idx < G * 64; idx += 256) {
-      const int g = idx >> 6, j = idx & 63;
-      const float M = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
-      const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2);
-      s_scale[g][j] = j < nc ? exp2f(__builtin_nontemporal_load(base + (size_t)(s0 + j) * (D + 2)) - M) : 0.0f;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-      const int g = idx / D, d = idx - g * D;
-      const float* base = a.ws + ((size_t)b * a.Hq + kvh * G + g) * a.nsplit * (D + 2) + 2 + d;
-      float num = s0 == 0 ? 0.0f : red_o[0][g][d];
-#pragma unroll 8
-      for (int j = 0; j < nc; ++j) num = __builtin_fmaf(s_scale[g][j], __builtin_nontemporal_load(base + (size_t)(s0 + j) * (D + 2)), num);
-      red_o[0][g][d] = num;
-    }
-    __syncthreads();
-  }
   for (int idx = threadIdx.x; idx < G * D; idx += 256) {
     const int g = idx / D, d = idx - g * D;
-    a.o[(size_t)b * a.q_bs + (size_t)(kvh * G + g) * a.q_hs + d] = (half_t)(red_o[0][g][d] / s_den[g]);
+    const float* row = a.ws_o + (((size_t)b * a.Hq + kvh * G + g) * D + d) * NSP;
+    float num = 0.0f;
+    for (int s0 = 0; s0 < ns; s0 += 32) {
+      f4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = s0 + 4 * j < ns ? __builtin_nontemporal_load((const f4*)(row + s0 + 4 * j)) : (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int sp = s0 + 4 * j;
+        if (sp + 0 < ns) num = __builtin_fmaf(s_w[g][sp + 0], v[j].x, num);
+        if (sp + 1 < ns) num = __builtin_fmaf(s_w[g][sp + 1], v[j].y, num);
+        if (sp + 2 < ns) num = __builtin_fmaf(s_w[g][sp + 2], v[j].z, num);
+        if (sp + 3 < ns) num = __builtin_fmaf(s_w[g][sp + 3], v[j].w, num);
+      }
+    }
+    a.o[(size_t)b * a.q_bs + (size_t)(kvh * G + g) * a.q_hs + d] = (half_t)num;
   }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int L = seq_len(a, b);
+  combine_group<D, G>(a, b, kvh, (L + a.chunk - 1) / a.chunk);
 }
 
 typedef void (*attn_fn)(AttnArgs);
 
-template <int D, int G>
+template <int D, int G, bool F>
 static attn_fn pick_steps(int nstep) {
   switch (nstep) {
-    case 1: return attn_partial_kernel<D, G, 1>;
-    case 2: return attn_partial_kernel<D, G, 2>;
-    case 4: return attn_partial_kernel<D, G, 4>;
-    default: return attn_partial_kernel<D, G, 8>;
+    case 1: return attn_partial_kernel<D, G, 1, F>;
+    case 2: return attn_partial_kernel<D, G, 2, F>;
+    case 4: return attn_partial_kernel<D, G, 4, F>;
+    case 8: return attn_partial_kernel<D, G, 8, F>;
+    default: return attn_partial_kernel<D, G, 16, F>;
+  }
+}
+template <int D, bool F>
+static attn_fn pick_g(int G, int nstep) {
+  switch (G) {
+    case 1: return pick_steps<D, 1, F>(nstep);
+    case 2: return pick_steps<D, 2, F>(nstep);
+    case 4: return pick_steps<D, 4, F>(nstep);
+    default: return pick_steps<D, 8, F>(nstep);
   }
 }
 template <int D>
-static attn_fn pick_g(int G, int nstep) {
+static attn_fn pick_combine(int G) {
   switch (G) {
-    case 1: return pick_steps<D, 1>(nstep);
-    case 2: return pick_steps<D, 2>(nstep);
-    case 4: return pick_steps<D, 4>(nstep);
-    default: return pick_steps<D, 8>(nstep);
+    case 1: return attn_combine_kernel<D, 1>;
+    case 2: return attn_combine_kernel<D, 2>;
+    case 4: return attn_combine_kernel<D, 4>;
+    default: return attn_combine_kernel<D, 8>;
   }
+}
+// 0 = two launches (partials, then combine: no cross-workgroup fences), 1 = fused combine in
+// the last-arriving workgroup (release/acquire fences + arrival counter).
+static int g_attn_mode = -1;
+static int attn_mode() {
+  if (g_attn_mode < 0) {
+    const char* e = getenv("AFX_ATTN_FUSED_COMBINE");
+    g_attn_mode = e && atoi(e) == 1 ? 1 : 0;
+  }
+  return g_attn_mode;
 }
 
 static int attn_cus() {
   static int cus = 0;
   if (!cus) {
     int dev = 0;
-    hipGetDevice(&dev);
+    (void)hipGetDevice(&dev);
     hipDeviceProp_t p;
     cus = hipGetDeviceProperties(&p, dev) == hipSuccess ? p.multiProcessorCount : 256;
   }
   return cus;
 }
 
-// Steps per wavefront (chunk = nstep * 4 * (512 / D) positions): the largest chunk that
-// still gives about two workgroups per CU.
+// Steps per wavefront (chunk = nstep * 4 * (512 / D) positions): the largest chunk that still
+// puts about one workgroup on every CU, and never more than kMaxSplits splits.  Returns 0 if
+// even the largest chunk leaves more than kMaxSplits splits.
 static int choose_nstep(int D, int B, int Hkv, int L, int want) {
-  if (want == 1 || want == 2 || want == 4 || want == 8) return want;
   const int pps = 512 / D;
-  const int target = 2 * attn_cus();
-  for (int ns = 8; ns >= 1; ns >>= 1) {
-    const int c = ns * 4 * pps;
-    const long long wgs = (long long)B * Hkv * ((L + c - 1) / c);
-    if (wgs >= target) return ns;
+  auto splits = [&](int ns) { const int c = ns * 4 * pps; return (L + c - 1) / c; };
+  if (want == 1 || want == 2 || want == 4 || want == 8 || want == 16) return splits(want) <= kMaxSplits ? want : 0;
+  const int target = attn_cus();
+  for (int ns = 16; ns >= 1; ns >>= 1) {
+    if (splits(ns) > kMaxSplits) return ns == 16 ? 0 : ns * 2;
+    if ((long long)B * Hkv * splits(ns) >= target) return ns;
   }
   return 1;
 }
@@ -306,11 +338,13 @@ extern "C" {
 
 // Workspace bytes needed by afx_decode_attn for a given shape (max_len = the longest ctx).
 long long afx_decode_attn_ws_bytes(int B, int Hq, int Hkv, int D, int max_len, int nstep_hint) {
-  if (D != 64 && D != 128) return -1;
+  if (D != 32 && D != 64 && D != 128 && D != 256) return -1;
   const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
+  if (ns == 0) return -2;
   const int chunk = ns * 4 * (512 / D);
   const long long nsplit = (max_len + chunk - 1) / chunk;
-  return (long long)B * Hq * nsplit * (D + 2) * 4 + (long long)B * Hkv * 4;
+  const long long nsp = (nsplit + 3) / 4 * 4;
+  return (long long)B * Hq * nsp * (D + 2) * 4 + (long long)B * Hkv * 4;
 }
 
 // q/o: element (b, h, d) at b*q_bs + h*q_hs + d.  K/V: (b, kvh, p, d) at b*kv_bs + kvh*kv_hs + p*D + d.
@@ -322,7 +356,7 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
                     const int* pos, int max_len, const void* mask, long long mask_bs, int causal_off,
                     float scale, void* ws, long long ws_bytes, int nstep_hint, void* stream) {
   AFX_REQUIRE(q && k && v && o && ws, "afx_decode_attn: null pointer");
-  AFX_REQUIRE(D == 64 || D == 128, "afx_decode_attn: head dim %d not supported (64, 128)", D);
+  AFX_REQUIRE(D == 32 || D == 64 || D == 128 || D == 256, "afx_decode_attn: head dim %d not supported (32, 64, 128, 256)", D);
   AFX_REQUIRE(B >= 1 && Hkv >= 1 && Hq % Hkv == 0, "afx_decode_attn: bad heads Hq=%d Hkv=%d", Hq, Hkv);
   const int G = Hq / Hkv;
   AFX_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "afx_decode_attn: GQA group %d not in {1,2,4,8}", G);
@@ -331,20 +365,36 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   AFX_REQUIRE((q_hs % 8) == 0 && (q_bs % 8) == 0 && (kv_hs % 8) == 0 && (kv_bs % 8) == 0,
               "afx_decode_attn: strides must be multiples of 8 elements");
   const long long need = afx_decode_attn_ws_bytes(B, Hq, Hkv, D, max_len, nstep_hint);
+  AFX_REQUIRE(need > 0, "afx_decode_attn: max_len=%d needs more than %d splits", max_len, kMaxSplits);
   AFX_REQUIRE(ws_bytes >= need, "afx_decode_attn: workspace %lld B < %lld B", ws_bytes, need);
   AttnArgs a = {};
   a.q = (const half_t*)q; a.k = (const half_t*)k; a.v = (const half_t*)v; a.o = (half_t*)o;
-  a.mask = (const half_t*)mask; a.pos = pos; a.ws = (float*)ws;
+  a.mask = (const half_t*)mask; a.pos = pos;
   a.q_bs = q_bs; a.q_hs = q_hs; a.kv_bs = kv_bs; a.kv_hs = kv_hs; a.mask_bs = mask_bs;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.L = ctx_len; a.Mmax = max_len; a.causal_off = causal_off;
   a.scale_log2 = scale * 1.4426950408889634f;
   const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
   a.chunk = ns * 4 * (512 / D);
   a.nsplit = (max_len + a.chunk - 1) / a.chunk;
-  a.counters = (int*)((char*)ws + need - (long long)B * Hkv * 4);
-  attn_fn fn = D == 64 ? pick_g<64>(G, ns) : pick_g<128>(G, ns);
+  a.nsp = (a.nsplit + 3) / 4 * 4;
+  a.ws_o = (float*)ws;
+  a.ws_ml = a.ws_o + (size_t)B * Hq * D * a.nsp;
+  a.counters = (int*)(a.ws_ml + (size_t)B * Hq * 2 * a.nsp);
+  const bool fused = attn_mode() == 1;
+  attn_fn fn;
+  if (fused)
+    fn = D == 32 ? pick_g<32, true>(G, ns) : D == 64 ? pick_g<64, true>(G, ns)
+       : D == 128 ? pick_g<128, true>(G, ns) : pick_g<256, true>(G, ns);
+  else
+    fn = D == 32 ? pick_g<32, false>(G, ns) : D == 64 ? pick_g<64, false>(G, ns)
+       : D == 128 ? pick_g<128, false>(G, ns) : pick_g<256, false>(G, ns);
   hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
-  return check_launch("afx_decode_attn");
+  int rc = check_launch("afx_decode_attn");
+  if (rc || fused) return rc;
+  attn_fn cf = D == 32 ? pick_combine<32>(G) : D == 64 ? pick_combine<64>(G) : D == 128 ? pick_combine<128>(G)
+                                                                                     : pick_combine<256>(G);
+  hipLaunchKernelGGL(cf, dim3(Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch("afx_decode_attn(combine)");
 }
 
 }  // extern "C"

@@ -29,6 +29,7 @@
 //   EPI_QKV    fused q|k|v rows; q and k rows are interleaved per head as (d, d+dh/2) pairs so
 //              RoPE (llm.py:96-105) is applied in registers; k and v are written straight into
 //              the resident cache at row pos (replaces the masked O(M) rewrite, llm.py:233).
+#include <stdlib.h>
 #include "afx_gemv_core.h"
 
 namespace afx {
@@ -110,82 +111,21 @@ __device__ __forceinline__ float row_scale(const GemvArgs& a, int fmt, int row) 
   return fmt == FMT_I8 ? (float)a.scale[row] : 1.0f;
 }
 
-template <int FMT, int M, int R, bool NORM>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int K = a.K, N = a.N;
-
-  const half_t* xbase;
-  int ldx;
-  if constexpr (NORM) {
-    half_t* xn = (half_t*)smem;
-    float* red = (float*)(smem + (size_t)M * K * sizeof(half_t));
-    rms_prologue<M>(a, xn, red);
-    xbase = xn;
-    ldx = K;
-  } else {
-    xbase = a.x;
-    ldx = a.ldx;
+// Copy the activations into LDS once per workgroup (the wavefronts re-read them per row tile).
+template <int M>
+__device__ void stage_x(const GemvArgs& a, half_t* xs) {
+  const int nv = a.K >> 3;
+  for (int m = 0; m < M; ++m) {
+    const half_t* xr = a.x + (size_t)(m < a.M ? m : a.M - 1) * a.ldx;
+    for (int v = threadIdx.x; v < nv; v += 256) *(u4*)(xs + (size_t)m * a.K + 8 * v) = *(const u4*)(xr + 8 * v);
   }
+  __syncthreads();
+}
 
-  const int row0 = (blockIdx.x * 4 + wave) * R;
-  if (row0 >= N) return;  // no barrier follows
-
-  const half_t* xp[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) xp[m] = xbase + (size_t)(m < a.M ? m : a.M - 1) * ldx;
-
-  const size_t rb = Fmt<FMT>::row_bytes(K);
-  const unsigned char* wrow[R];
-  const half_t* drow[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = row0 + r < N ? row0 + r : N - 1;   // clamp: tail rows are computed, not stored
-    wrow[r] = (const unsigned char*)a.w + (size_t)row * rb;
-    drow[r] = (FMT == FMT_Q4) ? a.scale + (size_t)row * (K >> 5) : nullptr;
-  }
-
-  const int nchunks = K / Fmt<FMT>::kWeightsPerChunk;
-  constexpr int U = (FMT == FMT_Q4) ? (R >= 4 ? 2 : 4) : (R >= 4 ? 4 : 8);
-  float acc[M][R];
-#pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
-
-  for (int cb = lane; cb < nchunks; cb += 64 * U) {
-    u4 wv[U][R];
-    u2 dv[U][R];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = cb + 64 * u;
-      const int cc = c < nchunks ? c : nchunks - 1;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        wv[u][r] = __builtin_nontemporal_load((const u4*)(wrow[r] + (size_t)cc * 16));
-        if constexpr (FMT == FMT_Q4) dv[u][r] = *(const u2*)(drow[r] + 4 * (cc >> 2));
-        else dv[u][r] = (u2){0u, 0u};
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = cb + 64 * u;
-      if (c < nchunks) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float part[M];
-#pragma unroll
-          for (int m = 0; m < M; ++m) part[m] = acc[m][r];
-          Fmt<FMT>::template dot<M>(wv[u][r], xp, c, K, dv[u][r], part);
-#pragma unroll
-          for (int m = 0; m < M; ++m) acc[m][r] = part[m];
-        }
-      }
-    }
-  }
-
-  // ---- reduce: lane owns row row0 + rr after the butterfly ----
+// Row-tile epilogue: reduce the wavefront's R row partials and apply the selected epilogue.
+template <int FMT, int M, int R>
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, float (&acc)[M][R], int row0, int lane) {
+  const int N = a.N;
   const int rr = reduced_row_of_lane<R>(lane);
   const int row = row0 + rr;
   constexpr int GROUP = 64 / R;          // lanes holding the same row
@@ -194,9 +134,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   for (int m = 0; m < M; ++m) {
     const float sum = wave_reduce_rows<R>(acc[m], lane);
     const bool live = m < a.M;
-    const float v = (row < N) ? sum * row_scale(a, FMT, row < N ? row : 0) +
-                                    (a.bias ? (float)a.bias[row < N ? row : 0] : 0.0f)
-                              : 0.0f;
+    const int rs = row < N ? row : 0;
+    const float v = (row < N) ? sum * row_scale(a, FMT, rs) + (a.bias ? (float)a.bias[rs] : 0.0f) : 0.0f;
     switch (a.epi) {
       case EPI_F16:
         if (writer && live && row < N) ((half_t*)a.y)[(size_t)m * a.ldy + row] = (half_t)v;
@@ -260,29 +199,140 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// Chunks per lane per pipeline unit (each lane has U*R 16-byte loads in flight per unit).
+template <int FMT, int M, int R>
+struct Units {
+  static constexpr int value = FMT == FMT_Q4 ? 2 : 4;
+};
+
+// Persistent, software-pipelined GEMV.  A row tile is 4 wavefronts x R rows; workgroups
+// stride over tiles.  Each wavefront walks (tile, chunk batch) units and keeps two register
+// buffers: the next unit's weight loads are in flight while the current unit is computed.
+// The first unit is requested before the x prologue (LDS staging or RMSNorm), so the
+// prologue's latency overlaps the first weight fetch.
+//   XS: 0 = x read from global memory, 1 = x staged in LDS, 2 = RMSNorm(x) into LDS.
+template <int FMT, int M, int R, int XS>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int U = Units<FMT, M, R>::value;
+  constexpr int XH = Fmt<FMT>::kXH2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int K = a.K, N = a.N;
+  const int nchunks = K / Fmt<FMT>::kWeightsPerChunk;
+  const int ntiles = (N + 4 * R - 1) / (4 * R);
+  const size_t rb = Fmt<FMT>::row_bytes(K);
+  const unsigned char* wbase = (const unsigned char*)a.w;
+
+  auto tile_live = [&](int t) { return t < ntiles && (t * 4 + wave) * R < N; };
+  auto load_unit = [&](u4 (&w)[U][R], u2 (&d)[U][R], int t, int c0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int row = (t * 4 + wave) * R + r;
+      row = row < N ? row : N - 1;                       // tail rows: computed, never stored
+      const unsigned char* wr = wbase + (size_t)row * rb;
+      const half_t* dr = FMT == FMT_Q4 ? a.scale + (size_t)row * (K >> 5) : nullptr;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int c = c0 + 64 * u + lane;
+        c = c < nchunks ? c : nchunks - 1;
+        w[u][r] = __builtin_nontemporal_load((const u4*)(wr + (size_t)c * 16));
+        d[u][r] = load_scales<FMT>(dr, c);
+      }
+    }
+  };
+
+  int t0 = blockIdx.x;
+  const bool live = tile_live(t0);
+  u4 wA[U][R], wB[U][R];
+  u2 dA[U][R], dB[U][R];
+  if (live) load_unit(wA, dA, t0, 0);
+
+  const half_t* xbase = a.x;
+  int ldx = a.ldx;
+  if constexpr (XS != 0) {
+    half_t* xs = (half_t*)smem;
+    if constexpr (XS == 2) rms_prologue<M>(a, xs, (float*)(smem + (size_t)M * K * sizeof(half_t)));
+    else stage_x<M>(a, xs);
+    xbase = xs;
+    ldx = K;
+  }
+  if (!live) return;   // no barrier follows
+
+  const half_t* xp[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xp[m] = xbase + (size_t)(m < a.M ? m : a.M - 1) * ldx;
+
+  float acc[M][R];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+  auto compute = [&](const u4 (&w)[U][R], const u2 (&d)[U][R], int c0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 64 * u + lane;
+      if (c < nchunks) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          h2 xv[XH];
+          Fmt<FMT>::load_x(xp[m], c, xv);
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[m][r] = Fmt<FMT>::dot(w[u][r], xv, d[u][r], acc[m][r]);
+        }
+      }
+    }
+  };
+  auto finish_tile = [&](int t) {
+    gemv_epilogue<FMT, M, R>(a, acc, (t * 4 + wave) * R, lane);
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+  };
+
+  int c0 = 0;
+  const int step = 64 * U;
+  for (;;) {
+    int t1 = t0, c1 = c0 + step;
+    if (c1 >= nchunks) { c1 = 0; t1 = t0 + gridDim.x; }
+    bool nxt = tile_live(t1);
+    if (nxt) load_unit(wB, dB, t1, c1);
+    compute(wA, dA, c0);
+    if (c1 == 0) finish_tile(t0);
+    if (!nxt) break;
+    t0 = t1; c0 = c1;
+
+    t1 = t0; c1 = c0 + step;
+    if (c1 >= nchunks) { c1 = 0; t1 = t0 + gridDim.x; }
+    nxt = tile_live(t1);
+    if (nxt) load_unit(wA, dA, t1, c1);
+    compute(wB, dB, c0);
+    if (c1 == 0) finish_tile(t0);
+    if (!nxt) break;
+    t0 = t1; c0 = c1;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------------
 typedef void (*gemv_fn)(GemvArgs);
 
 template <int FMT, int M, int R>
-static gemv_fn pick_norm(bool norm) {
-  return norm ? gemv_kernel<FMT, M, R, true> : gemv_kernel<FMT, M, R, false>;
+static gemv_fn pick_xs(int xs) {
+  return xs == 2 ? gemv_kernel<FMT, M, R, 2> : xs == 1 ? gemv_kernel<FMT, M, R, 1> : gemv_kernel<FMT, M, R, 0>;
 }
 template <int FMT, int M>
-static gemv_fn pick_r(int R, bool norm) {
-  switch (R) {
-    case 1: return pick_norm<FMT, M, 1>(norm);
-    case 2: return pick_norm<FMT, M, 2>(norm);
-    default: return pick_norm<FMT, M, 4>(norm);
-  }
+static gemv_fn pick_r(int R, int xs) {
+  return R >= 4 ? pick_xs<FMT, M, 4>(xs) : pick_xs<FMT, M, 2>(xs);
 }
 template <int FMT>
-static gemv_fn pick_m(int M, int R, bool norm) {
-  if (M <= 1) return pick_r<FMT, 1>(R, norm);
-  if (M <= 2) return pick_r<FMT, 2>(R, norm);
-  if (M <= 4) return pick_r<FMT, 4>(R, norm);
-  return pick_r<FMT, 8>(R, norm);
+static gemv_fn pick_m(int M, int R, int xs) {
+  if (M <= 1) return pick_r<FMT, 1>(R, xs);
+  if (M <= 2) return pick_r<FMT, 2>(R, xs);
+  if (M <= 4) return pick_r<FMT, 4>(R, xs);
+  return pick_r<FMT, 8>(R, xs);
 }
 static int mtile(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
@@ -290,27 +340,23 @@ static int g_cu_count = 0;
 static int cu_count() {
   if (g_cu_count == 0) {
     int dev = 0;
-    hipGetDevice(&dev);
+    (void)hipGetDevice(&dev);
     hipDeviceProp_t p;
     g_cu_count = (hipGetDeviceProperties(&p, dev) == hipSuccess) ? p.multiProcessorCount : 256;
   }
   return g_cu_count;
 }
 
-// Rows per wavefront: prefer the largest R whose grid fills whole "waves" of workgroups
-// across the CUs (tail effect), never going below one workgroup per CU when avoidable.
-static int choose_rows(int N, int want) {
-  if (want == 1 || want == 2 || want == 4) return want;
-  const int cus = cu_count();
-  int best = 4;
-  double best_eff = -1.0;
-  for (int R = 4; R >= 1; R >>= 1) {
-    const int g = (N + 4 * R - 1) / (4 * R);
-    const int waves = (g + cus - 1) / cus;
-    const double eff = (double)g / ((double)waves * cus);
-    if (eff > best_eff + 1e-9) { best_eff = eff; best = R; }
+// Workgroups resident per CU the persistent grid is sized for (register-limited occupancy
+// of the two-buffer pipeline is about 2 workgroups of 4 wavefronts per CU).
+static int g_wg_per_cu = 0;
+static int wg_per_cu() {
+  if (g_wg_per_cu == 0) {
+    const char* e = getenv("AFX_GEMV_WG_PER_CU");
+    const int v = e ? atoi(e) : 0;
+    g_wg_per_cu = v >= 1 && v <= 16 ? v : 2;
   }
-  return best;
+  return g_wg_per_cu;
 }
 
 static int launch(int fmt, GemvArgs& a, bool norm, int rows_hint, hipStream_t stream, const char* what) {
@@ -319,7 +365,7 @@ static int launch(int fmt, GemvArgs& a, bool norm, int rows_hint, hipStream_t st
   AFX_REQUIRE(a.N >= 1 && a.K >= 1, "%s: bad shape N=%d K=%d", what, a.N, a.K);
   const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : 8;
   AFX_REQUIRE(a.K % kq == 0, "%s: K=%d must be a multiple of %d", what, a.K, kq);
-  AFX_REQUIRE(norm || a.ldx % 8 == 0, "%s: ldx=%d must be a multiple of 8", what, a.ldx);
+  AFX_REQUIRE(a.ldx % 8 == 0, "%s: ldx=%d must be a multiple of 8", what, a.ldx);
   AFX_REQUIRE(((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.w & 15) == 0,
               "%s: x and weights must be 16-byte aligned", what);
   AFX_REQUIRE(fmt != FMT_I8 || a.scale, "%s: int8 weights need a scale vector", what);
@@ -327,21 +373,31 @@ static int launch(int fmt, GemvArgs& a, bool norm, int rows_hint, hipStream_t st
               "%s: Q4_0 weights need an 8-byte aligned block-scale array", what);
   if (a.epi == EPI_SWIGLU) AFX_REQUIRE(a.N % 2 == 0, "%s: SwiGLU needs interleaved gate/up rows", what);
   if (a.epi == EPI_RESID) AFX_REQUIRE(a.resid, "%s: residual pointer required", what);
-  int R = choose_rows(a.N, rows_hint);
-  if (a.epi == EPI_SWIGLU || a.epi == EPI_QKV) R = R < 2 ? 2 : R;  // pairs stay in one wavefront
   if (a.epi == EPI_QKV)
     AFX_REQUIRE(a.dh % 2 == 0 && a.nq % a.dh == 0 && a.nk % a.dh == 0 && a.pos && a.kcache && a.vcache,
                 "%s: bad fused-QKV arguments", what);
+  const int mt = mtile(a.M);
+  int R = rows_hint == 2 || rows_hint == 4 ? rows_hint : (mt >= 4 ? 2 : 4);
+  const size_t xbytes = (size_t)mt * a.K * sizeof(half_t);
+  int xs;
   size_t smem = 0;
   if (norm) {
     AFX_REQUIRE(a.gamma, "%s: RMSNorm prologue needs gamma", what);
-    smem = (size_t)mtile(a.M) * a.K * sizeof(half_t) + 8 * 4 * sizeof(float);
+    smem = xbytes + 8 * 4 * sizeof(float);
     AFX_REQUIRE(smem <= 65536, "%s: M*K=%d too large for the LDS norm prologue", what, a.M * a.K);
+    xs = 2;
+  } else if (xbytes <= 65536) {
+    smem = xbytes;
+    xs = 1;
+  } else {
+    xs = 0;
   }
-  gemv_fn fn = fmt == FMT_I8 ? pick_m<FMT_I8>(a.M, R, norm)
-             : fmt == FMT_Q4 ? pick_m<FMT_Q4>(a.M, R, norm)
-                             : pick_m<FMT_F16>(a.M, R, norm);
-  const int grid = (a.N + 4 * R - 1) / (4 * R);
+  gemv_fn fn = fmt == FMT_I8 ? pick_m<FMT_I8>(a.M, R, xs)
+             : fmt == FMT_Q4 ? pick_m<FMT_Q4>(a.M, R, xs)
+                             : pick_m<FMT_F16>(a.M, R, xs);
+  const int ntiles = (a.N + 4 * R - 1) / (4 * R);
+  const int cap = cu_count() * wg_per_cu();
+  const int grid = ntiles < cap ? ntiles : cap;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), smem, stream, a);
   return check_launch(what);
 }

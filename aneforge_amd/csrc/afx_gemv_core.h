@@ -19,39 +19,42 @@ __device__ __forceinline__ void load_x(const half_t* p, h2 (&out)[N8 * 4]) {
 }
 
 // ---- per-format chunk geometry and math ----
+// A "chunk" is the 16 weight bytes one lane loads per row: 16 int8 codes, 32 Q4 codes, or 8
+// fp16 weights.  load_x fetches the matching activations once per chunk (kXH2 fp16 pairs) so
+// they are reused across all rows a wavefront owns.
 template <int FMT> struct Fmt;
 
 template <> struct Fmt<FMT_I8> {
   static constexpr int kWeightsPerChunk = 16;
+  static constexpr int kXH2 = 8;
   __device__ static size_t row_bytes(int K) { return (size_t)K; }
-  // dot of one 16-code chunk with the 16 x values at k = 16c
-  template <int M>
-  __device__ static void dot(const u4& w, const half_t* const (&xp)[M], int c, int, const u2&,
-                             float (&acc)[M]) {
+  __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) { afx::load_x<2>(xrow + 16 * c, x); }
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2&, float acc) {
     h2 q[8];
     i8x4_to_h2(w.x, q[0], q[1]); i8x4_to_h2(w.y, q[2], q[3]);
     i8x4_to_h2(w.z, q[4], q[5]); i8x4_to_h2(w.w, q[6], q[7]);
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      h2 xv[8];
-      load_x<2>(xp[m] + 16 * c, xv);
-      float s = acc[m];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s = dot2(q[i], xv[i], s);
-      acc[m] = s;
-    }
+    for (int i = 0; i < 8; ++i) acc = dot2(q[i], x[i], acc);
+    return acc;
   }
 };
 
 template <> struct Fmt<FMT_Q4> {
   static constexpr int kWeightsPerChunk = 32;
+  static constexpr int kXH2 = 16;
   __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
   // chunk c = superblock sb*4 + word-group g; dword j of the chunk = elements 8g..8g+7 of
   // block 4sb+j; d = the 4 block scales of the superblock.
-  template <int M>
-  __device__ static void dot(const u4& w, const half_t* const (&xp)[M], int c, int, const u2& d,
-                             float (&acc)[M]) {
+  __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) {
     const int sb = c >> 2, g = c & 3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h2 t[4];
+      afx::load_x<1>(xrow + 32 * (4 * sb + j) + 8 * g, t);
+      x[4 * j + 0] = t[0]; x[4 * j + 1] = t[1]; x[4 * j + 2] = t[2]; x[4 * j + 3] = t[3];
+    }
+  }
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, float acc) {
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
     const h2 d01 = as_h2(d.x), d23 = as_h2(d.y);
     const float ds[4] = {(float)d01.x, (float)d01.y, (float)d23.x, (float)d23.y};
@@ -59,39 +62,35 @@ template <> struct Fmt<FMT_Q4> {
     for (int j = 0; j < 4; ++j) {
       h2 q[4];
       q4_word_to_h2(wd[j], q);
-      const int k0 = 32 * (4 * sb + j) + 8 * g;
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        h2 xv[4];
-        load_x<1>(xp[m] + k0, xv);
-        float s = dot2(q[0], xv[0], 0.0f);
-        s = dot2(q[1], xv[1], s);
-        s = dot2(q[2], xv[2], s);
-        s = dot2(q[3], xv[3], s);
-        acc[m] = __builtin_fmaf(ds[j], s, acc[m]);
-      }
+      float s = dot2(q[0], x[4 * j + 0], 0.0f);
+      s = dot2(q[1], x[4 * j + 1], s);
+      s = dot2(q[2], x[4 * j + 2], s);
+      s = dot2(q[3], x[4 * j + 3], s);
+      acc = __builtin_fmaf(ds[j], s, acc);
     }
+    return acc;
   }
 };
 
 template <> struct Fmt<FMT_F16> {
   static constexpr int kWeightsPerChunk = 8;
+  static constexpr int kXH2 = 4;
   __device__ static size_t row_bytes(int K) { return (size_t)K * 2; }
-  template <int M>
-  __device__ static void dot(const u4& w, const half_t* const (&xp)[M], int c, int, const u2&,
-                             float (&acc)[M]) {
-    const h2 q[4] = {as_h2(w.x), as_h2(w.y), as_h2(w.z), as_h2(w.w)};
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      h2 xv[4];
-      load_x<1>(xp[m] + 8 * c, xv);
-      float s = acc[m];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s = dot2(q[i], xv[i], s);
-      acc[m] = s;
-    }
+  __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) { afx::load_x<1>(xrow + 8 * c, x); }
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2&, float acc) {
+    acc = dot2(as_h2(w.x), x[0], acc);
+    acc = dot2(as_h2(w.y), x[1], acc);
+    acc = dot2(as_h2(w.z), x[2], acc);
+    acc = dot2(as_h2(w.w), x[3], acc);
+    return acc;
   }
 };
 
+// Q4 block scales for a chunk (4 fp16 in 8 bytes); other formats have none.
+template <int FMT>
+__device__ __forceinline__ u2 load_scales(const half_t* drow, int c) {
+  if constexpr (FMT == FMT_Q4) return *(const u2*)(drow + 4 * (c >> 2));
+  else return (u2){0u, 0u};
+}
 
 }  // namespace afx

@@ -70,7 +70,26 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
   if (!use_forced && logits) {
     float best = -INFINITY;
     int besti = 0x7fffffff;
-    for (int i = t; i < V; i += blockDim.x) {
+    // batches of 8 float4 per thread, all loads issued before the compares
+    const int nv4 = V >> 2;
+    const bool al = (((uintptr_t)logits) & 15) == 0;
+    for (int b0 = 0; al && b0 < nv4; b0 += 8 * (int)blockDim.x) {
+      float4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i4 = b0 + j * (int)blockDim.x + t;
+        v[j] = i4 < nv4 ? ((const float4*)logits)[i4] : float4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int base = 4 * (b0 + j * (int)blockDim.x + t);
+        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (e[k] > best || (e[k] == best && base + k < besti)) { best = e[k]; besti = base + k; }
+      }
+    }
+    for (int i = (al ? 4 * nv4 : 0) + t; i < V; i += blockDim.x) {
       const float v = logits[i];
       if (v > best || (v == best && i < besti)) { best = v; besti = i; }
     }

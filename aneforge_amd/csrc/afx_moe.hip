@@ -128,8 +128,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(MoeArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           wv[u][r] = *(const u4*)(wrow[r] + (size_t)cc * 16);
-          if constexpr (FMT == FMT_Q4) dv[u][r] = *(const u2*)(drow[r] + 4 * (cc >> 2));
-          else dv[u][r] = (u2){0u, 0u};
+          dv[u][r] = load_scales<FMT>(drow[r], cc);
         }
       }
 #pragma unroll
@@ -137,13 +136,11 @@ __global__ __launch_bounds__(256) void moe_group_kernel(MoeArgs a) {
         const int c = cb + 64 * u;
         if (c < nchunks) {
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            float part[MG];
+          for (int m = 0; m < MG; ++m) {
+            h2 xv[Fmt<FMT>::kXH2];
+            Fmt<FMT>::load_x(xp[m], c, xv);
 #pragma unroll
-            for (int m = 0; m < MG; ++m) part[m] = acc[m][r];
-            Fmt<FMT>::template dot<MG>(wv[u][r], xp, c, K, dv[u][r], part);
-#pragma unroll
-            for (int m = 0; m < MG; ++m) acc[m][r] = part[m];
+            for (int r = 0; r < R; ++r) acc[m][r] = Fmt<FMT>::dot(wv[u][r], xv, dv[u][r], acc[m][r]);
           }
         }
       }

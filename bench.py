@@ -265,7 +265,8 @@ def cpu_baseline_decode(seconds: float = 12.0):
     t_layer, t_head, n, t_end = [], [], 0, time.perf_counter() + seconds
     while time.perf_counter() < t_end or n < 2:
         t0 = time.perf_counter()
-        ref.cpu_decode_layer_f32(h, w, cfg, Kc, Vc, P + n, cos[P + n].astype(np.float32), sin[P + n].astype(np.float32))
+        p = P + (n % 64)
+        ref.cpu_decode_layer_f32(h, w, cfg, Kc, Vc, p, cos[p].astype(np.float32), sin[p].astype(np.float32))
         t1 = time.perf_counter()
         _ = h @ lm.T
         t2 = time.perf_counter()

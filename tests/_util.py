@@ -31,6 +31,16 @@ def check_f16(got, want, rtol=RTOL, atol=ATOL, min_cos=MIN_COS, what=""):
     assert c >= min_cos, f"{what}: cosine {c:.6f} < {min_cos}"
 
 
+def check_hidden(got, want, what=""):
+    """Residual-stream hidden states are sums of fp16-rounded terms: where h + f(h) cancels, a
+    one-ulp difference in an operand (ulp of the operand's magnitude) survives the subtraction.
+    The absolute tolerance is therefore one fp16 ulp of the layer's largest |value| (at least
+    1e-3), on top of rtol 1e-2 and cosine >= 0.9999."""
+    want = np.asarray(want, np.float64)
+    ulp = float(np.spacing(np.float16(np.abs(want).max())))
+    check_f16(got, want, atol=max(ATOL, ulp), what=what)
+
+
 def dev(a):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()

@@ -205,7 +205,8 @@ def test_decode_attn_cfg2(K, B, ctx):
         check_f16(got[b], want, what=f"attn b={b}")
 
 
-@pytest.mark.parametrize("Hq,Hkv,D,Mmax", [(4, 4, 64, 37), (8, 2, 128, 300), (16, 2, 64, 1000), (8, 1, 128, 5)])
+@pytest.mark.parametrize("Hq,Hkv,D,Mmax", [(4, 4, 64, 37), (8, 2, 128, 300), (16, 2, 64, 1000), (8, 1, 128, 5),
+                                           (4, 2, 32, 50), (4, 4, 256, 20)])
 def test_decode_attn_device_positions(K, Hq, Hkv, D, Mmax):
     say(f"decode attention pos-driven Hq={Hq} Hkv={Hkv} D={D} Mmax={Mmax}")
     rng = np.random.default_rng(40)

@@ -4,7 +4,7 @@ with tolerances tightened to the path's parity bar."""
 import numpy as np
 import pytest
 
-from _util import check_f16, cosine, say
+from _util import check_f16, check_hidden, cosine, say
 from oracle import ref
 
 pytestmark = pytest.mark.gpu
@@ -128,7 +128,7 @@ def test_per_layer_hidden_full_7b_layer_shape():
          "final_norm": np.ones(4096, np.float32), "lm_head": (rng.standard_normal((256, 4096)) * 0.02).astype(np.float32),
          "layers": []}
     for lh in layers_host:
-        lw = {k: E.QuantizedWeight("int8", q, s, q.shape) for k, (q, s) in lh.items() if k.startswith("w")}
+        lw = {k: E.QuantizedWeight("int8", v[0], v[1], v[0].shape) for k, v in lh.items() if k.startswith("w")}
         lw["attn_norm"], lw["mlp_norm"] = lh["attn_norm"], lh["mlp_norm"]
         w["layers"].append(lw)
     m = LlamaPrefill(cfg, w)
@@ -139,7 +139,7 @@ def test_per_layer_hidden_full_7b_layer_shape():
     # oracle: same codes, fp16 rounding points of the kernels
     ow = {"embed": w["embed"].astype(np.float16).astype(np.float32), "layers": []}
     for lh in layers_host:
-        e = {k: ref.dequant_w8(q, s) for k, (q, s) in lh.items() if k.startswith("w")}
+        e = {k: ref.dequant_w8(v[0], v[1]) for k, v in lh.items() if k.startswith("w")}
         e["attn_norm"], e["mlp_norm"] = lh["attn_norm"], lh["mlp_norm"]
         ow["layers"].append(e)
     oc = _ocfg(cfg)
@@ -156,7 +156,7 @@ def test_per_layer_hidden_full_7b_layer_shape():
                     mlp.enqueue(d)
                 got = d.h.float().cpu().numpy()
                 torch.cuda.synchronize()
-                check_f16(got, h, what=f"layer {li} hidden")
+                check_hidden(got, h, what=f"layer {li} hidden")
     m.release()
 
 

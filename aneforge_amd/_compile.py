@@ -1,0 +1,512 @@
+"""af.compile / compile_multi: lower a Tensor graph to a fixed sequence of HIP kernel launches
+on preallocated device buffers, replayed as one captured HIP graph per call.
+
+The reference lowers the graph to MIL + a weight BLOBFILE and hands it to Espresso
+(aneforge/_compile.py:1360-1404, :1013-1037); the call contract kept here is
+  Model(*arrays) -> fp32 ndarray, Model.input_view/output_view/execute/release
+  MultiModel(*arrays) -> {port: fp32}, .prog (a Program), .input_ports / .output_ports
+  compress= None | "int8" | "int4" | "blockwise" | "sparse" | "auto" | "q4_0",
+  compress_atol (accuracy gate, CompressionFallbackWarning), block_size.
+
+Weight encodings (aneforge/_compile.py:112-188): "int8" -> per-output-row int8 streamed by the
+int8 GEMV; "int4" (16-entry LUT) and "blockwise" (int8 per 32-column block) are accepted when
+their relative reconstruction error is <= compress_atol and are streamed as their exact fp16
+reconstruction, else they fall back ("int4" -> int8, "blockwise" -> fp16) with a warning;
+"sparse" is lossless and streams fp16; "auto" takes int8; "q4_0" (this build's addition) uses
+the GGUF Q4_0 GEMV.  bmm_weight int8 keeps the reference's one-scale-per-batch quirk
+(aneforge/_compile.py:117)."""
+from __future__ import annotations
+
+import warnings
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _blob
+from . import _engine as E
+from . import _kernels as K
+from ._runtime import Program
+from .graph import Tensor
+
+F16 = np.float16
+
+
+class CompressionFallbackWarning(UserWarning):
+    """compress= rejected weights and fell back to a wider encoding (aneforge/_compile.py:1073-1095)."""
+
+
+class PrecisionWarning(UserWarning):
+    pass
+
+
+# ----------------------------------------------------------------------------- weights
+@dataclass
+class _Enc:
+    n_weights: int = 0
+    rejected: dict = None
+
+    def __post_init__(self):
+        self.rejected = {}
+
+
+def _rel_err(rec, W):
+    W = np.asarray(W, np.float32)
+    return float(np.linalg.norm(rec - W) / (np.linalg.norm(W) + 1e-12))
+
+
+def _encode_weight(W, compress, atol, block_size, stats: _Enc, allow_q=True):
+    """-> Linear for a weight [N, K] following the reference's precedence sparse -> int4 ->
+    blockwise -> int8 -> fp16."""
+    stats.n_weights += 1
+    if isinstance(W, E.QuantizedWeight):
+        return E.pack_linear(W, None)
+    W = np.asarray(W, np.float32)
+    if not allow_q or compress is None:
+        return E.pack_linear(W, None)
+    if compress == "sparse":
+        nnz = int(np.count_nonzero(W))
+        if not (0 < nnz <= W.size // 2):
+            stats.rejected["sparse"] = stats.rejected.get("sparse", 0) + 1
+        return E.pack_linear(W, None)
+    if compress == "int4":
+        packed, cb = _blob.palettize_lut4(W)
+        idx = np.empty((W.shape[0], packed.shape[1] * 2), np.uint8)
+        idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
+        rec = cb.astype(np.float32)[idx[:, :W.shape[1]]]
+        if _rel_err(rec, W) <= atol:
+            return E.pack_linear(rec.astype(F16).astype(np.float32), None)
+        stats.rejected["int4"] = stats.rejected.get("int4", 0) + 1
+        return E.pack_linear(W, "int8")
+    if compress == "blockwise":
+        q, s, bs = _blob.quantize_blockwise(W, block_size)
+        N, Kd = W.shape
+        rec = (q.reshape(N, Kd // bs, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(N, Kd)
+        if _rel_err(rec, W) <= atol:
+            return E.pack_linear(rec.astype(F16).astype(np.float32), None)
+        stats.rejected["blockwise"] = stats.rejected.get("blockwise", 0) + 1
+        return E.pack_linear(W, None)
+    if compress in ("int8", "auto"):
+        return E.pack_linear(W, "int8")
+    if compress == "q4_0":
+        if W.shape[1] % 128 == 0:
+            return E.pack_linear(W, "q4_0")
+        stats.rejected["q4_0"] = stats.rejected.get("q4_0", 0) + 1
+        return E.pack_linear(W, "int8")
+    raise ValueError(f"unknown compress={compress!r}")
+
+
+def _fallback_signal(compress, atol, stats: _Enc):
+    if not stats.rejected or compress not in ("sparse", "int4", "blockwise", "q4_0"):
+        return
+    total = sum(stats.rejected.values())
+    detail = ", ".join(f"{e}: {n}" for e, n in sorted(stats.rejected.items()))
+    applied = "int8" if compress in ("int4", "q4_0") else "fp16"
+    warnings.warn(f"aneforge.compile: compress={compress!r} rejected {total}/{stats.n_weights} weights "
+                  f"({detail}); applied {applied}. To widen the tolerance, raise compress_atol "
+                  f"(currently {atol}). Silence: filter CompressionFallbackWarning.",
+                  CompressionFallbackWarning, stacklevel=3)
+
+
+# ----------------------------------------------------------------------------- lowering
+def _topo(outs):
+    order, seen = [], set()
+    stack = [(o, False) for o in reversed(outs)]
+    while stack:
+        t, done = stack.pop()
+        if done:
+            order.append(t)
+            continue
+        if id(t) in seen:
+            continue
+        seen.add(id(t))
+        stack.append((t, True))
+        for s in reversed(t.srcs):
+            if id(s) not in seen:
+                stack.append((s, False))
+    return order
+
+
+def _contig_strides(shape):
+    st, acc = [0] * len(shape), 1
+    for i in range(len(shape) - 1, -1, -1):
+        st[i] = acc
+        acc *= shape[i]
+    return st
+
+
+class _Lowering:
+    """Walks the graph once: allocates a device buffer per node, packs weights, and records
+    one closure per op (each closure enqueues kernels on the current stream)."""
+
+    _UNARY = {"relu": "relu", "silu": "silu", "sigmoid": "sigmoid", "tanh": "tanh", "exp": "exp",
+              "sqrt": "sqrt", "abs": "abs", "square": "square", "gelu_tanh": "gelu_tanh"}
+    _BIN = {"add", "sub", "mul", "real_div", "maximum", "minimum", "pow", "greater", "greater_equal",
+            "less", "less_equal", "equal", "not_equal"}
+    _RED = {"reduce_sum", "reduce_max", "reduce_mean", "reduce_min", "reduce_sum_square"}
+
+    def __init__(self, compress, atol, block_size):
+        self.compress, self.atol, self.block_size = compress, atol, block_size
+        self.stats = _Enc()
+        self.buf: dict[int, torch.Tensor] = {}
+        self.steps: list = []
+        self.keep: list = []     # packed weights / constants kept alive with the model
+
+    def out(self, t: Tensor) -> torch.Tensor:
+        b = torch.empty(t.shape if t.shape else (1,), dtype=torch.float16, device="cuda")
+        self.buf[id(t)] = b
+        return b
+
+    def lower(self, order):
+        for t in order:
+            fn = getattr(self, "_op_" + t.op, None)
+            if fn is None:
+                if t.op in self._UNARY:
+                    self._unary(t, self._UNARY[t.op])
+                elif t.op in self._BIN:
+                    self._binary(t)
+                elif t.op in self._RED:
+                    self._reduce(t)
+                else:
+                    raise NotImplementedError(f"aneforge_amd.compile: op {t.op!r} is not lowered")
+            else:
+                fn(t)
+
+    # -- leaves --
+    def _op_input(self, t):
+        self.out(t)
+
+    def _op_const_array(self, t):
+        v = torch.from_numpy(np.ascontiguousarray(np.asarray(t.attrs["value"], F16).reshape(t.shape or (1,))))
+        self.buf[id(t)] = v.cuda()
+
+    # -- elementwise --
+    def _unary(self, t, op, alpha=0.0, beta=0.0):
+        x, y = self.buf[id(t.srcs[0])], self.out(t)
+        self.steps.append(lambda: K._hip.call("afx_ew_unary", K.UNARY[op], K.P(x), K.P(y), x.numel(),
+                                               float(alpha), float(beta), K.stream()))
+
+    def _op_muls(self, t):
+        self._unary(t, "affine", t.attrs["k"], 0.0)
+
+    def _op_adds(self, t):
+        self._unary(t, "affine", 1.0, t.attrs["k"])
+
+    def _op_log(self, t):
+        self._unary(t, "log", t.attrs.get("eps", 0.0))
+
+    def _op_rsqrt(self, t):
+        self._unary(t, "rsqrt", t.attrs.get("eps", 0.0))
+
+    def _op_inverse(self, t):
+        self._unary(t, "inverse", t.attrs.get("eps", 0.0))
+
+    def _op_clip(self, t):
+        lo, hi = t.attrs["lo"], t.attrs["hi"]
+        a = self.buf[id(t.srcs[0])]
+        lo_t = torch.full((1,), lo, dtype=torch.float16, device="cuda")
+        hi_t = torch.full((1,), hi, dtype=torch.float16, device="cuda")
+        mid = torch.empty_like(a)
+        y = self.out(t)
+        self.keep += [lo_t, hi_t, mid]
+        shape = list(t.shape) or [1]
+        st = _contig_strides(shape)
+
+        def run():
+            K._hip.call("afx_ew_binary", K.EW["maximum"], K.P(a), K._ll(st), K.P(lo_t), K._ll([0] * len(shape)),
+                        K.P(mid), len(shape), K._ii(shape), K.stream())
+            K._hip.call("afx_ew_binary", K.EW["minimum"], K.P(mid), K._ll(st), K.P(hi_t), K._ll([0] * len(shape)),
+                        K.P(y), len(shape), K._ii(shape), K.stream())
+        self.steps.append(run)
+
+    def _binary(self, t):
+        a, b = self.buf[id(t.srcs[0])], self.buf[id(t.srcs[1])]
+        y = self.out(t)
+        shape = list(t.shape) or [1]
+        sa = K._bstrides(a.reshape(t.srcs[0].shape or (1,)), shape)
+        sb = K._bstrides(b.reshape(t.srcs[1].shape or (1,)), shape)
+        op = K.EW[t.op]
+        self.steps.append(lambda: K._hip.call("afx_ew_binary", op, K.P(a), K._ll(sa), K.P(b), K._ll(sb), K.P(y),
+                                               len(shape), K._ii(shape), K.stream()))
+
+    def _op_select(self, t):
+        c, a, b = (self.buf[id(s)] for s in t.srcs)
+        y = self.out(t)
+        shape = list(t.shape) or [1]
+        sc = K._bstrides(c.reshape(t.srcs[0].shape or (1,)), shape)
+        sa = K._bstrides(a.reshape(t.srcs[1].shape or (1,)), shape)
+        sb = K._bstrides(b.reshape(t.srcs[2].shape or (1,)), shape)
+        self.steps.append(lambda: K._hip.call("afx_ew_select", K.P(c), K._ll(sc), K.P(a), K._ll(sa), K.P(b),
+                                               K._ll(sb), K.P(y), len(shape), K._ii(shape), K.stream()))
+
+    # -- layout --
+    def _op_reshape(self, t):
+        self.buf[id(t)] = self.buf[id(t.srcs[0])].reshape(t.shape or (1,))
+
+    def _copy(self, src, src_strides, shape, dst, dst_strides=None, off=0):
+        self.steps.append(lambda: K.copy_strided(src, src_strides, shape, dst=dst, dst_strides=dst_strides,
+                                                 dst_offset=off))
+
+    def _op_transpose(self, t):
+        x = self.buf[id(t.srcs[0])]
+        st = _contig_strides(t.srcs[0].shape)
+        perm = t.attrs["perm"]
+        self._copy(x, [st[p] for p in perm], list(t.shape), self.out(t))
+
+    def _op_slice_by_size(self, t):
+        x = self.buf[id(t.srcs[0])]
+        st = _contig_strides(t.srcs[0].shape)
+        base = int(sum(b * s for b, s in zip(t.attrs["begin"], st)))
+        view = x.reshape(-1)[base:]
+        self._copy(view, st, list(t.shape), self.out(t))
+
+    def _op_concat(self, t):
+        y = self.out(t)
+        ax = t.attrs["axis"]
+        yst = _contig_strides(t.shape)
+        off = 0
+        for s in t.srcs:
+            x = self.buf[id(s)]
+            self._copy(x, _contig_strides(s.shape), list(s.shape), y, yst, off * yst[ax])
+            off += s.shape[ax]
+
+    # -- reductions, softmax, norms --
+    def _last_axis(self, t, x, axis):
+        """(tensor with `axis` moved last (copied if needed), its shape)."""
+        shape = list(t.srcs[0].shape)
+        if axis == len(shape) - 1:
+            return x, shape
+        perm = [i for i in range(len(shape)) if i != axis] + [axis]
+        tshape = [shape[p] for p in perm]
+        tmp = torch.empty(tshape, dtype=torch.float16, device="cuda")
+        self.keep.append(tmp)
+        st = _contig_strides(shape)
+        self._copy(x, [st[p] for p in perm], tshape, tmp)
+        return tmp, tshape
+
+    def _reduce(self, t):
+        x = self.buf[id(t.srcs[0])]
+        axes = sorted(t.attrs["axes"])
+        cur, cur_shape = x, list(t.srcs[0].shape)
+        for ax in reversed(axes):
+            fake = Tensor(cur_shape, "input")
+            tt = Tensor(cur_shape, t.op, [fake], {"axes": (ax,)})
+            self.buf[id(fake)] = cur
+            src, sshape = self._last_axis(tt, cur, ax)
+            rows, cols = int(np.prod(sshape[:-1])) if len(sshape) > 1 else 1, sshape[-1]
+            nxt = torch.empty([d if i != ax else 1 for i, d in enumerate(cur_shape)], dtype=torch.float16, device="cuda")
+            self.keep.append(nxt)
+            op = K.REDUCE[t.op]
+            self.steps.append(lambda src=src, nxt=nxt, rows=rows, cols=cols, op=op: K._hip.call(
+                "afx_reduce", op, K.P(src), K.P(nxt), rows, cols, K.stream()))
+            cur, cur_shape = nxt, list(nxt.shape)
+        self.buf[id(t)] = cur.reshape(t.shape)
+
+    def _op_softmax(self, t):
+        x = self.buf[id(t.srcs[0])]
+        ax = t.attrs["axis"]
+        src, sshape = self._last_axis(t, x, ax)
+        y = self.out(t)
+        cols = sshape[-1]
+        rows = int(np.prod(sshape)) // cols
+        if ax == len(t.shape) - 1:
+            self.steps.append(lambda: K._hip.call("afx_softmax", K.P(src), K.P(y), rows, cols, K.stream()))
+            return
+        tmp = torch.empty(sshape, dtype=torch.float16, device="cuda")
+        self.keep.append(tmp)
+        self.steps.append(lambda: K._hip.call("afx_softmax", K.P(src), K.P(tmp), rows, cols, K.stream()))
+        perm = [i for i in range(len(t.shape)) if i != ax] + [ax]
+        inv = [perm.index(i) for i in range(len(perm))]
+        st = _contig_strides(sshape)
+        self._copy(tmp, [st[p] for p in inv], list(t.shape), y)
+
+    def _op_rms_norm(self, t):
+        x = self.buf[id(t.srcs[0])]
+        D = t.shape[-1]
+        g = torch.from_numpy(np.asarray(t.attrs["gamma"], np.float32).astype(F16)).cuda()
+        self.keep.append(g)
+        y = self.out(t)
+        M = int(np.prod(t.shape)) // D
+        eps = t.attrs["eps"]
+        self.steps.append(lambda: K._hip.call("afx_rmsnorm", K.P(x), D, K.P(g), float(eps), K.P(y), D, M, D,
+                                               K.stream()))
+
+    # -- matmuls --
+    def _gemv_rows(self, lin: "E.Linear", x2, y2, bias=None):
+        """y2[M, N] = x2[M, K] @ W^T (+bias), in row blocks of up to 8 (the GEMV's M limit)."""
+        M = x2.shape[0]
+        for r0 in range(0, M, 8):
+            xs, ys = x2[r0:r0 + 8], y2[r0:r0 + 8]
+            self.steps.append(lambda xs=xs, ys=ys: K.linear(lin.fmt, lin.w, lin.scale, xs, y=ys, bias=bias))
+
+    def _op_matmul(self, t):
+        x = self.buf[id(t.srcs[0])]
+        W = t.attrs["wt"]
+        allow_q = not isinstance(W, np.ndarray) or W.ndim == 2
+        lin = _encode_weight(W, self.compress, self.atol, self.block_size, self.stats, allow_q)
+        bias = None
+        if "bias" in t.attrs:
+            bias = torch.from_numpy(np.asarray(t.attrs["bias"], np.float32).astype(F16)).cuda()
+        self.keep += [lin, bias]
+        y = self.out(t)
+        Kd = t.srcs[0].shape[-1]
+        self._gemv_rows(lin, x.reshape(-1, Kd), y.reshape(-1, lin.N), bias)
+
+    def _op_bmm_w(self, t):
+        """x [B, M, K] @ W [B, K, N]; int8 uses one scale per batch (the reference's quirk)."""
+        x = self.buf[id(t.srcs[0])]
+        W = np.asarray(t.attrs["wt"], np.float32)
+        B, Kd, N = W.shape
+        self.stats.n_weights += 1
+        if self.compress in ("int8", "auto", "int4"):
+            q, s = _blob.quantize_per_tensor_rows(W)                  # [B, K, N] codes, [B] scales
+            codes = np.ascontiguousarray(q.transpose(0, 2, 1)).reshape(B * N, Kd)
+            scales = np.repeat(s, N)
+            lin = E.Linear("int8", E._to_dev(codes), E._to_dev(scales), B * N, Kd)
+        else:
+            lin = E.pack_linear(np.ascontiguousarray(W.transpose(0, 2, 1)).reshape(B * N, Kd), None)
+        self.keep.append(lin)
+        y = self.out(t)
+        lead = t.srcs[0].shape
+        Mb = int(np.prod(lead[1:-1])) if len(lead) > 2 else 1
+        xb = x.reshape(B, Mb, Kd)
+        yb = y.reshape(B, Mb, N)
+        for b in range(B):
+            sub = E.Linear(lin.fmt, lin.w[b * N:(b + 1) * N], None if lin.scale is None else lin.scale[b * N:(b + 1) * N],
+                           N, Kd)
+            self.keep.append(sub)
+            self._gemv_rows(sub, xb[b], yb[b])
+
+    def _op_bmm(self, t):
+        a, b = self.buf[id(t.srcs[0])], self.buf[id(t.srcs[1])]
+        sa, sb = t.srcs[0].shape, t.srcs[1].shape
+        M, Kd, N = sa[-2] if len(sa) > 1 else 1, sa[-1], sb[-1]
+        ba = int(np.prod(sa[:-2])) if len(sa) > 2 else 1
+        bb = int(np.prod(sb[:-2])) if len(sb) > 2 else 1
+        if not (ba == bb or bb == 1 or ba == 1):
+            raise NotImplementedError(f"bmm: batch dims {sa[:-2]} vs {sb[:-2]} need equal sizes or 1")
+        y = self.out(t)
+        batch = max(ba, bb)
+        self.steps.append(lambda: K._hip.call("afx_bmm_f16", K.P(a), K.P(b), K.P(y), batch, M, N, Kd,
+                                               M * Kd if ba > 1 else 0, Kd * N if bb > 1 else 0, M * N,
+                                               K.stream()))
+
+    def _op_sdpa(self, t):
+        q, k, v = (self.buf[id(s)] for s in t.srcs[:3])
+        mask = self.buf[id(t.srcs[3])] if t.attrs.get("masked") else None
+        _, H, Sq, D = t.srcs[0].shape
+        _, Hkv, Skv, _ = t.srcs[1].shape
+        y = self.out(t)
+        causal_off = (Skv - Sq) if t.attrs.get("causal") else -1
+        ws = torch.zeros(K.attn_ws_bytes(Sq, H, Hkv, D, Skv) // 4 + 1, dtype=torch.float32, device="cuda")
+        self.keep.append(ws)
+        k4, v4 = k.reshape(1, Hkv, Skv, D), v.reshape(1, Hkv, Skv, D)
+        m2 = mask.reshape(Sq, Skv) if mask is not None else None
+        scale = t.attrs["scale"]
+        self.steps.append(lambda: K.decode_attn(q, k4, v4, o=y, ctx_len=Skv, scale=scale, mask=m2,
+                                                causal_off=causal_off, ws=ws, q_strides=(D, Sq * D),
+                                                kv_strides=(0, Skv * D), B=Sq, Hq=H))
+
+
+# ----------------------------------------------------------------------------- public API
+def _build(outs, compress, compress_atol, block_size):
+    if not torch.cuda.is_available():
+        raise RuntimeError("aneforge_amd.compile needs an MI355X GPU (no CPU fallback)")
+    order = _topo(outs)
+    inputs = sorted((t for t in order if t.op == "input"), key=lambda t: t.attrs.get("idx", 0))
+    if not inputs:
+        raise ValueError("aneforge.compile: graph has no inputs")
+    for i, t in enumerate(order):
+        t._name = f"t{i}"
+    low = _Lowering(compress, compress_atol, block_size)
+    low.lower(order)
+    _fallback_signal(compress, compress_atol, low.stats)
+    bufs = {t._name: low.buf[id(t)] for t in inputs}
+    for o in outs:
+        bufs[o._name] = low.buf[id(o)]
+    steps = low.steps
+
+    def plan():
+        for s in steps:
+            s()
+
+    prog = Program({t._name: t.shape for t in inputs}, {o._name: o.shape for o in outs}, plan, bufs)
+    prog._keep = (low.keep, low.buf)
+    return prog, inputs, order
+
+
+class Model:
+    """A compiled graph.  Call with the input arrays in af.input order -> fp32 ndarray."""
+
+    def __init__(self, prog: Program, inputs, out: Tensor, n_ops: int):
+        self._prog = prog
+        self._inputs = [(t._name, t.shape) for t in inputs]
+        self._input_tensors = list(inputs)
+        self._out_name, self._out_shape = out._name, out.shape
+        self.n_ops = n_ops
+
+    def __call__(self, *arrays):
+        if len(arrays) != len(self._inputs):
+            raise ValueError(f"expected {len(self._inputs)} input(s), got {len(arrays)}")
+        for (name, shape), a in zip(self._inputs, arrays):
+            a = np.asarray(a)
+            if tuple(a.shape) != tuple(shape):
+                raise ValueError(f"input '{name}' shape {a.shape} != compiled {shape}")
+            self._prog.set_input(name, a)
+        self._prog.execute()
+        return self._prog.read_output(self._out_name).astype(np.float32)
+
+    def input_view(self, name: str | None = None):
+        return self._prog.input_view(name or self._inputs[0][0])
+
+    def output_view(self):
+        return self._prog.output_view(self._out_name)
+
+    def execute(self) -> None:
+        self._prog.execute()
+
+    def release(self) -> None:
+        self._prog.release()
+
+
+class MultiModel:
+    """A compiled graph with several named outputs (aneforge/_compile.py:987-1011)."""
+
+    def __init__(self, prog: Program, inputs, outputs):
+        self.prog = prog
+        self.input_tensors = list(inputs)
+        self.output_tensors = list(outputs)
+        self.input_ports = [(t, t._name) for t in inputs]
+        self.output_ports = [(t, t._name) for t in outputs]
+
+    def __call__(self, *arrays) -> dict:
+        if len(arrays) != len(self.input_ports):
+            raise ValueError(f"expected {len(self.input_ports)} input(s), got {len(arrays)}")
+        out = self.prog.eval({name: np.asarray(a) for (_, name), a in zip(self.input_ports, arrays)})
+        return {name: out[name].astype(np.float32) for _, name in self.output_ports}
+
+    def release(self) -> None:
+        self.prog.release()
+
+
+def compile(out: Tensor, int8: bool = False, build_dir=None, opt="routes", compress: str | None = None,
+            compress_atol: float = 0.05, block_size: int = 32, validate: bool = False, target=None, **_):
+    """Lower `out` to one captured kernel sequence (aneforge/_compile.py:1360).  `int8=True`
+    aliases compress="int8"; `opt` / `target` are accepted for call compatibility (there is one
+    lowering on MI355X)."""
+    if out.op == "input":
+        out = out * 1.0
+    if int8 and compress is None:
+        compress = "int8"
+    prog, inputs, order = _build([out], compress, compress_atol, block_size)
+    return Model(prog, inputs, out, sum(1 for t in order if t.op != "input"))
+
+
+def compile_multi(outs, build_dir=None, int8: bool = False, compress: str | None = None,
+                  compress_atol: float = 0.05, block_size: int = 32) -> MultiModel:
+    """Lower several outputs into one program with named output ports (aneforge/_compile.py:1013)."""
+    outs = list(outs)
+    if int8 and compress is None:
+        compress = "int8"
+    prog, inputs, _ = _build(outs, compress, compress_atol, block_size)
+    return MultiModel(prog, inputs, outs)

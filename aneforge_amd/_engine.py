@@ -189,8 +189,6 @@ class AttentionDecode:
     def __init__(self, lw: dict, cfg, ls, compress):
         if cfg.norm_type != "rms":
             raise NotImplementedError("the device decode engine implements RMSNorm decoders (norm_type='rms')")
-        if ls.qk_norm:
-            raise NotImplementedError("QK-norm (Qwen3) is not fused on the device decode path yet")
         if cfg.rope and (cfg.rotary_dim not in (0, cfg.dh) or cfg.rope_interleaved):
             raise NotImplementedError("partial / interleaved RoPE is not fused on the device decode path yet")
         H, KV, dh, D = cfg.n_heads, cfg.n_kv_heads, cfg.dh, cfg.dim
@@ -207,6 +205,9 @@ class AttentionDecode:
         self.qkv = pack_linear(W, compress, bias)
         self.wo = pack_linear(lw["wo"], compress, lw.get("o_bias"))
         self.norm = _gamma(lw["attn_norm"], D)
+        self.qk_norm = bool(ls.qk_norm)
+        if self.qk_norm:
+            self.q_norm, self.k_norm = _gamma(lw["q_norm"], dh), _gamma(lw["k_norm"], dh)
         self.kc = self.vc = None
 
     @classmethod
@@ -215,6 +216,7 @@ class AttentionDecode:
         self = cls.__new__(cls)
         self.H, self.KV, self.dh, self.eps, self.rope = cfg.n_heads, cfg.n_kv_heads, cfg.dh, float(cfg.norm_eps), rope
         self.qkv, self.wo, self.norm = qkv, wo, norm
+        self.qk_norm = False
         self.kc = self.vc = None
         return self
 
@@ -234,7 +236,14 @@ class AttentionDecode:
         B, H, dh = eng.B, self.H, self.dh
         q = eng.q[:, :H * dh]
         K.qkv_rope_kv(self.qkv.fmt, self.qkv.w, self.qkv.scale, eng.h, self.norm, self.eps, self.qkv.bias,
-                      H * dh, self.KV * dh, dh, eng.cos, eng.sin, eng.pos, q, self.kc, self.vc, rope=self.rope)
+                      H * dh, self.KV * dh, dh, eng.cos, eng.sin, eng.pos, q, self.kc, self.vc,
+                      rope=self.rope and not self.qk_norm)
+        if self.qk_norm:       # QK-norm sits between the projection and RoPE (Qwen3)
+            K.head_norm_rope(q, H, dh, self.q_norm, self.eps, eng.cos, eng.sin, eng.pos, seq_stride=q.stride(0),
+                             head_stride=dh, pos_mul=0, kv_len=eng.M, M=B, rope=self.rope)
+            K.head_norm_rope(self.kc, self.KV, dh, self.k_norm, self.eps, eng.cos, eng.sin, eng.pos,
+                             seq_stride=self.kc.stride(0), head_stride=self.kc.stride(1), pos_mul=dh,
+                             kv_len=eng.M, M=B, rope=self.rope)
         K.decode_attn(q.view(B, H, dh), self.kc, self.vc, o=eng.a[:, :H * dh].view(B, H, dh), pos=eng.pos,
                       ws=eng.attn_ws)
         K.linear(self.wo.fmt, self.wo.w, self.wo.scale, eng.a[:, :H * dh], y=eng.h, bias=self.wo.bias,

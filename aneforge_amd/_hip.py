@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple] = {
     # norms, rope, sampling, generic tensor ops
     "afx_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _i, _i, _i, _vp]),
     "afx_rope": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp]),
+    "afx_head_norm_rope": (_i, [_vp, _ll, _ll, _i, _vp, _i, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "afx_embed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "afx_decode_advance": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp]),
     "afx_argmax": (_i, [_vp, _i, _i, _vp, _vp]),

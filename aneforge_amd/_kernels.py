@@ -172,6 +172,15 @@ def rope(x, cos_t, sin_t, pos0=0, rows_per_pos=None, pos_dev=None, y=None):
     return y
 
 
+def head_norm_rope(x, heads, dh, gamma, eps, cos_t=None, sin_t=None, pos=None, seq_stride=0, head_stride=None,
+                   pos_mul=0, kv_len=1 << 30, M=1, rope=True):
+    """In-place per-head RMSNorm (+RoPE) on `heads` rows of length dh inside x."""
+    _hip.call("afx_head_norm_rope", P(x), int(seq_stride), int(head_stride if head_stride is not None else dh),
+              int(pos_mul), P(pos), int(kv_len), int(heads), int(M), int(dh), P(gamma), float(eps), P(cos_t),
+              P(sin_t), int(bool(rope)), stream())
+    return x
+
+
 def embed(table, ids, out=None):
     M = ids.numel()
     V, D = table.shape

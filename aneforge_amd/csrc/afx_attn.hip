@@ -338,7 +338,7 @@ extern "C" {
 
 // Workspace bytes needed by afx_decode_attn for a given shape (max_len = the longest ctx).
 long long afx_decode_attn_ws_bytes(int B, int Hq, int Hkv, int D, int max_len, int nstep_hint) {
-  if (D != 32 && D != 64 && D != 128 && D != 256) return -1;
+  if (D != 8 && D != 16 && D != 32 && D != 64 && D != 128 && D != 256) return -1;
   const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
   if (ns == 0) return -2;
   const int chunk = ns * 4 * (512 / D);
@@ -356,7 +356,8 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
                     const int* pos, int max_len, const void* mask, long long mask_bs, int causal_off,
                     float scale, void* ws, long long ws_bytes, int nstep_hint, void* stream) {
   AFX_REQUIRE(q && k && v && o && ws, "afx_decode_attn: null pointer");
-  AFX_REQUIRE(D == 32 || D == 64 || D == 128 || D == 256, "afx_decode_attn: head dim %d not supported (32, 64, 128, 256)", D);
+  AFX_REQUIRE(D == 8 || D == 16 || D == 32 || D == 64 || D == 128 || D == 256,
+              "afx_decode_attn: head dim %d not supported (8, 16, 32, 64, 128, 256)", D);
   AFX_REQUIRE(B >= 1 && Hkv >= 1 && Hq % Hkv == 0, "afx_decode_attn: bad heads Hq=%d Hkv=%d", Hq, Hkv);
   const int G = Hq / Hkv;
   AFX_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "afx_decode_attn: GQA group %d not in {1,2,4,8}", G);
@@ -380,19 +381,18 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   a.ws_o = (float*)ws;
   a.ws_ml = a.ws_o + (size_t)B * Hq * D * a.nsp;
   a.counters = (int*)(a.ws_ml + (size_t)B * Hq * 2 * a.nsp);
-  const bool fused = attn_mode() == 1;
+  const bool fused = attn_mode() == 1 && D == 128;     // the fused variant is built for D = 128 only
   attn_fn fn;
   if (fused)
-    fn = D == 32 ? pick_g<32, true>(G, ns) : D == 64 ? pick_g<64, true>(G, ns)
-       : D == 128 ? pick_g<128, true>(G, ns) : pick_g<256, true>(G, ns);
+    fn = pick_g<128, true>(G, ns);
   else
-    fn = D == 32 ? pick_g<32, false>(G, ns) : D == 64 ? pick_g<64, false>(G, ns)
-       : D == 128 ? pick_g<128, false>(G, ns) : pick_g<256, false>(G, ns);
+    fn = D == 8 ? pick_g<8, false>(G, ns) : D == 16 ? pick_g<16, false>(G, ns) : D == 32 ? pick_g<32, false>(G, ns)
+       : D == 64 ? pick_g<64, false>(G, ns) : D == 128 ? pick_g<128, false>(G, ns) : pick_g<256, false>(G, ns);
   hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
   int rc = check_launch("afx_decode_attn");
   if (rc || fused) return rc;
-  attn_fn cf = D == 32 ? pick_combine<32>(G) : D == 64 ? pick_combine<64>(G) : D == 128 ? pick_combine<128>(G)
-                                                                                     : pick_combine<256>(G);
+  attn_fn cf = D == 8 ? pick_combine<8>(G) : D == 16 ? pick_combine<16>(G) : D == 32 ? pick_combine<32>(G)
+             : D == 64 ? pick_combine<64>(G) : D == 128 ? pick_combine<128>(G) : pick_combine<256>(G);
   hipLaunchKernelGGL(cf, dim3(Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_attn(combine)");
 }

@@ -41,6 +41,58 @@ __global__ void rope_kernel(const half_t* __restrict__ x, half_t* __restrict__ y
   y[(size_t)r * dh + j + half] = (half_t)(x2 * c2 + x1 * s2);
 }
 
+// ---- per-head RMSNorm then RoPE, in place (Qwen3 QK-norm, aneforge/llm.py:224-225 then :227) ----
+// Head h of sequence m lives at x + m*seq_stride + h*head_stride + pos_mul*pos[m] (pos_mul = dh for
+// a cache row, 0 for a q buffer).  One wavefront per (head, sequence); rows at pos outside
+// [0, kv_len) are skipped.
+__global__ __launch_bounds__(64) void head_norm_rope_kernel(half_t* __restrict__ x, long long seq_stride,
+                                                            long long head_stride, int pos_mul,
+                                                            const int* __restrict__ pos, int kv_len, int dh,
+                                                            const half_t* __restrict__ g, float eps,
+                                                            const half_t* __restrict__ cos_t,
+                                                            const half_t* __restrict__ sin_t, int rope) {
+  const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  const int p = pos ? pos[m] : 0;
+  if (pos && (p < 0 || p >= kv_len)) return;
+  half_t* r = x + (size_t)m * seq_stride + (size_t)h * head_stride + (size_t)pos_mul * p;
+  const int half = dh >> 1;
+  float v[4];                                        // dh <= 256: 4 values per lane
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    v[i] = d < dh ? (float)r[d] : 0.0f;
+    ss += v[i] * v[i];
+  }
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / __builtin_sqrtf(ss / (float)dh + eps);
+  float n[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    n[i] = d < dh ? (float)(half_t)(v[i] * rstd * (float)g[d]) : 0.0f;   // fp16 norm output
+  }
+  __shared__ float sh[256];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    if (d < dh) sh[d] = n[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    if (d >= dh) continue;
+    float o = n[i];
+    if (rope) {
+      const float c = (float)cos_t[(size_t)p * dh + d], s = (float)sin_t[(size_t)p * dh + d];
+      const float rot = d < half ? -sh[d + half] : sh[d - half];
+      o = o * c + rot * s;
+    }
+    r[d] = (half_t)o;
+  }
+}
+
 // ---- embedding gather: out[m] = table[ids[m]] ----
 __global__ void embed_kernel(const half_t* __restrict__ table, const int* __restrict__ ids,
                              half_t* __restrict__ out, int D, int vocab) {
@@ -373,6 +425,18 @@ int afx_rope(const void* x, void* y, int rows, int dh, const void* cos_tab, cons
                      (const half_t*)x, (half_t*)y, rows, dh, (const half_t*)cos_tab, (const half_t*)sin_tab,
                      pos_dev, pos0, rows_per_pos);
   return check_launch("afx_rope");
+}
+
+int afx_head_norm_rope(void* x, long long seq_stride, long long head_stride, int pos_mul, const int* pos,
+                       int kv_len, int heads, int M, int dh, const void* gamma, float eps, const void* cos_tab,
+                       const void* sin_tab, int rope, void* stream) {
+  AFX_REQUIRE(x && gamma && dh >= 2 && dh <= 256 && dh % 2 == 0 && heads >= 1 && M >= 1,
+              "afx_head_norm_rope: bad arguments (dh=%d)", dh);
+  AFX_REQUIRE(!rope || (cos_tab && sin_tab && pos), "afx_head_norm_rope: rope needs tables and positions");
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3(heads, M), dim3(64), 0, (hipStream_t)stream, (half_t*)x,
+                     seq_stride, head_stride, pos_mul, pos, kv_len, dh, (const half_t*)gamma, eps,
+                     (const half_t*)cos_tab, (const half_t*)sin_tab, rope);
+  return check_launch("afx_head_norm_rope");
 }
 
 int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vocab, void* stream) {

@@ -108,6 +108,11 @@ int afx_rmsnorm(const void* x, int ldx, const void* gamma, float eps, void* y, i
 /* x*cos + rotate_half(x)*sin (aneforge/llm.py:96-105) */
 int afx_rope(const void* x, void* y, int rows, int dh, const void* cos_tab, const void* sin_tab,
              const int* pos_dev, int pos0, int rows_per_pos, void* stream);
+/* per-head RMSNorm then RoPE in place (QK-norm of _attn_decode, aneforge/llm.py:224-225, 227);
+ * head h of row m at x + m*seq_stride + h*head_stride + pos_mul*pos[m] */
+int afx_head_norm_rope(void* x, long long seq_stride, long long head_stride, int pos_mul, const int* pos,
+                       int kv_len, int heads, int M, int dh, const void* gamma, float eps, const void* cos_tab,
+                       const void* sin_tab, int rope, void* stream);
 /* host embedding gather of LlamaPrefill.step (aneforge/llm.py:593-594), on the device */
 int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vocab, void* stream);
 /* One step of the device-resident decode loop (aneforge/llm.py:584-627 step/_sample/generate):

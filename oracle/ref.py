@@ -225,13 +225,15 @@ def topk_gate(probs16, k):
     return out
 
 
-def moe_route(hn16, router, k, renorm=True):
+def moe_route(hn16, router, k, renorm=True, exact=False):
     """Router: softmax(hn R^T) over experts (fp32+), probabilities taken at fp16 (the
     reference's fp16 tie semantics), top-k, optional renorm (aneforge/moe.py:53-56).
     Returns (gate [T, E] with zeros off the top-k, chosen index sets)."""
     lg = np.asarray(hn16, np.float64) @ np.asarray(router, np.float64).T
     p = np.exp(lg - lg.max(-1, keepdims=True))
-    p = (p / p.sum(-1, keepdims=True)).astype(f16).astype(np.float64)
+    p = p / p.sum(-1, keepdims=True)
+    if not exact:
+        p = p.astype(f16).astype(np.float64)          # the reference's fp16 tie semantics
     g = topk_gate(p, k)
     if renorm:
         g = g / g.sum(1, keepdims=True)
@@ -246,7 +248,7 @@ def moe_layer(h16, mlp_norm, router, Wg, Wu, Wd, k, renorm=True, eps=1e-5, exact
     act = fp16(silu(fp16 g) * fp16 u), y_e = fp16(act Wd_e^T), out = fp16(h + fp16(sum g*y))."""
     h = np.asarray(h16, np.float64)
     hn = rms_norm(h, mlp_norm, eps, exact)
-    gate, chosen = moe_route(hn, router, k, renorm)
+    gate, chosen = moe_route(hn, router, k, renorm, exact)
     T, D = h.shape
     comb = np.zeros((T, D))
     for t in range(T):
@@ -283,6 +285,12 @@ def decode_layer(h16, w, cfg, K, V, pos, cos_row, sin_row, exact=False, trace=No
     a = attention(q[None, :, None, :], K[None], V[None], 1.0 / np.sqrt(dh), [pos + 1], exact=exact)
     a = a.reshape(1, H * dh)
     h1 = r16(h + linear(a, w["wo"], w.get("o_bias"), exact), exact)
+    if "router" in w:                     # MoE MLP (aneforge/moe.py:48-63), experts as dequantised fp32
+        out, _, _ = moe_layer(h1, w["mlp_norm"], w["router"], w["wgate_exps"], w["wup_exps"], w["wdown_exps"],
+                              cfg["top_k"], cfg.get("norm_topk_prob", True), eps, exact)
+        if trace is not None:
+            trace.append(out.copy())
+        return out
     hn = rms_norm(h1, w["mlp_norm"], eps, exact)
     g = linear(hn, w["wgate"], None, exact)
     u = linear(hn, w["wup"], None, exact)

@@ -161,7 +161,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs& a, float (&acc)[M]
       }
       case EPI_QKV: {
         const float other = shfl_xor(v, GROUP);
-        const int p = a.pos[m];
+        const int p = live ? a.pos[m] : -1;          // pos has a.M entries; padded rows store nothing
         if (writer && live && row < N && p >= 0 && p < a.kv_len) {
           const int dh = a.dh, half = dh >> 1;
           const float self16 = (float)(half_t)v, other16 = (float)(half_t)other;

@@ -137,6 +137,8 @@ def decode_attn(q, k, v, o=None, ctx_len=None, pos=None, scale=None, mask=None, 
     Hkv, Mmax = k.shape[1], k.shape[2]
     if k.shape[-1] != D or v.shape != k.shape:
         raise ValueError(f"decode_attn: k {tuple(k.shape)} / v {tuple(v.shape)} do not match q")
+    if mask is not None and (mask.dim() != 2 or mask.shape[0] < B or mask.shape[1] < Mmax or mask.stride(1) != 1):
+        raise ValueError(f"decode_attn: mask must be [B, >= {Mmax}] with unit column stride, got {tuple(mask.shape)}")
     if o is None:
         o = torch.empty_like(q)
     qbs, qhs = q_strides if q_strides else (q.stride(0), q.stride(1))

@@ -8,16 +8,20 @@
 // subtraction, fp32 softmax, fp16 output).  Optional additive mask [B][Skv] and causal
 // alignment for the af.sdpa entry (aneforge/graph.py:993-1040).
 //
-// Kernel 1 (partial): grid (splits, KVH, B); one 256-thread workgroup handles `chunk`
+// Partial kernel: grid (splits, KVH, B); one 256-thread workgroup handles `chunk`
 // positions of one kv head for all G query heads that share it, so each K/V byte is read
 // from HBM once per GQA group.  D/8 lanes cover one 16-byte row slice each; every lane
-// issues all its K and V loads before any math.  Scores stay in registers (two-pass
-// softmax inside the chunk), P@V accumulates in fp32.  Output: (m, l, o[D]) per
-// (b, h, split) in a caller-provided fp32 workspace.
-// The last workgroup to finish a (b, kvh) group (agent-scope fence + arrival counter, which it
-// resets, so graph replays need no memset) rescales and sums the split partials and writes
-// the fp16 output: one launch per call.  The workspace's counter tail must be zero before the
-// first call.
+// issues all its K and V loads first.  The loads do not wait for the context length: row
+// indices are clamped to the cache bound (max_len), and positions at or past the length are
+// masked afterwards (scores to -inf, V to 0), so the device-side position load overlaps the
+// KV stream.  Scores stay in registers (two-pass softmax inside the chunk), P@V accumulates
+// in fp32, and the split partials (m, l, o[D]) go to a caller-provided fp32 workspace.
+// The last workgroup to arrive for a (b, kvh) group (agent-scope release/acquire fences and
+// an arrival counter, which that workgroup resets, so graph replays need no memset) rescales
+// and sums the group's split partials and writes the fp16 output.  The workspace's counter
+// tail must be zero before the first call.  That variant is opt-in (AFX_ATTN_FUSED_COMBINE=1):
+// each workgroup's agent-scope release writes back its XCD's L2, which costs more than a
+// second launch, so by default a separate combine kernel merges the splits.
 #include <stdlib.h>
 #include "afx_common.h"
 
@@ -64,21 +68,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int L = seq_len(a, b);
   const int p0 = split * C;
-  if (p0 >= L) return;   // whole workgroup: the combine ignores splits past L
-
   const int dl = lane % LPP;       // which 8-dim slice
   const int pl = lane / LPP;       // which position within the step
 
-  h2 qh[G][4];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const half_t* qp = a.q + (size_t)b * a.q_bs + (size_t)(kvh * G + g) * a.q_hs + dl * 8;
-    u4 t = *(const u4*)qp;
-    qh[g][0] = as_h2(t.x); qh[g][1] = as_h2(t.y); qh[g][2] = as_h2(t.z); qh[g][3] = as_h2(t.w);
-  }
-
+  // K and V rows first (clamped to the cache bound, masked later), then q and the length
   const half_t* kb = a.k + (size_t)b * a.kv_bs + (size_t)kvh * a.kv_hs + dl * 8;
   const half_t* vb = a.v + (size_t)b * a.kv_bs + (size_t)kvh * a.kv_hs + dl * 8;
   u4 kv[NSTEP], vv[NSTEP];
@@ -87,14 +81,31 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   for (int s = 0; s < NSTEP; ++s) {
     const int p = p0 + (wave + 4 * s) * PPS + pl;
     posn[s] = p;
-    const int pc = p < L ? p : L - 1;
+    const int pc = p < a.Mmax ? p : a.Mmax - 1;
     kv[s] = __builtin_nontemporal_load((const u4*)(kb + (size_t)pc * D));
   }
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) {
-    const int pc = posn[s] < L ? posn[s] : L - 1;
+    const int pc = posn[s] < a.Mmax ? posn[s] : a.Mmax - 1;
     vv[s] = __builtin_nontemporal_load((const u4*)(vb + (size_t)pc * D));
   }
+  h2 qh[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const half_t* qp = a.q + (size_t)b * a.q_bs + (size_t)(kvh * G + g) * a.q_hs + dl * 8;
+    u4 t = *(const u4*)qp;
+    qh[g][0] = as_h2(t.x); qh[g][1] = as_h2(t.y); qh[g][2] = as_h2(t.z); qh[g][3] = as_h2(t.w);
+  }
+  // additive mask entries (af.sdpa), loaded unconditionally from a valid address
+  float mk[NSTEP];
+  const half_t* mrow = a.mask ? a.mask + (size_t)b * a.mask_bs : a.q;
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const int pc = posn[s] < a.Mmax ? posn[s] : a.Mmax - 1;
+    mk[s] = (float)mrow[a.mask ? pc : 0];
+  }
+  const int L = seq_len(a, b);
+  const bool active = p0 < L;      // workgroup-uniform: an empty split only arrives (fused mode)
 
   // scores (log2 domain), identical in all LPP lanes of a position
   float sc[NSTEP][G];
@@ -110,7 +121,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
       for (int m = LPP / 2; m >= 1; m >>= 1) t += shfl_xor(t, m);
       float x = t * a.scale_log2;
-      if (a.mask) x += (float)a.mask[(size_t)b * a.mask_bs + (posn[s] < L ? posn[s] : 0)] * 1.4426950408889634f;
+      if (a.mask) x += mk[s] * 1.4426950408889634f;
       sc[s][g] = posn[s] < L ? x : -INFINITY;
     }
   }
@@ -145,7 +156,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   }
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) {
-    const h2 v0 = as_h2(vv[s].x), v1 = as_h2(vv[s].y), v2 = as_h2(vv[s].z), v3 = as_h2(vv[s].w);
+    const bool ok = posn[s] < L;
+    const h2 v0 = as_h2(ok ? vv[s].x : 0u), v1 = as_h2(ok ? vv[s].y : 0u);
+    const h2 v2 = as_h2(ok ? vv[s].z : 0u), v3 = as_h2(ok ? vv[s].w : 0u);
     const float vf[8] = {(float)v0.x, (float)v0.y, (float)v1.x, (float)v1.y,
                          (float)v2.x, (float)v2.y, (float)v3.x, (float)v3.y};
 #pragma unroll
@@ -179,7 +192,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   __syncthreads();
 
   const int NSP = a.nsp;
-  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+  for (int idx = threadIdx.x; active && idx < G * D; idx += 256) {
     const int g = idx / D, d = idx - g * D;
     const float acc = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
     const size_t bh = (size_t)b * a.Hq + kvh * G + g;
@@ -191,16 +204,16 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   }
 
   if constexpr (!FUSED) return;            // a separate combine launch merges the splits
-  // ---- the last workgroup of this (b, kvh) merges all split partials (no second launch) ----
-  const int ns = (L + C - 1) / C;            // splits that ran for this sequence
+  // ---- the last workgroup of this (b, kvh) to arrive merges the group's split partials ----
+  const int ns = (L + C - 1) / C;            // splits that hold data for this sequence
   __shared__ int s_last;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // write back this workgroup's partials
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // this workgroup's partials, agent-visible
   __syncthreads();
   if (threadIdx.x == 0) {
     int* ctr = a.counters + (size_t)b * a.Hkv + kvh;
-    const int prev = atomicAdd(ctr, 1);
-    s_last = prev == ns - 1;
-    if (s_last) atomicExch(ctr, 0);          // every split has arrived: reset for the next launch
+    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (int)gridDim.x - 1;
+    if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next call
   }
   __syncthreads();
   if (!s_last) return;
@@ -256,11 +269,70 @@ __device__ void combine_group(const AttnArgs& a, int b, int kvh, int ns) {
   }
 }
 
-template <int D, int G>
+// Separate combine launch: one workgroup per (head, sequence).  Thread (d, part) owns output
+// dim d and a contiguous range of the head's splits; every global load (the partial rows,
+// m and l of split t, the length) is issued at once, so the kernel costs one memory round
+// trip.  Split t's weight is exp2(m_t - max) / sum_s exp2(m_s - max) * l_s; splits at or past
+// ceil(L / chunk) hold no data for this sequence and get weight 0.
+template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-  const int kvh = blockIdx.x, b = blockIdx.y;
+  constexpr int P = 256 / D;                    // threads per output dim
+  constexpr int NV4 = kMaxSplits / 4 / P;       // float4 partial loads per thread (upper bound)
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int d = t % D, part = t / D;
+  const int NSP = a.nsp;                        // multiple of 4, <= kMaxSplits
+  const int per = ((NSP / 4 + P - 1) / P) * 4;  // splits per part
+  const int s0 = part * per;
+  const size_t bh = (size_t)b * a.Hq + h;
+  const float* row = a.ws_o + (bh * D + d) * NSP;
+  f4 ov[NV4];
+#pragma unroll
+  for (int j = 0; j < NV4; ++j) {
+    int s = s0 + 4 * j;
+    s = s < NSP - 4 ? s : NSP - 4;              // clamped reads are masked by weight 0 below
+    ov[j] = __builtin_nontemporal_load((const f4*)(row + s));
+  }
+  const int sm = t < NSP ? t : NSP - 1;
+  float mt = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 0) * NSP + sm);
+  float lt = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 1) * NSP + sm);
   const int L = seq_len(a, b);
-  combine_group<D, G>(a, b, kvh, (L + a.chunk - 1) / a.chunk);
+  const int ns = (L + a.chunk - 1) / a.chunk;
+  const bool valid = t < ns;
+  mt = valid ? mt : -INFINITY;
+  lt = valid ? lt : 0.0f;
+
+  __shared__ float red_m[4], red_l[4], s_w[kMaxSplits], s_num[256];
+  float mx = wave_max(mt);
+  if (lane == 0) red_m[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  const float w = valid ? exp2f(mt - mx) : 0.0f;
+  const float den = wave_sum(w * lt);
+  if (lane == 0) red_l[wave] = den;
+  if (t < kMaxSplits) s_w[t] = w;
+  __syncthreads();
+  const float inv = 1.0f / (red_l[0] + red_l[1] + red_l[2] + red_l[3]);
+  float num = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV4; ++j) {
+    const int s = s0 + 4 * j;
+    const float e[4] = {ov[j].x, ov[j].y, ov[j].z, ov[j].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sp = s + i;
+      const bool use = 4 * j < per && sp < ns;
+      num = __builtin_fmaf(use ? s_w[sp < kMaxSplits ? sp : 0] : 0.0f, e[i], num);
+    }
+  }
+  s_num[t] = num;
+  __syncthreads();
+  if (part == 0) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < P; ++q) tot += s_num[q * D + d];
+    a.o[(size_t)b * a.q_bs + (size_t)h * a.q_hs + d] = (half_t)(tot * inv);
+  }
 }
 
 typedef void (*attn_fn)(AttnArgs);
@@ -284,17 +356,8 @@ static attn_fn pick_g(int G, int nstep) {
     default: return pick_steps<D, 8, F>(nstep);
   }
 }
-template <int D>
-static attn_fn pick_combine(int G) {
-  switch (G) {
-    case 1: return attn_combine_kernel<D, 1>;
-    case 2: return attn_combine_kernel<D, 2>;
-    case 4: return attn_combine_kernel<D, 4>;
-    default: return attn_combine_kernel<D, 8>;
-  }
-}
-// 0 = two launches (partials, then combine: no cross-workgroup fences), 1 = fused combine in
-// the last-arriving workgroup (release/acquire fences + arrival counter).
+// 0 = two launches (default: partials, then the combine kernel), 1 = combine in the
+// last-arriving workgroup (release/acquire fences + arrival counter; built for D = 128).
 static int g_attn_mode = -1;
 static int attn_mode() {
   if (g_attn_mode < 0) {
@@ -381,7 +444,7 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   a.ws_o = (float*)ws;
   a.ws_ml = a.ws_o + (size_t)B * Hq * D * a.nsp;
   a.counters = (int*)(a.ws_ml + (size_t)B * Hq * 2 * a.nsp);
-  const bool fused = attn_mode() == 1 && D == 128;     // the fused variant is built for D = 128 only
+  const bool fused = attn_mode() == 1 && D == 128;
   attn_fn fn;
   if (fused)
     fn = pick_g<128, true>(G, ns);
@@ -391,9 +454,9 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
   int rc = check_launch("afx_decode_attn");
   if (rc || fused) return rc;
-  attn_fn cf = D == 8 ? pick_combine<8>(G) : D == 16 ? pick_combine<16>(G) : D == 32 ? pick_combine<32>(G)
-             : D == 64 ? pick_combine<64>(G) : D == 128 ? pick_combine<128>(G) : pick_combine<256>(G);
-  hipLaunchKernelGGL(cf, dim3(Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
+  attn_fn cf = D == 8 ? attn_combine_kernel<8> : D == 16 ? attn_combine_kernel<16> : D == 32 ? attn_combine_kernel<32>
+             : D == 64 ? attn_combine_kernel<64> : D == 128 ? attn_combine_kernel<128> : attn_combine_kernel<256>;
+  hipLaunchKernelGGL(cf, dim3(Hq, B), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_attn(combine)");
 }
 

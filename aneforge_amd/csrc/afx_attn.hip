@@ -55,6 +55,66 @@ __device__ __forceinline__ int seq_len(const AttnArgs& a, int b) {
   return L < 1 ? 1 : L;
 }
 
+// Cross-lane reductions without LDS (DPP row permutations and the gfx950 permlane swaps).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// v_permlane16_swap(a, b) exchanges the odd 16-lane rows of a with the even rows of b, and
+// v_permlane32_swap the upper 32 lanes of a with the lower 32 lanes of b.  With b a copy of a,
+// afterwards a and b hold each row (half) and its partner row (half), so op(a, b) reduces over
+// lane pairs 16 (32) apart in every lane.  Issued as inline assembly on two distinct registers
+// (the s_nop covers the VALU-write-then-permlane hazard): this compiler's builtin returns the
+// same half twice when its two results are combined.
+__device__ __forceinline__ void swap16(float v, float& r0, float& r1) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b;
+  asm volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "=&v"(b));
+  r0 = __builtin_bit_cast(float, a);
+  r1 = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ void swap32(float v, float& r0, float& r1) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b;
+  asm volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "=&v"(b));
+  r0 = __builtin_bit_cast(float, a);
+  r1 = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float swap16_sum(float v) { float a, b; swap16(v, a, b); return a + b; }
+__device__ __forceinline__ float swap32_sum(float v) { float a, b; swap32(v, a, b); return a + b; }
+__device__ __forceinline__ float swap16_max(float v) { float a, b; swap16(v, a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float swap32_max(float v) { float a, b; swap32(v, a, b); return fmaxf(a, b); }
+// Sum over each aligned group of LPP consecutive lanes (quad_perm xor 1 / xor 2, then the half
+// and full row mirrors, which pair the two halves of an 8 / 16 lane group); all lanes of the
+// group receive the sum.
+template <int LPP>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (LPP >= 2) v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]
+  if constexpr (LPP >= 4) v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]
+  if constexpr (LPP >= 8) v += dpp<0x141>(v);   // row_half_mirror
+  if constexpr (LPP >= 16) v += dpp<0x140>(v);  // row_mirror
+  if constexpr (LPP >= 32) v = swap16_sum(v);
+  return v;
+}
+// Reduce over the lanes that hold the same slot of different groups (lane % LPP equal):
+// rotations within a 16-lane row, then the cross-row swaps.
+template <int LPP>
+__device__ __forceinline__ float across_sum(float v) {
+  if constexpr (LPP <= 1) v += dpp<0x121>(v);   // row_ror:1
+  if constexpr (LPP <= 2) v += dpp<0x122>(v);   // row_ror:2
+  if constexpr (LPP <= 4) v += dpp<0x124>(v);   // row_ror:4
+  if constexpr (LPP <= 8) v += dpp<0x128>(v);   // row_ror:8
+  if constexpr (LPP <= 16) v = swap16_sum(v);
+  return swap32_sum(v);
+}
+template <int LPP>
+__device__ __forceinline__ float across_max(float v) {
+  if constexpr (LPP <= 1) v = fmaxf(v, dpp<0x121>(v));
+  if constexpr (LPP <= 2) v = fmaxf(v, dpp<0x122>(v));
+  if constexpr (LPP <= 4) v = fmaxf(v, dpp<0x124>(v));
+  if constexpr (LPP <= 8) v = fmaxf(v, dpp<0x128>(v));
+  if constexpr (LPP <= 16) v = swap16_max(v);
+  return swap32_max(v);
+}
+
 template <int D, int G>
 __device__ void combine_group(const AttnArgs& a, int b, int kvh, int ns);
 
@@ -118,8 +178,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       t = dot2(qh[g][1], k1, t);
       t = dot2(qh[g][2], k2, t);
       t = dot2(qh[g][3], k3, t);
-#pragma unroll
-      for (int m = LPP / 2; m >= 1; m >>= 1) t += shfl_xor(t, m);
+      t = group_sum<LPP>(t);
       float x = t * a.scale_log2;
       if (a.mask) x += mk[s] * 1.4426950408889634f;
       sc[s][g] = posn[s] < L ? x : -INFINITY;
@@ -133,9 +192,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     float m = -INFINITY;
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) m = fmaxf(m, sc[s][g]);
-#pragma unroll
-    for (int sh = LPP; sh < 64; sh <<= 1) m = fmaxf(m, shfl_xor(m, sh));
-    mx[g] = m;
+    mx[g] = across_max<LPP>(m);
   }
   if (lane == 0)
 #pragma unroll
@@ -172,12 +229,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   // reduce across the position groups of the wavefront
 #pragma unroll
   for (int g = 0; g < G; ++g) {
+    l[g] = across_sum<LPP>(l[g]);
 #pragma unroll
-    for (int sh = LPP; sh < 64; sh <<= 1) {
-      l[g] += shfl_xor(l[g], sh);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[g][i] += shfl_xor(o[g][i], sh);
-    }
+    for (int i = 0; i < 8; ++i) o[g][i] = across_sum<LPP>(o[g][i]);
   }
   if (lane < LPP) {
 #pragma unroll
@@ -274,10 +328,10 @@ __device__ void combine_group(const AttnArgs& a, int b, int kvh, int ns) {
 // m and l of split t, the length) is issued at once, so the kernel costs one memory round
 // trip.  Split t's weight is exp2(m_t - max) / sum_s exp2(m_s - max) * l_s; splits at or past
 // ceil(L / chunk) hold no data for this sequence and get weight 0.
-template <int D>
+template <int D, int NV4>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   constexpr int P = 256 / D;                    // threads per output dim
-  constexpr int NV4 = kMaxSplits / 4 / P;       // float4 partial loads per thread (upper bound)
+  // NV4: float4 partial loads per thread, >= ceil(nsp / 4 / P) (chosen by the host)
   const int h = blockIdx.x, b = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int d = t % D, part = t / D;
@@ -336,6 +390,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 }
 
 typedef void (*attn_fn)(AttnArgs);
+
+template <int D>
+static attn_fn pick_combine(int per4) {
+  constexpr int P = 256 / D, MAX4 = kMaxSplits / 4 / P;
+  if (per4 <= 2 && 2 <= MAX4) return attn_combine_kernel<D, 2 <= MAX4 ? 2 : MAX4>;
+  if (per4 <= 4 && 4 <= MAX4) return attn_combine_kernel<D, 4 <= MAX4 ? 4 : MAX4>;
+  if (per4 <= 8 && 8 <= MAX4) return attn_combine_kernel<D, 8 <= MAX4 ? 8 : MAX4>;
+  if (per4 <= 16 && 16 <= MAX4) return attn_combine_kernel<D, 16 <= MAX4 ? 16 : MAX4>;
+  return attn_combine_kernel<D, MAX4>;
+}
 
 template <int D, int G, bool F>
 static attn_fn pick_steps(int nstep) {
@@ -454,8 +518,9 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
   int rc = check_launch("afx_decode_attn");
   if (rc || fused) return rc;
-  attn_fn cf = D == 8 ? attn_combine_kernel<8> : D == 16 ? attn_combine_kernel<16> : D == 32 ? attn_combine_kernel<32>
-             : D == 64 ? attn_combine_kernel<64> : D == 128 ? attn_combine_kernel<128> : attn_combine_kernel<256>;
+  const int per4 = ((a.nsp / 4) + (256 / D) - 1) / (256 / D);   // float4 loads each combine thread needs
+  attn_fn cf = D == 8 ? pick_combine<8>(per4) : D == 16 ? pick_combine<16>(per4) : D == 32 ? pick_combine<32>(per4)
+             : D == 64 ? pick_combine<64>(per4) : D == 128 ? pick_combine<128>(per4) : pick_combine<256>(per4);
   hipLaunchKernelGGL(cf, dim3(Hq, B), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_attn(combine)");
 }

@@ -65,11 +65,13 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
   }
   AFX_REQUIRE((long long)a.K * (fmt == FMT_F16 ? 2 : 1) < (1LL << 31), "%s: K=%d too large", what, a.K);
   const int ntiles = grid_for((a.N + R - 1) / R);
-  if (a.M == 1 && a.K == 4096 && a.ldx >= a.K) {
-    // one unit covers a row: the register-resident fast path (static LDS only)
-    gemv_fn fr = fmt == FMT_I8 ? pick_gemv_row_i8(eg, R, norm)
-               : fmt == FMT_Q4 ? pick_gemv_row_q4(eg, R, norm)
-                               : pick_gemv_row_f16(eg, R, norm);
+  const int nchunks = a.K / (fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 32 : 8);
+  const int fu = a.M == 1 ? fast_units(fmt, nchunks) : 0;
+  if (fu) {
+    // a whole row fits the lanes' registers: the register-resident fast path (static LDS only)
+    gemv_fn fr = fmt == FMT_I8 ? pick_gemv_row_i8(eg, R, norm, fu)
+               : fmt == FMT_Q4 ? pick_gemv_row_q4(eg, R, norm, fu)
+                               : pick_gemv_row_f16(eg, R, norm, fu);
     hipLaunchKernelGGL(fr, dim3(ntiles), dim3(256), 0, stream, a);
     return check_launch(what);
   }

@@ -379,27 +379,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   if (lane == 0) gemv_store<M, R, EG>(a, v, row0, e_pos, h_res, h_cs, h_sn);
 }
 
-// Fast path for one activation row (M = 1) when one unit covers a whole weight row
-// (K = 64 lanes x FastUnits chunks: 4096 for every format).  Each lane keeps the x values of its
-// own chunks in registers: without a norm they are read straight from global memory (no LDS,
-// no barrier); with the RMSNorm prologue the workgroup normalises x once (each thread two
-// 16-byte vectors of x and gamma), shares it through LDS, and every lane then reads its chunks.
-template <int FMT> struct FastUnits { static constexpr int value = FMT == FMT_I8 ? 4 : FMT == FMT_Q4 ? 2 : 8; };
-template <int FMT> struct FastK {
-  static constexpr int value = 64 * FastUnits<FMT>::value * Fmt<FMT>::kWeightsPerChunk;
-};
-
-template <int FMT, int R, int NORM, int EG>
+// Fast path for one activation row (M = 1) with K at most 64 lanes x U chunks (U a compile-time
+// constant per shape family: int8 K = 4096 -> 4, 11008 -> 11; Q4_0 4096 -> 2, 11008 -> 6;
+// fp16 4096 -> 8).  Each lane keeps the x values of its own U chunks in registers: without a
+// norm they are read straight from global memory (no LDS, no barrier); with the RMSNorm
+// prologue the workgroup normalises x once (each thread a few 16-byte vectors of x and gamma),
+// shares it through LDS, and every lane then reads its chunks.  Chunks past K (the last unit
+// of a ragged row) read a clamped address and are zeroed by a select.
+template <int FMT, int R, int NORM, int EG, int U>
 __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
-  constexpr int U = FastUnits<FMT>::value;
-  constexpr int K = FastK<FMT>::value;
   constexpr int XH = Fmt<FMT>::kXH2;
+  constexpr int KMAX = 64 * U * Fmt<FMT>::kWeightsPerChunk;
+  constexpr int NVT = (KMAX / 8 + 255) / 256;          // norm vectors per thread
   static_assert(EG == EG_PLAIN || R == 2, "paired epilogues process row pairs");
-  static_assert(K == 2048 * 2, "the fast path covers K = 4096");
-  __shared__ __align__(16) half_t xs[NORM ? K : 8];
+  __shared__ __align__(16) half_t xs[NORM ? KMAX : 8];
   __shared__ float red[4];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int N = a.N;
+  const int N = a.N, K = a.K;
+  const int nchunks = K / Fmt<FMT>::kWeightsPerChunk;
   const int ngroups = (N + R - 1) / R;
   const int g = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + wave);
   const bool live = g < ngroups;
@@ -410,15 +407,23 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
 
   // activations first: the lane's own chunks (no norm) or this thread's share of x and gamma
   h2 xv[U][XH];
-  u4 xq[2], gq[2];
+  u4 xq[NVT], gq[NVT];
+  const int nv = K >> 3;
   if constexpr (NORM) {
-    xq[0] = *(const u4*)(a.x + 8 * t);
-    xq[1] = *(const u4*)(a.x + 8 * (t + 256));
-    gq[0] = *(const u4*)(a.gamma + 8 * t);
-    gq[1] = *(const u4*)(a.gamma + 8 * (t + 256));
+#pragma unroll
+    for (int i = 0; i < NVT; ++i) {
+      int f = t + 256 * i;
+      f = f < nv ? f : nv - 1;
+      xq[i] = *(const u4*)(a.x + 8 * f);
+      gq[i] = *(const u4*)(a.gamma + 8 * f);
+    }
   } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) Fmt<FMT>::load_x(a.x, 64 * u + lane, xv[u]);
+    for (int u = 0; u < U; ++u) {
+      int c = 64 * u + lane;
+      c = c < nchunks ? c : nchunks - 1;
+      Fmt<FMT>::load_x(a.x, c, xv[u]);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -432,8 +437,10 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
     const half_t* dr = FMT == FMT_Q4 ? a.scale + (size_t)row * (K >> 5) : nullptr;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      w[u][r] = __builtin_nontemporal_load(wr + 64 * u + lane);
-      d[u][r] = load_scales<FMT>(dr, 64 * u + lane);
+      int c = 64 * u + lane;
+      c = c < nchunks ? c : nchunks - 1;
+      w[u][r] = __builtin_nontemporal_load(wr + c);
+      d[u][r] = load_scales<FMT>(dr, c);
     }
   }
   half_t h_scale[R], h_bias[R], h_res[1][R], h_cs[1][R], h_sn[1][R];
@@ -443,18 +450,19 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   if constexpr (NORM) {
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      ss = dot2(as_h2(xq[i].x), as_h2(xq[i].x), ss);
-      ss = dot2(as_h2(xq[i].y), as_h2(xq[i].y), ss);
-      ss = dot2(as_h2(xq[i].z), as_h2(xq[i].z), ss);
-      ss = dot2(as_h2(xq[i].w), as_h2(xq[i].w), ss);
+    for (int i = 0; i < NVT; ++i) {
+      float q = dot2(as_h2(xq[i].x), as_h2(xq[i].x), 0.0f);
+      q = dot2(as_h2(xq[i].y), as_h2(xq[i].y), q);
+      q = dot2(as_h2(xq[i].z), as_h2(xq[i].z), q);
+      q = dot2(as_h2(xq[i].w), as_h2(xq[i].w), q);
+      ss += t + 256 * i < nv ? q : 0.0f;
     }
     ss = wave_sum_uniform(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     const float rstd = 1.0f / __builtin_sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + a.eps);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NVT; ++i) {
       uint32_t* xw = (uint32_t*)&xq[i];
       const uint32_t* gw = (const uint32_t*)&gq[i];
 #pragma unroll
@@ -465,11 +473,17 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
         r.y = (half_t)(((float)xx.y * rstd) * (float)gg.y);
         xw[jj] = as_u32(r);
       }
-      *(u4*)(xs + 8 * (t + 256 * i)) = xq[i];
+      int f = t + 256 * i;
+      f = f < nv ? f : nv - 1;                       // a clamped duplicate rewrites its own value
+      *(u4*)(xs + 8 * f) = xq[i];
     }
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < U; ++u) Fmt<FMT>::load_x(xs, 64 * u + lane, xv[u]);
+    for (int u = 0; u < U; ++u) {
+      int c = 64 * u + lane;
+      c = c < nchunks ? c : nchunks - 1;
+      Fmt<FMT>::load_x(xs, c, xv[u]);
+    }
   }
   if (!live) return;   // no barrier follows
 
@@ -477,9 +491,23 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
+  for (int u = 0; u < U; ++u) {
+    const bool ok = 64 * u + lane < nchunks;
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = Fmt<FMT>::dot(w[u][r], xv[u], d[u][r], acc[r]);
+    for (int r = 0; r < R; ++r) {
+      u4 wv = w[u][r];
+      u2 dv = d[u][r];
+      if (u == U - 1) {                              // only the last unit can hold chunks past K
+        if constexpr (FMT == FMT_Q4) {
+          dv.x = ok ? dv.x : 0u;
+          dv.y = ok ? dv.y : 0u;
+        } else {
+          wv.x = ok ? wv.x : 0u; wv.y = ok ? wv.y : 0u; wv.z = ok ? wv.z : 0u; wv.w = ok ? wv.w : 0u;
+        }
+      }
+      acc[r] = Fmt<FMT>::dot(wv, xv[u], dv, acc[r]);
+    }
+  }
 
   float v[1][R];
 #pragma unroll
@@ -511,20 +539,33 @@ gemv_fn pick_gemv(int mt, int eg, int R, int xs) {
        : mt == 4 ? pick_gemv_eg<FMT, 4>(eg, R, xs) : pick_gemv_eg<FMT, 8>(eg, R, xs);
 }
 
+template <int FMT, int U>
+gemv_fn pick_gemv_row_u(int eg, int R, int norm) {
+  if (eg == EG_QKV) return norm ? gemv_row_kernel<FMT, 2, 1, EG_QKV, U> : gemv_row_kernel<FMT, 2, 0, EG_QKV, U>;
+  if (eg == EG_SWIGLU) return norm ? gemv_row_kernel<FMT, 2, 1, EG_SWIGLU, U> : gemv_row_kernel<FMT, 2, 0, EG_SWIGLU, U>;
+  if (R == 2) return norm ? gemv_row_kernel<FMT, 2, 1, EG_PLAIN, U> : gemv_row_kernel<FMT, 2, 0, EG_PLAIN, U>;
+  return norm ? gemv_row_kernel<FMT, 1, 1, EG_PLAIN, U> : gemv_row_kernel<FMT, 1, 0, EG_PLAIN, U>;
+}
+// Chunks per lane the fast path is built for, per format (0: none); see gemv_row_kernel.
+__host__ __device__ inline int fast_units(int fmt, int nchunks) {
+  const int u = (nchunks + 63) / 64;
+  if (fmt == FMT_I8) return u == 4 || u == 11 ? u : 0;
+  if (fmt == FMT_Q4) return u == 2 || u == 6 ? u : 0;
+  return u == 8 ? u : 0;
+}
 template <int FMT>
-gemv_fn pick_gemv_row(int eg, int R, int norm) {
-  if (eg == EG_QKV) return norm ? gemv_row_kernel<FMT, 2, 1, EG_QKV> : gemv_row_kernel<FMT, 2, 0, EG_QKV>;
-  if (eg == EG_SWIGLU) return norm ? gemv_row_kernel<FMT, 2, 1, EG_SWIGLU> : gemv_row_kernel<FMT, 2, 0, EG_SWIGLU>;
-  if (R == 2) return norm ? gemv_row_kernel<FMT, 2, 1, EG_PLAIN> : gemv_row_kernel<FMT, 2, 0, EG_PLAIN>;
-  return norm ? gemv_row_kernel<FMT, 1, 1, EG_PLAIN> : gemv_row_kernel<FMT, 1, 0, EG_PLAIN>;
+gemv_fn pick_gemv_row(int eg, int R, int norm, int U) {
+  if constexpr (FMT == FMT_I8) return U == 11 ? pick_gemv_row_u<FMT, 11>(eg, R, norm) : pick_gemv_row_u<FMT, 4>(eg, R, norm);
+  else if constexpr (FMT == FMT_Q4) return U == 6 ? pick_gemv_row_u<FMT, 6>(eg, R, norm) : pick_gemv_row_u<FMT, 2>(eg, R, norm);
+  else return pick_gemv_row_u<FMT, 8>(eg, R, norm);
 }
 
 // Per-format selectors, each compiled in its own translation unit.
 gemv_fn pick_gemv_i8(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_q4(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_f16(int mt, int eg, int R, int xs);
-gemv_fn pick_gemv_row_i8(int eg, int R, int norm);
-gemv_fn pick_gemv_row_q4(int eg, int R, int norm);
-gemv_fn pick_gemv_row_f16(int eg, int R, int norm);
+gemv_fn pick_gemv_row_i8(int eg, int R, int norm, int U);
+gemv_fn pick_gemv_row_q4(int eg, int R, int norm, int U);
+gemv_fn pick_gemv_row_f16(int eg, int R, int norm, int U);
 
 }  // namespace afx

@@ -3,6 +3,7 @@
 // instead of reaching a kernel with extents it does not expect.
 #include <stdlib.h>
 #include "afx_gemv_impl.h"
+#include "afx_mfma.h"
 
 namespace afx {
 
@@ -18,6 +19,17 @@ static int cu_count() {
 }
 
 static int mtile(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+// Activation rows from which a linear runs on MFMA (AFX_MFMA_MIN_M overrides; 0 disables).
+static int g_mfma_min = -1;
+static int mfma_min_rows() {
+  if (g_mfma_min < 0) {
+    const char* e = getenv("AFX_MFMA_MIN_M");
+    const int v = e ? atoi(e) : -1;
+    g_mfma_min = v == 0 ? 1 << 30 : v > 0 ? v : 4;
+  }
+  return g_mfma_min;
+}
 
 // Rows per group: 2 when the epilogue pairs rows (SwiGLU, RoPE), else 1 (a hint of 2 or the
 // AFX_GEMV_R environment variable selects row pairs for plain epilogues too).
@@ -53,6 +65,13 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
     AFX_REQUIRE(a.dh >= 2 && a.dh % 2 == 0 && a.nq % a.dh == 0 && a.nk % a.dh == 0 && a.pos && a.kcache &&
                     a.vcache,
                 "%s: bad fused-QKV arguments", what);
+  // 4+ activation rows without a norm prologue: the dot products go to MFMA
+  if (a.M >= mfma_min_rows() && eg != EG_QKV && !a.gamma && mfma_supported(fmt, a.K) && a.N % 4 == 0) {
+    MfmaArgs m = {};
+    m.w = a.w; m.scale = a.scale; m.x = a.x; m.ldx = a.ldx; m.y = a.y; m.ldy = a.ldy;
+    m.bias = a.bias; m.resid = a.resid; m.M = a.M; m.N = a.N; m.K = a.K; m.epi = a.epi;
+    return mfma_launch(fmt, m, 1, stream, what);
+  }
   const int mt = mtile(a.M);
   const int R = choose_rows(rows_hint, eg != EG_PLAIN);
   const bool norm = a.gamma != nullptr;

@@ -12,6 +12,8 @@
 // The grid covers all E experts; workgroups of experts with no tokens exit at once, so the
 // launch shape is fixed and the whole layer is graph-capturable (no host round trip).
 #include "afx_gemv_core.h"
+#include "afx_gemv_impl.h"
+#include "afx_mfma.h"
 
 namespace afx {
 
@@ -219,6 +221,15 @@ int afx_moe_topk(const float* logits, int T, int E, int k, int renorm, float* ga
 // W: [E][2F][D] gate/up interleaved rows (format fmt), x: normed hidden [T][D].
 int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int T, int k, int E, int F, int D,
                    const int* cnt, const int* list, void* act, int rows_hint, void* stream) {
+  if (rows_hint == 0 && mfma_supported(fmt, D) && F % 2 == 0) {
+    MfmaArgs m = {};
+    m.w = w; m.scale = (const half_t*)scale; m.x = (const half_t*)x; m.ldx = D; m.y = act; m.ldy = F;
+    m.cnt = cnt; m.list = list; m.T = T; m.k = k; m.x_by_token = 1; m.N = 2 * F; m.K = D; m.epi = EPI_SWIGLU;
+    m.w_es = fmt_row_bytes(fmt, D) * 2 * F;
+    m.s_es = fmt == FMT_Q4 ? 2LL * F * (D / 32) : fmt == FMT_I8 ? 2LL * F : 0;
+    AFX_REQUIRE(T >= 1 && k >= 1 && E >= 1, "afx_moe_gateup: bad sizes");
+    return mfma_launch(fmt, m, E, (hipStream_t)stream, "afx_moe_gateup");
+  }
   MoeArgs a = {};
   a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)x; a.ldx = D; a.y = act; a.ldy = F;
   a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = 2 * F; a.K = D; a.epi = 1; a.x_by_token = 1;
@@ -231,6 +242,15 @@ int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int
 // W: [E][D][F], act: [T*k][F] -> y: [T*k][D] fp32.
 int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F, int D,
                  const int* cnt, const int* list, float* y, int rows_hint, void* stream) {
+  if (rows_hint == 0 && mfma_supported(fmt, F) && D % 4 == 0) {
+    MfmaArgs m = {};
+    m.w = w; m.scale = (const half_t*)scale; m.x = (const half_t*)act; m.ldx = F; m.y = y; m.ldy = D;
+    m.cnt = cnt; m.list = list; m.T = T; m.k = k; m.x_by_token = 0; m.N = D; m.K = F; m.epi = EPI_F32;
+    m.w_es = fmt_row_bytes(fmt, F) * D;
+    m.s_es = fmt == FMT_Q4 ? (long long)D * (F / 32) : fmt == FMT_I8 ? (long long)D : 0;
+    AFX_REQUIRE(T >= 1 && k >= 1 && E >= 1, "afx_moe_down: bad sizes");
+    return mfma_launch(fmt, m, E, (hipStream_t)stream, "afx_moe_down");
+  }
   MoeArgs a = {};
   a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)act; a.ldx = F; a.y = y; a.ldy = D;
   a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = D; a.K = F; a.epi = 0; a.x_by_token = 0;

@@ -157,6 +157,58 @@ def bench_attn(args, ctx=None, B=None):
             "GBps": byts / (ms * 1e-3) / 1e9, "frac": byts / (ms * 1e-3) / HBM_PEAK, "copies": copies}
 
 
+def bench_moe(args):
+    """cfg4: one MoE decode layer, 8 Q4_0 experts (gate/up 14336x4096, down 4096x14336), top-2 with
+    renormalisation, 16 tokens, fp16 router ~N(0, 0.02), gamma = 1, h ~N(0, 1).  Expert codes are
+    uniform nibbles written straight into the superblock layout on the device (the layout is a
+    bit-preserving permutation of GGUF Q4_0), block scales |N(0, 0.02)| / 8.  Timed as a captured
+    graph of the whole layer (norm, router, top-k + bucketing, grouped gate/up + SwiGLU, grouped
+    down, weighted combine + residual); algorithmic bytes = distinct active experts x 99 090 432 B
+    + router + activations."""
+    import torch
+    from aneforge_amd import _kernels as K
+    E, k, D, F, T = 8, 2, 4096, 14336, 16
+    g = torch.Generator(device="cuda").manual_seed(4)
+    gu_w = torch.randint(0, 256, (E * 2 * F, D // 2), dtype=torch.uint8, device="cuda", generator=g)
+    gu_d = (torch.randn((E * 2 * F, D // 32), device="cuda", generator=g).abs() * (0.02 / 8)).half()
+    dn_w = torch.randint(0, 256, (E * D, F // 2), dtype=torch.uint8, device="cuda", generator=g)
+    dn_d = (torch.randn((E * D, F // 32), device="cuda", generator=g).abs() * (0.02 / 8)).half()
+    router = (torch.randn((E, D), device="cuda", generator=g) * 0.02).half()
+    gamma = torch.ones(D, dtype=torch.float16, device="cuda")
+    h = torch.randn((T, D), device="cuda", generator=g).half()
+    hout = torch.empty_like(h)           # the layer output goes elsewhere so every replay routes alike
+    hn = torch.empty_like(h)
+    logits = torch.empty((T, E), dtype=torch.float32, device="cuda")
+    gate = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    sel = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    cnt = torch.empty((E,), dtype=torch.int32, device="cuda")
+    lst = torch.empty((E, T), dtype=torch.int32, device="cuda")
+    act = torch.empty((T * k, F), dtype=torch.float16, device="cuda")
+    y = torch.empty((T * k, D), dtype=torch.float32, device="cuda")
+
+    def layer():
+        K.rmsnorm(h, gamma, 1e-5, y=hn)
+        for r0 in range(0, T, 8):
+            K.linear("fp16", router, None, hn[r0:r0 + 8], y=logits[r0:r0 + 8], out_f32=True)
+        K.moe_topk(logits, k, True, gate, sel, cnt, lst)
+        K.moe_gateup("q4_0", gu_w, gu_d, hn, k, E, F, cnt, lst, act=act)
+        K.moe_down("q4_0", dn_w, dn_d, act, T, k, E, F, D, cnt, lst, y=y)
+        K.moe_combine(h, y, gate, out=hout)
+
+    layer()
+    torch.cuda.synchronize()
+    active = int((cnt > 0).sum().item())
+    gr = Graph(layer)
+    gr.launch()
+    reps = max(2, args.steps // 8)
+    ms = gr.time_ms(reps)
+    expert_bytes = 2 * F * (D // 32) * 18 + D * (F // 32) * 18
+    byts = active * expert_bytes + E * D * 2 + 2 * T * D * 2 + 2 * D
+    return {"workload": "cfg4 MoE decode layer: 8 Q4_0 experts, top-2, d4096, ffn 14336, 16 tokens",
+            "active_experts": active, "us": ms * 1e3, "bytes": byts, "GBps": byts / (ms * 1e-3) / 1e9,
+            "frac": byts / (ms * 1e-3) / HBM_PEAK}
+
+
 def bench_kernels(args):
     out = []
     a = argparse.Namespace(**vars(args))
@@ -169,6 +221,7 @@ def bench_kernels(args):
     for B in (1, 16):
         for ctx in (512, 2048, 8192):
             out.append(bench_attn(a, ctx, B))
+    out.append(bench_moe(a))
     return out
 
 
@@ -365,6 +418,9 @@ def main():
         return
     if args.workload == "attn":
         print(json.dumps(bench_attn(args)))
+        return
+    if args.workload == "moe":
+        print(json.dumps(bench_moe(args)))
         return
     if args.workload == "decode":
         res = bench_decode(args)

@@ -14,6 +14,7 @@ what the pinning tests compare against Hugging Face transformers and torch.
 Pinning status (see tests/test_oracle.py):
   quantize_per_row, dequant_w8          pinned: closed form + KATs (half-even rounding)
   q4_0 pack/unpack/dequant, quantize     pinned: ggml spec KATs + brute-force loop
+  dequant_q4_0_f16                      pinned: KAT (fp16 rounding of the fp32 product)
   quantize_blockwise                    pinned: closed form + reference property tests
   rms_norm                              pinned: torch + invariants
   rope_tables / rope / llama3 scaling    pinned: transformers' rope utilities + HF formula
@@ -100,6 +101,13 @@ def dequant_q4_0(blocks, N, K):
     codes, d = unpack_q4_0(blocks, N, K)
     vals = codes.astype(np.float32) - 8.0
     return (vals.reshape(N, K // Q4_BLOCK, Q4_BLOCK) * d.astype(np.float32)[:, :, None]).reshape(N, K)
+
+
+def dequant_q4_0_f16(blocks, N, K):
+    """The weights the reference multiplies with for a GGUF Q4_0 tensor: the ggml dequantisation
+    (code-8)*d taken in fp32, then converted to float16 (GGUFView.get's default dtype,
+    aneforge/_gguf.py:34-39).  Returned as fp32 holding those fp16 values."""
+    return dequant_q4_0(blocks, N, K).astype(f16).astype(np.float32)
 
 
 def quantize_q4_0(W):

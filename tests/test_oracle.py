@@ -317,3 +317,17 @@ def test_decoder_gqa_mapping_is_not_interleaved():
         lw["wo"] = wo[:, [0, 2, 1, 3]].reshape(lw["wo"].shape[0], 4 * dh)
     _, bad = ref.generate(prompt, 1, W, cfg, M=8, exact=True)
     assert np.abs(bad[0] - want).max() > 1e-3
+
+
+def test_q4_0_f16_dequant_matches_reference_rounding():
+    # GGUFView.get converts the fp32 ggml dequantisation to float16 (aneforge/_gguf.py:34-39):
+    # d = fp16(0.1) = 0.0999755859375, code 15 -> 7 * d = 0.6998291015625 (exact in fp32); the fp16
+    # grid there has spacing 2^-11, so it rounds to 1433/2048 = 0.69970703125 (1434/2048 is farther)
+    d = np.full((1, 1), 0.1, np.float16)
+    codes = np.full((1, 32), 15, np.uint8)
+    blocks = ref.pack_q4_0(codes, d)
+    exact = ref.dequant_q4_0(blocks, 1, 32)
+    assert exact[0, 0] == np.float32(0.6998291015625)
+    r = ref.dequant_q4_0_f16(blocks, 1, 32)
+    assert r[0, 0] == np.float32(1433 / 2048)
+    assert np.all(r == r[0, 0])

@@ -8,20 +8,19 @@
 // subtraction, fp32 softmax, fp16 output).  Optional additive mask [B][Skv] and causal
 // alignment for the af.sdpa entry (aneforge/graph.py:993-1040).
 //
-// Partial kernel: grid (splits, KVH, B); one 256-thread workgroup handles `chunk`
-// positions of one kv head for all G query heads that share it, so each K/V byte is read
-// from HBM once per GQA group.  D/8 lanes cover one 16-byte row slice each; every lane
+// Partial kernel: grid (splits, KVH, B); one workgroup of kAttnWaves wavefronts handles
+// `chunk` positions of one kv head for all G query heads that share it, so each K/V byte is
+// read from HBM once per GQA group.  D/8 lanes cover one 16-byte row slice each; every lane
 // issues all its K and V loads first.  The loads do not wait for the context length: row
 // indices are clamped to the cache bound (max_len), and positions at or past the length are
 // masked afterwards (scores to -inf, V to 0), so the device-side position load overlaps the
 // KV stream.  Scores stay in registers (two-pass softmax inside the chunk), P@V accumulates
-// in fp32, and the split partials (m, l, o[D]) go to a caller-provided fp32 workspace.
-// The last workgroup to arrive for a (b, kvh) group (agent-scope release/acquire fences and
-// an arrival counter, which that workgroup resets, so graph replays need no memset) rescales
-// and sums the group's split partials and writes the fp16 output.  The workspace's counter
-// tail must be zero before the first call.  That variant is opt-in (AFX_ATTN_FUSED_COMBINE=1):
-// each workgroup's agent-scope release writes back its XCD's L2, which costs more than a
-// second launch, so by default a separate combine kernel merges the splits.
+// in fp32, and the per-position-group partial sums meet in LDS (one pass per head block)
+// before the split partials (m, l, o[D]) go to a caller-provided fp32 workspace.
+// Combine kernel: one thread per (head, dim) merges that dim's split partials in one memory
+// round trip.  (A single-launch variant, in which the last workgroup to arrive merges the
+// splits, needs an agent-scope release per workgroup; on this part that writes back the
+// XCD's L2 and costs more than the second launch, so the merge is a launch of its own.)
 #include <stdlib.h>
 #include "afx_common.h"
 
@@ -38,7 +37,6 @@ struct AttnArgs {
   const int* pos;      // optional: ctx length of sequence b = pos[b] + 1 (device)
   float* ws_o;         // [B][Hq][D][nsp] split partial outputs (a (head, dim) row is contiguous)
   float* ws_ml;        // [B][Hq][2][nsp] split max (log2 domain) and row sum
-  int* counters;       // [B][Hkv] arrival counters (zero before first use; reset by the last arrival)
   long long q_bs, q_hs, kv_bs, kv_hs;
   long long mask_bs;
   int B, Hq, Hkv, L, Mmax, chunk, nsplit, nsp, causal_off;  // causal_off < 0: no causal masking
@@ -115,16 +113,52 @@ __device__ __forceinline__ float across_max(float v) {
   return swap32_max(v);
 }
 
-template <int D, int G>
-__device__ void combine_group(const AttnArgs& a, int b, int kvh, int ns);
+// Full-wavefront reductions through DPP (row shifts, then the row broadcasts into lane 63,
+// read back as a uniform scalar).  Lanes a step does not write keep `old`: 0 for a sum,
+// their own value for a max.
+template <int CTRL, int RMASK, bool MAX>
+__device__ __forceinline__ float dpp_combine(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  const float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(MAX ? iv : 0, iv, CTRL, RMASK, 0xf, false));
+  return MAX ? fmaxf(v, o) : v + o;
+}
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce_uniform(float v) {
+  v = dpp_combine<0x111, 0xf, MAX>(v);   // row_shr:1
+  v = dpp_combine<0x112, 0xf, MAX>(v);   // row_shr:2
+  v = dpp_combine<0x114, 0xf, MAX>(v);   // row_shr:4
+  v = dpp_combine<0x118, 0xf, MAX>(v);   // row_shr:8: lane 15 of each row holds the row's result
+  v = dpp_combine<0x142, 0xa, MAX>(v);   // row_bcast:15 into rows 1 and 3
+  v = dpp_combine<0x143, 0xc, MAX>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the total
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+// Sum over the lanes of a 16-lane row that hold the same slot (lane % LPP), for LPP <= 8.
+template <int LPP>
+__device__ __forceinline__ float row_slot_sum(float v) {
+  if constexpr (LPP <= 1) v += dpp<0x121>(v);   // row_ror:1
+  if constexpr (LPP <= 2) v += dpp<0x122>(v);   // row_ror:2
+  if constexpr (LPP <= 4) v += dpp<0x124>(v);   // row_ror:4
+  if constexpr (LPP <= 8) v += dpp<0x128>(v);   // row_ror:8
+  return v;
+}
 
-template <int D, int G, int NSTEP, bool FUSED>
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
-  constexpr int LPP = D / 8;        // lanes per position (16 B each)
-  constexpr int PPS = 64 / LPP;     // positions per wavefront step
-  constexpr int C = NSTEP * 4 * PPS;
-  __shared__ float red_m[4][G], red_l[4][G];
-  __shared__ float red_o[4][G][D];
+constexpr int kRedBytes = 32768;   // LDS for the cross-position partial sums of one pass
+
+// Partial kernel: grid (splits, KVH, B), NW wavefronts.  D/8 lanes cover one position's
+// 16-byte slices; a wavefront step covers 64/(D/8) positions, the workgroup NSTEP steps.
+template <int D, int G, int NSTEP, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_partial_kernel(AttnArgs a) {
+  constexpr int LPP = D / 8;                   // lanes per position
+  constexpr int PPS = 64 / LPP;                // positions per wavefront step
+  constexpr int C = NSTEP * NW * PPS;          // positions per workgroup (the split chunk)
+  constexpr int RG = LPP >= 16 ? PPS : 4;      // partial groups per wavefront after the in-row sums
+  constexpr int Q = NW * RG;                   // partial groups per workgroup
+  constexpr int HB0 = kRedBytes / (Q * D * 4);
+  constexpr int HB = HB0 >= G ? G : (HB0 >= 1 ? HB0 : 1);   // heads per LDS reduction pass
+  static_assert(G % HB == 0, "heads per pass must divide the group");
+  __shared__ float red_m[NW][G];
+  __shared__ float red_l[Q][G];
+  __shared__ float red_o[Q][HB][D];
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -139,7 +173,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   int posn[NSTEP];
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) {
-    const int p = p0 + (wave + 4 * s) * PPS + pl;
+    const int p = p0 + (wave + NW * s) * PPS + pl;
     posn[s] = p;
     const int pc = p < a.Mmax ? p : a.Mmax - 1;
     kv[s] = __builtin_nontemporal_load((const u4*)(kb + (size_t)pc * D));
@@ -165,7 +199,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     mk[s] = (float)mrow[a.mask ? pc : 0];
   }
   const int L = seq_len(a, b);
-  const bool active = p0 < L;      // workgroup-uniform: an empty split only arrives (fused mode)
+  const bool active = p0 < L;      // workgroup-uniform: a split past the length stores an empty partial
 
   // scores (log2 domain), identical in all LPP lanes of a position
   float sc[NSTEP][G];
@@ -199,8 +233,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     for (int g = 0; g < G; ++g) red_m[wave][g] = mx[g];
   __syncthreads();
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    mx[g] = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
+  for (int g = 0; g < G; ++g) {
+    float m = red_m[0][g];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, red_m[w][g]);
+    mx[g] = m;
+  }
 
   // probabilities, row sums and P@V
   float o[G][8];
@@ -220,215 +258,148 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
                          (float)v2.x, (float)v2.y, (float)v3.x, (float)v3.y};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float p = exp2f(sc[s][g] - mx[g]);   // 0 for masked positions
+      const float p = __builtin_amdgcn_exp2f(sc[s][g] - mx[g]);   // 0 for masked positions
       l[g] += p;
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[g][i] = __builtin_fmaf(p, vf[i], o[g][i]);
     }
   }
-  // reduce across the position groups of the wavefront
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = across_sum<LPP>(l[g]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[g][i] = across_sum<LPP>(o[g][i]);
-  }
-  if (lane < LPP) {
+  // narrow heads: sum the positions that share a 16-lane row first
+  if constexpr (LPP <= 8) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+      l[g] = row_slot_sum<LPP>(l[g]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) red_o[wave][g][dl * 8 + i] = o[g][i];
+      for (int i = 0; i < 8; ++i) o[g][i] = row_slot_sum<LPP>(o[g][i]);
     }
   }
-  if (lane == 0)
+  // the remaining Q partial groups meet in LDS
+  const bool writer = LPP >= 16 || (lane & 15) < LPP;
+  const int q = wave * RG + (LPP >= 16 ? lane / LPP : lane >> 4);
+  if (writer && dl == 0)
 #pragma unroll
-    for (int g = 0; g < G; ++g) red_l[wave][g] = l[g];
-  __syncthreads();
-
+    for (int g = 0; g < G; ++g) red_l[q][g] = l[g];
   const int NSP = a.nsp;
-  for (int idx = threadIdx.x; active && idx < G * D; idx += 256) {
-    const int g = idx / D, d = idx - g * D;
-    const float acc = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
-    const size_t bh = (size_t)b * a.Hq + kvh * G + g;
-    a.ws_o[(bh * D + d) * NSP + split] = acc;
-    if (d == 0) {
-      a.ws_ml[(bh * 2 + 0) * NSP + split] = mx[g];
-      a.ws_ml[(bh * 2 + 1) * NSP + split] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
-    }
-  }
-
-  if constexpr (!FUSED) return;            // a separate combine launch merges the splits
-  // ---- the last workgroup of this (b, kvh) to arrive merges the group's split partials ----
-  const int ns = (L + C - 1) / C;            // splits that hold data for this sequence
-  __shared__ int s_last;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // this workgroup's partials, agent-visible
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int* ctr = a.counters + (size_t)b * a.Hkv + kvh;
-    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (int)gridDim.x - 1;
-    if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next call
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // see the other workgroups' partials
-  combine_group<D, G>(a, b, kvh, ns);
-}
-
-// Merge the ns split partials of one (b, kvh) group: per head the global max and denominator,
-// then every output (head, dim) sums its contiguous row of partials with float4 loads.
-template <int D, int G>
-__device__ void combine_group(const AttnArgs& a, int b, int kvh, int ns) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int NSP = a.nsp;
-  __shared__ float s_w[G][kMaxSplits];       // exp2(m_s - M) / den per (head, split)
-  __shared__ float s_l[G][kMaxSplits];
-  for (int i = threadIdx.x; i < G * ns; i += 256) {
-    const int g = i / ns, sp = i - g * ns;
-    const size_t bh = (size_t)b * a.Hq + kvh * G + g;
-    s_w[g][sp] = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 0) * NSP + sp);
-    s_l[g][sp] = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 1) * NSP + sp);
-  }
-  __syncthreads();
-  for (int g = wave; g < G; g += 4) {
-    float m = -INFINITY;
-    for (int sp = lane; sp < ns; sp += 64) m = fmaxf(m, s_w[g][sp]);
-    m = wave_max(m);
-    float den = 0.0f;
-    for (int sp = lane; sp < ns; sp += 64) den += exp2f(s_w[g][sp] - m) * s_l[g][sp];
-    den = wave_sum(den);
-    const float inv = 1.0f / den;
-    for (int sp = lane; sp < ns; sp += 64) s_w[g][sp] = exp2f(s_w[g][sp] - m) * inv;
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-    const int g = idx / D, d = idx - g * D;
-    const float* row = a.ws_o + (((size_t)b * a.Hq + kvh * G + g) * D + d) * NSP;
-    float num = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += 32) {
-      f4 v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        v[j] = s0 + 4 * j < ns ? __builtin_nontemporal_load((const f4*)(row + s0 + 4 * j)) : (f4){0.f, 0.f, 0.f, 0.f};
+  for (int h0 = 0; h0 < G; h0 += HB) {
+    if (h0) __syncthreads();                  // the previous pass has read red_o
+    if (writer) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int sp = s0 + 4 * j;
-        if (sp + 0 < ns) num = __builtin_fmaf(s_w[g][sp + 0], v[j].x, num);
-        if (sp + 1 < ns) num = __builtin_fmaf(s_w[g][sp + 1], v[j].y, num);
-        if (sp + 2 < ns) num = __builtin_fmaf(s_w[g][sp + 2], v[j].z, num);
-        if (sp + 3 < ns) num = __builtin_fmaf(s_w[g][sp + 3], v[j].w, num);
+      for (int g = 0; g < HB; ++g) {
+        *(f4*)&red_o[q][g][dl * 8] = (f4){o[h0 + g][0], o[h0 + g][1], o[h0 + g][2], o[h0 + g][3]};
+        *(f4*)&red_o[q][g][dl * 8 + 4] = (f4){o[h0 + g][4], o[h0 + g][5], o[h0 + g][6], o[h0 + g][7]};
       }
     }
-    a.o[(size_t)b * a.q_bs + (size_t)(kvh * G + g) * a.q_hs + d] = (half_t)num;
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < HB * D; idx += NW * 64) {
+      const int g = idx / D, d = idx - g * D;
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < Q; ++j) acc += red_o[j][g][d];
+      const size_t bh = (size_t)b * a.Hq + kvh * G + h0 + g;
+      float* orow = a.ws_o + (bh * D + d) * NSP;
+      orow[split] = active ? acc : 0.0f;
+      for (int t = a.nsplit; split == a.nsplit - 1 && t < NSP; ++t) orow[t] = 0.0f;   // padding splits
+      if (d == 0) {
+        float lt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < Q; ++j) lt += red_l[j][h0 + g];
+        float* mrow = a.ws_ml + bh * 2 * NSP;
+        mrow[split] = active ? mx[h0 + g] : -INFINITY;
+        mrow[NSP + split] = active ? lt : 0.0f;
+        for (int t = a.nsplit; split == a.nsplit - 1 && t < NSP; ++t) {
+          mrow[t] = -INFINITY;
+          mrow[NSP + t] = 0.0f;
+        }
+      }
+    }
   }
 }
 
-// Separate combine launch: one workgroup per (head, sequence).  Thread (d, part) owns output
-// dim d and a contiguous range of the head's splits; every global load (the partial rows,
-// m and l of split t, the length) is issued at once, so the kernel costs one memory round
-// trip.  Split t's weight is exp2(m_t - max) / sum_s exp2(m_s - max) * l_s; splits at or past
-// ceil(L / chunk) hold no data for this sequence and get weight 0.
+// Combine launch: grid (Hq, B), max(D, 64) threads; thread d owns output dim d and issues
+// all its loads at once (its dim's row of split partials as NV4 float4s, the maxima and sums
+// of splits lane and lane + 64), so the kernel costs one memory round trip.  Every split slot
+// below nsp holds a partial from the same call (splits past the length and the padding slots
+// hold m = -inf, l = 0, o = 0), so the weights need no length:
+// w_t = exp2(m_t - max) / sum_s exp2(m_s - max) * l_s.  Every wavefront derives the weights
+// itself with DPP reductions, so there is no barrier.
 template <int D, int NV4>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-  constexpr int P = 256 / D;                    // threads per output dim
-  // NV4: float4 partial loads per thread, >= ceil(nsp / 4 / P) (chosen by the host)
+__global__ __launch_bounds__(D < 64 ? 64 : D) void attn_combine_kernel(AttnArgs a) {
+  constexpr int NT = D < 64 ? 64 : D;
+  static_assert(kMaxSplits == 128 && NV4 * 4 <= kMaxSplits, "two split statistics per lane");
   const int h = blockIdx.x, b = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int d = t % D, part = t / D;
   const int NSP = a.nsp;                        // multiple of 4, <= kMaxSplits
-  const int per = ((NSP / 4 + P - 1) / P) * 4;  // splits per part
-  const int s0 = part * per;
   const size_t bh = (size_t)b * a.Hq + h;
+  const int d = t < D ? t : D - 1;
   const float* row = a.ws_o + (bh * D + d) * NSP;
   f4 ov[NV4];
 #pragma unroll
   for (int j = 0; j < NV4; ++j) {
-    int s = s0 + 4 * j;
-    s = s < NSP - 4 ? s : NSP - 4;              // clamped reads are masked by weight 0 below
+    const int s = 4 * j < NSP - 4 ? 4 * j : NSP - 4;   // clamped repeats get weight 0 below
     ov[j] = __builtin_nontemporal_load((const f4*)(row + s));
   }
-  const int sm = t < NSP ? t : NSP - 1;
-  float mt = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 0) * NSP + sm);
-  float lt = __builtin_nontemporal_load(a.ws_ml + (bh * 2 + 1) * NSP + sm);
-  const int L = seq_len(a, b);
-  const int ns = (L + a.chunk - 1) / a.chunk;
-  const bool valid = t < ns;
-  mt = valid ? mt : -INFINITY;
-  lt = valid ? lt : 0.0f;
-
-  __shared__ float red_m[4], red_l[4], s_w[kMaxSplits], s_num[256];
-  float mx = wave_max(mt);
-  if (lane == 0) red_m[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-  const float w = valid ? exp2f(mt - mx) : 0.0f;
-  const float den = wave_sum(w * lt);
-  if (lane == 0) red_l[wave] = den;
-  if (t < kMaxSplits) s_w[t] = w;
-  __syncthreads();
-  const float inv = 1.0f / (red_l[0] + red_l[1] + red_l[2] + red_l[3]);
+  const float* mrow = a.ws_ml + bh * 2 * NSP;
+  const bool va = lane < NSP, vb = lane + 64 < NSP;
+  const int sa = va ? lane : 0, sb = vb ? lane + 64 : 0;
+  const float ma = __builtin_nontemporal_load(mrow + sa), la = __builtin_nontemporal_load(mrow + NSP + sa);
+  const float mb = __builtin_nontemporal_load(mrow + sb), lb = __builtin_nontemporal_load(mrow + NSP + sb);
+  const float mx = wave_reduce_uniform<true>(fmaxf(va ? ma : -INFINITY, vb ? mb : -INFINITY));
+  const float wa = va ? __builtin_amdgcn_exp2f(ma - mx) : 0.0f;   // exp2(-inf) = 0 for empty splits
+  const float wb = vb ? __builtin_amdgcn_exp2f(mb - mx) : 0.0f;
+  const float inv = 1.0f / wave_reduce_uniform<false>(wa * la + wb * lb);
+  __shared__ float s_w[NT / 64][kMaxSplits];    // per-wavefront copy: written and read by one wavefront
+  s_w[wave][lane] = wa * inv;
+  s_w[wave][lane + 64] = wb * inv;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float num = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV4; ++j) {
-    const int s = s0 + 4 * j;
-    const float e[4] = {ov[j].x, ov[j].y, ov[j].z, ov[j].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int sp = s + i;
-      const bool use = 4 * j < per && sp < ns;
-      num = __builtin_fmaf(use ? s_w[sp < kMaxSplits ? sp : 0] : 0.0f, e[i], num);
-    }
+    const f4 w = *(const f4*)&s_w[wave][4 * j];
+    num = __builtin_fmaf(w.x, ov[j].x, num);
+    num = __builtin_fmaf(w.y, ov[j].y, num);
+    num = __builtin_fmaf(w.z, ov[j].z, num);
+    num = __builtin_fmaf(w.w, ov[j].w, num);
   }
-  s_num[t] = num;
-  __syncthreads();
-  if (part == 0) {
-    float tot = 0.0f;
-#pragma unroll
-    for (int q = 0; q < P; ++q) tot += s_num[q * D + d];
-    a.o[(size_t)b * a.q_bs + (size_t)h * a.q_hs + d] = (half_t)(tot * inv);
-  }
+  if (t < D) a.o[(size_t)b * a.q_bs + (size_t)h * a.q_hs + d] = (half_t)num;
 }
 
 typedef void (*attn_fn)(AttnArgs);
 
+// NV4 float4 loads per combine thread: the smallest of 1, 2, 4, 8, 16, 32 covering nsp splits.
 template <int D>
-static attn_fn pick_combine(int per4) {
-  constexpr int P = 256 / D, MAX4 = kMaxSplits / 4 / P;
-  if (per4 <= 2 && 2 <= MAX4) return attn_combine_kernel<D, 2 <= MAX4 ? 2 : MAX4>;
-  if (per4 <= 4 && 4 <= MAX4) return attn_combine_kernel<D, 4 <= MAX4 ? 4 : MAX4>;
-  if (per4 <= 8 && 8 <= MAX4) return attn_combine_kernel<D, 8 <= MAX4 ? 8 : MAX4>;
-  if (per4 <= 16 && 16 <= MAX4) return attn_combine_kernel<D, 16 <= MAX4 ? 16 : MAX4>;
-  return attn_combine_kernel<D, MAX4>;
+static attn_fn pick_combine(int nsp) {
+  const int n4 = (nsp + 3) / 4;
+  if (n4 <= 1) return attn_combine_kernel<D, 1>;
+  if (n4 <= 2) return attn_combine_kernel<D, 2>;
+  if (n4 <= 4) return attn_combine_kernel<D, 4>;
+  if (n4 <= 8) return attn_combine_kernel<D, 8>;
+  if (n4 <= 16) return attn_combine_kernel<D, 16>;
+  return attn_combine_kernel<D, 32>;
 }
 
-template <int D, int G, bool F>
+constexpr int kAttnWaves = 4;   // wavefronts per partial workgroup
+
+template <int D, int G>
 static attn_fn pick_steps(int nstep) {
   switch (nstep) {
-    case 1: return attn_partial_kernel<D, G, 1, F>;
-    case 2: return attn_partial_kernel<D, G, 2, F>;
-    case 4: return attn_partial_kernel<D, G, 4, F>;
-    case 8: return attn_partial_kernel<D, G, 8, F>;
-    default: return attn_partial_kernel<D, G, 16, F>;
+    case 1: return attn_partial_kernel<D, G, 1, kAttnWaves>;
+    case 2: return attn_partial_kernel<D, G, 2, kAttnWaves>;
+    case 4: return attn_partial_kernel<D, G, 4, kAttnWaves>;
+    case 8: return attn_partial_kernel<D, G, 8, kAttnWaves>;
+    default: return attn_partial_kernel<D, G, 16, kAttnWaves>;
   }
 }
-template <int D, bool F>
+template <int D>
 static attn_fn pick_g(int G, int nstep) {
   switch (G) {
-    case 1: return pick_steps<D, 1, F>(nstep);
-    case 2: return pick_steps<D, 2, F>(nstep);
-    case 4: return pick_steps<D, 4, F>(nstep);
-    default: return pick_steps<D, 8, F>(nstep);
+    case 1: return pick_steps<D, 1>(nstep);
+    case 2: return pick_steps<D, 2>(nstep);
+    case 4: return pick_steps<D, 4>(nstep);
+    default: return pick_steps<D, 8>(nstep);
   }
-}
-// 0 = two launches (default: partials, then the combine kernel), 1 = combine in the
-// last-arriving workgroup (release/acquire fences + arrival counter; built for D = 128).
-static int g_attn_mode = -1;
-static int attn_mode() {
-  if (g_attn_mode < 0) {
-    const char* e = getenv("AFX_ATTN_FUSED_COMBINE");
-    g_attn_mode = e && atoi(e) == 1 ? 1 : 0;
-  }
-  return g_attn_mode;
 }
 
 static int attn_cus() {
@@ -442,12 +413,12 @@ static int attn_cus() {
   return cus;
 }
 
-// Steps per wavefront (chunk = nstep * 4 * (512 / D) positions): the largest chunk that still
+// Steps per wavefront (chunk = nstep * kAttnWaves * (512 / D) positions): the largest chunk that still
 // puts about one workgroup on every CU, and never more than kMaxSplits splits.  Returns 0 if
 // even the largest chunk leaves more than kMaxSplits splits.
 static int choose_nstep(int D, int B, int Hkv, int L, int want) {
   const int pps = 512 / D;
-  auto splits = [&](int ns) { const int c = ns * 4 * pps; return (L + c - 1) / c; };
+  auto splits = [&](int ns) { const int c = ns * kAttnWaves * pps; return (L + c - 1) / c; };
   if (want == 1 || want == 2 || want == 4 || want == 8 || want == 16) return splits(want) <= kMaxSplits ? want : 0;
   const int target = attn_cus();
   for (int ns = 16; ns >= 1; ns >>= 1) {
@@ -468,10 +439,10 @@ long long afx_decode_attn_ws_bytes(int B, int Hq, int Hkv, int D, int max_len, i
   if (D != 8 && D != 16 && D != 32 && D != 64 && D != 128 && D != 256) return -1;
   const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
   if (ns == 0) return -2;
-  const int chunk = ns * 4 * (512 / D);
+  const int chunk = ns * kAttnWaves * (512 / D);
   const long long nsplit = (max_len + chunk - 1) / chunk;
   const long long nsp = (nsplit + 3) / 4 * 4;
-  return (long long)B * Hq * nsp * (D + 2) * 4 + (long long)B * Hkv * 4;
+  return (long long)B * Hq * nsp * (D + 2) * 4;
 }
 
 // q/o: element (b, h, d) at b*q_bs + h*q_hs + d.  K/V: (b, kvh, p, d) at b*kv_bs + kvh*kv_hs + p*D + d.
@@ -502,26 +473,19 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.L = ctx_len; a.Mmax = max_len; a.causal_off = causal_off;
   a.scale_log2 = scale * 1.4426950408889634f;
   const int ns = choose_nstep(D, B, Hkv, max_len, nstep_hint);
-  a.chunk = ns * 4 * (512 / D);
+  a.chunk = ns * kAttnWaves * (512 / D);
   a.nsplit = (max_len + a.chunk - 1) / a.chunk;
   a.nsp = (a.nsplit + 3) / 4 * 4;
   a.ws_o = (float*)ws;
   a.ws_ml = a.ws_o + (size_t)B * Hq * D * a.nsp;
-  a.counters = (int*)(a.ws_ml + (size_t)B * Hq * 2 * a.nsp);
-  const bool fused = attn_mode() == 1 && D == 128;
-  attn_fn fn;
-  if (fused)
-    fn = pick_g<128, true>(G, ns);
-  else
-    fn = D == 8 ? pick_g<8, false>(G, ns) : D == 16 ? pick_g<16, false>(G, ns) : D == 32 ? pick_g<32, false>(G, ns)
-       : D == 64 ? pick_g<64, false>(G, ns) : D == 128 ? pick_g<128, false>(G, ns) : pick_g<256, false>(G, ns);
-  hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(256), 0, (hipStream_t)stream, a);
+  const attn_fn fn = D == 8 ? pick_g<8>(G, ns) : D == 16 ? pick_g<16>(G, ns) : D == 32 ? pick_g<32>(G, ns)
+                   : D == 64 ? pick_g<64>(G, ns) : D == 128 ? pick_g<128>(G, ns) : pick_g<256>(G, ns);
+  hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(kAttnWaves * 64), 0, (hipStream_t)stream, a);
   int rc = check_launch("afx_decode_attn");
-  if (rc || fused) return rc;
-  const int per4 = ((a.nsp / 4) + (256 / D) - 1) / (256 / D);   // float4 loads each combine thread needs
-  attn_fn cf = D == 8 ? pick_combine<8>(per4) : D == 16 ? pick_combine<16>(per4) : D == 32 ? pick_combine<32>(per4)
-             : D == 64 ? pick_combine<64>(per4) : D == 128 ? pick_combine<128>(per4) : pick_combine<256>(per4);
-  hipLaunchKernelGGL(cf, dim3(Hq, B), dim3(256), 0, (hipStream_t)stream, a);
+  if (rc) return rc;
+  const attn_fn cf = D == 8 ? pick_combine<8>(a.nsp) : D == 16 ? pick_combine<16>(a.nsp) : D == 32 ? pick_combine<32>(a.nsp)
+                   : D == 64 ? pick_combine<64>(a.nsp) : D == 128 ? pick_combine<128>(a.nsp) : pick_combine<256>(a.nsp);
+  hipLaunchKernelGGL(cf, dim3(Hq, B), dim3(D < 64 ? 64 : D), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_attn(combine)");
 }
 

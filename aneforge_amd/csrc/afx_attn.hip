@@ -35,7 +35,7 @@ struct AttnArgs {
   half_t* o;         // same strides as q
   const half_t* mask;  // optional additive mask [B][mask_bs] over positions
   const int* pos;      // optional: ctx length of sequence b = pos[b] + 1 (device)
-  float* ws_o;         // [B][Hq][D][nsp] split partial outputs (a (head, dim) row is contiguous)
+  float* ws_o;         // [B][Hq][nsp][D] split partial outputs (a split's head row is contiguous)
   float* ws_ml;        // [B][Hq][2][nsp] split max (log2 domain) and row sum
   long long q_bs, q_hs, kv_bs, kv_hs;
   long long mask_bs;
@@ -166,23 +166,20 @@ __global__ __launch_bounds__(NW * 64) void attn_partial_kernel(AttnArgs a) {
   const int dl = lane % LPP;       // which 8-dim slice
   const int pl = lane / LPP;       // which position within the step
 
-  // K and V rows first (clamped to the cache bound, masked later), then q and the length
+  // Loads: K rows, then q and the mask entries, then V rows (K/V row indices clamped to the
+  // cache bound, positions past the length masked later), so the scores start while V is
+  // still in flight.
+  int posn[NSTEP], pcl[NSTEP];
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    posn[s] = p0 + (wave + NW * s) * PPS + pl;
+    pcl[s] = posn[s] < a.Mmax ? posn[s] : a.Mmax - 1;
+  }
   const half_t* kb = a.k + (size_t)b * a.kv_bs + (size_t)kvh * a.kv_hs + dl * 8;
   const half_t* vb = a.v + (size_t)b * a.kv_bs + (size_t)kvh * a.kv_hs + dl * 8;
   u4 kv[NSTEP], vv[NSTEP];
-  int posn[NSTEP];
 #pragma unroll
-  for (int s = 0; s < NSTEP; ++s) {
-    const int p = p0 + (wave + NW * s) * PPS + pl;
-    posn[s] = p;
-    const int pc = p < a.Mmax ? p : a.Mmax - 1;
-    kv[s] = __builtin_nontemporal_load((const u4*)(kb + (size_t)pc * D));
-  }
-#pragma unroll
-  for (int s = 0; s < NSTEP; ++s) {
-    const int pc = posn[s] < a.Mmax ? posn[s] : a.Mmax - 1;
-    vv[s] = __builtin_nontemporal_load((const u4*)(vb + (size_t)pc * D));
-  }
+  for (int s = 0; s < NSTEP; ++s) kv[s] = __builtin_nontemporal_load((const u4*)(kb + (size_t)pcl[s] * D));
   h2 qh[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -193,11 +190,11 @@ __global__ __launch_bounds__(NW * 64) void attn_partial_kernel(AttnArgs a) {
   // additive mask entries (af.sdpa), loaded unconditionally from a valid address
   float mk[NSTEP];
   const half_t* mrow = a.mask ? a.mask + (size_t)b * a.mask_bs : a.q;
+  const int mstride = a.mask ? 1 : 0;
 #pragma unroll
-  for (int s = 0; s < NSTEP; ++s) {
-    const int pc = posn[s] < a.Mmax ? posn[s] : a.Mmax - 1;
-    mk[s] = (float)mrow[a.mask ? pc : 0];
-  }
+  for (int s = 0; s < NSTEP; ++s) mk[s] = (float)mrow[pcl[s] * mstride];
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) vv[s] = __builtin_nontemporal_load((const u4*)(vb + (size_t)pcl[s] * D));
   const int L = seq_len(a, b);
   const bool active = p0 < L;      // workgroup-uniform: a split past the length stores an empty partial
 
@@ -297,9 +294,9 @@ __global__ __launch_bounds__(NW * 64) void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < Q; ++j) acc += red_o[j][g][d];
       const size_t bh = (size_t)b * a.Hq + kvh * G + h0 + g;
-      float* orow = a.ws_o + (bh * D + d) * NSP;
-      orow[split] = active ? acc : 0.0f;
-      for (int t = a.nsplit; split == a.nsplit - 1 && t < NSP; ++t) orow[t] = 0.0f;   // padding splits
+      float* ocol = a.ws_o + bh * NSP * D + d;     // split t at ocol[t * D]: rows stored whole
+      ocol[(size_t)split * D] = active ? acc : 0.0f;
+      for (int t = a.nsplit; split == a.nsplit - 1 && t < NSP; ++t) ocol[(size_t)t * D] = 0.0f;   // padding splits
       if (d == 0) {
         float lt = 0.0f;
 #pragma unroll
@@ -317,8 +314,9 @@ __global__ __launch_bounds__(NW * 64) void attn_partial_kernel(AttnArgs a) {
 }
 
 // Combine launch: grid (Hq, B), max(D, 64) threads; thread d owns output dim d and issues
-// all its loads at once (its dim's row of split partials as NV4 float4s, the maxima and sums
-// of splits lane and lane + 64), so the kernel costs one memory round trip.  Every split slot
+// all its loads at once (its dim's value in each of 4 * NV4 split rows, coalesced across the
+// threads, and the maxima and sums of splits lane and lane + 64), so the kernel costs one
+// memory round trip.  Every split slot
 // below nsp holds a partial from the same call (splits past the length and the padding slots
 // hold m = -inf, l = 0, o = 0), so the weights need no length:
 // w_t = exp2(m_t - max) / sum_s exp2(m_s - max) * l_s.  Every wavefront derives the weights
@@ -332,12 +330,12 @@ __global__ __launch_bounds__(D < 64 ? 64 : D) void attn_combine_kernel(AttnArgs 
   const int NSP = a.nsp;                        // multiple of 4, <= kMaxSplits
   const size_t bh = (size_t)b * a.Hq + h;
   const int d = t < D ? t : D - 1;
-  const float* row = a.ws_o + (bh * D + d) * NSP;
-  f4 ov[NV4];
+  const float* col = a.ws_o + bh * NSP * D + d;  // split t's value at col[t * D]
+  float ov[4 * NV4];
 #pragma unroll
-  for (int j = 0; j < NV4; ++j) {
-    const int s = 4 * j < NSP - 4 ? 4 * j : NSP - 4;   // clamped repeats get weight 0 below
-    ov[j] = __builtin_nontemporal_load((const f4*)(row + s));
+  for (int j = 0; j < 4 * NV4; ++j) {
+    const int s = j < NSP ? j : NSP - 1;           // clamped repeats get weight 0 below
+    ov[j] = __builtin_nontemporal_load(col + (size_t)s * D);
   }
   const float* mrow = a.ws_ml + bh * 2 * NSP;
   const bool va = lane < NSP, vb = lane + 64 < NSP;
@@ -358,25 +356,30 @@ __global__ __launch_bounds__(D < 64 ? 64 : D) void attn_combine_kernel(AttnArgs 
 #pragma unroll
   for (int j = 0; j < NV4; ++j) {
     const f4 w = *(const f4*)&s_w[wave][4 * j];
-    num = __builtin_fmaf(w.x, ov[j].x, num);
-    num = __builtin_fmaf(w.y, ov[j].y, num);
-    num = __builtin_fmaf(w.z, ov[j].z, num);
-    num = __builtin_fmaf(w.w, ov[j].w, num);
+    num = __builtin_fmaf(w.x, ov[4 * j + 0], num);
+    num = __builtin_fmaf(w.y, ov[4 * j + 1], num);
+    num = __builtin_fmaf(w.z, ov[4 * j + 2], num);
+    num = __builtin_fmaf(w.w, ov[4 * j + 3], num);
   }
   if (t < D) a.o[(size_t)b * a.q_bs + (size_t)h * a.q_hs + d] = (half_t)num;
 }
 
 typedef void (*attn_fn)(AttnArgs);
 
-// NV4 float4 loads per combine thread: the smallest of 1, 2, 4, 8, 16, 32 covering nsp splits.
+// Split rows read by each combine thread: 4 * NV4, the smallest of 4, 8, 12, 16, 24, 32, 48,
+// 64, 96, 128 covering nsp.
 template <int D>
 static attn_fn pick_combine(int nsp) {
   const int n4 = (nsp + 3) / 4;
   if (n4 <= 1) return attn_combine_kernel<D, 1>;
   if (n4 <= 2) return attn_combine_kernel<D, 2>;
+  if (n4 <= 3) return attn_combine_kernel<D, 3>;
   if (n4 <= 4) return attn_combine_kernel<D, 4>;
+  if (n4 <= 6) return attn_combine_kernel<D, 6>;
   if (n4 <= 8) return attn_combine_kernel<D, 8>;
+  if (n4 <= 12) return attn_combine_kernel<D, 12>;
   if (n4 <= 16) return attn_combine_kernel<D, 16>;
+  if (n4 <= 24) return attn_combine_kernel<D, 24>;
   return attn_combine_kernel<D, 32>;
 }
 

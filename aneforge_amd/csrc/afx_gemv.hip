@@ -22,6 +22,18 @@ static int mtile(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
 // Activation rows from which a linear runs on MFMA (AFX_MFMA_MIN_M overrides; 0 disables).
 static int g_mfma_min = -1;
+// Fast path without a norm: 2 (default) stages x through LDS once per workgroup, so the four
+// wavefronts share one read of it; 0 (AFX_GEMV_XSTAGE=0) has every lane read its x chunks from
+// global memory, which costs L1 bandwidth the weight stream needs (x is twice the int8 row).
+static int xstage_mode() {
+  static int mode = -1;
+  if (mode < 0) {
+    const char* e = getenv("AFX_GEMV_XSTAGE");
+    mode = e && atoi(e) == 0 ? 0 : 2;
+  }
+  return mode;
+}
+
 static int mfma_min_rows() {
   if (g_mfma_min < 0) {
     const char* e = getenv("AFX_MFMA_MIN_M");
@@ -33,12 +45,14 @@ static int mfma_min_rows() {
 
 // Rows per group: 2 when the epilogue pairs rows (SwiGLU, RoPE), else 1 (a hint of 2 or the
 // AFX_GEMV_R environment variable selects row pairs for plain epilogues too).
-static int choose_rows(int hint, bool paired) {
+// Rows per wavefront: paired epilogues need 2; a RMSNorm prologue is paid once per workgroup,
+// so it takes 2 (half the workgroups); otherwise 1 (measured on MI355X for the 7B shapes).
+static int choose_rows(int hint, bool paired, bool norm) {
   if (paired) return 2;
   int R = hint;
   if (R != 1 && R != 2) {
     const char* e = getenv("AFX_GEMV_R");
-    R = e ? atoi(e) : 1;
+    R = e ? atoi(e) : (norm ? 2 : 1);
   }
   return R == 2 ? 2 : 1;
 }
@@ -73,8 +87,8 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
     return mfma_launch(fmt, m, 1, stream, what);
   }
   const int mt = mtile(a.M);
-  const int R = choose_rows(rows_hint, eg != EG_PLAIN);
   const bool norm = a.gamma != nullptr;
+  const int R = choose_rows(rows_hint, eg != EG_PLAIN, norm);
   size_t smem = gemv_lds_bytes(mt, a.K, norm);
   int xs = 1;
   if (smem > 65536) {
@@ -88,9 +102,10 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
   const int fu = a.M == 1 ? fast_units(fmt, nchunks) : 0;
   if (fu) {
     // a whole row fits the lanes' registers: the register-resident fast path (static LDS only)
-    gemv_fn fr = fmt == FMT_I8 ? pick_gemv_row_i8(eg, R, norm, fu)
-               : fmt == FMT_Q4 ? pick_gemv_row_q4(eg, R, norm, fu)
-                               : pick_gemv_row_f16(eg, R, norm, fu);
+    const int nm = norm ? 1 : xstage_mode();     // 2: x staged through LDS once per workgroup
+    gemv_fn fr = fmt == FMT_I8 ? pick_gemv_row_i8(eg, R, nm, fu)
+               : fmt == FMT_Q4 ? pick_gemv_row_q4(eg, R, nm, fu)
+                               : pick_gemv_row_f16(eg, R, nm, fu);
     hipLaunchKernelGGL(fr, dim3(ntiles), dim3(256), 0, stream, a);
     return check_launch(what);
   }

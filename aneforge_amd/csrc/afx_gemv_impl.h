@@ -381,11 +381,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 
 // Fast path for one activation row (M = 1) with K at most 64 lanes x U chunks (U a compile-time
 // constant per shape family: int8 K = 4096 -> 4, 11008 -> 11; Q4_0 4096 -> 2, 11008 -> 6;
-// fp16 4096 -> 8).  Each lane keeps the x values of its own U chunks in registers: without a
-// norm they are read straight from global memory (no LDS, no barrier); with the RMSNorm
-// prologue the workgroup normalises x once (each thread a few 16-byte vectors of x and gamma),
-// shares it through LDS, and every lane then reads its chunks.  Chunks past K (the last unit
-// of a ragged row) read a clamped address and are zeroed by a select.
+// fp16 4096 -> 8).  Each lane keeps the x values of its own U chunks in registers.  NORM = 1:
+// the workgroup normalises x once (each thread a few 16-byte vectors of x and gamma), shares it
+// through LDS, and every lane then reads its chunks; NORM = 2: the same staging without the
+// norm; NORM = 0: every lane reads its chunks straight from global memory (no LDS, no
+// barrier).  Chunks past K (the last unit of a ragged row) read a clamped address and are
+// zeroed by a select.
 template <int FMT, int R, int NORM, int EG, int U>
 __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   constexpr int XH = Fmt<FMT>::kXH2;
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
       int f = t + 256 * i;
       f = f < nv ? f : nv - 1;
       xq[i] = *(const u4*)(a.x + 8 * f);
-      gq[i] = *(const u4*)(a.gamma + 8 * f);
+      if constexpr (NORM == 1) gq[i] = *(const u4*)(a.gamma + 8 * f);
     }
   } else {
 #pragma unroll
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   gemv_epilogue_operands<FMT, 1, R, EG>(a, row0, e_pos, h_scale, h_bias, h_res, h_cs, h_sn);
   __builtin_amdgcn_sched_barrier(0);
 
-  if constexpr (NORM) {
+  if constexpr (NORM == 1) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NVT; ++i) {
@@ -473,6 +474,11 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
         r.y = (half_t)(((float)xx.y * rstd) * (float)gg.y);
         xw[jj] = as_u32(r);
       }
+    }
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < NVT; ++i) {
       int f = t + 256 * i;
       f = f < nv ? f : nv - 1;                       // a clamped duplicate rewrites its own value
       *(u4*)(xs + 8 * f) = xq[i];
@@ -541,6 +547,9 @@ gemv_fn pick_gemv(int mt, int eg, int R, int xs) {
 
 template <int FMT, int U>
 gemv_fn pick_gemv_row_u(int eg, int R, int norm) {
+  if (norm == 2 && eg == EG_PLAIN)                 // x staged once per workgroup through LDS, no norm
+    return R == 2 ? gemv_row_kernel<FMT, 2, 2, EG_PLAIN, U> : gemv_row_kernel<FMT, 1, 2, EG_PLAIN, U>;
+  if (norm == 2) norm = 0;
   if (eg == EG_QKV) return norm ? gemv_row_kernel<FMT, 2, 1, EG_QKV, U> : gemv_row_kernel<FMT, 2, 0, EG_QKV, U>;
   if (eg == EG_SWIGLU) return norm ? gemv_row_kernel<FMT, 2, 1, EG_SWIGLU, U> : gemv_row_kernel<FMT, 2, 0, EG_SWIGLU, U>;
   if (R == 2) return norm ? gemv_row_kernel<FMT, 2, 1, EG_PLAIN, U> : gemv_row_kernel<FMT, 2, 0, EG_PLAIN, U>;

@@ -9,6 +9,8 @@ weights) and a CPU baseline (the numpy oracle on a bounded sample, run on this h
 
 Kernel workloads (--workload gemv_w8 | gemv_q4 | attn | moe) time one configuration with
 rotating weight copies inside a captured graph (working set > 2x the 256 MB MALL).
+--workload copy streams a plain 1 GiB copy: the calibration run for the FETCH_SIZE /
+WRITE_SIZE counters behind roofline.traffic, and a measured copy ceiling.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode]
 """
@@ -31,7 +33,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv_w8", "gemv_q4", "attn", "moe", "kernels"])
+                    choices=["decode", "gemv_w8", "gemv_q4", "attn", "moe", "kernels", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--out", default=None, help="also append the JSON line to this file")
     ap.add_argument("--rows-hint", type=int, default=0)
@@ -209,6 +211,37 @@ def bench_moe(args):
             "frac": byts / (ms * 1e-3) / HBM_PEAK}
 
 
+def bench_copy(args):
+    """A plain streaming copy of known size (1 GiB read, 1 GiB written, fp16 elements) through
+    afx_copy_strided: under `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` it gives the factor that
+    turns those counters into HBM bytes."""
+    import torch
+    from aneforge_amd import _kernels as K
+    n = 1 << 29
+    src = torch.ones(n, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    gr = Graph(lambda: K.copy_strided(src, [1], [n], dst=dst))
+    for _ in range(max(1, args.warmup)):
+        gr.launch()
+    ms = gr.time_ms(max(1, args.steps))
+    gr.close()
+    return {"workload": "copy 1 GiB fp16 (afx_copy_strided)", "bytes_read": 2 * n, "bytes_written": 2 * n,
+            "us": ms * 1e3, "GBps": 4 * n / (ms * 1e-3) / 1e9}
+
+
+def profile_value(name: str, key: str):
+    """A figure recorded in a committed profile summary (a `key: value` line), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith(key + ":"):
+                    return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        return None
+    return None
+
+
 def bench_kernels(args):
     out = []
     a = argparse.Namespace(**vars(args))
@@ -382,11 +415,14 @@ def bench_decode(args):
                    "global_batch": 1, "seq_len": P + K_steps, "parallelism": "none (1 GPU)"},
         "decode": {"bytes_per_token": per_tok_bytes, "effective_GBps": per_tok_bytes * tok_s / 1e9,
                    "roofline_tokens_per_s": roof_tok_s, "frac_of_roofline": tok_s / roof_tok_s,
-                   "kernels_per_token": 5 * CFG3["n_layers"] + 2},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<int8> fused RMSNorm + gate/up + SwiGLU (22016x4096)",
+                   # per layer: QKV+RoPE+KV write, attention partials, split combine, o-proj, gate/up, down
+                   "kernels_per_token": 6 * CFG3["n_layers"] + 2},
+        "roofline": {"bound": "hbm",
+                     "kernel": "gemv_row_kernel<int8, R=2, norm, SwiGLU>: fused RMSNorm + gate/up + SwiGLU (22016x4096)",
                      "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK, "avg_launch_us": k_ms * 1e3, "bytes_per_launch": k_bytes,
-                     "traffic": None},
+                     # HBM bytes per launch from the FETCH_SIZE + WRITE_SIZE counter runs, copy-calibrated
+                     "traffic": profile_value("gemv_gateup_cfg3_pmc.md", "traffic_bytes_per_launch")},
     }
     if not args.no_cpu:
         log("timing the CPU baseline (bounded sample)")
@@ -421,6 +457,9 @@ def main():
         return
     if args.workload == "moe":
         print(json.dumps(bench_moe(args)))
+        return
+    if args.workload == "copy":
+        print(json.dumps(bench_copy(args)))
         return
     if args.workload == "decode":
         res = bench_decode(args)

@@ -22,11 +22,12 @@ struct MfmaArgs {
   int M;                   // dense: activation rows (<= 16 per token group; any count, in groups)
   int N, K;
   int epi;                 // EPI_F16 / EPI_RESID / EPI_F32 / EPI_SWIGLU (gemv epilogue codes)
+  int xbytes;              // set by mfma_launch: bytes of the activation rows the kernel may read
 };
 
 // Launch the MFMA kernel over E experts (1 for a dense linear).  Returns 0 or a negative code.
 int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const char* what);
-// Whether the MFMA path supports this shape (K divisibility for the 4-wave split).
+// Whether the MFMA path supports this shape (K divisible into steps, one or more per wavefront).
 bool mfma_supported(int fmt, int K);
 
 }  // namespace afx

@@ -16,11 +16,18 @@
 //          fp16((nibble - 8) * d): the fp16-rounded dequantised weight the reference multiplies
 //          with (it converts the ggml dequantisation to float16, aneforge/_gguf.py:34-39);
 //   fp16 : a chunk = 8 weights -> one A operand.
-// A workgroup owns 16 output rows; its 4 wavefronts split K evenly (each streams a quarter of
-// every row, all loads of a step issued before its MFMAs) and their partial 16x16 tiles are
-// summed through LDS by wavefront 0, which applies the epilogue.  MoE: the grid's y dimension
-// is the expert; workgroups of experts with no tokens exit at once (fixed launch shape, so the
-// layer stays graph-capturable).
+// A workgroup owns 16 output rows; its NW wavefronts split K evenly and their partial 16x16
+// tiles are summed through LDS by wavefront 0, which applies the epilogue.
+// Weight loads are row-contiguous: a batch is 4 steps = 16 rows x 256 bytes, fetched as four
+// loads in which 16 lanes read 256 contiguous bytes of one row (the MFMA layout would have 16
+// lanes touch 16 rows x 16 bytes per load), then transposed into the MFMA layout through a
+// wavefront-private LDS tile padded to 272 bytes per row (conflict-free 16-byte reads).  A
+// wavefront issues all its batches' weight loads at once (up to four; longer rows go in
+// rounds).  Activation rows of unused token columns read through a buffer resource at an
+// out-of-range offset, which returns zeros without a memory access.
+// MoE: the grid's y dimension is the expert; workgroups of experts with no tokens exit at once
+// (fixed launch shape, so the layer stays graph-capturable).
+#include <stdlib.h>
 #include "afx_gemv_impl.h"
 #include "afx_mfma.h"
 
@@ -33,7 +40,9 @@ template <> struct MfmaFmt<FMT_I8> { static constexpr int kK = 64, kMfma = 2; };
 template <> struct MfmaFmt<FMT_Q4> { static constexpr int kK = 128, kMfma = 4; };
 template <> struct MfmaFmt<FMT_F16> { static constexpr int kK = 32, kMfma = 1; };
 
-constexpr int kStepsPerBatch = 4;   // steps whose loads are in flight together
+constexpr int kSPB = 4;            // steps per batch: 16 rows x 256 bytes
+constexpr int kWRow = 256 + 16;    // LDS bytes per staged weight row
+constexpr int kSRow = 40;          // LDS bytes per staged Q4_0 scale row (4 superblocks x 8 B, padded)
 
 __device__ __forceinline__ h8 pack8(h2 a, h2 b, h2 c, h2 d) {
   h8 r;
@@ -41,13 +50,21 @@ __device__ __forceinline__ h8 pack8(h2 a, h2 b, h2 c, h2 d) {
   return r;
 }
 __device__ __forceinline__ h8 as_h8(u4 v) { return __builtin_bit_cast(h8, v); }
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-template <int FMT, int EG>
-__global__ __launch_bounds__(256) void mfma_kernel(MfmaArgs a) {
+template <int FMT, int EG, int NW, int NB>
+__global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
   constexpr int KS = MfmaFmt<FMT>::kK, NM = MfmaFmt<FMT>::kMfma;
-  __shared__ f4 red[4][64];
+  __shared__ __align__(16) unsigned char wl[NW][16 * kWRow];
+  __shared__ __align__(16) unsigned char sl[NW][FMT == FMT_Q4 ? 16 * kSRow : 16];
+  __shared__ f4 red[NW][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 15, g = lane >> 4;
+  const int r = lane & 15, g = lane >> 4;          // MFMA role: A row / B column, k slot
+  const int lr = lane >> 4, lc = lane & 15;        // load role: row lr + 4h, chunk lc of a batch
   const int e = blockIdx.y;
   const int N = a.N, K = a.K;
   const int n0 = blockIdx.x * 16;
@@ -55,84 +72,146 @@ __global__ __launch_bounds__(256) void mfma_kernel(MfmaArgs a) {
   const int* lst = nullptr;
   if (a.cnt) {
     ntok = a.cnt[e];
-    if (ntok <= 0) return;                       // whole workgroup: no barrier reached
+    if (ntok <= 0) return;                         // whole workgroup: no barrier reached
     lst = a.list + (size_t)e * a.T;
   }
   const unsigned char* wbase = (const unsigned char*)a.w + (size_t)e * a.w_es;
   const half_t* sbase = a.scale ? a.scale + (size_t)e * a.s_es : nullptr;
-  const int row = n0 + r < N ? n0 + r : N - 1;   // A row of this lane (tail rows computed, not stored)
   const size_t rowbytes = Fmt<FMT>::row_bytes(K);
-  const u4* wrow = (const u4*)(wbase + (size_t)row * rowbytes);
-  const half_t* drow = FMT == FMT_Q4 ? sbase + (size_t)row * (K >> 5) : nullptr;
+  const unsigned char* lrow[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int row = n0 + 4 * h + lr < N ? n0 + 4 * h + lr : N - 1;   // tail rows computed, not stored
+    lrow[h] = wbase + (size_t)row * rowbytes + lc * 16;
+  }
+  const half_t* srow = nullptr;
+  if constexpr (FMT == FMT_Q4) {
+    const int row = n0 + (lane >> 2) < N ? n0 + (lane >> 2) : N - 1;
+    srow = sbase + (size_t)row * (K >> 5) + 4 * (lane & 3);
+  }
   const int nsteps = K / KS;
-  const int s0 = nsteps * wave / 4, s1 = nsteps * (wave + 1) / 4;   // this wavefront's K quarter
+  const int s0 = nsteps * wave / NW, s1 = nsteps * (wave + 1) / NW;   // this wavefront's K range
+  const int nb = (s1 - s0 + kSPB - 1) / kSPB;
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, a.xbytes);
+  unsigned char* wls = wl[wave];
+  unsigned char* sls = sl[wave];
+  constexpr int kOOB = 0x7fff0000;
+
+  const int nsw = s1 - s0;                         // steps of this wavefront
 
   for (int tg = 0; tg < ntok; tg += 16) {
     const int ti = tg + r;                        // B column (token) of this lane
     const bool tok_ok = ti < ntok;
-    const int tc = tok_ok ? ti : ntok - 1;
-    int xr = tc;
+    int xr = tok_ok ? ti : 0;
     if (lst) {
-      const int ent = lst[tc];
+      const int ent = lst[tok_ok ? ti : 0];
       xr = a.x_by_token ? ent / a.k : ent;
     }
-    const half_t* xrow = a.x + (size_t)xr * a.ldx;
+    const int xoff = tok_ok ? xr * a.ldx * 2 : kOOB;      // out of range: reads zeros
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int sb = s0; sb < s1; sb += kStepsPerBatch) {
-      u4 wv[kStepsPerBatch];
-      u2 dv[kStepsPerBatch];
-      u4 xv[kStepsPerBatch][NM];
+    // rounds of NB batches (NB = this shape's batches per wavefront when that is at most 4):
+    // all of a round's weight loads are issued at once
+    for (int b0 = 0; b0 < nb; b0 += NB) {
+      u4 wq[NB][4];
+      u2 sq[NB];
 #pragma unroll
-      for (int i = 0; i < kStepsPerBatch; ++i) {
-        const int s = sb + i < s1 ? sb + i : s1 - 1;   // a clamped repeat is masked below
-        const int c = s * 4 + g;                       // 16-byte chunk of this lane
-        wv[i] = __builtin_nontemporal_load(wrow + c);
-        if constexpr (FMT == FMT_Q4) dv[i] = *(const u2*)(drow + 4 * s);
+      for (int b = 0; b < NB; ++b) {
+        // batch b0 + b, clamped per lane to the row (a clamped chunk is loaded but never used)
+        const int sb = s0 + (b0 + b) * kSPB;
+        int c = sb * 4 + lc;
+        c = c < nsteps * 4 ? c : nsteps * 4 - 1;
 #pragma unroll
-        for (int j = 0; j < NM; ++j) {
-          int kx;
-          if constexpr (FMT == FMT_I8) kx = s * KS + 16 * g + 8 * j;
-          else if constexpr (FMT == FMT_Q4) kx = 32 * (4 * s + j) + 8 * g;
-          else kx = s * KS + 8 * g;
-          xv[i][j] = *(const u4*)(xrow + kx);
+        for (int h = 0; h < 4; ++h) wq[b][h] = __builtin_nontemporal_load((const u4*)(lrow[h] + (size_t)(c - lc) * 16));
+        if constexpr (FMT == FMT_Q4) {
+          int q = sb + (lane & 3);
+          q = q < nsteps ? q : nsteps - 1;
+          sq[b] = *(const u2*)(srow + (size_t)(q - (lane & 3)) * 4);
         }
       }
+      // activations: one batch (4 steps) per load group; int8/fp16 keep two groups in flight
+      // (the next batch's loads go out before this batch's math), Q4_0 one (its group is 4x larger)
+      constexpr int XG = NM <= 2 ? 2 : 1;
+      auto load_x = [&](u4 (&xv)[kSPB][NM], int b) {
 #pragma unroll
-      for (int i = 0; i < kStepsPerBatch; ++i) {
-        if (sb + i >= s1) break;                       // wavefront-uniform
+        for (int t = 0; t < kSPB; ++t) {
+          const int i = (b0 + b) * kSPB + t;       // step relative to s0
+          const int s = s0 + i;
+          const bool in = i < nsw;
 #pragma unroll
-        for (int j = 0; j < NM; ++j) {
-          h8 av;
-          if constexpr (FMT == FMT_I8) {
-            h2 q0, q1, q2, q3;
-            i8x4_to_h2(j == 0 ? wv[i].x : wv[i].z, q0, q1);
-            i8x4_to_h2(j == 0 ? wv[i].y : wv[i].w, q2, q3);
-            av = pack8(q0, q1, q2, q3);
-          } else if constexpr (FMT == FMT_Q4) {
-            const uint32_t wd = j == 0 ? wv[i].x : j == 1 ? wv[i].y : j == 2 ? wv[i].z : wv[i].w;
-            const h2 dd = as_h2(j < 2 ? dv[i].x : dv[i].y);
-            const half_t d = (j & 1) ? dd.y : dd.x;
-            const h2 d2 = {d, d};
-            h2 q[4];
-            q4_word_to_h2(wd, q);
-            av = pack8(q[0] * d2, q[1] * d2, q[2] * d2, q[3] * d2);   // fp16((nibble - 8) * d)
-          } else {
-            av = as_h8(wv[i]);
+          for (int j = 0; j < NM; ++j) {
+            int kx;
+            if constexpr (FMT == FMT_I8) kx = s * KS + 16 * g + 8 * j;
+            else if constexpr (FMT == FMT_Q4) kx = 32 * (4 * s + j) + 8 * g;
+            else kx = s * KS + 8 * g;
+            xv[t][j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xoff + kx * 2 : kOOB, 0, 0));
           }
-          h8 bv = as_h8(xv[i][j]);
-          if (!tok_ok) bv = (h8){0, 0, 0, 0, 0, 0, 0, 0};
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+        }
+      };
+      u4 xv[XG][kSPB][NM];
+      if constexpr (XG == 2) load_x(xv[0], 0);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (b0 + b >= nb) break;                   // wavefront-uniform
+        if constexpr (XG == 2) {
+          if (b + 1 < NB) load_x(xv[(b + 1) & 1], b + 1);
+        } else {
+          load_x(xv[0], b);
+        }
+        u4 (&xb)[kSPB][NM] = xv[XG == 2 ? (b & 1) : 0];
+        // stage the batch, then read it back in the MFMA layout (row r, chunk 4 * step + g)
+        if (b) wave_sync_lds();                    // the previous batch's reads are done
+#pragma unroll
+        for (int h = 0; h < 4; ++h) *(u4*)(wls + (4 * h + lr) * kWRow + lc * 16) = wq[b][h];
+        if constexpr (FMT == FMT_Q4) *(u2*)(sls + (lane >> 2) * kSRow + (lane & 3) * 8) = sq[b];
+        wave_sync_lds();
+        u4 wv[kSPB];
+        u2 dv[kSPB];
+#pragma unroll
+        for (int t = 0; t < kSPB; ++t) {
+          wv[t] = *(const u4*)(wls + r * kWRow + (4 * t + g) * 16);
+          if constexpr (FMT == FMT_Q4) dv[t] = *(const u2*)(sls + r * kSRow + t * 8);
+        }
+#pragma unroll
+        for (int t = 0; t < kSPB; ++t) {
+          if ((b0 + b) * kSPB + t >= nsw) break;   // wavefront-uniform
+#pragma unroll
+          for (int j = 0; j < NM; ++j) {
+            h8 av;
+            if constexpr (FMT == FMT_I8) {
+              h2 q0, q1, q2, q3;
+              i8x4_to_h2(j == 0 ? wv[t].x : wv[t].z, q0, q1);
+              i8x4_to_h2(j == 0 ? wv[t].y : wv[t].w, q2, q3);
+              av = pack8(q0, q1, q2, q3);
+            } else if constexpr (FMT == FMT_Q4) {
+              const uint32_t wd = j == 0 ? wv[t].x : j == 1 ? wv[t].y : j == 2 ? wv[t].z : wv[t].w;
+              const h2 dd = as_h2(j < 2 ? dv[t].x : dv[t].y);
+              const half_t d = (j & 1) ? dd.y : dd.x;
+              const h2 d2 = {d, d};
+              h2 q[4];
+              q4_word_to_h2(wd, q);
+              av = pack8(q[0] * d2, q[1] * d2, q[2] * d2, q[3] * d2);   // fp16((nibble - 8) * d)
+            } else {
+              av = as_h8(wv[t]);
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, as_h8(xb[t][j]), acc, 0, 0, 0);
+          }
         }
       }
+      wave_sync_lds();                             // the round's reads are done before the next round's writes
     }
-    // sum the four K quarters; wavefront 0 finishes the tile
+    // sum the K ranges; wavefront 0 finishes the tile
     red[wave][lane] = acc;
     __syncthreads();
     if (wave == 0) {
-      const f4 p1 = red[1][lane], p2 = red[2][lane], p3 = red[3][lane];
       float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = acc[i] + p1[i] + p2[i] + p3[i];
+      for (int i = 0; i < 4; ++i) v[i] = acc[i];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) {
+        const f4 p = red[w][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += p[i];
+      }
       const int rb = n0 + 4 * g;                   // output rows rb .. rb + 3 of token ti
       if constexpr (FMT == FMT_I8) {
         const u2 sv = *(const u2*)(sbase + (rb < N ? rb : 0));
@@ -174,9 +253,28 @@ __global__ __launch_bounds__(256) void mfma_kernel(MfmaArgs a) {
 
 typedef void (*mfma_fn)(MfmaArgs);
 
+template <int FMT, int EG, int NW>
+static mfma_fn pick_mfma_b(int nb) {
+  switch (nb) {
+    case 1: return mfma_kernel<FMT, EG, NW, 1>;
+    case 2: return mfma_kernel<FMT, EG, NW, 2>;
+    case 3: return mfma_kernel<FMT, EG, NW, 3>;
+    default: return mfma_kernel<FMT, EG, NW, 4>;
+  }
+}
+template <int FMT, int EG>
+static mfma_fn pick_mfma_w(int nw, int nb) {
+  return nw == 4 ? pick_mfma_b<FMT, EG, 4>(nb) : nw == 8 ? pick_mfma_b<FMT, EG, 8>(nb) : pick_mfma_b<FMT, EG, 16>(nb);
+}
+static mfma_fn pick_mfma(int fmt, bool swiglu, int nw, int nb) {
+  if (fmt == FMT_I8) return swiglu ? pick_mfma_w<FMT_I8, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_I8, EG_PLAIN>(nw, nb);
+  if (fmt == FMT_Q4) return swiglu ? pick_mfma_w<FMT_Q4, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_Q4, EG_PLAIN>(nw, nb);
+  return swiglu ? pick_mfma_w<FMT_F16, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_F16, EG_PLAIN>(nw, nb);
+}
+
 bool mfma_supported(int fmt, int K) {
   const int ks = fmt == FMT_I8 ? 64 : fmt == FMT_Q4 ? 128 : 32;
-  return K % ks == 0 && K / ks >= 4;
+  return K % ks == 0 && K / ks >= 8;                           // at least one step per wavefront
 }
 
 int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const char* what) {
@@ -190,12 +288,32 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
   AFX_REQUIRE(fmt != FMT_Q4 || (a.scale && ((uintptr_t)a.scale & 7) == 0), "%s: Q4_0 needs aligned block scales", what);
   AFX_REQUIRE(a.cnt ? (a.list && a.T >= 1 && a.k >= 1) : (a.M >= 1), "%s: bad token description", what);
   AFX_REQUIRE(a.epi != EPI_RESID || a.resid, "%s: residual pointer required", what);
+  const long long xrows = a.cnt ? (a.x_by_token ? a.T : (long long)a.T * a.k) : a.M;
+  const long long xbytes = xrows * a.ldx * 2;
+  AFX_REQUIRE(xbytes < 0x7fff0000LL, "%s: activations span %lld bytes (limit 2 GiB)", what, xbytes);
+  const long long rowb = fmt == FMT_I8 ? a.K : fmt == FMT_Q4 ? a.K / 2 : 2LL * a.K;
+  AFX_REQUIRE((long long)a.N * rowb + 65536 < 0x7fff0000LL,
+              "%s: a weight matrix of %d x %d exceeds the 2 GiB buffer range", what, a.N, a.K);
+  MfmaArgs b = a;
+  b.xbytes = (int)xbytes;
   const bool swiglu = a.epi == EPI_SWIGLU;
-  mfma_fn fn;
-  if (fmt == FMT_I8) fn = swiglu ? mfma_kernel<FMT_I8, EG_SWIGLU> : mfma_kernel<FMT_I8, EG_PLAIN>;
-  else if (fmt == FMT_Q4) fn = swiglu ? mfma_kernel<FMT_Q4, EG_SWIGLU> : mfma_kernel<FMT_Q4, EG_PLAIN>;
-  else fn = swiglu ? mfma_kernel<FMT_F16, EG_SWIGLU> : mfma_kernel<FMT_F16, EG_PLAIN>;
-  hipLaunchKernelGGL(fn, dim3((a.N + 15) / 16, E), dim3(256), 0, stream, a);
+  // wavefronts per workgroup: the fewest of 4, 8, 16 that leave each wavefront at most four
+  // batches; batches per round = batches per wavefront, capped at 4 (measured on MI355X);
+  // AFX_MFMA_WAVES=4|8|16 overrides when that count also leaves at most four batches
+  const int ks = fmt == FMT_I8 ? 64 : fmt == FMT_Q4 ? 128 : 32;
+  const int nsteps = a.K / ks;
+  auto batches = [&](int w) { return ((nsteps + w - 1) / w + kSPB - 1) / kSPB; };
+  static int nw_env = -1;
+  if (nw_env < 0) {
+    const char* e = getenv("AFX_MFMA_WAVES");
+    nw_env = e ? atoi(e) : 0;
+  }
+  int nw = batches(4) <= 4 ? 4 : batches(8) <= 4 ? 8 : 16;
+  if ((nw_env == 4 || nw_env == 8 || nw_env == 16) && batches(nw_env) <= 4) nw = nw_env;   // tuning override
+  const int nbw = batches(nw) < 4 ? batches(nw) : 4;
+  AFX_REQUIRE(nsteps >= nw, "%s: K=%d too short for %d K ranges", what, a.K, nw);
+  mfma_fn fn = pick_mfma(fmt, swiglu, nw, nbw);
+  hipLaunchKernelGGL(fn, dim3((a.N + 15) / 16, E), dim3(nw * 64), 0, stream, b);
   return check_launch(what);
 }
 

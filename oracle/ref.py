@@ -21,7 +21,8 @@ Pinning status (see tests/test_oracle.py):
   attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
   topk_gate / moe_layer                 pinned: reference tie KAT + HF Qwen3-MoE block
   decoder step / generate               pinned: HF LlamaForCausalLM (tiny, fp32)
-  palettize_lut4                        parity unpinned (loose properties only)
+  palettize_lut4 (aneforge_amd._blob)   pinned: vectors recorded from the reference function
+                                        (tests/golden/make_lut4_vectors.py, lut4_vectors.npz)
 """
 from __future__ import annotations
 

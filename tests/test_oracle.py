@@ -331,3 +331,19 @@ def test_q4_0_f16_dequant_matches_reference_rounding():
     r = ref.dequant_q4_0_f16(blocks, 1, 32)
     assert r[0, 0] == np.float32(1433 / 2048)
     assert np.all(r == r[0, 0])
+
+
+def test_palettize_lut4_matches_reference_vectors():
+    # vectors recorded from the reference's palettize_lut4 (aneforge/_blob.py:28-43) by
+    # tests/golden/make_lut4_vectors.py: packed indices and fp16 codebook must match bit for bit
+    import os
+    from aneforge_amd import _blob
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "lut4_vectors.npz"))
+    names = sorted({k.split("__")[0] for k in z.files})
+    assert len(names) == 5
+    for name in names:
+        W = z[f"{name}__W"]
+        packed, cb = _blob.palettize_lut4(W)
+        assert packed.dtype == np.uint8 and cb.dtype == np.float16, name
+        np.testing.assert_array_equal(packed, z[f"{name}__packed"], err_msg=name)
+        np.testing.assert_array_equal(cb.view(np.uint16), z[f"{name}__codebook"].view(np.uint16), err_msg=name)

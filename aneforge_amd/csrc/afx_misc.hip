@@ -8,6 +8,54 @@
 namespace afx {
 
 // ---- RMSNorm (aneforge/graph.py:293-301; textbook form as in tests/test_moe.py:26) ----
+// Vector form: each thread keeps up to NV 16-byte vectors of its row in registers between the
+// sum of squares and the scaling (D % 8 == 0, 16-byte aligned rows, D <= 2048 * NV).
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const half_t* __restrict__ x, int ldx,
+                                                          const half_t* __restrict__ g, float eps,
+                                                          half_t* __restrict__ y, int ldy, int D) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, t = threadIdx.x;
+  const int nv = D >> 3;
+  const u4* xr = (const u4*)(x + (size_t)m * ldx);
+  u4 xv[NV], gv[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int f = t + 256 * i < nv ? t + 256 * i : nv - 1;
+    xv[i] = xr[f];
+    gv[i] = ((const u4*)g)[f];
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float q = dot2(as_h2(xv[i].x), as_h2(xv[i].x), 0.0f);
+    q = dot2(as_h2(xv[i].y), as_h2(xv[i].y), q);
+    q = dot2(as_h2(xv[i].z), as_h2(xv[i].z), q);
+    q = dot2(as_h2(xv[i].w), as_h2(xv[i].w), q);
+    ss += t + 256 * i < nv ? q : 0.0f;
+  }
+  ss = wave_sum(ss);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  const float rstd = 1.0f / __builtin_sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
+  u4* yr = (u4*)(y + (size_t)m * ldy);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (t + 256 * i >= nv) break;
+    uint32_t* xw = (uint32_t*)&xv[i];
+    const uint32_t* gw = (const uint32_t*)&gv[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const h2 xx = as_h2(xw[j]), gg = as_h2(gw[j]);
+      h2 o;
+      o.x = (half_t)(((float)xx.x * rstd) * (float)gg.x);
+      o.y = (half_t)(((float)xx.y * rstd) * (float)gg.y);
+      xw[j] = as_u32(o);
+    }
+    yr[t + 256 * i] = xv[i];
+  }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const half_t* __restrict__ x, int ldx,
                                                       const half_t* __restrict__ g, float eps,
                                                       half_t* __restrict__ y, int ldy, int D) {
@@ -411,6 +459,15 @@ extern "C" {
 
 int afx_rmsnorm(const void* x, int ldx, const void* gamma, float eps, void* y, int ldy, int M, int D, void* stream) {
   AFX_REQUIRE(x && gamma && y && M >= 1 && D >= 1, "afx_rmsnorm: bad arguments");
+  const bool vec = D % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && D <= 8192 && (((uintptr_t)x | (uintptr_t)y |
+                   (uintptr_t)gamma) & 15) == 0;
+  if (vec) {
+    const int nv = (D / 8 + 255) / 256;
+    auto fn = nv <= 1 ? rmsnorm_vec_kernel<1> : nv <= 2 ? rmsnorm_vec_kernel<2> : rmsnorm_vec_kernel<4>;
+    hipLaunchKernelGGL(fn, dim3(M), dim3(256), 0, (hipStream_t)stream, (const half_t*)x, ldx, (const half_t*)gamma,
+                       eps, (half_t*)y, ldy, D);
+    return check_launch("afx_rmsnorm");
+  }
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (const half_t*)x, ldx,
                      (const half_t*)gamma, eps, (half_t*)y, ldy, D);
   return check_launch("afx_rmsnorm");

@@ -17,45 +17,60 @@
 
 namespace afx {
 
+// One wavefront per token (tokens w, w + 4, ... for wavefront w); lane l owns experts l, l + 64, ...
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                        int renorm, float* __restrict__ gate,
                                                        int* __restrict__ sel, int* __restrict__ cnt,
                                                        int* __restrict__ list) {
   extern __shared__ int s_sel[];   // [T][k]
-  const int t = threadIdx.x;
-  for (int tt = t; tt < T; tt += blockDim.x) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int kMaxPerLane = 33;  // E <= 2049 = 64 * 32 + 1
+  for (int tt = wave; tt < T; tt += 4) {
     const float* lr = logits + (size_t)tt * E;
+    float lg[kMaxPerLane];
     float m = -INFINITY;
-    for (int e = 0; e < E; ++e) m = fmaxf(m, lr[e]);
-    float s = 0.0f;
-    for (int e = 0; e < E; ++e) s += expf(lr[e] - m);
-    const float inv = 1.0f / s;
-    // k rounds: max of the fp16 probabilities, lowest index on exact ties
-    float picked[64];
-    int chosen[64];
-    float tot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) {
+      const int e = lane + 64 * j;
+      lg[j] = e < E ? lr[e] : -INFINITY;
+      m = fmaxf(m, lg[j]);
+    }
+    m = wave_max(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) sum += lane + 64 * j < E ? expf(lg[j] - m) : 0.0f;
+    const float inv = 1.0f / wave_sum(sum);
+    // probabilities rounded to fp16 (-1 marks experts this lane does not own)
+    float p[kMaxPerLane];
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) p[j] = lane + 64 * j < E ? (float)(half_t)(expf(lg[j] - m) * inv) : -1.0f;
+    // k rounds: max of the fp16 probabilities, lowest index on exact ties; lane r keeps round r
+    float tot = 0.0f, mine = 0.0f;
+    int mine_e = 0;
     for (int r = 0; r < k; ++r) {
       float best = -1.0f;
-      int bi = -1;
-      for (int e = 0; e < E; ++e) {
-        bool used = false;
-        for (int q = 0; q < r; ++q) used |= chosen[q] == e;
-        if (used) continue;
-        const float p = (float)(half_t)(expf(lr[e] - m) * inv);
-        if (p > best) { best = p; bi = e; }
-      }
-      chosen[r] = bi;
-      picked[r] = best;
-      tot += best;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < kMaxPerLane; ++j)
+        if (p[j] > best) { best = p[j]; bi = lane + 64 * j; }   // ascending index: first max wins
+      const float wb = wave_max(best);
+      float cand = best == wb ? (float)bi : 3.0e38f;
+      cand = -wave_max(-cand);                   // lowest index holding the maximum
+      const int win = (int)cand;
+#pragma unroll
+      for (int j = 0; j < kMaxPerLane; ++j)
+        if (lane + 64 * j == win) p[j] = -1.0f;  // taken
+      if (lane == r) { mine = wb; mine_e = win; }
+      tot += wb;
     }
-    for (int r = 0; r < k; ++r) {
-      gate[(size_t)tt * k + r] = renorm ? picked[r] / tot : picked[r];
-      sel[(size_t)tt * k + r] = chosen[r];
-      s_sel[tt * k + r] = chosen[r];
+    if (lane < k) {
+      gate[(size_t)tt * k + lane] = renorm ? mine / tot : mine;
+      sel[(size_t)tt * k + lane] = mine_e;
+      s_sel[tt * k + lane] = mine_e;
     }
   }
   __syncthreads();
-  for (int e = t; e < E; e += blockDim.x) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int c = 0;
     for (int i = 0; i < T * k; ++i)
       if (s_sel[i] == e) list[(size_t)e * T + c++] = i;

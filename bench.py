@@ -348,27 +348,35 @@ def cpu_baseline_decode(seconds: float = 12.0):
     cos, sin = ref.rope_tables(P + 64, dh)
     cfg = {"n_heads": H, "n_kv_heads": KV, "dh": dh, "norm_eps": 1e-5}
     h = rng.standard_normal((1, D)).astype(np.float32)
-    t_layer, t_head, n, t_end = [], [], 0, time.perf_counter() + seconds
-    while time.perf_counter() < t_end or n < 2:
-        t0 = time.perf_counter()
-        p = P + (n % 64)
-        ref.cpu_decode_layer_f32(h, w, cfg, Kc, Vc, p, cos[p].astype(np.float32), sin[p].astype(np.float32))
-        t1 = time.perf_counter()
-        _ = h @ lm.T
-        t2 = time.perf_counter()
-        t_layer.append(t1 - t0)
-        t_head.append(t2 - t1)
-        n += 1
+    def sample(budget):
+        t_layer, t_head, n, t_end = [], [], 0, time.perf_counter() + budget
+        while time.perf_counter() < t_end or n < 2:
+            t0 = time.perf_counter()
+            p = P + (n % 64)
+            ref.cpu_decode_layer_f32(h, w, cfg, Kc, Vc, p, cos[p].astype(np.float32), sin[p].astype(np.float32))
+            t1 = time.perf_counter()
+            _ = h @ lm.T
+            t2 = time.perf_counter()
+            t_layer.append(t1 - t0)
+            t_head.append(t2 - t1)
+            n += 1
+        return 32 * min(t_layer) + min(t_head), n
+
+    per_tok, n = sample(seconds)
+    threads, per_tok_1, n1 = len(os.sched_getaffinity(0)), None, 0
     try:
-        from threadpoolctl import threadpool_info
+        from threadpoolctl import threadpool_info, threadpool_limits
         threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        with threadpool_limits(limits=1, user_api="blas"):
+            per_tok_1, n1 = sample(seconds / 3)
     except Exception:
-        threads = len(os.sched_getaffinity(0))
-    per_tok = 32 * min(t_layer) + min(t_head)
+        pass
     return {"value": 1.0 / per_tok, "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "value_1thread": None if per_tok_1 is None else 1.0 / per_tok_1,
+            "host_cores_available": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count(),
             "sample": f"numpy fp32 restatement of the reference CPU decode (bench/decode_measurement.py:86-132 + "
                       f"GQA/RoPE) on one 4096/11008/32-head layer at pos {P} + the 32000x4096 lm_head, min of "
-                      f"{n} reps, extrapolated to 32 layers; host cores available {len(os.sched_getaffinity(0))}"}
+                      f"{n} reps ({n1} at 1 BLAS thread), extrapolated to 32 layers"}
 
 
 def bench_decode(args):

@@ -68,6 +68,10 @@ SIGNATURES: dict[str, tuple] = {
     "afx_moe_topk": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "afx_moe_gateup": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
     "afx_moe_down": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
+    # batched prefill
+    "afx_gemm": (_i, [_i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
+    "afx_qkv_split_rope": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i, _vp, _vp, _ll, _i, _vp]),
+    "afx_prefill_attn": (_i, [_vp, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _vp]),
     "afx_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }
 

@@ -5,6 +5,7 @@ from __future__ import annotations
 
 import ctypes as C
 
+import numpy as np
 import torch
 
 from . import _hip
@@ -332,3 +333,39 @@ def moe_combine(h, y, gate, shared=None, out=None):
         out = torch.empty_like(h)
     _hip.call("afx_moe_combine", P(h), P(y), P(gate), P(shared), P(out), T, k, D, stream())
     return out
+
+
+# ----------------------------------------------------------------------------- batched prefill
+GEMM_EPI = {"f16": 0, "resid": 1, "f32": 2, "swiglu": 3}
+
+
+def gemm(fmt, w, scale, x, y=None, bias=None, residual=None, epi="f16"):
+    """MFMA GEMM for many rows: y = epi(x @ W^T); epi "swiglu" writes [M, N/2]."""
+    _dev(w, x)
+    M, Kd = x.shape
+    N = w.shape[0]
+    if y is None:
+        cols = N // 2 if epi == "swiglu" else N
+        y = torch.empty((M, cols), dtype=torch.float32 if epi == "f32" else torch.float16, device=x.device)
+    if epi == "resid" and residual is None:
+        residual = y
+    _hip.call("afx_gemm", FMT[fmt], P(w), P(scale), P(x), x.stride(0), P(y), y.stride(0), M, N, Kd, P(bias),
+              P(residual), GEMM_EPI[epi], stream())
+    return y
+
+
+def qkv_split_rope(qkv, nq, nk, dh, cos_t, sin_t, pos0, q, kcache, vcache, rope=True):
+    """Prompt projection rows -> RoPE'd q and cache rows at positions pos0 .. pos0 + M - 1."""
+    M = qkv.shape[0]
+    _hip.call("afx_qkv_split_rope", P(qkv), qkv.stride(0), M, nq, nk, dh, P(cos_t), P(sin_t), int(pos0), int(rope),
+              P(q), q.stride(0), P(kcache), P(vcache), kcache.stride(-3), kcache.shape[-2], stream())
+
+
+def prefill_attn(q, kcache, vcache, o, pos0, Hq, Hkv, scale=None):
+    """Causal GQA attention of q [M, Hq*D] (query m at pos0 + m) over cache rows [0, pos0 + m]."""
+    M = q.shape[0]
+    D = kcache.shape[-1]
+    scale = 1.0 / float(np.sqrt(D)) if scale is None else float(scale)
+    _hip.call("afx_prefill_attn", P(q), q.stride(0), P(kcache), P(vcache), kcache.stride(-3), kcache.shape[-2],
+              P(o), o.stride(0), M, int(pos0), Hq, Hkv, D, scale, stream())
+    return o

@@ -1,0 +1,211 @@
+// Tiled MFMA GEMM for many activation rows (the batched prefill's linears):
+//
+//   Y[m, n] = epilogue( sum_k X[m, k] * W^[n, k] ),   X fp16 [M][K] (row stride ldx),
+//   W int8 codes with an fp16 row scale (W^ = q * s, the compress="int8" linear,
+//   aneforge/_compile.py:171-179 and 375-385) or fp16 [N][K].
+//
+// Prefill multiplies the same weights by hundreds or thousands of token rows, so unlike the
+// decode GEMV this is a dense contraction that v_mfma_f32_16x16x32_f16 bounds.  A 256-thread
+// workgroup computes a 128 x 128 tile of Y; its four wavefronts own 64 x 64 quarters, each as
+// 4 x 4 MFMA tiles (16 fp32 accumulators per lane).  K advances 64 at a time through two LDS
+// stages: the next stage's global loads are issued before the current stage's MFMAs and land in
+// the other stage afterwards, one barrier per step.  LDS rows are padded (144 bytes for fp16,
+// 72 for int8) so the 16-byte / 8-byte fragment reads of 16 rows hit distinct banks.
+// Fragments: A lane l = row l % 16, k 8 * (l / 16) .. + 7 (activations); B lane l = column
+// l % 16 (output feature), same k (weights; int8 codes converted exactly to fp16 in
+// registers, the row scale applied to the fp32 result); D lane l = rows 4 * (l / 16) + i,
+// column l % 16.
+// Tiles are assigned so that the row tiles of one weight tile run consecutively on one XCD
+// (dispatch is round-robin over the 8 XCDs): each weight tile is then fetched into one L2.
+#include "afx_gemv_impl.h"
+
+namespace afx {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+constexpr int kGBM = 128, kGBN = 128, kGBK = 64;
+constexpr int kGAStride = kGBK * 2 + 16;            // bytes per staged activation row
+
+template <int FMT> struct GemmW;
+template <> struct GemmW<FMT_I8> { static constexpr int kRow = kGBK, kStride = kGBK + 8, kChunks = 2; };
+template <> struct GemmW<FMT_F16> { static constexpr int kRow = kGBK * 2, kStride = kGBK * 2 + 16, kChunks = 4; };
+
+struct GemmArgs {
+  const void* w;          // [N][K] codes (int8) or values (fp16)
+  const half_t* scale;    // int8: [N] row scales
+  const half_t* bias;     // [N] or null
+  const half_t* x;        // [M] rows of K, stride ldx
+  void* y;                // output rows, stride ldy (fp16, or fp32 for EPI_F32)
+  const half_t* resid;    // EPI_RESID: [M][ldy] fp16 (may alias y)
+  int ldx, ldy, M, N, K, epi, tiles_m, tiles, per_xcd;
+};
+
+__device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
+  h2 a, b, c, d;
+  i8x4_to_h2(v.x, a, b);
+  i8x4_to_h2(v.y, c, d);
+  h8 r;
+  r[0] = a.x; r[1] = a.y; r[2] = b.x; r[3] = b.y; r[4] = c.x; r[5] = c.y; r[6] = d.x; r[7] = d.y;
+  return r;
+}
+
+template <int FMT, int EG>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+  constexpr int WS = GemmW<FMT>::kStride, WR = GemmW<FMT>::kRow, WC = GemmW<FMT>::kChunks;
+  __shared__ __align__(16) unsigned char As[2][kGBM * kGAStride];
+  __shared__ __align__(16) unsigned char Bs[2][kGBN * WS];
+  // tile: the XCD (id % 8) gets a contiguous range of logical tiles, row tiles fastest
+  const int id = blockIdx.x;
+  const int logical = (id & 7) * a.per_xcd + (id >> 3);
+  if (logical >= a.tiles) return;                   // whole workgroup: no barrier reached
+  const int n0 = (logical / a.tiles_m) * kGBN, m0 = (logical % a.tiles_m) * kGBM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = a.M, N = a.N, K = a.K;
+  const int nk = K / kGBK;
+
+  // global-load roles: activations 4 x 16 B per thread (row c / 8, chunk c % 8), weights WC x 16 B
+  const half_t* xp[4];
+  int aoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, r = c >> 3, ch = c & 7;
+    const int m = m0 + r < M ? m0 + r : M - 1;     // clamped rows are computed, not stored
+    xp[i] = a.x + (size_t)m * a.ldx + ch * 8;
+    aoff[i] = r * kGAStride + ch * 16;
+  }
+  const unsigned char* wp[WC];
+  int boff[WC];
+#pragma unroll
+  for (int i = 0; i < WC; ++i) {
+    const int c = tid + 256 * i;
+    const int r = FMT == FMT_I8 ? c >> 2 : c >> 3, ch = FMT == FMT_I8 ? c & 3 : c & 7;
+    const int n = n0 + r < N ? n0 + r : N - 1;
+    wp[i] = (const unsigned char*)a.w + (size_t)n * (FMT == FMT_I8 ? K : 2 * K) + ch * 16;
+    boff[i] = r * WS + ch * 16;
+  }
+  u4 ra[4], rb[WC];
+  auto load = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = *(const u4*)(xp[i] + (size_t)kt * kGBK);
+#pragma unroll
+    for (int i = 0; i < WC; ++i) rb[i] = __builtin_nontemporal_load((const u4*)(wp[i] + (size_t)kt * WR));
+  };
+  auto stage = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(u4*)(As[s] + aoff[i]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < WC; ++i) {
+      if constexpr (FMT == FMT_I8) {               // 72-byte rows: two 8-byte stores keep alignment
+        *(u2*)(Bs[s] + boff[i]) = (u2){rb[i].x, rb[i].y};
+        *(u2*)(Bs[s] + boff[i] + 8) = (u2){rb[i].z, rb[i].w};
+      } else {
+        *(u4*)(Bs[s] + boff[i]) = rb[i];
+      }
+    }
+  };
+
+  f4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  load(0);
+  stage(0);
+  __syncthreads();
+  const int fr = lane & 15, fg = lane >> 4;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int s = kt & 1;
+    if (kt + 1 < nk) load(kt + 1);                 // next stage streams during this stage's MFMAs
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      h8 af[4], bf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = __builtin_bit_cast(h8, *(const u4*)(As[s] + (wm * 64 + i * 16 + fr) * kGAStride + (kk * 32 + 8 * fg) * 2));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const unsigned char* bp = Bs[s] + (wn * 64 + j * 16 + fr) * WS;
+        if constexpr (FMT == FMT_I8) bf[j] = i8x8_to_h8(*(const u2*)(bp + kk * 32 + 8 * fg));
+        else bf[j] = __builtin_bit_cast(h8, *(const u4*)(bp + (kk * 32 + 8 * fg) * 2));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) stage(s ^ 1);                 // the other stage was last read before the previous barrier
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 4 * fg + i of column fr in every 16 x 16 tile
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 64 + j * 16 + fr;
+    const int nc = n < N ? n : N - 1;
+    const float sc = FMT == FMT_I8 ? (float)a.scale[nc] : 1.0f;
+    const float bi = a.bias ? (float)a.bias[nc] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
+        const float v = acc[i][j][r] * sc + bi;
+        if constexpr (EG == EG_SWIGLU) {
+          // gate row n (even) and up row n + 1 sit in lanes l and l ^ 1
+          const float pv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
+          if ((fr & 1) == 0 && m < M && n < N) {
+            const float g = (float)(half_t)v, u = (float)(half_t)pv;
+            ((half_t*)a.y)[(size_t)m * a.ldy + (n >> 1)] = (half_t)(silu(g) * u);
+          }
+        } else {
+          if (m < M && n < N) {
+            if (a.epi == EPI_F32) ((float*)a.y)[(size_t)m * a.ldy + n] = v;
+            else if (a.epi == EPI_RESID)
+              ((half_t*)a.y)[(size_t)m * a.ldy + n] = (half_t)((float)a.resid[(size_t)m * a.ldy + n] + (float)(half_t)v);
+            else ((half_t*)a.y)[(size_t)m * a.ldy + n] = (half_t)v;
+          }
+        }
+      }
+    }
+  }
+}
+
+typedef void (*gemm_fn)(GemmArgs);
+
+}  // namespace afx
+
+using namespace afx;
+
+extern "C" {
+
+// Y = epilogue(X @ W^T) for M activation rows (batched prefill).  fmt: 0 = int8 + row scale,
+// 2 = fp16.  epi: 0 fp16, 1 fp16 + residual (resid [M][ldy], may alias y), 2 fp32, 3 SwiGLU
+// over interleaved gate/up rows (y[m][n/2] = silu(g) * u, ldy >= N/2).
+int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy, int M, int N,
+             int K, const void* bias, const void* residual, int epi, void* stream) {
+  AFX_REQUIRE(fmt == FMT_I8 || fmt == FMT_F16, "afx_gemm: format %d not supported (int8 = 0, fp16 = 2)", fmt);
+  AFX_REQUIRE(w && x && y, "afx_gemm: null pointer");
+  AFX_REQUIRE(M >= 1 && N >= 16 && N % 16 == 0 && K >= kGBK && K % kGBK == 0,
+              "afx_gemm: need M >= 1, N %% 16 == 0, K %% 64 == 0 (M=%d N=%d K=%d)", M, N, K);
+  AFX_REQUIRE(ldx >= K && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0,
+              "afx_gemm: x and weights must be 16-byte aligned rows (ldx %% 8 == 0)");
+  AFX_REQUIRE(epi >= 0 && epi <= 3, "afx_gemm: unknown epilogue %d", epi);
+  AFX_REQUIRE(fmt != FMT_I8 || scale, "afx_gemm: int8 weights need row scales");
+  AFX_REQUIRE(epi != EPI_RESID || residual, "afx_gemm: residual pointer required");
+  AFX_REQUIRE(epi == EPI_SWIGLU ? ldy >= N / 2 : ldy >= N, "afx_gemm: ldy=%d too small", ldy);
+  GemmArgs a = {};
+  a.w = w; a.scale = (const half_t*)scale; a.bias = (const half_t*)bias; a.x = (const half_t*)x; a.y = y;
+  a.resid = (const half_t*)residual; a.ldx = ldx; a.ldy = ldy; a.M = M; a.N = N; a.K = K; a.epi = epi;
+  a.tiles_m = (M + kGBM - 1) / kGBM;
+  a.tiles = a.tiles_m * ((N + kGBN - 1) / kGBN);
+  a.per_xcd = (a.tiles + 7) / 8;
+  gemm_fn fn;
+  if (fmt == FMT_I8) fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_I8, EG_SWIGLU> : gemm_kernel<FMT_I8, EG_PLAIN>;
+  else fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_F16, EG_SWIGLU> : gemm_kernel<FMT_F16, EG_PLAIN>;
+  hipLaunchKernelGGL(fn, dim3(8 * a.per_xcd), dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch("afx_gemm");
+}
+
+}  // extern "C"

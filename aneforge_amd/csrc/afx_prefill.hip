@@ -1,0 +1,257 @@
+// Batched prefill around the MFMA GEMM (afx_gemm.hip): the fused projection's split into
+// q / cache rows with RoPE, and causal GQA flash attention over the resident cache.
+//
+// afx_qkv_split_rope: the prompt's [q | k | v] projection rows (q and k rows in RoPE-pair
+// order, as the decode path packs them) -> RoPE'd q [M][Hq*dh] and K/V cache rows at positions
+// pos0 .. pos0 + M - 1.  Same arithmetic as the decode epilogue: the fp16 projection value,
+// then (x0 c0 - x1 s0, x1 c1 + x0 s1) in fp32 with the fp16 tables (aneforge/llm.py:96-105,
+// rows written as in the reference's cache update, aneforge/llm.py:149-168).
+//
+// afx_prefill_attn: o = softmax(q K^T * scale + causal) V for query m at position pos0 + m over
+// cache rows [0, pos0 + m] (aneforge/llm.py:149-168: the prompt attends the cache and itself;
+// GQA head h reads kv head h / G, llm.py:205-211), fp32 scores and softmax, fp16 output.
+// A 256-thread workgroup takes 64 queries of one head; each wavefront 16 of them as MFMA rows.
+// Key blocks of 64 go through LDS: K row-major (the B operand of S = Q K^T reads 16 contiguous
+// bytes of a key row), V transposed while staged (the B operand of O += P V needs 8
+// consecutive keys of one dim).  S stays in registers for an online softmax (row max and sum
+// by DPP rotations inside the 16-lane rows that hold one query row's scores); P goes through a
+// wavefront-private LDS tile to change from the MFMA result layout to the operand layout.
+#include "afx_common.h"
+
+namespace afx {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__global__ void qkv_split_rope_kernel(const half_t* __restrict__ qkv, int ldqkv, int M, int nq, int nk, int dh,
+                                      const half_t* __restrict__ cos_t, const half_t* __restrict__ sin_t,
+                                      int pos0, int rope, half_t* __restrict__ q, int ldq,
+                                      half_t* __restrict__ kc, half_t* __restrict__ vc, long long kv_hs) {
+  const int pairs = (nq + 2 * nk) >> 1;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * pairs) return;
+  const int m = (int)(i / pairs), pr = (int)(i - (long long)m * pairs);
+  const int row0 = 2 * pr, p = pos0 + m;
+  const half_t* src = qkv + (size_t)m * ldqkv + row0;
+  const float v0 = (float)src[0], v1 = (float)src[1];
+  if (row0 < nq + nk) {
+    const bool isk = row0 >= nq;
+    const int rl = isk ? row0 - nq : row0;
+    const int head = rl / dh, d = (rl - head * dh) >> 1, half = dh >> 1;
+    float o0 = v0, o1 = v1;                      // row0 holds dim d, row0 + 1 dim d + dh / 2
+    if (rope) {
+      const float c0 = (float)cos_t[(size_t)p * dh + d], s0 = (float)sin_t[(size_t)p * dh + d];
+      const float c1 = (float)cos_t[(size_t)p * dh + d + half], s1 = (float)sin_t[(size_t)p * dh + d + half];
+      o0 = v0 * c0 - v1 * s0;
+      o1 = v1 * c1 + v0 * s1;
+    }
+    half_t* dst = isk ? kc + (size_t)head * kv_hs + (size_t)p * dh : q + (size_t)m * ldq + (size_t)head * dh;
+    dst[d] = (half_t)o0;
+    dst[d + half] = (half_t)o1;
+  } else {
+    const int rl = row0 - nq - nk;
+    const int head = rl / dh, d = rl - head * dh;
+    half_t* dst = vc + (size_t)head * kv_hs + (size_t)p * dh + d;
+    dst[0] = (half_t)v0;
+    dst[1] = (half_t)v1;
+  }
+}
+
+constexpr int kPD = 128;                 // head dim
+constexpr int kPQ = 64, kPK = 64;        // queries per workgroup, keys per block
+constexpr int kKStride = kPD * 2 + 16;   // bytes per staged K row
+constexpr int kVStride = kPK * 2 + 16;   // bytes per staged V^T row (one dim, 64 keys)
+constexpr int kPStride = kPK * 2 + 16;   // bytes per staged P row
+
+struct PrefillAttnArgs {
+  const half_t* q; const half_t* k; const half_t* v; half_t* o;
+  long long kv_hs;
+  int ldq, ldo, M, pos0, Hq, Hkv, Mmax;
+  float scale_log2;
+};
+
+// max / sum over the 16 lanes of each DPP row (every lane receives the result)
+template <bool MAX>
+__device__ __forceinline__ float row16(float v) {
+  auto f = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = f(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false)));
+  v = f(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false)));
+  v = f(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false)));
+  v = f(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false)));
+  return v;
+}
+
+__global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
+  __shared__ __align__(16) unsigned char Ks[kPK * kKStride];
+  __shared__ __align__(16) unsigned char Vt[kPD * kVStride];
+  __shared__ __align__(16) unsigned char Ps[4][16 * kPStride];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int h = blockIdx.y, kvh = h / (a.Hq / a.Hkv);
+  const int m0 = blockIdx.x * kPQ;
+  const int mlast = m0 + kPQ - 1 < a.M - 1 ? m0 + kPQ - 1 : a.M - 1;
+  const int kend = a.pos0 + mlast;               // last key any query of this workgroup sees
+  const int nkb = kend / kPK + 1;
+  const half_t* kbase = a.k + (size_t)kvh * a.kv_hs;
+  const half_t* vbase = a.v + (size_t)kvh * a.kv_hs;
+
+  // this lane's query fragments (row fr of the wavefront's 16, dims ks * 32 + 8 * fg ..)
+  const int mq = m0 + wave * 16 + fr;
+  const half_t* qrow = a.q + (size_t)(mq < a.M ? mq : a.M - 1) * a.ldq + (size_t)h * kPD;
+  h8 qf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = __builtin_bit_cast(h8, *(const u4*)(qrow + ks * 32 + 8 * fg));
+  // positions of the four query rows this lane's results belong to
+  int qpos[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qpos[i] = a.pos0 + m0 + wave * 16 + 4 * fg + i;
+
+  f4 acc[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) acc[d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+  float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, lrow[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  unsigned char* pw = Ps[wave];
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int key0 = kb * kPK;
+    // stage K (row-major) and V (transposed): K as 4 x 16 B per thread, V one key per lane
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, r = c >> 4, ch = c & 15;
+      const int key = key0 + r < a.Mmax ? key0 + r : a.Mmax - 1;   // past the cache: masked below
+      *(u4*)(Ks + r * kKStride + ch * 16) = *(const u4*)(kbase + (size_t)key * kPD + ch * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ch = wave * 4 + i;                 // dims ch * 8 .. + 7 of key `lane`
+      const int key = key0 + lane < a.Mmax ? key0 + lane : a.Mmax - 1;
+      const u4 vv = *(const u4*)(vbase + (size_t)key * kPD + ch * 8);
+      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        *(uint16_t*)(Vt + (ch * 8 + 2 * j) * kVStride + lane * 2) = (uint16_t)(w4[j] & 0xffffu);
+        *(uint16_t*)(Vt + (ch * 8 + 2 * j + 1) * kVStride + lane * 2) = (uint16_t)(w4[j] >> 16);
+      }
+    }
+    __syncthreads();
+
+    // S = Q K^T for 16 queries x 64 keys (four 16-key tiles)
+    f4 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s[j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const h8 kf = __builtin_bit_cast(h8, *(const u4*)(Ks + (j * 16 + fr) * kKStride + (ks * 32 + 8 * fg) * 2));
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[ks], kf, s[j], 0, 0, 0);
+      }
+    }
+    // online softmax (log2 domain); lane holds rows 4 * fg + i, key j * 16 + fr
+    float alpha[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float bm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = key0 + j * 16 + fr;
+        const float x = key <= qpos[i] ? s[j][i] * a.scale_log2 : -INFINITY;
+        s[j][i] = x;
+        bm = fmaxf(bm, x);
+      }
+      bm = row16<true>(bm);
+      const float mn = fmaxf(mrow[i], bm);         // finite: every row sees key 0 in block 0
+      alpha[i] = __builtin_amdgcn_exp2f(mrow[i] - mn);
+      mrow[i] = mn;
+      float rs = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = __builtin_amdgcn_exp2f(s[j][i] - mn);
+        s[j][i] = p;
+        rs += p;
+      }
+      lrow[i] = lrow[i] * alpha[i] + row16<false>(rs);
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[d][i] *= alpha[i];
+    // P (fp16) through the wavefront's LDS tile into the A-operand layout
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *(half_t*)(pw + (4 * fg + i) * kPStride + (j * 16 + fr) * 2) = (half_t)s[j][i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    h8 pf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) pf[ks] = __builtin_bit_cast(h8, *(const u4*)(pw + fr * kPStride + (ks * 32 + 8 * fg) * 2));
+    // O += P V over eight 16-dim tiles
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const h8 vf = __builtin_bit_cast(h8, *(const u4*)(Vt + (d * 16 + fr) * kVStride + (ks * 32 + 8 * fg) * 2));
+        acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vf, acc[d], 0, 0, 0);
+      }
+    __syncthreads();                               // Ks, Vt and this wavefront's P are reused next block
+  }
+
+  // o = acc / l: lane holds rows 4 * fg + i of dim d * 16 + fr
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + wave * 16 + 4 * fg + i;
+    if (m >= a.M) continue;
+    const float inv = 1.0f / lrow[i];
+    half_t* orow = a.o + (size_t)m * a.ldo + (size_t)h * kPD;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) orow[d * 16 + fr] = (half_t)(acc[d][i] * inv);
+  }
+}
+
+}  // namespace afx
+
+using namespace afx;
+
+extern "C" {
+
+// qkv [M][ldqkv] = [q (nq) | k (nk) | v (nk)] projection rows, q and k in RoPE-pair order
+// (row 2i = dim i, 2i + 1 = dim i + dh/2 of a head).  Writes q [M][ldq] (natural order) and cache
+// rows kc/vc[head][pos0 + m][dh] (head stride kv_hs elements, cache length kv_len).
+int afx_qkv_split_rope(const void* qkv, int ldqkv, int M, int nq, int nk, int dh, const void* cos_tab,
+                       const void* sin_tab, int pos0, int rope, void* q, int ldq, void* kcache, void* vcache,
+                       long long kv_hs, int kv_len, void* stream) {
+  AFX_REQUIRE(qkv && q && kcache && vcache && (!rope || (cos_tab && sin_tab)), "afx_qkv_split_rope: null pointer");
+  AFX_REQUIRE(M >= 1 && dh >= 2 && dh % 2 == 0 && nq % dh == 0 && nk % dh == 0 && ldqkv >= nq + 2 * nk && ldq >= nq,
+              "afx_qkv_split_rope: bad sizes");
+  AFX_REQUIRE(pos0 >= 0 && pos0 + M <= kv_len && kv_hs >= (long long)kv_len * dh,
+              "afx_qkv_split_rope: positions %d..%d outside the %d-row cache", pos0, pos0 + M - 1, kv_len);
+  const long long n = (long long)M * ((nq + 2 * nk) / 2);
+  hipLaunchKernelGGL(qkv_split_rope_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const half_t*)qkv, ldqkv, M, nq, nk, dh, (const half_t*)cos_tab, (const half_t*)sin_tab, pos0,
+                     rope, (half_t*)q, ldq, (half_t*)kcache, (half_t*)vcache, kv_hs);
+  return check_launch("afx_qkv_split_rope");
+}
+
+// Causal GQA attention of M prompt queries (query m at position pos0 + m) over cache rows
+// [0, pos0 + m] (head dim 128).  q [M][ldq] and o [M][ldo] hold head h at h * 128; the cache is
+// k/v[kvh][Mmax][128] with head stride kv_hs elements.
+int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vcache, long long kv_hs, int Mmax,
+                     void* o, int ldo, int M, int pos0, int Hq, int Hkv, int D, float scale, void* stream) {
+  AFX_REQUIRE(q && kcache && vcache && o, "afx_prefill_attn: null pointer");
+  AFX_REQUIRE(D == kPD, "afx_prefill_attn: head dim %d not supported (128)", D);
+  AFX_REQUIRE(Hkv >= 1 && Hq % Hkv == 0, "afx_prefill_attn: bad heads Hq=%d Hkv=%d", Hq, Hkv);
+  AFX_REQUIRE(M >= 1 && pos0 >= 0 && pos0 + M <= Mmax && kv_hs >= (long long)Mmax * D,
+              "afx_prefill_attn: positions %d..%d outside the %d-row cache", pos0, pos0 + M - 1, Mmax);
+  AFX_REQUIRE(ldq % 8 == 0 && ldq >= Hq * D && ldo >= Hq * D && kv_hs % 8 == 0 &&
+              (((uintptr_t)q | (uintptr_t)kcache | (uintptr_t)vcache) & 15) == 0,
+              "afx_prefill_attn: q / cache must be 16-byte aligned rows");
+  PrefillAttnArgs a = {};
+  a.q = (const half_t*)q; a.k = (const half_t*)kcache; a.v = (const half_t*)vcache; a.o = (half_t*)o;
+  a.kv_hs = kv_hs; a.ldq = ldq; a.ldo = ldo; a.M = M; a.pos0 = pos0; a.Hq = Hq; a.Hkv = Hkv; a.Mmax = Mmax;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(prefill_attn_kernel, dim3((M + kPQ - 1) / kPQ, Hq), dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch("afx_prefill_attn");
+}
+
+}  // extern "C"

@@ -157,6 +157,23 @@ int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int
 int afx_moe_combine(const void* h, const float* y, const float* gate, const void* shared, void* out, int T,
                     int k, int D, void* stream);
 
+/* ---- batched prefill --------------------------------------------------------------------- */
+
+/* Y = epilogue(X @ W^T) for M prompt rows on MFMA: the linears of the reference's batched
+ * prefill (_prefiller, aneforge/llm.py:149-168, 489-544) with the compress="int8" weights of
+ * aneforge/_compile.py:171-179 / 375-385 (fmt 0) or fp16 (fmt 2).  epi: 0 fp16, 1 fp16 +
+ * residual, 2 fp32, 3 SwiGLU over interleaved gate/up rows (aneforge/llm.py:171-175). */
+int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy, int M, int N,
+             int K, const void* bias, const void* residual, int epi, void* stream);
+/* prompt [q | k | v] rows -> RoPE'd q and K/V cache rows at pos0.. (aneforge/llm.py:96-105, 149-168) */
+int afx_qkv_split_rope(const void* qkv, int ldqkv, int M, int nq, int nk, int dh, const void* cos_tab,
+                       const void* sin_tab, int pos0, int rope, void* q, int ldq, void* kcache, void* vcache,
+                       long long kv_hs, int kv_len, void* stream);
+/* causal GQA attention of the prompt over the resident cache (_attn_prefill_kv, aneforge/llm.py:149-168;
+ * GQA as _repeat_kv3, :205-211; softmax as aneforge/_bridges/ane_sdpa_fused.py:57-68) */
+int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vcache, long long kv_hs, int Mmax,
+                     void* o, int ldo, int M, int pos0, int Hq, int Hkv, int D, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

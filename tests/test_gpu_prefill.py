@@ -1,0 +1,109 @@
+"""Parity of the batched-prefill kernels (MFMA GEMM, q/cache split with RoPE, causal GQA flash
+attention) against the oracle, at sizes the oracle finishes in seconds."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _util import check_f16, check_hidden, dev, host, say
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(fmt, N, K, rng):
+    import torch
+    if fmt == "int8":
+        q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = (np.abs(rng.normal(0, 0.02, N)) / 127).astype(np.float16)
+        return dev(q), dev(s), ref.dequant_w8(q, s)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    return dev(w), None, w.astype(np.float32)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp16"])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 128), (70, 384, 320), (300, 256, 640)])
+@pytest.mark.parametrize("epi", ["f16", "resid", "f32", "swiglu"])
+def test_gemm_matches_oracle(fmt, M, N, K, epi):
+    import torch
+    from aneforge_amd import _kernels as Kn
+    rng = np.random.default_rng(M * 1000 + N + K)
+    w, s, Wf = _weights(fmt, N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float16) if epi in ("f16", "f32") else None
+    say(f"gemm {fmt} M={M} N={N} K={K} epi={epi}")
+    want_lin = np.asarray(x, np.float64) @ np.asarray(Wf, np.float64).T
+    if bias is not None:
+        want_lin = want_lin + bias.astype(np.float64)
+    if epi == "resid":
+        r = rng.standard_normal((M, N)).astype(np.float16)
+        y = dev(r)
+        Kn.gemm(fmt, w, s, dev(x), y=y, residual=y, epi="resid")
+        want = ref.r16(r.astype(np.float64) + ref.r16(want_lin))
+        check_hidden(host(y), want, what=f"gemm {fmt} resid")
+        return
+    got = Kn.gemm(fmt, w, s, dev(x), bias=None if bias is None else dev(bias), epi=epi)
+    if epi == "swiglu":
+        g, u = ref.r16(want_lin[:, 0::2]), ref.r16(want_lin[:, 1::2])
+        check_f16(host(got), ref.r16(ref.silu(g) * u), what=f"gemm {fmt} swiglu")
+    elif epi == "f32":
+        check_f16(host(got), want_lin, what=f"gemm {fmt} f32")
+    else:
+        check_f16(host(got), ref.r16(want_lin), what=f"gemm {fmt} f16")
+
+
+def test_gemm_rejects_bad_shapes():
+    import torch
+    from aneforge_amd import _kernels as Kn
+    w = torch.zeros((256, 100), dtype=torch.float16, device="cuda")
+    x = torch.zeros((4, 100), dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="K % 64"):
+        Kn.gemm("fp16", w, None, x)
+
+
+@pytest.mark.parametrize("M,pos0", [(1, 0), (5, 3), (40, 17)])
+def test_qkv_split_rope_matches_oracle(M, pos0):
+    import torch
+    from aneforge_amd import _blob
+    from aneforge_amd import _kernels as Kn
+    H, KV, dh, Mmax = 2, 1, 64, 64
+    rng = np.random.default_rng(M + 31 * pos0)
+    nq, nk = H * dh, KV * dh
+    nat = rng.standard_normal((M, nq + 2 * nk)).astype(np.float16)     # natural [q | k | v]
+    pq, pk = _blob.rope_pair_order(H, dh), _blob.rope_pair_order(KV, dh)
+    packed = np.concatenate([nat[:, :nq][:, pq], nat[:, nq:nq + nk][:, pk], nat[:, nq + nk:]], 1)
+    cos, sin = ref.rope_tables(Mmax, dh)
+    q = torch.zeros((M, nq), dtype=torch.float16, device="cuda")
+    kc = torch.zeros((KV, Mmax, dh), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((KV, Mmax, dh), dtype=torch.float16, device="cuda")
+    say(f"qkv_split_rope M={M} pos0={pos0}")
+    Kn.qkv_split_rope(dev(packed), nq, nk, dh, dev(cos), dev(sin), pos0, q, kc, vc)
+    p = np.arange(pos0, pos0 + M)
+    want_q = ref.rope(nat[:, :nq].reshape(M, H, dh), cos[p][:, None], sin[p][:, None]).reshape(M, nq)
+    want_k = ref.rope(nat[:, nq:nq + nk].reshape(M, KV, dh), cos[p][:, None], sin[p][:, None])
+    check_f16(host(q), want_q, what="q")
+    got_k, got_v = host(kc), host(vc)
+    check_f16(got_k[:, pos0:pos0 + M].transpose(1, 0, 2), want_k, what="k rows")
+    np.testing.assert_array_equal(got_v[:, pos0:pos0 + M].transpose(1, 0, 2),
+                                  nat[:, nq + nk:].reshape(M, KV, dh))
+    assert not got_k[:, :pos0].any() and not got_k[:, pos0 + M:].any()     # other rows untouched
+
+
+@pytest.mark.parametrize("M,pos0,Hq,Hkv", [(1, 0, 4, 2), (70, 37, 4, 2), (130, 0, 8, 2), (64, 190, 2, 2)])
+def test_prefill_attention_matches_oracle(M, pos0, Hq, Hkv):
+    import torch
+    from aneforge_amd import _kernels as Kn
+    D, Mmax = 128, 256
+    rng = np.random.default_rng(M + pos0 + Hq)
+    L = pos0 + M
+    Kc = np.zeros((Hkv, Mmax, D), np.float16)
+    Vc = np.zeros((Hkv, Mmax, D), np.float16)
+    Kc[:, :L] = rng.standard_normal((Hkv, L, D)).astype(np.float16)
+    Vc[:, :L] = rng.standard_normal((Hkv, L, D)).astype(np.float16)
+    q = rng.standard_normal((M, Hq * D)).astype(np.float16)
+    o = torch.zeros((M, Hq * D), dtype=torch.float16, device="cuda")
+    say(f"prefill_attn M={M} pos0={pos0} Hq={Hq} Hkv={Hkv}")
+    Kn.prefill_attn(dev(q), dev(Kc), dev(Vc), o, pos0, Hq, Hkv)
+    mask = np.where(np.arange(L)[None, :] <= pos0 + np.arange(M)[:, None], 0.0, -np.inf)
+    want = ref.attention(q.reshape(M, Hq, D).transpose(1, 0, 2)[None], Kc[None, :, :L], Vc[None, :, :L], mask=mask)
+    check_f16(host(o), want[0].transpose(1, 0, 2).reshape(M, Hq * D), what="prefill attention")

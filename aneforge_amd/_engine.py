@@ -249,6 +249,25 @@ class AttentionDecode:
         K.linear(self.wo.fmt, self.wo.w, self.wo.scale, eng.a[:, :H * dh], y=eng.h, bias=self.wo.bias,
                  residual=eng.h)
 
+    def prefill_supported(self) -> bool:
+        lin = (self.qkv, self.wo)
+        return (not self.qk_norm and self.dh == 128 and all(l.fmt in ("int8", "fp16") for l in lin)
+                and all(l.K % 64 == 0 and l.N % 16 == 0 for l in lin))
+
+    def prefill(self, eng, X, pos0: int, bufs: dict):
+        """Prompt rows X [m, D] at positions pos0.. (in place): RMSNorm -> [q|k|v] GEMM -> RoPE +
+        cache rows -> causal GQA attention over the cache -> o-proj GEMM + residual."""
+        m, H, KV, dh = X.shape[0], self.H, self.KV, self.dh
+        hn = bufs["hn"][:m]
+        K.rmsnorm(X, self.norm, self.eps, y=hn)
+        qkv = bufs["qkv"][:m, :self.qkv.N]
+        K.gemm(self.qkv.fmt, self.qkv.w, self.qkv.scale, hn, y=qkv, bias=self.qkv.bias)
+        q = bufs["q"][:m, :H * dh]
+        K.qkv_split_rope(qkv, H * dh, KV * dh, dh, eng.cos, eng.sin, pos0, q, self.kc[0], self.vc[0], rope=self.rope)
+        a = bufs["a"][:m, :H * dh]
+        K.prefill_attn(q, self.kc[0], self.vc[0], a, pos0, H, KV)
+        K.gemm(self.wo.fmt, self.wo.w, self.wo.scale, a, y=X, residual=X, bias=self.wo.bias, epi="resid")
+
     @property
     def nbytes(self):
         return self.qkv.nbytes + self.wo.nbytes + self.norm.numel() * 2
@@ -285,6 +304,19 @@ class SwiGLUDecode:
         act = eng.act[:, :self.F]
         K.linear_swiglu(self.gu.fmt, self.gu.w, self.gu.scale, eng.h, self.norm, self.eps, act=act)
         K.linear(self.down.fmt, self.down.w, self.down.scale, act, y=eng.h, residual=eng.h)
+
+    def prefill_supported(self) -> bool:
+        lin = (self.gu, self.down)
+        return all(l.fmt in ("int8", "fp16") and l.K % 64 == 0 and l.N % 16 == 0 for l in lin)
+
+    def prefill(self, eng, X, pos0: int, bufs: dict):
+        """Prompt rows X [m, D] in place: RMSNorm -> gate/up GEMM + SwiGLU -> down GEMM + residual."""
+        m = X.shape[0]
+        hn = bufs["hn"][:m]
+        K.rmsnorm(X, self.norm, self.eps, y=hn)
+        act = bufs["act"][:m, :self.F]
+        K.gemm(self.gu.fmt, self.gu.w, self.gu.scale, hn, y=act, epi="swiglu")
+        K.gemm(self.down.fmt, self.down.w, self.down.scale, act, y=X, residual=X, epi="resid")
 
     @property
     def nbytes(self):
@@ -386,6 +418,50 @@ class DecodeEngine:
             self.step.zero_()
             self.pos.fill_(pos0)
             K.embed(self.embed, torch.tensor(prompt[:1], dtype=torch.int32, device="cuda"), out=self.h)
+
+    # -- batched prefill --
+    def prefill_supported(self) -> bool:
+        return all(getattr(m, "prefill_supported", lambda: False)() and getattr(p, "prefill_supported", lambda: False)()
+                   for m, p in self.layers)
+
+    def _prefill_buffers(self, C: int) -> dict:
+        if getattr(self, "_pf", None) is None or self._pf["x"].shape[0] < C:
+            cfg, dev = self.cfg, "cuda"
+            nqkv = max([m.qkv.N for m, _ in self.layers] + [16])
+            fmax = max([getattr(p, "F", 0) for _, p in self.layers] + [8])
+            hq = cfg.n_heads * cfg.dh
+            z = lambda c: torch.empty((C, c), dtype=torch.float16, device=dev)
+            self._pf = {"x": z(cfg.dim), "hn": z(cfg.dim), "qkv": z(nqkv), "q": z(hq), "a": z(hq), "act": z(fmax)}
+        return self._pf
+
+    def prefill(self, prompt, chunk: int = 2048):
+        """reset(prompt), then fill the cache for prompt[:-1] in one pass per layer (MFMA GEMMs and
+        causal flash attention, `chunk` prompt rows at a time), leaving the engine where the
+        len(prompt) - 1 forced steps of run() would: pos = step = n - 1, history = prompt[1:],
+        h = embed[prompt[-1]].  Falls back to the forced steps when a layer has no batched path."""
+        prompt = [int(t) for t in prompt]
+        self.reset(prompt)
+        n = len(prompt) - 1
+        if n <= 0:
+            return
+        if not self.prefill_supported():
+            self.run(n, 0)
+            return
+        C = max(1, min(int(chunk), n))
+        bufs = self._prefill_buffers(C)
+        with torch.cuda.stream(self.stream):
+            ids = torch.tensor(prompt, dtype=torch.int32, device="cuda")
+            for c0 in range(0, n, C):
+                m = min(C, n - c0)
+                X = bufs["x"][:m]
+                K.embed(self.embed, ids[c0:c0 + m], out=X)
+                for mixer, mlp in self.layers:
+                    mixer.prefill(self, X, c0, bufs)
+                    mlp.prefill(self, X, c0, bufs)
+            self.hist[:n].copy_(ids[1:n + 1])
+            self.pos.fill_(n)
+            self.step.fill_(n)
+            K.embed(self.embed, ids[n:n + 1], out=self.h)
 
     def run(self, n_prefill: int, n_decode: int, graph: bool = True):
         """Enqueue n_prefill forced steps then n_decode greedy steps (no host sync)."""

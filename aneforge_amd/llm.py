@@ -280,8 +280,7 @@ class LlamaPrefill:
         """Run the prompt through the resident cache; returns the engine positioned after it."""
         ids = [int(t) for t in token_ids]
         d = self._decoder(M or max(len(ids), 1))
-        d.reset(ids)
-        d.run(len(ids) - 1, 0)
+        d.prefill(ids)
         return d
 
     def prefill(self, token_ids):
@@ -309,14 +308,19 @@ class LlamaPrefill:
         use_dev = self.ane_lm_head if ane_lm_head is None else bool(ane_lm_head)
         d = self._decoder(M)
         t0 = time.perf_counter()
-        d.reset(prompt)
+        if batched_prefill:
+            d.prefill(prompt)                  # batched MFMA prefill (forced steps where unsupported)
+            n_run = 0
+        else:
+            d.reset(prompt)
+            n_run = len(prompt) - 1
         n_pre = len(prompt) - 1
         n_gen = max(0, min(max_new_tokens, M - len(prompt)))
         greedy = temperature <= 0.0
         if greedy and use_dev and not eos and on_token is None and on_stage is None:
-            d.run(n_pre, n_gen)
+            d.run(n_run, n_gen)
             return d.history(n_pre, n_gen)
-        d.run(n_pre, 0)
+        d.run(n_run, 0)
         if on_stage is not None:
             d.sync()
             on_stage("prefill", time.perf_counter() - t0)

@@ -11,6 +11,7 @@ Kernel workloads (--workload gemv_w8 | gemv_q4 | attn | moe) time one configurat
 rotating weight copies inside a captured graph (working set > 2x the 256 MB MALL).
 --workload copy streams a plain 1 GiB copy: the calibration run for the FETCH_SIZE /
 WRITE_SIZE counters behind roofline.traffic, and a measured copy ceiling.
+--workload prefill times the batched MFMA prefill of a --ctx-token prompt on the cfg3 model.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode]
 """
@@ -33,7 +34,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv_w8", "gemv_q4", "attn", "moe", "kernels", "copy"])
+                    choices=["decode", "gemv_w8", "gemv_q4", "attn", "moe", "kernels", "copy", "prefill"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--out", default=None, help="also append the JSON line to this file")
     ap.add_argument("--rows-hint", type=int, default=0)
@@ -379,6 +380,41 @@ def cpu_baseline_decode(seconds: float = 12.0):
                       f"{n} reps ({n1} at 1 BLAS thread), extrapolated to 32 layers"}
 
 
+def bench_prefill(args):
+    """Batched prefill of a --ctx-token prompt (default 2048) through the 32-layer cfg3 model
+    (int8 weights): MFMA GEMMs + causal flash attention, filling the resident cache.  Timed with
+    HIP events on the engine stream over `steps` prefills after `warmup`; FLOPs = 2 x linear
+    weights x prompt rows + causal attention (2 x 2 x Hq x dh x sum of context lengths)."""
+    import ctypes
+    import torch
+    from aneforge_amd import _hip
+    P = int(args.ctx)
+    log(f"building cfg3 engine (32 layers int8) for a {P}-token batched prefill")
+    cfg, eng, layers = build_cfg3_engine(P, 0)
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, CFG3["vocab"], P + 1)]
+    for _ in range(max(1, args.warmup)):
+        eng.prefill(prompt)
+    eng.sync()
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    _hip.call("afx_event_create", ctypes.byref(e0))
+    _hip.call("afx_event_create", ctypes.byref(e1))
+    reps = max(1, min(args.steps, 8))
+    _hip.call("afx_event_record", e0, eng.stream.cuda_stream)
+    for _ in range(reps):
+        eng.prefill(prompt)
+    _hip.call("afx_event_record", e1, eng.stream.cuda_stream)
+    ms = ctypes.c_float()
+    _hip.call("afx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+    torch.cuda.synchronize()
+    per = ms.value / reps
+    D, F, H, KV, dh = CFG3["dim"], CFG3["ffn_dim"], CFG3["n_heads"], CFG3["n_kv_heads"], 128
+    lin = D * (H * dh + 2 * KV * dh) + H * dh * D + 2 * F * D + F * D
+    flops = 2.0 * CFG3["n_layers"] * P * (lin + 2 * H * dh * (P + 1) / 2.0)
+    return {"workload": f"cfg3 batched prefill, {P}-token prompt, 32 layers int8 (MFMA GEMM + causal flash attention)",
+            "prompt_tokens": P, "ms": per, "tokens_per_s": P / (per * 1e-3), "TFLOPs": flops / (per * 1e-3) / 1e12,
+            "mfma_peak_TFLOPs_fp16": 2500.0}
+
+
 def bench_decode(args):
     import ctypes
     import torch
@@ -468,6 +504,9 @@ def main():
         return
     if args.workload == "copy":
         print(json.dumps(bench_copy(args)))
+        return
+    if args.workload == "prefill":
+        print(json.dumps(bench_prefill(args)))
         return
     if args.workload == "decode":
         res = bench_decode(args)

@@ -90,6 +90,33 @@ def test_linear_int8_bias_residual_inplace(K):
     check_f16(host(rd), want, what="bias+residual")
 
 
+@pytest.mark.parametrize("M,N,Kd", [(4, 100, 512), (6, 4096, 4096), (8, 1004, 11008), (5, 22016, 4096)])
+def test_linear_int8_mfma_rows_and_tails(K, M, N, Kd):
+    # 4..8 activation rows take the MFMA path; N % 16 != 0 exercises the partial last tile
+    say(f"linear int8 MFMA M={M} N={N} K={Kd}")
+    q, s = _w8(N, Kd, 40 + M)
+    x = np.random.default_rng(41 + M).standard_normal((M, Kd)).astype(np.float16)
+    got = host(K.linear("int8", dev(q), dev(s), dev(x)))
+    check_f16(got, ref.linear(x, ref.dequant_w8(q, s)), what="int8 linear (MFMA)")
+
+
+def test_linear_mfma_bias_residual_and_fp16(K):
+    say("MFMA path: bias + residual in place (int8), fp16 weights")
+    rng = np.random.default_rng(42)
+    q, s = _w8(260, 1024, 43)
+    x = rng.standard_normal((5, 1024)).astype(np.float16)
+    b = rng.standard_normal(260).astype(np.float16)
+    r = rng.standard_normal((5, 260)).astype(np.float16)
+    rd = dev(r)
+    K.linear("int8", dev(q), dev(s), dev(x), y=rd, bias=dev(b), residual=rd)
+    want = ref.r16(r.astype(np.float64) + ref.linear(x, ref.dequant_w8(q, s), b))
+    check_hidden(host(rd), want, what="MFMA bias+residual")
+    w = (rng.standard_normal((512, 2048)) * 0.02).astype(np.float16)
+    x2 = rng.standard_normal((7, 2048)).astype(np.float16)
+    got = host(K.linear("fp16", dev(w), None, dev(x2)))
+    check_f16(got, ref.linear(x2, w.astype(np.float32)), what="fp16 MFMA")
+
+
 @pytest.mark.parametrize("M,N,Kd", [(1, 11008, 4096), (1, 4096, 11008), (4, 11008, 4096), (4, 4096, 11008),
                                     (8, 11008, 4096), (8, 4096, 11008), (3, 100, 384)])
 def test_linear_q4_0_cfg1(K, M, N, Kd):
@@ -374,3 +401,67 @@ def test_moe_layer_sparse_dispatch(K, fmt):
     want, wgate, chosen = ref.moe_layer(h, g, router, Gf, Uf, Df, k, True, 1e-5)
     assert [sorted(r) for r in host(sel).tolist()] == chosen
     check_hidden(out, want, what="moe")           # residual-stream output: fp16-ulp atol
+
+
+def test_moe_topk_largest_expert_count_with_ties(K):
+    # E = 2049 (the reference's upper bound) and k = 64: probabilities on power-of-two levels with
+    # many exact ties, so the lowest-index rule decides most picks
+    say("moe top-k E=2049 k=64 with ties")
+    rng = np.random.default_rng(70)
+    T, E, k = 3, 2049, 64
+    levels = rng.integers(1, 12, (T, E))
+    lg = np.log(2.0 ** -levels.astype(np.float64)).astype(np.float32)
+    gate, sel, cnt, lst = K.moe_topk(dev(lg), k, renorm=False)
+    p = np.exp(lg.astype(np.float64) - lg.max(1, keepdims=True).astype(np.float64))
+    p16 = (p / p.sum(1, keepdims=True)).astype(np.float16)
+    want = ref.topk_gate(p16, k)
+    got_sel = host(sel)
+    for t in range(T):
+        assert sorted(got_sel[t].tolist()) == np.flatnonzero(want[t]).tolist(), f"token {t}"
+    np.testing.assert_allclose(host(gate), np.take_along_axis(want, got_sel.astype(np.int64), 1), rtol=1e-3)
+    c = host(cnt)
+    assert c.sum() == T * k and c.max() <= T
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4_0"])
+def test_moe_expert_with_more_than_16_tokens(K, fmt):
+    # 40 tokens, 2 experts, top-1: an expert receives > 16 tokens, so the MFMA kernel runs
+    # several token groups over the same weights
+    say(f"moe E=2 k=1 T=40 D=F=1024 fmt={fmt}")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(71)
+    E, k, T, D, F = 2, 1, 40, 1024, 1024
+    router = rng.normal(0, 0.2, (E, D)).astype(np.float16)
+    h = rng.standard_normal((T, D)).astype(np.float16)
+    g = np.ones(D, np.float16)
+    Wg = rng.normal(0, 0.05, (E, F, D)).astype(np.float32)
+    Wu = rng.normal(0, 0.05, (E, F, D)).astype(np.float32)
+    Wd = rng.normal(0, 0.05, (E, D, F)).astype(np.float32)
+    gu, dn, Gf, Uf, Df = [], [], [], [], []
+    for e in range(E):
+        if fmt == "q4_0":
+            bg, bu, bd = _blob.quantize_q4_0(Wg[e]), _blob.quantize_q4_0(Wu[e]), _blob.quantize_q4_0(Wd[e])
+            Gf.append(ref.dequant_q4_0_f16(bg, F, D)); Uf.append(ref.dequant_q4_0_f16(bu, F, D))
+            Df.append(ref.dequant_q4_0_f16(bd, D, F))
+            qg, dg = _blob.q4_0_to_superblock(bg, F, D)
+            qu, du = _blob.q4_0_to_superblock(bu, F, D)
+            gu.append((_blob.interleave_rows(qg, qu), _blob.interleave_rows(dg, du)))
+            dn.append(_blob.q4_0_to_superblock(bd, D, F))
+        else:
+            qg, sg = _blob.quantize_per_row(Wg[e]); qu, su = _blob.quantize_per_row(Wu[e]); qd, sd = _blob.quantize_per_row(Wd[e])
+            Gf.append(ref.dequant_w8(qg, sg)); Uf.append(ref.dequant_w8(qu, su)); Df.append(ref.dequant_w8(qd, sd))
+            gu.append((_blob.interleave_rows(qg, qu), _blob.interleave_rows(sg, su)))
+            dn.append((qd, sd))
+    wgu = np.stack([a for a, _ in gu]); sgu = np.stack([b for _, b in gu])
+    wdn = np.stack([a for a, _ in dn]); sdn = np.stack([b for _, b in dn])
+    hd = dev(h)
+    hn = K.rmsnorm(hd, dev(g), 1e-5)
+    logits = torch.cat([K.linear("fp16", dev(router), None, hn[i:i + 8], out_f32=True) for i in range(0, T, 8)])
+    gate, sel, cnt, lst = K.moe_topk(logits, k, renorm=True)
+    assert host(cnt).max() > 16
+    act = K.moe_gateup(fmt, dev(wgu), dev(sgu), hn, k, E, F, cnt, lst)
+    y = K.moe_down(fmt, dev(wdn), dev(sdn), act, T, k, E, F, D, cnt, lst)
+    out = host(K.moe_combine(hd, y, gate))
+    want, _, chosen = ref.moe_layer(h, g, router, Gf, Uf, Df, k, True, 1e-5)
+    assert [sorted(r) for r in host(sel).tolist()] == chosen
+    check_hidden(out, want, what="moe >16 tokens")

@@ -422,6 +422,14 @@ static int attn_cus() {
 static int choose_nstep(int D, int B, int Hkv, int L, int want) {
   const int pps = 512 / D;
   auto splits = [&](int ns) { const int c = ns * kAttnWaves * pps; return (L + c - 1) / c; };
+  if (want == 0) {                              // tuning override: AFX_ATTN_NSTEP=1|2|4|8|16
+    static int env = -1;
+    if (env < 0) {
+      const char* e = getenv("AFX_ATTN_NSTEP");
+      env = e ? atoi(e) : 0;
+    }
+    want = env;
+  }
   if (want == 1 || want == 2 || want == 4 || want == 8 || want == 16) return splits(want) <= kMaxSplits ? want : 0;
   const int target = attn_cus();
   for (int ns = 16; ns >= 1; ns >>= 1) {

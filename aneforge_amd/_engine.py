@@ -251,7 +251,7 @@ class AttentionDecode:
 
     def prefill_supported(self) -> bool:
         lin = (self.qkv, self.wo)
-        return (not self.qk_norm and self.dh == 128 and all(l.fmt in ("int8", "fp16") for l in lin)
+        return (self.dh == 128 and all(l.fmt in ("int8", "fp16") for l in lin)
                 and all(l.K % 64 == 0 and l.N % 16 == 0 for l in lin))
 
     def prefill(self, eng, X, pos0: int, bufs: dict):
@@ -263,7 +263,14 @@ class AttentionDecode:
         qkv = bufs["qkv"][:m, :self.qkv.N]
         K.gemm(self.qkv.fmt, self.qkv.w, self.qkv.scale, hn, y=qkv, bias=self.qkv.bias)
         q = bufs["q"][:m, :H * dh]
-        K.qkv_split_rope(qkv, H * dh, KV * dh, dh, eng.cos, eng.sin, pos0, q, self.kc[0], self.vc[0], rope=self.rope)
+        K.qkv_split_rope(qkv, H * dh, KV * dh, dh, eng.cos, eng.sin, pos0, q, self.kc[0], self.vc[0],
+                         rope=self.rope and not self.qk_norm)
+        if self.qk_norm:       # QK-norm sits between the projection and RoPE (Qwen3)
+            pos = torch.arange(pos0, pos0 + m, dtype=torch.int32, device="cuda")
+            K.head_norm_rope(q, H, dh, self.q_norm, self.eps, eng.cos, eng.sin, pos, seq_stride=q.stride(0),
+                             head_stride=dh, pos_mul=0, kv_len=eng.M, M=m, rope=self.rope)
+            K.head_norm_rope(self.kc[0], KV, dh, self.k_norm, self.eps, eng.cos, eng.sin, pos, seq_stride=0,
+                             head_stride=self.kc.stride(1), pos_mul=dh, kv_len=eng.M, M=m, rope=self.rope)
         a = bufs["a"][:m, :H * dh]
         K.prefill_attn(q, self.kc[0], self.vc[0], a, pos0, H, KV)
         K.gemm(self.wo.fmt, self.wo.w, self.wo.scale, a, y=X, residual=X, bias=self.wo.bias, epi="resid")

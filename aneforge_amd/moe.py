@@ -111,10 +111,14 @@ class MoEDecode:
         self._bufs = None
 
     def bind(self, eng):
+        self._bufs = self._make_bufs(eng.B)
+        self._pf = None
+
+    def _make_bufs(self, B):
         import torch
-        B, D, E, k, F = eng.B, self.D, self.E, self.k, self.F
+        D, E, k, F = self.D, self.E, self.k, self.F
         dev = "cuda"
-        self._bufs = {
+        bufs = {
             "hn": torch.empty((B, D), dtype=torch.float16, device=dev),
             "logits": torch.empty((B, E), dtype=torch.float32, device=dev),
             "gate": torch.empty((B, k), dtype=torch.float32, device=dev),
@@ -126,11 +130,12 @@ class MoEDecode:
         }
         if self.shared:
             Fs = self.sh_gu.N // 2
-            self._bufs.update({"sh_act": torch.empty((B, Fs), dtype=torch.float16, device=dev),
-                               "sh_y": torch.empty((B, D), dtype=torch.float16, device=dev),
-                               "sh_g": torch.empty((B, 1), dtype=torch.float16, device=dev),
-                               "sh_gs": torch.empty((B, 1), dtype=torch.float16, device=dev),
-                               "sh": torch.empty((B, D), dtype=torch.float16, device=dev)})
+            bufs.update({"sh_act": torch.empty((B, Fs), dtype=torch.float16, device=dev),
+                         "sh_y": torch.empty((B, D), dtype=torch.float16, device=dev),
+                         "sh_g": torch.empty((B, 1), dtype=torch.float16, device=dev),
+                         "sh_gs": torch.empty((B, 1), dtype=torch.float16, device=dev),
+                         "sh": torch.empty((B, D), dtype=torch.float16, device=dev)})
+        return bufs
 
     def reset(self, eng):
         pass
@@ -152,9 +157,11 @@ class MoEDecode:
                    self.F, self.D, b["cnt"], b["list"], y=b["y"][:T * self.k])
         shared = None
         if self.shared:
-            K.linear_swiglu(self.sh_gu.fmt, self.sh_gu.w, self.sh_gu.scale, b["hn"][:T], act=b["sh_act"][:T])
-            K.linear(self.sh_down.fmt, self.sh_down.w, self.sh_down.scale, b["sh_act"][:T], y=b["sh_y"][:T])
-            K.linear("fp16", self.sh_gate.w, None, b["hn"][:T], y=b["sh_g"][:T])
+            for r0 in range(0, T, 8):          # the shared expert's GEMVs take up to 8 rows a call
+                r1 = min(T, r0 + 8)
+                K.linear_swiglu(self.sh_gu.fmt, self.sh_gu.w, self.sh_gu.scale, b["hn"][r0:r1], act=b["sh_act"][r0:r1])
+                K.linear(self.sh_down.fmt, self.sh_down.w, self.sh_down.scale, b["sh_act"][r0:r1], y=b["sh_y"][r0:r1])
+                K.linear("fp16", self.sh_gate.w, None, b["hn"][r0:r1], y=b["sh_g"][r0:r1])
             K._hip.call("afx_ew_unary", K.UNARY["sigmoid"], K.P(b["sh_g"]), K.P(b["sh_gs"]), T, 0.0, 0.0, K.stream())
             shape = [T, self.D]
             K._hip.call("afx_ew_binary", K.EW["mul"], K.P(b["sh_y"]), K._ll([self.D, 1]), K.P(b["sh_gs"]),
@@ -164,6 +171,16 @@ class MoEDecode:
 
     def enqueue(self, eng):
         self.run(eng.h, self._bufs)
+
+    # batched prefill: the same layer over a chunk of prompt rows (grouped expert GEMMs on MFMA)
+    def prefill_supported(self) -> bool:
+        return True
+
+    def prefill(self, eng, X, pos0: int, bufs: dict):
+        T = X.shape[0]
+        if self._pf is None or self._pf["hn"].shape[0] < T:
+            self._pf = self._make_bufs(T)
+        self.run(X, self._pf)
 
     @property
     def nbytes(self):

@@ -158,10 +158,10 @@ def test_compile_multi_share_buffer_keeps_state_resident():
         mm.prog.share_buffer(0, om[y], 0, inm[id(s)])      # only before the first execute
 
 
-def _moe_model(E=8, k=2, D=128, F=128, layers=2, vocab=64, qk=False, seed=0):
+def _moe_model(E=8, k=2, D=128, F=128, layers=2, vocab=64, qk=False, seed=0, dh=32):
     rng = np.random.default_rng(seed)
     R = lambda *s: (rng.standard_normal(s) / np.sqrt(s[-1])).astype(np.float32)
-    H, KV, dh = 4, 2, 32
+    H, KV = 4, 2
     cfg = af.LlamaConfig(dim=D, n_layers=layers, n_heads=H, n_kv_heads=KV, ffn_dim=F, vocab=vocab,
                          layers=[af.LayerSpec(mlp="moe", qk_norm=qk) for _ in range(layers)],
                          extra={"n_experts": E, "n_experts_per_tok": k, "norm_topk_prob": True})
@@ -211,6 +211,38 @@ def test_moe_decoder_generate_matches_oracle(compress, qk):
     want, lgs = ref.generate(prompt, 8, ow, ocfg, M=len(prompt) + 8)
     from test_gpu_llm import _assert_tokens_match
     _assert_tokens_match(got, want, lgs, f"moe {compress}")
+    m.release()
+
+
+@pytest.mark.parametrize("compress,qk", [(None, True), ("int8", False), ("int8", True)])
+def test_batched_prefill_moe_and_qk_norm(compress, qk):
+    """Batched prefill through MoE MLPs (grouped MFMA experts over the prompt rows) and QK-norm
+    attention (per-head norm + RoPE on q and the cache rows): same state as the forced steps,
+    generation as the oracle."""
+    say(f"batched prefill MoE compress={compress} qk_norm={qk}")
+    cfg, w = _moe_model(D=512, F=256, qk=qk, dh=128, seed=3)
+    enc = {None: lambda W: np.asarray(W, np.float32).astype(np.float16).astype(np.float32),
+           "int8": lambda W: ref.dequant_w8(*ref.quantize_per_row(W))}[compress]
+    m = af.LlamaPrefill(cfg, w, compress=compress)
+    prompt = [int(t) for t in np.random.default_rng(8).integers(0, cfg.vocab, 90)]
+    M = len(prompt) + 8
+    d = m._decoder(M)
+    assert d.prefill_supported()
+    d.prefill(prompt)
+    d.sync()
+    kb = [mx.kc.float().cpu().numpy() for mx, _ in d.layers]
+    d.reset(prompt)
+    d.run(len(prompt) - 1, 0)
+    d.sync()
+    n = len(prompt) - 1
+    for li, (mx, _) in enumerate(d.layers):
+        want_k = mx.kc.float().cpu().numpy()[..., :n, :]
+        assert cosine(kb[li][..., :n, :], want_k) >= 0.9999, f"layer {li} k cache"
+    got = m.generate(prompt, max_new_tokens=6)
+    ow, ocfg = _oracle_weights(cfg, w, enc)
+    want, lgs = ref.generate(prompt, 6, ow, ocfg, M=M)
+    from test_gpu_llm import _assert_tokens_match
+    _assert_tokens_match(got, want, lgs, f"batched prefill moe {compress} qk={qk}")
     m.release()
 
 

@@ -146,7 +146,7 @@ def decode_attn(q, k, v, o=None, ctx_len=None, pos=None, scale=None, mask=None, 
     kbs, khs = kv_strides if kv_strides else (k.stride(0), k.stride(1))
     need = attn_ws_bytes(B, Hq, Hkv, D, Mmax, nstep_hint)
     if ws is None or ws.numel() * ws.element_size() < need:
-        ws = torch.zeros(need // 4 + 1, dtype=torch.float32, device=q.device)   # counters start at 0
+        ws = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
     scale = (1.0 / D ** 0.5) if scale is None else float(scale)
     _hip.call("afx_decode_attn", P(q), P(k), P(v), P(o), qbs, qhs, kbs, khs, B, Hq, Hkv, D,
               int(ctx_len if ctx_len is not None else Mmax), P(pos), Mmax, P(mask),

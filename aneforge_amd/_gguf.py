@@ -7,7 +7,15 @@ dequantising them, so the Q4_0 kernels stream the file's own 4-bit codes.
 
 Format: magic "GGUF", version 3, tensor count, metadata count, metadata key/values, tensor infos
 (name, dims with dims[0] innermost, ggml type, offset), data section aligned to
-general.alignment (default 32).  Dequantisers: F32, F16, BF16, Q4_0, Q8_0."""
+general.alignment (default 32).
+
+Dequantisers (the ggml block formats that llama.cpp quantisations write; the reference gets the
+same float32 values from gguf.quants.dequantize and then casts to the requested dtype):
+  F32, F16, BF16; Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1 (32-weight blocks);
+  Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K (256-weight super-blocks).
+Each is evaluated in float32 in the order gguf-py uses (block scale x sub-block scale first, then
+x code, then minus the block minimum), so the fp16 cast matches the reference's value exactly.
+The importance-matrix "IQ" and ternary formats are not decoded (NotImplementedError names them)."""
 from __future__ import annotations
 
 import mmap as _mmap
@@ -18,10 +26,17 @@ from typing import Any
 import numpy as np
 
 GGUF_MAGIC = b"GGUF"
-# ggml tensor types used here: (elements per block, bytes per block)
-GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q8_0": 8, "BF16": 30}
-_BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 30: (1, 2)}
+QK_K = 256
+# ggml tensor types read here: type id, and (elements per block, bytes per block)
+GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q8_1": 9,
+        "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_K": 15, "BF16": 30}
+_BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 9: (32, 36),
+          10: (QK_K, 84), 11: (QK_K, 110), 12: (QK_K, 144), 13: (QK_K, 176), 14: (QK_K, 210),
+          15: (QK_K, 292), 30: (1, 2)}
 _NAMES = {v: k for k, v in GGML.items()}
+# other ggml type ids, named in errors
+_UNSUPPORTED = {16: "IQ2_XXS", 17: "IQ2_XS", 18: "IQ3_XXS", 19: "IQ1_S", 20: "IQ4_NL", 21: "IQ3_S", 22: "IQ2_S",
+                23: "IQ4_XS", 29: "IQ1_M", 34: "TQ1_0", 35: "TQ2_0", 39: "MXFP4"}
 
 # metadata value types
 _U8, _I8, _U16, _I16, _U32, _I32, _F32, _BOOL, _STR, _ARR, _U64, _I64, _F64 = range(13)
@@ -85,7 +100,7 @@ def _nbytes(ttype, shape):
     n = int(np.prod(shape))
     per, size = _BLOCK.get(ttype, (None, None))
     if per is None:
-        raise NotImplementedError(f"GGUF tensor type {ttype} is not supported by this reader")
+        raise NotImplementedError(f"GGUF tensor type {_UNSUPPORTED.get(ttype, ttype)} is not supported by this reader")
     return n // per * size
 
 
@@ -142,6 +157,161 @@ class GGUFReader:
         return self._mm
 
 
+# ----------------------------------------------------------------------------- block decoders
+# Each takes the blocks as uint8 [n, bytes per block] and returns float32 [n, elements per block].
+def _f16(b) -> np.ndarray:
+    """Little-endian fp16 fields [n, 2] -> float32 [n, 1]."""
+    return np.ascontiguousarray(b).view(np.float16).astype(np.float32)
+
+
+def _halves(qs) -> np.ndarray:
+    """16 bytes of nibbles -> 32 codes: element j < 16 is the low nibble of byte j, element 16 + j
+    the high nibble (the 32-weight ggml blocks)."""
+    return np.concatenate([qs & 15, qs >> 4], axis=1)
+
+
+def _lsb_bits(b) -> np.ndarray:
+    """Bytes [n, m] -> bits [n, 8m]: bit i of the little-endian bit string."""
+    return np.unpackbits(np.ascontiguousarray(b), axis=1, bitorder="little")
+
+
+def _crumbs(qs, groups) -> np.ndarray:
+    """2-bit fields of 32-byte rows: element 128h + 32s + l = (qs[32h + l] >> 2s) & 3 for each
+    32-byte row h and shift s (the Q2_K / Q3_K low bits, the Q6_K high bits)."""
+    n = qs.shape[0]
+    sh = np.arange(0, 8, 2, dtype=np.uint8)
+    return ((qs.reshape(n, groups, 1, 32) >> sh[None, None, :, None]) & 3).reshape(n, groups * 128)
+
+
+def _k4_scale_min(sc):
+    """The 12-byte Q4_K / Q5_K scale field -> 6-bit scale and min of each of the 8 sub-blocks:
+    j < 4: scale = b[j] & 63, min = b[j + 4] & 63; j >= 4: the low 4 bits come from b[j + 4]
+    (scale: low nibble, min: high nibble) and the top 2 bits from bits 6-7 of b[j - 4] (scale)
+    and b[j] (min)."""
+    lo, mid, hi = sc[:, 0:4], sc[:, 4:8], sc[:, 8:12]
+    scale = np.concatenate([lo & 63, (hi & 15) | ((lo >> 6) << 4)], axis=1)
+    mins = np.concatenate([mid & 63, (hi >> 4) | ((mid >> 6) << 4)], axis=1)
+    return scale.astype(np.float32), mins.astype(np.float32)
+
+
+def _q4_0(b):
+    return _f16(b[:, 0:2]) * (_halves(b[:, 2:18]).astype(np.float32) - 8.0)
+
+
+def _q4_1(b):
+    return _f16(b[:, 0:2]) * _halves(b[:, 4:20]).astype(np.float32) + _f16(b[:, 2:4])
+
+
+def _q5(b, off):
+    """5-bit codes of Q5_0 / Q5_1: the nibble of _halves, bit 4 = bit j of the 32-bit field qh."""
+    return (_halves(b[:, off + 4:off + 20]) | (_lsb_bits(b[:, off:off + 4]) << 4)).astype(np.float32)
+
+
+def _q5_0(b):
+    return _f16(b[:, 0:2]) * (_q5(b, 2) - 16.0)
+
+
+def _q5_1(b):
+    return _f16(b[:, 0:2]) * _q5(b, 4) + _f16(b[:, 2:4])
+
+
+def _q8_0(b):
+    return _f16(b[:, 0:2]) * b[:, 2:34].copy().view(np.int8).astype(np.float32)
+
+
+def _q8_1(b):
+    return _f16(b[:, 0:2]) * b[:, 4:36].copy().view(np.int8).astype(np.float32)
+
+
+def _q2_k(b):
+    """84 B: scales[16] (low nibble: scale, high: min of each 16-weight sub-block), 2-bit codes
+    qs[64], fp16 d, fp16 dmin.  w = d*scale * q - dmin*min."""
+    n = b.shape[0]
+    sc = b[:, 0:16]
+    dl = _f16(b[:, 80:82]) * (sc & 15).astype(np.float32)
+    ml = _f16(b[:, 82:84]) * (sc >> 4).astype(np.float32)
+    q = _crumbs(b[:, 16:80], 2).astype(np.float32).reshape(n, 16, 16)
+    return (dl[:, :, None] * q - ml[:, :, None]).reshape(n, QK_K)
+
+
+def _q3_k(b):
+    """110 B: hmask[32], 2-bit codes qs[64], 12-byte packed signed 6-bit scales, fp16 d.
+    Element e = 32i + l has high bit (hmask[l] >> i) & 1; q = low2 - (4 if that bit is clear)."""
+    n = b.shape[0]
+    hbit = _lsb_bits(b[:, 0:32]).reshape(n, 32, 8).transpose(0, 2, 1).reshape(n, QK_K)
+    low = _crumbs(b[:, 32:96], 2).astype(np.int8)
+    q = (low - ((hbit ^ 1).astype(np.int8) << 2)).astype(np.float32).reshape(n, 16, 16)
+    s = b[:, 96:108]
+    i = np.arange(16)
+    lo4 = (s[:, i % 8] >> (4 * (i // 8)).astype(np.uint8)) & 15
+    hi2 = (s[:, 8 + i % 4] >> (2 * (i // 4)).astype(np.uint8)) & 3
+    scale = ((lo4 | (hi2 << 4)).astype(np.int8) - 32).astype(np.float32)
+    dl = _f16(b[:, 108:110]) * scale
+    return (dl[:, :, None] * q).reshape(n, QK_K)
+
+
+def _k4_codes(qs):
+    """128 bytes of Q4_K / Q5_K nibbles -> 256 codes: element 64c + 32h + l = (qs[32c + l] >> 4h) & 15."""
+    n = qs.shape[0]
+    sh = np.array([0, 4], dtype=np.uint8)
+    return ((qs.reshape(n, 4, 1, 32) >> sh[None, None, :, None]) & 15).reshape(n, QK_K)
+
+
+def _q4_k(b):
+    """144 B: fp16 d, fp16 dmin, 12-byte scales/mins, codes[128].  w = d*scale_j * q - dmin*min_j
+    over 8 sub-blocks of 32."""
+    n = b.shape[0]
+    scale, mins = _k4_scale_min(b[:, 4:16])
+    dl = _f16(b[:, 0:2]) * scale
+    ml = _f16(b[:, 2:4]) * mins
+    q = _k4_codes(b[:, 16:144]).astype(np.float32).reshape(n, 8, 32)
+    return (dl[:, :, None] * q - ml[:, :, None]).reshape(n, QK_K)
+
+
+def _q5_k(b):
+    """176 B: fp16 d, fp16 dmin, 12-byte scales/mins, qh[32], codes[128]; bit 4 of element
+    32j + l is bit j of qh[l]."""
+    n = b.shape[0]
+    scale, mins = _k4_scale_min(b[:, 4:16])
+    dl = _f16(b[:, 0:2]) * scale
+    ml = _f16(b[:, 2:4]) * mins
+    hbit = _lsb_bits(b[:, 16:48]).reshape(n, 32, 8).transpose(0, 2, 1).reshape(n, QK_K)
+    q = (_k4_codes(b[:, 48:176]) | (hbit << 4)).astype(np.float32).reshape(n, 8, 32)
+    return (dl[:, :, None] * q - ml[:, :, None]).reshape(n, QK_K)
+
+
+def _q6_k(b):
+    """210 B: ql[128] (low 4 bits: element 128h + 64s + l from byte 64h + l, nibble s), qh[64]
+    (high 2 bits, the _crumbs layout), int8 scales[16] per 16 weights, fp16 d.  q = code - 32."""
+    n = b.shape[0]
+    ql = b[:, 0:128]
+    sh = np.array([0, 4], dtype=np.uint8)
+    low = ((ql.reshape(n, 2, 1, 64) >> sh[None, None, :, None]) & 15).reshape(n, QK_K)
+    high = _crumbs(b[:, 128:192], 2)
+    q = ((low | (high << 4)).astype(np.int16) - 32).astype(np.float32).reshape(n, 16, 16)
+    dl = _f16(b[:, 208:210]) * b[:, 192:208].copy().view(np.int8).astype(np.float32)
+    return (dl[:, :, None] * q).reshape(n, QK_K)
+
+
+def _q8_k(b):
+    """292 B: fp32 d, int8 codes[256], int16 block sums[16] (not needed to decode)."""
+    d = np.ascontiguousarray(b[:, 0:4]).view(np.float32)
+    return d * b[:, 4:260].copy().view(np.int8).astype(np.float32)
+
+
+_DECODE = {2: _q4_0, 3: _q4_1, 6: _q5_0, 7: _q5_1, 8: _q8_0, 9: _q8_1,
+           10: _q2_k, 11: _q3_k, 12: _q4_k, 13: _q5_k, 14: _q6_k, 15: _q8_k}
+
+
+def dequantize_blocks(ttype: int, blocks) -> np.ndarray:
+    """Raw blocks (uint8, any shape whose size is a whole number of blocks) -> float32 [n, per]."""
+    if ttype not in _DECODE:
+        raise NotImplementedError(f"GGUF tensor type {_NAMES.get(ttype, _UNSUPPORTED.get(ttype, ttype))} "
+                                  "is not dequantised by this reader")
+    size = _BLOCK[ttype][1]
+    return _DECODE[ttype](np.asarray(blocks, np.uint8).reshape(-1, size))
+
+
 def dequantize(info: TensorInfo) -> np.ndarray:
     """-> float32 array in numpy order."""
     t = info.tensor_type
@@ -152,18 +322,7 @@ def dequantize(info: TensorInfo) -> np.ndarray:
         return np.asarray(info.data).astype(np.float32)
     if t == 30:
         return (np.asarray(info.data, np.uint16).astype(np.uint32) << 16).view(np.float32)
-    if t == 2:       # Q4_0: fp16 d, 16 bytes of nibbles (low = elements 0..15, high = 16..31)
-        b = np.asarray(info.data).reshape(-1, 18)
-        d = b[:, :2].copy().view(np.float16).astype(np.float32)
-        q = b[:, 2:]
-        vals = np.concatenate([q & 15, q >> 4], axis=1).astype(np.float32) - 8.0
-        return (vals * d).reshape(shape)
-    if t == 8:       # Q8_0: fp16 d, 32 int8 codes
-        b = np.asarray(info.data).reshape(-1, 34)
-        d = b[:, :2].copy().view(np.float16).astype(np.float32)
-        q = b[:, 2:].copy().view(np.int8).astype(np.float32)
-        return (q * d).reshape(shape)
-    raise NotImplementedError(f"GGUF tensor type {_NAMES.get(t, t)} is not dequantised by this reader")
+    return dequantize_blocks(t, info.data).reshape(shape)
 
 
 class GGUFView:

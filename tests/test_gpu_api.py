@@ -267,6 +267,71 @@ def test_qk_norm_decoder_matches_hf_qwen3():
     assert cosine(got, want) > 0.999 and int(np.argmax(got)) == int(np.argmax(want))
 
 
+def _kq_rows(kind, rows, K, rng):
+    """Random valid K-quant rows (block bytes [rows, K / 256 * block size]) with weights of about
+    0.05-0.1, packed by the element-by-element encoders of test_gguf_codecs."""
+    from test_gguf_codecs import enc_q4_k, enc_q5_k, enc_q6_k
+    out = []
+    for _ in range(rows * K // 256):
+        if kind == "Q6_K":
+            out.append(enc_q6_k(0.0005, [int(v) for v in rng.integers(-16, 16, 16)],
+                                [int(v) for v in rng.integers(-32, 32, 256)]))
+        elif kind == "Q4_K":
+            sc = [int(v) for v in rng.integers(4, 9, 8)]
+            out.append(enc_q4_k(0.002, 0.002, sc, [round(7.5 * s) for s in sc], [int(v) for v in rng.integers(0, 16, 256)]))
+        else:
+            sc = [int(v) for v in rng.integers(2, 5, 8)]
+            out.append(enc_q5_k(0.002, 0.002, sc, [round(15.5 * s) for s in sc], [int(v) for v in rng.integers(0, 32, 256)]))
+    return np.frombuffer(b"".join(out), np.uint8).reshape(rows, -1)
+
+
+def test_load_gguf_k_quant_file(tmp_path):
+    """A Q4_K_M-style Qwen3-MoE GGUF (Q4_K gate/up experts, Q5_K down experts, Q6_K attention,
+    fp16 elsewhere): load_gguf dequantises the K-quants on the host to fp16, as the reference's
+    GGUFView.get does (aneforge/_gguf.py:34-39), and the decode matches the oracle over the same
+    fp16 weights."""
+    from aneforge_amd import _gguf
+    say("moe.load_gguf on a synthetic K-quant GGUF")
+    E, D, F, L, dh, H, KV = 4, 256, 256, 1, 64, 4, 2
+    cfg, w = _moe_model(E=E, D=D, F=F, layers=L, qk=True, seed=9, dh=dh)
+    rng = np.random.default_rng(9)
+    dec = lambda kind, raw, rows, K: _gguf.dequantize_blocks(_gguf.GGML[kind], raw).reshape(rows, K)
+    tensors = {"token_embd.weight": w["embed"].astype(np.float16), "output_norm.weight": w["final_norm"],
+               "output.weight": w["lm_head"].astype(np.float16)}
+    for i, lw in enumerate(w["layers"]):
+        b = f"blk.{i}."
+        for key, nm, rows in (("wq", "attn_q", H * dh), ("wk", "attn_k", KV * dh), ("wv", "attn_v", KV * dh),
+                              ("wo", "attn_output", D)):
+            raw = _kq_rows("Q6_K", rows, 256, rng)
+            tensors[b + nm + ".weight"] = ("Q6_K", raw, (rows, 256))
+            lw[key] = dec("Q6_K", raw, rows, 256)
+        tensors.update({b + "attn_norm.weight": lw["attn_norm"], b + "ffn_norm.weight": lw["mlp_norm"],
+                        b + "ffn_gate_inp.weight": lw["router"].astype(np.float16),
+                        b + "attn_q_norm.weight": lw["q_norm"], b + "attn_k_norm.weight": lw["k_norm"]})
+        for key, nm in (("wgate_exps", "ffn_gate_exps"), ("wup_exps", "ffn_up_exps")):
+            raws = [_kq_rows("Q4_K", F, D, rng) for _ in range(E)]
+            tensors[b + nm + ".weight"] = ("Q4_K", np.concatenate(raws), (E, F, D))
+            lw[key] = np.stack([dec("Q4_K", r, F, D) for r in raws])
+        raws = [_kq_rows("Q5_K", D, F, rng) for _ in range(E)]               # GGUF down: [E, dim, ffn]
+        tensors[b + "ffn_down_exps.weight"] = ("Q5_K", np.concatenate(raws), (E, D, F))
+        lw["wdown_exps"] = np.stack([dec("Q5_K", r, D, F).T for r in raws])   # canonical [E, ffn, dim]
+    meta = {"general.architecture": "qwen3moe", "qwen3moe.block_count": L, "qwen3moe.expert_count": E,
+            "qwen3moe.expert_used_count": 2, "qwen3moe.embedding_length": D, "qwen3moe.attention.head_count": H,
+            "qwen3moe.attention.head_count_kv": KV, "qwen3moe.attention.key_length": dh,
+            "qwen3moe.rope.freq_base": 10000.0, "qwen3moe.attention.layer_norm_rms_epsilon": 1e-5}
+    path = str(tmp_path / "tiny-moe-kq.gguf")
+    _gguf.write_gguf(path, meta, tensors)
+    m = af.moe.load_gguf(path)
+    assert m.cfg.extra["n_experts"] == E and m.cfg.layers[0].qk_norm
+    prompt = [5, 6, 7]
+    got = m.generate(prompt, max_new_tokens=6)
+    enc16 = lambda W: np.asarray(W, np.float32).astype(np.float16).astype(np.float32)
+    ow, ocfg = _oracle_weights(cfg, w, enc16)
+    want, lgs = ref.generate(prompt, 6, ow, ocfg, M=len(prompt) + 6)
+    from test_gpu_llm import _assert_tokens_match
+    _assert_tokens_match(got, want, lgs, "gguf k-quants")
+
+
 def test_load_gguf_q4_0_experts_stay_4bit(tmp_path):
     """A synthetic Qwen3-MoE GGUF (Q4_0 experts, fp16 elsewhere) written by aneforge_amd._gguf:
     load_gguf streams the file's own codes (bit-identical to the file) and decodes like the oracle."""

@@ -5,6 +5,7 @@ behind the reference's Python API (aneforge/__init__.py:13-38):
   af.compile(out, compress=...) -> Model                      kernel lowering (_compile.py)
   af.LlamaConfig / af.LlamaPrefill / af.load_llm / af.rope     decoder on the device (llm.py)
   af.moe (load_gguf, _moe, _topk_gate)                         sparse MoE (moe.py)
+  aneforge_amd.speculative.spec_generate                       greedy speculative decoding (speculative.py)
 
 Compute runs in hand-written HIP kernels for gfx950 (libaneforge_hip.so, include/aneforge_hip.h);
 PyTorch-ROCm only allocates device memory and provides streams.  There is no CPU fallback."""

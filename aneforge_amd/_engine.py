@@ -470,6 +470,69 @@ class DecodeEngine:
             self.step.fill_(n)
             K.embed(self.embed, ids[n:n + 1], out=self.h)
 
+    # -- speculative decoding: reposition, force, verify --
+    def seek(self, pos: int, tok: int):
+        """Make `tok` the pending input at position `pos`, keeping cache rows [0, pos); the next
+        steps are greedy and record their tokens at hist[pos], hist[pos + 1], ..."""
+        if not 0 <= pos < self.M:
+            raise ValueError(f"seek: position {pos} outside the {self.M}-row cache")
+        with torch.cuda.stream(self.stream):
+            self.pos.fill_(pos)
+            self.step.fill_(pos)
+            self.n_forced.zero_()
+            K.embed(self.embed, torch.tensor([int(tok)], dtype=torch.int32, device="cuda"), out=self.h)
+
+    def force_next(self, step: int, tok: int):
+        """The step with counter `step` (the pending one) emits `tok` instead of its argmax."""
+        with torch.cuda.stream(self.stream):
+            self.forced[step].fill_(int(tok))
+            self.n_forced.fill_(step + 1)
+
+    def verify(self, tokens, pos0: int) -> np.ndarray:
+        """Greedy next token after each of `tokens`, fed at positions pos0, pos0 + 1, ...: their K/V
+        rows overwrite the cache from pos0 on and row i attends to rows [0, pos0 + i].  Layers with a
+        batched path run all rows at once (the prefill kernels); otherwise one forced step per row.
+        Returns int64 [len(tokens)] (lowest index on ties); pos / step / h are left unspecified."""
+        toks = [int(t) for t in tokens]
+        n = len(toks)
+        if n == 0 or pos0 < 0 or pos0 + n > self.M:
+            raise ValueError(f"verify: {n} rows at position {pos0} do not fit the {self.M}-row cache")
+        if getattr(self, "_vf", None) is None or self._vf["ids"].shape[0] < n:
+            self._vf = {"ids": torch.empty(n, dtype=torch.int32, device="cuda"),
+                        "hn": torch.empty((n, self.cfg.dim), dtype=torch.float16, device="cuda"),
+                        "logits": torch.empty((n, self.V), dtype=torch.float32, device="cuda")}
+        out = self._vf["ids"][:n]
+        with torch.cuda.stream(self.stream):
+            ids = torch.tensor(toks, dtype=torch.int32, device="cuda")
+            if self.prefill_supported():
+                bufs = self._prefill_buffers(n)
+                X = bufs["x"][:n]
+                K.embed(self.embed, ids, out=X)
+                for mixer, mlp in self.layers:
+                    mixer.prefill(self, X, pos0, bufs)
+                    mlp.prefill(self, X, pos0, bufs)
+                hn, lg = self._vf["hn"][:n], self._vf["logits"][:n]
+                K.rmsnorm(X, self.final_norm, self.cfg.norm_eps, y=hn)
+                for r in range(0, n, 8):                   # the head GEMV takes up to 8 rows
+                    K.linear(self.head.fmt, self.head.w, self.head.scale, hn[r:r + 8], y=lg[r:r + 8],
+                             out_f32=True)
+                K.argmax(lg, out=out)
+            else:
+                self.pos.fill_(pos0)
+                self.step.fill_(pos0)
+                K.embed(self.embed, ids[:1], out=self.h)
+                if n > 1:
+                    self.forced[pos0:pos0 + n - 1].copy_(ids[1:])
+                self.n_forced.fill_(pos0 + n - 1)
+                for i in range(n):
+                    self.enqueue_layers()
+                    self.enqueue_head()
+                    K.argmax(self.logits, out=out[i:i + 1])
+                    if i + 1 < n:
+                        self.enqueue_advance(False)
+        self.sync()
+        return out.cpu().numpy().astype(np.int64)
+
     def run(self, n_prefill: int, n_decode: int, graph: bool = True):
         """Enqueue n_prefill forced steps then n_decode greedy steps (no host sync)."""
         if graph:

@@ -513,9 +513,7 @@ class DecodeEngine:
                     mlp.prefill(self, X, pos0, bufs)
                 hn, lg = self._vf["hn"][:n], self._vf["logits"][:n]
                 K.rmsnorm(X, self.final_norm, self.cfg.norm_eps, y=hn)
-                for r in range(0, n, 8):                   # the head GEMV takes up to 8 rows
-                    K.linear(self.head.fmt, self.head.w, self.head.scale, hn[r:r + 8], y=lg[r:r + 8],
-                             out_f32=True)
+                K.linear(self.head.fmt, self.head.w, self.head.scale, hn, y=lg, out_f32=True)
                 K.argmax(lg, out=out)
             else:
                 self.pos.fill_(pos0)

@@ -62,7 +62,7 @@ static int grid_for(int ngroups) { return (ngroups + 3) / 4; }
 
 static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t stream, const char* what) {
   AFX_REQUIRE(a.w && a.x && a.y, "%s: null pointer argument", what);
-  AFX_REQUIRE(a.M >= 1 && a.M <= 8, "%s: M=%d must be in [1, 8]", what, a.M);
+  AFX_REQUIRE(a.M >= 1, "%s: M=%d must be >= 1", what, a.M);
   AFX_REQUIRE(a.N >= 1 && a.K >= 1, "%s: bad shape N=%d K=%d", what, a.N, a.K);
   const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : 8;
   AFX_REQUIRE(a.K % kq == 0, "%s: K=%d must be a multiple of %d", what, a.K, kq);
@@ -79,12 +79,32 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
     AFX_REQUIRE(a.dh >= 2 && a.dh % 2 == 0 && a.nq % a.dh == 0 && a.nk % a.dh == 0 && a.pos && a.kcache &&
                     a.vcache,
                 "%s: bad fused-QKV arguments", what);
-  // 4+ activation rows without a norm prologue: the dot products go to MFMA
+  // 4+ activation rows without a norm prologue: the dot products go to MFMA (any row count, in
+  // groups of 16); the vector kernels below take at most 8 rows
   if (a.M >= mfma_min_rows() && eg != EG_QKV && !a.gamma && mfma_supported(fmt, a.K) && a.N % 4 == 0) {
     MfmaArgs m = {};
     m.w = a.w; m.scale = a.scale; m.x = a.x; m.ldx = a.ldx; m.y = a.y; m.ldy = a.ldy;
     m.bias = a.bias; m.resid = a.resid; m.M = a.M; m.N = a.N; m.K = a.K; m.epi = a.epi;
     return mfma_launch(fmt, m, 1, stream, what);
+  }
+  if (a.M > 8) {
+    // the vector kernels take up to 8 rows: launch them 8 rows at a time
+    const size_t ysz = a.epi == EPI_F32 ? 4 : 2;
+    for (int r0 = 0; r0 < a.M; r0 += 8) {
+      GemvArgs c = a;
+      c.M = a.M - r0 < 8 ? a.M - r0 : 8;
+      c.x = a.x + (size_t)r0 * a.ldx;
+      c.y = (unsigned char*)a.y + (size_t)r0 * a.ldy * ysz;
+      if (a.resid) c.resid = a.resid + (size_t)r0 * a.ldy;
+      if (eg == EG_QKV) {
+        c.pos = a.pos + r0;
+        c.kcache = a.kcache + (size_t)r0 * a.kv_seq_stride;
+        c.vcache = a.vcache + (size_t)r0 * a.kv_seq_stride;
+      }
+      const int rc = launch(fmt, c, eg, rows_hint, stream, what);
+      if (rc) return rc;
+    }
+    return 0;
   }
   const int mt = mtile(a.M);
   const bool norm = a.gamma != nullptr;

@@ -17,33 +17,38 @@
 
 namespace afx {
 
-// One wavefront per token (tokens w, w + 4, ... for wavefront w); lane l owns experts l, l + 64, ...
-__global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
-                                                       int renorm, float* __restrict__ gate,
-                                                       int* __restrict__ sel, int* __restrict__ cnt,
-                                                       int* __restrict__ list) {
+// One wavefront per token (tokens w, w + W, ... for the workgroup's W wavefronts); lane l owns
+// experts l, l + 64, ..., l + 64 * (J - 1), J = ceil(E / 64) rounded up to an instantiated count.
+template <int J>
+__global__ __launch_bounds__(1024) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                        int renorm, float* __restrict__ gate,
+                                                        int* __restrict__ sel, int* __restrict__ cnt,
+                                                        int* __restrict__ list) {
   extern __shared__ int s_sel[];   // [T][k]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  constexpr int kMaxPerLane = 33;  // E <= 2049 = 64 * 32 + 1
-  for (int tt = wave; tt < T; tt += 4) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int tt = wave; tt < T; tt += nw) {
     const float* lr = logits + (size_t)tt * E;
-    float lg[kMaxPerLane];
+    float lg[J];
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+    for (int j = 0; j < J; ++j) {
       const int e = lane + 64 * j;
       lg[j] = e < E ? lr[e] : -INFINITY;
       m = fmaxf(m, lg[j]);
     }
     m = wave_max(m);
+    float ex[J];
     float sum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) sum += lane + 64 * j < E ? expf(lg[j] - m) : 0.0f;
+    for (int j = 0; j < J; ++j) {
+      ex[j] = lane + 64 * j < E ? expf(lg[j] - m) : 0.0f;
+      sum += ex[j];
+    }
     const float inv = 1.0f / wave_sum(sum);
     // probabilities rounded to fp16 (-1 marks experts this lane does not own)
-    float p[kMaxPerLane];
+    float p[J];
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) p[j] = lane + 64 * j < E ? (float)(half_t)(expf(lg[j] - m) * inv) : -1.0f;
+    for (int j = 0; j < J; ++j) p[j] = lane + 64 * j < E ? (float)(half_t)(ex[j] * inv) : -1.0f;
     // k rounds: max of the fp16 probabilities, lowest index on exact ties; lane r keeps round r
     float tot = 0.0f, mine = 0.0f;
     int mine_e = 0;
@@ -51,14 +56,14 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
       float best = -1.0f;
       int bi = 0x7fffffff;
 #pragma unroll
-      for (int j = 0; j < kMaxPerLane; ++j)
+      for (int j = 0; j < J; ++j)
         if (p[j] > best) { best = p[j]; bi = lane + 64 * j; }   // ascending index: first max wins
       const float wb = wave_max(best);
       float cand = best == wb ? (float)bi : 3.0e38f;
       cand = -wave_max(-cand);                   // lowest index holding the maximum
       const int win = (int)cand;
 #pragma unroll
-      for (int j = 0; j < kMaxPerLane; ++j)
+      for (int j = 0; j < J; ++j)
         if (lane + 64 * j == win) p[j] = -1.0f;  // taken
       if (lane == r) { mine = wb; mine_e = win; }
       tot += wb;
@@ -228,7 +233,11 @@ int afx_moe_topk(const float* logits, int T, int E, int k, int renorm, float* ga
   AFX_REQUIRE(logits && gate && sel && cnt && list, "afx_moe_topk: null pointer");
   AFX_REQUIRE(k >= 1 && k <= E && E <= 2049 && k <= 64, "afx_moe_topk: need 1 <= k <= E <= 2049 (k <= 64); got k=%d E=%d", k, E);
   AFX_REQUIRE(T >= 1 && T * k <= 16384, "afx_moe_topk: T=%d out of range", T);
-  hipLaunchKernelGGL(moe_topk_kernel, dim3(1), dim3(256), (size_t)T * k * sizeof(int), (hipStream_t)stream,
+  const int jn = (E + 63) / 64;
+  auto fn = jn <= 1 ? moe_topk_kernel<1> : jn <= 2 ? moe_topk_kernel<2> : jn <= 4 ? moe_topk_kernel<4>
+          : jn <= 8 ? moe_topk_kernel<8> : jn <= 16 ? moe_topk_kernel<16> : moe_topk_kernel<33>;
+  const int waves = T < 16 ? T : 16;               // one wavefront per token, up to 16 at a time
+  hipLaunchKernelGGL(fn, dim3(1), dim3(64 * waves), (size_t)T * k * sizeof(int), (hipStream_t)stream,
                      logits, T, E, k, renorm, gate, sel, cnt, list);
   return check_launch("afx_moe_topk");
 }

@@ -148,8 +148,7 @@ class MoEDecode:
         from . import _kernels as K
         T = h.shape[0]
         K.rmsnorm(h, self.norm, self.eps, y=b["hn"][:T])
-        for r0 in range(0, T, 8):
-            K.linear("fp16", self.router.w, None, b["hn"][r0:r0 + 8], y=b["logits"][r0:r0 + 8], out_f32=True)
+        K.linear("fp16", self.router.w, None, b["hn"][:T], y=b["logits"][:T], out_f32=True)
         K.moe_topk(b["logits"][:T], self.k, self.renorm, b["gate"][:T], b["sel"][:T], b["cnt"], b["list"])
         K.moe_gateup(self.gu.fmt, self.gu.w, self.gu.scale, b["hn"][:T], self.k, self.E, self.F, b["cnt"],
                      b["list"], act=b["act"][:T * self.k])
@@ -157,11 +156,9 @@ class MoEDecode:
                    self.F, self.D, b["cnt"], b["list"], y=b["y"][:T * self.k])
         shared = None
         if self.shared:
-            for r0 in range(0, T, 8):          # the shared expert's GEMVs take up to 8 rows a call
-                r1 = min(T, r0 + 8)
-                K.linear_swiglu(self.sh_gu.fmt, self.sh_gu.w, self.sh_gu.scale, b["hn"][r0:r1], act=b["sh_act"][r0:r1])
-                K.linear(self.sh_down.fmt, self.sh_down.w, self.sh_down.scale, b["sh_act"][r0:r1], y=b["sh_y"][r0:r1])
-                K.linear("fp16", self.sh_gate.w, None, b["hn"][r0:r1], y=b["sh_g"][r0:r1])
+            K.linear_swiglu(self.sh_gu.fmt, self.sh_gu.w, self.sh_gu.scale, b["hn"][:T], act=b["sh_act"][:T])
+            K.linear(self.sh_down.fmt, self.sh_down.w, self.sh_down.scale, b["sh_act"][:T], y=b["sh_y"][:T])
+            K.linear("fp16", self.sh_gate.w, None, b["hn"][:T], y=b["sh_g"][:T])
             K._hip.call("afx_ew_unary", K.UNARY["sigmoid"], K.P(b["sh_g"]), K.P(b["sh_gs"]), T, 0.0, 0.0, K.stream())
             shape = [T, self.D]
             K._hip.call("afx_ew_binary", K.EW["mul"], K.P(b["sh_y"]), K._ll([self.D, 1]), K.P(b["sh_gs"]),

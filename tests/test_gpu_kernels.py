@@ -59,7 +59,8 @@ def _w8(N, Kd, seed):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(1, 4096, 4096), (1, 1000, 1024), (3, 777, 4112), (8, 256, 11008),
-                                    (5, 6144, 4096), (2, 22016, 4096), (1, 4096, 11008)])
+                                    (5, 6144, 4096), (2, 22016, 4096), (1, 4096, 11008),
+                                    (12, 777, 4112), (20, 1000, 1024)])   # > 8 rows: vector in 8s / MFMA
 def test_linear_int8(K, M, N, Kd):
     say(f"linear int8 M={M} N={N} K={Kd}")
     q, s = _w8(N, Kd, 20 + M)
@@ -181,13 +182,13 @@ def test_linear_swiglu(K):
     check_f16(got, ref.r16(ref.silu(gg) * uu), what="swiglu")
 
 
-@pytest.mark.parametrize("M,H,KV,dh,pos", [(1, 32, 8, 128, 2048), (2, 4, 2, 64, 5)])
+@pytest.mark.parametrize("M,H,KV,dh,pos", [(1, 32, 8, 128, 2048), (2, 4, 2, 64, 5), (10, 4, 2, 64, 5)])
 def test_qkv_rope_kv_fused(K, M, H, KV, dh, pos):
     say(f"fused qkv+rope+kv write M={M} H={H} KV={KV} dh={dh} pos={pos}")
     from aneforge_amd import _blob
     rng = np.random.default_rng(30)
     D = H * dh if H * dh >= 1024 else 1024
-    Mmax = pos + 4
+    Mmax = pos + M + 3
     qq, sq = _w8(H * dh, D, 31)
     qk, sk = _w8(KV * dh, D, 32)
     qv, sv = _w8(KV * dh, D, 33)

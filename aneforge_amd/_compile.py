@@ -9,9 +9,11 @@ The reference lowers the graph to MIL + a weight BLOBFILE and hands it to Espres
   compress_atol (accuracy gate, CompressionFallbackWarning), block_size.
 
 Weight encodings (aneforge/_compile.py:112-188): "int8" -> per-output-row int8 streamed by the
-int8 GEMV; "int4" (16-entry LUT) and "blockwise" (int8 per 32-column block) are accepted when
-their relative reconstruction error is <= compress_atol and are streamed as their exact fp16
-reconstruction, else they fall back ("int4" -> int8, "blockwise" -> fp16) with a warning;
+int8 GEMV; "int4" (16-entry LUT) and "blockwise" (int8 per block_size-column block) are accepted
+when their relative reconstruction error is <= compress_atol, else they fall back ("int4" -> int8,
+"blockwise" -> fp16) with a warning.  Accepted blockwise weights with 32-column blocks (K % 64 == 0)
+stream their int8 codes and block scales (the kernels form fp16(q * s)); other block sizes and
+int4 stream their exact fp16 reconstruction;
 "sparse" is lossless and streams fp16; "auto" takes int8; "q4_0" (this build's addition) uses
 the GGUF Q4_0 GEMV.  bmm_weight int8 keeps the reference's one-scale-per-batch quirk
 (aneforge/_compile.py:117)."""
@@ -83,7 +85,7 @@ def _encode_weight(W, compress, atol, block_size, stats: _Enc, allow_q=True):
         N, Kd = W.shape
         rec = (q.reshape(N, Kd // bs, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(N, Kd)
         if _rel_err(rec, W) <= atol:
-            return E.pack_linear(rec.astype(F16).astype(np.float32), None)
+            return E.pack_encoded(*E.blockwise_encoding(q, s, bs))
         stats.rejected["blockwise"] = stats.rejected.get("blockwise", 0) + 1
         return E.pack_linear(W, None)
     if compress in ("int8", "auto"):

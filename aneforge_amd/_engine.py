@@ -36,7 +36,7 @@ F16 = np.float16
 @dataclass
 class Linear:
     """A weight [N, K] resident on the device in one of the kernel formats."""
-    fmt: str                          # "int8" | "q4_0" | "fp16"
+    fmt: str                          # "int8" | "q4_0" | "fp16" | "blockwise"
     w: torch.Tensor
     scale: torch.Tensor | None
     N: int
@@ -127,7 +127,8 @@ def _to_dev(a, dtype=None) -> torch.Tensor:
 
 def encode(W: np.ndarray, compress: str | None):
     """Host encoding of a float weight [N, K] -> (fmt, codes, scale) following `compress=`
-    (aneforge/_compile.py:112-188: per-row int8; blockwise and LUT4 are reconstructed to fp16).
+    (aneforge/_compile.py:112-188: per-row int8; blockwise streams its int8 codes and 32-weight
+    block scales; LUT4 is reconstructed to fp16).
     Already-encoded weights keep their codes."""
     if isinstance(W, QuantizedWeight):
         q = W.to_superblock()
@@ -147,10 +148,7 @@ def encode(W: np.ndarray, compress: str | None):
         qs, d = _blob.q4_0_to_superblock(_blob.quantize_q4_0(W), N, Kd)
         return "q4_0", qs, d
     if compress == "blockwise":
-        q, s, bs = _blob.quantize_blockwise(W, 32)
-        N, Kd = W.shape
-        rec = (q.reshape(N, Kd // bs, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(N, Kd)
-        return "fp16", rec.astype(F16), None
+        return blockwise_encoding(*_blob.quantize_blockwise(W, 32))
     if compress == "int4":
         packed, cb = _blob.palettize_lut4(W)
         idx = np.empty((W.shape[0], packed.shape[1] * 2), np.uint8)
@@ -158,6 +156,23 @@ def encode(W: np.ndarray, compress: str | None):
         rec = cb.astype(np.float32)[idx[:, :W.shape[1]]]
         return "fp16", rec.astype(F16), None
     raise ValueError(f"unknown compress={compress!r}")
+
+
+def blockwise_encoding(q, s, bs):
+    """quantize_blockwise output -> (fmt, codes, scale): the kernels' "blockwise" format (int8
+    codes, fp16 scale [N, K/32]) for 32-weight blocks and K % 64 == 0, else the exact fp16
+    reconstruction fp16(q * s) the reference's weights equal."""
+    N, Kd = q.shape
+    if bs == 32 and Kd % 64 == 0:
+        return "blockwise", np.ascontiguousarray(q, np.int8), np.ascontiguousarray(s, F16)
+    rec = (q.reshape(N, Kd // bs, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(N, Kd)
+    return "fp16", rec.astype(F16), None
+
+
+def pack_encoded(fmt, w, s, bias=None) -> Linear:
+    N, Kd = w.shape[0], (w.shape[1] * 2 if fmt == "q4_0" else w.shape[1])
+    return Linear(fmt, _to_dev(w), None if s is None else _to_dev(s), N, Kd,
+                  None if bias is None else _to_dev(np.asarray(bias, np.float32).astype(F16)))
 
 
 def pack_linear(W, compress, bias=None) -> Linear:
@@ -251,7 +266,7 @@ class AttentionDecode:
 
     def prefill_supported(self) -> bool:
         lin = (self.qkv, self.wo)
-        return (self.dh == 128 and all(l.fmt in ("int8", "fp16") for l in lin)
+        return (self.dh == 128 and all(l.fmt in ("int8", "fp16", "blockwise") for l in lin)
                 and all(l.K % 64 == 0 and l.N % 16 == 0 for l in lin))
 
     def prefill(self, eng, X, pos0: int, bufs: dict):
@@ -314,7 +329,7 @@ class SwiGLUDecode:
 
     def prefill_supported(self) -> bool:
         lin = (self.gu, self.down)
-        return all(l.fmt in ("int8", "fp16") and l.K % 64 == 0 and l.N % 16 == 0 for l in lin)
+        return all(l.fmt in ("int8", "fp16", "blockwise") and l.K % 64 == 0 and l.N % 16 == 0 for l in lin)
 
     def prefill(self, eng, X, pos0: int, bufs: dict):
         """Prompt rows X [m, D] in place: RMSNorm -> gate/up GEMM + SwiGLU -> down GEMM + residual."""

@@ -85,6 +85,23 @@ __global__ void dequant_i8_kernel(const uint32_t* __restrict__ q, const half_t* 
   *(float4*)(out + 4 * i) = o;
 }
 
+// compress="blockwise": fp16(q * s[row][k / 32]) -- the reference's reconstructed weight.
+__global__ void dequant_bw_kernel(const uint32_t* __restrict__ q, const half_t* __restrict__ s,
+                                  float* __restrict__ out, int N, int K) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;   // one dword = 4 codes
+  const long long nw = (long long)N * (K >> 2);
+  if (i >= nw) return;
+  const int row = (int)(i / (K >> 2)), k0 = (int)(i - (long long)row * (K >> 2)) * 4;
+  h2 lo, hi;
+  i8x4_to_h2(q[i], lo, hi);
+  const half_t sc = s[(size_t)row * (K >> 5) + (k0 >> 5)];
+  const h2 s2 = {sc, sc};
+  lo = lo * s2;
+  hi = hi * s2;
+  float4 o = {(float)lo.x, (float)lo.y, (float)hi.x, (float)hi.y};
+  *(float4*)(out + 4 * i) = o;
+}
+
 __global__ void dequant_q4_kernel(const uint32_t* __restrict__ qs, const half_t* __restrict__ d,
                                   float* __restrict__ out, int N, int K) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;   // one word = 8 elements
@@ -143,6 +160,11 @@ int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, in
     AFX_REQUIRE(K % 128 == 0, "afx_dequant: Q4_0 K must be a multiple of 128");
     const long long nw = (long long)N * (K / 8);
     hipLaunchKernelGGL(dequant_q4_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint32_t*)w, (const half_t*)scale, out, N, K);
+  } else if (fmt == 3) {
+    AFX_REQUIRE(K % 32 == 0 && ((uintptr_t)w & 3) == 0, "afx_dequant: blockwise K must be a multiple of 32");
+    const long long nw = (long long)N * (K / 4);
+    hipLaunchKernelGGL(dequant_bw_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, (const uint32_t*)w, (const half_t*)scale, out, N, K);
   } else {
     return set_error("afx_dequant: unknown format %d", fmt);

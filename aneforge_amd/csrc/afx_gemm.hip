@@ -2,7 +2,8 @@
 //
 //   Y[m, n] = epilogue( sum_k X[m, k] * W^[n, k] ),   X fp16 [M][K] (row stride ldx),
 //   W int8 codes with an fp16 row scale (W^ = q * s, the compress="int8" linear,
-//   aneforge/_compile.py:171-179 and 375-385) or fp16 [N][K].
+//   aneforge/_compile.py:171-179 and 375-385), int8 codes with an fp16 scale per 32-weight block
+//   (compress="blockwise": W^ = fp16(q * s[n][k / 32]), the reference's reconstruction) or fp16 [N][K].
 //
 // Prefill multiplies the same weights by hundreds or thousands of token rows, so unlike the
 // decode GEMV this is a dense contraction that v_mfma_f32_16x16x32_f16 bounds.  A 256-thread
@@ -29,10 +30,11 @@ constexpr int kGAStride = kGBK * 2 + 16;            // bytes per staged activati
 template <int FMT> struct GemmW;
 template <> struct GemmW<FMT_I8> { static constexpr int kRow = kGBK, kStride = kGBK + 8, kChunks = 2; };
 template <> struct GemmW<FMT_F16> { static constexpr int kRow = kGBK * 2, kStride = kGBK * 2 + 16, kChunks = 4; };
+template <> struct GemmW<FMT_BW> { static constexpr int kRow = kGBK, kStride = kGBK + 8, kChunks = 2; };
 
 struct GemmArgs {
   const void* w;          // [N][K] codes (int8) or values (fp16)
-  const half_t* scale;    // int8: [N] row scales
+  const half_t* scale;    // int8: [N] row scales; blockwise: [N][K/32] block scales
   const half_t* bias;     // [N] or null
   const half_t* x;        // [M] rows of K, stride ldx
   void* y;                // output rows, stride ldy (fp16, or fp32 for EPI_F32)
@@ -52,8 +54,10 @@ __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
 template <int FMT, int EG>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   constexpr int WS = GemmW<FMT>::kStride, WR = GemmW<FMT>::kRow, WC = GemmW<FMT>::kChunks;
+  constexpr bool kCodes = FMT == FMT_I8 || FMT == FMT_BW;   // one byte per weight
   __shared__ __align__(16) unsigned char As[2][kGBM * kGAStride];
   __shared__ __align__(16) unsigned char Bs[2][kGBN * WS];
+  __shared__ uint32_t Ss[2][FMT == FMT_BW ? kGBN : 1];    // blockwise: the 2 block scales of each row's step
   // tile: the XCD (id % 8) gets a contiguous range of logical tiles, row tiles fastest
   const int id = blockIdx.x;
   const int logical = (id & 7) * a.per_xcd + (id >> 3);
@@ -79,24 +83,34 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < WC; ++i) {
     const int c = tid + 256 * i;
-    const int r = FMT == FMT_I8 ? c >> 2 : c >> 3, ch = FMT == FMT_I8 ? c & 3 : c & 7;
+    const int r = kCodes ? c >> 2 : c >> 3, ch = kCodes ? c & 3 : c & 7;
     const int n = n0 + r < N ? n0 + r : N - 1;
-    wp[i] = (const unsigned char*)a.w + (size_t)n * (FMT == FMT_I8 ? K : 2 * K) + ch * 16;
+    wp[i] = (const unsigned char*)a.w + (size_t)n * (kCodes ? K : 2 * K) + ch * 16;
     boff[i] = r * WS + ch * 16;
   }
+  const half_t* sp = nullptr;                       // blockwise: thread t < 128 carries row n0 + t's scales
+  if constexpr (FMT == FMT_BW) {
+    const int n = n0 + (tid & 127) < N ? n0 + (tid & 127) : N - 1;
+    sp = a.scale + (size_t)n * (K >> 5);
+  }
   u4 ra[4], rb[WC];
+  uint32_t rs = 0;
   auto load = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) ra[i] = *(const u4*)(xp[i] + (size_t)kt * kGBK);
 #pragma unroll
     for (int i = 0; i < WC; ++i) rb[i] = __builtin_nontemporal_load((const u4*)(wp[i] + (size_t)kt * WR));
+    if constexpr (FMT == FMT_BW) rs = *(const uint32_t*)(sp + 2 * kt);
   };
   auto stage = [&](int s) {
+    if constexpr (FMT == FMT_BW) {
+      if (tid < kGBN) Ss[s][tid] = rs;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) *(u4*)(As[s] + aoff[i]) = ra[i];
 #pragma unroll
     for (int i = 0; i < WC; ++i) {
-      if constexpr (FMT == FMT_I8) {               // 72-byte rows: two 8-byte stores keep alignment
+      if constexpr (kCodes) {                      // 72-byte rows: two 8-byte stores keep alignment
         *(u2*)(Bs[s] + boff[i]) = (u2){rb[i].x, rb[i].y};
         *(u2*)(Bs[s] + boff[i] + 8) = (u2){rb[i].z, rb[i].w};
       } else {
@@ -127,8 +141,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const unsigned char* bp = Bs[s] + (wn * 64 + j * 16 + fr) * WS;
-        if constexpr (FMT == FMT_I8) bf[j] = i8x8_to_h8(*(const u2*)(bp + kk * 32 + 8 * fg));
-        else bf[j] = __builtin_bit_cast(h8, *(const u4*)(bp + (kk * 32 + 8 * fg) * 2));
+        if constexpr (FMT == FMT_I8) {
+          bf[j] = i8x8_to_h8(*(const u2*)(bp + kk * 32 + 8 * fg));
+        } else if constexpr (FMT == FMT_BW) {       // k 32kk .. 32kk + 31 is block kk of the step
+          const h2 sp2 = as_h2(Ss[s][wn * 64 + j * 16 + fr]);
+          const half_t sc = kk ? sp2.y : sp2.x;
+          const h8 s8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+          bf[j] = i8x8_to_h8(*(const u2*)(bp + kk * 32 + 8 * fg)) * s8;   // fp16(q * s)
+        } else {
+          bf[j] = __builtin_bit_cast(h8, *(const u4*)(bp + (kk * 32 + 8 * fg) * 2));
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -181,11 +203,12 @@ using namespace afx;
 extern "C" {
 
 // Y = epilogue(X @ W^T) for M activation rows (batched prefill).  fmt: 0 = int8 + row scale,
-// 2 = fp16.  epi: 0 fp16, 1 fp16 + residual (resid [M][ldy], may alias y), 2 fp32, 3 SwiGLU
+// 2 = fp16, 3 = int8 + fp16 scale per 32-weight block.  epi: 0 fp16, 1 fp16 + residual (resid [M][ldy], may alias y), 2 fp32, 3 SwiGLU
 // over interleaved gate/up rows (y[m][n/2] = silu(g) * u, ldy >= N/2).
 int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy, int M, int N,
              int K, const void* bias, const void* residual, int epi, void* stream) {
-  AFX_REQUIRE(fmt == FMT_I8 || fmt == FMT_F16, "afx_gemm: format %d not supported (int8 = 0, fp16 = 2)", fmt);
+  AFX_REQUIRE(fmt == FMT_I8 || fmt == FMT_F16 || fmt == FMT_BW,
+              "afx_gemm: format %d not supported (int8 = 0, fp16 = 2, blockwise = 3)", fmt);
   AFX_REQUIRE(w && x && y, "afx_gemm: null pointer");
   AFX_REQUIRE(M >= 1 && N >= 16 && N % 16 == 0 && K >= kGBK && K % kGBK == 0,
               "afx_gemm: need M >= 1, N %% 16 == 0, K %% 64 == 0 (M=%d N=%d K=%d)", M, N, K);
@@ -193,6 +216,7 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
               "afx_gemm: x and weights must be 16-byte aligned rows (ldx %% 8 == 0)");
   AFX_REQUIRE(epi >= 0 && epi <= 3, "afx_gemm: unknown epilogue %d", epi);
   AFX_REQUIRE(fmt != FMT_I8 || scale, "afx_gemm: int8 weights need row scales");
+  AFX_REQUIRE(fmt != FMT_BW || (scale && ((uintptr_t)scale & 3) == 0), "afx_gemm: blockwise weights need aligned block scales");
   AFX_REQUIRE(epi != EPI_RESID || residual, "afx_gemm: residual pointer required");
   AFX_REQUIRE(epi == EPI_SWIGLU ? ldy >= N / 2 : ldy >= N, "afx_gemm: ldy=%d too small", ldy);
   GemmArgs a = {};
@@ -203,6 +227,7 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   a.per_xcd = (a.tiles + 7) / 8;
   gemm_fn fn;
   if (fmt == FMT_I8) fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_I8, EG_SWIGLU> : gemm_kernel<FMT_I8, EG_PLAIN>;
+  else if (fmt == FMT_BW) fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_BW, EG_SWIGLU> : gemm_kernel<FMT_BW, EG_PLAIN>;
   else fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_F16, EG_SWIGLU> : gemm_kernel<FMT_F16, EG_PLAIN>;
   hipLaunchKernelGGL(fn, dim3(8 * a.per_xcd), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("afx_gemm");

@@ -5,7 +5,7 @@
 
 namespace afx {
 
-enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2 };
+enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2, FMT_BW = 3 };
 
 // ---- x sources: global memory or the LDS copy written by the norm prologue ----
 template <int N8>
@@ -72,6 +72,28 @@ template <> struct Fmt<FMT_Q4> {
   }
 };
 
+// compress="blockwise": int8 codes [N][K] with one fp16 scale per 32 consecutive weights of a row,
+// scale[N][K/32] (aneforge/_blob.py:46-56 with block_size 32).  The weight is the reference's
+// reconstruction fp16(q * s) (one v_pk_mul_f16 per pair, exact product rounded once); a 16-code
+// chunk lies in one block.  d.x = the scales of chunks 4i..4i+3 (two fp16), d.y = which half.
+template <> struct Fmt<FMT_BW> {
+  static constexpr int kWeightsPerChunk = 16;
+  static constexpr int kXH2 = 8;
+  __device__ static size_t row_bytes(int K) { return (size_t)K; }
+  __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) { afx::load_x<2>(xrow + 16 * c, x); }
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, float acc) {
+    const h2 sp = as_h2(d.x);
+    const half_t s = d.y ? sp.y : sp.x;
+    const h2 s2 = {s, s};
+    h2 q[8];
+    i8x4_to_h2(w.x, q[0], q[1]); i8x4_to_h2(w.y, q[2], q[3]);
+    i8x4_to_h2(w.z, q[4], q[5]); i8x4_to_h2(w.w, q[6], q[7]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = dot2(q[i] * s2, x[i], acc);
+    return acc;
+  }
+};
+
 template <> struct Fmt<FMT_F16> {
   static constexpr int kWeightsPerChunk = 8;
   static constexpr int kXH2 = 4;
@@ -86,11 +108,15 @@ template <> struct Fmt<FMT_F16> {
   }
 };
 
-// Q4 block scales for a chunk (4 fp16 in 8 bytes); other formats have none.
+// Block scales for a chunk: Q4, the 4 fp16 of its superblock; blockwise, the 2 fp16 of chunks
+// 4i..4i+3 and the half that is the chunk's; other formats have none.
 template <int FMT>
 __device__ __forceinline__ u2 load_scales(const half_t* drow, int c) {
   if constexpr (FMT == FMT_Q4) return *(const u2*)(drow + 4 * (c >> 2));
+  else if constexpr (FMT == FMT_BW) return (u2){*(const uint32_t*)(drow + 2 * (c >> 2)), (uint32_t)((c >> 1) & 1)};
   else return (u2){0u, 0u};
 }
+// Whether the format carries per-block scales in a [N][K/32] array.
+template <int FMT> constexpr bool has_block_scales() { return FMT == FMT_Q4 || FMT == FMT_BW; }
 
 }  // namespace afx

@@ -9,6 +9,8 @@
 //   FMT_Q4  : Q4_0 blocks of 32 along K, one fp16 scale d per block, repacked into the
 //             "superblock" layout (afx_q4_0_repack): W^ = (nibble-8)*d[n, k/32]
 //   FMT_F16 : plain fp16 [N, K] (lm_head, router)
+//   FMT_BW  : int8 codes [N, K] + fp16 scale per 32-weight block s[N, K/32] (compress="blockwise",
+//             aneforge/_blob.py:46-56): W^ = fp16(q * s[n, k/32])
 //
 // Work decomposition.  The kernel is HBM-bound, and at decode sizes (17-90 MB) it only gets
 // near the bandwidth floor with many small, independent work items and nothing serialised
@@ -101,6 +103,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 }
 __device__ __forceinline__ u4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));   // nt: streamed once
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 __device__ __forceinline__ u2 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
@@ -253,7 +258,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;   // a tail row is computed, never stored
     wr[r] = make_rsrc((const unsigned char*)a.w + (size_t)row * rowbytes, rowbytes);
-    if constexpr (FMT == FMT_Q4) dr[r] = make_rsrc(a.scale + (size_t)row * (K >> 5), K >> 4);
+    if constexpr (has_block_scales<FMT>()) dr[r] = make_rsrc(a.scale + (size_t)row * (K >> 5), K >> 4);
   }
   u4 wA[U][R], wB[U][R];
   u2 dA[U][R], dB[U][R];
@@ -265,6 +270,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         const int c = j * 64 * U + 64 * u + lane;
         w[u][r] = buf_load16(wr[r], c * 16);
         if constexpr (FMT == FMT_Q4) d[u][r] = buf_load8(dr[r], (c >> 2) * 8);
+        if constexpr (FMT == FMT_BW) d[u][r] = (u2){buf_load4(dr[r], (c >> 2) * 4), (uint32_t)((c >> 1) & 1)};
       }
     }
   };
@@ -435,7 +441,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;
     const u4* wr = (const u4*)((const unsigned char*)a.w + (size_t)row * Fmt<FMT>::row_bytes(K));
-    const half_t* dr = FMT == FMT_Q4 ? a.scale + (size_t)row * (K >> 5) : nullptr;
+    const half_t* dr = has_block_scales<FMT>() ? a.scale + (size_t)row * (K >> 5) : nullptr;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int c = 64 * u + lane;
@@ -558,13 +564,14 @@ gemv_fn pick_gemv_row_u(int eg, int R, int norm) {
 // Chunks per lane the fast path is built for, per format (0: none); see gemv_row_kernel.
 __host__ __device__ inline int fast_units(int fmt, int nchunks) {
   const int u = (nchunks + 63) / 64;
-  if (fmt == FMT_I8) return u == 4 || u == 11 ? u : 0;
+  if (fmt == FMT_I8 || fmt == FMT_BW) return u == 4 || u == 11 ? u : 0;
   if (fmt == FMT_Q4) return u == 2 || u == 6 ? u : 0;
   return u == 8 ? u : 0;
 }
 template <int FMT>
 gemv_fn pick_gemv_row(int eg, int R, int norm, int U) {
-  if constexpr (FMT == FMT_I8) return U == 11 ? pick_gemv_row_u<FMT, 11>(eg, R, norm) : pick_gemv_row_u<FMT, 4>(eg, R, norm);
+  if constexpr (FMT == FMT_I8 || FMT == FMT_BW)
+    return U == 11 ? pick_gemv_row_u<FMT, 11>(eg, R, norm) : pick_gemv_row_u<FMT, 4>(eg, R, norm);
   else if constexpr (FMT == FMT_Q4) return U == 6 ? pick_gemv_row_u<FMT, 6>(eg, R, norm) : pick_gemv_row_u<FMT, 2>(eg, R, norm);
   else return pick_gemv_row_u<FMT, 8>(eg, R, norm);
 }
@@ -573,8 +580,10 @@ gemv_fn pick_gemv_row(int eg, int R, int norm, int U) {
 gemv_fn pick_gemv_i8(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_q4(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_f16(int mt, int eg, int R, int xs);
+gemv_fn pick_gemv_bw(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_row_i8(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_q4(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_f16(int eg, int R, int norm, int U);
+gemv_fn pick_gemv_row_bw(int eg, int R, int norm, int U);
 
 }  // namespace afx

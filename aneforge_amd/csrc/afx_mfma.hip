@@ -15,7 +15,9 @@
 //   Q4_0 : a superblock chunk = 8 codes of each of 4 blocks -> four A operands, each
 //          fp16((nibble - 8) * d): the fp16-rounded dequantised weight the reference multiplies
 //          with (it converts the ggml dequantisation to float16, aneforge/_gguf.py:34-39);
-//   fp16 : a chunk = 8 weights -> one A operand.
+//   fp16 : a chunk = 8 weights -> one A operand;
+//   blockwise int8 (one fp16 scale per 32-weight block): like int8, each operand multiplied by
+//          its block's scale in fp16, i.e. the reference's reconstructed weight fp16(q * s).
 // A workgroup owns 16 output rows; its NW wavefronts split K evenly and their partial 16x16
 // tiles are summed through LDS by wavefront 0, which applies the epilogue.
 // Weight loads are row-contiguous: a batch is 4 steps = 16 rows x 256 bytes, fetched as four
@@ -39,6 +41,7 @@ template <int FMT> struct MfmaFmt;
 template <> struct MfmaFmt<FMT_I8> { static constexpr int kK = 64, kMfma = 2; };    // k per step (64 lanes)
 template <> struct MfmaFmt<FMT_Q4> { static constexpr int kK = 128, kMfma = 4; };
 template <> struct MfmaFmt<FMT_F16> { static constexpr int kK = 32, kMfma = 1; };
+template <> struct MfmaFmt<FMT_BW> { static constexpr int kK = 64, kMfma = 2; };
 
 constexpr int kSPB = 4;            // steps per batch: 16 rows x 256 bytes
 constexpr int kWRow = 256 + 16;    // LDS bytes per staged weight row
@@ -60,7 +63,7 @@ template <int FMT, int EG, int NW, int NB>
 __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
   constexpr int KS = MfmaFmt<FMT>::kK, NM = MfmaFmt<FMT>::kMfma;
   __shared__ __align__(16) unsigned char wl[NW][16 * kWRow];
-  __shared__ __align__(16) unsigned char sl[NW][FMT == FMT_Q4 ? 16 * kSRow : 16];
+  __shared__ __align__(16) unsigned char sl[NW][has_block_scales<FMT>() ? 16 * kSRow : 16];
   __shared__ f4 red[NW][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;          // MFMA role: A row / B column, k slot
@@ -84,10 +87,13 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
     const int row = n0 + 4 * h + lr < N ? n0 + 4 * h + lr : N - 1;   // tail rows computed, not stored
     lrow[h] = wbase + (size_t)row * rowbytes + lc * 16;
   }
+  // block scales: lane l stages row l / 4's scales of step (batch step) l % 4 -- Q4 4 per
+  // step (8 bytes), blockwise 2 per step (4 bytes)
+  constexpr int kSPS = FMT == FMT_Q4 ? 4 : 2;     // block scales per step
   const half_t* srow = nullptr;
-  if constexpr (FMT == FMT_Q4) {
+  if constexpr (has_block_scales<FMT>()) {
     const int row = n0 + (lane >> 2) < N ? n0 + (lane >> 2) : N - 1;
-    srow = sbase + (size_t)row * (K >> 5) + 4 * (lane & 3);
+    srow = sbase + (size_t)row * (K >> 5) + kSPS * (lane & 3);
   }
   const int nsteps = K / KS;
   const int s0 = nsteps * wave / NW, s1 = nsteps * (wave + 1) / NW;   // this wavefront's K range
@@ -122,10 +128,11 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
         c = c < nsteps * 4 ? c : nsteps * 4 - 1;
 #pragma unroll
         for (int h = 0; h < 4; ++h) wq[b][h] = __builtin_nontemporal_load((const u4*)(lrow[h] + (size_t)(c - lc) * 16));
-        if constexpr (FMT == FMT_Q4) {
+        if constexpr (has_block_scales<FMT>()) {
           int q = sb + (lane & 3);
           q = q < nsteps ? q : nsteps - 1;
-          sq[b] = *(const u2*)(srow + (size_t)(q - (lane & 3)) * 4);
+          if constexpr (FMT == FMT_Q4) sq[b] = *(const u2*)(srow + (size_t)(q - (lane & 3)) * 4);
+          else sq[b] = (u2){*(const uint32_t*)(srow + (size_t)(q - (lane & 3)) * 2), 0u};
         }
       }
       // activations: one batch (4 steps) per load group; int8/fp16 keep two groups in flight
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
 #pragma unroll
           for (int j = 0; j < NM; ++j) {
             int kx;
-            if constexpr (FMT == FMT_I8) kx = s * KS + 16 * g + 8 * j;
+            if constexpr (FMT == FMT_I8 || FMT == FMT_BW) kx = s * KS + 16 * g + 8 * j;
             else if constexpr (FMT == FMT_Q4) kx = 32 * (4 * s + j) + 8 * g;
             else kx = s * KS + 8 * g;
             xv[t][j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? xoff + kx * 2 : kOOB, 0, 0));
@@ -163,6 +170,7 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
 #pragma unroll
         for (int h = 0; h < 4; ++h) *(u4*)(wls + (4 * h + lr) * kWRow + lc * 16) = wq[b][h];
         if constexpr (FMT == FMT_Q4) *(u2*)(sls + (lane >> 2) * kSRow + (lane & 3) * 8) = sq[b];
+        if constexpr (FMT == FMT_BW) *(uint32_t*)(sls + (lane >> 2) * kSRow + (lane & 3) * 4) = sq[b].x;
         wave_sync_lds();
         u4 wv[kSPB];
         u2 dv[kSPB];
@@ -170,6 +178,7 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
         for (int t = 0; t < kSPB; ++t) {
           wv[t] = *(const u4*)(wls + r * kWRow + (4 * t + g) * 16);
           if constexpr (FMT == FMT_Q4) dv[t] = *(const u2*)(sls + r * kSRow + t * 8);
+          if constexpr (FMT == FMT_BW) dv[t] = (u2){*(const uint32_t*)(sls + r * kSRow + t * 4), 0u};
         }
 #pragma unroll
         for (int t = 0; t < kSPB; ++t) {
@@ -182,6 +191,15 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
               i8x4_to_h2(j == 0 ? wv[t].x : wv[t].z, q0, q1);
               i8x4_to_h2(j == 0 ? wv[t].y : wv[t].w, q2, q3);
               av = pack8(q0, q1, q2, q3);
+            } else if constexpr (FMT == FMT_BW) {
+              // chunk 4t + g holds k 16g .. 16g + 15 of the step: block g / 2 of its two
+              const h2 sp = as_h2(dv[t].x);
+              const half_t s = (g >> 1) ? sp.y : sp.x;
+              const h2 s2 = {s, s};
+              h2 q0, q1, q2, q3;
+              i8x4_to_h2(j == 0 ? wv[t].x : wv[t].z, q0, q1);
+              i8x4_to_h2(j == 0 ? wv[t].y : wv[t].w, q2, q3);
+              av = pack8(q0 * s2, q1 * s2, q2 * s2, q3 * s2);   // fp16(q * s)
             } else if constexpr (FMT == FMT_Q4) {
               const uint32_t wd = j == 0 ? wv[t].x : j == 1 ? wv[t].y : j == 2 ? wv[t].z : wv[t].w;
               const h2 dd = as_h2(j < 2 ? dv[t].x : dv[t].y);
@@ -268,17 +286,18 @@ static mfma_fn pick_mfma_w(int nw, int nb) {
 }
 static mfma_fn pick_mfma(int fmt, bool swiglu, int nw, int nb) {
   if (fmt == FMT_I8) return swiglu ? pick_mfma_w<FMT_I8, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_I8, EG_PLAIN>(nw, nb);
+  if (fmt == FMT_BW) return swiglu ? pick_mfma_w<FMT_BW, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_BW, EG_PLAIN>(nw, nb);
   if (fmt == FMT_Q4) return swiglu ? pick_mfma_w<FMT_Q4, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_Q4, EG_PLAIN>(nw, nb);
   return swiglu ? pick_mfma_w<FMT_F16, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_F16, EG_PLAIN>(nw, nb);
 }
 
 bool mfma_supported(int fmt, int K) {
-  const int ks = fmt == FMT_I8 ? 64 : fmt == FMT_Q4 ? 128 : 32;
+  const int ks = fmt == FMT_I8 || fmt == FMT_BW ? 64 : fmt == FMT_Q4 ? 128 : 32;
   return K % ks == 0 && K / ks >= 8;                           // at least one step per wavefront
 }
 
 int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const char* what) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 2, "%s: unknown weight format %d", what, fmt);
+  AFX_REQUIRE(fmt >= 0 && fmt <= 3, "%s: unknown weight format %d", what, fmt);
   AFX_REQUIRE(a.w && a.x && a.y, "%s: null pointer", what);
   AFX_REQUIRE(a.N >= 1 && a.N % 4 == 0, "%s: N=%d must be a multiple of 4", what, a.N);
   AFX_REQUIRE(mfma_supported(fmt, a.K), "%s: K=%d does not fit the MFMA split", what, a.K);
@@ -286,12 +305,13 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
               "%s: x and weights must be 16-byte aligned (ldx %% 8 == 0)", what);
   AFX_REQUIRE(fmt != FMT_I8 || (a.scale && ((uintptr_t)a.scale & 7) == 0), "%s: int8 needs aligned row scales", what);
   AFX_REQUIRE(fmt != FMT_Q4 || (a.scale && ((uintptr_t)a.scale & 7) == 0), "%s: Q4_0 needs aligned block scales", what);
+  AFX_REQUIRE(fmt != FMT_BW || (a.scale && ((uintptr_t)a.scale & 3) == 0), "%s: blockwise needs aligned block scales", what);
   AFX_REQUIRE(a.cnt ? (a.list && a.T >= 1 && a.k >= 1) : (a.M >= 1), "%s: bad token description", what);
   AFX_REQUIRE(a.epi != EPI_RESID || a.resid, "%s: residual pointer required", what);
   const long long xrows = a.cnt ? (a.x_by_token ? a.T : (long long)a.T * a.k) : a.M;
   const long long xbytes = xrows * a.ldx * 2;
   AFX_REQUIRE(xbytes < 0x7fff0000LL, "%s: activations span %lld bytes (limit 2 GiB)", what, xbytes);
-  const long long rowb = fmt == FMT_I8 ? a.K : fmt == FMT_Q4 ? a.K / 2 : 2LL * a.K;
+  const long long rowb = fmt == FMT_I8 || fmt == FMT_BW ? a.K : fmt == FMT_Q4 ? a.K / 2 : 2LL * a.K;
   AFX_REQUIRE((long long)a.N * rowb + 65536 < 0x7fff0000LL,
               "%s: a weight matrix of %d x %d exceeds the 2 GiB buffer range", what, a.N, a.K);
   MfmaArgs b = a;
@@ -300,7 +320,7 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
   // wavefronts per workgroup: the fewest of 4, 8, 16 that leave each wavefront at most four
   // batches; batches per round = batches per wavefront, capped at 4 (measured on MI355X);
   // AFX_MFMA_WAVES=4|8|16 overrides when that count also leaves at most four batches
-  const int ks = fmt == FMT_I8 ? 64 : fmt == FMT_Q4 ? 128 : 32;
+  const int ks = fmt == FMT_I8 || fmt == FMT_BW ? 64 : fmt == FMT_Q4 ? 128 : 32;
   const int nsteps = a.K / ks;
   auto batches = [&](int w) { return ((nsteps + w - 1) / w + kSPB - 1) / kSPB; };
   static int nw_env = -1;

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(MoeArgs a) {
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;
     wrow[r] = wbase + (size_t)row * rb;
-    drow[r] = (FMT == FMT_Q4) ? sbase + (size_t)row * (K >> 5) : nullptr;
+    drow[r] = has_block_scales<FMT>() ? sbase + (size_t)row * (K >> 5) : nullptr;
   }
   const int nchunks = K / Fmt<FMT>::kWeightsPerChunk;
   const int rr = reduced_row_of_lane<R>(lane);
@@ -209,18 +209,19 @@ static moe_fn pick_moe(int R) {
 }
 
 static int moe_launch(int fmt, MoeArgs& a, int E, int R, hipStream_t stream, const char* what) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 2, "%s: unknown weight format %d", what, fmt);
-  const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : 8;
+  AFX_REQUIRE(fmt >= 0 && fmt <= 3, "%s: unknown weight format %d", what, fmt);
+  const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : fmt == FMT_BW ? 64 : 8;
   AFX_REQUIRE(a.K % kq == 0, "%s: K=%d must be a multiple of %d", what, a.K, kq);
   AFX_REQUIRE(a.w && a.x && a.y && a.cnt && a.list, "%s: null pointer", what);
   AFX_REQUIRE(fmt == FMT_F16 || a.scale, "%s: quantized weights need scales", what);
-  moe_fn fn = fmt == FMT_I8 ? pick_moe<FMT_I8>(R) : fmt == FMT_Q4 ? pick_moe<FMT_Q4>(R) : pick_moe<FMT_F16>(R);
+  moe_fn fn = fmt == FMT_I8 ? pick_moe<FMT_I8>(R) : fmt == FMT_Q4 ? pick_moe<FMT_Q4>(R)
+            : fmt == FMT_BW ? pick_moe<FMT_BW>(R) : pick_moe<FMT_F16>(R);
   const int gx = (a.N + 4 * R - 1) / (4 * R);
   hipLaunchKernelGGL(fn, dim3(gx, E), dim3(256), 0, stream, a);
   return check_launch(what);
 }
 
-static long long fmt_row_bytes(int fmt, int K) { return fmt == FMT_I8 ? K : fmt == FMT_Q4 ? K / 2 : 2LL * K; }
+static long long fmt_row_bytes(int fmt, int K) { return fmt == FMT_I8 || fmt == FMT_BW ? K : fmt == FMT_Q4 ? K / 2 : 2LL * K; }
 
 }  // namespace afx
 
@@ -250,7 +251,7 @@ int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int
     m.w = w; m.scale = (const half_t*)scale; m.x = (const half_t*)x; m.ldx = D; m.y = act; m.ldy = F;
     m.cnt = cnt; m.list = list; m.T = T; m.k = k; m.x_by_token = 1; m.N = 2 * F; m.K = D; m.epi = EPI_SWIGLU;
     m.w_es = fmt_row_bytes(fmt, D) * 2 * F;
-    m.s_es = fmt == FMT_Q4 ? 2LL * F * (D / 32) : fmt == FMT_I8 ? 2LL * F : 0;
+    m.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? 2LL * F * (D / 32) : fmt == FMT_I8 ? 2LL * F : 0;
     AFX_REQUIRE(T >= 1 && k >= 1 && E >= 1, "afx_moe_gateup: bad sizes");
     return mfma_launch(fmt, m, E, (hipStream_t)stream, "afx_moe_gateup");
   }
@@ -258,7 +259,7 @@ int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int
   a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)x; a.ldx = D; a.y = act; a.ldy = F;
   a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = 2 * F; a.K = D; a.epi = 1; a.x_by_token = 1;
   a.w_es = fmt_row_bytes(fmt, D) * 2 * F;
-  a.s_es = fmt == FMT_Q4 ? 2LL * F * (D / 32) : 2LL * F;
+  a.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? 2LL * F * (D / 32) : 2LL * F;
   const int R = rows_hint == 1 || rows_hint == 2 || rows_hint == 4 ? (rows_hint < 2 ? 2 : rows_hint) : 4;
   return moe_launch(fmt, a, E, R, (hipStream_t)stream, "afx_moe_gateup");
 }
@@ -271,7 +272,7 @@ int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int
     m.w = w; m.scale = (const half_t*)scale; m.x = (const half_t*)act; m.ldx = F; m.y = y; m.ldy = D;
     m.cnt = cnt; m.list = list; m.T = T; m.k = k; m.x_by_token = 0; m.N = D; m.K = F; m.epi = EPI_F32;
     m.w_es = fmt_row_bytes(fmt, F) * D;
-    m.s_es = fmt == FMT_Q4 ? (long long)D * (F / 32) : fmt == FMT_I8 ? (long long)D : 0;
+    m.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? (long long)D * (F / 32) : fmt == FMT_I8 ? (long long)D : 0;
     AFX_REQUIRE(T >= 1 && k >= 1 && E >= 1, "afx_moe_down: bad sizes");
     return mfma_launch(fmt, m, E, (hipStream_t)stream, "afx_moe_down");
   }
@@ -279,7 +280,7 @@ int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int
   a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)act; a.ldx = F; a.y = y; a.ldy = D;
   a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = D; a.K = F; a.epi = 0; a.x_by_token = 0;
   a.w_es = fmt_row_bytes(fmt, F) * D;
-  a.s_es = fmt == FMT_Q4 ? (long long)D * (F / 32) : (long long)D;
+  a.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? (long long)D * (F / 32) : (long long)D;
   const int R = rows_hint == 1 || rows_hint == 2 || rows_hint == 4 ? rows_hint : 4;
   return moe_launch(fmt, a, E, R, (hipStream_t)stream, "afx_moe_down");
 }

@@ -51,10 +51,13 @@ int afx_event_destroy(void* ev);
 
 /* ---- weight-streaming linear layers --------------------------------------------------- */
 
-/* y[M][N] = x[M][K] @ W^T (+bias) (+residual, may alias y); M <= 8; out_f32 selects fp32 y.
- * Replaces the compress="int8" linear: constexpr_affine_dequantize(axis=0) + matmul
- * (aneforge/_compile.py:171-179, 375-385; aneforge/graph.py:187-195), the fp16 weight path,
- * and the GGUF Q4_0 weights the reference dequantises on the host (aneforge/_gguf.py:34-39). */
+/* y[M][N] = x[M][K] @ W^T (+bias) (+residual, may alias y); out_f32 selects fp32 y.  Any M:
+ * 4+ rows without a norm prologue run on MFMA, otherwise the vector kernels take 8 rows a launch.
+ * fmt 0: the compress="int8" linear, constexpr_affine_dequantize(axis=0) + matmul
+ * (aneforge/_compile.py:171-179, 375-385; aneforge/graph.py:187-195); 1: the GGUF Q4_0 weights
+ * the reference dequantises on the host (aneforge/_gguf.py:34-39); 2: fp16; 3: compress=
+ * "blockwise" with 32-weight blocks, int8 codes + fp16 scale[N][K/32], weight fp16(q * s)
+ * (aneforge/_blob.py:46-56, constexpr_blockwise_shift_scale in aneforge/_compile.py:112-188). */
 int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                int M, int N, int K, const void* bias, const void* residual, int out_f32,
                int rows_hint, void* stream);
@@ -84,7 +87,7 @@ int afx_qkv_rope_kv(int fmt, const void* w, const void* scale, const void* h, in
 int afx_q4_0_repack(const void* blocks, void* qs, void* d, int N, int K, void* stream);
 int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, void* stream);
 /* Dequantise through the GEMV's own unpack path into fp32 (bit-exact check of
- * quantize_per_row / Q4_0 reconstruction, aneforge/_blob.py:20-25). */
+ * quantize_per_row / Q4_0 / quantize_blockwise reconstruction, aneforge/_blob.py:20-25, 46-56). */
 int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream);
 
 /* ---- attention -------------------------------------------------------------------------- */
@@ -161,7 +164,8 @@ int afx_moe_combine(const void* h, const float* y, const float* gate, const void
 
 /* Y = epilogue(X @ W^T) for M prompt rows on MFMA: the linears of the reference's batched
  * prefill (_prefiller, aneforge/llm.py:149-168, 489-544) with the compress="int8" weights of
- * aneforge/_compile.py:171-179 / 375-385 (fmt 0) or fp16 (fmt 2).  epi: 0 fp16, 1 fp16 +
+ * aneforge/_compile.py:171-179 / 375-385 (fmt 0), fp16 (fmt 2) or compress="blockwise" (fmt 3,
+ * 32-weight blocks, aneforge/_blob.py:46-56).  epi: 0 fp16, 1 fp16 +
  * residual, 2 fp32, 3 SwiGLU over interleaved gate/up rows (aneforge/llm.py:171-175). */
 int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy, int M, int N,
              int K, const void* bias, const void* residual, int epi, void* stream);

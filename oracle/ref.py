@@ -16,6 +16,7 @@ Pinning status (see tests/test_oracle.py):
   q4_0 pack/unpack/dequant, quantize     pinned: ggml spec KATs + brute-force loop
   dequant_q4_0_f16                      pinned: KAT (fp16 rounding of the fp32 product)
   quantize_blockwise                    pinned: closed form + reference property tests
+  dequant_blockwise                     pinned: KAT (an fp16 round-half-even tie of the product)
   rms_norm                              pinned: torch + invariants
   rope_tables / rope / llama3 scaling    pinned: transformers' rope utilities + HF formula
   attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
@@ -65,6 +66,16 @@ def quantize_blockwise(W, block_size=32):
     s = np.maximum(np.abs(Wb).max(axis=2) / np.float32(127.0), np.float32(1e-8))
     q = np.clip(np.round(Wb / s[:, :, None]), -127, 127).astype(np.int8).reshape(OUT, IN)
     return q, s.astype(f16), bs
+
+
+def dequant_blockwise(q, s, bs=32):
+    """The blockwise reconstruction data * scale (aneforge/_blob.py:46-56 docstring,
+    constexpr_blockwise_shift_scale in aneforge/_compile.py:112-188) as fp16 weights: each
+    int8 x fp16 product is exact in fp32 and rounded once to fp16."""
+    q = np.asarray(q, np.int8)
+    N, K = q.shape
+    p = q.reshape(N, K // bs, bs).astype(np.float32) * np.asarray(s, f16).astype(np.float32)[:, :, None]
+    return p.astype(f16).astype(np.float32).reshape(N, K)
 
 
 # ----------------------------------------------------------------------------- Q4_0 codec

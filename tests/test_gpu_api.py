@@ -197,12 +197,13 @@ def _oracle_weights(cfg, w, enc):
     return ow, ocfg
 
 
-@pytest.mark.parametrize("compress,qk", [(None, False), ("int8", True), ("q4_0", False)])
+@pytest.mark.parametrize("compress,qk", [(None, False), ("int8", True), ("q4_0", False), ("blockwise", False)])
 def test_moe_decoder_generate_matches_oracle(compress, qk):
     say(f"LlamaPrefill with MoE layers compress={compress} qk_norm={qk}")
     cfg, w = _moe_model(qk=qk)
     enc = {None: lambda W: np.asarray(W, np.float32).astype(np.float16).astype(np.float32),
            "int8": lambda W: ref.dequant_w8(*ref.quantize_per_row(W)),
+           "blockwise": lambda W: ref.dequant_blockwise(*ref.quantize_blockwise(W, 32)),
            "q4_0": lambda W: ref.dequant_q4_0(ref.quantize_q4_0(W), *np.asarray(W).shape)}[compress]
     m = af.LlamaPrefill(cfg, w, compress=compress)
     prompt = [3, 9, 27, 1]

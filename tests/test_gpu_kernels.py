@@ -70,6 +70,31 @@ def test_linear_int8(K, M, N, Kd):
     check_f16(got, want, what="int8 linear")
 
 
+def _bw(N, Kd, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-127, 128, (N, Kd), dtype=np.int8)
+    s = (np.abs(rng.normal(0, 0.02, (N, Kd // 32))) / 127 + 1e-5).astype(np.float16)
+    return q, s
+
+
+def test_dequant_blockwise_bit_exact(K):
+    say("dequant blockwise [300, 4096]")
+    q, s = _bw(300, 4096, 12)
+    got = host(K.dequant("blockwise", dev(q), dev(s), 300, 4096))
+    assert np.array_equal(got.view(np.uint32), ref.dequant_blockwise(q, s).view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 4096, 4096), (1, 4096, 11008), (3, 1000, 1024), (1, 777, 4160),
+                                    (6, 777, 4160), (8, 1024, 4096), (20, 1000, 1024), (12, 778, 1088)])
+def test_linear_blockwise(K, M, N, Kd):
+    # fast path (M = 1, K 4096 / 11008), generic vector path, MFMA (M >= 4, N % 4 == 0), 8-row chunks
+    say(f"linear blockwise M={M} N={N} K={Kd}")
+    q, s = _bw(N, Kd, 60 + M)
+    x = np.random.default_rng(61).standard_normal((M, Kd)).astype(np.float16)
+    got = host(K.linear("blockwise", dev(q), dev(s), dev(x)))
+    check_f16(got, ref.linear(x, ref.dequant_blockwise(q, s)), what="blockwise linear")
+
+
 def test_linear_int8_cfg0_seeded(K):
     say("linear int8 cfg0 (seeded 4096x4096)")
     from aneforge_amd import workloads

@@ -40,6 +40,9 @@ def _effective(w, compress):
             return ref.dequant_w8(*_blob.quantize_per_row(W))
         if compress == "q4_0":
             return ref.dequant_q4_0(_blob.quantize_q4_0(W), *W.shape)
+        if compress == "blockwise":
+            q, sc, bs = _blob.quantize_blockwise(W, 32)
+            return ref.dequant_blockwise(q, sc, bs)
         raise ValueError(compress)
 
     out = {"embed": np.asarray(w["embed"], np.float32).astype(np.float16).astype(np.float32),
@@ -72,7 +75,7 @@ def _assert_tokens_match(got, want, logits, what, rel_gap=2e-3):
     assert len(got) == len(want), f"{what}: {len(got)} tokens vs {len(want)}"
 
 
-@pytest.mark.parametrize("compress", [None, "int8", "q4_0"])
+@pytest.mark.parametrize("compress", [None, "int8", "q4_0", "blockwise"])
 def test_generate_matches_oracle(compress):
     from aneforge_amd.llm import LlamaConfig, LlamaPrefill
     say(f"LlamaPrefill.generate vs oracle compress={compress}")
@@ -179,7 +182,7 @@ def test_prefill_matches_huggingface_llama():
     assert cosine(got, want) > 0.999 and int(np.argmax(got)) == int(np.argmax(want))
 
 
-@pytest.mark.parametrize("compress,chunk", [("int8", 2048), ("int8", 48), (None, 2048)])
+@pytest.mark.parametrize("compress,chunk", [("int8", 2048), ("int8", 48), (None, 2048), ("blockwise", 2048)])
 def test_batched_prefill_matches_forced_steps_and_oracle(compress, chunk):
     """The MFMA batched prefill (head dim 128) leaves the same cache and state as the
     token-by-token forced steps, and generation from it matches the oracle."""

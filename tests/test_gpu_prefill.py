@@ -17,11 +17,15 @@ def _weights(fmt, N, K, rng):
         q = rng.integers(-127, 128, (N, K), dtype=np.int8)
         s = (np.abs(rng.normal(0, 0.02, N)) / 127).astype(np.float16)
         return dev(q), dev(s), ref.dequant_w8(q, s)
+    if fmt == "blockwise":
+        q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        s = (np.abs(rng.normal(0, 0.02, (N, K // 32))) / 127 + 1e-5).astype(np.float16)
+        return dev(q), dev(s), ref.dequant_blockwise(q, s)
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
     return dev(w), None, w.astype(np.float32)
 
 
-@pytest.mark.parametrize("fmt", ["int8", "fp16"])
+@pytest.mark.parametrize("fmt", ["int8", "fp16", "blockwise"])
 @pytest.mark.parametrize("M,N,K", [(1, 256, 128), (70, 384, 320), (300, 256, 640)])
 @pytest.mark.parametrize("epi", ["f16", "resid", "f32", "swiglu"])
 def test_gemm_matches_oracle(fmt, M, N, K, epi):

@@ -60,6 +60,19 @@ def test_quantize_blockwise_matches_reference_properties():
     assert bs2 == 30                                                   # clamps to a divisor of IN
 
 
+def test_dequant_blockwise_known_answer():
+    # 3 x fp16(0.1) = 3 x 0.0999755859375 = 0.2999267578125 = 1228.5 fp16 ulps (2^-12):
+    # round-half-even -> 1228 ulps = 0.2998046875; -127 x 2^-7 = -0.9921875 exact; the second
+    # block's scale (2.0) must not leak into the first block
+    q = np.zeros((1, 64), np.int8)
+    q[0, 0], q[0, 1], q[0, 32] = 3, -127, 5
+    w = ref.dequant_blockwise(q, np.array([[0.1, 2.0]], np.float16), 32)
+    assert w[0, 0] == np.float32(0.2998046875)
+    assert w[0, 32] == np.float32(10.0) and w[0, 2] == 0.0 and w[0, 63] == 0.0
+    w2 = ref.dequant_blockwise(q, np.array([[2.0 ** -7, 2.0]], np.float16), 32)
+    assert w2[0, 1] == np.float32(-0.9921875)
+
+
 # ----------------------------------------------------------------------------- Q4_0
 def test_q4_0_known_answer_blocks():
     # d = 1.0, qs all 0x80 -> low nibble 0 -> -8 for elements 0..15, high nibble 8 -> 0 for 16..31

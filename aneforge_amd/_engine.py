@@ -175,6 +175,26 @@ def pack_encoded(fmt, w, s, bias=None) -> Linear:
                   None if bias is None else _to_dev(np.asarray(bias, np.float32).astype(F16)))
 
 
+_GEMM_FMTS = ("int8", "fp16")                    # formats the prefill GEMM reads as packed
+
+
+def prefill_gemm(eng, lin: "Linear", x, y, residual=None, epi="f16"):
+    """The batched prefill's linear: afx_gemm on the packed weights (int8, fp16), or on the fp16
+    expansion of the others in the engine's weight scratch (Q4_0, blockwise).  Prefill is
+    compute-bound, so one expansion per matrix per prompt chunk costs little; for blockwise it
+    measured faster than scaling the codes inside the GEMM (40.7 vs 48.2 ms for the 2048-token
+    cfg3 prompt: the in-GEMM products lengthen its LDS-bound fragment path)."""
+    if lin.fmt in _GEMM_FMTS:
+        return K.gemm(lin.fmt, lin.w, lin.scale, x, y=y, bias=lin.bias, residual=residual, epi=epi)
+    w16 = eng.weight_scratch(lin.N * lin.K).view(lin.N, lin.K)
+    K.dequant_f16(lin.fmt, lin.w, lin.scale, lin.N, lin.K, out=w16)
+    return K.gemm("fp16", w16, None, x, y=y, bias=lin.bias, residual=residual, epi=epi)
+
+
+def _prefill_fmt_ok(lin: "Linear") -> bool:
+    return lin.fmt in ("int8", "fp16", "q4_0", "blockwise") and lin.K % 64 == 0 and lin.N % 16 == 0
+
+
 def pack_linear(W, compress, bias=None) -> Linear:
     fmt, w, s = encode(W, compress)
     N, Kd = _shape(W)
@@ -265,9 +285,7 @@ class AttentionDecode:
                  residual=eng.h)
 
     def prefill_supported(self) -> bool:
-        lin = (self.qkv, self.wo)
-        return (self.dh == 128 and all(l.fmt in ("int8", "fp16", "blockwise") for l in lin)
-                and all(l.K % 64 == 0 and l.N % 16 == 0 for l in lin))
+        return self.dh == 128 and all(_prefill_fmt_ok(l) for l in (self.qkv, self.wo))
 
     def prefill(self, eng, X, pos0: int, bufs: dict):
         """Prompt rows X [m, D] at positions pos0.. (in place): RMSNorm -> [q|k|v] GEMM -> RoPE +
@@ -276,7 +294,7 @@ class AttentionDecode:
         hn = bufs["hn"][:m]
         K.rmsnorm(X, self.norm, self.eps, y=hn)
         qkv = bufs["qkv"][:m, :self.qkv.N]
-        K.gemm(self.qkv.fmt, self.qkv.w, self.qkv.scale, hn, y=qkv, bias=self.qkv.bias)
+        prefill_gemm(eng, self.qkv, hn, qkv)
         q = bufs["q"][:m, :H * dh]
         K.qkv_split_rope(qkv, H * dh, KV * dh, dh, eng.cos, eng.sin, pos0, q, self.kc[0], self.vc[0],
                          rope=self.rope and not self.qk_norm)
@@ -288,7 +306,7 @@ class AttentionDecode:
                              head_stride=self.kc.stride(1), pos_mul=dh, kv_len=eng.M, M=m, rope=self.rope)
         a = bufs["a"][:m, :H * dh]
         K.prefill_attn(q, self.kc[0], self.vc[0], a, pos0, H, KV)
-        K.gemm(self.wo.fmt, self.wo.w, self.wo.scale, a, y=X, residual=X, bias=self.wo.bias, epi="resid")
+        prefill_gemm(eng, self.wo, a, X, residual=X, epi="resid")
 
     @property
     def nbytes(self):
@@ -328,8 +346,7 @@ class SwiGLUDecode:
         K.linear(self.down.fmt, self.down.w, self.down.scale, act, y=eng.h, residual=eng.h)
 
     def prefill_supported(self) -> bool:
-        lin = (self.gu, self.down)
-        return all(l.fmt in ("int8", "fp16", "blockwise") and l.K % 64 == 0 and l.N % 16 == 0 for l in lin)
+        return all(_prefill_fmt_ok(l) for l in (self.gu, self.down))
 
     def prefill(self, eng, X, pos0: int, bufs: dict):
         """Prompt rows X [m, D] in place: RMSNorm -> gate/up GEMM + SwiGLU -> down GEMM + residual."""
@@ -337,8 +354,8 @@ class SwiGLUDecode:
         hn = bufs["hn"][:m]
         K.rmsnorm(X, self.norm, self.eps, y=hn)
         act = bufs["act"][:m, :self.F]
-        K.gemm(self.gu.fmt, self.gu.w, self.gu.scale, hn, y=act, epi="swiglu")
-        K.gemm(self.down.fmt, self.down.w, self.down.scale, act, y=X, residual=X, epi="resid")
+        prefill_gemm(eng, self.gu, hn, act, epi="swiglu")
+        prefill_gemm(eng, self.down, act, X, residual=X, epi="resid")
 
     @property
     def nbytes(self):
@@ -445,6 +462,13 @@ class DecodeEngine:
     def prefill_supported(self) -> bool:
         return all(getattr(m, "prefill_supported", lambda: False)() and getattr(p, "prefill_supported", lambda: False)()
                    for m, p in self.layers)
+
+    def weight_scratch(self, n: int) -> torch.Tensor:
+        """An fp16 buffer of at least n elements for prefill_gemm's weight expansion (reused by every
+        layer in stream order)."""
+        if getattr(self, "_w16", None) is None or self._w16.numel() < n:
+            self._w16 = torch.empty(n, dtype=torch.float16, device="cuda")
+        return self._w16[:n]
 
     def _prefill_buffers(self, C: int) -> dict:
         if getattr(self, "_pf", None) is None or self._pf["x"].shape[0] < C:

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "afx_q4_0_repack": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "afx_q4_0_unpack": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "afx_dequant": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp]),
+    "afx_dequant_f16": (_i, [_i, _vp, _vp, _vp, _ll, _i, _i, _vp]),
     # attention
     "afx_decode_attn_ws_bytes": (_ll, [_i, _i, _i, _i, _i, _i]),
     "afx_decode_attn": (_i, [_vp, _vp, _vp, _vp, _ll, _ll, _ll, _ll, _i, _i, _i, _i, _i, _vp, _i, _vp, _ll,

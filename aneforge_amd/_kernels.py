@@ -113,6 +113,15 @@ def q4_unpack(qs, d, N, K):
     return out
 
 
+def dequant_f16(fmt, w, scale, N, K, out=None):
+    """Weights as fp16 [N, K] (row stride out.stride(0)): the values the kernels multiply with."""
+    _dev(w, scale)
+    if out is None:
+        out = torch.empty((N, K), dtype=torch.float16, device=w.device)
+    _hip.call("afx_dequant_f16", FMT[fmt], P(w), P(scale), P(out), out.stride(0), N, K, stream())
+    return out
+
+
 def dequant(fmt, w, scale, N, K):
     out = torch.empty((N, K), dtype=torch.float32, device=w.device)
     _hip.call("afx_dequant", FMT[fmt], P(w), P(scale), P(out), N, K, stream())

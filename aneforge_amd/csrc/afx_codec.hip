@@ -12,7 +12,7 @@
 // (see q4_word_to_h2).  A 16-byte load at offset 16g of a superblock therefore yields word g
 // of four consecutive blocks - exactly one MFMA B-operand slot per block, and 32 weights for
 // the dot2 GEMV.  Block scales stay row-major: d[row][K/32].
-#include "afx_common.h"
+#include "afx_gemv_core.h"
 
 namespace afx {
 
@@ -122,6 +122,38 @@ __global__ void dequant_q4_kernel(const uint32_t* __restrict__ qs, const half_t*
   }
 }
 
+// Weights as fp16 rows out[n * ldo + k], the values the GEMV / MFMA kernels multiply with:
+// int8 fp16(q * s[n]); Q4_0 fp16((nibble - 8) * d) (the reference's GGUF fp16 weights);
+// blockwise fp16(q * s[n][k / 32]).  One thread per 8 weights, one 16-byte store.
+template <int FMT>
+__global__ void dequant_f16_kernel(const void* __restrict__ w, const half_t* __restrict__ s,
+                                   half_t* __restrict__ out, long long ldo, int N, int K) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per = K >> 3;
+  if (i >= (long long)N * per) return;
+  const int row = (int)(i / per), c = (int)(i - (long long)row * per);
+  h2 v[4];
+  int k0;
+  half_t sc;
+  if constexpr (FMT == FMT_Q4) {
+    // superblock word c: elements 8g .. 8g + 7 of block 4 * (c / 16) + c % 4, g = (c / 4) % 4
+    const int blk = 4 * (c >> 4) + (c & 3);
+    k0 = 32 * blk + 8 * ((c >> 2) & 3);
+    q4_word_to_h2(((const uint32_t*)w)[i], v);
+    sc = s[(size_t)row * (K >> 5) + blk];
+  } else {
+    const u2 q = ((const u2*)w)[i];
+    i8x4_to_h2(q.x, v[0], v[1]);
+    i8x4_to_h2(q.y, v[2], v[3]);
+    k0 = 8 * c;
+    sc = FMT == FMT_BW ? s[(size_t)row * (K >> 5) + (k0 >> 5)] : s[row];
+  }
+  const h2 s2 = {sc, sc};
+  u4 o;
+  o.x = as_u32(v[0] * s2); o.y = as_u32(v[1] * s2); o.z = as_u32(v[2] * s2); o.w = as_u32(v[3] * s2);
+  *(u4*)(out + (size_t)row * ldo + k0) = o;
+}
+
 }  // namespace afx
 
 using namespace afx;
@@ -149,6 +181,29 @@ int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, v
 }
 
 // Dequantise through the GEMV unpack path: fmt 0 = int8 [N][K] + s[N]; fmt 1 = Q4_0 superblock.
+// fmt 0 int8, 1 Q4_0 (superblock layout), 3 blockwise -> fp16 rows of stride ldo (elements).
+int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,
+                    void* stream) {
+  AFX_REQUIRE(w && scale && out, "afx_dequant_f16: null pointer");
+  AFX_REQUIRE(fmt == 0 || fmt == 1 || fmt == 3, "afx_dequant_f16: format %d has no scales to apply", fmt);
+  const int kq = fmt == 1 ? 128 : fmt == 3 ? 32 : 8;
+  AFX_REQUIRE(N >= 1 && K >= kq && K % kq == 0, "afx_dequant_f16: K=%d must be a multiple of %d", K, kq);
+  AFX_REQUIRE(ldo >= K && ldo % 8 == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)w & 7) == 0,
+              "afx_dequant_f16: out rows must be 16-byte aligned (ldo %% 8 == 0) and ldo >= K");
+  const long long n8 = (long long)N * (K / 8);
+  const dim3 grid((unsigned)((n8 + 255) / 256));
+  if (fmt == 0)
+    hipLaunchKernelGGL(dequant_f16_kernel<FMT_I8>, grid, dim3(256), 0, (hipStream_t)stream, w,
+                       (const half_t*)scale, (half_t*)out, ldo, N, K);
+  else if (fmt == 1)
+    hipLaunchKernelGGL(dequant_f16_kernel<FMT_Q4>, grid, dim3(256), 0, (hipStream_t)stream, w,
+                       (const half_t*)scale, (half_t*)out, ldo, N, K);
+  else
+    hipLaunchKernelGGL(dequant_f16_kernel<FMT_BW>, grid, dim3(256), 0, (hipStream_t)stream, w,
+                       (const half_t*)scale, (half_t*)out, ldo, N, K);
+  return check_launch("afx_dequant_f16");
+}
+
 int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream) {
   AFX_REQUIRE(w && scale && out, "afx_dequant: null pointer");
   if (fmt == 0) {

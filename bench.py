@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--rows-hint", type=int, default=0)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--weights", default="int8", choices=["int8", "q4_0", "blockwise"],
+                    help="linear weight format of the cfg3 model for --workload prefill")
     return ap.parse_args()
 
 
@@ -275,7 +277,7 @@ def cfg3_token_bytes(pos: int) -> int:
     return L * (per_layer_w + per_layer_s + per_layer_g) + V * D * 2 + 2 * D + kv
 
 
-def build_cfg3_engine(steps: int, warmup: int):
+def build_cfg3_engine(steps: int, warmup: int, fmt: str = "int8"):
     import torch
     from aneforge_amd import _engine as E
     from aneforge_amd.llm import LlamaConfig
@@ -287,7 +289,14 @@ def build_cfg3_engine(steps: int, warmup: int):
     g = torch.Generator(device="cuda").manual_seed(3)
 
     def i8(N, Kd):
+        if fmt == "q4_0":                       # random codes in the superblock layout + block scales
+            q = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
+            d = (torch.rand((N, Kd // 32), device="cuda", generator=g) * 0.005).half()
+            return E.Linear("q4_0", q, d, N, Kd)
         q = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
+        if fmt == "blockwise":
+            s = (torch.rand((N, Kd // 32), device="cuda", generator=g) * (0.02 / 127)).half()
+            return E.Linear("blockwise", q, s, N, Kd)
         s = (torch.randn(N, device="cuda", generator=g).abs() * (0.02 / 127)).half()
         return E.Linear("int8", q, s, N, Kd)
 
@@ -389,8 +398,8 @@ def bench_prefill(args):
     import torch
     from aneforge_amd import _hip
     P = int(args.ctx)
-    log(f"building cfg3 engine (32 layers int8) for a {P}-token batched prefill")
-    cfg, eng, layers = build_cfg3_engine(P, 0)
+    log(f"building cfg3 engine (32 layers {args.weights}) for a {P}-token batched prefill")
+    cfg, eng, layers = build_cfg3_engine(P, 0, args.weights)
     prompt = [int(t) for t in np.random.default_rng(5).integers(0, CFG3["vocab"], P + 1)]
     for _ in range(max(1, args.warmup)):
         eng.prefill(prompt)
@@ -410,7 +419,7 @@ def bench_prefill(args):
     D, F, H, KV, dh = CFG3["dim"], CFG3["ffn_dim"], CFG3["n_heads"], CFG3["n_kv_heads"], 128
     lin = D * (H * dh + 2 * KV * dh) + H * dh * D + 2 * F * D + F * D
     flops = 2.0 * CFG3["n_layers"] * P * (lin + 2 * H * dh * (P + 1) / 2.0)
-    return {"workload": f"cfg3 batched prefill, {P}-token prompt, 32 layers int8 (MFMA GEMM + causal flash attention)",
+    return {"workload": f"cfg3 batched prefill, {P}-token prompt, 32 layers {args.weights} (MFMA GEMM + causal flash attention)",
             "prompt_tokens": P, "ms": per, "tokens_per_s": P / (per * 1e-3), "TFLOPs": flops / (per * 1e-3) / 1e12,
             "mfma_peak_TFLOPs_fp16": 2500.0}
 

@@ -89,6 +89,11 @@ int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, v
 /* Dequantise through the GEMV's own unpack path into fp32 (bit-exact check of
  * quantize_per_row / Q4_0 / quantize_blockwise reconstruction, aneforge/_blob.py:20-25, 46-56). */
 int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream);
+/* The same weights as fp16 rows out[n * ldo + k] (fmt 0 int8, 1 Q4_0, 3 blockwise): the fp16 values the
+ * reference multiplies with -- for Q4_0 the fp16 cast of GGUFView.get (aneforge/_gguf.py:34-39).  The
+ * batched prefill expands formats its GEMM does not read (Q4_0) into fp16 this way, one matrix at a time. */
+int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,
+                    void* stream);
 
 /* ---- attention -------------------------------------------------------------------------- */
 

@@ -84,6 +84,30 @@ def test_dequant_blockwise_bit_exact(K):
     assert np.array_equal(got.view(np.uint32), ref.dequant_blockwise(q, s).view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt", ["int8", "q4_0", "blockwise"])
+def test_dequant_f16_bit_exact(K, fmt):
+    # the fp16 weights the batched prefill expands a matrix to (rows of a wider scratch buffer)
+    say(f"dequant_f16 {fmt} [72, 1024]")
+    from aneforge_amd import _blob
+    N, Kd = 72, 1024
+    rng = np.random.default_rng(13)
+    if fmt == "int8":
+        q, s = _w8(N, Kd, 14)
+        want = (q.astype(np.float32) * s.astype(np.float32)[:, None]).astype(np.float16)
+    elif fmt == "blockwise":
+        q, s = _bw(N, Kd, 14)
+        want = ref.dequant_blockwise(q, s).astype(np.float16)
+    else:
+        blocks = ref.quantize_q4_0(rng.standard_normal((N, Kd)).astype(np.float32) * 0.05)
+        q, s = _blob.q4_0_to_superblock(blocks, N, Kd)
+        want = ref.dequant_q4_0_f16(blocks, N, Kd).astype(np.float16)
+    out = torch.full((N, Kd + 64), 7.0, dtype=torch.float16, device="cuda")
+    K.dequant_f16(fmt, dev(q), dev(s), N, Kd, out=out[:, :Kd])
+    got = host(out)
+    assert np.array_equal(got[:, :Kd].view(np.uint16), want.view(np.uint16))
+    assert (got[:, Kd:] == 7.0).all()                    # the padding columns are untouched
+
+
 @pytest.mark.parametrize("M,N,Kd", [(1, 4096, 4096), (1, 4096, 11008), (3, 1000, 1024), (1, 777, 4160),
                                     (6, 777, 4160), (8, 1024, 4096), (20, 1000, 1024), (12, 778, 1088)])
 def test_linear_blockwise(K, M, N, Kd):

@@ -182,7 +182,8 @@ def test_prefill_matches_huggingface_llama():
     assert cosine(got, want) > 0.999 and int(np.argmax(got)) == int(np.argmax(want))
 
 
-@pytest.mark.parametrize("compress,chunk", [("int8", 2048), ("int8", 48), (None, 2048), ("blockwise", 2048)])
+@pytest.mark.parametrize("compress,chunk", [("int8", 2048), ("int8", 48), (None, 2048), ("blockwise", 2048),
+                                            ("q4_0", 2048), ("q4_0", 48)])
 def test_batched_prefill_matches_forced_steps_and_oracle(compress, chunk):
     """The MFMA batched prefill (head dim 128) leaves the same cache and state as the
     token-by-token forced steps, and generation from it matches the oracle."""

@@ -56,11 +56,12 @@ class Linear:
 
 @dataclass
 class QuantizedWeight:
-    """Weights that arrive already encoded (GGUF Q4_0 bytes, int8 codes + row scales): packing
-    keeps the codes bit-for-bit instead of round-tripping through float.
+    """Weights that arrive already encoded (GGUF Q4_0 / Q8_0 bytes, int8 codes + row scales):
+    packing keeps the codes bit-for-bit instead of round-tripping through float.
       fmt "int8":      codes int8 [N, K], scale fp16 [N]
       fmt "q4_0":      codes uint8 [N, K/2] superblock layout, scale fp16 [N, K/32]
-      fmt "q4_0_gguf": codes uint8 [N, K/32*18] GGUF block bytes, scale None"""
+      fmt "q4_0_gguf": codes uint8 [N, K/32*18] GGUF block bytes, scale None
+      fmt "blockwise": codes int8 [N, K], scale fp16 [N, K/32] (GGUF Q8_0 blocks, K % 64 == 0)"""
     fmt: str
     codes: np.ndarray
     scale: np.ndarray | None
@@ -82,6 +83,9 @@ class QuantizedWeight:
         N, Kd = self.shape
         if self.fmt == "int8":
             return self.codes.astype(np.float32) * self.scale.astype(np.float32)[:, None]
+        if self.fmt == "blockwise":
+            return (self.codes.reshape(N, Kd // 32, 32).astype(np.float32)
+                    * self.scale.astype(np.float32)[:, :, None]).reshape(N, Kd)
         q = self if self.fmt == "q4_0" else self.to_superblock()
         blocks = _blob.superblock_to_q4_0(q.codes, q.scale, N, Kd)
         codes, d = _blob.q4_0_codes(blocks, N, Kd)

@@ -2,8 +2,8 @@
 `gguf` package, aneforge/_gguf.py:10-46, which is not part of this build).
 
 GGUFView keeps the reference's accessors (meta, arch, tn, field, sc, has, get, drop_pages) and
-adds `quantized(name)`, which returns Q4_0 tensors as QuantizedWeight codes instead of
-dequantising them, so the Q4_0 kernels stream the file's own 4-bit codes.
+adds `quantized(name)`, which returns Q4_0 and Q8_0 tensors as QuantizedWeight codes instead of
+dequantising them, so the Q4_0 / blockwise kernels stream the file's own codes.
 
 Format: magic "GGUF", version 3, tensor count, metadata count, metadata key/values, tensor infos
 (name, dims with dims[0] innermost, ggml type, offset), data section aligned to
@@ -349,20 +349,31 @@ class GGUFView:
         return dequantize(self.tn[name]).astype(dtype)
 
     def quantized(self, name: str):
-        """Q4_0 tensors as QuantizedWeight codes: a 2-D tensor -> one QuantizedWeight [rows, K];
-        a 3-D expert stack [E, rows, K] -> a list of E QuantizedWeights.  None for other types."""
+        """Tensors the kernels stream in their file encoding, as QuantizedWeight codes: Q4_0 (the
+        Q4_0 kernels) and Q8_0 with rows of a multiple of 64 (the blockwise kernels: Q8_0's
+        fp16(d * q) is their weight).  A 2-D tensor -> one QuantizedWeight [rows, K]; a 3-D expert
+        stack [E, rows, K] -> a list of E.  None for other types."""
         t = self.tn[name]
-        if t.tensor_type != GGML["Q4_0"]:
-            return None
-        from ._engine import QuantizedWeight
         shape = tuple(reversed(t.shape))
         Kd = shape[-1]
-        raw = np.asarray(t.data).reshape(-1, Kd // 32 * 18)
+        from ._engine import QuantizedWeight
+        if t.tensor_type == GGML["Q4_0"]:
+            raw = np.asarray(t.data).reshape(-1, Kd // 32 * 18)
+            make = lambda r, n: QuantizedWeight("q4_0_gguf", r, None, (n, Kd))
+        elif t.tensor_type == GGML["Q8_0"] and Kd % 64 == 0:
+            b = np.asarray(t.data).reshape(-1, Kd // 32, 34)
+            raw = (np.ascontiguousarray(b[:, :, 2:]).view(np.int8).reshape(-1, Kd),
+                   np.ascontiguousarray(b[:, :, :2]).view(np.float16).reshape(-1, Kd // 32))
+            make = lambda r, n: QuantizedWeight("blockwise", r[0], r[1], (n, Kd))
+        else:
+            return None
         if len(shape) == 2:
-            return QuantizedWeight("q4_0_gguf", raw, None, (shape[0], Kd))
+            return make(raw, shape[0])
         E, rows = shape[0], shape[1]
+        if isinstance(raw, tuple):
+            return [make((raw[0][e * rows:(e + 1) * rows], raw[1][e * rows:(e + 1) * rows]), rows) for e in range(E)]
         raw = raw.reshape(E, rows, -1)
-        return [QuantizedWeight("q4_0_gguf", raw[e], None, (rows, Kd)) for e in range(E)]
+        return [make(raw[e], rows) for e in range(E)]
 
     def drop_pages(self) -> None:
         mm = self.reader._mmap

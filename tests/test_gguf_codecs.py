@@ -233,3 +233,28 @@ def test_unsupported_types_are_named():
         _gguf._nbytes(16, (256,))
     with pytest.raises(NotImplementedError, match="IQ4_NL"):
         _gguf.dequantize_blocks(20, np.zeros(18, np.uint8))
+
+
+def test_q8_0_tensors_stream_as_blockwise_codes(tmp_path):
+    # Q8_0 = fp16 d + 32 int8 codes per block: the kernels' blockwise format (weight fp16(d * q))
+    rng = np.random.default_rng(8)
+    E, rows, K = 3, 4, 128
+    d = rng.uniform(0.001, 0.01, (E * rows, K // 32)).astype(np.float16)
+    q = rng.integers(-127, 128, (E * rows, K), dtype=np.int8)
+    blocks = b"".join(h16(d[r, b]) + q[r, 32 * b:32 * b + 32].tobytes() for r in range(E * rows) for b in range(K // 32))
+    raw = np.frombuffer(blocks, np.uint8).reshape(E * rows, -1)
+    p = str(tmp_path / "q8.gguf")
+    _gguf.write_gguf(p, {"general.architecture": "llama", "llama.block_count": 1},
+                     {"exps": ("Q8_0", raw, (E, rows, K)), "one": ("Q8_0", raw[:rows], (rows, K)),
+                      "odd": ("Q8_0", raw[:rows, :34 * 3], (rows, 96))})
+    g = _gguf.GGUFView(p)
+    experts = g.quantized("exps")
+    assert len(experts) == E
+    for e, w in enumerate(experts):
+        assert w.fmt == "blockwise" and w.shape == (rows, K)
+        np.testing.assert_array_equal(w.codes, q[e * rows:(e + 1) * rows])
+        np.testing.assert_array_equal(w.scale, d[e * rows:(e + 1) * rows])
+        want = _gguf.dequantize_blocks(_gguf.GGML["Q8_0"], raw[e * rows:(e + 1) * rows]).reshape(rows, K)
+        np.testing.assert_array_equal(w.dequant(), want)
+    assert g.quantized("one").fmt == "blockwise"
+    assert g.quantized("odd") is None                 # K = 96: not a multiple of 64, dequantised instead

@@ -333,6 +333,60 @@ def test_load_gguf_k_quant_file(tmp_path):
     _assert_tokens_match(got, want, lgs, "gguf k-quants")
 
 
+def _q8_0_rows(W):
+    """Float rows [n, K] -> GGUF Q8_0 block bytes [n, K/32*34] (d = max|w| / 127 per block)."""
+    W = np.asarray(W, np.float32)
+    n, K = W.shape
+    b = W.reshape(n, K // 32, 32)
+    d = (np.abs(b).max(axis=2) / 127.0).astype(np.float16)
+    q = np.clip(np.rint(b / np.maximum(d.astype(np.float32), 1e-8)[:, :, None]), -127, 127).astype(np.int8)
+    out = np.empty((n, K // 32, 34), np.uint8)
+    out[:, :, :2] = d.view(np.uint8).reshape(n, K // 32, 2)
+    out[:, :, 2:] = q.view(np.uint8)
+    return out.reshape(n, -1)
+
+
+def test_load_gguf_q8_0_experts_stream_as_blockwise(tmp_path):
+    """Q8_0 expert tensors stream as their own int8 codes + block scales (the blockwise kernels),
+    and the decode matches the oracle over fp16(d * q), the reference's GGUFView.get weights."""
+    from aneforge_amd import _gguf
+    say("moe.load_gguf on a synthetic Q8_0-expert GGUF")
+    cfg, w = _moe_model(qk=False, seed=6)
+    E, D, F, L = 8, 128, 128, 2
+    tensors = {"token_embd.weight": w["embed"].astype(np.float16), "output_norm.weight": w["final_norm"],
+               "output.weight": w["lm_head"].astype(np.float16)}
+    dq = lambda raw, n, K: _gguf.dequantize_blocks(_gguf.GGML["Q8_0"], raw).reshape(n, K)
+    for i, lw in enumerate(w["layers"]):
+        b = f"blk.{i}."
+        tensors.update({b + "attn_q.weight": lw["wq"].astype(np.float16), b + "attn_k.weight": lw["wk"].astype(np.float16),
+                        b + "attn_v.weight": lw["wv"].astype(np.float16),
+                        b + "attn_output.weight": lw["wo"].astype(np.float16), b + "attn_norm.weight": lw["attn_norm"],
+                        b + "ffn_norm.weight": lw["mlp_norm"], b + "ffn_gate_inp.weight": lw["router"].astype(np.float16)})
+        for key, nm in (("wgate_exps", "ffn_gate_exps"), ("wup_exps", "ffn_up_exps")):
+            raws = [_q8_0_rows(lw[key][e]) for e in range(E)]
+            tensors[b + nm + ".weight"] = ("Q8_0", np.concatenate(raws), (E, F, D))
+            lw[key] = np.stack([dq(r, F, D) for r in raws])
+        raws = [_q8_0_rows(np.ascontiguousarray(lw["wdown_exps"][e].T)) for e in range(E)]
+        tensors[b + "ffn_down_exps.weight"] = ("Q8_0", np.concatenate(raws), (E, D, F))
+        lw["wdown_exps"] = np.stack([dq(r, D, F).T for r in raws])
+    meta = {"general.architecture": "qwen3moe", "qwen3moe.block_count": L, "qwen3moe.expert_count": E,
+            "qwen3moe.expert_used_count": 2, "qwen3moe.embedding_length": D, "qwen3moe.attention.head_count": 4,
+            "qwen3moe.attention.head_count_kv": 2, "qwen3moe.attention.key_length": 32,
+            "qwen3moe.rope.freq_base": 10000.0, "qwen3moe.attention.layer_norm_rms_epsilon": 1e-5}
+    path = str(tmp_path / "tiny-moe-q8.gguf")
+    _gguf.write_gguf(path, meta, tensors)
+    m = af.moe.load_gguf(path)
+    prompt = [5, 6, 7]
+    got = m.generate(prompt, max_new_tokens=6)
+    mlp = m._layers[0][1]
+    assert mlp.gu.fmt == "blockwise" and mlp.down.fmt == "blockwise"
+    enc16 = lambda W: np.asarray(W, np.float32).astype(np.float16).astype(np.float32)
+    ow, ocfg = _oracle_weights(cfg, w, enc16)
+    want, lgs = ref.generate(prompt, 6, ow, ocfg, M=len(prompt) + 6)
+    from test_gpu_llm import _assert_tokens_match
+    _assert_tokens_match(got, want, lgs, "gguf q8_0")
+
+
 def test_load_gguf_q4_0_experts_stay_4bit(tmp_path):
     """A synthetic Qwen3-MoE GGUF (Q4_0 experts, fp16 elsewhere) written by aneforge_amd._gguf:
     load_gguf streams the file's own codes (bit-identical to the file) and decodes like the oracle."""

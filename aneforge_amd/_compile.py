@@ -12,8 +12,9 @@ Weight encodings (aneforge/_compile.py:112-188): "int8" -> per-output-row int8 s
 int8 GEMV; "int4" (16-entry LUT) and "blockwise" (int8 per block_size-column block) are accepted
 when their relative reconstruction error is <= compress_atol, else they fall back ("int4" -> int8,
 "blockwise" -> fp16) with a warning.  Accepted blockwise weights with 32-column blocks (K % 64 == 0)
-stream their int8 codes and block scales (the kernels form fp16(q * s)); other block sizes and
-int4 stream their exact fp16 reconstruction;
+stream their int8 codes and block scales (the kernels form fp16(q * s)); accepted int4 weights with
+K % 32 == 0 stream their 4-bit indices and codebook (the kernels look up the entry); other shapes
+stream their exact fp16 reconstruction;
 "sparse" is lossless and streams fp16; "auto" takes int8; "q4_0" (this build's addition) uses
 the GGUF Q4_0 GEMV.  bmm_weight int8 keeps the reference's one-scale-per-batch quirk
 (aneforge/_compile.py:117)."""
@@ -77,7 +78,7 @@ def _encode_weight(W, compress, atol, block_size, stats: _Enc, allow_q=True):
         idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
         rec = cb.astype(np.float32)[idx[:, :W.shape[1]]]
         if _rel_err(rec, W) <= atol:
-            return E.pack_linear(rec.astype(F16).astype(np.float32), None)
+            return E.pack_encoded(*E.lut4_encoding(packed, cb, W.shape[1]))
         stats.rejected["int4"] = stats.rejected.get("int4", 0) + 1
         return E.pack_linear(W, "int8")
     if compress == "blockwise":

@@ -36,7 +36,7 @@ F16 = np.float16
 @dataclass
 class Linear:
     """A weight [N, K] resident on the device in one of the kernel formats."""
-    fmt: str                          # "int8" | "q4_0" | "fp16" | "blockwise"
+    fmt: str                          # "int8" | "q4_0" | "fp16" | "blockwise" | "lut4"
     w: torch.Tensor
     scale: torch.Tensor | None
     N: int
@@ -61,7 +61,9 @@ class QuantizedWeight:
       fmt "int8":      codes int8 [N, K], scale fp16 [N]
       fmt "q4_0":      codes uint8 [N, K/2] superblock layout, scale fp16 [N, K/32]
       fmt "q4_0_gguf": codes uint8 [N, K/32*18] GGUF block bytes, scale None
-      fmt "blockwise": codes int8 [N, K], scale fp16 [N, K/32] (GGUF Q8_0 blocks, K % 64 == 0)"""
+      fmt "blockwise": codes int8 [N, K], scale fp16 [N, K/32] (GGUF Q8_0 blocks, K % 64 == 0)
+      fmt "lut4":      codes uint8 [N, K/2] int4 indices (column 2j low nibble), scale fp16 [N, 16]:
+                       each row's codebook, the palettize_lut4 codebook of its source tensor"""
     fmt: str
     codes: np.ndarray
     scale: np.ndarray | None
@@ -86,6 +88,10 @@ class QuantizedWeight:
         if self.fmt == "blockwise":
             return (self.codes.reshape(N, Kd // 32, 32).astype(np.float32)
                     * self.scale.astype(np.float32)[:, :, None]).reshape(N, Kd)
+        if self.fmt == "lut4":
+            idx = np.empty((N, Kd), np.uint8)
+            idx[:, 0::2], idx[:, 1::2] = self.codes & 15, self.codes >> 4
+            return np.take_along_axis(self.scale.astype(np.float32), idx.astype(np.int64), axis=1)
         q = self if self.fmt == "q4_0" else self.to_superblock()
         blocks = _blob.superblock_to_q4_0(q.codes, q.scale, N, Kd)
         codes, d = _blob.q4_0_codes(blocks, N, Kd)
@@ -154,12 +160,33 @@ def encode(W: np.ndarray, compress: str | None):
     if compress == "blockwise":
         return blockwise_encoding(*_blob.quantize_blockwise(W, 32))
     if compress == "int4":
-        packed, cb = _blob.palettize_lut4(W)
-        idx = np.empty((W.shape[0], packed.shape[1] * 2), np.uint8)
-        idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
-        rec = cb.astype(np.float32)[idx[:, :W.shape[1]]]
-        return "fp16", rec.astype(F16), None
+        return lut4_encoding(*_blob.palettize_lut4(W), W.shape[1])
     raise ValueError(f"unknown compress={compress!r}")
+
+
+def lut4_encoding(packed, cb, Kd):
+    """palettize_lut4 output -> (fmt, codes, scale): the kernels' "lut4" format (the indices as
+    they are, the codebook repeated per row) for K % 32 == 0, else the exact fp16 reconstruction."""
+    N = packed.shape[0]
+    if Kd % 32 == 0:
+        return "lut4", np.ascontiguousarray(packed, np.uint8), np.tile(np.asarray(cb, F16).reshape(1, 16), (N, 1))
+    idx = np.empty((N, packed.shape[1] * 2), np.uint8)
+    idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
+    return "fp16", np.asarray(cb, np.float32)[idx[:, :Kd]].astype(F16), None
+
+
+def per_tensor(W, compress):
+    """A source weight about to be fused with others (q|k|v, gate|up, expert stacks): int4 is
+    encoded here, per tensor, as the reference compresses each linear with its own codebook;
+    the other encodings are per row or per block, so fusing before encoding is exact."""
+    if compress != "int4" or isinstance(W, QuantizedWeight):
+        return W
+    W = np.asarray(W, np.float32)
+    if W.shape[1] % 32:
+        return W                                    # no lut4 kernel for this width: encoded after fusing
+    packed, cb = _blob.palettize_lut4(W)
+    fmt, codes, scale = lut4_encoding(packed, cb, W.shape[1])
+    return QuantizedWeight(fmt, codes, scale, W.shape)
 
 
 def blockwise_encoding(q, s, bs):
@@ -196,7 +223,7 @@ def prefill_gemm(eng, lin: "Linear", x, y, residual=None, epi="f16"):
 
 
 def _prefill_fmt_ok(lin: "Linear") -> bool:
-    return lin.fmt in ("int8", "fp16", "q4_0", "blockwise") and lin.K % 64 == 0 and lin.N % 16 == 0
+    return lin.fmt in ("int8", "fp16", "q4_0", "blockwise", "lut4") and lin.K % 64 == 0 and lin.N % 16 == 0
 
 
 def pack_linear(W, compress, bias=None) -> Linear:
@@ -234,7 +261,8 @@ class AttentionDecode:
         self.H, self.KV, self.dh, self.eps, self.rope = H, KV, dh, float(cfg.norm_eps), bool(cfg.rope)
         pq = _blob.rope_pair_order(H, dh) if self.rope else np.arange(H * dh)
         pk = _blob.rope_pair_order(KV, dh) if self.rope else np.arange(KV * dh)
-        W = _cat([_rows(lw["wq"], pq), _rows(lw["wk"], pk), lw["wv"]])
+        src = {k: per_tensor(lw[k], compress) for k in ("wq", "wk", "wv")}
+        W = _cat([_rows(src["wq"], pq), _rows(src["wk"], pk), src["wv"]])
         bias = None
         if any(k in lw for k in ("q_bias", "k_bias", "v_bias")):
             bq = np.asarray(lw.get("q_bias", np.zeros(H * dh)), np.float32)
@@ -324,7 +352,7 @@ class SwiGLUDecode:
         D = cfg.dim
         self.F = _shape(lw["wgate"])[0]
         self.eps = float(cfg.norm_eps)
-        self.gu = pack_linear(_interleave(lw["wgate"], lw["wup"]), compress)
+        self.gu = pack_linear(_interleave(per_tensor(lw["wgate"], compress), per_tensor(lw["wup"], compress)), compress)
         self.down = pack_linear(lw["wdown"], compress)
         self.norm = _gamma(lw["mlp_norm"], D)
 

@@ -125,6 +125,24 @@ __global__ void dequant_q4_kernel(const uint32_t* __restrict__ qs, const half_t*
 // Weights as fp16 rows out[n * ldo + k], the values the GEMV / MFMA kernels multiply with:
 // int8 fp16(q * s[n]); Q4_0 fp16((nibble - 8) * d) (the reference's GGUF fp16 weights);
 // blockwise fp16(q * s[n][k / 32]).  One thread per 8 weights, one 16-byte store.
+// compress="int4": codebook[row][index]; one thread per 8 columns (4 bytes of indices).
+template <typename T>
+__global__ void dequant_l4_kernel(const uint32_t* __restrict__ idx, const half_t* __restrict__ cb,
+                                  T* __restrict__ out, long long ldo, int N, int K) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per = K >> 3;
+  if (i >= (long long)N * per) return;
+  const int row = (int)(i / per), c = (int)(i - (long long)row * per);
+  const uint32_t w = idx[i];
+  cb += 16 * (size_t)row;
+  T* o = out + (size_t)row * ldo + 8 * c;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    o[2 * b] = (T)cb[(w >> (8 * b)) & 15];
+    o[2 * b + 1] = (T)cb[(w >> (8 * b + 4)) & 15];
+  }
+}
+
 template <int FMT>
 __global__ void dequant_f16_kernel(const void* __restrict__ w, const half_t* __restrict__ s,
                                    half_t* __restrict__ out, long long ldo, int N, int K) {
@@ -181,18 +199,21 @@ int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, v
 }
 
 // Dequantise through the GEMV unpack path: fmt 0 = int8 [N][K] + s[N]; fmt 1 = Q4_0 superblock.
-// fmt 0 int8, 1 Q4_0 (superblock layout), 3 blockwise -> fp16 rows of stride ldo (elements).
+// fmt 0 int8, 1 Q4_0 (superblock layout), 3 blockwise, 4 int4 codebook -> fp16 rows of stride ldo.
 int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,
                     void* stream) {
   AFX_REQUIRE(w && scale && out, "afx_dequant_f16: null pointer");
-  AFX_REQUIRE(fmt == 0 || fmt == 1 || fmt == 3, "afx_dequant_f16: format %d has no scales to apply", fmt);
+  AFX_REQUIRE(fmt == 0 || fmt == 1 || fmt == 3 || fmt == 4, "afx_dequant_f16: format %d has no scales to apply", fmt);
   const int kq = fmt == 1 ? 128 : fmt == 3 ? 32 : 8;
   AFX_REQUIRE(N >= 1 && K >= kq && K % kq == 0, "afx_dequant_f16: K=%d must be a multiple of %d", K, kq);
   AFX_REQUIRE(ldo >= K && ldo % 8 == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)w & 7) == 0,
               "afx_dequant_f16: out rows must be 16-byte aligned (ldo %% 8 == 0) and ldo >= K");
   const long long n8 = (long long)N * (K / 8);
   const dim3 grid((unsigned)((n8 + 255) / 256));
-  if (fmt == 0)
+  if (fmt == 4)
+    hipLaunchKernelGGL(dequant_l4_kernel<half_t>, grid, dim3(256), 0, (hipStream_t)stream, (const uint32_t*)w,
+                       (const half_t*)scale, (half_t*)out, ldo, N, K);
+  else if (fmt == 0)
     hipLaunchKernelGGL(dequant_f16_kernel<FMT_I8>, grid, dim3(256), 0, (hipStream_t)stream, w,
                        (const half_t*)scale, (half_t*)out, ldo, N, K);
   else if (fmt == 1)
@@ -216,6 +237,11 @@ int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, in
     const long long nw = (long long)N * (K / 8);
     hipLaunchKernelGGL(dequant_q4_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, (const uint32_t*)w, (const half_t*)scale, out, N, K);
+  } else if (fmt == 4) {
+    AFX_REQUIRE(K % 8 == 0 && ((uintptr_t)w & 3) == 0, "afx_dequant: int4 K must be a multiple of 8");
+    const long long n8 = (long long)N * (K / 8);
+    hipLaunchKernelGGL(dequant_l4_kernel<float>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint32_t*)w, (const half_t*)scale, out, (long long)K, N, K);
   } else if (fmt == 3) {
     AFX_REQUIRE(K % 32 == 0 && ((uintptr_t)w & 3) == 0, "afx_dequant: blockwise K must be a multiple of 32");
     const long long nw = (long long)N * (K / 4);

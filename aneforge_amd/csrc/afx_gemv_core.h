@@ -5,7 +5,7 @@
 
 namespace afx {
 
-enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2, FMT_BW = 3 };
+enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2, FMT_BW = 3, FMT_L4 = 4 };
 
 // ---- x sources: global memory or the LDS copy written by the norm prologue ----
 template <int N8>
@@ -19,17 +19,23 @@ __device__ __forceinline__ void load_x(const half_t* p, h2 (&out)[N8 * 4]) {
 }
 
 // ---- per-format chunk geometry and math ----
+// Ctx: per-row state a format's dot product needs beyond the chunk (the LUT4 codebook's byte
+// tables), built once per row a wavefront owns from the scale pointer; empty for the others.
+struct NoCtx {
+  __device__ static NoCtx make(const half_t*, int) { return {}; }
+};
 // A "chunk" is the 16 weight bytes one lane loads per row: 16 int8 codes, 32 Q4 codes, or 8
 // fp16 weights.  load_x fetches the matching activations once per chunk (kXH2 fp16 pairs) so
 // they are reused across all rows a wavefront owns.
 template <int FMT> struct Fmt;
 
 template <> struct Fmt<FMT_I8> {
+  using Ctx = NoCtx;
   static constexpr int kWeightsPerChunk = 16;
   static constexpr int kXH2 = 8;
   __device__ static size_t row_bytes(int K) { return (size_t)K; }
   __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) { afx::load_x<2>(xrow + 16 * c, x); }
-  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2&, float acc) {
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2&, const Ctx&, float acc) {
     h2 q[8];
     i8x4_to_h2(w.x, q[0], q[1]); i8x4_to_h2(w.y, q[2], q[3]);
     i8x4_to_h2(w.z, q[4], q[5]); i8x4_to_h2(w.w, q[6], q[7]);
@@ -40,6 +46,7 @@ template <> struct Fmt<FMT_I8> {
 };
 
 template <> struct Fmt<FMT_Q4> {
+  using Ctx = NoCtx;
   static constexpr int kWeightsPerChunk = 32;
   static constexpr int kXH2 = 16;
   __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
@@ -54,7 +61,7 @@ template <> struct Fmt<FMT_Q4> {
       x[4 * j + 0] = t[0]; x[4 * j + 1] = t[1]; x[4 * j + 2] = t[2]; x[4 * j + 3] = t[3];
     }
   }
-  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, float acc) {
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, const Ctx&, float acc) {
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
     const h2 d01 = as_h2(d.x), d23 = as_h2(d.y);
     const float ds[4] = {(float)d01.x, (float)d01.y, (float)d23.x, (float)d23.y};
@@ -77,11 +84,12 @@ template <> struct Fmt<FMT_Q4> {
 // reconstruction fp16(q * s) (one v_pk_mul_f16 per pair, exact product rounded once); a 16-code
 // chunk lies in one block.  d.x = the scales of chunks 4i..4i+3 (two fp16), d.y = which half.
 template <> struct Fmt<FMT_BW> {
+  using Ctx = NoCtx;
   static constexpr int kWeightsPerChunk = 16;
   static constexpr int kXH2 = 8;
   __device__ static size_t row_bytes(int K) { return (size_t)K; }
   __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) { afx::load_x<2>(xrow + 16 * c, x); }
-  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, float acc) {
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, const Ctx&, float acc) {
     const h2 sp = as_h2(d.x);
     const half_t s = d.y ? sp.y : sp.x;
     const h2 s2 = {s, s};
@@ -95,15 +103,80 @@ template <> struct Fmt<FMT_BW> {
 };
 
 template <> struct Fmt<FMT_F16> {
+  using Ctx = NoCtx;
   static constexpr int kWeightsPerChunk = 8;
   static constexpr int kXH2 = 4;
   __device__ static size_t row_bytes(int K) { return (size_t)K * 2; }
   __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) { afx::load_x<1>(xrow + 8 * c, x); }
-  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2&, float acc) {
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2&, const Ctx&, float acc) {
     acc = dot2(as_h2(w.x), x[0], acc);
     acc = dot2(as_h2(w.y), x[1], acc);
     acc = dot2(as_h2(w.z), x[2], acc);
     acc = dot2(as_h2(w.w), x[3], acc);
+    return acc;
+  }
+};
+
+// compress="int4" (the reference's palettize_lut4, aneforge/_blob.py:28-43): a 16-entry fp16
+// codebook per row, scale[N][16] (the codebook of the tensor the row came from, so fused q|k|v
+// and gate|up matrices keep each tensor's own), 4-bit indices [N][K/2], byte j of a row =
+// index of column 2j (low nibble) | index of column 2j + 1 (high nibble).  The weight is the
+// codebook entry itself.  A chunk is 16 bytes = 32 columns; the lookup is pure VALU: the
+// codebook's low and high bytes sit in 8 registers and v_perm_b32 picks four entries of an
+// 8-entry half per instruction, v_bfi chooses the half by bit 3 of each index.  Columns come
+// out as (c0, c2), (c4, c6), (c1, c3), (c5, c7) pairs, so load_x delivers x in that order.
+struct L4Ctx {
+  uint32_t lo[4], hi[4];   // lo[i] = low bytes of entries 4i .. 4i + 3; hi[i] = their high bytes
+  __device__ static L4Ctx make(const half_t* scale, int row) {
+    const half_t* cb = scale + 16 * (size_t)row;
+    const u4 a = *(const u4*)cb, b = *(const u4*)(cb + 8);      // entries 0..7 and 8..15
+    const uint32_t e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};   // dword k = entries 2k, 2k + 1
+    L4Ctx c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c.lo[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x06040200u);
+      c.hi[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x07050301u);
+    }
+    return c;
+  }
+};
+__device__ __forceinline__ void l4_lookup(const L4Ctx& t, uint32_t idx, uint32_t& lb, uint32_t& hb) {
+  // idx: four indices 0..15, one per byte
+  const uint32_t sel = idx & 0x07070707u;
+  const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;     // 0xFF in the bytes whose index is >= 8
+  const uint32_t l0 = __builtin_amdgcn_perm(t.lo[1], t.lo[0], sel), l1 = __builtin_amdgcn_perm(t.lo[3], t.lo[2], sel);
+  const uint32_t h0 = __builtin_amdgcn_perm(t.hi[1], t.hi[0], sel), h1 = __builtin_amdgcn_perm(t.hi[3], t.hi[2], sel);
+  lb = (m & l1) | (~m & l0);
+  hb = (m & h1) | (~m & h0);
+}
+template <> struct Fmt<FMT_L4> {
+  using Ctx = L4Ctx;
+  static constexpr int kWeightsPerChunk = 32;
+  static constexpr int kXH2 = 16;
+  __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
+  // x of the chunk's 32 columns as (x0, x2), (x4, x6), (x1, x3), (x5, x7) per group of 8
+  __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const u4 v = *(const u4*)(xrow + 32 * c + 8 * g);          // natural pairs (x0,x1) .. (x6,x7)
+      x[4 * g + 0] = as_h2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u));
+      x[4 * g + 1] = as_h2(__builtin_amdgcn_perm(v.w, v.z, 0x05040100u));
+      x[4 * g + 2] = as_h2(__builtin_amdgcn_perm(v.y, v.x, 0x07060302u));
+      x[4 * g + 3] = as_h2(__builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+    }
+  }
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2&, const Ctx& t, float acc) {
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t la, ha, lb, hb;
+      l4_lookup(t, wd[g] & 0x0F0F0F0Fu, la, ha);           // columns 0, 2, 4, 6 of the group
+      l4_lookup(t, (wd[g] >> 4) & 0x0F0F0F0Fu, lb, hb);    // columns 1, 3, 5, 7
+      acc = dot2(as_h2(__builtin_amdgcn_perm(ha, la, 0x05010400u)), x[4 * g + 0], acc);   // (c0, c2)
+      acc = dot2(as_h2(__builtin_amdgcn_perm(ha, la, 0x07030602u)), x[4 * g + 1], acc);   // (c4, c6)
+      acc = dot2(as_h2(__builtin_amdgcn_perm(hb, lb, 0x05010400u)), x[4 * g + 2], acc);   // (c1, c3)
+      acc = dot2(as_h2(__builtin_amdgcn_perm(hb, lb, 0x07030602u)), x[4 * g + 3], acc);   // (c5, c7)
+    }
     return acc;
   }
 };

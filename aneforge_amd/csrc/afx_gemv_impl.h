@@ -9,6 +9,8 @@
 //   FMT_Q4  : Q4_0 blocks of 32 along K, one fp16 scale d per block, repacked into the
 //             "superblock" layout (afx_q4_0_repack): W^ = (nibble-8)*d[n, k/32]
 //   FMT_F16 : plain fp16 [N, K] (lm_head, router)
+//   FMT_L4  : 4-bit indices [N, K/2] into one fp16 16-entry codebook per tensor (compress="int4",
+//             aneforge/_blob.py:28-43): W^ = codebook[index]
 //   FMT_BW  : int8 codes [N, K] + fp16 scale per 32-weight block s[N, K/32] (compress="blockwise",
 //             aneforge/_blob.py:46-56): W^ = fp16(q * s[n, k/32])
 //
@@ -77,7 +79,7 @@ struct GemvArgs {
 constexpr int kStageUnroll = 4;     // 16-byte staging loads per thread in flight per batch
 constexpr int kBufDword3 = 0x00020000;   // raw buffer descriptor word 3 (gfx9 family)
 
-template <int FMT> struct Units { static constexpr int value = FMT == FMT_Q4 ? 2 : 4; };
+template <int FMT> struct Units { static constexpr int value = FMT == FMT_Q4 || FMT == FMT_L4 ? 2 : 4; };
 
 // Bytes of LDS the kernel needs: staged x rows, gamma, and the cross-wave norm partials.
 __host__ __device__ inline size_t gemv_lds_bytes(int Mt, int K, bool norm) {
@@ -352,17 +354,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   for (int m = 0; m < M; ++m)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+  typename Fmt<FMT>::Ctx fctx[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) fctx[r] = Fmt<FMT>::Ctx::make(a.scale, row0 + r < N ? row0 + r : N - 1);
   auto compute = [&](const u4 (&w)[U][R], const u2 (&d)[U][R], int j) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      int c = j * 64 * U + 64 * u + lane;
-      c = c < nchunks ? c : nchunks - 1;          // x of a real chunk; the weights past K read as zero
+      const int craw = j * 64 * U + 64 * u + lane;
+      const int c = craw < nchunks ? craw : nchunks - 1;   // x of a real chunk; the weights past K read as zero
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         h2 xv[XH];
         Fmt<FMT>::load_x(xp[m], c, xv);
+        if constexpr (FMT == FMT_L4) {            // index 0 past K still looks up an entry: zero its x
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = Fmt<FMT>::dot(w[u][r], xv, d[u][r], acc[m][r]);
+          for (int i = 0; i < XH; ++i) xv[i] = craw < nchunks ? xv[i] : (h2){(half_t)0.0f, (half_t)0.0f};
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = Fmt<FMT>::dot(w[u][r], xv, d[u][r], fctx[r], acc[m][r]);
       }
     }
   };
@@ -497,6 +506,15 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
       Fmt<FMT>::load_x(xs, c, xv[u]);
     }
   }
+  if constexpr (FMT == FMT_L4) {                  // chunks past K: index 0 still looks up an entry
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < XH; ++i) xv[u][i] = 64 * u + lane < nchunks ? xv[u][i] : (h2){(half_t)0.0f, (half_t)0.0f};
+  }
+  typename Fmt<FMT>::Ctx fctx[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) fctx[r] = Fmt<FMT>::Ctx::make(a.scale, row0 + r < N ? row0 + r : N - 1);
   if (!live) return;   // no barrier follows
 
   float acc[R];
@@ -517,7 +535,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
           wv.x = ok ? wv.x : 0u; wv.y = ok ? wv.y : 0u; wv.z = ok ? wv.z : 0u; wv.w = ok ? wv.w : 0u;
         }
       }
-      acc[r] = Fmt<FMT>::dot(wv, xv[u], dv, acc[r]);
+      acc[r] = Fmt<FMT>::dot(wv, xv[u], dv, fctx[r], acc[r]);
     }
   }
 
@@ -565,14 +583,15 @@ gemv_fn pick_gemv_row_u(int eg, int R, int norm) {
 __host__ __device__ inline int fast_units(int fmt, int nchunks) {
   const int u = (nchunks + 63) / 64;
   if (fmt == FMT_I8 || fmt == FMT_BW) return u == 4 || u == 11 ? u : 0;
-  if (fmt == FMT_Q4) return u == 2 || u == 6 ? u : 0;
+  if (fmt == FMT_Q4 || fmt == FMT_L4) return u == 2 || u == 6 ? u : 0;
   return u == 8 ? u : 0;
 }
 template <int FMT>
 gemv_fn pick_gemv_row(int eg, int R, int norm, int U) {
   if constexpr (FMT == FMT_I8 || FMT == FMT_BW)
     return U == 11 ? pick_gemv_row_u<FMT, 11>(eg, R, norm) : pick_gemv_row_u<FMT, 4>(eg, R, norm);
-  else if constexpr (FMT == FMT_Q4) return U == 6 ? pick_gemv_row_u<FMT, 6>(eg, R, norm) : pick_gemv_row_u<FMT, 2>(eg, R, norm);
+  else if constexpr (FMT == FMT_Q4 || FMT == FMT_L4)
+    return U == 6 ? pick_gemv_row_u<FMT, 6>(eg, R, norm) : pick_gemv_row_u<FMT, 2>(eg, R, norm);
   else return pick_gemv_row_u<FMT, 8>(eg, R, norm);
 }
 
@@ -581,9 +600,11 @@ gemv_fn pick_gemv_i8(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_q4(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_f16(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_bw(int mt, int eg, int R, int xs);
+gemv_fn pick_gemv_l4(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_row_i8(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_q4(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_f16(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_bw(int eg, int R, int norm, int U);
+gemv_fn pick_gemv_row_l4(int eg, int R, int norm, int U);
 
 }  // namespace afx

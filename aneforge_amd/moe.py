@@ -90,6 +90,12 @@ class MoEDecode:
         self.norm = E._gamma(lw["mlp_norm"], D)
         self.router = E.pack_linear(np.asarray(lw["router"], np.float32), None)
         gate, up, down = lw["wgate_exps"], lw["wup_exps"], lw["wdown_exps"]
+        if compress == "int4" and not isinstance(gate, (list, tuple)):
+            # one codebook per expert matrix (the reference compresses each linear separately)
+            g_, u_, d_ = (np.asarray(a, np.float32) for a in (gate, up, down))
+            gate = [E.per_tensor(g_[e], compress) for e in range(self.E)]
+            up = [E.per_tensor(u_[e], compress) for e in range(self.E)]
+            down = [E.per_tensor(np.ascontiguousarray(d_[e].T), compress) for e in range(self.E)]
         if isinstance(gate, (list, tuple)):          # per-expert QuantizedWeight lists
             F = gate[0].shape[0]
             gu = E._cat([E._interleave(g, u) for g, u in zip(gate, up)])
@@ -104,7 +110,8 @@ class MoEDecode:
         self.down = E.pack_linear(dn, compress)
         self.shared = None
         if "wgate_sh" in lw:
-            self.sh_gu = E.pack_linear(E._interleave(lw["wgate_sh"], lw["wup_sh"]), compress)
+            self.sh_gu = E.pack_linear(E._interleave(E.per_tensor(lw["wgate_sh"], compress),
+                                                     E.per_tensor(lw["wup_sh"], compress)), compress)
             self.sh_down = E.pack_linear(lw["wdown_sh"], compress)
             self.sh_gate = E.pack_linear(np.asarray(lw["shared_gate"], np.float32).reshape(1, D), None)
             self.shared = True

@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--rows-hint", type=int, default=0)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--ctx", type=int, default=2048)
-    ap.add_argument("--weights", default="int8", choices=["int8", "q4_0", "blockwise"],
+    ap.add_argument("--weights", default="int8", choices=["int8", "q4_0", "blockwise", "lut4"],
                     help="linear weight format of the cfg3 model for --workload prefill")
     return ap.parse_args()
 
@@ -293,6 +293,10 @@ def build_cfg3_engine(steps: int, warmup: int, fmt: str = "int8"):
             q = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
             d = (torch.rand((N, Kd // 32), device="cuda", generator=g) * 0.005).half()
             return E.Linear("q4_0", q, d, N, Kd)
+        if fmt == "lut4":                       # random indices + a codebook per row
+            q = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
+            cb = (torch.randn((N, 16), device="cuda", generator=g) * 0.02).half()
+            return E.Linear("lut4", q, cb, N, Kd)
         q = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
         if fmt == "blockwise":
             s = (torch.rand((N, Kd // 32), device="cuda", generator=g) * (0.02 / 127)).half()

@@ -17,6 +17,7 @@ Pinning status (see tests/test_oracle.py):
   dequant_q4_0_f16                      pinned: KAT (fp16 rounding of the fp32 product)
   quantize_blockwise                    pinned: closed form + reference property tests
   dequant_blockwise                     pinned: KAT (an fp16 round-half-even tie of the product)
+  dequant_lut4                          pinned: KAT (hand-packed nibbles -> their codebook entries)
   rms_norm                              pinned: torch + invariants
   rope_tables / rope / llama3 scaling    pinned: transformers' rope utilities + HF formula
   attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
@@ -66,6 +67,18 @@ def quantize_blockwise(W, block_size=32):
     s = np.maximum(np.abs(Wb).max(axis=2) / np.float32(127.0), np.float32(1e-8))
     q = np.clip(np.round(Wb / s[:, :, None]), -127, 127).astype(np.int8).reshape(OUT, IN)
     return q, s.astype(f16), bs
+
+
+def dequant_lut4(packed, codebooks, K):
+    """The int4 palettization's reconstruction (aneforge/_blob.py:28-43 docstring): each column's
+    fp16 codebook entry.  packed [N, ceil(K/2)] (column 2j in the low nibble of byte j),
+    codebooks [N, 16] (one per row) or [16] (one for the tensor); returned as fp32."""
+    packed = np.asarray(packed, np.uint8)
+    idx = np.empty((packed.shape[0], packed.shape[1] * 2), np.int64)
+    idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
+    cb = np.asarray(codebooks, f16).astype(np.float32)
+    cb = np.broadcast_to(cb, (packed.shape[0], 16)) if cb.ndim == 1 else cb
+    return np.take_along_axis(cb, idx[:, :K], axis=1)
 
 
 def dequant_blockwise(q, s, bs=32):

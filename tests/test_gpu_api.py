@@ -177,6 +177,12 @@ def _moe_model(E=8, k=2, D=128, F=128, layers=2, vocab=64, qk=False, seed=0, dh=
     return cfg, w
 
 
+def _lut4_rec(W):
+    from aneforge_amd import _blob
+    packed, cb = _blob.palettize_lut4(np.asarray(W, np.float32))
+    return ref.dequant_lut4(packed, cb, np.asarray(W).shape[1])
+
+
 def _oracle_weights(cfg, w, enc):
     ow = {"embed": w["embed"].astype(np.float16).astype(np.float32), "final_norm": w["final_norm"],
           "lm_head": w["lm_head"].astype(np.float16).astype(np.float32), "layers": []}
@@ -197,13 +203,15 @@ def _oracle_weights(cfg, w, enc):
     return ow, ocfg
 
 
-@pytest.mark.parametrize("compress,qk", [(None, False), ("int8", True), ("q4_0", False), ("blockwise", False)])
+@pytest.mark.parametrize("compress,qk", [(None, False), ("int8", True), ("q4_0", False), ("blockwise", False),
+                                         ("int4", False)])
 def test_moe_decoder_generate_matches_oracle(compress, qk):
     say(f"LlamaPrefill with MoE layers compress={compress} qk_norm={qk}")
     cfg, w = _moe_model(qk=qk)
     enc = {None: lambda W: np.asarray(W, np.float32).astype(np.float16).astype(np.float32),
            "int8": lambda W: ref.dequant_w8(*ref.quantize_per_row(W)),
            "blockwise": lambda W: ref.dequant_blockwise(*ref.quantize_blockwise(W, 32)),
+           "int4": lambda W: _lut4_rec(W),
            "q4_0": lambda W: ref.dequant_q4_0(ref.quantize_q4_0(W), *np.asarray(W).shape)}[compress]
     m = af.LlamaPrefill(cfg, w, compress=compress)
     prompt = [3, 9, 27, 1]

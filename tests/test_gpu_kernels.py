@@ -84,7 +84,25 @@ def test_dequant_blockwise_bit_exact(K):
     assert np.array_equal(got.view(np.uint32), ref.dequant_blockwise(q, s).view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt", ["int8", "q4_0", "blockwise"])
+def _l4(N, Kd, seed):
+    rng = np.random.default_rng(seed)
+    packed = rng.integers(0, 256, (N, Kd // 2), dtype=np.uint8)
+    cb = (rng.standard_normal((N, 16)) * 0.05).astype(np.float16)      # a different codebook per row
+    return packed, cb
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 4096, 4096), (1, 4096, 11008), (3, 1000, 1024), (1, 777, 4128),
+                                    (6, 777, 4128), (12, 256, 11008)])
+def test_linear_lut4(K, M, N, Kd):
+    # fast path (M = 1, K 4096 / 11008), generic path with a ragged last unit (K = 4128), 8-row chunks
+    say(f"linear lut4 M={M} N={N} K={Kd}")
+    packed, cb = _l4(N, Kd, 70 + M)
+    x = np.random.default_rng(71).standard_normal((M, Kd)).astype(np.float16)
+    got = host(K.linear("lut4", dev(packed), dev(cb), dev(x)))
+    check_f16(got, ref.linear(x, ref.dequant_lut4(packed, cb, Kd)), what="lut4 linear")
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4_0", "blockwise", "lut4"])
 def test_dequant_f16_bit_exact(K, fmt):
     # the fp16 weights the batched prefill expands a matrix to (rows of a wider scratch buffer)
     say(f"dequant_f16 {fmt} [72, 1024]")
@@ -97,6 +115,9 @@ def test_dequant_f16_bit_exact(K, fmt):
     elif fmt == "blockwise":
         q, s = _bw(N, Kd, 14)
         want = ref.dequant_blockwise(q, s).astype(np.float16)
+    elif fmt == "lut4":
+        q, s = _l4(N, Kd, 14)
+        want = ref.dequant_lut4(q, s, Kd).astype(np.float16)
     else:
         blocks = ref.quantize_q4_0(rng.standard_normal((N, Kd)).astype(np.float32) * 0.05)
         q, s = _blob.q4_0_to_superblock(blocks, N, Kd)

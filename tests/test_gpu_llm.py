@@ -43,6 +43,9 @@ def _effective(w, compress):
         if compress == "blockwise":
             q, sc, bs = _blob.quantize_blockwise(W, 32)
             return ref.dequant_blockwise(q, sc, bs)
+        if compress == "int4":                       # one codebook per tensor, as the reference
+            packed, cb = _blob.palettize_lut4(W)
+            return ref.dequant_lut4(packed, cb, W.shape[1])
         raise ValueError(compress)
 
     out = {"embed": np.asarray(w["embed"], np.float32).astype(np.float16).astype(np.float32),
@@ -75,7 +78,7 @@ def _assert_tokens_match(got, want, logits, what, rel_gap=2e-3):
     assert len(got) == len(want), f"{what}: {len(got)} tokens vs {len(want)}"
 
 
-@pytest.mark.parametrize("compress", [None, "int8", "q4_0", "blockwise"])
+@pytest.mark.parametrize("compress", [None, "int8", "q4_0", "blockwise", "int4"])
 def test_generate_matches_oracle(compress):
     from aneforge_amd.llm import LlamaConfig, LlamaPrefill
     say(f"LlamaPrefill.generate vs oracle compress={compress}")
@@ -183,7 +186,7 @@ def test_prefill_matches_huggingface_llama():
 
 
 @pytest.mark.parametrize("compress,chunk", [("int8", 2048), ("int8", 48), (None, 2048), ("blockwise", 2048),
-                                            ("q4_0", 2048), ("q4_0", 48)])
+                                            ("q4_0", 2048), ("q4_0", 48), ("int4", 2048)])
 def test_batched_prefill_matches_forced_steps_and_oracle(compress, chunk):
     """The MFMA batched prefill (head dim 128) leaves the same cache and state as the
     token-by-token forced steps, and generation from it matches the oracle."""

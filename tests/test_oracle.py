@@ -346,6 +346,16 @@ def test_q4_0_f16_dequant_matches_reference_rounding():
     assert np.all(r == r[0, 0])
 
 
+def test_dequant_lut4_known_answer():
+    # byte 0x21: column 0 -> entry 1, column 1 -> entry 2; byte 0xF0: column 2 -> 0, column 3 -> 15;
+    # the second row uses its own codebook
+    cb = np.stack([np.arange(16, dtype=np.float16) * np.float16(0.5), -np.arange(16, dtype=np.float16)])
+    packed = np.array([[0x21, 0xF0], [0x21, 0xF0]], np.uint8)
+    w = ref.dequant_lut4(packed, cb, 4)
+    np.testing.assert_array_equal(w, np.array([[0.5, 1.0, 0.0, 7.5], [-1.0, -2.0, 0.0, -15.0]], np.float32))
+    np.testing.assert_array_equal(ref.dequant_lut4(packed[:1], cb[0], 3), np.array([[0.5, 1.0, 0.0]], np.float32))
+
+
 def test_palettize_lut4_matches_reference_vectors():
     # vectors recorded from the reference's palettize_lut4 (aneforge/_blob.py:28-43) by
     # tests/golden/make_lut4_vectors.py: packed indices and fp16 codebook must match bit for bit

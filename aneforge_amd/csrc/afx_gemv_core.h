@@ -140,14 +140,18 @@ struct L4Ctx {
     return c;
   }
 };
-__device__ __forceinline__ void l4_lookup(const L4Ctx& t, uint32_t idx, uint32_t& lb, uint32_t& hb) {
-  // idx: four indices 0..15, one per byte
-  const uint32_t sel = idx & 0x07070707u;
-  const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;     // 0xFF in the bytes whose index is >= 8
+// Four entries at once.  sel: the low 3 bits of four indices, one per byte (upper bits zero);
+// m: 0xFF in the bytes whose index is >= 8.
+__device__ __forceinline__ void l4_lookup(const L4Ctx& t, uint32_t sel, uint32_t m, uint32_t& lb, uint32_t& hb) {
   const uint32_t l0 = __builtin_amdgcn_perm(t.lo[1], t.lo[0], sel), l1 = __builtin_amdgcn_perm(t.lo[3], t.lo[2], sel);
   const uint32_t h0 = __builtin_amdgcn_perm(t.hi[1], t.hi[0], sel), h1 = __builtin_amdgcn_perm(t.hi[3], t.hi[2], sel);
   lb = (m & l1) | (~m & l0);
   hb = (m & h1) | (~m & h0);
+}
+// Byte masks from bit 7 of each byte of s: v_perm selectors 8..11 replicate the sign bit of bytes
+// 1, 3, 5, 7 of the 64-bit source {a, b}; with a = s and b = s << 8 those are bits 7, 23, 15, 31 of s.
+__device__ __forceinline__ uint32_t l4_bit7_mask(uint32_t s) {
+  return __builtin_amdgcn_perm(s, s << 8, 0x0B090A08u);
 }
 template <> struct Fmt<FMT_L4> {
   using Ctx = L4Ctx;
@@ -170,8 +174,10 @@ template <> struct Fmt<FMT_L4> {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       uint32_t la, ha, lb, hb;
-      l4_lookup(t, wd[g] & 0x0F0F0F0Fu, la, ha);           // columns 0, 2, 4, 6 of the group
-      l4_lookup(t, (wd[g] >> 4) & 0x0F0F0F0Fu, lb, hb);    // columns 1, 3, 5, 7
+      // low nibbles: columns 0, 2, 4, 6 of the group (bit 3 of each byte -> bit 7 via << 4);
+      // high nibbles: columns 1, 3, 5, 7 (bit 7 of each byte as it is)
+      l4_lookup(t, wd[g] & 0x07070707u, l4_bit7_mask(wd[g] << 4), la, ha);
+      l4_lookup(t, (wd[g] >> 4) & 0x07070707u, l4_bit7_mask(wd[g]), lb, hb);
       acc = dot2(as_h2(__builtin_amdgcn_perm(ha, la, 0x05010400u)), x[4 * g + 0], acc);   // (c0, c2)
       acc = dot2(as_h2(__builtin_amdgcn_perm(ha, la, 0x07030602u)), x[4 * g + 1], acc);   // (c4, c6)
       acc = dot2(as_h2(__builtin_amdgcn_perm(hb, lb, 0x05010400u)), x[4 * g + 2], acc);   // (c1, c3)

@@ -9,8 +9,9 @@
 //   FMT_Q4  : Q4_0 blocks of 32 along K, one fp16 scale d per block, repacked into the
 //             "superblock" layout (afx_q4_0_repack): W^ = (nibble-8)*d[n, k/32]
 //   FMT_F16 : plain fp16 [N, K] (lm_head, router)
-//   FMT_L4  : 4-bit indices [N, K/2] into one fp16 16-entry codebook per tensor (compress="int4",
-//             aneforge/_blob.py:28-43): W^ = codebook[index]
+//   FMT_L4  : 4-bit indices [N, K/2] (column 2j in the low nibble of byte j) into a 16-entry fp16
+//             codebook per row, scale[N, 16] (compress="int4", aneforge/_blob.py:28-43; each row holds
+//             its source tensor's codebook): W^ = codebook[n][index]
 //   FMT_BW  : int8 codes [N, K] + fp16 scale per 32-weight block s[N, K/32] (compress="blockwise",
 //             aneforge/_blob.py:46-56): W^ = fp16(q * s[n, k/32])
 //
@@ -366,12 +367,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       for (int m = 0; m < M; ++m) {
         h2 xv[XH];
         Fmt<FMT>::load_x(xp[m], c, xv);
-        if constexpr (FMT == FMT_L4) {            // index 0 past K still looks up an entry: zero its x
 #pragma unroll
-          for (int i = 0; i < XH; ++i) xv[i] = craw < nchunks ? xv[i] : (h2){(half_t)0.0f, (half_t)0.0f};
+        for (int r = 0; r < R; ++r) {
+          const float t = Fmt<FMT>::dot(w[u][r], xv, d[u][r], fctx[r], acc[m][r]);
+          // LUT4: index 0 of a chunk past K still looks up an entry, so drop that chunk's sum
+          acc[m][r] = FMT != FMT_L4 || craw < nchunks ? t : acc[m][r];
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = Fmt<FMT>::dot(w[u][r], xv, d[u][r], fctx[r], acc[m][r]);
       }
     }
   };
@@ -506,12 +507,6 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
       Fmt<FMT>::load_x(xs, c, xv[u]);
     }
   }
-  if constexpr (FMT == FMT_L4) {                  // chunks past K: index 0 still looks up an entry
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int i = 0; i < XH; ++i) xv[u][i] = 64 * u + lane < nchunks ? xv[u][i] : (h2){(half_t)0.0f, (half_t)0.0f};
-  }
   typename Fmt<FMT>::Ctx fctx[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) fctx[r] = Fmt<FMT>::Ctx::make(a.scale, row0 + r < N ? row0 + r : N - 1);
@@ -531,11 +526,13 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
         if constexpr (FMT == FMT_Q4) {
           dv.x = ok ? dv.x : 0u;
           dv.y = ok ? dv.y : 0u;
-        } else {
+        } else if constexpr (FMT != FMT_L4) {
           wv.x = ok ? wv.x : 0u; wv.y = ok ? wv.y : 0u; wv.z = ok ? wv.z : 0u; wv.w = ok ? wv.w : 0u;
         }
       }
-      acc[r] = Fmt<FMT>::dot(wv, xv[u], dv, fctx[r], acc[r]);
+      const float t = Fmt<FMT>::dot(wv, xv[u], dv, fctx[r], acc[r]);
+      // LUT4: index 0 still looks up an entry, so a chunk past K drops its whole sum
+      acc[r] = FMT == FMT_L4 && u == U - 1 && !ok ? acc[r] : t;
     }
   }
 

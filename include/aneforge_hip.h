@@ -57,7 +57,10 @@ int afx_event_destroy(void* ev);
  * (aneforge/_compile.py:171-179, 375-385; aneforge/graph.py:187-195); 1: the GGUF Q4_0 weights
  * the reference dequantises on the host (aneforge/_gguf.py:34-39); 2: fp16; 3: compress=
  * "blockwise" with 32-weight blocks, int8 codes + fp16 scale[N][K/32], weight fp16(q * s)
- * (aneforge/_blob.py:46-56, constexpr_blockwise_shift_scale in aneforge/_compile.py:112-188). */
+ * (aneforge/_blob.py:46-56, constexpr_blockwise_shift_scale in aneforge/_compile.py:112-188);
+ * 4: compress="int4", palettize_lut4's packed indices [N][K/2] (column 2j in the low nibble of byte
+ * j) + a 16-entry fp16 codebook per row scale[N][16], weight codebook[n][index] (aneforge/_blob.py:
+ * 28-43, constexpr_lut_to_dense in aneforge/_compile.py:149; vector kernels at any M). */
 int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                int M, int N, int K, const void* bias, const void* residual, int out_f32,
                int rows_hint, void* stream);
@@ -89,7 +92,7 @@ int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, v
 /* Dequantise through the GEMV's own unpack path into fp32 (bit-exact check of
  * quantize_per_row / Q4_0 / quantize_blockwise reconstruction, aneforge/_blob.py:20-25, 46-56). */
 int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream);
-/* The same weights as fp16 rows out[n * ldo + k] (fmt 0 int8, 1 Q4_0, 3 blockwise): the fp16 values the
+/* The same weights as fp16 rows out[n * ldo + k] (fmt 0 int8, 1 Q4_0, 3 blockwise, 4 int4): the fp16 values the
  * reference multiplies with -- for Q4_0 the fp16 cast of GGUFView.get (aneforge/_gguf.py:34-39).  The
  * batched prefill expands formats its GEMM does not read (Q4_0) into fp16 this way, one matrix at a time. */
 int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,

@@ -6,6 +6,7 @@ plus GGUF Q4_0, and the packing into the layouts the HIP kernels stream.
   palettize_lut4     16-entry per-tensor LUT, 4-bit indices      (aneforge/_blob.py:28-43)
   quantize_q4_0      ggml Q4_0 blocks (18 B / 32 weights) from fp weights
   q4_0_to_superblock GGUF Q4_0 bytes -> (qs, d) superblock layout (host twin of afx_q4_0_repack)
+  q4_k_repack        GGUF Q4_K bytes -> (codes, header) the Q4_K kernels read (host twin of afx_q4_k_repack)
 
 The encodings must produce the reference's bytes, so their steps match the reference's; the
 code is this package's own.  The BLOBFILE container is ANE-specific and is not rebuilt."""
@@ -144,3 +145,24 @@ def interleave_rows(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     out = np.empty((a.shape[0] * 2,) + a.shape[1:], a.dtype)
     out[0::2], out[1::2] = a, b
     return out
+
+
+def q4_k_repack(blocks: np.ndarray, N: int, K: int) -> tuple[np.ndarray, np.ndarray]:
+    """Host twin of afx_q4_k_repack: GGUF Q4_K super-blocks (144 B: fp16 d, fp16 dmin, 12 bytes of
+    6-bit scales and mins, 128 code bytes) -> (codes uint8 [N, K/2]: each super-block's 128 code
+    bytes as they are; header int32 [N, K/256 * 5]: per super-block {d | dmin << 16} and, for each
+    sub-block pair p, the bytes {sc(2p), sc(2p+1), m(2p), m(2p+1)}).  The 12-byte field: j < 4:
+    sc = b[j] & 63, m = b[j+4] & 63; j >= 4: sc = (b[j+4] & 15) | (b[j-4] >> 6) << 4,
+    m = (b[j+4] >> 4) | (b[j] >> 6) << 4."""
+    if K % 256:
+        raise ValueError(f"Q4_K rows need K % 256 == 0 (got {K})")
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(N, K // 256, 144)
+    codes = np.ascontiguousarray(b[:, :, 16:]).reshape(N, K // 2)
+    f = b[:, :, 4:16].astype(np.uint32)
+    lo, mid, hi = f[..., 0:4], f[..., 4:8], f[..., 8:12]
+    sc = np.concatenate([lo & 63, (hi & 15) | ((lo >> 6) << 4)], axis=-1)      # [N, nb, 8]
+    mn = np.concatenate([mid & 63, (hi >> 4) | ((mid >> 6) << 4)], axis=-1)
+    hdr = np.empty((N, K // 256, 5), np.uint32)
+    hdr[..., 0] = np.ascontiguousarray(b[:, :, 0:4]).view(np.uint32)[..., 0]
+    hdr[..., 1:] = sc[..., 0::2] | (sc[..., 1::2] << 8) | (mn[..., 0::2] << 16) | (mn[..., 1::2] << 24)
+    return codes, hdr.reshape(N, -1).view(np.int32)

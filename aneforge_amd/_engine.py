@@ -36,7 +36,7 @@ F16 = np.float16
 @dataclass
 class Linear:
     """A weight [N, K] resident on the device in one of the kernel formats."""
-    fmt: str                          # "int8" | "q4_0" | "fp16" | "blockwise" | "lut4"
+    fmt: str                          # "int8" | "q4_0" | "fp16" | "blockwise" | "lut4" | "q4_k"
     w: torch.Tensor
     scale: torch.Tensor | None
     N: int
@@ -63,7 +63,9 @@ class QuantizedWeight:
       fmt "q4_0_gguf": codes uint8 [N, K/32*18] GGUF block bytes, scale None
       fmt "blockwise": codes int8 [N, K], scale fp16 [N, K/32] (GGUF Q8_0 blocks, K % 64 == 0)
       fmt "lut4":      codes uint8 [N, K/2] int4 indices (column 2j low nibble), scale fp16 [N, 16]:
-                       each row's codebook, the palettize_lut4 codebook of its source tensor"""
+                       each row's codebook, the palettize_lut4 codebook of its source tensor
+      fmt "q4_k":      codes uint8 [N, K/2] GGUF Q4_K code bytes, scale int32 [N, K/256*5] super-block
+                       headers ({d, dmin} + unpacked 6-bit scales/mins; _blob.q4_k_repack)"""
     fmt: str
     codes: np.ndarray
     scale: np.ndarray | None
@@ -92,6 +94,15 @@ class QuantizedWeight:
             idx = np.empty((N, Kd), np.uint8)
             idx[:, 0::2], idx[:, 1::2] = self.codes & 15, self.codes >> 4
             return np.take_along_axis(self.scale.astype(np.float32), idx.astype(np.int64), axis=1)
+        if self.fmt == "q4_k":
+            h = np.ascontiguousarray(self.scale).view(np.uint32).reshape(N, Kd // 256, 5)
+            dd = np.ascontiguousarray(h[..., 0]).view(np.float16).reshape(N, Kd // 256, 2).astype(np.float32)
+            sm = ((h[..., 1:, None] >> (8 * np.arange(4, dtype=np.uint32))) & 255).astype(np.float32)  # [N,nb,p,4]
+            ds = dd[..., 0, None, None] * sm[..., :2]          # [N, nb, pair, 2]: sub-blocks 2p, 2p+1
+            dm = dd[..., 1, None, None] * sm[..., 2:]
+            c = self.codes.reshape(N, Kd // 256, 4, 32)
+            q = np.stack([c & 15, c >> 4], axis=3).astype(np.float32)      # [N, nb, pair, half, 32]
+            return (ds[..., None] * q - dm[..., None]).reshape(N, Kd)
         q = self if self.fmt == "q4_0" else self.to_superblock()
         blocks = _blob.superblock_to_q4_0(q.codes, q.scale, N, Kd)
         codes, d = _blob.q4_0_codes(blocks, N, Kd)
@@ -201,7 +212,7 @@ def blockwise_encoding(q, s, bs):
 
 
 def pack_encoded(fmt, w, s, bias=None) -> Linear:
-    N, Kd = w.shape[0], (w.shape[1] * 2 if fmt == "q4_0" else w.shape[1])
+    N, Kd = w.shape[0], (w.shape[1] * 2 if fmt in ("q4_0", "lut4", "q4_k") else w.shape[1])
     return Linear(fmt, _to_dev(w), None if s is None else _to_dev(s), N, Kd,
                   None if bias is None else _to_dev(np.asarray(bias, np.float32).astype(F16)))
 
@@ -223,7 +234,7 @@ def prefill_gemm(eng, lin: "Linear", x, y, residual=None, epi="f16"):
 
 
 def _prefill_fmt_ok(lin: "Linear") -> bool:
-    return lin.fmt in ("int8", "fp16", "q4_0", "blockwise", "lut4") and lin.K % 64 == 0 and lin.N % 16 == 0
+    return lin.fmt in ("int8", "fp16", "q4_0", "blockwise", "lut4", "q4_k") and lin.K % 64 == 0 and lin.N % 16 == 0
 
 
 def pack_linear(W, compress, bias=None) -> Linear:

@@ -71,6 +71,65 @@ __global__ void q4_unpack_kernel(const uint32_t* __restrict__ qs, const half_t* 
   for (int i = 0; i < 16; ++i) dst[2 + i] = (uint8_t)(e[i] | (e[i + 16] << 4));
 }
 
+// GGUF Q4_K super-block (ggml block_q4_K, 144 B: fp16 d, fp16 dmin, 12 bytes of 6-bit scales and
+// mins, 128 code bytes) -> codes [N][K/2] (the 128 code bytes as they are) + 5 dwords per
+// super-block in hdr [N][K/256][5]: {d | dmin << 16}, then {sc(2p), sc(2p+1), m(2p), m(2p+1)} for
+// pairs p = 0..3.  The 12-byte field: j < 4: sc = b[j] & 63, m = b[j + 4] & 63; j >= 4: sc =
+// (b[j + 4] & 15) | (b[j - 4] >> 6) << 4, m = (b[j + 4] >> 4) | (b[j] >> 6) << 4.
+__device__ __forceinline__ void k4_scale_min(const uint8_t* b, int j, uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = b[j] & 63;
+    m = b[j + 4] & 63;
+  } else {
+    sc = (b[j + 4] & 15) | ((b[j - 4] >> 6) << 4);
+    m = (b[j + 4] >> 4) | ((b[j] >> 6) << 4);
+  }
+}
+
+__global__ void q4k_repack_kernel(const uint8_t* __restrict__ blocks, uint8_t* __restrict__ qs,
+                                  uint32_t* __restrict__ hdr, int N, int K) {
+  const int nb = K >> 8;
+  const long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= (long long)N * nb) return;
+  const uint8_t* src = blocks + b * 144;
+  uint32_t* h = hdr + b * 5;                     // row-major over (row, super-block)
+  h[0] = (uint32_t)src[0] | ((uint32_t)src[1] << 8) | ((uint32_t)src[2] << 16) | ((uint32_t)src[3] << 24);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    uint32_t s0, m0, s1, m1;
+    k4_scale_min(src + 4, 2 * p, s0, m0);
+    k4_scale_min(src + 4, 2 * p + 1, s1, m1);
+    h[1 + p] = s0 | (s1 << 8) | (m0 << 16) | (m1 << 24);
+  }
+  uint8_t* dst = qs + b * 128;
+#pragma unroll
+  for (int i = 0; i < 128; ++i) dst[i] = src[16 + i];
+}
+
+// Q4_K weights as T rows out[n * ldo + k]: one thread per code dword (elements 4 apart in two
+// runs 32 apart), through the GEMV's own Fmt<FMT_Q4K> arithmetic.
+template <typename T>
+__global__ void dequant_q4k_kernel(const uint32_t* __restrict__ qs, const uint32_t* __restrict__ hdr,
+                                   T* __restrict__ out, long long ldo, int N, int K) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per = K >> 3;                        // code dwords per row
+  if (i >= (long long)N * per) return;
+  const int row = (int)(i / per), w = (int)(i - (long long)row * per);
+  const int sb = w >> 5, b0 = 4 * (w & 31), p = b0 >> 5, l0 = b0 & 31;
+  const uint32_t* h = hdr + ((size_t)row * (K >> 8) + sb) * 5;
+  const h2 dd = as_h2(h[0]);
+  const uint32_t sm = h[1 + p];
+  const float dsa = (float)dd.x * ubyte_f32(sm, 0), dsb = (float)dd.x * ubyte_f32(sm, 1);
+  const float dma = (float)dd.y * ubyte_f32(sm, 2), dmb = (float)dd.y * ubyte_f32(sm, 3);
+  const uint32_t q = qs[i], lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+  T* o = out + (size_t)row * ldo + 256 * sb + 64 * p + l0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    o[t] = (T)(half_t)__builtin_fmaf(dsa, ubyte_f32(lo, t), -dma);
+    o[32 + t] = (T)(half_t)__builtin_fmaf(dsb, ubyte_f32(hi, t), -dmb);
+  }
+}
+
 // out[n][k] = code * scale as fp32, through the GEMV's own unpack helpers.
 __global__ void dequant_i8_kernel(const uint32_t* __restrict__ q, const half_t* __restrict__ s,
                                   float* __restrict__ out, int N, int K) {
@@ -188,6 +247,17 @@ int afx_q4_0_repack(const void* blocks, void* qs, void* d, int N, int K, void* s
   return check_launch("afx_q4_0_repack");
 }
 
+// GGUF Q4_K super-blocks [N][K/256] (144 B each) -> codes qs [N][K/2] + headers hdr [N][K/256][5] u32.
+int afx_q4_k_repack(const void* blocks, void* qs, void* hdr, int N, int K, void* stream) {
+  AFX_REQUIRE(blocks && qs && hdr, "afx_q4_k_repack: null pointer");
+  AFX_REQUIRE(N >= 1 && K >= 256 && K % 256 == 0, "afx_q4_k_repack: K=%d must be a positive multiple of 256", K);
+  AFX_REQUIRE(((uintptr_t)hdr & 3) == 0, "afx_q4_k_repack: hdr must be 4-byte aligned");
+  const long long nblk = (long long)N * (K / 256);
+  hipLaunchKernelGGL(q4k_repack_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)blocks, (uint8_t*)qs, (uint32_t*)hdr, N, K);
+  return check_launch("afx_q4_k_repack");
+}
+
 // Inverse of afx_q4_0_repack (round-trip check back to GGUF bytes).
 int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, void* stream) {
   AFX_REQUIRE(blocks && qs && d, "afx_q4_0_unpack: null pointer");
@@ -199,12 +269,13 @@ int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, v
 }
 
 // Dequantise through the GEMV unpack path: fmt 0 = int8 [N][K] + s[N]; fmt 1 = Q4_0 superblock.
-// fmt 0 int8, 1 Q4_0 (superblock layout), 3 blockwise, 4 int4 codebook -> fp16 rows of stride ldo.
+// fmt 0 int8, 1 Q4_0 (superblock layout), 3 blockwise, 4 int4 codebook, 5 Q4_K -> fp16 rows of stride ldo.
 int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,
                     void* stream) {
   AFX_REQUIRE(w && scale && out, "afx_dequant_f16: null pointer");
-  AFX_REQUIRE(fmt == 0 || fmt == 1 || fmt == 3 || fmt == 4, "afx_dequant_f16: format %d has no scales to apply", fmt);
-  const int kq = fmt == 1 ? 128 : fmt == 3 ? 32 : 8;
+  AFX_REQUIRE(fmt == 0 || fmt == 1 || fmt == 3 || fmt == 4 || fmt == 5,
+              "afx_dequant_f16: format %d has no scales to apply", fmt);
+  const int kq = fmt == 1 ? 128 : fmt == 3 ? 32 : fmt == 5 ? 256 : 8;
   AFX_REQUIRE(N >= 1 && K >= kq && K % kq == 0, "afx_dequant_f16: K=%d must be a multiple of %d", K, kq);
   AFX_REQUIRE(ldo >= K && ldo % 8 == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)w & 7) == 0,
               "afx_dequant_f16: out rows must be 16-byte aligned (ldo %% 8 == 0) and ldo >= K");
@@ -213,6 +284,9 @@ int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long l
   if (fmt == 4)
     hipLaunchKernelGGL(dequant_l4_kernel<half_t>, grid, dim3(256), 0, (hipStream_t)stream, (const uint32_t*)w,
                        (const half_t*)scale, (half_t*)out, ldo, N, K);
+  else if (fmt == 5)
+    hipLaunchKernelGGL(dequant_q4k_kernel<half_t>, grid, dim3(256), 0, (hipStream_t)stream, (const uint32_t*)w,
+                       (const uint32_t*)scale, (half_t*)out, ldo, N, K);
   else if (fmt == 0)
     hipLaunchKernelGGL(dequant_f16_kernel<FMT_I8>, grid, dim3(256), 0, (hipStream_t)stream, w,
                        (const half_t*)scale, (half_t*)out, ldo, N, K);
@@ -242,6 +316,12 @@ int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, in
     const long long n8 = (long long)N * (K / 8);
     hipLaunchKernelGGL(dequant_l4_kernel<float>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, (const uint32_t*)w, (const half_t*)scale, out, (long long)K, N, K);
+  } else if (fmt == 5) {
+    AFX_REQUIRE(K % 256 == 0 && ((uintptr_t)w & 3) == 0 && ((uintptr_t)scale & 3) == 0,
+                "afx_dequant: Q4_K K must be a multiple of 256");
+    const long long n8 = (long long)N * (K / 8);
+    hipLaunchKernelGGL(dequant_q4k_kernel<float>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint32_t*)w, (const uint32_t*)scale, out, (long long)K, N, K);
   } else if (fmt == 3) {
     AFX_REQUIRE(K % 32 == 0 && ((uintptr_t)w & 3) == 0, "afx_dequant: blockwise K must be a multiple of 32");
     const long long nw = (long long)N * (K / 4);

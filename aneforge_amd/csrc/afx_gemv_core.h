@@ -5,7 +5,7 @@
 
 namespace afx {
 
-enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2, FMT_BW = 3, FMT_L4 = 4 };
+enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2, FMT_BW = 3, FMT_L4 = 4, FMT_Q4K = 5 };
 
 // ---- x sources: global memory or the LDS copy written by the norm prologue ----
 template <int N8>
@@ -187,15 +187,81 @@ template <> struct Fmt<FMT_L4> {
   }
 };
 
+// GGUF Q4_K (ggml block_q4_K: 256-weight super-blocks of 8 sub-blocks of 32 with 6-bit scales and
+// mins; the reference dequantises it with gguf-py through GGUFView.get, aneforge/_gguf.py:34-39),
+// repacked by afx_q4_k_repack: codes [N][K/2] keep each super-block's 128 code bytes in ggml order
+// (byte 32p + l: element 64p + l in the low nibble, 64p + 32 + l in the high nibble), and the scale
+// array holds 5 dwords per super-block: {fp16 d | fp16 dmin << 16}, then for each sub-block pair p
+// the bytes {sc(2p), sc(2p + 1), m(2p), m(2p + 1)} (the 6-bit fields, unpacked).  The weight is the
+// reference's fp16(d*sc*q - dmin*m) with gguf-py's float32 steps: d*sc and dmin*m are exact in
+// fp32, and so is d*sc*q (17 + 4 bits), so one fma rounds exactly where gguf-py's subtraction does.
+// Chunk c of a row: super-block c / 8, pair p = (c / 2) % 4, half h = c % 2; its low nibbles are
+// elements 256(c / 8) + 64p + 16h + 0..15 (sub-block 2p), its high nibbles those + 32 (2p + 1).
+__device__ __forceinline__ float ubyte_f32(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
+template <> struct Fmt<FMT_Q4K> {
+  using Ctx = NoCtx;
+  static constexpr int kWeightsPerChunk = 32;
+  static constexpr int kXH2 = 16;
+  __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
+  // x of the two 16-element runs: x[0..7] the low-nibble run, x[8..15] the high-nibble run
+  __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) {
+    const half_t* p = xrow + 256 * (c >> 3) + 64 * ((c >> 1) & 3) + 16 * (c & 1);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const u4 v = *(const u4*)(p + 32 * r + 8 * i);
+        x[8 * r + 4 * i + 0] = as_h2(v.x); x[8 * r + 4 * i + 1] = as_h2(v.y);
+        x[8 * r + 4 * i + 2] = as_h2(v.z); x[8 * r + 4 * i + 3] = as_h2(v.w);
+      }
+  }
+  // d.x = {d, dmin} of the super-block, d.y = the pair's scale and min bytes
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, const Ctx&, float acc) {
+    const h2 dd = as_h2(d.x);
+    const float dsup = (float)dd.x, dmin = (float)dd.y;
+    const float dsa = dsup * ubyte_f32(d.y, 0), dsb = dsup * ubyte_f32(d.y, 1);
+    const float dma = dmin * ubyte_f32(d.y, 2), dmb = dmin * ubyte_f32(d.y, 3);
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {                  // dword k: elements 4k..4k+3 of both runs
+      uint32_t lo = wd[k] & 0x0F0F0F0Fu, hi = (wd[k] >> 4) & 0x0F0F0F0Fu;
+      // opaque to the optimiser, so each byte converts with one v_cvt_f32_ubyte<n> (it would
+      // otherwise re-extract every nibble from wd with a v_bfe first)
+      asm("" : "+v"(lo), "+v"(hi));
+      h2 a0, a1, b0, b1;
+      a0.x = (half_t)__builtin_fmaf(dsa, ubyte_f32(lo, 0), -dma);
+      a0.y = (half_t)__builtin_fmaf(dsa, ubyte_f32(lo, 1), -dma);
+      a1.x = (half_t)__builtin_fmaf(dsa, ubyte_f32(lo, 2), -dma);
+      a1.y = (half_t)__builtin_fmaf(dsa, ubyte_f32(lo, 3), -dma);
+      b0.x = (half_t)__builtin_fmaf(dsb, ubyte_f32(hi, 0), -dmb);
+      b0.y = (half_t)__builtin_fmaf(dsb, ubyte_f32(hi, 1), -dmb);
+      b1.x = (half_t)__builtin_fmaf(dsb, ubyte_f32(hi, 2), -dmb);
+      b1.y = (half_t)__builtin_fmaf(dsb, ubyte_f32(hi, 3), -dmb);
+      acc = dot2(a0, x[2 * k], acc);
+      acc = dot2(a1, x[2 * k + 1], acc);
+      acc = dot2(b0, x[8 + 2 * k], acc);
+      acc = dot2(b1, x[8 + 2 * k + 1], acc);
+    }
+    return acc;
+  }
+};
+
 // Block scales for a chunk: Q4, the 4 fp16 of its superblock; blockwise, the 2 fp16 of chunks
-// 4i..4i+3 and the half that is the chunk's; other formats have none.
+// 4i..4i+3 and the half that is the chunk's; Q4_K, {d, dmin} and the pair's scale/min bytes;
+// other formats have none.
 template <int FMT>
 __device__ __forceinline__ u2 load_scales(const half_t* drow, int c) {
   if constexpr (FMT == FMT_Q4) return *(const u2*)(drow + 4 * (c >> 2));
   else if constexpr (FMT == FMT_BW) return (u2){*(const uint32_t*)(drow + 2 * (c >> 2)), (uint32_t)((c >> 1) & 1)};
-  else return (u2){0u, 0u};
+  else if constexpr (FMT == FMT_Q4K) {
+    const uint32_t* q = (const uint32_t*)drow + 5 * (c >> 3);
+    return (u2){q[0], q[1 + ((c >> 1) & 3)]};
+  } else return (u2){0u, 0u};
 }
-// Whether the format carries per-block scales in a [N][K/32] array.
-template <int FMT> constexpr bool has_block_scales() { return FMT == FMT_Q4 || FMT == FMT_BW; }
+// Whether the format carries per-block scales in a per-row array, and that row's length in halves.
+template <int FMT> constexpr bool has_block_scales() { return FMT == FMT_Q4 || FMT == FMT_BW || FMT == FMT_Q4K; }
+template <int FMT> __host__ __device__ constexpr long long scale_row_halves(int K) {
+  return FMT == FMT_Q4K ? (long long)(K >> 8) * 10 : (long long)(K >> 5);
+}
 
 }  // namespace afx

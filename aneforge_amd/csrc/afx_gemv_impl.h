@@ -80,7 +80,7 @@ struct GemvArgs {
 constexpr int kStageUnroll = 4;     // 16-byte staging loads per thread in flight per batch
 constexpr int kBufDword3 = 0x00020000;   // raw buffer descriptor word 3 (gfx9 family)
 
-template <int FMT> struct Units { static constexpr int value = FMT == FMT_Q4 || FMT == FMT_L4 ? 2 : 4; };
+template <int FMT> struct Units { static constexpr int value = FMT == FMT_Q4 || FMT == FMT_L4 || FMT == FMT_Q4K ? 2 : 4; };
 
 // Bytes of LDS the kernel needs: staged x rows, gamma, and the cross-wave norm partials.
 __host__ __device__ inline size_t gemv_lds_bytes(int Mt, int K, bool norm) {
@@ -261,7 +261,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;   // a tail row is computed, never stored
     wr[r] = make_rsrc((const unsigned char*)a.w + (size_t)row * rowbytes, rowbytes);
-    if constexpr (has_block_scales<FMT>()) dr[r] = make_rsrc(a.scale + (size_t)row * (K >> 5), K >> 4);
+    if constexpr (has_block_scales<FMT>())
+      dr[r] = make_rsrc(a.scale + (size_t)row * scale_row_halves<FMT>(K), 2 * scale_row_halves<FMT>(K));
   }
   u4 wA[U][R], wB[U][R];
   u2 dA[U][R], dB[U][R];
@@ -274,6 +275,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         w[u][r] = buf_load16(wr[r], c * 16);
         if constexpr (FMT == FMT_Q4) d[u][r] = buf_load8(dr[r], (c >> 2) * 8);
         if constexpr (FMT == FMT_BW) d[u][r] = (u2){buf_load4(dr[r], (c >> 2) * 4), (uint32_t)((c >> 1) & 1)};
+        if constexpr (FMT == FMT_Q4K)       // past K both read as zero: d = dmin = 0, weight 0
+          d[u][r] = (u2){buf_load4(dr[r], (c >> 3) * 20), buf_load4(dr[r], (c >> 3) * 20 + 4 + 4 * ((c >> 1) & 3))};
       }
     }
   };
@@ -451,7 +454,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;
     const u4* wr = (const u4*)((const unsigned char*)a.w + (size_t)row * Fmt<FMT>::row_bytes(K));
-    const half_t* dr = has_block_scales<FMT>() ? a.scale + (size_t)row * (K >> 5) : nullptr;
+    const half_t* dr = has_block_scales<FMT>() ? a.scale + (size_t)row * scale_row_halves<FMT>(K) : nullptr;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int c = 64 * u + lane;
@@ -526,6 +529,8 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
         if constexpr (FMT == FMT_Q4) {
           dv.x = ok ? dv.x : 0u;
           dv.y = ok ? dv.y : 0u;
+        } else if constexpr (FMT == FMT_Q4K) {
+          dv.x = ok ? dv.x : 0u;                     // d = dmin = 0: weight 0 for any code
         } else if constexpr (FMT != FMT_L4) {
           wv.x = ok ? wv.x : 0u; wv.y = ok ? wv.y : 0u; wv.z = ok ? wv.z : 0u; wv.w = ok ? wv.w : 0u;
         }
@@ -580,14 +585,14 @@ gemv_fn pick_gemv_row_u(int eg, int R, int norm) {
 __host__ __device__ inline int fast_units(int fmt, int nchunks) {
   const int u = (nchunks + 63) / 64;
   if (fmt == FMT_I8 || fmt == FMT_BW) return u == 4 || u == 11 ? u : 0;
-  if (fmt == FMT_Q4 || fmt == FMT_L4) return u == 2 || u == 6 ? u : 0;
+  if (fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K) return u == 2 || u == 6 ? u : 0;
   return u == 8 ? u : 0;
 }
 template <int FMT>
 gemv_fn pick_gemv_row(int eg, int R, int norm, int U) {
   if constexpr (FMT == FMT_I8 || FMT == FMT_BW)
     return U == 11 ? pick_gemv_row_u<FMT, 11>(eg, R, norm) : pick_gemv_row_u<FMT, 4>(eg, R, norm);
-  else if constexpr (FMT == FMT_Q4 || FMT == FMT_L4)
+  else if constexpr (FMT == FMT_Q4 || FMT == FMT_L4 || FMT == FMT_Q4K)
     return U == 6 ? pick_gemv_row_u<FMT, 6>(eg, R, norm) : pick_gemv_row_u<FMT, 2>(eg, R, norm);
   else return pick_gemv_row_u<FMT, 8>(eg, R, norm);
 }
@@ -598,10 +603,12 @@ gemv_fn pick_gemv_q4(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_f16(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_bw(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_l4(int mt, int eg, int R, int xs);
+gemv_fn pick_gemv_q4k(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_row_i8(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_q4(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_f16(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_bw(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_l4(int eg, int R, int norm, int U);
+gemv_fn pick_gemv_row_q4k(int eg, int R, int norm, int U);
 
 }  // namespace afx

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(MoeArgs a) {
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;
     wrow[r] = wbase + (size_t)row * rb;
-    drow[r] = has_block_scales<FMT>() ? sbase + (size_t)row * (K >> 5) : nullptr;
+    drow[r] = has_block_scales<FMT>() ? sbase + (size_t)row * scale_row_halves<FMT>(K) : nullptr;
   }
   const int nchunks = K / Fmt<FMT>::kWeightsPerChunk;
   typename Fmt<FMT>::Ctx fctx[R];
@@ -212,20 +212,27 @@ static moe_fn pick_moe(int R) {
 }
 
 static int moe_launch(int fmt, MoeArgs& a, int E, int R, hipStream_t stream, const char* what) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 4, "%s: unknown weight format %d", what, fmt);
-  const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : fmt == FMT_BW ? 64 : fmt == FMT_L4 ? 32 : 8;
+  AFX_REQUIRE(fmt >= 0 && fmt <= 5, "%s: unknown weight format %d", what, fmt);
+  const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : fmt == FMT_BW ? 64 : fmt == FMT_L4 ? 32
+               : fmt == FMT_Q4K ? 256 : 8;
   AFX_REQUIRE(a.K % kq == 0, "%s: K=%d must be a multiple of %d", what, a.K, kq);
   AFX_REQUIRE(a.w && a.x && a.y && a.cnt && a.list, "%s: null pointer", what);
   AFX_REQUIRE(fmt == FMT_F16 || a.scale, "%s: quantized weights need scales", what);
   moe_fn fn = fmt == FMT_I8 ? pick_moe<FMT_I8>(R) : fmt == FMT_Q4 ? pick_moe<FMT_Q4>(R)
-            : fmt == FMT_BW ? pick_moe<FMT_BW>(R) : fmt == FMT_L4 ? pick_moe<FMT_L4>(R) : pick_moe<FMT_F16>(R);
+            : fmt == FMT_BW ? pick_moe<FMT_BW>(R) : fmt == FMT_L4 ? pick_moe<FMT_L4>(R)
+            : fmt == FMT_Q4K ? pick_moe<FMT_Q4K>(R) : pick_moe<FMT_F16>(R);
   const int gx = (a.N + 4 * R - 1) / (4 * R);
   hipLaunchKernelGGL(fn, dim3(gx, E), dim3(256), 0, stream, a);
   return check_launch(what);
 }
 
 static long long fmt_row_bytes(int fmt, int K) {
-  return fmt == FMT_I8 || fmt == FMT_BW ? K : fmt == FMT_Q4 || fmt == FMT_L4 ? K / 2 : 2LL * K;
+  return fmt == FMT_I8 || fmt == FMT_BW ? K : fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K ? K / 2 : 2LL * K;
+}
+// Elements (halves) of one expert's scale array: rows of `rows` weights over K.
+static long long fmt_scale_halves(int fmt, long long rows, int K) {
+  return fmt == FMT_Q4 || fmt == FMT_BW ? rows * (K / 32) : fmt == FMT_L4 ? rows * 16
+       : fmt == FMT_Q4K ? rows * (K / 256) * 10 : rows;
 }
 
 }  // namespace afx
@@ -264,7 +271,7 @@ int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int
   a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)x; a.ldx = D; a.y = act; a.ldy = F;
   a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = 2 * F; a.K = D; a.epi = 1; a.x_by_token = 1;
   a.w_es = fmt_row_bytes(fmt, D) * 2 * F;
-  a.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? 2LL * F * (D / 32) : fmt == FMT_L4 ? 2LL * F * 16 : 2LL * F;
+  a.s_es = fmt_scale_halves(fmt, 2LL * F, D);
   const int R = rows_hint == 1 || rows_hint == 2 || rows_hint == 4 ? (rows_hint < 2 ? 2 : rows_hint) : 4;
   return moe_launch(fmt, a, E, R, (hipStream_t)stream, "afx_moe_gateup");
 }
@@ -285,7 +292,7 @@ int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int
   a.w = w; a.scale = (const half_t*)scale; a.x = (const half_t*)act; a.ldx = F; a.y = y; a.ldy = D;
   a.cnt = cnt; a.list = list; a.T = T; a.k = k; a.N = D; a.K = F; a.epi = 0; a.x_by_token = 0;
   a.w_es = fmt_row_bytes(fmt, F) * D;
-  a.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? (long long)D * (F / 32) : fmt == FMT_L4 ? (long long)D * 16 : (long long)D;
+  a.s_es = fmt_scale_halves(fmt, D, F);
   const int R = rows_hint == 1 || rows_hint == 2 || rows_hint == 4 ? rows_hint : 4;
   return moe_launch(fmt, a, E, R, (hipStream_t)stream, "afx_moe_down");
 }

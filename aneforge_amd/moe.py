@@ -10,7 +10,7 @@ GEMVs all run on the device (afx_moe_*), so a MoE layer stays inside the capture
 Canonical per-layer weights (as the reference): mlp_norm, router [E, dim],
 wgate_exps / wup_exps [E, ffn, dim], wdown_exps [E, ffn, dim] (down stored transposed for the
 batched act @ wdown); Qwen2-MoE adds wgate_sh / wup_sh / wdown_sh / shared_gate.  Expert
-weights may also arrive as already-encoded QuantizedWeight stacks (GGUF Q4_0 from load_gguf),
+weights may also arrive as already-encoded QuantizedWeight stacks (GGUF Q4_0 / Q4_K / Q8_0 from load_gguf),
 in which case their codes are streamed as they are."""
 from __future__ import annotations
 
@@ -96,7 +96,14 @@ class MoEDecode:
             gate = [E.per_tensor(g_[e], compress) for e in range(self.E)]
             up = [E.per_tensor(u_[e], compress) for e in range(self.E)]
             down = [E.per_tensor(np.ascontiguousarray(d_[e].T), compress) for e in range(self.E)]
-        if isinstance(gate, (list, tuple)):          # per-expert QuantizedWeight lists
+        if isinstance(gate, (list, tuple)) or isinstance(down, (list, tuple)):
+            # per-expert matrices: QuantizedWeight codes (GGUF Q4_0 / Q4_K / Q8_0), with float stacks of
+            # a file's other types split per expert alongside ([F, D] gate/up, [D, F] down)
+            if not isinstance(gate, (list, tuple)):
+                gate, up = list(np.asarray(gate, np.float32)), list(np.asarray(up, np.float32))
+            if not isinstance(down, (list, tuple)):
+                d_ = np.asarray(down, np.float32)
+                down = [np.ascontiguousarray(d_[e].T) for e in range(self.E)]
             F = gate[0].shape[0]
             gu = E._cat([E._interleave(g, u) for g, u in zip(gate, up)])
             dn = E._cat(list(down))                   # [E*D, F] rows
@@ -289,7 +296,7 @@ def load_gguf(path: str, n_layers: int | None = None, compress: str | None = Non
         extra={"n_experts": E, "n_experts_per_tok": k, "norm_topk_prob": arch != "qwen2moe"})
 
     def experts(name):
-        """An expert stack: per-expert QuantizedWeight when the file holds Q4_0 codes, else fp16."""
+        """An expert stack: per-expert QuantizedWeight when the file holds Q4_0 / Q4_K / Q8_0 codes, else fp16."""
         q = gg.quantized(name)
         if q is not None:
             return q

@@ -60,7 +60,9 @@ int afx_event_destroy(void* ev);
  * (aneforge/_blob.py:46-56, constexpr_blockwise_shift_scale in aneforge/_compile.py:112-188);
  * 4: compress="int4", palettize_lut4's packed indices [N][K/2] (column 2j in the low nibble of byte
  * j) + a 16-entry fp16 codebook per row scale[N][16], weight codebook[n][index] (aneforge/_blob.py:
- * 28-43, constexpr_lut_to_dense in aneforge/_compile.py:149; vector kernels at any M). */
+ * 28-43, constexpr_lut_to_dense in aneforge/_compile.py:149; vector kernels at any M);
+ * 5: GGUF Q4_K after afx_q4_k_repack, weight fp16(d*sc*q - dmin*m) as the reference's
+ * GGUFView.get produces it (aneforge/_gguf.py:34-39; K % 256 == 0, vector kernels at any M). */
 int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                int M, int N, int K, const void* bias, const void* residual, int out_f32,
                int rows_hint, void* stream);
@@ -89,10 +91,15 @@ int afx_qkv_rope_kv(int fmt, const void* w, const void* scale, const void* h, in
  * gguf.quants.dequantize, aneforge/_gguf.py:34-39, which this keeps in 4-bit form). */
 int afx_q4_0_repack(const void* blocks, void* qs, void* d, int N, int K, void* stream);
 int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, void* stream);
+/* GGUF Q4_K super-blocks [N][K/256] (144 B: fp16 d, fp16 dmin, 12 B of 6-bit scales/mins, 128 B of
+ * codes; reference: GGUFView.get -> gguf.quants.dequantize, aneforge/_gguf.py:34-39, kept 4-bit here)
+ * -> codes qs [N][K/2] (the code bytes as they are) + hdr [N][K/256][5] u32 ({d | dmin << 16}, then
+ * per sub-block pair p the bytes {sc(2p), sc(2p+1), m(2p), m(2p+1)}), the fmt 5 weight/scale pair. */
+int afx_q4_k_repack(const void* blocks, void* qs, void* hdr, int N, int K, void* stream);
 /* Dequantise through the GEMV's own unpack path into fp32 (bit-exact check of
  * quantize_per_row / Q4_0 / quantize_blockwise reconstruction, aneforge/_blob.py:20-25, 46-56). */
 int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream);
-/* The same weights as fp16 rows out[n * ldo + k] (fmt 0 int8, 1 Q4_0, 3 blockwise, 4 int4): the fp16 values the
+/* The same weights as fp16 rows out[n * ldo + k] (fmt 0 int8, 1 Q4_0, 3 blockwise, 4 int4, 5 Q4_K): the fp16 values the
  * reference multiplies with -- for Q4_0 the fp16 cast of GGUFView.get (aneforge/_gguf.py:34-39).  The
  * batched prefill expands formats its GEMM does not read (Q4_0) into fp16 this way, one matrix at a time. */
 int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,

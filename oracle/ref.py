@@ -18,6 +18,7 @@ Pinning status (see tests/test_oracle.py):
   quantize_blockwise                    pinned: closed form + reference property tests
   dequant_blockwise                     pinned: KAT (an fp16 round-half-even tie of the product)
   dequant_lut4                          pinned: KAT (hand-packed nibbles -> their codebook entries)
+  dequant_q4_k(_f16)                    pinned: KAT (closed-form block) + element-by-element block encoder
   rms_norm                              pinned: torch + invariants
   rope_tables / rope / llama3 scaling    pinned: transformers' rope utilities + HF formula
   attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
@@ -133,6 +134,40 @@ def dequant_q4_0_f16(blocks, N, K):
     (code-8)*d taken in fp32, then converted to float16 (GGUFView.get's default dtype,
     aneforge/_gguf.py:34-39).  Returned as fp32 holding those fp16 values."""
     return dequant_q4_0(blocks, N, K).astype(f16).astype(np.float32)
+
+
+def dequant_q4_k(blocks):
+    """GGUF Q4_K super-blocks uint8 [n, 144] -> fp32 weights [n, 256], the way gguf-py's Q4_K
+    dequantiser evaluates ggml's block_q4_K (the reference calls it through GGUFView.get,
+    aneforge/_gguf.py:34-39): fp16 d and dmin at bytes 0-3; a 12-byte field of 6-bit scales and
+    mins (ggml get_scale_min_k4: sub-block j < 4 takes sc = b[j] & 63, m = b[j+4] & 63; j >= 4
+    takes the low 4 bits from b[j+4] (sc low nibble, m high nibble) and the top 2 bits from bits
+    6-7 of b[j-4] (sc) and b[j] (m)); 128 code bytes where byte 32c + l holds element 64c + l in
+    its low nibble and 64c + 32 + l in its high nibble.  Weight = (d*sc) * q - (dmin*m), each step
+    in float32."""
+    b = np.asarray(blocks, np.uint8).reshape(-1, 144)
+    out = np.empty((b.shape[0], 256), np.float32)
+    d = b[:, 0:2].copy().view(f16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(f16).astype(np.float32)[:, 0]
+    f = b[:, 4:16].astype(np.int64)
+    for j in range(8):
+        if j < 4:
+            sc, m = f[:, j] & 63, f[:, j + 4] & 63
+        else:
+            sc = (f[:, j + 4] & 15) | ((f[:, j - 4] >> 6) << 4)
+            m = (f[:, j + 4] >> 4) | ((f[:, j] >> 6) << 4)
+        c, h = j // 2, j % 2
+        q = ((b[:, 16 + 32 * c:16 + 32 * c + 32] >> (4 * h)) & 15).astype(np.float32)
+        dl = (d * sc.astype(np.float32)).astype(np.float32)
+        ml = (dmin * m.astype(np.float32)).astype(np.float32)
+        out[:, 32 * j:32 * j + 32] = dl[:, None] * q - ml[:, None]
+    return out
+
+
+def dequant_q4_k_f16(blocks, N, K):
+    """A GGUF Q4_K tensor [N, K] as the fp16 weights the reference multiplies with (GGUFView.get's
+    fp16 cast of the float32 dequantisation), returned as fp32 holding those fp16 values."""
+    return dequant_q4_k(blocks).reshape(N, K).astype(f16).astype(np.float32)
 
 
 def quantize_q4_0(W):

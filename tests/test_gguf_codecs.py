@@ -225,7 +225,10 @@ def test_gguf_file_with_k_quant_tensors_reads_like_the_blocks(tmp_path):
     assert got.shape == (rows, K) and got.dtype == np.float16
     want = _gguf.dequantize_blocks(_gguf.GGML["Q4_K"], raw).reshape(rows, K).astype(np.float16)
     np.testing.assert_array_equal(got, want)
-    assert g.quantized("w") is None                    # only Q4_0 stays packed on the device
+    q = g.quantized("w")                               # Q4_K streams as its own codes on the device
+    assert q.fmt == "q4_k" and q.shape == (rows, K)
+    assert np.array_equal(q.codes, raw.reshape(rows, K // 256, 144)[:, :, 16:].reshape(rows, K // 2))
+    np.testing.assert_array_equal(q.dequant().astype(np.float16), want)   # the same fp16 weights as get()
 
 
 def test_unsupported_types_are_named():

@@ -370,3 +370,27 @@ def test_palettize_lut4_matches_reference_vectors():
         assert packed.dtype == np.uint8 and cb.dtype == np.float16, name
         np.testing.assert_array_equal(packed, z[f"{name}__packed"], err_msg=name)
         np.testing.assert_array_equal(cb.view(np.uint16), z[f"{name}__codebook"].view(np.uint16), err_msg=name)
+
+
+def test_dequant_q4_k_kat_and_encoder():
+    # closed form: d = 0.5, dmin = 0.25, scale_j = j + 1, min_j = 2j, every code 3
+    # -> w = 0.5 (j + 1) 3 - 0.25 (2j) = 1.5 + j for the 32 elements of sub-block j
+    from test_gguf_codecs import enc_q4_k
+    blk = np.frombuffer(enc_q4_k(0.5, 0.25, [j + 1 for j in range(8)], [2 * j for j in range(8)], [3] * 256), np.uint8)
+    e = np.arange(256)
+    np.testing.assert_array_equal(ref.dequant_q4_k(blk)[0], (1.5 + e // 32).astype(np.float32))
+    # element-by-element encoder: chosen 6-bit scales / mins (top bits set, so the j >= 4 packing
+    # matters) and codes decode to d*sc*q - dmin*m in float32
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        d, dmin = float(np.float16(rng.uniform(1e-3, 0.1))), float(np.float16(rng.uniform(1e-3, 0.1)))
+        sc = [int(v) for v in rng.integers(0, 64, 8)]
+        mn = [int(v) for v in rng.integers(0, 64, 8)]
+        q = [int(v) for v in rng.integers(0, 16, 256)]
+        blk = np.frombuffer(enc_q4_k(d, dmin, sc, mn, q), np.uint8)
+        want = np.array([np.float32(np.float32(d) * np.float32(sc[i // 32])) * np.float32(q[i])
+                         - np.float32(np.float32(dmin) * np.float32(mn[i // 32])) for i in range(256)], np.float32)
+        np.testing.assert_array_equal(ref.dequant_q4_k(blk)[0], want)
+    # the fp16 weights are that float32 value cast once
+    assert ref.dequant_q4_k_f16(blk, 1, 256).dtype == np.float32
+    np.testing.assert_array_equal(ref.dequant_q4_k_f16(blk, 1, 256)[0], want.astype(np.float16).astype(np.float32))

@@ -448,6 +448,10 @@ class DecodeEngine:
         self.n_forced = torch.zeros(1, dtype=torch.int32, device=dev)
         self.hist = torch.zeros(self.M + 8, dtype=torch.int32, device=dev)
         self.forced = torch.zeros(self.M + 8, dtype=torch.int32, device=dev)
+        # sampling: {temperature, top_p, top_k} and one uniform per step, both read on the device
+        self.smp_params = torch.zeros(3, dtype=torch.float64, device=dev)
+        self.uniforms = torch.zeros(self.M + 8, dtype=torch.float64, device=dev)
+        self.smp_ws = torch.empty(self.V, dtype=torch.float64, device=dev)
         if rope_tables is None:
             from .llm import rope_tables as _rt
             rope_tables = _rt(self.M, dh, cfg.rope_base, cfg.rotary_dim, cfg.rope_interleaved, cfg.rope_scaling)
@@ -458,7 +462,7 @@ class DecodeEngine:
             mixer.bind(self)
             mlp.bind(self)
         self.stream = torch.cuda.Stream()
-        self._g_fwd = self._g_dec = None
+        self._g_fwd = self._g_dec = self._g_smp = None
 
     # -- enqueue helpers (on the current stream) --
     def enqueue_layers(self):
@@ -474,12 +478,44 @@ class DecodeEngine:
         K.decode_advance(self.logits if with_logits else None, self.tok, self.pos, self.hist, self.step,
                          self.embed, self.h, self.forced, self.n_forced)
 
+    def enqueue_sample(self):
+        """The step's token from the logits by the device sampler, queued as forced[step]."""
+        K.sample(self.logits[0], self.smp_params, self.uniforms, step=self.step, forced=self.forced,
+                 n_forced=self.n_forced, ws=self.smp_ws)
+
     def _graphs(self):
         if self._g_dec is None:
             self._g_fwd = _Graph(self.stream, lambda: (self.enqueue_layers(), self.enqueue_advance(False)))
             self._g_dec = _Graph(self.stream, lambda: (self.enqueue_layers(), self.enqueue_head(),
                                                       self.enqueue_advance(True)))
         return self._g_fwd, self._g_dec
+
+    def set_sampling(self, temperature: float, top_p: float, top_k: int, uniforms, step0: int):
+        """Sampling parameters and the uniforms of steps step0, step0 + 1, ... (one per token)."""
+        u = np.asarray(uniforms, np.float64)
+        if step0 + len(u) > self.uniforms.numel():
+            raise ValueError("more sampled steps than the cache holds")
+        with torch.cuda.stream(self.stream):
+            self.smp_params.copy_(torch.tensor([float(temperature), float(top_p), float(top_k or 0)],
+                                               dtype=torch.float64))
+            if len(u):
+                self.uniforms[step0:step0 + len(u)].copy_(torch.from_numpy(u))
+
+    def run_sampled(self, n: int, graph: bool = True):
+        """Enqueue n decode steps whose tokens come from the device sampler (no host sync)."""
+        if graph:
+            if self._g_smp is None:
+                self._g_smp = _Graph(self.stream, lambda: (self.enqueue_layers(), self.enqueue_head(),
+                                                          self.enqueue_sample(), self.enqueue_advance(False)))
+            for _ in range(n):
+                self._g_smp.launch()
+        else:
+            with torch.cuda.stream(self.stream):
+                for _ in range(n):
+                    self.enqueue_layers()
+                    self.enqueue_head()
+                    self.enqueue_sample()
+                    self.enqueue_advance(False)
 
     # -- host control --
     def reset(self, prompt, pos0: int = 0, zero_state: bool = True):
@@ -643,10 +679,10 @@ class DecodeEngine:
         return self.logits[0].cpu().numpy()
 
     def close(self):
-        for g in (self._g_fwd, self._g_dec):
+        for g in (self._g_fwd, self._g_dec, self._g_smp):
             if g is not None:
                 g.close()
-        self._g_fwd = self._g_dec = None
+        self._g_fwd = self._g_dec = self._g_smp = None
 
     @property
     def weight_bytes(self) -> int:

@@ -48,6 +48,7 @@ SIGNATURES: dict[str, tuple] = {
     "afx_dequant_f16": (_i, [_i, _vp, _vp, _vp, _ll, _i, _i, _vp]),
     # attention
     "afx_decode_attn_ws_bytes": (_ll, [_i, _i, _i, _i, _i, _i]),
+    "afx_sample": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _ll, _vp]),
     "afx_decode_attn": (_i, [_vp, _vp, _vp, _vp, _ll, _ll, _ll, _ll, _i, _i, _i, _i, _i, _vp, _i, _vp, _ll,
                              _i, _f, _vp, _ll, _i, _vp]),
     # norms, rope, sampling, generic tensor ops

@@ -211,6 +211,20 @@ def embed(table, ids, out=None):
     return out
 
 
+def sample(logits, params, uniforms, step=None, forced=None, n_forced=None, out=None, ws=None):
+    """Device sampling of the next token from fp32 logits [V] (see afx_sample).  params: float64
+    [3] {temperature, top_p, top_k}; uniforms: float64, u = uniforms[step] (uniforms[0] without step)."""
+    _dev(logits, params, uniforms, step, forced, n_forced, out)
+    V = logits.numel()
+    if forced is None and out is None:
+        out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    if ws is None or ws.numel() < V:
+        ws = torch.empty(V, dtype=torch.float64, device=logits.device)
+    _hip.call("afx_sample", P(logits), V, P(params), P(uniforms), P(step), P(forced), P(n_forced), P(out),
+              P(ws), ws.numel() * 8, stream())
+    return out
+
+
 def decode_advance(logits, tok, pos, hist, step, embed_table=None, h=None, forced=None, n_forced=None):
     """Next token (forced prompt token or greedy argmax) + bookkeeping + embedding gather."""
     V = logits.shape[-1] if logits is not None else 0

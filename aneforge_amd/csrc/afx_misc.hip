@@ -451,6 +451,248 @@ static int make_shape(Shape5& s, int rank, const int* dim, const long long* sa, 
   return 0;
 }
 
+
+// ---- temperature / top-k / top-p sampling on the device (the reference's _sample,
+// aneforge/llm.py:406-419, with np.random.choice's inverse-CDF draw) ----
+// One workgroup of 1024 threads.  Logits are ranked by an order-preserving 32-bit key of their
+// fp32 value: logits / T is monotone in the logit and fp32 -> fp64 is exact, so the k-th largest
+// scaled logit and the top-p nucleus are thresholds on that key.  Both thresholds come from a
+// 4-pass radix select (8 bits a pass; counts for top-k, fp64 probability mass for top-p) over
+// per-wavefront LDS histograms.  Ties at the top-p threshold keep the highest indices first (what
+// np.argsort(p)[::-1] gives for tied values in a stably sorted array).  The draw: the first index
+// whose running kept mass (in index order) exceeds u * total, u = uniforms[*step].
+constexpr int kSampleThreads = 1024;
+constexpr int kSampleWaves = kSampleThreads / 64;
+
+__device__ __forceinline__ uint32_t logit_key(float x) {
+  if (x != x) x = -INFINITY;                         // NaN ranks below every number
+  const uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_logit(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+struct SampleSmem {
+  union {
+    unsigned cnt[kSampleWaves][256];
+    double mass[kSampleWaves][256];
+  } h;
+  double wsum[kSampleWaves];
+  unsigned wmax[kSampleWaves];
+  unsigned prefix, mask;
+  long long remaining;
+  double above, target;
+  long long wtie[kSampleWaves];
+  int token, last;
+};
+
+// Radix select over keys matching the current prefix.  COUNT: the key holding the remaining-th
+// largest element; otherwise the key at which the mass from the top first reaches target.
+template <bool COUNT>
+__device__ void radix_select(const float* logits, const double* e, int V, unsigned floor_key, SampleSmem& sm) {
+  const int t = threadIdx.x, wave = t >> 6;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = t; i < kSampleWaves * 256; i += kSampleThreads) {
+      if (COUNT) (&sm.h.cnt[0][0])[i] = 0u;
+      else (&sm.h.mass[0][0])[i] = 0.0;
+    }
+    __syncthreads();
+    const unsigned prefix = sm.prefix, mask = sm.mask;
+    for (int i = t; i < V; i += kSampleThreads) {
+      const unsigned k = logit_key(logits[i]);
+      if (k < floor_key || (k & mask) != prefix) continue;
+      const int bin = (k >> shift) & 255;
+      if (COUNT) atomicAdd(&sm.h.cnt[wave][bin], 1u);
+      else atomicAdd(&sm.h.mass[wave][bin], e[i]);
+    }
+    __syncthreads();
+    if (t < 256) {                                   // merge the wavefront copies in a fixed order
+      if (COUNT) {
+        unsigned c = 0;
+        for (int w = 0; w < kSampleWaves; ++w) c += sm.h.cnt[w][t];
+        sm.h.cnt[0][t] = c;
+      } else {
+        double m = 0.0;
+        for (int w = 0; w < kSampleWaves; ++w) m += sm.h.mass[w][t];
+        sm.h.mass[0][t] = m;
+      }
+    }
+    __syncthreads();
+    if (t == 0) {
+      int b = 255;
+      if (COUNT) {
+        long long acc = 0;
+        for (; b > 0 && acc + (long long)sm.h.cnt[0][b] < sm.remaining; --b) acc += sm.h.cnt[0][b];
+        sm.remaining -= acc;
+      } else {
+        double acc = sm.above;
+        for (; b > 0 && acc + sm.h.mass[0][b] < sm.target; --b) acc += sm.h.mass[0][b];
+        sm.above = acc;
+      }
+      sm.prefix |= (unsigned)b << shift;
+      sm.mask |= 255u << shift;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(
+    const float* __restrict__ logits, int V, const double* __restrict__ params, const double* __restrict__ uniforms,
+    const int* __restrict__ step, int* __restrict__ forced, int* __restrict__ n_forced, int* __restrict__ out,
+    double* __restrict__ e) {
+  __shared__ SampleSmem sm;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const double temp = params[0], top_p = params[1];
+  const long long top_k = (long long)params[2];
+  const int s = step ? step[0] : 0;
+  const double u = uniforms[s];
+
+  // 1. the largest key (greedy: the lowest index holding it, like np.argmax)
+  unsigned mk = 0;
+  for (int i = t; i < V; i += kSampleThreads) mk = max(mk, logit_key(logits[i]));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mk = max(mk, (unsigned)__shfl_xor((int)mk, m, 64));
+  if (lane == 0) sm.wmax[wave] = mk;
+  if (t == 0) { sm.token = 0x7fffffff; sm.last = -1; sm.prefix = 0u; sm.mask = 0u; sm.above = 0.0; }
+  __syncthreads();
+  mk = sm.wmax[0];
+  for (int w = 1; w < kSampleWaves; ++w) mk = max(mk, sm.wmax[w]);
+  if (!(temp > 0.0)) {
+    for (int i = t; i < V; i += kSampleThreads)
+      if (logit_key(logits[i]) == mk) { atomicMin(&sm.token, i); break; }
+    __syncthreads();
+  } else {
+    const double lgmax = (double)key_logit(mk) / temp;
+    // 2. top-k: keep the logits >= the k-th largest (ties included, as lg < kth -> -inf)
+    unsigned kfloor = 0u;
+    if (top_k > 0 && top_k < V) {
+      if (t == 0) sm.remaining = top_k;
+      __syncthreads();
+      radix_select<true>(logits, e, V, 0u, sm);
+      kfloor = sm.prefix;
+      __syncthreads();
+      if (t == 0) { sm.prefix = 0u; sm.mask = 0u; }
+    }
+    // 3. e_i = exp(lg_i - lg_max) for the kept logits, and their sum
+    double part = 0.0;
+    for (int i = t; i < V; i += kSampleThreads) {
+      const float x = logits[i];
+      const double v = logit_key(x) >= kfloor && x == x ? exp((double)x / temp - lgmax) : 0.0;
+      e[i] = v;
+      part += v;
+    }
+    part = wave_sum_f64(part);
+    if (lane == 0) sm.wsum[wave] = part;
+    __syncthreads();
+    double Z = 0.0;
+    for (int w = 0; w < kSampleWaves; ++w) Z += sm.wsum[w];
+    // 4. top-p: the smallest top set whose mass reaches top_p * Z
+    unsigned pkey = kfloor;
+    long long ntie = 0;                              // tied logits kept at pkey (0: no top-p cut)
+    if (top_p > 0.0 && top_p < 1.0) {
+      if (t == 0) sm.target = top_p * Z;
+      __syncthreads();
+      radix_select<false>(logits, e, V, kfloor, sm);
+      pkey = sm.prefix;
+      const double q = exp((double)key_logit(pkey) / temp - lgmax);
+      const double need = sm.target - sm.above;
+      ntie = need > 0.0 ? (long long)ceil(need / q) : 1;
+      if (ntie < 1) ntie = 1;
+    }
+    __syncthreads();
+    // 5. the kept set: keys above pkey, and at pkey the first ntie ties counted from the highest
+    // index down (all of them without a top-p cut).  Thread t owns indices [i0, i1).
+    const int per = (V + kSampleThreads - 1) / kSampleThreads;
+    const int i0 = min(V, t * per), i1 = min(V, i0 + per);
+    long long rties = 0;                             // ties at pkey in this thread's range
+    if (ntie)
+      for (int i = i0; i < i1; ++i) rties += logit_key(logits[i]) == pkey;
+    long long ties_after = 0;                        // ties at pkey in higher threads' ranges
+    if (ntie) {
+      long long suf = rties;                         // inclusive suffix sum within the wavefront
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) {
+        const long long o = __shfl_down(suf, m, 64);
+        if (lane + m < 64) suf += o;
+      }
+      if (lane == 0) sm.wtie[wave] = suf;
+      __syncthreads();
+      ties_after = suf - rties;
+      for (int w = wave + 1; w < kSampleWaves; ++w) ties_after += sm.wtie[w];
+    }
+    // kept mass of the range, in index order
+    double local = 0.0;
+    {
+      long long higher = ties_after + rties;         // ties at indices >= i (before visiting i)
+      for (int i = i0; i < i1; ++i) {
+        const unsigned k = logit_key(logits[i]);
+        const bool tie = ntie && k == pkey;
+        if (tie) --higher;                           // now: ties at indices > i
+        if (k >= pkey && (!tie || higher < ntie)) local += e[i];
+      }
+    }
+    // exclusive prefix of the kept mass over threads, summed in a fixed order
+    double incl = local;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const double o = __shfl_up(incl, m, 64);
+      if (lane >= m) incl += o;
+    }
+    if (lane == 63) sm.wsum[wave] = incl;
+    __syncthreads();
+    double excl = incl - local, total = 0.0;
+    for (int w = 0; w < kSampleWaves; ++w) {
+      if (w < wave) excl += sm.wsum[w];
+      total += sm.wsum[w];
+    }
+    // np.random.choice: the first index whose cumulative probability exceeds u
+    const double target = u * total;
+    int pick = 0x7fffffff, last = -1;
+    if (local > 0.0 && target < excl + local) {
+      double run = excl;
+      long long higher = ties_after + rties;
+      for (int i = i0; i < i1; ++i) {
+        const unsigned k = logit_key(logits[i]);
+        const bool tie = ntie && k == pkey;
+        if (tie) --higher;
+        if (!(k >= pkey && (!tie || higher < ntie)) || e[i] == 0.0) continue;
+        last = i;
+        run += e[i];
+        if (run > target) { pick = i; break; }
+      }
+      if (pick == 0x7fffffff && excl <= target) pick = last;   // rounding inside the range
+    }
+    if (excl <= target || local > 0.0) atomicMin(&sm.token, pick);
+    __syncthreads();
+    if (sm.token == 0x7fffffff) {                    // target at the very end: the highest kept index
+      int hi = -1;
+      long long higher = ties_after + rties;
+      for (int i = i0; i < i1; ++i) {
+        const unsigned k = logit_key(logits[i]);
+        const bool tie = ntie && k == pkey;
+        if (tie) --higher;
+        if (k >= pkey && (!tie || higher < ntie) && e[i] > 0.0) hi = i;
+      }
+      atomicMax(&sm.last, hi);
+      __syncthreads();
+      if (t == 0) sm.token = sm.last < 0 ? 0 : sm.last;
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    int tok = sm.token;
+    if (tok < 0 || tok >= V) tok = 0;
+    if (forced) forced[s] = tok;
+    if (n_forced) n_forced[0] = s + 1;
+    if (out) out[0] = tok;
+  }
+}
 }  // namespace afx
 
 using namespace afx;
@@ -514,6 +756,19 @@ int afx_decode_advance(const float* logits, int V, const int* forced, const int*
                      n_forced, tok, pos, hist, hist_cap, step, (const half_t*)embed, (half_t*)h, D,
                      vocab > 0 ? vocab : V);
   return check_launch("afx_decode_advance");
+}
+
+// params: device {temperature, top_p, top_k} as doubles; u = uniforms[*step] (uniforms[0] without
+// step).  The token goes to forced[*step] (and n_forced = *step + 1, so afx_decode_advance takes
+// it) and/or out[0].  ws: V doubles.
+int afx_sample(const float* logits, int V, const double* params, const double* uniforms, const int* step,
+               int* forced, int* n_forced, int* out, double* ws, long long ws_bytes, void* stream) {
+  AFX_REQUIRE(logits && params && uniforms && ws && V >= 1, "afx_sample: bad arguments");
+  AFX_REQUIRE(forced || out, "afx_sample: no output");
+  AFX_REQUIRE(ws_bytes >= 8LL * V, "afx_sample: workspace %lld B < %lld B", ws_bytes, 8LL * V);
+  hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, (hipStream_t)stream, logits, V, params,
+                     uniforms, step, forced, n_forced, out, ws);
+  return check_launch("afx_sample");
 }
 
 int afx_argmax(const float* x, int M, int V, int* out, void* stream) {

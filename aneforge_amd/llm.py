@@ -298,8 +298,10 @@ class LlamaPrefill:
                  temperature=0.0, top_p=1.0, top_k=0, batched_prefill=True, prefill_pad=None, on_stage=None,
                  ane_lm_head=None):
         """Autoregressive generation over the resident KV cache (aneforge/llm.py:560-633).
-        Greedy decoding runs entirely on the device (one graph replay per token, one host read
-        at the end when no eos / on_token is given).  Sampling reads the logits per token."""
+        Greedy decoding and temperature / top-k / top-p sampling run entirely on the device (one
+        graph replay per token, one host read at the end when no eos / on_token is given); the
+        sampler draws with one np.random.random_sample() per token, as the reference's
+        np.random.choice does."""
         prompt = [int(t) for t in token_ids]
         if not prompt:
             raise ValueError("generate needs at least one prompt token")
@@ -317,8 +319,15 @@ class LlamaPrefill:
         n_pre = len(prompt) - 1
         n_gen = max(0, min(max_new_tokens, M - len(prompt)))
         greedy = temperature <= 0.0
-        if greedy and use_dev and not eos and on_token is None and on_stage is None:
-            d.run(n_run, n_gen)
+        if use_dev and not eos and on_token is None and on_stage is None:
+            if greedy:
+                d.run(n_run, n_gen)
+            else:
+                # device sampling: one uniform per token from numpy's global generator, the draws
+                # the reference's per-token np.random.choice makes
+                d.run(n_run, 0)
+                d.set_sampling(temperature, top_p, top_k, np.random.random_sample(n_gen), n_pre)
+                d.run_sampled(n_gen)
             return d.history(n_pre, n_gen)
         d.run(n_run, 0)
         if on_stage is not None:
@@ -331,19 +340,18 @@ class LlamaPrefill:
             if greedy and use_dev:
                 d.run(0, 1)
                 nxt = d.history(n_pre + i, 1)[0]
-            else:
+            elif use_dev:
+                d.set_sampling(temperature, top_p, top_k, [np.random.random_sample()], n_pre + i)
+                d.run_sampled(1)
+                nxt = d.history(n_pre + i, 1)[0]
+            else:                                    # host lm_head (ane_lm_head=False)
                 with torch.cuda.stream(d.stream):
                     d.enqueue_layers()
-                    if use_dev:
-                        d.enqueue_head()
-                if use_dev:
-                    logits = d.logits_host()
-                else:
-                    d.sync()
-                    hn = d.h.float().cpu().numpy()[0]
-                    g = np.asarray(self.w["final_norm"], np.float64)
-                    hn = hn / np.sqrt((hn.astype(np.float64) ** 2).mean() + self.cfg.norm_eps) * g
-                    logits = self._host_logits(hn.astype(np.float16).astype(np.float32))
+                d.sync()
+                hn = d.h.float().cpu().numpy()[0]
+                g = np.asarray(self.w["final_norm"], np.float64)
+                hn = hn / np.sqrt((hn.astype(np.float64) ** 2).mean() + self.cfg.norm_eps) * g
+                logits = self._host_logits(hn.astype(np.float16).astype(np.float32))
                 nxt = self._sample(logits, temperature, top_p, top_k)
                 k = n_pre + i
                 with torch.cuda.stream(d.stream):

@@ -131,6 +131,14 @@ int afx_rope(const void* x, void* y, int rows, int dh, const void* cos_tab, cons
 int afx_head_norm_rope(void* x, long long seq_stride, long long head_stride, int pos_mul, const int* pos,
                        int kv_len, int heads, int M, int dh, const void* gamma, float eps, const void* cos_tab,
                        const void* sin_tab, int rope, void* stream);
+/* The next token of LlamaPrefill._sample (aneforge/llm.py:406-419) on the device: argmax (lowest
+ * index) when temperature <= 0, else logits / T, the top-k logits (ties included), the top-p nucleus
+ * (ties at its edge kept from the highest index down), and np.random.choice's draw: the first index
+ * whose cumulative kept probability exceeds u.  params: device doubles {temperature, top_p, top_k};
+ * u = uniforms[*step] (uniforms[0] when step is NULL).  The token goes to forced[*step] with
+ * n_forced = *step + 1 (afx_decode_advance then takes it) and/or out[0].  ws: V doubles. */
+int afx_sample(const float* logits, int V, const double* params, const double* uniforms, const int* step,
+               int* forced, int* n_forced, int* out, double* ws, long long ws_bytes, void* stream);
 /* host embedding gather of LlamaPrefill.step (aneforge/llm.py:593-594), on the device */
 int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vocab, void* stream);
 /* One step of the device-resident decode loop (aneforge/llm.py:584-627 step/_sample/generate):

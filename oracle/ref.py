@@ -19,6 +19,8 @@ Pinning status (see tests/test_oracle.py):
   dequant_blockwise                     pinned: KAT (an fp16 round-half-even tie of the product)
   dequant_lut4                          pinned: KAT (hand-packed nibbles -> their codebook entries)
   dequant_q4_k(_f16)                    pinned: KAT (closed-form block) + element-by-element block encoder
+  sample                                pinned: numpy's own RandomState.choice on the same draws, top-k /
+                                        top-p support and frequency properties
   rms_norm                              pinned: torch + invariants
   rope_tables / rope / llama3 scaling    pinned: transformers' rope utilities + HF formula
   attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
@@ -384,6 +386,32 @@ def decode_step(tok, pos, W, cfg, caches, tables, exact=False, trace=None):
         K, V = caches[li]
         h = decode_layer(h, lw, cfg, K, V, pos, cos[pos], sin[pos], exact, trace)
     return logits(h, W["final_norm"], W["lm_head"], cfg["norm_eps"], exact)[0]
+
+
+def sample(logits, temperature, top_p, top_k, u):
+    """LlamaPrefill._sample (aneforge/llm.py:406-419) with np.random.choice's uniform given as u:
+    argmax when temperature <= 0; else lg = logits / T in float64, the logits below the k-th largest
+    set to -inf, p = exp(lg - max) / sum, the top-p nucleus (sorted descending, the prefix whose
+    cumulative sum first reaches top_p, renormalised), then numpy's legacy choice(n, p=p): cdf =
+    cumsum(p) / cdf[-1], the token is searchsorted(cdf, u, 'right').  Ties in the nucleus sort are
+    ordered by a stable argsort (the highest index first after the reversal)."""
+    if temperature <= 0.0:
+        return int(np.argmax(logits))
+    lg = np.asarray(logits, np.float32).astype(np.float64) / temperature
+    if top_k and 0 < top_k < lg.size:
+        lg[lg < np.partition(lg, -top_k)[-top_k]] = -np.inf
+    p = np.exp(lg - lg.max())
+    p /= p.sum()
+    if 0.0 < top_p < 1.0:
+        order = np.argsort(p, kind="stable")[::-1]
+        cum = np.cumsum(p[order])
+        keep = order[:int(np.searchsorted(cum, top_p)) + 1]
+        m = np.zeros_like(p)
+        m[keep] = p[keep]
+        p = m / m.sum()
+    cdf = np.cumsum(p)
+    cdf /= cdf[-1]
+    return int(np.searchsorted(cdf, u, side="right"))
 
 
 def generate(prompt, n_new, W, cfg, M, exact=False, caches=None, start_pos=None):

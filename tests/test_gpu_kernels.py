@@ -404,6 +404,30 @@ def test_decode_attn_mask_and_causal(K):
     check_f16(host(o2)[0], want2, what="mask")
 
 
+# ----------------------------------------------------------------------------- sampling
+@pytest.mark.parametrize("V,grid", [(32000, 0.0), (1000, 0.25), (151936, 0.0)])
+def test_sample_matches_oracle(K, V, grid):
+    # temperature / top-k / top-p / the inverse-CDF draw against the oracle's restatement of the
+    # reference's _sample; grid > 0 rounds the logits so ties are common (top-k and nucleus edges)
+    say(f"device sampling V={V} ties={grid > 0}")
+    rng = np.random.default_rng(V)
+    logits = (rng.standard_normal(V) * 2.5).astype(np.float32)
+    if grid:
+        logits = (np.round(logits / grid) * grid).astype(np.float32)
+    lg = dev(logits)
+    ws = torch.empty(V, dtype=torch.float64, device="cuda")
+    us = np.concatenate([[0.0, 0.5, 1.0 - 1e-12], rng.random(21)])
+    for T, top_p, top_k in [(0.0, 1.0, 0), (1.0, 1.0, 0), (0.7, 1.0, 0), (0.8, 1.0, 40), (1.0, 0.9, 0),
+                            (0.8, 0.9, 40), (1.3, 0.5, 5), (1.0, 0.999, 0), (0.6, 0.95, 1), (2.0, 0.3, V + 5)]:
+        params = torch.tensor([T, top_p, float(top_k)], dtype=torch.float64, device="cuda")
+        uni = torch.from_numpy(us).cuda()
+        for j, u in enumerate(us):
+            step = torch.tensor([j], dtype=torch.int32, device="cuda")
+            got = int(host(K.sample(lg, params, uni, step=step, ws=ws))[0])
+            want = ref.sample(logits, T, top_p, top_k, float(u))
+            assert got == want, f"T={T} top_p={top_p} top_k={top_k} u={u}: {got} vs {want}"
+
+
 # ----------------------------------------------------------------------------- small ops
 def test_rmsnorm_rope_embed_argmax(K):
     say("rmsnorm / rope / embed / argmax")

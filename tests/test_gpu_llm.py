@@ -121,6 +121,34 @@ def test_generate_streams_and_stops_on_eos():
     assert len(m.generate([3, 4], max_new_tokens=50, max_len=6)) == 4      # cache-full stop (pos >= M-1)
 
 
+def test_device_sampling_steps_match_oracle_and_generate_paths():
+    # each sampled step: the token the device sampler queued equals the oracle's _sample on the
+    # same step's logits and uniform; generate's graph loop and its per-token loop agree
+    from aneforge_amd.llm import LlamaConfig, LlamaPrefill
+    say("device sampling in the decode engine")
+    cfg = LlamaConfig(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, ffn_dim=512, vocab=512)
+    m = LlamaPrefill(cfg, _random_weights(cfg, seed=4), compress="int8")
+    prompt = [7, 8, 9, 10]
+    n_pre = len(prompt) - 1
+    d = m._decoder(len(prompt) + 10)
+    d.prefill(prompt)
+    rng = np.random.default_rng(3)
+    for i, (T, top_p, top_k) in enumerate([(0.9, 1.0, 0), (1.2, 0.9, 0), (0.8, 0.95, 30), (1.0, 0.5, 3),
+                                            (0.7, 1.0, 50), (1.5, 0.8, 0)]):
+        u = float(rng.random())
+        d.set_sampling(T, top_p, top_k, [u], n_pre + i)
+        d.run_sampled(1, graph=i % 2 == 0)
+        tok = d.history(n_pre + i, 1)[0]
+        assert tok == ref.sample(d.logits_host(), T, top_p, top_k, u), f"step {i}"
+    np.random.seed(11)
+    a = m.generate(prompt, max_new_tokens=8, temperature=0.8, top_p=0.9, top_k=40)
+    np.random.seed(11)
+    seen = []
+    b = m.generate(prompt, max_new_tokens=8, temperature=0.8, top_p=0.9, top_k=40, on_token=seen.append)
+    assert a == b and len(a) == 8
+    m.release()
+
+
 def test_per_layer_hidden_full_7b_layer_shape():
     """One cfg3 layer at its real shape (d 4096, 32/8 heads, FFN 11008, int8 codes as cfg0)
     after a 3-token prompt: per-layer hidden cosine >= 0.9999 and fp16 tolerance."""

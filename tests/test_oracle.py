@@ -394,3 +394,35 @@ def test_dequant_q4_k_kat_and_encoder():
     # the fp16 weights are that float32 value cast once
     assert ref.dequant_q4_k_f16(blk, 1, 256).dtype == np.float32
     np.testing.assert_array_equal(ref.dequant_q4_k_f16(blk, 1, 256)[0], want.astype(np.float16).astype(np.float32))
+
+
+def test_sample_matches_numpy_choice_and_its_filters():
+    # the draw: numpy's legacy RandomState.choice(n, p=p) consumes one random_sample() and returns
+    # the inverse-CDF index; ref.sample given that same uniform must return the same token
+    rng = np.random.default_rng(21)
+    for trial in range(200):
+        V = int(rng.integers(2, 400))
+        logits = (rng.standard_normal(V) * rng.uniform(0.5, 4)).astype(np.float32)
+        T, top_p, top_k = float(rng.uniform(0.3, 2.0)), 1.0, 0
+        lg = logits.astype(np.float64) / T
+        pr = np.exp(lg - lg.max()); pr /= pr.sum()
+        want = np.random.RandomState(trial).choice(V, p=pr)
+        u = np.random.RandomState(trial).random_sample()
+        assert ref.sample(logits, T, top_p, top_k, u) == want
+    logits = (rng.standard_normal(1000) * 3).astype(np.float32)
+    us = (np.arange(4000) + 0.5) / 4000
+    # top-k: only the k largest logits are ever drawn, top_k = 1 is argmax
+    top5 = set(np.argsort(logits)[-5:].tolist())
+    assert {ref.sample(logits, 1.0, 1.0, 5, u) for u in us} == top5
+    assert {ref.sample(logits, 1.0, 1.0, 1, u) for u in us[::50]} == {int(np.argmax(logits))}
+    # top-p: the drawn set is the smallest top set whose probability reaches top_p
+    p = np.exp(logits.astype(np.float64) - logits.max()); p /= p.sum()
+    srt = np.argsort(p)[::-1]
+    n = int(np.argmax(np.cumsum(p[srt]) >= 0.7)) + 1
+    assert {ref.sample(logits, 1.0, 0.7, 0, u) for u in us} == set(srt[:n].tolist())
+    assert {ref.sample(logits, 1.0, 1e-9, 0, u) for u in us[::50]} == {int(np.argmax(logits))}
+    # frequencies over a fine grid of u follow the renormalised probabilities
+    keep = srt[:n]
+    cnt = np.bincount([ref.sample(logits, 1.0, 0.7, 0, u) for u in us], minlength=1000)
+    np.testing.assert_allclose(cnt[keep] / len(us), p[keep] / p[keep].sum(), atol=2.0 / len(us))
+    assert ref.sample(logits, 0.0, 0.5, 3, 0.3) == int(np.argmax(logits))      # T <= 0: greedy

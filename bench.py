@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--rows-hint", type=int, default=0)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--ctx", type=int, default=2048)
-    ap.add_argument("--weights", default="int8", choices=["int8", "q4_0", "blockwise", "lut4"],
+    ap.add_argument("--weights", default="int8", choices=["int8", "q4_0", "blockwise", "lut4", "q4_k"],
                     help="linear weight format of the cfg3 model for --workload prefill")
     return ap.parse_args()
 
@@ -293,6 +293,12 @@ def build_cfg3_engine(steps: int, warmup: int, fmt: str = "int8"):
             q = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
             d = (torch.rand((N, Kd // 32), device="cuda", generator=g) * 0.005).half()
             return E.Linear("q4_0", q, d, N, Kd)
+        if fmt == "q4_k":                       # random Q4_K codes + super-block headers (d, dmin, 6-bit sc/m)
+            q = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
+            h = (torch.randint(0, 64, (N, Kd // 256, 5, 4), dtype=torch.int32, device="cuda", generator=g)
+                 << (8 * torch.arange(4, dtype=torch.int32, device="cuda"))).sum(-1, dtype=torch.int32)
+            h[:, :, 0] = 0x18001400                 # d = 2^-10 (fp16 0x1400), dmin = 2^-9 (0x1800)
+            return E.Linear("q4_k", q, h.reshape(N, -1).contiguous(), N, Kd)
         if fmt == "lut4":                       # random indices + a codebook per row
             q = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
             cb = (torch.randn((N, 16), device="cuda", generator=g) * 0.02).half()

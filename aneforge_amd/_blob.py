@@ -7,6 +7,7 @@ plus GGUF Q4_0, and the packing into the layouts the HIP kernels stream.
   quantize_q4_0      ggml Q4_0 blocks (18 B / 32 weights) from fp weights
   q4_0_to_superblock GGUF Q4_0 bytes -> (qs, d) superblock layout (host twin of afx_q4_0_repack)
   q4_k_repack        GGUF Q4_K bytes -> (codes, header) the Q4_K kernels read (host twin of afx_q4_k_repack)
+  q6_k_repack        GGUF Q6_K bytes -> (codes, side words) the Q6_K kernels read (host twin of afx_q6_k_repack)
 
 The encodings must produce the reference's bytes, so their steps match the reference's; the
 code is this package's own.  The BLOBFILE container is ANE-specific and is not rebuilt."""
@@ -166,3 +167,31 @@ def q4_k_repack(blocks: np.ndarray, N: int, K: int) -> tuple[np.ndarray, np.ndar
     hdr[..., 0] = np.ascontiguousarray(b[:, :, 0:4]).view(np.uint32)[..., 0]
     hdr[..., 1:] = sc[..., 0::2] | (sc[..., 1::2] << 8) | (mn[..., 0::2] << 16) | (mn[..., 1::2] << 24)
     return codes, hdr.reshape(N, -1).view(np.int32)
+
+
+def q6_k_repack(blocks: np.ndarray, N: int, K: int) -> tuple[np.ndarray, np.ndarray]:
+    """Host twin of afx_q6_k_repack: GGUF Q6_K super-blocks (210 B: ql[128], qh[64], int8 scales[16],
+    fp16 d; element e = 128h + 32s + l has low bits nibble s >> 1 of ql[64h + 32(s & 1) + l] and high
+    bits 2s..2s+1 of qh[32h + l], scale e // 16) -> (codes uint8 [N, K/2]: per 32-weight chunk, byte j
+    of code dword k = low bits of elements 8k + j | 8k + 4 + j << 4; side int32 [N, K/32 * 3]: per
+    chunk H0, H1 (byte j of H_p: high bits of elements 16p + j, +4, +8, +12 at bits 0, 2, 4, 6) and
+    scale(0..15) | scale(16..31) << 8 | d << 16)."""
+    if K % 256:
+        raise ValueError(f"Q6_K rows need K % 256 == 0 (got {K})")
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(N, K // 256, 210)
+    ql, qh = b[:, :, 0:128].astype(np.uint32), b[:, :, 128:192].astype(np.uint32)
+    e = np.arange(256)
+    h, s, l = e >> 7, (e >> 5) & 3, e & 31
+    lo = (ql[:, :, 64 * h + 32 * (s & 1) + l] >> (4 * (s >> 1))) & 15           # [N, nb, 256]
+    hi = (qh[:, :, 32 * h + l] >> (2 * s)) & 3
+    lo = lo.reshape(N, K // 32, 4, 2, 4)                                        # [N, chunk, k, half, j]
+    codes = (lo[:, :, :, 0, :] | (lo[:, :, :, 1, :] << 4)).astype(np.uint8).reshape(N, K // 2)
+    hi = hi.reshape(N, K // 32, 2, 4, 4)                                        # [N, chunk, p, q, j]
+    H = (hi[:, :, :, 0, :] | (hi[:, :, :, 1, :] << 2) | (hi[:, :, :, 2, :] << 4) | (hi[:, :, :, 3, :] << 6))
+    H = (H << (8 * np.arange(4, dtype=np.uint32))).sum(-1).astype(np.uint32)   # [N, chunk, p]
+    sc = b[:, :, 192:208].reshape(N, K // 32, 2).astype(np.uint32)              # two per chunk
+    d = np.repeat(np.ascontiguousarray(b[:, :, 208:210]).view(np.uint16)[..., 0].astype(np.uint32), 8, axis=1)
+    side = np.empty((N, K // 32, 3), np.uint32)
+    side[..., 0:2] = H
+    side[..., 2] = sc[..., 0] | (sc[..., 1] << 8) | (d << 16)
+    return codes, side.reshape(N, -1).view(np.int32)

@@ -36,7 +36,7 @@ F16 = np.float16
 @dataclass
 class Linear:
     """A weight [N, K] resident on the device in one of the kernel formats."""
-    fmt: str                          # "int8" | "q4_0" | "fp16" | "blockwise" | "lut4" | "q4_k"
+    fmt: str                          # "int8" | "q4_0" | "fp16" | "blockwise" | "lut4" | "q4_k" | "q6_k"
     w: torch.Tensor
     scale: torch.Tensor | None
     N: int
@@ -65,7 +65,9 @@ class QuantizedWeight:
       fmt "lut4":      codes uint8 [N, K/2] int4 indices (column 2j low nibble), scale fp16 [N, 16]:
                        each row's codebook, the palettize_lut4 codebook of its source tensor
       fmt "q4_k":      codes uint8 [N, K/2] GGUF Q4_K code bytes, scale int32 [N, K/256*5] super-block
-                       headers ({d, dmin} + unpacked 6-bit scales/mins; _blob.q4_k_repack)"""
+                       headers ({d, dmin} + unpacked 6-bit scales/mins; _blob.q4_k_repack)
+      fmt "q6_k":      codes uint8 [N, K/2] GGUF Q6_K low 4-bit parts by 32-weight chunk, scale int32
+                       [N, K/32*3] side words (high 2-bit parts, scales, d; _blob.q6_k_repack)"""
     fmt: str
     codes: np.ndarray
     scale: np.ndarray | None
@@ -94,6 +96,17 @@ class QuantizedWeight:
             idx = np.empty((N, Kd), np.uint8)
             idx[:, 0::2], idx[:, 1::2] = self.codes & 15, self.codes >> 4
             return np.take_along_axis(self.scale.astype(np.float32), idx.astype(np.int64), axis=1)
+        if self.fmt == "q6_k":
+            side = np.ascontiguousarray(self.scale).view(np.uint32).reshape(N, Kd // 32, 3)
+            c = self.codes.reshape(N, Kd // 32, 4, 4).astype(np.uint32)          # [N, chunk, k, j]
+            lo = np.stack([c & 15, c >> 4], axis=3).reshape(N, Kd // 32, 32)     # element 8k + 4h + j
+            H = (side[..., 0:2, None] >> (8 * np.arange(4, dtype=np.uint32))) & 255   # [N, chunk, p, j]
+            hi = np.stack([(H >> (2 * q)) & 3 for q in range(4)], axis=3).reshape(N, Kd // 32, 32)
+            sc = np.stack([side[..., 2] & 255, (side[..., 2] >> 8) & 255], -1).astype(np.uint8).view(np.int8)
+            d = (side[..., 2] >> 16).astype(np.uint16).view(np.float16).astype(np.float32)
+            ds = d[..., None] * sc.astype(np.float32)                            # [N, chunk, 2]
+            q = (lo | (hi << 4)).astype(np.float32) - 32.0
+            return (q.reshape(N, Kd // 32, 2, 16) * ds[..., None]).reshape(N, Kd)
         if self.fmt == "q4_k":
             h = np.ascontiguousarray(self.scale).view(np.uint32).reshape(N, Kd // 256, 5)
             dd = np.ascontiguousarray(h[..., 0]).view(np.float16).reshape(N, Kd // 256, 2).astype(np.float32)
@@ -212,7 +225,7 @@ def blockwise_encoding(q, s, bs):
 
 
 def pack_encoded(fmt, w, s, bias=None) -> Linear:
-    N, Kd = w.shape[0], (w.shape[1] * 2 if fmt in ("q4_0", "lut4", "q4_k") else w.shape[1])
+    N, Kd = w.shape[0], (w.shape[1] * 2 if fmt in ("q4_0", "lut4", "q4_k", "q6_k") else w.shape[1])
     return Linear(fmt, _to_dev(w), None if s is None else _to_dev(s), N, Kd,
                   None if bias is None else _to_dev(np.asarray(bias, np.float32).astype(F16)))
 
@@ -234,7 +247,7 @@ def prefill_gemm(eng, lin: "Linear", x, y, residual=None, epi="f16"):
 
 
 def _prefill_fmt_ok(lin: "Linear") -> bool:
-    return lin.fmt in ("int8", "fp16", "q4_0", "blockwise", "lut4", "q4_k") and lin.K % 64 == 0 and lin.N % 16 == 0
+    return lin.fmt in ("int8", "fp16", "q4_0", "blockwise", "lut4", "q4_k", "q6_k") and lin.K % 64 == 0 and lin.N % 16 == 0
 
 
 def pack_linear(W, compress, bias=None) -> Linear:

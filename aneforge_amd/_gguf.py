@@ -2,8 +2,8 @@
 `gguf` package, aneforge/_gguf.py:10-46, which is not part of this build).
 
 GGUFView keeps the reference's accessors (meta, arch, tn, field, sc, has, get, drop_pages) and
-adds `quantized(name)`, which returns Q4_0, Q4_K and Q8_0 tensors as QuantizedWeight codes instead
-of dequantising them, so the Q4_0 / Q4_K / blockwise kernels stream the file's own codes.
+adds `quantized(name)`, which returns Q4_0, Q4_K, Q6_K and Q8_0 tensors as QuantizedWeight codes
+instead of dequantising them, so the Q4_0 / Q4_K / Q6_K / blockwise kernels stream the file's own codes.
 
 Format: magic "GGUF", version 3, tensor count, metadata count, metadata key/values, tensor infos
 (name, dims with dims[0] innermost, ggml type, offset), data section aligned to
@@ -350,7 +350,7 @@ class GGUFView:
 
     def quantized(self, name: str):
         """Tensors the kernels stream in their file encoding, as QuantizedWeight codes: Q4_0 (the
-        Q4_0 kernels), Q4_K (the Q4_K kernels, after a byte repack of each super-block's header)
+        Q4_0 kernels), Q4_K and Q6_K (their kernels, after a lossless byte repack of each super-block)
         and Q8_0 with rows of a multiple of 64 (the blockwise kernels: Q8_0's fp16(d * q) is their
         weight).  A 2-D tensor -> one QuantizedWeight [rows, K]; a 3-D expert
         stack [E, rows, K] -> a list of E.  None for other types."""
@@ -366,6 +366,11 @@ class GGUFView:
             b = np.asarray(t.data).reshape(-1, Kd // 256 * 144)
             raw = q4_k_repack(b, b.shape[0], Kd)
             make = lambda r, n: QuantizedWeight("q4_k", r[0], r[1], (n, Kd))
+        elif t.tensor_type == GGML["Q6_K"] and Kd % 256 == 0:
+            from ._blob import q6_k_repack
+            b = np.asarray(t.data).reshape(-1, Kd // 256 * 210)
+            raw = q6_k_repack(b, b.shape[0], Kd)
+            make = lambda r, n: QuantizedWeight("q6_k", r[0], r[1], (n, Kd))
         elif t.tensor_type == GGML["Q8_0"] and Kd % 64 == 0:
             b = np.asarray(t.data).reshape(-1, Kd // 32, 34)
             raw = (np.ascontiguousarray(b[:, :, 2:]).view(np.int8).reshape(-1, Kd),

@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     # codecs
     "afx_q4_0_repack": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "afx_q4_k_repack": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "afx_q6_k_repack": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "afx_q4_0_unpack": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "afx_dequant": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp]),
     "afx_dequant_f16": (_i, [_i, _vp, _vp, _vp, _ll, _i, _i, _vp]),

@@ -10,7 +10,7 @@ import torch
 
 from . import _hip
 
-FMT = {"int8": 0, "q4_0": 1, "fp16": 2, "blockwise": 3, "lut4": 4, "q4_k": 5}
+FMT = {"int8": 0, "q4_0": 1, "fp16": 2, "blockwise": 3, "lut4": 4, "q4_k": 5, "q6_k": 6}
 EW = {"add": 0, "sub": 1, "mul": 2, "real_div": 3, "maximum": 4, "minimum": 5, "pow": 6,
       "greater_equal": 7, "greater": 8, "equal": 9, "less": 10, "less_equal": 11, "not_equal": 12}
 UNARY = {"silu": 0, "sigmoid": 1, "relu": 2, "exp": 3, "tanh": 4, "affine": 5, "sqrt": 6, "abs": 7,
@@ -47,7 +47,7 @@ def linear(fmt: str, w, scale, x, y=None, bias=None, residual=None, out_f32=Fals
     _dev(w, x, scale, bias, residual)
     M, K = x.shape
     N = w.shape[0]
-    if fmt in ("q4_0", "lut4", "q4_k") and w.shape[1] * 2 != K or fmt in ("int8", "blockwise") and w.shape[1] != K:
+    if fmt in ("q4_0", "lut4", "q4_k", "q6_k") and w.shape[1] * 2 != K or fmt in ("int8", "blockwise") and w.shape[1] != K:
         raise ValueError(f"linear: weight {tuple(w.shape)} does not match K={K} for {fmt}")
     if y is None:
         y = torch.empty((M, N), dtype=torch.float32 if out_f32 else torch.float16, device=x.device)
@@ -114,6 +114,15 @@ def q4_k_repack(blocks, N, K):
     hdr = torch.empty((N, K // 256 * 5), dtype=torch.int32, device=blocks.device)
     _hip.call("afx_q4_k_repack", P(blocks), P(qs), P(hdr), N, K, stream())
     return qs, hdr
+
+
+def q6_k_repack(blocks, N, K):
+    """GGUF Q6_K bytes [N, K/256*210] (uint8, device) -> (codes uint8 [N, K/2], side int32 [N, K/32*3])."""
+    _dev(blocks)
+    qs = torch.empty((N, K // 2), dtype=torch.uint8, device=blocks.device)
+    sw = torch.empty((N, K // 32 * 3), dtype=torch.int32, device=blocks.device)
+    _hip.call("afx_q6_k_repack", P(blocks), P(qs), P(sw), N, K, stream())
+    return qs, sw
 
 
 def q4_unpack(qs, d, N, K):

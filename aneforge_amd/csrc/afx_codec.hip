@@ -130,6 +130,74 @@ __global__ void dequant_q4k_kernel(const uint32_t* __restrict__ qs, const uint32
   }
 }
 
+// GGUF Q6_K super-block (ggml block_q6_K, 210 B: ql[128], qh[64], int8 scales[16], fp16 d) -> the
+// chunked layout of Fmt<FMT_Q6K>: codes [N][K/2] (per 32-weight chunk, code dword k byte j = low
+// nibbles of elements 8k + j and 8k + 4 + j) + 3 side dwords per chunk in sw [N][K/32][3].  In the
+// ggml block, element e = 128h + 32s + l takes its low 4 bits from nibble s >> 1 of ql[64h + 32(s & 1)
+// + l], its high 2 bits from bits 2s..2s+1 of qh[32h + l], and scale e / 16.
+__global__ void q6k_repack_kernel(const uint8_t* __restrict__ blocks, uint32_t* __restrict__ qs,
+                                  uint32_t* __restrict__ sw, int N, int K) {
+  const long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= (long long)N * (K >> 8)) return;
+  const uint8_t* src = blocks + b * 210;
+  auto lo4 = [&](int e) -> uint32_t {
+    const int h = e >> 7, s = (e >> 5) & 3, l = e & 31;
+    return (src[64 * h + 32 * (s & 1) + l] >> (4 * (s >> 1))) & 15u;
+  };
+  auto hi2 = [&](int e) -> uint32_t {
+    const int h = e >> 7, s = (e >> 5) & 3, l = e & 31;
+    return (src[128 + 32 * h + l] >> (2 * s)) & 3u;
+  };
+  const uint32_t dbits = (uint32_t)src[208] | ((uint32_t)src[209] << 8);
+  uint32_t* q = qs + b * 32;                       // 8 chunks x 4 dwords
+  uint32_t* w = sw + b * 24;                       // 8 chunks x 3 dwords
+  for (int c = 0; c < 8; ++c) {
+    const int e0 = 32 * c;
+    for (int k = 0; k < 4; ++k) {
+      uint32_t v = 0;
+      for (int j = 0; j < 4; ++j) v |= (lo4(e0 + 8 * k + j) | (lo4(e0 + 8 * k + 4 + j) << 4)) << (8 * j);
+      q[4 * c + k] = v;
+    }
+    for (int p = 0; p < 2; ++p) {
+      uint32_t v = 0;
+      for (int j = 0; j < 4; ++j) {
+        const int f = e0 + 16 * p + j;
+        v |= (hi2(f) | (hi2(f + 4) << 2) | (hi2(f + 8) << 4) | (hi2(f + 12) << 6)) << (8 * j);
+      }
+      w[3 * c + p] = v;
+    }
+    w[3 * c + 2] = (uint32_t)src[192 + (e0 >> 4)] | ((uint32_t)src[192 + (e0 >> 4) + 1] << 8) | (dbits << 16);
+  }
+}
+
+// Q6_K weights as T rows out[n * ldo + k]: one thread per code dword, the Fmt<FMT_Q6K> arithmetic.
+template <typename T>
+__global__ void dequant_q6k_kernel(const uint32_t* __restrict__ qs, const uint32_t* __restrict__ sw,
+                                   T* __restrict__ out, long long ldo, int N, int K) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per = K >> 3;
+  if (i >= (long long)N * per) return;
+  const int row = (int)(i / per), w = (int)(i - (long long)row * per);
+  const int c = w >> 2, k = w & 3;
+  const uint32_t* s3 = sw + ((size_t)row * (K >> 5) + c) * 3;
+  const float dsup = (float)as_h2(s3[2]).y;
+  const float ds = dsup * (float)(int8_t)((s3[2] >> (k < 2 ? 0 : 8)) & 0xFFu);
+  const uint32_t H = s3[k >> 1], q = qs[i];
+  const uint32_t lo = (q & 0x0F0F0F0Fu) | ((k & 1 ? H : H << 4) & 0x30303030u);
+  const uint32_t hi = ((q >> 4) & 0x0F0F0F0Fu) | ((k & 1 ? H >> 2 : H << 2) & 0x30303030u);
+  T* o = out + (size_t)row * ldo + 32 * c + 8 * k;
+  // gguf-py's product (d*sc) * (q - 32), bit for bit including the sign of a zero weight (the GEMV's
+  // fma form gives +0 where this gives -0, which changes no product with x).  The empty asm keeps
+  // the product a v_mul_f32: fused into a v_fma_mix with a +0 addend it would turn -0 into +0.
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    float a = ds * (ubyte_f32(lo, t) - 32.0f), b = ds * (ubyte_f32(hi, t) - 32.0f);
+    asm("" : "+v"(a), "+v"(b));
+    o[t] = (T)(half_t)a;
+    o[4 + t] = (T)(half_t)b;
+  }
+}
+
 // out[n][k] = code * scale as fp32, through the GEMV's own unpack helpers.
 __global__ void dequant_i8_kernel(const uint32_t* __restrict__ q, const half_t* __restrict__ s,
                                   float* __restrict__ out, int N, int K) {
@@ -258,6 +326,17 @@ int afx_q4_k_repack(const void* blocks, void* qs, void* hdr, int N, int K, void*
   return check_launch("afx_q4_k_repack");
 }
 
+// GGUF Q6_K super-blocks [N][K/256] (210 B each) -> codes qs [N][K/2] + side words sw [N][K/32][3] u32.
+int afx_q6_k_repack(const void* blocks, void* qs, void* sw, int N, int K, void* stream) {
+  AFX_REQUIRE(blocks && qs && sw, "afx_q6_k_repack: null pointer");
+  AFX_REQUIRE(N >= 1 && K >= 256 && K % 256 == 0, "afx_q6_k_repack: K=%d must be a positive multiple of 256", K);
+  AFX_REQUIRE(((uintptr_t)qs & 3) == 0 && ((uintptr_t)sw & 3) == 0, "afx_q6_k_repack: outputs must be 4-byte aligned");
+  const long long nblk = (long long)N * (K / 256);
+  hipLaunchKernelGGL(q6k_repack_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)blocks, (uint32_t*)qs, (uint32_t*)sw, N, K);
+  return check_launch("afx_q6_k_repack");
+}
+
 // Inverse of afx_q4_0_repack (round-trip check back to GGUF bytes).
 int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, void* stream) {
   AFX_REQUIRE(blocks && qs && d, "afx_q4_0_unpack: null pointer");
@@ -269,13 +348,13 @@ int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, v
 }
 
 // Dequantise through the GEMV unpack path: fmt 0 = int8 [N][K] + s[N]; fmt 1 = Q4_0 superblock.
-// fmt 0 int8, 1 Q4_0 (superblock layout), 3 blockwise, 4 int4 codebook, 5 Q4_K -> fp16 rows of stride ldo.
+// fmt 0 int8, 1 Q4_0 (superblock layout), 3 blockwise, 4 int4 codebook, 5 Q4_K, 6 Q6_K -> fp16 rows of stride ldo.
 int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,
                     void* stream) {
   AFX_REQUIRE(w && scale && out, "afx_dequant_f16: null pointer");
-  AFX_REQUIRE(fmt == 0 || fmt == 1 || fmt == 3 || fmt == 4 || fmt == 5,
+  AFX_REQUIRE(fmt == 0 || fmt == 1 || fmt == 3 || fmt == 4 || fmt == 5 || fmt == 6,
               "afx_dequant_f16: format %d has no scales to apply", fmt);
-  const int kq = fmt == 1 ? 128 : fmt == 3 ? 32 : fmt == 5 ? 256 : 8;
+  const int kq = fmt == 1 ? 128 : fmt == 3 ? 32 : fmt == 5 || fmt == 6 ? 256 : 8;
   AFX_REQUIRE(N >= 1 && K >= kq && K % kq == 0, "afx_dequant_f16: K=%d must be a multiple of %d", K, kq);
   AFX_REQUIRE(ldo >= K && ldo % 8 == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)w & 7) == 0,
               "afx_dequant_f16: out rows must be 16-byte aligned (ldo %% 8 == 0) and ldo >= K");
@@ -286,6 +365,9 @@ int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long l
                        (const half_t*)scale, (half_t*)out, ldo, N, K);
   else if (fmt == 5)
     hipLaunchKernelGGL(dequant_q4k_kernel<half_t>, grid, dim3(256), 0, (hipStream_t)stream, (const uint32_t*)w,
+                       (const uint32_t*)scale, (half_t*)out, ldo, N, K);
+  else if (fmt == 6)
+    hipLaunchKernelGGL(dequant_q6k_kernel<half_t>, grid, dim3(256), 0, (hipStream_t)stream, (const uint32_t*)w,
                        (const uint32_t*)scale, (half_t*)out, ldo, N, K);
   else if (fmt == 0)
     hipLaunchKernelGGL(dequant_f16_kernel<FMT_I8>, grid, dim3(256), 0, (hipStream_t)stream, w,
@@ -321,6 +403,12 @@ int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, in
                 "afx_dequant: Q4_K K must be a multiple of 256");
     const long long n8 = (long long)N * (K / 8);
     hipLaunchKernelGGL(dequant_q4k_kernel<float>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint32_t*)w, (const uint32_t*)scale, out, (long long)K, N, K);
+  } else if (fmt == 6) {
+    AFX_REQUIRE(K % 32 == 0 && ((uintptr_t)w & 3) == 0 && ((uintptr_t)scale & 3) == 0,
+                "afx_dequant: Q6_K K must be a multiple of 32");
+    const long long n8 = (long long)N * (K / 8);
+    hipLaunchKernelGGL(dequant_q6k_kernel<float>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, (const uint32_t*)w, (const uint32_t*)scale, out, (long long)K, N, K);
   } else if (fmt == 3) {
     AFX_REQUIRE(K % 32 == 0 && ((uintptr_t)w & 3) == 0, "afx_dequant: blockwise K must be a multiple of 32");

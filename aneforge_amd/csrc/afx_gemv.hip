@@ -65,7 +65,7 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
   AFX_REQUIRE(a.M >= 1, "%s: M=%d must be >= 1", what, a.M);
   AFX_REQUIRE(a.N >= 1 && a.K >= 1, "%s: bad shape N=%d K=%d", what, a.N, a.K);
   const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : fmt == FMT_BW ? 64 : fmt == FMT_L4 ? 32
-               : fmt == FMT_Q4K ? 256 : 8;
+               : fmt == FMT_Q4K || fmt == FMT_Q6K ? 256 : 8;
   AFX_REQUIRE(a.K % kq == 0, "%s: K=%d must be a multiple of %d", what, a.K, kq);
   AFX_REQUIRE(a.ldx % 8 == 0 && a.ldx >= a.K, "%s: ldx=%d must be a multiple of 8 and >= K", what, a.ldx);
   AFX_REQUIRE(((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.w & 15) == 0,
@@ -80,6 +80,8 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
               "%s: Q4_0 weights need an 8-byte aligned block-scale array", what);
   AFX_REQUIRE(fmt != FMT_Q4K || (a.scale && ((uintptr_t)a.scale & 3) == 0),
               "%s: Q4_K weights need a 4-byte aligned super-block header array", what);
+  AFX_REQUIRE(fmt != FMT_Q6K || (a.scale && ((uintptr_t)a.scale & 3) == 0),
+              "%s: Q6_K weights need a 4-byte aligned side-word array", what);
   if (eg == EG_SWIGLU) AFX_REQUIRE(a.N % 2 == 0, "%s: SwiGLU needs interleaved gate/up rows", what);
   if (a.epi == EPI_RESID) AFX_REQUIRE(a.resid, "%s: residual pointer required", what);
   if (eg == EG_QKV)
@@ -125,7 +127,8 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
   }
   AFX_REQUIRE((long long)a.K * (fmt == FMT_F16 ? 2 : 1) < (1LL << 31), "%s: K=%d too large", what, a.K);
   const int ntiles = grid_for((a.N + R - 1) / R);
-  const int nchunks = a.K / (fmt == FMT_I8 || fmt == FMT_BW ? 16 : fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K ? 32 : 8);
+  const int nchunks = a.K / (fmt == FMT_I8 || fmt == FMT_BW ? 16
+                             : fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K || fmt == FMT_Q6K ? 32 : 8);
   const int fu = a.M == 1 ? fast_units(fmt, nchunks) : 0;
   if (fu) {
     // a whole row fits the lanes' registers: the register-resident fast path (static LDS only)
@@ -135,6 +138,7 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
                : fmt == FMT_BW ? pick_gemv_row_bw(eg, R, nm, fu)
                : fmt == FMT_L4 ? pick_gemv_row_l4(eg, R, nm, fu)
                : fmt == FMT_Q4K ? pick_gemv_row_q4k(eg, R, nm, fu)
+               : fmt == FMT_Q6K ? pick_gemv_row_q6k(eg, R, nm, fu)
                                : pick_gemv_row_f16(eg, R, nm, fu);
     hipLaunchKernelGGL(fr, dim3(ntiles), dim3(256), 0, stream, a);
     return check_launch(what);
@@ -144,6 +148,7 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
              : fmt == FMT_BW ? pick_gemv_bw(mt, eg, R, xs)
              : fmt == FMT_L4 ? pick_gemv_l4(mt, eg, R, xs)
              : fmt == FMT_Q4K ? pick_gemv_q4k(mt, eg, R, xs)
+             : fmt == FMT_Q6K ? pick_gemv_q6k(mt, eg, R, xs)
                              : pick_gemv_f16(mt, eg, R, xs);
   hipLaunchKernelGGL(fn, dim3(ntiles), dim3(256), smem, stream, a);
   return check_launch(what);
@@ -170,7 +175,7 @@ extern "C" {
 int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                int M, int N, int K, const void* bias, const void* residual, int out_f32,
                int rows_hint, void* stream) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 5, "afx_linear: unknown weight format %d", fmt);
+  AFX_REQUIRE(fmt >= 0 && fmt <= 6, "afx_linear: unknown weight format %d", fmt);
   AFX_REQUIRE(!(residual && out_f32), "afx_linear: residual add needs an fp16 output");
   AFX_REQUIRE(ldy >= N, "afx_linear: ldy=%d < N=%d", ldy, N);
   GemvArgs a = base_args(w, scale, x, ldx, y, ldy, M, N, K, bias,
@@ -183,7 +188,7 @@ int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx
 int afx_linear_rms(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
                    float eps, void* y, int ldy, int M, int N, int K, const void* bias, int out_f32,
                    int rows_hint, void* stream) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 5, "afx_linear_rms: unknown weight format %d", fmt);
+  AFX_REQUIRE(fmt >= 0 && fmt <= 6, "afx_linear_rms: unknown weight format %d", fmt);
   AFX_REQUIRE(gamma, "afx_linear_rms: RMSNorm prologue needs gamma");
   AFX_REQUIRE(ldy >= N, "afx_linear_rms: ldy=%d < N=%d", ldy, N);
   GemvArgs a = base_args(w, scale, x, ldx, y, ldy, M, N, K, bias, out_f32 ? EPI_F32 : EPI_F16);
@@ -196,7 +201,7 @@ int afx_linear_rms(int fmt, const void* w, const void* scale, const void* x, int
 int afx_linear_swiglu(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
                       float eps, int norm, void* act, int ld_act, int M, int N, int K, int rows_hint,
                       void* stream) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 5, "afx_linear_swiglu: unknown weight format %d", fmt);
+  AFX_REQUIRE(fmt >= 0 && fmt <= 6, "afx_linear_swiglu: unknown weight format %d", fmt);
   AFX_REQUIRE(!norm || gamma, "afx_linear_swiglu: RMSNorm prologue needs gamma");
   AFX_REQUIRE(ld_act >= N / 2, "afx_linear_swiglu: ld_act=%d < N/2=%d", ld_act, N / 2);
   GemvArgs a = base_args(w, scale, x, ldx, act, ld_act, M, N, K, nullptr, EPI_SWIGLU);
@@ -213,7 +218,7 @@ int afx_qkv_rope_kv(int fmt, const void* w, const void* scale, const void* h, in
                     const void* cos_tab, const void* sin_tab, int rope, const int* pos, void* qout,
                     int ldq, void* kcache, void* vcache, long long kv_seq_stride,
                     long long kv_head_stride, int kv_len, int M, int K, int rows_hint, void* stream) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 5, "afx_qkv_rope_kv: unknown weight format %d", fmt);
+  AFX_REQUIRE(fmt >= 0 && fmt <= 6, "afx_qkv_rope_kv: unknown weight format %d", fmt);
   AFX_REQUIRE(nv == nk, "afx_qkv_rope_kv: k and v row counts differ (%d vs %d)", nk, nv);
   AFX_REQUIRE(!rope || (cos_tab && sin_tab), "afx_qkv_rope_kv: rope tables required");
   AFX_REQUIRE(!norm || gamma, "afx_qkv_rope_kv: RMSNorm prologue needs gamma");

@@ -5,7 +5,7 @@
 
 namespace afx {
 
-enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2, FMT_BW = 3, FMT_L4 = 4, FMT_Q4K = 5 };
+enum { FMT_I8 = 0, FMT_Q4 = 1, FMT_F16 = 2, FMT_BW = 3, FMT_L4 = 4, FMT_Q4K = 5, FMT_Q6K = 6 };
 
 // ---- x sources: global memory or the LDS copy written by the norm prologue ----
 template <int N8>
@@ -21,6 +21,7 @@ __device__ __forceinline__ void load_x(const half_t* p, h2 (&out)[N8 * 4]) {
 // ---- per-format chunk geometry and math ----
 // Ctx: per-row state a format's dot product needs beyond the chunk (the LUT4 codebook's byte
 // tables), built once per row a wavefront owns from the scale pointer; empty for the others.
+// S: the per-chunk side word loaded with each chunk (block scales; Q6_K's high bits and scales).
 struct NoCtx {
   __device__ static NoCtx make(const half_t*, int) { return {}; }
 };
@@ -31,6 +32,7 @@ template <int FMT> struct Fmt;
 
 template <> struct Fmt<FMT_I8> {
   using Ctx = NoCtx;
+  using S = u2;
   static constexpr int kWeightsPerChunk = 16;
   static constexpr int kXH2 = 8;
   __device__ static size_t row_bytes(int K) { return (size_t)K; }
@@ -47,6 +49,7 @@ template <> struct Fmt<FMT_I8> {
 
 template <> struct Fmt<FMT_Q4> {
   using Ctx = NoCtx;
+  using S = u2;
   static constexpr int kWeightsPerChunk = 32;
   static constexpr int kXH2 = 16;
   __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
@@ -85,6 +88,7 @@ template <> struct Fmt<FMT_Q4> {
 // chunk lies in one block.  d.x = the scales of chunks 4i..4i+3 (two fp16), d.y = which half.
 template <> struct Fmt<FMT_BW> {
   using Ctx = NoCtx;
+  using S = u2;
   static constexpr int kWeightsPerChunk = 16;
   static constexpr int kXH2 = 8;
   __device__ static size_t row_bytes(int K) { return (size_t)K; }
@@ -104,6 +108,7 @@ template <> struct Fmt<FMT_BW> {
 
 template <> struct Fmt<FMT_F16> {
   using Ctx = NoCtx;
+  using S = u2;
   static constexpr int kWeightsPerChunk = 8;
   static constexpr int kXH2 = 4;
   __device__ static size_t row_bytes(int K) { return (size_t)K * 2; }
@@ -155,6 +160,7 @@ __device__ __forceinline__ uint32_t l4_bit7_mask(uint32_t s) {
 }
 template <> struct Fmt<FMT_L4> {
   using Ctx = L4Ctx;
+  using S = u2;
   static constexpr int kWeightsPerChunk = 32;
   static constexpr int kXH2 = 16;
   __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
@@ -200,6 +206,7 @@ template <> struct Fmt<FMT_L4> {
 __device__ __forceinline__ float ubyte_f32(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
 template <> struct Fmt<FMT_Q4K> {
   using Ctx = NoCtx;
+  using S = u2;
   static constexpr int kWeightsPerChunk = 32;
   static constexpr int kXH2 = 16;
   __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
@@ -246,22 +253,74 @@ template <> struct Fmt<FMT_Q4K> {
   }
 };
 
-// Block scales for a chunk: Q4, the 4 fp16 of its superblock; blockwise, the 2 fp16 of chunks
+// GGUF Q6_K (ggml block_q6_K: 256 weights as 4-bit low parts ql, 2-bit high parts qh, int8 scales
+// per 16 weights and an fp16 d; the reference dequantises it with gguf-py through GGUFView.get,
+// aneforge/_gguf.py:34-39), repacked by afx_q6_k_repack into chunks of 32 consecutive weights:
+// code dword k (k = 0..3) holds elements 8k + j in the low nibble and 8k + 4 + j in the high
+// nibble of byte j; the side word is {H0, H1, sc_a | sc_b << 8 | d << 16} with H0 the high 2-bit
+// parts of elements 0..15 and H1 of 16..31 (byte j of H_p: bits 0-1 element 16p + j, 2-3 element
+// 16p + 4 + j, 4-5 element 16p + 8 + j, 6-7 element 16p + 12 + j), sc_a / sc_b the int8 scales of
+// elements 0..15 / 16..31.  The weight is the reference's fp16(d*sc * (q - 32)): d*sc is exact in
+// fp32 (11 + 8 bits) and so is its product with q - 32, so fma(d*sc, q, -32*d*sc) is that value
+// (as +0 where gguf-py's product is -0, which adds nothing different to a dot product).
+template <> struct Fmt<FMT_Q6K> {
+  using Ctx = NoCtx;
+  using S = u4;
+  static constexpr int kWeightsPerChunk = 32;
+  static constexpr int kXH2 = 16;
+  __device__ static size_t row_bytes(int K) { return (size_t)(K >> 1); }
+  __device__ static void load_x(const half_t* xrow, int c, h2 (&x)[kXH2]) { afx::load_x<4>(xrow + 32 * c, x); }
+  __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u4& d, const Ctx&, float acc) {
+    const float dsup = (float)as_h2(d.z).y;
+    const float dsa = dsup * (float)(int8_t)(d.z & 0xFFu), dsb = dsup * (float)(int8_t)((d.z >> 8) & 0xFFu);
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t hh[2] = {d.x, d.y};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {                  // dword k: elements 8k..8k+3 (low) and 8k+4..8k+7 (high)
+      const uint32_t H = hh[k >> 1];
+      uint32_t lo = (wd[k] & 0x0F0F0F0Fu) | ((k & 1 ? H : H << 4) & 0x30303030u);
+      uint32_t hi = ((wd[k] >> 4) & 0x0F0F0F0Fu) | ((k & 1 ? H >> 2 : H << 2) & 0x30303030u);
+      asm("" : "+v"(lo), "+v"(hi));                // one v_cvt_f32_ubyte<n> per byte below
+      const float ds = k < 2 ? dsa : dsb, off = -32.0f * ds;
+      h2 a0, a1, b0, b1;
+      a0.x = (half_t)__builtin_fmaf(ds, ubyte_f32(lo, 0), off);
+      a0.y = (half_t)__builtin_fmaf(ds, ubyte_f32(lo, 1), off);
+      a1.x = (half_t)__builtin_fmaf(ds, ubyte_f32(lo, 2), off);
+      a1.y = (half_t)__builtin_fmaf(ds, ubyte_f32(lo, 3), off);
+      b0.x = (half_t)__builtin_fmaf(ds, ubyte_f32(hi, 0), off);
+      b0.y = (half_t)__builtin_fmaf(ds, ubyte_f32(hi, 1), off);
+      b1.x = (half_t)__builtin_fmaf(ds, ubyte_f32(hi, 2), off);
+      b1.y = (half_t)__builtin_fmaf(ds, ubyte_f32(hi, 3), off);
+      acc = dot2(a0, x[4 * k], acc);
+      acc = dot2(a1, x[4 * k + 1], acc);
+      acc = dot2(b0, x[4 * k + 2], acc);
+      acc = dot2(b1, x[4 * k + 3], acc);
+    }
+    return acc;
+  }
+};
+
+// Per-chunk side words: Q4, the 4 fp16 of its superblock; blockwise, the 2 fp16 of chunks
 // 4i..4i+3 and the half that is the chunk's; Q4_K, {d, dmin} and the pair's scale/min bytes;
-// other formats have none.
+// Q6_K, the chunk's 3 dwords; other formats have none.
 template <int FMT>
-__device__ __forceinline__ u2 load_scales(const half_t* drow, int c) {
+__device__ __forceinline__ typename Fmt<FMT>::S load_scales(const half_t* drow, int c) {
   if constexpr (FMT == FMT_Q4) return *(const u2*)(drow + 4 * (c >> 2));
   else if constexpr (FMT == FMT_BW) return (u2){*(const uint32_t*)(drow + 2 * (c >> 2)), (uint32_t)((c >> 1) & 1)};
   else if constexpr (FMT == FMT_Q4K) {
     const uint32_t* q = (const uint32_t*)drow + 5 * (c >> 3);
     return (u2){q[0], q[1 + ((c >> 1) & 3)]};
-  } else return (u2){0u, 0u};
+  } else if constexpr (FMT == FMT_Q6K) {
+    const uint32_t* q = (const uint32_t*)drow + 3 * c;
+    return (u4){q[0], q[1], q[2], 0u};
+  } else return typename Fmt<FMT>::S{};
 }
-// Whether the format carries per-block scales in a per-row array, and that row's length in halves.
-template <int FMT> constexpr bool has_block_scales() { return FMT == FMT_Q4 || FMT == FMT_BW || FMT == FMT_Q4K; }
+// Whether the format carries per-chunk side words in a per-row array, and that row's length in halves.
+template <int FMT> constexpr bool has_block_scales() {
+  return FMT == FMT_Q4 || FMT == FMT_BW || FMT == FMT_Q4K || FMT == FMT_Q6K;
+}
 template <int FMT> __host__ __device__ constexpr long long scale_row_halves(int K) {
-  return FMT == FMT_Q4K ? (long long)(K >> 8) * 10 : (long long)(K >> 5);
+  return FMT == FMT_Q4K ? (long long)(K >> 8) * 10 : FMT == FMT_Q6K ? (long long)(K >> 5) * 6 : (long long)(K >> 5);
 }
 
 }  // namespace afx

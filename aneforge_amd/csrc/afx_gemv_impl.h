@@ -80,7 +80,9 @@ struct GemvArgs {
 constexpr int kStageUnroll = 4;     // 16-byte staging loads per thread in flight per batch
 constexpr int kBufDword3 = 0x00020000;   // raw buffer descriptor word 3 (gfx9 family)
 
-template <int FMT> struct Units { static constexpr int value = FMT == FMT_Q4 || FMT == FMT_L4 || FMT == FMT_Q4K ? 2 : 4; };
+template <int FMT> struct Units {
+  static constexpr int value = FMT == FMT_Q4 || FMT == FMT_L4 || FMT == FMT_Q4K || FMT == FMT_Q6K ? 2 : 4;
+};
 
 // Bytes of LDS the kernel needs: staged x rows, gamma, and the cross-wave norm partials.
 __host__ __device__ inline size_t gemv_lds_bytes(int Mt, int K, bool norm) {
@@ -265,8 +267,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       dr[r] = make_rsrc(a.scale + (size_t)row * scale_row_halves<FMT>(K), 2 * scale_row_halves<FMT>(K));
   }
   u4 wA[U][R], wB[U][R];
-  u2 dA[U][R], dB[U][R];
-  auto load_unit = [&](u4 (&w)[U][R], u2 (&d)[U][R], int j) {
+  using SW = typename Fmt<FMT>::S;
+  SW dA[U][R], dB[U][R];
+  auto load_unit = [&](u4 (&w)[U][R], SW (&d)[U][R], int j) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -277,6 +280,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         if constexpr (FMT == FMT_BW) d[u][r] = (u2){buf_load4(dr[r], (c >> 2) * 4), (uint32_t)((c >> 1) & 1)};
         if constexpr (FMT == FMT_Q4K)       // past K both read as zero: d = dmin = 0, weight 0
           d[u][r] = (u2){buf_load4(dr[r], (c >> 3) * 20), buf_load4(dr[r], (c >> 3) * 20 + 4 + 4 * ((c >> 1) & 3))};
+        if constexpr (FMT == FMT_Q6K)       // past K all zero: d = 0, weight 0
+          d[u][r] = (u4){buf_load4(dr[r], c * 12), buf_load4(dr[r], c * 12 + 4), buf_load4(dr[r], c * 12 + 8), 0u};
       }
     }
   };
@@ -361,7 +366,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   typename Fmt<FMT>::Ctx fctx[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) fctx[r] = Fmt<FMT>::Ctx::make(a.scale, row0 + r < N ? row0 + r : N - 1);
-  auto compute = [&](const u4 (&w)[U][R], const u2 (&d)[U][R], int j) {
+  auto compute = [&](const u4 (&w)[U][R], const SW (&d)[U][R], int j) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int craw = j * 64 * U + 64 * u + lane;
@@ -449,7 +454,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
 
   // the group's weight rows, one 16-byte chunk per lane per unit
   u4 w[U][R];
-  u2 d[U][R];
+  typename Fmt<FMT>::S d[U][R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r < N ? row0 + r : N - 1;
@@ -524,13 +529,15 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       u4 wv = w[u][r];
-      u2 dv = d[u][r];
+      typename Fmt<FMT>::S dv = d[u][r];
       if (u == U - 1) {                              // only the last unit can hold chunks past K
         if constexpr (FMT == FMT_Q4) {
           dv.x = ok ? dv.x : 0u;
           dv.y = ok ? dv.y : 0u;
         } else if constexpr (FMT == FMT_Q4K) {
           dv.x = ok ? dv.x : 0u;                     // d = dmin = 0: weight 0 for any code
+        } else if constexpr (FMT == FMT_Q6K) {
+          dv.z = ok ? dv.z : 0u;                     // d = 0: weight 0 for any code
         } else if constexpr (FMT != FMT_L4) {
           wv.x = ok ? wv.x : 0u; wv.y = ok ? wv.y : 0u; wv.z = ok ? wv.z : 0u; wv.w = ok ? wv.w : 0u;
         }
@@ -585,14 +592,14 @@ gemv_fn pick_gemv_row_u(int eg, int R, int norm) {
 __host__ __device__ inline int fast_units(int fmt, int nchunks) {
   const int u = (nchunks + 63) / 64;
   if (fmt == FMT_I8 || fmt == FMT_BW) return u == 4 || u == 11 ? u : 0;
-  if (fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K) return u == 2 || u == 6 ? u : 0;
+  if (fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K || fmt == FMT_Q6K) return u == 2 || u == 6 ? u : 0;
   return u == 8 ? u : 0;
 }
 template <int FMT>
 gemv_fn pick_gemv_row(int eg, int R, int norm, int U) {
   if constexpr (FMT == FMT_I8 || FMT == FMT_BW)
     return U == 11 ? pick_gemv_row_u<FMT, 11>(eg, R, norm) : pick_gemv_row_u<FMT, 4>(eg, R, norm);
-  else if constexpr (FMT == FMT_Q4 || FMT == FMT_L4 || FMT == FMT_Q4K)
+  else if constexpr (FMT == FMT_Q4 || FMT == FMT_L4 || FMT == FMT_Q4K || FMT == FMT_Q6K)
     return U == 6 ? pick_gemv_row_u<FMT, 6>(eg, R, norm) : pick_gemv_row_u<FMT, 2>(eg, R, norm);
   else return pick_gemv_row_u<FMT, 8>(eg, R, norm);
 }
@@ -604,11 +611,13 @@ gemv_fn pick_gemv_f16(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_bw(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_l4(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_q4k(int mt, int eg, int R, int xs);
+gemv_fn pick_gemv_q6k(int mt, int eg, int R, int xs);
 gemv_fn pick_gemv_row_i8(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_q4(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_f16(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_bw(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_l4(int eg, int R, int norm, int U);
 gemv_fn pick_gemv_row_q4k(int eg, int R, int norm, int U);
+gemv_fn pick_gemv_row_q6k(int eg, int R, int norm, int U);
 
 }  // namespace afx

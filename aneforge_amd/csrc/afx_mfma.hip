@@ -292,7 +292,7 @@ static mfma_fn pick_mfma(int fmt, bool swiglu, int nw, int nb) {
 }
 
 bool mfma_supported(int fmt, int K) {
-  if (fmt == FMT_L4 || fmt == FMT_Q4K) return false;          // int4 codebook, Q4_K: vector kernels only
+  if (fmt == FMT_L4 || fmt == FMT_Q4K || fmt == FMT_Q6K) return false;   // int4 codebook, K-quants: vector kernels
   const int ks = fmt == FMT_I8 || fmt == FMT_BW ? 64 : fmt == FMT_Q4 ? 128 : 32;
   return K % ks == 0 && K / ks >= 8;                           // at least one step per wavefront
 }

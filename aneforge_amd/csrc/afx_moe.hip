@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(MoeArgs a) {
     constexpr int U = 2;
     for (int cb = lane; cb < nchunks; cb += 64 * U) {
       u4 wv[U][R];
-      u2 dv[U][R];
+      typename Fmt<FMT>::S dv[U][R];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = cb + 64 * u;
@@ -212,27 +212,28 @@ static moe_fn pick_moe(int R) {
 }
 
 static int moe_launch(int fmt, MoeArgs& a, int E, int R, hipStream_t stream, const char* what) {
-  AFX_REQUIRE(fmt >= 0 && fmt <= 5, "%s: unknown weight format %d", what, fmt);
+  AFX_REQUIRE(fmt >= 0 && fmt <= 6, "%s: unknown weight format %d", what, fmt);
   const int kq = fmt == FMT_I8 ? 16 : fmt == FMT_Q4 ? 128 : fmt == FMT_BW ? 64 : fmt == FMT_L4 ? 32
-               : fmt == FMT_Q4K ? 256 : 8;
+               : fmt == FMT_Q4K || fmt == FMT_Q6K ? 256 : 8;
   AFX_REQUIRE(a.K % kq == 0, "%s: K=%d must be a multiple of %d", what, a.K, kq);
   AFX_REQUIRE(a.w && a.x && a.y && a.cnt && a.list, "%s: null pointer", what);
   AFX_REQUIRE(fmt == FMT_F16 || a.scale, "%s: quantized weights need scales", what);
   moe_fn fn = fmt == FMT_I8 ? pick_moe<FMT_I8>(R) : fmt == FMT_Q4 ? pick_moe<FMT_Q4>(R)
             : fmt == FMT_BW ? pick_moe<FMT_BW>(R) : fmt == FMT_L4 ? pick_moe<FMT_L4>(R)
-            : fmt == FMT_Q4K ? pick_moe<FMT_Q4K>(R) : pick_moe<FMT_F16>(R);
+            : fmt == FMT_Q4K ? pick_moe<FMT_Q4K>(R) : fmt == FMT_Q6K ? pick_moe<FMT_Q6K>(R) : pick_moe<FMT_F16>(R);
   const int gx = (a.N + 4 * R - 1) / (4 * R);
   hipLaunchKernelGGL(fn, dim3(gx, E), dim3(256), 0, stream, a);
   return check_launch(what);
 }
 
 static long long fmt_row_bytes(int fmt, int K) {
-  return fmt == FMT_I8 || fmt == FMT_BW ? K : fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K ? K / 2 : 2LL * K;
+  return fmt == FMT_I8 || fmt == FMT_BW ? K : fmt == FMT_Q4 || fmt == FMT_L4 || fmt == FMT_Q4K || fmt == FMT_Q6K ? K / 2
+       : 2LL * K;
 }
 // Elements (halves) of one expert's scale array: rows of `rows` weights over K.
 static long long fmt_scale_halves(int fmt, long long rows, int K) {
   return fmt == FMT_Q4 || fmt == FMT_BW ? rows * (K / 32) : fmt == FMT_L4 ? rows * 16
-       : fmt == FMT_Q4K ? rows * (K / 256) * 10 : rows;
+       : fmt == FMT_Q4K ? rows * (K / 256) * 10 : fmt == FMT_Q6K ? rows * (K / 32) * 6 : rows;
 }
 
 }  // namespace afx

@@ -10,7 +10,7 @@ GEMVs all run on the device (afx_moe_*), so a MoE layer stays inside the capture
 Canonical per-layer weights (as the reference): mlp_norm, router [E, dim],
 wgate_exps / wup_exps [E, ffn, dim], wdown_exps [E, ffn, dim] (down stored transposed for the
 batched act @ wdown); Qwen2-MoE adds wgate_sh / wup_sh / wdown_sh / shared_gate.  Expert
-weights may also arrive as already-encoded QuantizedWeight stacks (GGUF Q4_0 / Q4_K / Q8_0 from load_gguf),
+weights may also arrive as already-encoded QuantizedWeight stacks (GGUF Q4_0 / Q4_K / Q6_K / Q8_0 from load_gguf),
 in which case their codes are streamed as they are."""
 from __future__ import annotations
 
@@ -97,7 +97,7 @@ class MoEDecode:
             up = [E.per_tensor(u_[e], compress) for e in range(self.E)]
             down = [E.per_tensor(np.ascontiguousarray(d_[e].T), compress) for e in range(self.E)]
         if isinstance(gate, (list, tuple)) or isinstance(down, (list, tuple)):
-            # per-expert matrices: QuantizedWeight codes (GGUF Q4_0 / Q4_K / Q8_0), with float stacks of
+            # per-expert matrices: QuantizedWeight codes (GGUF Q4_0 / Q4_K / Q6_K / Q8_0), with float stacks of
             # a file's other types split per expert alongside ([F, D] gate/up, [D, F] down)
             if not isinstance(gate, (list, tuple)):
                 gate, up = list(np.asarray(gate, np.float32)), list(np.asarray(up, np.float32))
@@ -296,7 +296,7 @@ def load_gguf(path: str, n_layers: int | None = None, compress: str | None = Non
         extra={"n_experts": E, "n_experts_per_tok": k, "norm_topk_prob": arch != "qwen2moe"})
 
     def experts(name):
-        """An expert stack: per-expert QuantizedWeight when the file holds Q4_0 / Q4_K / Q8_0 codes, else fp16."""
+        """An expert stack: per-expert QuantizedWeight when the file holds Q4_0 / Q4_K / Q6_K / Q8_0 codes, else fp16."""
         q = gg.quantized(name)
         if q is not None:
             return q

@@ -62,7 +62,8 @@ int afx_event_destroy(void* ev);
  * j) + a 16-entry fp16 codebook per row scale[N][16], weight codebook[n][index] (aneforge/_blob.py:
  * 28-43, constexpr_lut_to_dense in aneforge/_compile.py:149; vector kernels at any M);
  * 5: GGUF Q4_K after afx_q4_k_repack, weight fp16(d*sc*q - dmin*m) as the reference's
- * GGUFView.get produces it (aneforge/_gguf.py:34-39; K % 256 == 0, vector kernels at any M). */
+ * GGUFView.get produces it (aneforge/_gguf.py:34-39; K % 256 == 0, vector kernels at any M);
+ * 6: GGUF Q6_K after afx_q6_k_repack, weight fp16(d*sc * (q - 32)) (the same reference path). */
 int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                int M, int N, int K, const void* bias, const void* residual, int out_f32,
                int rows_hint, void* stream);
@@ -96,10 +97,15 @@ int afx_q4_0_unpack(const void* qs, const void* d, void* blocks, int N, int K, v
  * -> codes qs [N][K/2] (the code bytes as they are) + hdr [N][K/256][5] u32 ({d | dmin << 16}, then
  * per sub-block pair p the bytes {sc(2p), sc(2p+1), m(2p), m(2p+1)}), the fmt 5 weight/scale pair. */
 int afx_q4_k_repack(const void* blocks, void* qs, void* hdr, int N, int K, void* stream);
+/* GGUF Q6_K super-blocks [N][K/256] (210 B: ql[128], qh[64], int8 scales[16], fp16 d; reference:
+ * GGUFView.get -> gguf.quants.dequantize, aneforge/_gguf.py:34-39, kept 6-bit here) -> codes qs
+ * [N][K/2] (per 32-weight chunk, byte j of dword k = low 4 bits of elements 8k+j | 8k+4+j << 4) +
+ * sw [N][K/32][3] u32 (the chunk's high 2-bit parts, its two scales and d), the fmt 6 pair. */
+int afx_q6_k_repack(const void* blocks, void* qs, void* sw, int N, int K, void* stream);
 /* Dequantise through the GEMV's own unpack path into fp32 (bit-exact check of
  * quantize_per_row / Q4_0 / quantize_blockwise reconstruction, aneforge/_blob.py:20-25, 46-56). */
 int afx_dequant(int fmt, const void* w, const void* scale, float* out, int N, int K, void* stream);
-/* The same weights as fp16 rows out[n * ldo + k] (fmt 0 int8, 1 Q4_0, 3 blockwise, 4 int4, 5 Q4_K): the fp16 values the
+/* The same weights as fp16 rows out[n * ldo + k] (fmt 0 int8, 1 Q4_0, 3 blockwise, 4 int4, 5 Q4_K, 6 Q6_K): the fp16 values the
  * reference multiplies with -- for Q4_0 the fp16 cast of GGUFView.get (aneforge/_gguf.py:34-39).  The
  * batched prefill expands formats its GEMM does not read (Q4_0) into fp16 this way, one matrix at a time. */
 int afx_dequant_f16(int fmt, const void* w, const void* scale, void* out, long long ldo, int N, int K,

@@ -18,7 +18,7 @@ Pinning status (see tests/test_oracle.py):
   quantize_blockwise                    pinned: closed form + reference property tests
   dequant_blockwise                     pinned: KAT (an fp16 round-half-even tie of the product)
   dequant_lut4                          pinned: KAT (hand-packed nibbles -> their codebook entries)
-  dequant_q4_k(_f16)                    pinned: KAT (closed-form block) + element-by-element block encoder
+  dequant_q4_k(_f16), dequant_q6_k(_f16)  pinned: KATs (closed-form blocks) + element-by-element block encoders
   sample                                pinned: numpy's own RandomState.choice on the same draws, top-k /
                                         top-p support and frequency properties
   rms_norm                              pinned: torch + invariants
@@ -164,6 +164,34 @@ def dequant_q4_k(blocks):
         ml = (dmin * m.astype(np.float32)).astype(np.float32)
         out[:, 32 * j:32 * j + 32] = dl[:, None] * q - ml[:, None]
     return out
+
+
+def dequant_q6_k(blocks):
+    """GGUF Q6_K super-blocks uint8 [n, 210] -> fp32 weights [n, 256], as gguf-py's Q6_K dequantiser
+    evaluates ggml's block_q6_K (the reference calls it through GGUFView.get, aneforge/_gguf.py:34-39):
+    ql[128] at byte 0, qh[64] at 128, int8 scales[16] at 192, fp16 d at 208.  ggml's loop over the
+    two 128-weight halves h and l < 32: element 128h + l = (ql[64h + l] & 15) | ((qh[32h + l] >> 0) & 3)
+    << 4, element + 32 = (ql[64h + 32 + l] & 15) | ((qh >> 2) & 3) << 4, element + 64 = (ql[64h + l] >> 4)
+    | ((qh >> 4) & 3) << 4, element + 96 = (ql[64h + 32 + l] >> 4) | ((qh >> 6) & 3) << 4; weight =
+    (d * scale[e // 16]) * (q - 32) in float32."""
+    b = np.asarray(blocks, np.uint8).reshape(-1, 210)
+    n = b.shape[0]
+    q = np.empty((n, 256), np.int64)
+    for h in range(2):
+        ql, qh = b[:, 64 * h:64 * h + 64].astype(np.int64), b[:, 128 + 32 * h:128 + 32 * h + 32].astype(np.int64)
+        q[:, 128 * h + 0:128 * h + 32] = (ql[:, :32] & 15) | ((qh & 3) << 4)
+        q[:, 128 * h + 32:128 * h + 64] = (ql[:, 32:] & 15) | (((qh >> 2) & 3) << 4)
+        q[:, 128 * h + 64:128 * h + 96] = (ql[:, :32] >> 4) | (((qh >> 4) & 3) << 4)
+        q[:, 128 * h + 96:128 * h + 128] = (ql[:, 32:] >> 4) | (((qh >> 6) & 3) << 4)
+    sc = b[:, 192:208].copy().view(np.int8).astype(np.float32)
+    d = b[:, 208:210].copy().view(f16).astype(np.float32)[:, 0]
+    dl = (d[:, None] * sc).astype(np.float32)                      # [n, 16]
+    return (np.repeat(dl, 16, axis=1) * (q - 32).astype(np.float32)).astype(np.float32)
+
+
+def dequant_q6_k_f16(blocks, N, K):
+    """A GGUF Q6_K tensor [N, K] as the fp16 weights the reference multiplies with, as fp32 values."""
+    return dequant_q6_k(blocks).reshape(N, K).astype(f16).astype(np.float32)
 
 
 def dequant_q4_k_f16(blocks, N, K):

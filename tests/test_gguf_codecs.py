@@ -231,6 +231,22 @@ def test_gguf_file_with_k_quant_tensors_reads_like_the_blocks(tmp_path):
     np.testing.assert_array_equal(q.dequant().astype(np.float16), want)   # the same fp16 weights as get()
 
 
+def test_q6_k_tensors_stream_as_codes(tmp_path):
+    rng = np.random.default_rng(8)
+    rows, K = 3, 512
+    blocks = [enc_q6_k(float(np.float16(rng.uniform(0.001, 0.05))), [int(v) for v in rng.integers(-128, 128, 16)],
+                       [int(v) for v in rng.integers(-32, 32, 256)]) for _ in range(rows * K // 256)]
+    raw = np.frombuffer(b"".join(blocks), np.uint8).reshape(rows, -1)
+    p = str(tmp_path / "q6.gguf")
+    _gguf.write_gguf(p, {"general.architecture": "llama", "llama.block_count": 1}, {"w": ("Q6_K", raw, (rows, K))})
+    g = _gguf.GGUFView(p)
+    want = _gguf.dequantize_blocks(_gguf.GGML["Q6_K"], raw).reshape(rows, K).astype(np.float16)
+    np.testing.assert_array_equal(g.get("w"), want)
+    q = g.quantized("w")                               # the chunked 6-bit layout, same fp16 weights
+    assert q.fmt == "q6_k" and q.shape == (rows, K) and q.codes.shape == (rows, K // 2)
+    np.testing.assert_array_equal(q.dequant().astype(np.float16), want)
+
+
 def test_unsupported_types_are_named():
     with pytest.raises(NotImplementedError, match="IQ2_XXS"):
         _gguf._nbytes(16, (256,))

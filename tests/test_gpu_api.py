@@ -295,10 +295,10 @@ def _kq_rows(kind, rows, K, rng):
 
 
 def test_load_gguf_k_quant_file(tmp_path):
-    """A Q4_K_M-style Qwen3-MoE GGUF (Q4_K gate/up experts, Q5_K down experts, Q6_K attention,
-    fp16 elsewhere): load_gguf dequantises the K-quants on the host to fp16, as the reference's
-    GGUFView.get does (aneforge/_gguf.py:34-39), and the decode matches the oracle over the same
-    fp16 weights."""
+    """A Q4_K_M-style Qwen3-MoE GGUF (Q4_K gate/up experts, Q6_K down experts and attention,
+    fp16 elsewhere): the experts stream as their Q4_K / Q6_K codes, the attention weights are
+    dequantised on the host to fp16 as the reference's GGUFView.get does (aneforge/_gguf.py:34-39),
+    and the decode matches the oracle over the same fp16 weights."""
     from aneforge_amd import _gguf
     say("moe.load_gguf on a synthetic K-quant GGUF")
     E, D, F, L, dh, H, KV = 4, 256, 256, 1, 64, 4, 2
@@ -321,9 +321,9 @@ def test_load_gguf_k_quant_file(tmp_path):
             raws = [_kq_rows("Q4_K", F, D, rng) for _ in range(E)]
             tensors[b + nm + ".weight"] = ("Q4_K", np.concatenate(raws), (E, F, D))
             lw[key] = np.stack([dec("Q4_K", r, F, D) for r in raws])
-        raws = [_kq_rows("Q5_K", D, F, rng) for _ in range(E)]               # GGUF down: [E, dim, ffn]
-        tensors[b + "ffn_down_exps.weight"] = ("Q5_K", np.concatenate(raws), (E, D, F))
-        lw["wdown_exps"] = np.stack([dec("Q5_K", r, D, F).T for r in raws])   # canonical [E, ffn, dim]
+        raws = [_kq_rows("Q6_K", D, F, rng) for _ in range(E)]               # GGUF down: [E, dim, ffn]
+        tensors[b + "ffn_down_exps.weight"] = ("Q6_K", np.concatenate(raws), (E, D, F))
+        lw["wdown_exps"] = np.stack([dec("Q6_K", r, D, F).T for r in raws])   # canonical [E, ffn, dim]
     meta = {"general.architecture": "qwen3moe", "qwen3moe.block_count": L, "qwen3moe.expert_count": E,
             "qwen3moe.expert_used_count": 2, "qwen3moe.embedding_length": D, "qwen3moe.attention.head_count": H,
             "qwen3moe.attention.head_count_kv": KV, "qwen3moe.attention.key_length": dh,
@@ -334,6 +334,8 @@ def test_load_gguf_k_quant_file(tmp_path):
     assert m.cfg.extra["n_experts"] == E and m.cfg.layers[0].qk_norm
     prompt = [5, 6, 7]
     got = m.generate(prompt, max_new_tokens=6)
+    mlp = m._layers[0][1]                              # layers materialise on first use
+    assert mlp.gu.fmt == "q4_k" and mlp.down.fmt == "q6_k"   # the experts stream as their K-quant codes
     enc16 = lambda W: np.asarray(W, np.float32).astype(np.float16).astype(np.float32)
     ow, ocfg = _oracle_weights(cfg, w, enc16)
     want, lgs = ref.generate(prompt, 6, ow, ocfg, M=len(prompt) + 6)

@@ -144,6 +144,44 @@ def test_linear_q4_k(K, M, N, Kd):
     check_f16(got, ref.linear(x, ref.dequant_q4_k_f16(blocks, N, Kd)), what="q4_k linear")
 
 
+def _q6k(N, Kd, seed):
+    # random GGUF Q6_K super-blocks: random ql / qh / int8 scales, a sane fp16 d
+    rng = np.random.default_rng(seed)
+    nb = N * Kd // 256
+    b = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
+    b[:, 208:210] = (np.abs(rng.standard_normal(nb)) * 0.0005 + 1e-5).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(N, Kd // 256 * 210)
+
+
+@pytest.mark.parametrize("N,Kd", [(3, 256), (257, 4096), (64, 11008)])
+def test_q6_k_repack_and_dequant_bit_exact(K, N, Kd):
+    say(f"q6_k repack + dequant N={N} K={Kd}")
+    from aneforge_amd import _blob
+    blocks = _q6k(N, Kd, 25 + N)
+    qs, sw = K.q6_k_repack(dev(blocks), N, Kd)
+    hq, hs = _blob.q6_k_repack(blocks, N, Kd)                # the device repack equals its host twin
+    assert np.array_equal(host(qs), hq) and np.array_equal(host(sw), hs)
+    want = ref.dequant_q6_k_f16(blocks, N, Kd)               # gguf-py's float32 steps, then fp16
+    got = host(K.dequant("q6_k", qs, sw, N, Kd))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    out = torch.full((N, Kd + 64), 7.0, dtype=torch.float16, device="cuda")
+    K.dequant_f16("q6_k", qs, sw, N, Kd, out=out[:, :Kd])
+    got16 = host(out)
+    assert np.array_equal(got16[:, :Kd].view(np.uint16), want.astype(np.float16).view(np.uint16))
+    assert (got16[:, Kd:] == 7.0).all()
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 4096, 4096), (1, 4096, 11008), (1, 22016, 4096), (3, 1000, 1024),
+                                    (1, 777, 4352), (5, 777, 4352), (12, 256, 11008)])
+def test_linear_q6_k(K, M, N, Kd):
+    say(f"linear q6_k M={M} N={N} K={Kd}")
+    blocks = _q6k(N, Kd, 90 + M)
+    qs, sw = K.q6_k_repack(dev(blocks), N, Kd)
+    x = np.random.default_rng(91).standard_normal((M, Kd)).astype(np.float16)
+    got = host(K.linear("q6_k", qs, sw, dev(x)))
+    check_f16(got, ref.linear(x, ref.dequant_q6_k_f16(blocks, N, Kd)), what="q6_k linear")
+
+
 @pytest.mark.parametrize("fmt", ["int8", "q4_0", "blockwise", "lut4"])
 def test_dequant_f16_bit_exact(K, fmt):
     # the fp16 weights the batched prefill expands a matrix to (rows of a wider scratch buffer)

@@ -426,3 +426,21 @@ def test_sample_matches_numpy_choice_and_its_filters():
     cnt = np.bincount([ref.sample(logits, 1.0, 0.7, 0, u) for u in us], minlength=1000)
     np.testing.assert_allclose(cnt[keep] / len(us), p[keep] / p[keep].sum(), atol=2.0 / len(us))
     assert ref.sample(logits, 0.0, 0.5, 3, 0.3) == int(np.argmax(logits))      # T <= 0: greedy
+
+
+def test_dequant_q6_k_kat_and_encoder():
+    # closed form: d = 0.25, scale_i = i - 8 (signed), code(e) = e % 64 -> w = 0.25 (e//16 - 8) (e%64 - 32)
+    from test_gguf_codecs import enc_q6_k
+    e = np.arange(256)
+    blk = np.frombuffer(enc_q6_k(0.25, [i - 8 for i in range(16)], [int(v) - 32 for v in e % 64]), np.uint8)
+    np.testing.assert_array_equal(ref.dequant_q6_k(blk)[0], (0.25 * (e // 16 - 8) * (e % 64 - 32)).astype(np.float32))
+    # element-by-element encoder: random scales and 6-bit codes decode to (d * sc) * (q - 32) in float32
+    rng = np.random.default_rng(6)
+    for _ in range(20):
+        d = float(np.float16(rng.uniform(1e-3, 0.05)))
+        sc = [int(v) for v in rng.integers(-128, 128, 16)]
+        q = [int(v) for v in rng.integers(-32, 32, 256)]
+        blk = np.frombuffer(enc_q6_k(d, sc, q), np.uint8)
+        want = np.array([np.float32(np.float32(d) * np.float32(sc[i // 16])) * np.float32(q[i]) for i in range(256)],
+                        np.float32)
+        np.testing.assert_array_equal(ref.dequant_q6_k(blk)[0], want)

@@ -7,7 +7,7 @@ at batch 1.  A "step" is one decode token (all layers + lm_head + argmax, one HI
 gate/up int8 GEMV, timed live with HIP events on its launch stream over all 32 layers'
 weights) and a CPU baseline (the numpy oracle on a bounded sample, run on this host).
 
-Kernel workloads (--workload gemv_w8 | gemv_q4 | attn | moe) time one configuration with
+Kernel workloads (--workload gemv_w8 | gemv_q4 | gemv_formats | attn | moe) time one configuration with
 rotating weight copies inside a captured graph (working set > 2x the 256 MB MALL).
 --workload copy streams a plain 1 GiB copy: the calibration run for the FETCH_SIZE /
 WRITE_SIZE counters behind roofline.traffic, and a measured copy ceiling.
@@ -34,7 +34,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv_w8", "gemv_q4", "attn", "moe", "kernels", "copy", "prefill"])
+                    choices=["decode", "gemv_w8", "gemv_q4", "gemv_formats", "attn", "moe", "kernels", "copy",
+                             "prefill"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--out", default=None, help="also append the JSON line to this file")
     ap.add_argument("--rows-hint", type=int, default=0)
@@ -118,6 +119,69 @@ def bench_gemv_w8(args):
     return {"workload": "cfg0 int8 per-channel GEMV 4096x4096", "batch": B, "us": ms * 1e3,
             "bytes": byts, "GBps": byts / (ms * 1e-3) / 1e9, "frac": byts / (ms * 1e-3) / HBM_PEAK,
             "copies": copies}
+
+
+def _format_weights(fmt, N, Kd, copies, g):
+    """Random weights of one format (codes + side arrays) for a GEMV timing, `copies` distinct sets."""
+    import torch
+    out = []
+    for _ in range(copies):
+        if fmt == "fp16":
+            out.append(((torch.randn((N, Kd), device="cuda", generator=g) * 0.02).half(), None))
+        elif fmt in ("int8", "blockwise"):
+            q = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
+            sh = (N, Kd // 32) if fmt == "blockwise" else (N,)
+            out.append((q, (torch.rand(sh, device="cuda", generator=g) * 1e-4).half()))
+        elif fmt == "q4_0":
+            out.append((torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g),
+                        (torch.rand((N, Kd // 32), device="cuda", generator=g) * 0.005).half()))
+        elif fmt == "lut4":
+            out.append((torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g),
+                        (torch.randn((N, 16), device="cuda", generator=g) * 0.02).half()))
+        elif fmt == "q4_k":
+            h = torch.randint(0, 2 ** 31 - 1, (N, Kd // 256, 5), dtype=torch.int32, device="cuda", generator=g)
+            h[:, :, 0] = 0x18001400                   # d = 2^-10, dmin = 2^-9
+            out.append((torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g),
+                        h.reshape(N, -1).contiguous()))
+        elif fmt == "q6_k":
+            h = torch.randint(0, 2 ** 31 - 1, (N, Kd // 32, 3), dtype=torch.int32, device="cuda", generator=g)
+            h[:, :, 2] = 0x1C000305                   # d = 2^-8, scales 5 and 3
+            out.append((torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g),
+                        h.reshape(N, -1).contiguous()))
+    return out
+
+
+def _format_bytes(fmt, N, Kd):
+    """Weight + side-array bytes of one [N, K] matrix in a kernel format."""
+    return {"fp16": 2 * N * Kd, "int8": N * Kd + 2 * N, "blockwise": N * Kd + N * Kd // 16,
+            "q4_0": N * Kd // 2 + N * Kd // 16, "lut4": N * Kd // 2 + 32 * N,
+            "q4_k": N * Kd // 2 + N * Kd // 256 * 20, "q6_k": N * Kd // 2 + N * Kd // 32 * 12}[fmt]
+
+
+def bench_gemv_formats(args):
+    """Every weight format's B=1 GEMV at the 7B shapes (4096x4096, 22016x4096, 4096x11008), on
+    rotating weight copies in a graph: microseconds and the format's bytes per microsecond."""
+    import torch
+    from aneforge_amd import _kernels as K
+    g = torch.Generator(device="cuda").manual_seed(4)
+    rows = []
+    for N, Kd in ((4096, 4096), (22016, 4096), (4096, 11008)):
+        for fmt in ("fp16", "int8", "blockwise", "q4_0", "lut4", "q4_k", "q6_k"):
+            byts = _format_bytes(fmt, N, Kd)
+            copies = n_copies(byts)
+            ws = _format_weights(fmt, N, Kd, copies, g)
+            x = torch.randn((1, Kd), device="cuda", generator=g).half()
+            y = torch.empty((1, N), dtype=torch.float16, device="cuda")
+            gr = Graph(lambda: [K.linear(fmt, w, sc, x, y=y) for w, sc in ws])
+            for _ in range(3):
+                gr.launch()
+            ms = min(gr.time_ms(max(1, args.steps // 8)) for _ in range(3)) / copies
+            gr.close()
+            rows.append({"workload": f"GEMV {fmt} {N}x{Kd} B=1", "us": ms * 1e3, "bytes": byts,
+                         "GBps": byts / (ms * 1e-3) / 1e9, "frac": byts / (ms * 1e-3) / HBM_PEAK, "copies": copies})
+            del ws
+            torch.cuda.empty_cache()
+    return rows
 
 
 def bench_gemv_q4(args, N=11008, Kd=4096):
@@ -498,8 +562,8 @@ def bench_decode(args):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
-                                   "design-only, see DESIGN.md)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the multi-GPU sharding "
+                                   "of the decode is designed, not built)"}))
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -511,6 +575,10 @@ def main():
         return
     if args.workload == "gemv_w8":
         print(json.dumps(bench_gemv_w8(args)))
+        return
+    if args.workload == "gemv_formats":
+        for r in bench_gemv_formats(args):
+            print(json.dumps(r), flush=True)
         return
     if args.workload == "gemv_q4":
         print(json.dumps(bench_gemv_q4(args)))

@@ -149,8 +149,11 @@ def dequant(fmt, w, scale, N, K):
 # --------------------------------------------------------------------------- attention
 def attn_ws_bytes(B, Hq, Hkv, D, max_len, nstep_hint=0) -> int:
     n = _hip.load().afx_decode_attn_ws_bytes(B, Hq, Hkv, D, max_len, nstep_hint)
-    if n < 0:
+    if n == -1:
         raise ValueError(f"decode attention: unsupported head dim {D}")
+    if n < 0:
+        raise ValueError(f"decode attention: a {max_len}-position cache needs more than 128 splits "
+                         f"at this split size (nstep {nstep_hint or 'from AFX_ATTN_NSTEP'})")
     return int(n)
 
 

@@ -51,3 +51,17 @@ def test_errors_surface_as_runtime_error_without_a_gpu():
         # non-null dummy addresses: validation rejects k before anything is dereferenced
         _hip.call("afx_moe_topk", 256, 1, 8, 9, 1, 256, 256, 256, 256, None)
     assert "k <= E" in _hip.last_error()
+
+
+def test_attention_workspace_sizes_and_their_errors_without_a_gpu():
+    # the workspace query is host arithmetic: a head dim outside {8..256} and a cache too long for the
+    # requested split size are told apart
+    import pytest
+    from aneforge_amd import _kernels as K
+    n = K.attn_ws_bytes(1, 32, 8, 128, 2048)
+    assert n > 0 and n % 4 == 0
+    assert K.attn_ws_bytes(16, 32, 8, 128, 8192) > n
+    with pytest.raises(ValueError, match="head dim"):
+        K.attn_ws_bytes(1, 32, 8, 100, 2048)
+    with pytest.raises(ValueError, match="128 splits"):
+        K.attn_ws_bytes(1, 32, 8, 128, 8192, nstep_hint=1)

@@ -96,12 +96,15 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
     m.bias = a.bias; m.resid = a.resid; m.M = a.M; m.N = a.N; m.K = a.K; m.epi = a.epi;
     return mfma_launch(fmt, m, 1, stream, what);
   }
-  if (a.M > 8) {
-    // the vector kernels take up to 8 rows: launch them 8 rows at a time
+  // the vector kernels take up to 8 rows a launch; with a norm prologue, as many as fit the 64 KB of
+  // LDS that stage the normalised rows (8 rows up to K = 3633, 4 to 6547, 2 to 10917, 1 to 16380)
+  int mmax = 8;
+  while (a.gamma && mmax > 1 && gemv_lds_bytes(mmax, a.K, true) > 65536) mmax >>= 1;
+  if (a.M > mmax) {
     const size_t ysz = a.epi == EPI_F32 ? 4 : 2;
-    for (int r0 = 0; r0 < a.M; r0 += 8) {
+    for (int r0 = 0; r0 < a.M; r0 += mmax) {
       GemvArgs c = a;
-      c.M = a.M - r0 < 8 ? a.M - r0 : 8;
+      c.M = a.M - r0 < mmax ? a.M - r0 : mmax;
       c.x = a.x + (size_t)r0 * a.ldx;
       c.y = (unsigned char*)a.y + (size_t)r0 * a.ldy * ysz;
       if (a.resid) c.resid = a.resid + (size_t)r0 * a.ldy;
@@ -110,7 +113,7 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
         c.kcache = a.kcache + (size_t)r0 * a.kv_seq_stride;
         c.vcache = a.vcache + (size_t)r0 * a.kv_seq_stride;
       }
-      const int rc = launch(fmt, c, eg, rows_hint, stream, what);
+      const int rc = launch(fmt, c, eg, rows_hint, stream, what);   // c.M <= mmax: no further split
       if (rc) return rc;
     }
     return 0;

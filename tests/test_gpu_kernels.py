@@ -7,7 +7,7 @@ wavefront's slab, partial attention splits)."""
 import numpy as np
 import pytest
 
-from _util import check_f16, check_hidden, cosine, dev, host, say
+from _util import MIN_COS, check_f16, check_hidden, cosine, dev, host, say
 from oracle import ref
 
 pytestmark = pytest.mark.gpu
@@ -440,6 +440,42 @@ def test_decode_attn_mask_and_causal(K):
                   kv_strides=(0, Skv * D), B=Sq, Hq=H)
     want2 = np.stack([ref.attention(q[:, :, s:s + 1], k, v, mask=m[s:s + 1])[0, :, 0] for s in range(Sq)], 1)
     check_f16(host(o2)[0], want2, what="mask")
+
+
+@pytest.mark.parametrize("fmt,M,N,Kd", [("int8", 8, 300, 4096), ("q4_0", 16, 52, 4480), ("q6_k", 9, 466, 5632),
+                                         ("int8", 3, 128, 11008), ("fp16", 5, 64, 16000)])
+def test_norm_prologue_linears_split_rows_to_fit_lds(K, fmt, M, N, Kd):
+    # RMSNorm-prologue linears stage M normalised rows in 64 KB of LDS; larger M * K runs in row groups
+    say(f"rms linear + swiglu {fmt} M={M} N={N} K={Kd}")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(M * 1000 + N)
+    if fmt == "int8":
+        q, s = _w8(N, Kd, 33)
+        w, sc, W = dev(q), dev(s), ref.dequant_w8(q, s)
+    elif fmt == "fp16":
+        W16 = (rng.standard_normal((N, Kd)) * 0.02).astype(np.float16)
+        w, sc, W = dev(W16), None, W16.astype(np.float32)
+    elif fmt == "q4_0":
+        blocks = ref.quantize_q4_0((rng.standard_normal((N, Kd)) * 0.05).astype(np.float32))
+        qs, d = _blob.q4_0_to_superblock(blocks, N, Kd)
+        w, sc, W = dev(qs), dev(d), ref.dequant_q4_0(blocks, N, Kd)
+    else:
+        blocks = _q6k(N, Kd, 7)
+        w, sc = K.q6_k_repack(dev(blocks), N, Kd)
+        W = ref.dequant_q6_k_f16(blocks, N, Kd)
+    x = rng.standard_normal((M, Kd)).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, Kd).astype(np.float16)
+    hn = ref.rms_norm(x, g, 1e-5)
+    yd = host(K.linear_rms(fmt, w, sc, dev(x), dev(g), 1e-5)).astype(np.float32)
+    check_f16(yd, ref.linear(hn, W), what="rms linear")
+    # The SwiGLU epilogue rounds the same fp32 accumulators to fp16 before silu(g) * u. Where one
+    # factor is small beside K terms of this size, accumulation-order noise inside the linear's own
+    # tolerance is >1% of it, so the epilogue is pinned against the device linear checked above and
+    # the whole against the oracle's product by cosine.
+    act = host(K.linear_swiglu(fmt, w, sc, dev(x), gamma=dev(g), eps=1e-5))
+    check_f16(act, ref.r16(ref.silu(yd[:, 0::2]) * yd[:, 1::2]), what="rms swiglu epilogue")
+    yy = ref.linear(hn, W).astype(np.float16).astype(np.float32)
+    assert cosine(act, ref.silu(yy[:, 0::2]) * yy[:, 1::2]) >= MIN_COS
 
 
 # ----------------------------------------------------------------------------- sampling

@@ -268,6 +268,44 @@ def test_linear_mfma_bias_residual_and_fp16(K):
     check_f16(got, ref.linear(x2, w.astype(np.float32)), what="fp16 MFMA")
 
 
+@pytest.mark.parametrize("fmt,M,N,Kd", [("int8", 16, 4100, 4096), ("q4_0", 16, 4100, 4096), ("blockwise", 9, 4100, 4096),
+                                         ("fp16", 12, 4100, 2048), ("q4_0", 4, 11008, 2048), ("int8", 13, 8200, 1024)])
+def test_linear_mfma_persistent_tiles_and_epilogues(K, fmt, M, N, Kd):
+    # dense linears of <= 16 rows whose K fits one batch per wavefront run on the persistent
+    # MFMA kernel (one workgroup per CU walking the 16-row tiles): N = 4100 gives workgroup 0 a
+    # second, ragged tile; plain, bias + residual, fp32 and SwiGLU epilogues
+    say(f"linear MFMA persistent fmt={fmt} M={M} N={N} K={Kd}")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(N + M + Kd)
+    if fmt == "int8":
+        q, s = _w8(N, Kd, 90 + M)
+        w, sc, W = dev(q), dev(s), ref.dequant_w8(q, s)
+    elif fmt == "blockwise":
+        q, s = _bw(N, Kd, 91 + M)
+        w, sc, W = dev(q), dev(s), ref.dequant_blockwise(q, s)
+    elif fmt == "fp16":
+        W16 = (rng.standard_normal((N, Kd)) * 0.02).astype(np.float16)
+        w, sc, W = dev(W16), None, W16.astype(np.float32)
+    else:
+        blocks = ref.quantize_q4_0((rng.standard_normal((N, Kd)) * 0.05).astype(np.float32))
+        qs, d = _blob.q4_0_to_superblock(blocks, N, Kd)
+        # the MFMA operand is the fp16 weight fp16((code - 8) * d), as GGUFView.get hands it over
+        w, sc, W = dev(qs), dev(d), ref.dequant_q4_0_f16(blocks, N, Kd)
+    x = rng.standard_normal((M, Kd)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    r = rng.standard_normal((M, N)).astype(np.float16)
+    y = host(K.linear(fmt, w, sc, dev(x)))
+    check_f16(y, ref.linear(x, W), what=f"{fmt} persistent MFMA")
+    got = host(K.linear(fmt, w, sc, dev(x), bias=dev(b), residual=dev(r)))
+    check_hidden(got, ref.r16(r.astype(np.float64) + ref.linear(x, W, b)), what=f"{fmt} bias+residual")
+    got32 = host(K.linear(fmt, w, sc, dev(x), out_f32=True))
+    check_f16(got32, ref.linear(x, W, exact=True), what=f"{fmt} fp32 out")
+    # interleaved gate/up rows: the epilogue rounds gate and up to fp16 before silu(g) * u
+    act = host(K.linear_swiglu(fmt, w, sc, dev(x)))
+    yd = y.astype(np.float32)
+    check_f16(act, ref.r16(ref.silu(yd[:, 0::2]) * yd[:, 1::2]), what=f"{fmt} swiglu epilogue")
+
+
 @pytest.mark.parametrize("M,N,Kd", [(1, 11008, 4096), (1, 4096, 11008), (4, 11008, 4096), (4, 4096, 11008),
                                     (8, 11008, 4096), (8, 4096, 11008), (3, 100, 384)])
 def test_linear_q4_0_cfg1(K, M, N, Kd):

@@ -23,6 +23,7 @@ struct MfmaArgs {
   int N, K;
   int epi;                 // EPI_F16 / EPI_RESID / EPI_F32 / EPI_SWIGLU (gemv epilogue codes)
   int xbytes;              // set by mfma_launch: bytes of the activation rows the kernel may read
+  int E;                   // set by mfma_launch: experts (1 for a dense linear)
 };
 
 // Launch the MFMA kernel over E experts (1 for a dense linear).  Returns 0 or a negative code.

@@ -282,15 +282,17 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
   }
 }
 
-// Persistent variant for a dense linear of at most 16 activation rows whose K range per
-// wavefront is one batch (<= kSPB steps).  One workgroup per CU walks the 16-row tiles
-// blockIdx.x, + gridDim.x, ...  Each wavefront loads its slice of x into registers once and
-// keeps it for every tile (x leaves L2 once per workgroup instead of once per tile), and the
-// next tile's weight loads go out before the current tile's MFMAs.  The cross-wavefront sums
+// Persistent variant for at most 16 activation rows (dense) or 16 tokens (MoE) whose K range
+// per wavefront is one batch (<= kSPB steps).  One workgroup per CU walks 16-row tiles: a dense
+// linear's tiles blockIdx.x, + gridDim.x, ...; MoE, a contiguous range of the active experts'
+// (expert, tile) units.  Each wavefront loads its slice of x into registers once (MoE: again
+// when the expert changes) and keeps it for every tile (x leaves L2 about once per workgroup
+// instead of once per tile), and the weight loads of the next PD tiles are in flight while a
+// tile's MFMAs run.  The cross-wavefront sums
 // alternate between two LDS buffers: one barrier per tile (wavefront 0 reads tile i's buffer
 // before it reaches the barrier of tile i + 1; the other wavefronts write that buffer again
 // only for tile i + 2, after that barrier).
-template <int FMT, int EG, int NW>
+template <int FMT, int EG, int NW, int PD, bool MOE>
 __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   constexpr int KS = MfmaFmt<FMT>::kK, NM = MfmaFmt<FMT>::kMfma;
   constexpr int kSPS = FMT == FMT_Q4 ? 4 : 2;     // block scales per step (Q4_0, blockwise)
@@ -310,46 +312,102 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   unsigned char* wls = wl[wave];
   unsigned char* sls = sl[wave];
 
-  // this wavefront's slice of x in the B-operand layout (token column r, k slot g)
-  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, a.xbytes);
-  const bool tok_ok = r < a.M;
-  const int xoff = tok_ok ? r * a.ldx * 2 : kOOB;  // out of range: reads zeros
-  u4 xv[kSPB][NM];
-#pragma unroll
-  for (int t = 0; t < kSPB; ++t) {
-    const int s = s0 + t;
-#pragma unroll
-    for (int j = 0; j < NM; ++j) {
-      int kx;
-      if constexpr (FMT == FMT_I8 || FMT == FMT_BW) kx = s * KS + 16 * g + 8 * j;
-      else if constexpr (FMT == FMT_Q4) kx = 32 * (4 * s + j) + 8 * g;
-      else kx = s * KS + 8 * g;
-      xv[t][j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xrs, t < nsw ? xoff + kx * 2 : kOOB, 0, 0));
-    }
+  // Work units.  A dense linear walks the tiles blockIdx.x, + G, ...  MoE (cnt != null) takes a
+  // contiguous, expert-major range of the active experts' (expert, tile) units, so its x (the
+  // expert's routed rows) changes at most a few times per workgroup.  Every branch depends only
+  // on blockIdx / gridDim and the expert counts (workgroup-uniform): all wavefronts meet every
+  // barrier.
+  const int G = gridDim.x;
+  int v = blockIdx.x, vend = ntiles, vstep = G;
+  if constexpr (MOE) {
+    int nact = 0;
+    for (int e = 0; e < a.E; ++e) nact += a.cnt[e] > 0;
+    const long long U = (long long)nact * ntiles;
+    v = (int)(U * blockIdx.x / G);
+    vend = (int)(U * (blockIdx.x + 1) / G);
+    vstep = 1;
   }
+  if (v >= vend) return;                           // whole workgroup, before any barrier
+  // unit -> (expert, tile); MoE units are mapped in ascending order, the active expert map_e
+  // covering units [map_base, map_base + ntiles)
+  int map_e = -1, map_base = -ntiles;
+  auto unit = [&](int u, int& e, int& tile) {
+    if constexpr (!MOE) {
+      e = 0;
+      tile = u;
+      return;
+    }
+    while (u >= map_base + ntiles) {
+      do { ++map_e; } while (map_e < a.E - 1 && a.cnt[map_e] <= 0);
+      map_base += ntiles;
+    }
+    e = map_e;
+    tile = u - map_base;
+  };
+
+  // this wavefront's slice of x in the B-operand layout (token column r, k slot g), for the
+  // expert xe (MoE: column r is entry r of the expert's list; dense: activation row r)
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, a.xbytes);
+  bool tok_ok = false;
+  int yr = r, xe = -1;
+  u4 xv[kSPB][NM];
+  auto load_x = [&](int e) {
+    int xr = r;
+    tok_ok = r < a.M;
+    if constexpr (MOE) {
+      const int* lst = a.list + (size_t)e * a.T;
+      tok_ok = r < a.cnt[e];
+      const int ent = tok_ok ? lst[r] : 0;
+      xr = a.x_by_token ? ent / a.k : ent;
+      yr = ent;                                    // output row: the entry
+    }
+    const int xoff = tok_ok ? xr * a.ldx * 2 : kOOB;   // out of range: reads zeros
+#pragma unroll
+    for (int t = 0; t < kSPB; ++t) {
+      const int s = s0 + t;
+#pragma unroll
+      for (int j = 0; j < NM; ++j) {
+        int kx;
+        if constexpr (FMT == FMT_I8 || FMT == FMT_BW) kx = s * KS + 16 * g + 8 * j;
+        else if constexpr (FMT == FMT_Q4) kx = 32 * (4 * s + j) + 8 * g;
+        else kx = s * KS + 8 * g;
+        xv[t][j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xrs, t < nsw ? xoff + kx * 2 : kOOB, 0, 0));
+      }
+    }
+    xe = e;
+  };
 
   // One tile's weights for this wavefront's steps: 16 rows x 256 bytes, row-contiguous (chunks
   // past this wavefront's range belong to the next one: loaded, never used; clamped at the row
   // end), and the steps' block scales (lane l: row l / 4, step s0 + l % 4).
-  auto load_tile = [&](int tile, u4 (&wq)[4], u2& sq) {
+  auto load_tile = [&](int e, int tile, u4 (&wq)[4], u2& sq) {
+    const unsigned char* wb = wbase + (size_t)e * a.w_es;
     const int n0 = tile * 16;
     int c = s0 * 4 + lc;
     c = c < nsteps * 4 ? c : nsteps * 4 - 1;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
       const int row = n0 + 4 * h + lr < N ? n0 + 4 * h + lr : N - 1;   // tail rows computed, not stored
-      wq[h] = __builtin_nontemporal_load((const u4*)(wbase + (size_t)row * rowbytes + (size_t)c * 16));
+      wq[h] = __builtin_nontemporal_load((const u4*)(wb + (size_t)row * rowbytes + (size_t)c * 16));
     }
     if constexpr (has_block_scales<FMT>()) {
       const int row = n0 + (lane >> 2) < N ? n0 + (lane >> 2) : N - 1;
       int q = s0 + (lane & 3);
       q = q < nsteps ? q : nsteps - 1;
-      const half_t* sp = a.scale + (size_t)row * (K >> 5) + (size_t)q * kSPS;
+      const half_t* sp = a.scale + (size_t)e * a.s_es + (size_t)row * (K >> 5) + (size_t)q * kSPS;
       if constexpr (FMT == FMT_Q4) sq = *(const u2*)sp;
       else sq = (u2){*(const uint32_t*)sp, 0u};
     }
   };
-  auto compute_tile = [&](int tile, const u4 (&wq)[4], const u2& sq, f4 (&rd)[NW][64]) {
+  auto compute_tile = [&](int e, int tile, const u4 (&wq)[4], const u2& sq, f4 (&rd)[NW][64]) {
+    if constexpr (MOE) {
+      // the next expert's rows; the full wait keeps these loads from leaving the compiler's
+      // wait counts (in-order, shared with the prefetched tiles) pending past the branch
+      if (e != xe) {
+        load_x(e);
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+    }
     wave_sync_lds();                               // the previous tile's staged reads are done
 #pragma unroll
     for (int h = 0; h < 4; ++h) *(u4*)(wls + (4 * h + lr) * kWRow + lc * 16) = wq[h];
@@ -385,30 +443,52 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] += p[i];
       }
-      mfma_store<FMT, EG>(a, a.scale, v, tile * 16 + 4 * g, tok_ok, r);
+      mfma_store<FMT, EG>(a, a.scale + (size_t)e * a.s_es, v, tile * 16 + 4 * g, tok_ok, yr);
     }
   };
 
-  // Tiles in pairs, so the two weight buffers have fixed registers (a second tile in flight
-  // measured slower: 10.7 against 10.2 us for Q4_0 11008 x 4096 at 4 rows).  Every branch
-  // depends only on blockIdx / gridDim (workgroup-uniform): all wavefronts meet every barrier.
-  const int G = gridDim.x;
-  u4 wa[4], wb[4];
-  u2 sa = {0u, 0u}, sb = {0u, 0u};
-  int tile = blockIdx.x;                           // the grid never exceeds the tile count
-  load_tile(tile, wa, sa);
-  for (;;) {
-    const int t1 = tile + G;
-    if (t1 < ntiles) load_tile(t1, wb, sb);
-    __builtin_amdgcn_sched_barrier(0);
-    compute_tile(tile, wa, sa, red[0]);
-    if (t1 >= ntiles) break;
-    const int t2 = t1 + G;
-    if (t2 < ntiles) load_tile(t2, wa, sa);
-    __builtin_amdgcn_sched_barrier(0);
-    compute_tile(t1, wb, sb, red[1]);
-    if (t2 >= ntiles) break;
-    tile = t2;
+  // PD units in flight ahead of the one being computed: unit j in buffer j % (PD + 1), the
+  // buffers rotated by a fully unrolled inner loop (fixed registers).  PD = 1 for a few units
+  // per workgroup (a deeper prefetch measured slower there: 10.7 against 10.2 us for Q4_0
+  // 11008 x 4096 at 4 rows), PD = 3 for long runs of units (MoE).
+  constexpr int NBUF = PD + 1;
+  u4 wq[NBUF][4];
+  u2 sq[NBUF];
+  int eu[NBUF], tu[NBUF];
+#pragma unroll
+  for (int b = 0; b < NBUF; ++b) {
+    sq[b] = (u2){0u, 0u};
+    eu[b] = 0;
+    tu[b] = 0;
+  }
+  unit(v, eu[0], tu[0]);
+  load_x(eu[0]);
+  load_tile(eu[0], tu[0], wq[0], sq[0]);
+#pragma unroll
+  for (int b = 1; b < PD; ++b) {
+    const int vb = v + b * vstep;
+    if (vb < vend) {
+      unit(vb, eu[b], tu[b]);
+      load_tile(eu[b], tu[b], wq[b], sq[b]);
+    }
+  }
+  int i = 0;                                       // units computed so far
+  bool more = true;
+  while (more) {
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) {
+      if (!more) break;
+      const int vi = v + i * vstep;
+      const int vp = vi + PD * vstep;              // prefetch unit i + PD into buffer (b + PD) % NBUF
+      if (vp < vend) {
+        unit(vp, eu[(b + PD) % NBUF], tu[(b + PD) % NBUF]);
+        load_tile(eu[(b + PD) % NBUF], tu[(b + PD) % NBUF], wq[(b + PD) % NBUF], sq[(b + PD) % NBUF]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute_tile(eu[b], tu[b], wq[b], sq[b], red[i & 1]);
+      ++i;
+      more = vi + vstep < vend;
+    }
   }
 }
 
@@ -434,19 +514,28 @@ static mfma_fn pick_mfma(int fmt, bool swiglu, int nw, int nb) {
   return swiglu ? pick_mfma_w<FMT_F16, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_F16, EG_PLAIN>(nw, nb);
 }
 
-template <int FMT, int EG>
+template <int FMT, int EG, int PD, bool MOE>
 static mfma_fn pick_mfma_px_w(int nw) {
-  return nw == 4 ? mfma_px_kernel<FMT, EG, 4> : nw == 8 ? mfma_px_kernel<FMT, EG, 8> : mfma_px_kernel<FMT, EG, 16>;
+  if constexpr (FMT == FMT_Q4)   // Q4_0 never takes 16 wavefronts (its x slice would not fit 128 VGPRs)
+    return nw == 4 ? mfma_px_kernel<FMT, EG, 4, PD, MOE> : mfma_px_kernel<FMT, EG, 8, PD, MOE>;
+  else   // 16 wavefronts keep one unit of prefetch: three would spill at the 128-VGPR cap
+    return nw == 4 ? mfma_px_kernel<FMT, EG, 4, PD, MOE>
+         : nw == 8 ? mfma_px_kernel<FMT, EG, 8, PD, MOE> : mfma_px_kernel<FMT, EG, 16, 1, MOE>;
 }
-static mfma_fn pick_mfma_px(int fmt, bool swiglu, int nw) {
-  if (fmt == FMT_I8) return swiglu ? pick_mfma_px_w<FMT_I8, EG_SWIGLU>(nw) : pick_mfma_px_w<FMT_I8, EG_PLAIN>(nw);
-  if (fmt == FMT_BW) return swiglu ? pick_mfma_px_w<FMT_BW, EG_SWIGLU>(nw) : pick_mfma_px_w<FMT_BW, EG_PLAIN>(nw);
-  if (fmt == FMT_Q4) {
-    // Q4_0 never takes 16 wavefronts (the x slice would not fit the 128-VGPR budget)
-    return swiglu ? (nw == 4 ? mfma_px_kernel<FMT_Q4, EG_SWIGLU, 4> : mfma_px_kernel<FMT_Q4, EG_SWIGLU, 8>)
-                  : (nw == 4 ? mfma_px_kernel<FMT_Q4, EG_PLAIN, 4> : mfma_px_kernel<FMT_Q4, EG_PLAIN, 8>);
-  }
-  return swiglu ? pick_mfma_px_w<FMT_F16, EG_SWIGLU>(nw) : pick_mfma_px_w<FMT_F16, EG_PLAIN>(nw);
+template <int FMT, bool MOE>
+static mfma_fn pick_mfma_px_f(bool swiglu, int nw, int pd) {
+  if (pd == 3) return swiglu ? pick_mfma_px_w<FMT, EG_SWIGLU, 3, MOE>(nw) : pick_mfma_px_w<FMT, EG_PLAIN, 3, MOE>(nw);
+  return swiglu ? pick_mfma_px_w<FMT, EG_SWIGLU, 1, MOE>(nw) : pick_mfma_px_w<FMT, EG_PLAIN, 1, MOE>(nw);
+}
+template <bool MOE>
+static mfma_fn pick_mfma_px_m(int fmt, bool swiglu, int nw, int pd) {
+  if (fmt == FMT_I8) return pick_mfma_px_f<FMT_I8, MOE>(swiglu, nw, pd);
+  if (fmt == FMT_BW) return pick_mfma_px_f<FMT_BW, MOE>(swiglu, nw, pd);
+  if (fmt == FMT_Q4) return pick_mfma_px_f<FMT_Q4, MOE>(swiglu, nw, pd);
+  return pick_mfma_px_f<FMT_F16, MOE>(swiglu, nw, pd);
+}
+static mfma_fn pick_mfma_px(int fmt, bool swiglu, int nw, int pd, bool moe) {
+  return moe ? pick_mfma_px_m<true>(fmt, swiglu, nw, pd) : pick_mfma_px_m<false>(fmt, swiglu, nw, pd);
 }
 
 static int mfma_cus() {
@@ -486,23 +575,26 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
               "%s: a weight matrix of %d x %d exceeds the 2 GiB buffer range", what, a.N, a.K);
   MfmaArgs b = a;
   b.xbytes = (int)xbytes;
+  b.E = E;
   const bool swiglu = a.epi == EPI_SWIGLU;
   // wavefronts per workgroup: the fewest of 4, 8, 16 that leave each wavefront at most four
   // batches; batches per round = batches per wavefront, capped at 4 (measured on MI355X);
   // AFX_MFMA_WAVES=4|8|16 overrides when that count also leaves at most four batches
   const int ks = fmt == FMT_I8 || fmt == FMT_BW ? 64 : fmt == FMT_Q4 ? 128 : 32;
   const int nsteps = a.K / ks;
-  // Persistent variant (dense, <= 16 rows): the most wavefronts (up to 8 for Q4_0, whose x slice
-  // takes 64 VGPRs, else 16) that leave each one a single batch; AFX_MFMA_PX=0 disables it,
-  // AFX_MFMA_PX_WAVES=4|8|16 caps the wavefronts.
-  static int px_env = -2, px_waves = 0;
+  // Persistent variant (dense <= 16 rows, MoE <= 16 tokens): the most wavefronts (up to 8 for
+  // Q4_0, whose x slice takes 64 VGPRs, else 16) that leave each one a single batch;
+  // AFX_MFMA_PX=0 disables it, AFX_MFMA_PX_WAVES=4|8|16 caps the wavefronts.
+  static int px_env = -2, px_waves = 0, px_depth = 0;
   if (px_env == -2) {
     const char* e = getenv("AFX_MFMA_PX");
     px_env = e ? atoi(e) : 1;
     const char* w = getenv("AFX_MFMA_PX_WAVES");
     px_waves = w ? atoi(w) : 0;
+    const char* d = getenv("AFX_MFMA_PX_DEPTH");
+    px_depth = d ? atoi(d) : 0;
   }
-  if (px_env != 0 && E == 1 && !a.cnt && a.M <= 16) {
+  if (px_env != 0 && (a.cnt ? a.T <= 16 : E == 1 && a.M <= 16)) {
     int cap = fmt == FMT_Q4 ? 8 : 16;
     if (px_waves == 4 || px_waves == 8 || px_waves == 16) cap = px_waves < cap ? px_waves : cap;
     int pw = 0;
@@ -510,8 +602,14 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
       if (nsteps >= w && (nsteps + w - 1) / w <= kSPB) { pw = w; break; }
     if (pw) {
       const int ntiles = (a.N + 15) / 16;
-      const int grid = ntiles < mfma_cus() ? ntiles : mfma_cus();
-      mfma_fn fn = pick_mfma_px(fmt, swiglu, pw);
+      const long long units = (long long)ntiles * E;   // MoE: units of empty experts are skipped
+      const int grid = units < mfma_cus() ? (int)units : mfma_cus();
+      // prefetch depth: three units ahead for long runs of units per workgroup, else one;
+      // AFX_MFMA_PX_DEPTH=1|3 overrides
+      int pd = (units + grid - 1) / grid >= 6 ? 3 : 1;
+      if (px_depth == 1 || px_depth == 3) pd = px_depth;
+      if (pw == 16) pd = 1;
+      mfma_fn fn = pick_mfma_px(fmt, swiglu, pw, pd, a.cnt != nullptr);
       hipLaunchKernelGGL(fn, dim3(grid), dim3(pw * 64), 0, stream, b);
       return check_launch(what);
     }

@@ -649,6 +649,46 @@ def test_moe_layer_sparse_dispatch(K, fmt):
     check_hidden(out, want, what="moe")           # residual-stream output: fp16-ulp atol
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "int8"])
+def test_moe_gateup_units_cross_experts_and_skip_empty_ones(K, fmt):
+    # 12 tokens top-2 over 5 experts, expert 2 routed no token; 2100 intermediate rows (263
+    # tiles per expert): with at most 16 tokens per expert the persistent MFMA kernel gives each
+    # workgroup a contiguous range of the active experts' tiles, and the ranges cross experts
+    say(f"moe gate/up E=5 (one empty) k=2 T=12 D=1024 F=2100 fmt={fmt}")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(75)
+    E, k, T, D, F = 5, 2, 12, 1024, 2100
+    x = rng.standard_normal((T, D)).astype(np.float16)
+    Wg = rng.normal(0, 0.05, (E, F, D)).astype(np.float32)
+    Wu = rng.normal(0, 0.05, (E, F, D)).astype(np.float32)
+    ws, ss, Gf, Uf = [], [], [], []
+    for e in range(E):
+        if fmt == "q4_0":
+            bg, bu = _blob.quantize_q4_0(Wg[e]), _blob.quantize_q4_0(Wu[e])
+            Gf.append(ref.dequant_q4_0_f16(bg, F, D)); Uf.append(ref.dequant_q4_0_f16(bu, F, D))
+            qg, dg = _blob.q4_0_to_superblock(bg, F, D)
+            qu, du = _blob.q4_0_to_superblock(bu, F, D)
+        else:
+            qg, dg = _blob.quantize_per_row(Wg[e]); qu, du = _blob.quantize_per_row(Wu[e])
+            Gf.append(ref.dequant_w8(qg, dg)); Uf.append(ref.dequant_w8(qu, du))
+        ws.append(_blob.interleave_rows(qg, qu)); ss.append(_blob.interleave_rows(dg, du))
+    active = [0, 1, 3, 4]
+    pick = [rng.choice(active, 2, replace=False) for _ in range(T)]
+    cnt = np.zeros(E, np.int32)
+    lst = np.zeros((E, T), np.int32)
+    for t in range(T):
+        for slot, e in enumerate(pick[t]):
+            lst[e, cnt[e]] = t * k + slot
+            cnt[e] += 1
+    assert cnt[2] == 0 and cnt.max() <= 16
+    act = host(K.moe_gateup(fmt, dev(np.stack(ws)), dev(np.stack(ss)), dev(x), k, E, F, dev(cnt), dev(lst)))
+    for t in range(T):
+        for slot, e in enumerate(pick[t]):
+            g = ref.linear(x[t:t + 1], Gf[e])
+            u = ref.linear(x[t:t + 1], Uf[e])
+            check_f16(act[t * k + slot:t * k + slot + 1], ref.r16(ref.silu(g) * u), what=f"token {t} expert {e}")
+
+
 def test_moe_topk_largest_expert_count_with_ties(K):
     # E = 2049 (the reference's upper bound) and k = 64: probabilities on power-of-two levels with
     # many exact ties, so the lowest-index rule decides most picks

@@ -269,11 +269,13 @@ def test_linear_mfma_bias_residual_and_fp16(K):
 
 
 @pytest.mark.parametrize("fmt,M,N,Kd", [("int8", 16, 4100, 4096), ("q4_0", 16, 4100, 4096), ("blockwise", 9, 4100, 4096),
-                                         ("fp16", 12, 4100, 2048), ("q4_0", 4, 11008, 2048), ("int8", 13, 8200, 1024)])
+                                         ("fp16", 12, 4100, 2048), ("q4_0", 4, 11008, 2048), ("int8", 13, 8200, 1024),
+                                         ("q4_0", 5, 25000, 4096)])
 def test_linear_mfma_persistent_tiles_and_epilogues(K, fmt, M, N, Kd):
     # dense linears of <= 16 rows whose K fits one batch per wavefront run on the persistent
     # MFMA kernel (one workgroup per CU walking the 16-row tiles): N = 4100 gives workgroup 0 a
-    # second, ragged tile; plain, bias + residual, fp32 and SwiGLU epilogues
+    # second, ragged tile; N = 25000 (Q4_0, >= 6 tiles per workgroup) keeps three tiles of weights
+    # in flight; plain, bias + residual, fp32 and SwiGLU epilogues
     say(f"linear MFMA persistent fmt={fmt} M={M} N={N} K={Kd}")
     from aneforge_amd import _blob
     rng = np.random.default_rng(N + M + Kd)

@@ -44,6 +44,7 @@ template <> struct MfmaFmt<FMT_F16> { static constexpr int kK = 32, kMfma = 1; }
 template <> struct MfmaFmt<FMT_BW> { static constexpr int kK = 64, kMfma = 2; };
 
 constexpr int kSPB = 4;            // steps per batch: 16 rows x 256 bytes
+constexpr int kPxMaxExperts = 2056; // experts the persistent kernel's LDS list holds (the reference allows 2049)
 constexpr int kWRow = 256 + 16;    // LDS bytes per staged weight row
 constexpr int kSRow = 40;          // LDS bytes per staged Q4_0 scale row (4 superblocks x 8 B, padded)
 
@@ -318,31 +319,44 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   // on blockIdx / gridDim and the expert counts (workgroup-uniform): all wavefronts meet every
   // barrier.
   const int G = gridDim.x;
+  // MoE: the active experts, in order, compacted into LDS by the whole workgroup (a ballot prefix
+  // per 64 experts), so a unit's expert is one LDS read and the expert count costs E / (64 NW)
+  // rounds of loads, not E dependent ones.
+  __shared__ int act_e[MOE ? kPxMaxExperts : 1];
+  __shared__ int wcnt[NW];
   int v = blockIdx.x, vend = ntiles, vstep = G;
   if constexpr (MOE) {
     int nact = 0;
-    for (int e = 0; e < a.E; ++e) nact += a.cnt[e] > 0;
+    for (int base = 0; base < a.E; base += NW * 64) {
+      const int e = base + (int)threadIdx.x;
+      const bool act = e < a.E && a.cnt[e] > 0;
+      const unsigned long long m = __ballot(act);
+      if (lane == 0) wcnt[wave] = __popcll(m);
+      __syncthreads();
+      int off = nact, tot = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        off += w < wave ? wcnt[w] : 0;
+        tot += wcnt[w];
+      }
+      if (act) act_e[off + __popcll(m & ((1ull << lane) - 1))] = e;
+      nact += tot;
+      __syncthreads();                             // wcnt is rewritten next round; act_e is complete
+    }
     const long long U = (long long)nact * ntiles;
     v = (int)(U * blockIdx.x / G);
     vend = (int)(U * (blockIdx.x + 1) / G);
     vstep = 1;
   }
-  if (v >= vend) return;                           // whole workgroup, before any barrier
-  // unit -> (expert, tile); MoE units are mapped in ascending order, the active expert map_e
-  // covering units [map_base, map_base + ntiles)
-  int map_e = -1, map_base = -ntiles;
+  if (v >= vend) return;                           // whole workgroup, after its last barrier
   auto unit = [&](int u, int& e, int& tile) {
-    if constexpr (!MOE) {
+    if constexpr (MOE) {
+      e = act_e[u / ntiles];
+      tile = u % ntiles;
+    } else {
       e = 0;
       tile = u;
-      return;
     }
-    while (u >= map_base + ntiles) {
-      do { ++map_e; } while (map_e < a.E - 1 && a.cnt[map_e] <= 0);
-      map_base += ntiles;
-    }
-    e = map_e;
-    tile = u - map_base;
   };
 
   // this wavefront's slice of x in the B-operand layout (token column r, k slot g), for the
@@ -594,7 +608,7 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
     const char* d = getenv("AFX_MFMA_PX_DEPTH");
     px_depth = d ? atoi(d) : 0;
   }
-  if (px_env != 0 && (a.cnt ? a.T <= 16 : E == 1 && a.M <= 16)) {
+  if (px_env != 0 && (a.cnt ? a.T <= 16 && E <= kPxMaxExperts : E == 1 && a.M <= 16)) {
     int cap = fmt == FMT_Q4 ? 8 : 16;
     if (px_waves == 4 || px_waves == 8 || px_waves == 16) cap = px_waves < cap ? px_waves : cap;
     int pw = 0;

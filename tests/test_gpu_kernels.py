@@ -691,6 +691,31 @@ def test_moe_gateup_units_cross_experts_and_skip_empty_ones(K, fmt):
             check_f16(act[t * k + slot:t * k + slot + 1], ref.r16(ref.silu(g) * u), what=f"token {t} expert {e}")
 
 
+def test_moe_gateup_many_experts_few_active(K):
+    # 600 experts, 24 of them routed: the persistent MFMA kernel compacts the active experts
+    # into LDS over several rounds of the whole workgroup (512 threads per round)
+    say("moe gate/up E=600 (24 active) k=2 T=12 D=1024 F=64 int8")
+    rng = np.random.default_rng(76)
+    E, k, T, D, F = 600, 2, 12, 1024, 64
+    q = rng.integers(-127, 128, (E, 2 * F, D), dtype=np.int8)                 # gate/up rows interleaved
+    s = (np.abs(rng.normal(0, 0.02, (E, 2 * F))) / 127).astype(np.float16)
+    x = rng.standard_normal((T, D)).astype(np.float16)
+    active = rng.choice(E, 24, replace=False)
+    pick = [rng.choice(active, 2, replace=False) for _ in range(T)]
+    cnt = np.zeros(E, np.int32)
+    lst = np.zeros((E, T), np.int32)
+    for t in range(T):
+        for slot, e in enumerate(pick[t]):
+            lst[e, cnt[e]] = t * k + slot
+            cnt[e] += 1
+    act = host(K.moe_gateup("int8", dev(q), dev(s), dev(x), k, E, F, dev(cnt), dev(lst)))
+    for t in range(T):
+        for slot, e in enumerate(pick[t]):
+            W = ref.dequant_w8(q[e], s[e])
+            g, u = ref.linear(x[t:t + 1], W[0::2]), ref.linear(x[t:t + 1], W[1::2])
+            check_f16(act[t * k + slot:t * k + slot + 1], ref.r16(ref.silu(g) * u), what=f"token {t} expert {e}")
+
+
 def test_moe_topk_largest_expert_count_with_ties(K):
     # E = 2049 (the reference's upper bound) and k = 64: probabilities on power-of-two levels with
     # many exact ties, so the lowest-index rule decides most picks

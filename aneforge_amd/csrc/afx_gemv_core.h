@@ -64,19 +64,22 @@ template <> struct Fmt<FMT_Q4> {
       x[4 * j + 0] = t[0]; x[4 * j + 1] = t[1]; x[4 * j + 2] = t[2]; x[4 * j + 3] = t[3];
     }
   }
+  // The weight is fp16((code - 8) * d), one v_pk_mul_f16 per pair (the exact product rounded
+  // once): the value GGUFView.get hands the reference's matmul (aneforge/_gguf.py:34-39), and the
+  // one the MFMA and prefill kernels multiply with.
   __device__ static float dot(const u4& w, const h2 (&x)[kXH2], const u2& d, const Ctx&, float acc) {
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
     const h2 d01 = as_h2(d.x), d23 = as_h2(d.y);
-    const float ds[4] = {(float)d01.x, (float)d01.y, (float)d23.x, (float)d23.y};
+    const half_t dh[4] = {d01.x, d01.y, d23.x, d23.y};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       h2 q[4];
       q4_word_to_h2(wd[j], q);
-      float s = dot2(q[0], x[4 * j + 0], 0.0f);
-      s = dot2(q[1], x[4 * j + 1], s);
-      s = dot2(q[2], x[4 * j + 2], s);
-      s = dot2(q[3], x[4 * j + 3], s);
-      acc = __builtin_fmaf(ds[j], s, acc);
+      const h2 d2 = {dh[j], dh[j]};
+      acc = dot2(q[0] * d2, x[4 * j + 0], acc);
+      acc = dot2(q[1] * d2, x[4 * j + 1], acc);
+      acc = dot2(q[2] * d2, x[4 * j + 2], acc);
+      acc = dot2(q[3] * d2, x[4 * j + 3], acc);
     }
     return acc;
   }

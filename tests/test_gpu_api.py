@@ -43,7 +43,7 @@ def test_compile_encodings(compress):
     if compress is None or compress == "sparse":
         Wf = W.astype(np.float16).astype(np.float32)
     elif compress == "q4_0":
-        Wf = ref.dequant_q4_0(ref.quantize_q4_0(W), 96, 256)
+        Wf = ref.dequant_q4_0_f16(ref.quantize_q4_0(W), 96, 256)
     elif compress == "blockwise":
         q, s, bs = ref.quantize_blockwise(W, 32)
         Wf = (q.reshape(96, 8, 32) * s.astype(np.float32)[:, :, None]).reshape(96, 256).astype(np.float16).astype(np.float32)
@@ -212,7 +212,7 @@ def test_moe_decoder_generate_matches_oracle(compress, qk):
            "int8": lambda W: ref.dequant_w8(*ref.quantize_per_row(W)),
            "blockwise": lambda W: ref.dequant_blockwise(*ref.quantize_blockwise(W, 32)),
            "int4": lambda W: _lut4_rec(W),
-           "q4_0": lambda W: ref.dequant_q4_0(ref.quantize_q4_0(W), *np.asarray(W).shape)}[compress]
+           "q4_0": lambda W: ref.dequant_q4_0_f16(ref.quantize_q4_0(W), *np.asarray(W).shape)}[compress]
     m = af.LlamaPrefill(cfg, w, compress=compress)
     prompt = [3, 9, 27, 1]
     got = m.generate(prompt, max_new_tokens=8)
@@ -436,9 +436,9 @@ def test_load_gguf_q4_0_experts_stay_4bit(tmp_path):
     enc16 = lambda W: np.asarray(W, np.float32).astype(np.float16).astype(np.float32)
     ow, ocfg = _oracle_weights(cfg, w, enc16)
     for i, lw in enumerate(w["layers"]):
-        ow["layers"][i]["wgate_exps"] = [ref.dequant_q4_0(ref.quantize_q4_0(g), F, D) for g in lw["wgate_exps"]]
-        ow["layers"][i]["wup_exps"] = [ref.dequant_q4_0(ref.quantize_q4_0(u), F, D) for u in lw["wup_exps"]]
-        ow["layers"][i]["wdown_exps"] = [ref.dequant_q4_0(ref.quantize_q4_0(np.ascontiguousarray(d.T)), D, F)
+        ow["layers"][i]["wgate_exps"] = [ref.dequant_q4_0_f16(ref.quantize_q4_0(g), F, D) for g in lw["wgate_exps"]]
+        ow["layers"][i]["wup_exps"] = [ref.dequant_q4_0_f16(ref.quantize_q4_0(u), F, D) for u in lw["wup_exps"]]
+        ow["layers"][i]["wdown_exps"] = [ref.dequant_q4_0_f16(ref.quantize_q4_0(np.ascontiguousarray(d.T)), D, F)
                                          for d in lw["wdown_exps"]]
     want, lgs = ref.generate(prompt, 6, ow, ocfg, M=len(prompt) + 6)
     from test_gpu_llm import _assert_tokens_match

@@ -316,7 +316,7 @@ def test_linear_q4_0_cfg1(K, M, N, Kd):
     c = workloads.cfg1_gemv_q4(N, Kd, M)
     qs, d = K.q4_repack(dev(c["blocks"]), N, Kd)
     got = host(K.linear("q4_0", qs, d, dev(c["x"])))
-    want = ref.linear(c["x"], ref.dequant_q4_0(c["blocks"], N, Kd))
+    want = ref.linear(c["x"], ref.dequant_q4_0_f16(c["blocks"], N, Kd))
     check_f16(got, want, what="q4_0 linear")
 
 
@@ -345,7 +345,7 @@ def test_linear_rms_prologue(K, fmt):
         from aneforge_amd import workloads
         c = workloads.cfg1_gemv_q4(N, Kd, 1, seed=26)
         wd, sd = K.q4_repack(dev(c["blocks"]), N, Kd)
-        Wf = ref.dequant_q4_0(c["blocks"], N, Kd)
+        Wf = ref.dequant_q4_0_f16(c["blocks"], N, Kd)
     else:
         Wf16 = rng.normal(0, 0.02, (N, Kd)).astype(np.float16)
         wd, sd, Wf = dev(Wf16), None, Wf16.astype(np.float32)
@@ -498,7 +498,7 @@ def test_norm_prologue_linears_split_rows_to_fit_lds(K, fmt, M, N, Kd):
     elif fmt == "q4_0":
         blocks = ref.quantize_q4_0((rng.standard_normal((N, Kd)) * 0.05).astype(np.float32))
         qs, d = _blob.q4_0_to_superblock(blocks, N, Kd)
-        w, sc, W = dev(qs), dev(d), ref.dequant_q4_0(blocks, N, Kd)
+        w, sc, W = dev(qs), dev(d), ref.dequant_q4_0_f16(blocks, N, Kd)
     else:
         blocks = _q6k(N, Kd, 7)
         w, sc = K.q6_k_repack(dev(blocks), N, Kd)

@@ -55,7 +55,8 @@ int afx_event_destroy(void* ev);
  * 4+ rows without a norm prologue run on MFMA, otherwise the vector kernels take 8 rows a launch.
  * fmt 0: the compress="int8" linear, constexpr_affine_dequantize(axis=0) + matmul
  * (aneforge/_compile.py:171-179, 375-385; aneforge/graph.py:187-195); 1: the GGUF Q4_0 weights
- * the reference dequantises on the host (aneforge/_gguf.py:34-39); 2: fp16; 3: compress=
+ * the reference dequantises on the host and casts to fp16 (aneforge/_gguf.py:34-39), weight
+ * fp16((code - 8) * d); 2: fp16; 3: compress=
  * "blockwise" with 32-weight blocks, int8 codes + fp16 scale[N][K/32], weight fp16(q * s)
  * (aneforge/_blob.py:46-56, constexpr_blockwise_shift_scale in aneforge/_compile.py:112-188);
  * 4: compress="int4", palettize_lut4's packed indices [N][K/2] (column 2j in the low nibble of byte

@@ -52,6 +52,8 @@ SIGNATURES: dict[str, tuple] = {
     "afx_sample": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _ll, _vp]),
     "afx_decode_attn": (_i, [_vp, _vp, _vp, _vp, _ll, _ll, _ll, _ll, _i, _i, _i, _i, _i, _vp, _i, _vp, _ll,
                              _i, _f, _vp, _ll, _i, _vp]),
+    "afx_decode_attn_noalloc": (_i, [_vp, _vp, _vp, _vp, _ll, _ll, _ll, _ll, _i, _i, _i, _i, _i, _vp, _i, _vp,
+                                     _ll, _i, _f, _i, _vp]),
     # norms, rope, sampling, generic tensor ops
     "afx_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _i, _i, _i, _vp]),
     "afx_rope": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp]),

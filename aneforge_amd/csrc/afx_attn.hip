@@ -22,11 +22,21 @@
 // splits, needs an agent-scope release per workgroup; on this part that writes back the
 // XCD's L2 and costs more than the second launch, so the merge is a launch of its own.)
 #include <stdlib.h>
+#include <mutex>
 #include "afx_common.h"
 
 namespace afx {
 
 constexpr int kMaxSplits = 128;   // partials per (b, head); the chunk grows so ctx/chunk <= this
+
+// Split partials of afx_decode_attn_noalloc: a file-scope device array instead of a caller
+// workspace.  Every device the library runs on holds its own copy until the process ends.  In
+// host code `scratch` only names the symbol; its device address comes from hipGetSymbolAddress,
+// once per device (scratch_ptr below).  16 MiB holds B * Hq * splits * (D + 2) fp32 partials for
+// every decode-attention shape of the 7B models at the default split size (B = 16, 32 heads,
+// ctx 8192: 8.5 MB; B = 1: at most 0.6 MB).
+constexpr long long kScratchBytes = 16ll << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 struct AttnArgs {
   const half_t* q;   // [B][Hq][D] via strides
@@ -498,6 +508,65 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
                    : D == 64 ? pick_combine<64>(a.nsp) : D == 128 ? pick_combine<128>(a.nsp) : pick_combine<256>(a.nsp);
   hipLaunchKernelGGL(cf, dim3(Hq, B), dim3(D < 64 ? 64 : D), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_attn(combine)");
+}
+
+}  // extern "C"
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];   // device address of `scratch` on each device, once resolved
+
+// The calling thread's current device's copy of `scratch` (resolved on its first call there).
+int scratch_ptr(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error("afx_decode_attn_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error("afx_decode_attn_noalloc: device %d >= %d", dev, kMaxDevices);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) return set_error("afx_decode_attn_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return set_error("afx_decode_attn_noalloc: stream is on device %d, current device is %d", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error("afx_decode_attn_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+// afx_decode_attn with its split partials in the device's `scratch` array: no allocation and
+// no workspace argument.  Shapes whose partials exceed kScratchBytes are rejected.  Calls that
+// overlap on one device share the array and race; every split slot is written by each call
+// before the combine reads it, so nothing needs clearing between calls.
+int afx_decode_attn_noalloc(const void* q, const void* k, const void* v, void* o, long long q_bs,
+                            long long q_hs, long long kv_bs, long long kv_hs, int B, int Hq, int Hkv, int D,
+                            int ctx_len, const int* pos, int max_len, const void* mask, long long mask_bs,
+                            int causal_off, float scale, int nstep_hint, void* stream) {
+  const long long need = afx_decode_attn_ws_bytes(B, Hq, Hkv, D, max_len, nstep_hint);
+  AFX_REQUIRE(need != -1, "afx_decode_attn_noalloc: head dim %d not supported (8, 16, 32, 64, 128, 256)", D);
+  AFX_REQUIRE(need > 0, "afx_decode_attn_noalloc: max_len=%d needs more than %d splits", max_len, kMaxSplits);
+  AFX_REQUIRE(need <= kScratchBytes,
+              "afx_decode_attn_noalloc: B=%d Hq=%d D=%d max_len=%d needs %lld B of split partials, more than "
+              "the %lld B scratch array (use afx_decode_attn with a workspace)",
+              B, Hq, D, max_len, need, kScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_ptr(stream, &ws);
+  if (rc) return rc;
+  return afx_decode_attn(q, k, v, o, q_bs, q_hs, kv_bs, kv_hs, B, Hq, Hkv, D, ctx_len, pos, max_len, mask,
+                         mask_bs, causal_off, scale, ws, kScratchBytes, nstep_hint, stream);
 }
 
 }  // extern "C"

@@ -124,6 +124,16 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
                     long long kv_bs, long long kv_hs, int B, int Hq, int Hkv, int D, int ctx_len,
                     const int* pos, int max_len, const void* mask, long long mask_bs, int causal_off,
                     float scale, void* ws, long long ws_bytes, int nstep_hint, void* stream);
+/* No counterpart in the reference.  afx_decode_attn without a workspace, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * the split partials go to a 16 MiB device array inside the library, one per device, held until the
+ * process ends.  Calls whose partials (afx_decode_attn_ws_bytes) exceed 16 MiB fail with an error.
+ * The stream must belong to the calling thread's current device.  Calls that overlap on one device
+ * share the array and race. */
+int afx_decode_attn_noalloc(const void* q, const void* k, const void* v, void* o, long long q_bs,
+                            long long q_hs, long long kv_bs, long long kv_hs, int B, int Hq, int Hkv, int D,
+                            int ctx_len, const int* pos, int max_len, const void* mask, long long mask_bs,
+                            int causal_off, float scale, int nstep_hint, void* stream);
 
 /* ---- norms, rope, sampling -------------------------------------------------------------- */
 

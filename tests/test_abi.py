@@ -65,3 +65,16 @@ def test_attention_workspace_sizes_and_their_errors_without_a_gpu():
         K.attn_ws_bytes(1, 32, 8, 100, 2048)
     with pytest.raises(ValueError, match="128 splits"):
         K.attn_ws_bytes(1, 32, 8, 128, 8192, nstep_hint=1)
+
+
+def test_noalloc_attention_rejects_shapes_beyond_its_scratch_without_a_gpu():
+    # the size check is host arithmetic before any device call: 64 sequences of 32 heads at 8192
+    # positions need 34 MB of split partials, more than the 16 MiB array
+    import pytest
+    from aneforge_amd import _hip
+    with pytest.raises(RuntimeError, match="scratch array"):
+        _hip.call("afx_decode_attn_noalloc", 256, 256, 256, 256, 32 * 128, 128, 8 * 8192 * 128, 8192 * 128,
+                  64, 32, 8, 128, 8192, None, 8192, None, 0, -1, 0.088, 16, None)
+    with pytest.raises(RuntimeError, match="head dim"):
+        _hip.call("afx_decode_attn_noalloc", 256, 256, 256, 256, 32 * 100, 100, 8 * 64 * 100, 64 * 100,
+                  1, 32, 8, 100, 64, None, 64, None, 0, -1, 0.1, 0, None)

@@ -73,6 +73,24 @@ def cfg3_layer_host(dim=4096, n_heads=32, n_kv_heads=8, ffn=11008, seed=3, layer
     return lw
 
 
+def cfg3_kv_host(layer: int, prefill: int = 2048, n_kv_heads: int = 8, dh: int = 128, seed: int = 3):
+    """Layer `layer`'s prefilled cache rows [0, prefill): K then V, each N(0, 1) fp16 [KV, prefill, dh]."""
+    rng = np.random.default_rng((seed, 2000 + layer))
+    k = rng.standard_normal((n_kv_heads, prefill, dh)).astype(F16)
+    v = rng.standard_normal((n_kv_heads, prefill, dh)).astype(F16)
+    return k, v
+
+
+def cfg3_embed_head_host(vocab: int = 32000, dim: int = 4096, seed: int = 3):
+    """Embedding table N(0, 1) * 0.02 and lm_head N(0, 0.02), both fp16 [vocab, dim], and the
+    first token id."""
+    rng = np.random.default_rng((seed, 1000))
+    embed = (rng.standard_normal((vocab, dim)) * 0.02).astype(F16)
+    head = rng.normal(0, 0.02, (vocab, dim)).astype(F16)
+    tok0 = int(rng.integers(0, vocab))
+    return embed, head, tok0
+
+
 def cfg4_moe(T=16, dim=4096, ffn=14336, E=8, seed=4):
     """Router fp16 N(0, 0.02), Q4_0 experts as cfg1 (gate/up [ffn, dim], down [dim, ffn]),
     hidden states N(0, 1), rms gamma = 1."""

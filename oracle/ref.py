@@ -26,6 +26,7 @@ Pinning status (see tests/test_oracle.py):
   attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
   topk_gate / moe_layer                 pinned: reference tie KAT + HF Qwen3-MoE block
   decoder step / generate               pinned: HF LlamaForCausalLM (tiny, fp32)
+  decode_rows                           pinned: n sequential decode_layer calls (dense and MoE layers)
   palettize_lut4 (aneforge_amd._blob)   pinned: vectors recorded from the reference function
                                         (tests/golden/make_lut4_vectors.py, lut4_vectors.npz)
 """
@@ -343,19 +344,27 @@ def moe_layer(h16, mlp_norm, router, Wg, Wu, Wd, k, renorm=True, eps=1e-5, exact
     """MoE SwiGLU MLP with residual (aneforge/moe.py:48-63), active experts only (identical to
     the dense all-expert sum because unselected experts carry weight 0).  Wg/Wu [E, F, D] and
     Wd [E, D, F] as dequantised fp32; rounding points follow the HIP kernels:
-    act = fp16(silu(fp16 g) * fp16 u), y_e = fp16(act Wd_e^T), out = fp16(h + fp16(sum g*y))."""
+    act = fp16(silu(fp16 g) * fp16 u), y_e = fp16(act Wd_e^T), out = fp16(h + fp16(sum g*y)).
+    Each active expert's weights are taken to float64 once, for all the tokens routed to it; the
+    per-token sum runs over its experts in ascending index order."""
     h = np.asarray(h16, np.float64)
     hn = rms_norm(h, mlp_norm, eps, exact)
     gate, chosen = moe_route(hn, router, k, renorm, exact)
     T, D = h.shape
+    ys = {}
+    for e in sorted({e for c in chosen for e in c}):
+        rows = [t for t in range(T) if e in chosen[t]]
+        x = hn[rows]
+        g = r16(x @ np.asarray(Wg[e], np.float64).T, exact)
+        u = r16(x @ np.asarray(Wu[e], np.float64).T, exact)
+        a = r16(silu(g) * u, exact)
+        y = r16(a @ np.asarray(Wd[e], np.float64).T, exact)
+        for i, t in enumerate(rows):
+            ys[t, e] = y[i]
     comb = np.zeros((T, D))
     for t in range(T):
         for e in chosen[t]:
-            g = r16(hn[t] @ np.asarray(Wg[e], np.float64).T, exact)
-            u = r16(hn[t] @ np.asarray(Wu[e], np.float64).T, exact)
-            a = r16(silu(g) * u, exact)
-            y = r16(a @ np.asarray(Wd[e], np.float64).T, exact)
-            comb[t] += gate[t, e] * y
+            comb[t] += gate[t, e] * ys[t, e]
     return r16(h + r16(comb, exact), exact), gate, chosen
 
 
@@ -399,10 +408,51 @@ def decode_layer(h16, w, cfg, K, V, pos, cos_row, sin_row, exact=False, trace=No
     return out
 
 
+def decode_rows(h16, w, cfg, K, V, pos0, cos, sin, exact=False):
+    """decode_layer for n consecutive tokens at positions pos0 .. pos0 + n - 1 in one pass over
+    the layer's weights (teacher forcing: the n input hidden rows are given).  Row t writes cache
+    row pos0 + t and attends to rows [0, pos0 + t], so the result is that of n decode_layer calls
+    in order (aneforge/llm.py:214-237, :171-175).  cos/sin are the full [M, dh] tables; K/V
+    [KV, M, dh] are updated in place.  Returns the new hidden rows [n, D]."""
+    H, KV, dh, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg["dh"], cfg["norm_eps"]
+    h = np.asarray(h16, np.float64)
+    n = h.shape[0]
+    xn = rms_norm(h, w["attn_norm"], eps, exact)
+    q = linear(xn, w["wq"], w.get("q_bias"), exact).reshape(n, H, dh)
+    k = linear(xn, w["wk"], w.get("k_bias"), exact).reshape(n, KV, dh)
+    v = linear(xn, w["wv"], w.get("v_bias"), exact).reshape(n, KV, dh)
+    if "q_norm" in w:
+        q = rms_norm(q, w["q_norm"], eps, exact)
+        k = rms_norm(k, w["k_norm"], eps, exact)
+    if cfg.get("rope", True):
+        c = np.asarray(cos)[pos0:pos0 + n, None, :]
+        s = np.asarray(sin)[pos0:pos0 + n, None, :]
+        q = rope(q, c, s, exact)
+        k = rope(k, c, s, exact)
+    K[:, pos0:pos0 + n] = k.transpose(1, 0, 2)
+    V[:, pos0:pos0 + n] = v.transpose(1, 0, 2)
+    Kb = np.broadcast_to(K, (n,) + K.shape)
+    Vb = np.broadcast_to(V, (n,) + V.shape)
+    a = attention(q[:, :, None, :], Kb, Vb, 1.0 / np.sqrt(dh), pos0 + 1 + np.arange(n), exact=exact)
+    a = a.reshape(n, H * dh)
+    h1 = r16(h + linear(a, w["wo"], w.get("o_bias"), exact), exact)
+    if "router" in w:
+        out, _, _ = moe_layer(h1, w["mlp_norm"], w["router"], w["wgate_exps"], w["wup_exps"], w["wdown_exps"],
+                              cfg["top_k"], cfg.get("norm_topk_prob", True), eps, exact)
+        return out
+    hn = rms_norm(h1, w["mlp_norm"], eps, exact)
+    g = linear(hn, w["wgate"], None, exact)
+    u = linear(hn, w["wup"], None, exact)
+    act = r16(silu(g) * u, exact)
+    return r16(h1 + linear(act, w["wdown"], None, exact), exact)
+
+
 def logits(h16, final_norm, lm_head, eps=1e-5, exact=False):
-    """Final RMSNorm then the fp16 lm_head, logits kept in float64 (aneforge/llm.py:395-404)."""
+    """Final RMSNorm then the fp16 lm_head, logits kept in float64 (aneforge/llm.py:395-404).
+    One row of logits per hidden row: [n, vocab]."""
     hn = rms_norm(h16, final_norm, eps, exact)
-    return np.asarray(hn, np.float64).reshape(1, -1) @ np.asarray(lm_head, np.float64).T
+    lm = np.asarray(lm_head, np.float64)
+    return np.asarray(hn, np.float64).reshape(-1, lm.shape[1]) @ lm.T
 
 
 def decode_step(tok, pos, W, cfg, caches, tables, exact=False, trace=None):

@@ -1,0 +1,235 @@
+"""Two BASELINE configurations at their full shapes against the oracle.
+
+cfg3: the 32-layer 7B-shape int8 decode (d 4096, 32/8 heads, SwiGLU 11008, vocab 32000, fp16
+lm_head), its KV cache prefilled with N(0, 1) rows [0, 2048), 128 greedy steps from position 2048.
+Checks, after the reference's decode-exactness tests (tests/test_llm.py:39-101):
+  - element-wise (rtol 1e-2, atol 1e-3 or one fp16 ulp of the layer's magnitude, cosine >= 0.9999)
+    where both sides start from the same input: each layer at step 0 fed the device's own input
+    hidden state, and the lm_head at every step fed the device's own final hidden state;
+  - cosine >= 0.9999 where the oracle runs free from its own hidden states (each layer at step 0,
+    every step's final hidden state and logits): fp16 rounding differences compound over 32
+    layers, so element-wise bounds do not apply there;
+  - greedy-token equality at every step. The oracle is teacher-forced with the device's tokens,
+    so each step's logits come from the same history and one pass over each layer's weights
+    serves all 128 steps (oracle.ref.decode_rows);
+  - the graph-replayed steps give the per-token steps' tokens and logits exactly.
+
+cfg4: one MoE decode layer, 8 Q4_0 experts (gate/up 14336x4096, down 4096x14336), top-2 with
+renormalisation, 16 tokens (tests/test_moe.py:23-57): the exact routing sets and the output.
+
+Host memory stays bounded: cfg3 keeps the int8 codes (5.9 GB) and expands one layer at a time."""
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+from _util import check_f16, check_hidden, cosine, say
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+P, STEPS = 2048, 128
+
+
+def _f64_layer(lh):
+    """A layer's int8 codes x row scales in float64 (exact: each product has <= 19 significant
+    bits), expanded with torch's CPU threads."""
+    out = {}
+    for k, v in lh.items():
+        if k.startswith("w"):
+            q, s = v
+            out[k] = (torch.from_numpy(q).to(torch.float64)
+                      * torch.from_numpy(s.astype(np.float64))[:, None]).numpy()
+        else:
+            out[k] = np.asarray(v, np.float64)
+    return out
+
+
+def test_cfg3_full_model_parity_128_steps():
+    from aneforge_amd import _engine as E, workloads
+    from aneforge_amd.llm import LlamaConfig, LlamaPrefill
+    c = workloads.CFG3
+    L, D, V, KVH, dh = c["n_layers"], c["dim"], c["vocab"], c["n_kv_heads"], 128
+    say(f"cfg3 full model: {L} layers int8, KV prefilled to {P}, {STEPS} greedy steps (host draw)")
+    with ThreadPoolExecutor(16) as ex:
+        host_layers = list(ex.map(lambda i: workloads.cfg3_layer_host(layer=i), range(L)))
+        kv = list(ex.map(lambda i: workloads.cfg3_kv_host(i, P), range(L)))
+    embed, head, tok0 = workloads.cfg3_embed_head_host()
+    w = {"embed": embed, "final_norm": np.ones(D, np.float16), "lm_head": head, "layers": []}
+    for lh in host_layers:
+        lw = {k: E.QuantizedWeight("int8", v[0], v[1], v[0].shape) for k, v in lh.items() if k.startswith("w")}
+        lw["attn_norm"], lw["mlp_norm"] = lh["attn_norm"], lh["mlp_norm"]
+        w["layers"].append(lw)
+    cfg = LlamaConfig(dim=D, n_layers=L, n_heads=c["n_heads"], n_kv_heads=KVH, ffn_dim=c["ffn_dim"], vocab=V)
+    m = LlamaPrefill(cfg, w)
+    d = m._decoder(P + STEPS + 8)
+    for (mixer, _), (k, v) in zip(d.layers, kv):
+        mixer.kc[0, :, :P].copy_(torch.from_numpy(k))
+        mixer.vc[0, :, :P].copy_(torch.from_numpy(v))
+    d.reset([tok0], pos0=P, zero_state=False)
+    say("cfg3 device: step 0 layer by layer, then per-token steps, then the same steps as graph replays")
+    hs, finals, logits = [], [], []
+    with torch.cuda.stream(d.stream):
+        for mixer, mlp in d.layers:
+            mixer.enqueue(d)
+            mlp.enqueue(d)
+            hs.append(d.h.clone())
+        finals.append(d.h.clone())
+        d.enqueue_head()
+        logits.append(d.logits.clone())
+        d.enqueue_advance(True)
+        for _ in range(1, STEPS):
+            d.enqueue_layers()
+            finals.append(d.h.clone())
+            d.enqueue_head()
+            logits.append(d.logits.clone())
+            d.enqueue_advance(True)
+    toks = d.history(0, STEPS)
+    last = d.logits_host().copy()
+    d.reset([tok0], pos0=P, zero_state=False)          # rows >= P are rewritten by the replays
+    d.run(0, STEPS)
+    assert d.history(0, STEPS) == toks, "graph-replayed steps differ from the per-token steps"
+    assert np.array_equal(d.logits_host(), last)
+    hs = [t.float().cpu().numpy()[0] for t in hs]
+    finals = np.stack([t.float().cpu().numpy()[0] for t in finals])
+    logits = np.stack([t.cpu().numpy()[0] for t in logits])
+    m.release()
+
+    say("cfg3 oracle: teacher-forced rows, one layer at a time")
+    oc = {"n_heads": c["n_heads"], "n_kv_heads": KVH, "dh": dh, "norm_eps": c["norm_eps"]}
+    cos, sin = ref.rope_tables(P + STEPS, dh)
+    rows = ref.r16(embed[[tok0] + toks[:-1]].astype(np.float64))
+    h_in = ref.r16(embed[tok0].astype(np.float64)).reshape(1, -1)
+    q0, s0 = host_layers[0]["wq"]
+    with ThreadPoolExecutor(1) as ex:
+        nxt = ex.submit(_f64_layer, host_layers[0])
+        for li in range(L):
+            wl = nxt.result()
+            if li + 1 < L:
+                nxt = ex.submit(_f64_layer, host_layers[li + 1])
+            if li == 0:                     # the expansion is the oracle's int8 dequant, bit for bit
+                assert np.array_equal(wl["wq"][:64], ref.dequant_w8(q0[:64], s0[:64]).astype(np.float64))
+            Kc = np.zeros((KVH, P + STEPS, dh))
+            Vc = np.zeros((KVH, P + STEPS, dh))
+            Kc[:, :P], Vc[:, :P] = kv[li]
+            # layer li alone, on the device's own input hidden state
+            Ki, Vi = Kc[:, :P + 1].copy(), Vc[:, :P + 1].copy()
+            iso = ref.decode_layer(h_in, wl, oc, Ki, Vi, P, cos[P], sin[P])
+            check_hidden(hs[li], iso[0], what=f"cfg3 layer {li} step 0 (device input)")
+            assert cosine(hs[li], iso[0]) >= 0.9999
+            h_in = hs[li].reshape(1, -1)
+            # all steps through layer li, free running from the oracle's own hidden states
+            rows = ref.decode_rows(rows, wl, oc, Kc, Vc, P, cos, sin)
+            c0 = cosine(hs[li], rows[0])
+            assert c0 >= 0.9999, f"cfg3 layer {li} step 0 (free-running oracle): cosine {c0:.6f}"
+            del wl
+    # the head on the device's own final hidden state, every step
+    head_on_dev = ref.logits(finals, np.ones(D), head, c["norm_eps"])
+    for s in range(STEPS):
+        check_f16(logits[s], head_on_dev[s], what=f"cfg3 lm_head step {s} (device input)")
+    # free running: final hidden states, logits and greedy tokens
+    want = ref.logits(rows, np.ones(D), head, c["norm_eps"])
+    near_ties = []
+    for s in range(STEPS):
+        cf, cl = cosine(finals[s], rows[s]), cosine(logits[s], want[s])
+        assert cf >= 0.9999 and cl >= 0.9999, f"cfg3 step {s}: hidden cosine {cf:.6f}, logits cosine {cl:.6f}"
+        t = int(np.argmax(want[s]))
+        if toks[s] != t:
+            top = np.sort(want[s])[-2:]
+            gap = (top[1] - top[0]) / np.abs(want[s]).max()
+            assert gap < 2e-3 and want[s][toks[s]] >= top[0] - 1e-6, \
+                f"cfg3 step {s}: device token {toks[s]} vs oracle {t} with a clear margin {gap:.2e}"
+            near_ties.append(s)
+    err = np.abs(logits - want).max() / np.abs(want).max()
+    say(f"cfg3: {STEPS} steps, tokens equal except near-ties at {near_ties}; free-running logits max rel err {err:.2e}")
+    assert len(near_ties) <= 2
+
+
+def test_cfg4_moe_layer_full_shape():
+    from aneforge_amd import _blob, _engine as E, workloads
+    from aneforge_amd.llm import LayerSpec, LlamaConfig
+    from aneforge_amd.moe import MoEDecode
+    c4 = workloads.CFG4
+    Ex, k, D, F, T = c4["n_experts"], c4["top_k"], c4["dim"], c4["ffn"], c4["tokens"]
+    say(f"cfg4 MoE layer: E={Ex} top-{k} D={D} F={F} T={T}, Q4_0 experts (host draw, default_rng(4))")
+    c = workloads.cfg4_moe(T=T, dim=D, ffn=F, E=Ex)
+    ex_ = c["experts"]
+
+    def sb(args):
+        blocks, n, kk = args
+        qs, dd = _blob.q4_0_to_superblock(blocks, n, kk)
+        return E.QuantizedWeight("q4_0", qs, dd, (n, kk))
+
+    jobs = [(e["gate"], F, D) for e in ex_] + [(e["up"], F, D) for e in ex_] + [(e["down"], D, F) for e in ex_]
+    with ThreadPoolExecutor(16) as pool:
+        qw = list(pool.map(sb, jobs))
+    lw = {"mlp_norm": c["mlp_norm"], "router": c["router"], "wgate_exps": qw[:Ex], "wup_exps": qw[Ex:2 * Ex],
+          "wdown_exps": qw[2 * Ex:]}
+    cfg = LlamaConfig(dim=D, n_layers=1, n_heads=32, n_kv_heads=8, ffn_dim=F, vocab=32,
+                      extra={"n_experts": Ex, "n_experts_per_tok": k, "norm_topk_prob": True})
+    moe = MoEDecode(lw, cfg, LayerSpec(mlp="moe"), None)
+    bufs = moe._make_bufs(T)
+    h = torch.from_numpy(c["h"]).cuda()
+    say("cfg4 device layer")
+    moe.run(h, bufs)
+    torch.cuda.synchronize()
+    out = h.cpu().numpy()
+    sel = bufs["sel"].cpu().numpy()
+    cnt = bufs["cnt"].cpu().numpy()
+    del moe, bufs
+    say("cfg4 oracle")
+    with ThreadPoolExecutor(16) as pool:
+        deq = list(pool.map(lambda j: ref.dequant_q4_0_f16(*j), jobs))
+    want, gate, chosen = ref.moe_layer(c["h"], c["mlp_norm"], c["router"], deq[:Ex], deq[Ex:2 * Ex],
+                                       deq[2 * Ex:], k, True, 1e-5)
+    assert [sorted(r) for r in sel.tolist()] == chosen
+    assert cnt.tolist() == [sum(e in r for r in chosen) for e in range(Ex)]
+    active = sum(1 for n in cnt if n > 0)
+    say(f"cfg4: routing sets equal, {active} experts active")
+    check_hidden(out, want, what="cfg4 MoE layer output")
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4_0"])
+def test_moe_down_and_dense_linear_at_k14336(fmt):
+    """The cfg4 expert down projection's shape (K = 14336: the widest tile-per-workgroup MFMA
+    launch) for int8 as well as Q4_0, through afx_moe_down over a host-made routing of 16 tokens
+    x top-2 over 8 experts, and a dense linear at K = 14336 with 20 rows (two token groups)."""
+    from aneforge_amd import _blob, _kernels as K
+    from _util import dev, host
+    E, k, T, D, F = 8, 2, 16, 4096, 14336
+    say(f"moe down + dense linear at K={F} fmt={fmt}")
+    rng = np.random.default_rng(90)
+    act = rng.standard_normal((T * k, F)).astype(np.float16)
+
+    def weights(n, kk, seed):
+        r = np.random.default_rng(seed)
+        if fmt == "int8":
+            q = r.integers(-127, 128, (n, kk), dtype=np.int8)
+            s = (np.abs(r.normal(0, 0.02, n)) / 127).astype(np.float16)
+            return q, s, ref.dequant_w8(q, s)
+        from aneforge_amd import workloads
+        codes = r.integers(0, 16, (n, kk), dtype=np.uint8)
+        d = (np.abs(r.normal(0, 0.02, (n, kk // 32))) / 8).astype(np.float16)
+        blocks = workloads.q4_blocks_from_codes(codes, d)
+        qs, dd = _blob.q4_0_to_superblock(blocks, n, kk)
+        return qs, dd, ref.dequant_q4_0_f16(blocks, n, kk)
+
+    with ThreadPoolExecutor(8) as pool:
+        ws = list(pool.map(lambda e: weights(D, F, 900 + e), range(E)))
+    pick = [rng.choice(E, k, replace=False) for _ in range(T)]
+    cnt = np.zeros(E, np.int32)
+    lst = np.zeros((E, T), np.int32)
+    for t in range(T):
+        for slot, e in enumerate(pick[t]):
+            lst[e, cnt[e]] = t * k + slot
+            cnt[e] += 1
+    y = host(K.moe_down(fmt, dev(np.concatenate([w[0] for w in ws])), dev(np.concatenate([w[1] for w in ws])),
+                        dev(act), T, k, E, F, D, dev(cnt), dev(lst)))
+    for t in range(T):
+        for slot, e in enumerate(pick[t]):
+            r = t * k + slot
+            check_f16(y[r], ref.linear(act[r:r + 1], ws[e][2], exact=True)[0], what=f"moe down token {t} expert {e}")
+    x = rng.standard_normal((20, F)).astype(np.float16)
+    got = host(K.linear(fmt, dev(ws[0][0]), dev(ws[0][1]), dev(x)))
+    check_f16(got, ref.linear(x, ws[0][2]), what=f"dense linear 20x{F} -> {D}")

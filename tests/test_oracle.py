@@ -332,6 +332,57 @@ def test_decoder_gqa_mapping_is_not_interleaved():
     assert np.abs(bad[0] - want).max() > 1e-3
 
 
+def test_decode_rows_matches_sequential_decode_layer_and_hf():
+    # teacher-forced rows through one layer at a time == the token-by-token decode, and a prefill
+    # from position 0 reproduces HF's logits at every prompt position
+    m = _hf_tiny_llama(seed=2)
+    W, cfg = _oracle_weights(m)
+    prompt = [5, 9, 2, 33, 17, 60, 1]
+    n, M, dh = len(prompt), 12, cfg["dh"]
+    cos, sin = ref.rope_tables(M, dh)
+    with torch.no_grad():
+        want = m(torch.tensor(prompt)[None]).logits[0].numpy()
+    for exact in (True, False):
+        seq = [(np.zeros((2, M, dh)), np.zeros((2, M, dh))) for _ in W["layers"]]
+        rows = [(np.zeros((2, M, dh)), np.zeros((2, M, dh))) for _ in W["layers"]]
+        H = ref.r16(np.asarray(W["embed"])[prompt], exact)
+        for li, lw in enumerate(W["layers"]):
+            H = ref.decode_rows(H, lw, cfg, *rows[li], 0, cos, sin, exact)
+        for p, tok in enumerate(prompt):
+            h = ref.r16(np.asarray(W["embed"])[tok].reshape(1, -1), exact)
+            for li, lw in enumerate(W["layers"]):
+                h = ref.decode_layer(h, lw, cfg, *seq[li], p, cos[p], sin[p], exact)
+            tol = 1e-12 if exact else float(np.spacing(np.float16(np.abs(h).max())))
+            assert np.abs(H[p] - h[0]).max() <= tol, (exact, p)
+        for li in range(len(W["layers"])):
+            for a, b in zip(rows[li], seq[li]):
+                assert np.abs(a - b).max() <= (1e-12 if exact else 2e-3)
+        if exact:
+            lg = ref.logits(H, W["final_norm"], W["lm_head"], cfg["norm_eps"], exact=True)
+            assert np.abs(lg - want).max() <= 1e-5 * np.abs(want).max()
+
+
+def test_decode_rows_moe_layer_matches_sequential():
+    rng = np.random.default_rng(12)
+    D, H, KV, dh, F, E = 32, 4, 2, 8, 16, 6
+    cfg = {"n_heads": H, "n_kv_heads": KV, "dh": dh, "norm_eps": 1e-5, "top_k": 2}
+    R = lambda *s: rng.standard_normal(s) * 0.3
+    lw = {"wq": R(H * dh, D), "wk": R(KV * dh, D), "wv": R(KV * dh, D), "wo": R(D, H * dh),
+          "attn_norm": np.ones(D), "mlp_norm": rng.uniform(0.8, 1.2, D), "router": R(E, D),
+          "wgate_exps": R(E, F, D), "wup_exps": R(E, F, D), "wdown_exps": R(E, D, F)}
+    M, pos0, n = 10, 3, 5
+    cos, sin = ref.rope_tables(M, dh)
+    K0, V0 = rng.standard_normal((KV, M, dh)), rng.standard_normal((KV, M, dh))
+    X = ref.r16(rng.standard_normal((n, D)))
+    Kr, Vr = K0.copy(), V0.copy()
+    got = ref.decode_rows(X, lw, cfg, Kr, Vr, pos0, cos, sin)
+    Ks, Vs = K0.copy(), V0.copy()
+    for t in range(n):
+        want = ref.decode_layer(X[t:t + 1], lw, cfg, Ks, Vs, pos0 + t, cos[pos0 + t], sin[pos0 + t])
+        assert np.abs(got[t] - want[0]).max() <= float(np.spacing(np.float16(np.abs(want).max()))), t
+    assert np.array_equal(Kr[:, :pos0], K0[:, :pos0]) and np.abs(Kr - Ks).max() <= 2e-3
+
+
 def test_q4_0_f16_dequant_matches_reference_rounding():
     # GGUFView.get converts the fp32 ggml dequantisation to float16 (aneforge/_gguf.py:34-39):
     # d = fp16(0.1) = 0.0999755859375, code 15 -> 7 * d = 0.6998291015625 (exact in fp32); the fp16

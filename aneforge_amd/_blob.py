@@ -28,15 +28,6 @@ def quantize_per_row(W: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return np.clip(codes, -127, 127).astype(np.int8), scale.astype(F16)
 
 
-def quantize_per_tensor_rows(W: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """The reference's bmm_weight quirk (aneforge/_compile.py:117 reshapes [B, K, N] to
-    [B, K*N] before quantize_per_row): ONE scale per leading index.  W [B, ...] -> (codes
-    with W's shape, fp16 scale [B])."""
-    B = W.shape[0]
-    q, s = quantize_per_row(np.asarray(W).reshape(B, -1))
-    return q.reshape(W.shape), s
-
-
 def quantize_blockwise(W: np.ndarray, block_size: int = 32) -> tuple[np.ndarray, np.ndarray, int]:
     """[OUT, IN] -> (int8 [OUT, IN], fp16 scale [OUT, IN/bs], bs); bs clamps down to a divisor of IN."""
     W32 = np.asarray(W, dtype=np.float32)

@@ -16,8 +16,9 @@ stream their int8 codes and block scales (the kernels form fp16(q * s)); accepte
 K % 32 == 0 stream their 4-bit indices and codebook (the kernels look up the entry); other shapes
 stream their exact fp16 reconstruction;
 "sparse" is lossless and streams fp16; "auto" takes int8; "q4_0" (this build's addition) uses
-the GGUF Q4_0 GEMV.  bmm_weight int8 keeps the reference's one-scale-per-batch quirk
-(aneforge/_compile.py:117)."""
+the GGUF Q4_0 GEMV.  bmm_weight encodes W [B, K, N] as the reference does, on W.reshape(B, K*N)
+(aneforge/_compile.py:117): int8 gets one scale per batch, int4 one codebook for the tensor, and
+blockwise blocks run along the flattened K*N."""
 from __future__ import annotations
 
 import warnings
@@ -355,19 +356,49 @@ class _Lowering:
         Kd = t.srcs[0].shape[-1]
         self._gemv_rows(lin, x.reshape(-1, Kd), y.reshape(-1, lin.N), bias)
 
+    def _bmm_weight_rows(self, W):
+        """The weight of x[B, M, K] @ W[B, K, N] as device rows [B*N, K] (batch b's output column n is
+        row b*N + n), encoded as the reference's em.weight encodes a bmm weight: on W.reshape(B, K*N)
+        (aneforge/_compile.py:112-188, :393-399), so every encoding sees each batch as one row.
+          int4      16-entry codebook over the whole tensor, if within compress_atol; else int8
+          blockwise int8 + scale per block of block_size consecutive elements of K*N, if within
+                    compress_atol; else fp16
+          int8, auto, and the int4 fallback: one scale per batch
+        The codes are re-laid along K for the kernels; the weights they give are the reference's."""
+        B, Kd, N = W.shape
+        flat = W.reshape(B, Kd * N)
+        to_rows = lambda a: np.ascontiguousarray(a.reshape(B, Kd, N).transpose(0, 2, 1)).reshape(B * N, Kd)
+        mode = self.compress
+        if mode == "int4" and (Kd * N) % 2 == 0:
+            packed, cb = _blob.palettize_lut4(flat)
+            idx = np.empty((B, Kd * N), np.uint8)
+            idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
+            if _rel_err(cb.astype(np.float32)[idx], flat) <= self.atol:
+                rows = to_rows(idx)                                  # [B*N, K] indices along K
+                if Kd % 32 == 0:
+                    return E.pack_encoded("lut4", rows[:, 0::2] | (rows[:, 1::2] << 4),
+                                          np.tile(np.asarray(cb, F16).reshape(1, 16), (B * N, 1)))
+                return E.pack_encoded("fp16", cb[rows], None)
+            self.stats.rejected["int4"] = self.stats.rejected.get("int4", 0) + 1
+        if mode == "blockwise":
+            q, s, bs = _blob.quantize_blockwise(flat, self.block_size)
+            rec = (q.reshape(B, -1, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(B, -1)
+            if _rel_err(rec, flat) <= self.atol:
+                return E.pack_encoded("fp16", to_rows(rec.astype(F16)), None)
+            self.stats.rejected["blockwise"] = self.stats.rejected.get("blockwise", 0) + 1
+            mode = None
+        if mode in ("int8", "auto", "int4", "q4_0"):
+            q, s = _blob.quantize_per_row(flat)                      # one scale per batch
+            return E.pack_encoded("int8", to_rows(q), np.repeat(s, N))
+        return E.pack_encoded("fp16", to_rows(flat.astype(F16)), None)
+
     def _op_bmm_w(self, t):
-        """x [B, M, K] @ W [B, K, N]; int8 uses one scale per batch (the reference's quirk)."""
+        """x [B, M, K] @ W [B, K, N], one weight-streaming linear per batch."""
         x = self.buf[id(t.srcs[0])]
         W = np.asarray(t.attrs["wt"], np.float32)
         B, Kd, N = W.shape
         self.stats.n_weights += 1
-        if self.compress in ("int8", "auto", "int4"):
-            q, s = _blob.quantize_per_tensor_rows(W)                  # [B, K, N] codes, [B] scales
-            codes = np.ascontiguousarray(q.transpose(0, 2, 1)).reshape(B * N, Kd)
-            scales = np.repeat(s, N)
-            lin = E.Linear("int8", E._to_dev(codes), E._to_dev(scales), B * N, Kd)
-        else:
-            lin = E.pack_linear(np.ascontiguousarray(W.transpose(0, 2, 1)).reshape(B * N, Kd), None)
+        lin = self._bmm_weight_rows(W)
         self.keep.append(lin)
         y = self.out(t)
         lead = t.srcs[0].shape
@@ -375,10 +406,34 @@ class _Lowering:
         xb = x.reshape(B, Mb, Kd)
         yb = y.reshape(B, Mb, N)
         for b in range(B):
-            sub = E.Linear(lin.fmt, lin.w[b * N:(b + 1) * N], None if lin.scale is None else lin.scale[b * N:(b + 1) * N],
-                           N, Kd)
+            rows = slice(b * N, (b + 1) * N)
+            sub = E.Linear(lin.fmt, lin.w[rows], None if lin.scale is None else lin.scale[rows], N, Kd)
             self.keep.append(sub)
             self._gemv_rows(sub, xb[b], yb[b])
+
+    def _op_topk_mask(self, t):
+        """The MoE router gate's top-k selection (aneforge/moe.py:21-37) as one kernel."""
+        x = self.buf[id(t.srcs[0])]
+        T, Ex = t.shape
+        y = self.out(t)
+        k = t.attrs["k"]
+        self.steps.append(lambda: K._hip.call("afx_topk_mask", K.P(x), T, Ex, k, K.P(y), K.stream()))
+
+    def _op_moe_mlp(self, t):
+        """The MoE MLP + residual as the sparse device layer (moe.MoEDecode) over the node's T rows."""
+        from .moe import MoEDecode
+        x = self.buf[id(t.srcs[0])]
+        layer = MoEDecode(t.attrs["w"], t.attrs["cfg"], t.attrs["ls"], self.compress)
+        T = t.shape[0]
+        bufs = layer._make_bufs(T)
+        y = self.out(t)
+        self.keep += [layer, bufs]
+        self.stats.n_weights += 1
+
+        def run():
+            y.copy_(x)
+            layer.run(y, bufs)
+        self.steps.append(run)
 
     def _op_bmm(self, t):
         a, b = self.buf[id(t.srcs[0])], self.buf[id(t.srcs[1])]

@@ -9,8 +9,9 @@ Here the whole step runs on the GPU:
               afx_linear        o-proj GEMV + residual add (in place on h)
               afx_linear_swiglu RMSNorm + gate/up GEMV + SwiGLU
               afx_linear        down GEMV + residual add
-  head:       afx_linear_rms    final RMSNorm + fp16 lm_head -> fp32 logits
-  advance:    afx_decode_advance next token (prompt token or greedy argmax), pos/step, embedding
+  head:       afx_lm_head       final RMSNorm + fp16 lm_head -> fp32 logits + greedy-pick slots
+  advance:    afx_decode_advance next token (prompt token, or the greedy pick with the reference's
+                                 lm_head near-tie rule), pos/step, embedding
 
 Position, step counter, prompt tokens and the generated-token history live in device memory,
 so one step is captured once as a HIP graph and replayed for every token with no host sync.
@@ -443,7 +444,7 @@ class DecodeEngine:
     """All layers + head + advance for one sequence (B=1) with a resident cache of M rows."""
 
     def __init__(self, cfg, layers, embed: torch.Tensor, head: Linear, final_norm: torch.Tensor, M: int,
-                 rope_tables=None):
+                 rope_tables=None, head32: torch.Tensor | None = None, tie_margin: float | None = 3e-3):
         self.cfg, self.layers, self.embed, self.head, self.final_norm = cfg, layers, embed, head, final_norm
         self.M, self.B = int(M), 1
         D, H, dh = cfg.dim, cfg.n_heads, cfg.dh
@@ -455,6 +456,17 @@ class DecodeEngine:
         fmax = max([getattr(m, "F", 0) for _, m in layers] + [8])
         self.act = torch.zeros((1, fmax), dtype=torch.float16, device=dev)
         self.logits = torch.zeros((1, self.V), dtype=torch.float32, device=dev)
+        # lm_head greedy-pick slots, its normalised input row, and the near-tie rule's margin (a device
+        # scalar, so a changed margin applies to already captured graphs); head32 holds the head in
+        # fp32 when the checkpoint's values are not fp16-exact (the reference recomputes with them)
+        self.slots = torch.zeros(((self.V + 7) // 8, 4), dtype=torch.float32, device=dev)
+        self.hn = torch.zeros(D, dtype=torch.float16, device=dev)
+        self.tie_margin = torch.zeros(1, dtype=torch.float32, device=dev)
+        self.head32 = head32
+        self.margin = tie_margin
+        self._tie_on = tie_margin is not None and head.fmt == "fp16" and head.bias is None
+        if self._tie_on:
+            self.tie_margin.fill_(float(tie_margin))
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.tok = torch.zeros(1, dtype=torch.int32, device=dev)
         self.step = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -484,12 +496,31 @@ class DecodeEngine:
             mlp.enqueue(self)
 
     def enqueue_head(self):
-        K.linear_rms(self.head.fmt, self.head.w, self.head.scale, self.h, self.final_norm, self.cfg.norm_eps,
-                     y=self.logits, out_f32=True)
+        if self.head.fmt == "fp16" and self.head.bias is None:
+            K.lm_head(self.head.w, self.h, self.final_norm, self.cfg.norm_eps, logits=self.logits, slots=self.slots,
+                      hn=self.hn)
+        else:
+            K.linear_rms(self.head.fmt, self.head.w, self.head.scale, self.h, self.final_norm, self.cfg.norm_eps,
+                         y=self.logits, bias=self.head.bias, out_f32=True)
+
+    def set_tie_margin(self, margin: float | None):
+        """The greedy near-tie margin (relative to max |logit|); None turns the recompute off."""
+        was_on, self.margin = self._tie_on, margin
+        self._tie_on = margin is not None and self.head.fmt == "fp16" and self.head.bias is None
+        if self._tie_on:
+            with torch.cuda.stream(self.stream):
+                self.tie_margin.fill_(float(margin))
+        if was_on != self._tie_on:                    # the captured steps change shape: capture again
+            self.close()
 
     def enqueue_advance(self, with_logits: bool):
+        fused = with_logits and self.head.fmt == "fp16" and self.head.bias is None
+        tie = fused and self._tie_on
         K.decode_advance(self.logits if with_logits else None, self.tok, self.pos, self.hist, self.step,
-                         self.embed, self.h, self.forced, self.n_forced)
+                         self.embed, self.h, self.forced, self.n_forced, slots=self.slots if fused else None,
+                         tie_margin=self.tie_margin if tie else None, hn=self.hn if tie else None,
+                         head16=self.head.w if tie and self.head32 is None else None,
+                         head32=self.head32 if tie else None)
 
     def enqueue_sample(self):
         """The step's token from the logits by the device sampler, queued as forced[step]."""

@@ -37,6 +37,7 @@ SIGNATURES: dict[str, tuple] = {
     # weight-streaming linear layers
     "afx_linear": (_i, [_i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
     "afx_linear_rms": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
+    "afx_lm_head": (_i, [_i, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _vp, _vp, _vp]),
     "afx_linear_swiglu": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "afx_qkv_rope_kv": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp,
                              _vp, _i, _vp, _vp, _ll, _ll, _i, _i, _i, _i, _vp]),
@@ -59,7 +60,8 @@ SIGNATURES: dict[str, tuple] = {
     "afx_rope": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _vp]),
     "afx_head_norm_rope": (_i, [_vp, _ll, _ll, _i, _vp, _i, _i, _i, _i, _vp, _f, _vp, _vp, _i, _vp]),
     "afx_embed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
-    "afx_decode_advance": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp]),
+    "afx_decode_advance": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp,
+                                _i, _i, _vp]),
     "afx_argmax": (_i, [_vp, _i, _i, _vp, _vp]),
     "afx_fill_i32": (_i, [_vp, _i, _i, _vp]),
     "afx_fill_f16": (_i, [_vp, _ll, _f, _vp]),
@@ -74,6 +76,7 @@ SIGNATURES: dict[str, tuple] = {
     "afx_moe_topk": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "afx_moe_gateup": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
     "afx_moe_down": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
+    "afx_topk_mask": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     # batched prefill
     "afx_gemm": (_i, [_i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
     "afx_qkv_split_rope": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i, _vp, _vp, _ll, _i, _vp]),

@@ -237,12 +237,31 @@ def sample(logits, params, uniforms, step=None, forced=None, n_forced=None, out=
     return out
 
 
-def decode_advance(logits, tok, pos, hist, step, embed_table=None, h=None, forced=None, n_forced=None):
-    """Next token (forced prompt token or greedy argmax) + bookkeeping + embedding gather."""
+def decode_advance(logits, tok, pos, hist, step, embed_table=None, h=None, forced=None, n_forced=None,
+                   slots=None, tie_margin=None, hn=None, head16=None, head32=None):
+    """Next token (forced prompt token, or the greedy pick with the lm_head tie rule when tie_margin
+    is given) + bookkeeping + embedding gather (see afx_decode_advance)."""
     V = logits.shape[-1] if logits is not None else 0
     vocab, D = (embed_table.shape if embed_table is not None else (V, 0))
-    _hip.call("afx_decode_advance", P(logits), V, P(forced), P(n_forced), P(tok), P(pos), P(hist),
-              hist.numel() if hist is not None else 0, P(step), P(embed_table), P(h), D, vocab, stream())
+    if tie_margin is not None:
+        D = hn.numel()
+    _hip.call("afx_decode_advance", P(logits), P(slots), V, P(tie_margin), P(hn), P(head16), P(head32),
+              P(forced), P(n_forced), P(tok), P(pos), P(hist), hist.numel() if hist is not None else 0, P(step),
+              P(embed_table), P(h), D, vocab, stream())
+
+
+def lm_head(w, x, gamma, eps, logits=None, slots=None, hn=None):
+    """fp32 logits [1, N] = rms_norm(x [1, K]) @ W^T for an fp16 head, plus the greedy-pick slots
+    (float32 [ceil(N/8), 4]) and, if hn is given, the fp16 normalised row (see afx_lm_head)."""
+    _dev(w, x, gamma, logits, slots, hn)
+    N, Kd = w.shape
+    if logits is None:
+        logits = torch.empty((1, N), dtype=torch.float32, device=x.device)
+    if slots is None:
+        slots = torch.empty(((N + 7) // 8, 4), dtype=torch.float32, device=x.device)
+    _hip.call("afx_lm_head", FMT["fp16"], P(w), None, P(x), P(gamma), float(eps), P(logits), N, Kd, P(slots),
+              P(hn), stream())
+    return logits, slots
 
 
 def argmax(x, out=None):

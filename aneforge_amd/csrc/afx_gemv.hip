@@ -157,6 +157,19 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
   return check_launch(what);
 }
 
+// Greedy-pick summaries of logits rows [8s, 8s + 8) for slot s (the lm_head's generic path; the
+// fused head kernel writes the same slots from its workgroups of 8 rows).
+__global__ __launch_bounds__(256) void head_slots_kernel(const float* __restrict__ y, int N, float4* __restrict__ slots) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s * 8 >= N) return;
+  float4 acc = float4{-INFINITY, __int_as_float(0x7fffffff), -INFINITY, 0.0f};
+  for (int r = s * 8; r < s * 8 + 8 && r < N; ++r) {
+    const float v = y[r];
+    acc = top2_merge(acc, float4{v, __int_as_float(r), -INFINITY, fabsf(v)});
+  }
+  slots[s] = acc;
+}
+
 static GemvArgs base_args(const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                           int M, int N, int K, const void* bias, int epi) {
   GemvArgs a = {};
@@ -197,6 +210,36 @@ int afx_linear_rms(int fmt, const void* w, const void* scale, const void* x, int
   GemvArgs a = base_args(w, scale, x, ldx, y, ldy, M, N, K, bias, out_f32 ? EPI_F32 : EPI_F16);
   a.gamma = (const half_t*)gamma; a.eps = eps;
   return launch(fmt, a, EG_PLAIN, rows_hint, (hipStream_t)stream, "afx_linear_rms");
+}
+
+// The lm_head (aneforge/llm.py:338-404) for one hidden row: logits[N] (fp32) = rms_norm(x, gamma, eps)
+// @ W^T, plus slots[ceil(N/8)] greedy-pick summaries of the logits (rows 8s .. 8s + 7 each) and,
+// when hn_out is given, the fp16 normalised row the products used.
+int afx_lm_head(int fmt, const void* w, const void* scale, const void* x, const void* gamma, float eps,
+                float* logits, int N, int K, float* slots, void* hn_out, void* stream) {
+  AFX_REQUIRE(fmt == FMT_F16, "afx_lm_head: the head streams fp16 weights (fmt 2), got fmt %d", fmt);
+  AFX_REQUIRE(gamma && slots && logits, "afx_lm_head: needs gamma, logits and slots");
+  AFX_REQUIRE(((uintptr_t)slots & 15) == 0 && (!hn_out || ((uintptr_t)hn_out & 15) == 0),
+              "afx_lm_head: slots and hn_out must be 16-byte aligned");
+  GemvArgs a = base_args(w, scale, x, K, logits, N, 1, N, K, nullptr, EPI_F32);
+  a.gamma = (const half_t*)gamma; a.eps = eps;
+  a.slots = slots; a.hn_out = (half_t*)hn_out;
+  const int fu = K % 8 == 0 ? fast_units(fmt, K / 8) : 0;
+  if (fu) {
+    // the fused kernel: 4 wavefronts of 2 rows per workgroup, one slot per workgroup
+    AFX_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)gamma & 15) == 0,
+                "afx_lm_head: x, gamma and weights must be 16-byte aligned");
+    gemv_fn fr = pick_gemv_row_f16(EG_HEAD, 2, 1, fu);
+    AFX_REQUIRE(fr, "afx_lm_head: no fused kernel for K=%d", K);
+    hipLaunchKernelGGL(fr, dim3(grid_for((N + 1) / 2)), dim3(256), 0, (hipStream_t)stream, a);
+    return check_launch("afx_lm_head");
+  }
+  const int rc = launch(fmt, a, EG_PLAIN, 0, (hipStream_t)stream, "afx_lm_head");
+  if (rc) return rc;
+  const int ns = (N + 7) / 8;
+  hipLaunchKernelGGL(head_slots_kernel, dim3((ns + 255) / 256), dim3(256), 0, (hipStream_t)stream, logits, N,
+                     (float4*)slots);
+  return check_launch("afx_lm_head(slots)");
 }
 
 // SwiGLU MLP front half: act[m][i] = silu(g_i) * u_i with (g, u) = rms_norm(x) @ Wgu^T, where

@@ -45,13 +45,16 @@
 //   EG_QKV     fused q|k|v rows; q and k rows are interleaved per head as (d, d+dh/2) pairs so
 //              RoPE (llm.py:96-105) is applied to the pair; k and v are written straight into
 //              the resident cache at row pos (replaces the masked O(M) rewrite, llm.py:233).
+//   EG_HEAD    the lm_head (llm.py:338-404): fp32 logits, and per workgroup one slot with its
+//              rows' largest logit, that logit's row (the lowest on ties), the second largest
+//              and the largest magnitude, so the greedy pick and its tie margin need no rescan.
 #pragma once
 #include "afx_gemv_core.h"
 
 namespace afx {
 
 enum { EPI_F16 = 0, EPI_RESID = 1, EPI_F32 = 2, EPI_SWIGLU = 3, EPI_QKV = 4 };
-enum { EG_PLAIN = 0, EG_SWIGLU = 1, EG_QKV = 2 };
+enum { EG_PLAIN = 0, EG_SWIGLU = 1, EG_QKV = 2, EG_HEAD = 3 };
 
 struct GemvArgs {
   const void* w;          // weights (format above)
@@ -75,6 +78,8 @@ struct GemvArgs {
   float eps;
   int nq, nk;             // EG_QKV: number of q rows (H*dh) and k rows (KVH*dh); v rows follow
   int dh, rope;           // EG_QKV: head dim; rope on/off
+  float* slots;           // EG_HEAD: per workgroup {top-1, its row (int bits), top-2, max |y|}
+  half_t* hn_out;         // norm prologue: workgroup 0 also writes the fp16 normalised row here
 };
 
 constexpr int kStageUnroll = 4;     // 16-byte staging loads per thread in flight per batch
@@ -347,6 +352,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
           xq[jj] = as_u32(r);
         }
         *(u4*)(xs + (size_t)f * 8) = xv;
+        if (a.hn_out && blockIdx.x == 0 && f < nv) *(u4*)(a.hn_out + 8 * f) = xv;
       }
     }
     __syncthreads();
@@ -417,6 +423,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   constexpr int KMAX = 64 * U * Fmt<FMT>::kWeightsPerChunk;
   constexpr int NVT = (KMAX / 8 + 255) / 256;          // norm vectors per thread
   static_assert(EG == EG_PLAIN || R == 2, "paired epilogues process row pairs");
+  static_assert(EG != EG_HEAD || NORM == 1, "the lm_head variant has the norm prologue");
   __shared__ __align__(16) half_t xs[NORM ? KMAX : 8];
   __shared__ float red[4];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -499,6 +506,13 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
         xw[jj] = as_u32(r);
       }
     }
+    if constexpr (EG == EG_HEAD) {
+      if (a.hn_out && blockIdx.x == 0) {
+#pragma unroll
+        for (int i = 0; i < NVT; ++i)
+          if (t + 256 * i < nv) *(u4*)(a.hn_out + 8 * (t + 256 * i)) = xq[i];
+      }
+    }
   }
   if constexpr (NORM) {
 #pragma unroll
@@ -518,7 +532,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   typename Fmt<FMT>::Ctx fctx[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) fctx[r] = Fmt<FMT>::Ctx::make(a.scale, row0 + r < N ? row0 + r : N - 1);
-  if (!live) return;   // no barrier follows
+  if (EG != EG_HEAD && !live) return;   // no barrier follows (the head variant meets one below)
 
   float acc[R];
 #pragma unroll
@@ -552,7 +566,31 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
 #pragma unroll
   for (int r = 0; r < R; ++r)
     v[0][r] = wave_sum_uniform(acc[r]) * (float)h_scale[r] + (a.bias ? (float)h_bias[r] : 0.0f);
-  if (lane == 0) gemv_store<1, R, EG>(a, v, row0, e_pos, h_res, h_cs, h_sn);
+  if constexpr (EG == EG_HEAD) {
+    __shared__ float4 part[4];
+    float t1 = -INFINITY, t2 = -INFINITY, ma = 0.0f;
+    int i1 = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {           // rows ascend, so an equal value keeps the lower row
+      const int row = row0 + r;
+      if (!live || row >= N) continue;
+      const float y = v[0][r];
+      ma = fmaxf(ma, fabsf(y));
+      if (y > t1) { t2 = t1; t1 = y; i1 = row; }
+      else t2 = fmaxf(t2, y);
+      if (lane == 0) ((float*)a.y)[row] = y;
+    }
+    if (lane == 0) part[wave] = float4{t1, __int_as_float(i1), t2, ma};
+    __syncthreads();
+    if (t == 0) {
+      float4 s = part[0];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) s = top2_merge(s, part[w]);
+      ((float4*)a.slots)[blockIdx.x] = s;
+    }
+  } else {
+    if (lane == 0) gemv_store<1, R, EG>(a, v, row0, e_pos, h_res, h_cs, h_sn);
+  }
 }
 
 typedef void (*gemv_fn)(GemvArgs);
@@ -580,6 +618,10 @@ gemv_fn pick_gemv(int mt, int eg, int R, int xs) {
 
 template <int FMT, int U>
 gemv_fn pick_gemv_row_u(int eg, int R, int norm) {
+  if constexpr (FMT == FMT_F16) {
+    if (eg == EG_HEAD) return norm == 1 ? gemv_row_kernel<FMT, 2, 1, EG_HEAD, U> : nullptr;
+  }
+  if (eg == EG_HEAD) return nullptr;
   if (norm == 2 && eg == EG_PLAIN)                 // x staged once per workgroup through LDS, no norm
     return R == 2 ? gemv_row_kernel<FMT, 2, 2, EG_PLAIN, U> : gemv_row_kernel<FMT, 1, 2, EG_PLAIN, U>;
   if (norm == 2) norm = 0;

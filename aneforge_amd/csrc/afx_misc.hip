@@ -154,80 +154,149 @@ __global__ void embed_kernel(const half_t* __restrict__ table, const int* __rest
 
 // ---- one step of the device-resident decode loop ----
 // The next token is forced[*step] while *step < *n_forced (prompt tokens, token-by-token
-// prefill), else argmax(logits) (lowest index on ties, like np.argmax; greedy _sample).  Then
+// prefill), else the greedy pick (lowest index on ties, like np.argmax; greedy _sample).  Then
 // hist[*step] = token, ++*step, ++*pos, h = embed[token].  One workgroup; every input that
 // changes between steps lives in device memory, so the step replays as a captured graph.
-__global__ __launch_bounds__(1024) void decode_advance_kernel(
-    const float* __restrict__ logits, int V, const int* __restrict__ forced, const int* __restrict__ n_forced,
-    int* __restrict__ tok, int* __restrict__ pos, int* __restrict__ hist, int hist_cap, int* __restrict__ step,
-    const half_t* __restrict__ embed, half_t* __restrict__ h, int D, int vocab) {
-  __shared__ float bv[16];
-  __shared__ int bi[16];
-  __shared__ int chosen;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int s = step[0];
-  const bool use_forced = forced && n_forced && s < n_forced[0];
-  if (!use_forced && logits) {
-    float best = -INFINITY;
-    int besti = 0x7fffffff;
-    // batches of 8 float4 per thread, all loads issued before the compares
-    const int nv4 = V >> 2;
-    const bool al = (((uintptr_t)logits) & 15) == 0;
-    for (int b0 = 0; al && b0 < nv4; b0 += 8 * (int)blockDim.x) {
-      float4 v[8];
+//
+// The greedy pick comes from the lm_head's slot summaries when given (else from the logits), with
+// the reference's near-tie rule (aneforge/llm.py:395-404): when the two largest logits are closer
+// than margin * max |logit|, every logit inside that window of the largest is recomputed exactly
+// (fp64 sum of the staged fp16 hidden row times the head row, fp32 head rows when the checkpoint's
+// head is not fp16-exact) and the largest exact value wins, the lowest index on an exact tie.
+struct AdvanceArgs {
+  const float* logits;
+  const float4* slots;     // optional: ceil(V / 8) summaries from afx_lm_head
+  int V;
+  const float* margin;     // optional (device): the tie margin; null = plain argmax
+  const half_t* hn;        // the head's normalised input row [D]
+  const half_t* head16;    // head rows [V][D], fp16 ...
+  const float* head32;     // ... or fp32 (preferred when given)
+  const int* forced;
+  const int* n_forced;
+  int* tok;
+  int* pos;
+  int* hist;
+  int hist_cap;
+  int* step;
+  const half_t* embed;
+  half_t* h;
+  int D, vocab;
+};
+
+__device__ __forceinline__ float4 shfl_xor_f4(float4 v, int m) {
+  return float4{__shfl_xor(v.x, m, 64), __shfl_xor(v.y, m, 64), __shfl_xor(v.z, m, 64), __shfl_xor(v.w, m, 64)};
+}
+
+__global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
+  __shared__ float4 wpart[16];
+  __shared__ double xbest[16];
+  __shared__ int xidx[16];
+  __shared__ int chosen, near_tie;
+  __shared__ float4 top_all;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
+  const float4 none = float4{-INFINITY, __int_as_float(0x7fffffff), -INFINITY, 0.0f};
+  // 1. the greedy summaries, loaded before the step counter is known (they do not depend on it)
+  float4 acc = none;
+  if (a.slots) {
+    const int ns = (a.V + 7) >> 3;
+    for (int b0 = 0; b0 < ns; b0 += 4 * (int)blockDim.x) {
+      float4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = b0 + j * (int)blockDim.x + t;
+        v[j] = i < ns ? a.slots[i] : none;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = top2_merge(acc, v[j]);
+    }
+  } else if (a.logits) {
+    for (int b0 = 0; b0 < a.V; b0 += 8 * (int)blockDim.x) {
+      float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int i4 = b0 + j * (int)blockDim.x + t;
-        v[j] = i4 < nv4 ? ((const float4*)logits)[i4] : float4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        const int i = b0 + j * (int)blockDim.x + t;
+        v[j] = i < a.V ? a.logits[i] : -INFINITY;
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int base = 4 * (b0 + j * (int)blockDim.x + t);
-        const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (e[k] > best || (e[k] == best && base + k < besti)) { best = e[k]; besti = base + k; }
+        const int i = b0 + j * (int)blockDim.x + t;
+        if (i < a.V) acc = top2_merge(acc, float4{v[j], __int_as_float(i), -INFINITY, fabsf(v[j])});
       }
     }
-    for (int i = (al ? 4 * nv4 : 0) + t; i < V; i += blockDim.x) {
-      const float v = logits[i];
-      if (v > best || (v == best && i < besti)) { best = v; besti = i; }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(best, m, 64);
-      const int oi = __shfl_xor(besti, m, 64);
-      if (ov > best || (ov == best && oi < besti)) { best = ov; besti = oi; }
-    }
-    if (lane == 0) { bv[wave] = best; bi[wave] = besti; }
   }
+  const int s = a.step[0];
+  const bool use_forced = a.forced && a.n_forced && s < a.n_forced[0];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc = top2_merge(acc, shfl_xor_f4(acc, m));
+  if (lane == 0) wpart[wave] = acc;
   __syncthreads();
   if (t == 0) {
-    int bidx;
-    if (use_forced) {
-      bidx = forced[s];
-    } else if (!logits) {
-      bidx = 0;                  // a forced-only step run past its prompt: inert token
-    } else {
-      const int nw = blockDim.x >> 6;
-      float b = bv[0];
-      bidx = bi[0];
-      for (int w = 1; w < nw; ++w)
-        if (bv[w] > b || (bv[w] == b && bi[w] < bidx)) { b = bv[w]; bidx = bi[w]; }
-      if (bidx >= V) bidx = 0;   // all-NaN logits: deterministic fallback
+    float4 top = wpart[0];
+    for (int w = 1; w < nw; ++w) top = top2_merge(top, wpart[w]);
+    top_all = top;
+    int nt = 0;
+    if (!use_forced && (a.logits || a.slots) && a.margin && a.logits && a.hn && (a.head16 || a.head32) &&
+        __builtin_isfinite(top.x) && __builtin_isfinite(top.w)) {
+      const double gap = (double)top.x - (double)top.z;
+      nt = gap < (double)a.margin[0] * ((double)top.w + 1e-9);
     }
-    bidx = bidx < 0 ? 0 : (bidx >= vocab ? vocab - 1 : bidx);
-    chosen = bidx;
-    tok[0] = bidx;
-    if (s < hist_cap) hist[s] = bidx;
-    step[0] = s + 1;
-    pos[0] = pos[0] + 1;
+    near_tie = nt;
   }
   __syncthreads();
-  if (embed) {
-    const u4* src = (const u4*)(embed + (size_t)chosen * D);
-    u4* dst = (u4*)h;
-    for (int i = t; i < D / 8; i += blockDim.x) dst[i] = src[i];
+  int pick = __float_as_int(top_all.y);
+  if (near_tie) {
+    // every logit within the window of the largest, recomputed exactly; one wavefront per candidate
+    const float4 top = top_all;
+    const double lo = (double)top.x - (double)a.margin[0] * ((double)top.w + 1e-9);
+    double best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int base = wave * 64; base < a.V; base += nw * 64) {
+      const int i = base + lane;
+      const float lv = i < a.V ? a.logits[i] : -INFINITY;
+      unsigned long long m = __ballot((double)lv >= lo);
+      while (m) {
+        const int c = base + __ffsll((long long)m) - 1;
+        m &= m - 1;
+        double d = 0.0;
+        if (a.head32) {
+          const float* wr = a.head32 + (size_t)c * a.D;
+          for (int k = lane; k < a.D; k += 64) d += (double)(float)a.hn[k] * (double)wr[k];
+        } else {
+          const half_t* wr = a.head16 + (size_t)c * a.D;
+          for (int k = lane; k < a.D; k += 64) d += (double)(float)a.hn[k] * (double)(float)wr[k];
+        }
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) d += __shfl_xor(d, sh, 64);
+        if (d > best || (d == best && c < bi)) { best = d; bi = c; }
+      }
+    }
+    if (lane == 0) { xbest[wave] = best; xidx[wave] = bi; }
+    __syncthreads();
+    if (t == 0) {
+      double b = xbest[0];
+      int bx = xidx[0];
+      for (int w = 1; w < nw; ++w)
+        if (xbest[w] > b || (xbest[w] == b && xidx[w] < bx)) { b = xbest[w]; bx = xidx[w]; }
+      if (bx != 0x7fffffff) pick = bx;
+    }
+  }
+  if (t == 0) {
+    int bidx;
+    if (use_forced) bidx = a.forced[s];
+    else if (!a.logits && !a.slots) bidx = 0;   // a forced-only step run past its prompt: inert token
+    else bidx = pick >= a.V || pick < 0 ? 0 : pick;   // all-NaN logits: deterministic fallback
+    bidx = bidx < 0 ? 0 : (bidx >= a.vocab ? a.vocab - 1 : bidx);
+    chosen = bidx;
+    a.tok[0] = bidx;
+    if (s < a.hist_cap) a.hist[s] = bidx;
+    a.step[0] = s + 1;
+    a.pos[0] = a.pos[0] + 1;
+  }
+  __syncthreads();
+  if (a.embed) {
+    const u4* src = (const u4*)(a.embed + (size_t)chosen * a.D);
+    u4* dst = (u4*)a.h;
+    for (int i = t; i < a.D / 8; i += blockDim.x) dst[i] = src[i];
   }
 }
 
@@ -745,16 +814,23 @@ int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vo
   return check_launch("afx_embed");
 }
 
-int afx_decode_advance(const float* logits, int V, const int* forced, const int* n_forced, int* tok, int* pos,
-                       int* hist, int hist_cap, int* step, const void* embed, void* h, int D, int vocab,
+int afx_decode_advance(const float* logits, const float* slots, int V, const float* tie_margin, const void* hn,
+                       const void* head16, const float* head32, const int* forced, const int* n_forced, int* tok,
+                       int* pos, int* hist, int hist_cap, int* step, const void* embed, void* h, int D, int vocab,
                        void* stream) {
-  AFX_REQUIRE(tok && pos && step && (logits || forced), "afx_decode_advance: bad arguments");
-  AFX_REQUIRE(!logits || V >= 1, "afx_decode_advance: V must be positive");
+  AFX_REQUIRE(tok && pos && step && (logits || slots || forced), "afx_decode_advance: bad arguments");
+  AFX_REQUIRE(!(logits || slots) || V >= 1, "afx_decode_advance: V must be positive");
   AFX_REQUIRE(!embed || (h && D % 8 == 0 && vocab >= 1), "afx_decode_advance: embed gather needs h, D % 8 == 0");
-  AFX_REQUIRE(logits || n_forced, "afx_decode_advance: a forced-only step needs n_forced");
-  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, V, forced,
-                     n_forced, tok, pos, hist, hist_cap, step, (const half_t*)embed, (half_t*)h, D,
-                     vocab > 0 ? vocab : V);
+  AFX_REQUIRE(logits || slots || n_forced, "afx_decode_advance: a forced-only step needs n_forced");
+  AFX_REQUIRE(!slots || ((uintptr_t)slots & 15) == 0, "afx_decode_advance: slots must be 16-byte aligned");
+  AFX_REQUIRE(!tie_margin || (logits && hn && (head16 || head32) && D >= 1),
+              "afx_decode_advance: the tie margin needs the logits, the head's input row and its weights");
+  AdvanceArgs a = {};
+  a.logits = logits; a.slots = (const float4*)slots; a.V = V; a.margin = tie_margin;
+  a.hn = (const half_t*)hn; a.head16 = (const half_t*)head16; a.head32 = head32;
+  a.forced = forced; a.n_forced = n_forced; a.tok = tok; a.pos = pos; a.hist = hist; a.hist_cap = hist_cap;
+  a.step = step; a.embed = (const half_t*)embed; a.h = (half_t*)h; a.D = D; a.vocab = vocab > 0 ? vocab : V;
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_advance");
 }
 

@@ -240,7 +240,65 @@ static long long fmt_scale_halves(int fmt, long long rows, int K) {
 
 using namespace afx;
 
+namespace afx {
+
+// The graph form of the top-k gate: y[t, e] = x[t, e] for the k experts a row picks, else 0.
+// x holds fp16 probabilities; one wavefront per row, lane l owns experts l, l + 64, ...; each of
+// the k rounds takes the row maximum and, among experts holding exactly that fp16 value, the
+// lowest index, so a row never keeps more than k experts (aneforge/moe.py:21-37).
+template <int J>
+__global__ __launch_bounds__(256) void topk_mask_kernel(const half_t* __restrict__ x, int T, int E, int k,
+                                                        half_t* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const half_t* xr = x + (size_t)row * E;
+  half_t* yr = y + (size_t)row * E;
+  float v[J];
+  bool keep[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? (float)xr[e] : -INFINITY;
+    keep[j] = false;
+  }
+  for (int r = 0; r < k; ++r) {
+    float best = -INFINITY;
+    int at = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (lane + 64 * j < E && !keep[j] && (v[j] > best || at == 0x7fffffff)) { best = v[j]; at = lane + 64 * j; }
+    const float top = wave_max(best);
+    float cand = (at != 0x7fffffff && best == top) ? (float)at : 3.0e38f;
+    const int win = (int)(-wave_max(-cand));
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (lane + 64 * j == win) keep[j] = true;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) yr[e] = keep[j] ? xr[e] : (half_t)0.0f;
+  }
+}
+
+}  // namespace afx
+
+using namespace afx;
+
 extern "C" {
+
+int afx_topk_mask(const void* x, int T, int E, int k, void* y, void* stream) {
+  AFX_REQUIRE(x && y, "afx_topk_mask: null pointer");
+  AFX_REQUIRE(k >= 1 && k <= E && E <= 2049, "afx_topk_mask: need 1 <= k <= E <= 2049; got k=%d E=%d", k, E);
+  AFX_REQUIRE(T >= 1, "afx_topk_mask: T=%d", T);
+  const int jn = (E + 63) / 64;
+  auto fn = jn <= 1 ? topk_mask_kernel<1> : jn <= 2 ? topk_mask_kernel<2> : jn <= 4 ? topk_mask_kernel<4>
+          : jn <= 8 ? topk_mask_kernel<8> : jn <= 16 ? topk_mask_kernel<16> : topk_mask_kernel<33>;
+  hipLaunchKernelGGL(fn, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, (const half_t*)x, T, E, k,
+                     (half_t*)y);
+  return check_launch("afx_topk_mask");
+}
 
 int afx_moe_topk(const float* logits, int T, int E, int k, int renorm, float* gate, int* sel, int* cnt,
                  int* list, void* stream) {

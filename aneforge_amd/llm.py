@@ -27,7 +27,9 @@ class ModelType(str, Enum):
     QWEN = "qwen"
 
 
-_DENSE_INCOMPATIBLE = {ModelType.GEMMA2, ModelType.GEMMA3, ModelType.GEMMA3_TEXT}
+# Architectures whose semantics the dense Llama path would drop (Gemma's sqrt(dim) embedding scale,
+# (1 + w) norms and GeGLU; Gemma-2/3 softcapping and sliding attention): rejected, never mis-loaded.
+_DENSE_INCOMPATIBLE = {ModelType.GEMMA, ModelType.GEMMA2, ModelType.GEMMA3, ModelType.GEMMA3_TEXT}
 
 
 @dataclass
@@ -138,6 +140,7 @@ class LlamaPrefill:
         self.lmhead_tie_margin = 3e-3
         self._lmT = None
         self._lmh = None                   # device lm_head (Linear) once packed
+        self._lmh32 = None                 # its fp32 values when the checkpoint's are not fp16-exact
         self._lmh_off = False
         self._layers = None                # packed device layers
         self._embed = None
@@ -145,17 +148,19 @@ class LlamaPrefill:
         self._dec = None                   # DecodeEngine for the current max length
 
     # -- planning kept for API compatibility (aneforge/llm.py:425-433) --
+    _ENCODED_BYTES = {"int8": 1.0, "blockwise": 1.0, "int4": 0.5, "q4_0": 0.5}   # per weight; fp16 is 2
+
     def _layer_chunks(self):
-        """Contiguous layer groups under the reference's per-program byte and layer caps.  The
-        device engine runs every layer in one graph; the plan is kept because callers use it."""
-        per = sum(int(np.asarray(v).size) for v in self.w["layers"][0].values()
-                  if isinstance(v, (np.ndarray, list, tuple))) * 2
-        if self.compress in ("int8", "blockwise"):
-            per //= 2
-        elif self.compress in ("int4", "q4_0"):
-            per //= 4
-        n = max(1, min(self.cfg.n_layers, self._chunk_max_layers, int(self._chunk_bytes // max(per, 1))))
-        return [range(i, min(i + n, self.cfg.n_layers)) for i in range(0, self.cfg.n_layers, n)]
+        """The reference's layer grouping: consecutive layers whose weights, at this compress=
+        encoding, stay under the per-program byte budget, and at most `_chunk_max_layers` a group.
+        The device engine itself runs every layer in one graph; callers that plan by chunk get the
+        same plan as on the reference."""
+        n_layers = self.cfg.n_layers
+        elems = sum(np.size(v) for v in self.w["layers"][0].values() if isinstance(v, (np.ndarray, list, tuple)))
+        layer_bytes = max(1, int(elems * self._ENCODED_BYTES.get(self.compress, 2.0)))
+        size = max(1, min(n_layers, self._chunk_max_layers, int(self._chunk_bytes // layer_bytes)))
+        bounds = list(range(0, n_layers, size)) + [n_layers]
+        return [range(lo, hi) for lo, hi in zip(bounds[:-1], bounds[1:])]
 
     def _spec(self, i: int) -> LayerSpec:
         if self.cfg.layers:
@@ -193,17 +198,26 @@ class LlamaPrefill:
         self._embed = _eng._to_dev(np.asarray(self.w["embed"], np.float32).astype(np.float16))
         self._final_norm = _eng._gamma(self.w["final_norm"], cfg.dim)
         self._lmh = _eng.pack_linear(self.w["lm_head"], None)   # the head stays fp16 (llm.py:279)
+        # the near-tie recompute uses the checkpoint's own head values (aneforge/llm.py:350-355 computes
+        # in fp32): when they are not all fp16-exact, an fp32 copy stays on the device for it
+        lm = np.asarray(self.w["lm_head"])
+        self._lmh32 = None
+        if lm.dtype != np.float16 and not np.array_equal(lm.astype(np.float16).astype(lm.dtype), lm):
+            self._lmh32 = _eng._to_dev(np.ascontiguousarray(lm, np.float32))
         return layers
 
     def _decoder(self, M: int):
         M = int(M)
         self._check_positions(M)
         if self._dec is not None and self._dec.M == M:
+            if self._dec.margin != self.lmhead_tie_margin:
+                self._dec.set_tie_margin(self.lmhead_tie_margin)
             return self._dec
         if self._dec is not None:
             self._dec.close()
         layers = self._pack()
-        self._dec = _eng.DecodeEngine(self.cfg, layers, self._embed, self._lmh, self._final_norm, M)
+        self._dec = _eng.DecodeEngine(self.cfg, layers, self._embed, self._lmh, self._final_norm, M,
+                                      head32=self._lmh32, tie_margin=self.lmhead_tie_margin)
         return self._dec
 
     def warmup(self, max_len):
@@ -218,7 +232,7 @@ class LlamaPrefill:
             self._dec.close()
         self._dec = None
         self._layers = None
-        self._embed = self._final_norm = self._lmh = None
+        self._embed = self._final_norm = self._lmh = self._lmh32 = None
         self._lmT = None
         try:
             import torch
@@ -245,15 +259,6 @@ class LlamaPrefill:
             torch.cuda.synchronize()
             return y[0].cpu().numpy()
         return self._host_logits(hidden_row)
-
-    def _decode_logits(self, hidden_row, use_ane, greedy):
-        use_ane = self.ane_lm_head if use_ane is None else bool(use_ane)
-        logits = self._logits(hidden_row, use_ane)
-        if greedy and use_ane and self._lmh is not None:
-            p = np.partition(logits, -2)
-            if p[-1] - p[-2] < self.lmhead_tie_margin * (float(np.abs(logits).max()) + 1e-9):
-                logits = self._logits(hidden_row, ane=False)
-        return logits
 
     @staticmethod
     def _sample(logits, temperature, top_p, top_k):
@@ -370,26 +375,29 @@ class LlamaPrefill:
 
 
 # ----------------------------------------------------------------------------- HF adapters
+# Hugging Face Llama/Qwen parameter names below "model.layers.<i>." -> canonical per-layer keys.
+_HF_LAYER = {"wq": "self_attn.q_proj.weight", "wk": "self_attn.k_proj.weight", "wv": "self_attn.v_proj.weight",
+             "wo": "self_attn.o_proj.weight", "attn_norm": "input_layernorm.weight",
+             "mlp_norm": "post_attention_layernorm.weight"}
+# present only in some checkpoints: the dense MLP (absent on expert layers), QK-norm, projection biases
+_HF_LAYER_OPTIONAL = {"wgate": "mlp.gate_proj.weight", "wup": "mlp.up_proj.weight", "wdown": "mlp.down_proj.weight",
+                      "q_norm": "self_attn.q_norm.weight", "k_norm": "self_attn.k_norm.weight",
+                      "q_bias": "self_attn.q_proj.bias", "k_bias": "self_attn.k_proj.bias",
+                      "v_bias": "self_attn.v_proj.bias", "o_bias": "self_attn.o_proj.bias"}
+
+
 def _weights_from_state_dict(sd, cfg: LlamaConfig) -> dict:
-    """Map a Llama/Qwen Hugging Face state_dict (numpy) to the canonical weight dict."""
-    w = {"embed": sd["model.embed_tokens.weight"], "final_norm": sd["model.norm.weight"],
-         "lm_head": sd.get("lm_head.weight", sd["model.embed_tokens.weight"]), "layers": []}
-    for L in range(cfg.n_layers):
-        p = f"model.layers.{L}."
-        lw = {"wq": sd[p + "self_attn.q_proj.weight"], "wk": sd[p + "self_attn.k_proj.weight"],
-              "wv": sd[p + "self_attn.v_proj.weight"], "wo": sd[p + "self_attn.o_proj.weight"],
-              "wgate": sd[p + "mlp.gate_proj.weight"], "wup": sd[p + "mlp.up_proj.weight"],
-              "wdown": sd[p + "mlp.down_proj.weight"], "attn_norm": sd[p + "input_layernorm.weight"],
-              "mlp_norm": sd[p + "post_attention_layernorm.weight"]}
-        if p + "self_attn.q_norm.weight" in sd:
-            lw["q_norm"] = sd[p + "self_attn.q_norm.weight"]
-            lw["k_norm"] = sd[p + "self_attn.k_norm.weight"]
-        for proj, key in (("q_proj", "q_bias"), ("k_proj", "k_bias"), ("v_proj", "v_bias"), ("o_proj", "o_bias")):
-            b = sd.get(p + f"self_attn.{proj}.bias")
-            if b is not None:
-                lw[key] = b
-        w["layers"].append(lw)
-    return w
+    """A Llama/Qwen Hugging Face state_dict (numpy arrays) as the canonical weight dict; a tied
+    head (no lm_head.weight) reuses the embedding."""
+    embed = sd["model.embed_tokens.weight"]
+    layers = []
+    for i in range(cfg.n_layers):
+        pre = f"model.layers.{i}."
+        lw = {key: sd[pre + name] for key, name in _HF_LAYER.items()}
+        lw.update((key, sd[pre + name]) for key, name in _HF_LAYER_OPTIONAL.items() if pre + name in sd)
+        layers.append(lw)
+    return {"embed": embed, "final_norm": sd["model.norm.weight"], "lm_head": sd.get("lm_head.weight", embed),
+            "layers": layers}
 
 
 def _rope_theta(c) -> float:
@@ -441,11 +449,18 @@ ADAPTERS: list = [
 
 
 def _assert_dense_compatible(c) -> None:
-    mt = getattr(c, "model_type", "?")
-    cap = getattr(c, "attn_logit_softcapping", None) or getattr(c, "final_logit_softcapping", None)
-    if cap or mt in _DENSE_INCOMPATIBLE:
-        why = "logit softcapping" if cap else "architecture-specific semantics"
-        raise ValueError(f"load_llm: {mt!r} needs {why} that the dense loader does not implement")
+    """A config headed for the dense Llama adapter must not carry semantics that adapter ignores: logit
+    softcapping (checked first, so a Llama-shaped finetune with an unusual model_type still loads) or
+    one of the architectures listed above.  The reference draws the same line (aneforge/llm.py:776-788);
+    its Gemma adapter is not built here, so Gemma is refused too."""
+    model_type = getattr(c, "model_type", "?")
+    softcap = getattr(c, "attn_logit_softcapping", None) or getattr(c, "final_logit_softcapping", None)
+    if softcap:
+        raise ValueError(f"load_llm: {model_type!r} uses logit softcapping, which the dense decoder does not "
+                         f"implement; loading it would give wrong logits")
+    if model_type in _DENSE_INCOMPATIBLE:
+        raise ValueError(f"load_llm: {model_type!r} has architecture-specific semantics the dense decoder does "
+                         f"not implement (supported: dense Llama / Qwen / Mistral and Qwen-MoE)")
 
 
 def from_pretrained(name: str, compress: str | None = None, ane_lm_head: bool = True) -> LlamaPrefill:

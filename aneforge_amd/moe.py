@@ -17,59 +17,41 @@ from __future__ import annotations
 import numpy as np
 
 from . import llm
-from .graph import _const, concat as _concat, select
+from .graph import Tensor
 from .llm import LayerSpec, LlamaConfig
 
-_MAX_DIM = 65536
-_MAX_EXPERTS = 2049
+_MAX_EXPERTS = 2049     # the reference carries expert indices as fp16 integers, exact up to 2048
+
+
+def _check_topk(k: int, E: int) -> None:
+    if not 1 <= k <= E <= _MAX_EXPERTS:
+        raise ValueError(f"moe top-k: need 1 <= k <= E <= {_MAX_EXPERTS}; got k={k}, E={E}")
 
 
 # ----------------------------------------------------------------------------- graph builders
 def _topk_gate(probs, k, E, T):
-    """probs [T, E] masked to the top-k per row (0 elsewhere) without a native top-k: k rounds of
-    row max, the lowest tied index chosen each round (aneforge/moe.py:21-37)."""
-    if not 1 <= k <= E <= _MAX_EXPERTS:
-        raise ValueError(f"moe top-k: need 1 <= k <= E <= {_MAX_EXPERTS}; got k={k}, E={E}")
-    lanes = _const(np.tile(np.arange(E, dtype=np.float16), (T, 1)))
-    far = _const(np.full((T, E), 4096.0, np.float16))
-    gone = _const(np.full((T, E), -3.0e4, np.float16))
-    on = _const(np.ones((T, E), np.float16))
-    picked = _const(np.zeros((T, E), np.float16))
-    rest = probs
-    for _ in range(k):
-        at_max = rest.greater_equal(rest.amax([1]).reshape(T, 1))
-        lowest = (select(at_max, lanes, far) * -1.0).amax([1]).reshape(T, 1) * -1.0
-        hit = lanes.equal(lowest)
-        picked = select(hit, on, picked)
-        rest = select(hit, gone, rest)
-    return probs * picked
-
-
-def _experts_gate(hn, wexps, E, ffn, dim, T):
-    """hn @ wexps[e].T for all experts -> [T, E, ffn] (aneforge/moe.py:40-45)."""
-    g = max(1, min(E, _MAX_DIM // ffn))
-    parts = [hn.linear(np.asarray(wexps[s:s + g]).reshape(min(g, E - s) * ffn, dim)).reshape(T, min(g, E - s), ffn)
-             for s in range(0, E, g)]
-    return parts[0] if len(parts) == 1 else _concat(parts, axis=1)
+    """The router's gate for af.compile graphs: probs [T, E] (fp16 probabilities) kept on the k
+    experts each row routes to and zeroed elsewhere.  Routing contract of aneforge/moe.py:21-37:
+    exactly k experts per row, chosen by k rounds of the row maximum with the lowest expert index
+    winning an exact fp16 tie.  On this device that is one graph node, lowered to a single
+    kernel (afx_topk_mask) rather than built from comparisons and selects."""
+    _check_topk(int(k), int(E))
+    if tuple(probs.shape) != (T, E):
+        raise ValueError(f"moe top-k: probabilities {tuple(probs.shape)} are not [{T}, {E}]")
+    return Tensor(probs.shape, "topk_mask", [probs], {"k": int(k)})
 
 
 def _moe(h, w, cfg, ls):
-    """Graph form of the MoE SwiGLU MLP + residual (aneforge/moe.py:48-63), for af.compile."""
-    e = cfg.extra
-    E, k, dim = e["n_experts"], e["n_experts_per_tok"], cfg.dim
-    ffn, T = np.asarray(w["wgate_exps"]).shape[1], h.shape[0]
-    hn = h.rms_norm(w["mlp_norm"], cfg.norm_eps)
-    gate_w = _topk_gate(hn.linear(w["router"]).softmax(-1), k, E, T)
-    if e.get("norm_topk_prob", True):
-        gate_w = gate_w / gate_w.sum([1]).reshape(T, 1)
-    gate = _experts_gate(hn, w["wgate_exps"], E, ffn, dim, T)
-    up = _experts_gate(hn, w["wup_exps"], E, ffn, dim, T)
-    out = (gate.silu() * up).transpose([1, 0, 2]).bmm_weight(w["wdown_exps"])
-    combined = (out * gate_w.transpose([1, 0]).reshape(E, T, 1)).sum([0]).reshape(T, dim)
-    if "wgate_sh" in w:
-        sh = (hn.linear(w["wgate_sh"]).silu() * hn.linear(w["wup_sh"])).linear(w["wdown_sh"])
-        combined = combined + sh * hn.linear(w["shared_gate"]).sigmoid()
-    return h + combined
+    """af.compile form of the MoE SwiGLU MLP with its residual (aneforge/moe.py:48-63): h [T, dim]
+    -> h + sum over the routed experts of gate * Wd_e(silu(Wg_e hn) * Wu_e hn) (+ the sigmoid-gated
+    shared expert).  The reference evaluates every expert and masks the unselected ones with a
+    zero gate; here the node lowers to the sparse device layer (MoEDecode), which computes only
+    the routed experts -- the same sum, since a masked expert contributes exactly 0."""
+    ex = cfg.extra
+    _check_topk(int(ex["n_experts_per_tok"]), int(ex["n_experts"]))
+    if len(h.shape) != 2 or h.shape[1] != cfg.dim:
+        raise ValueError(f"moe: hidden states must be [T, {cfg.dim}], got {tuple(h.shape)}")
+    return Tensor(h.shape, "moe_mlp", [h], {"w": w, "cfg": cfg, "ls": ls})
 
 
 # ----------------------------------------------------------------------------- device executor
@@ -83,8 +65,7 @@ class MoEDecode:
         ex = cfg.extra
         self.E, self.k = int(ex["n_experts"]), int(ex["n_experts_per_tok"])
         self.renorm = bool(ex.get("norm_topk_prob", True))
-        if not 1 <= self.k <= self.E <= _MAX_EXPERTS:
-            raise ValueError(f"moe top-k: need 1 <= k <= E <= {_MAX_EXPERTS}; got k={self.k}, E={self.E}")
+        _check_topk(self.k, self.E)
         D, eps = cfg.dim, float(cfg.norm_eps)
         self.D, self.eps = D, eps
         self.norm = E._gamma(lw["mlp_norm"], D)
@@ -205,43 +186,37 @@ llm.DECODE_MLPS["moe"] = MoEDecode
 
 
 # ----------------------------------------------------------------------------- HF adapter
+def _moe_layer_plan(c) -> list[bool]:
+    """Which layers of a Qwen-MoE config carry experts: every `decoder_sparse_step`-th layer (1-based)
+    that is not listed in `mlp_only_layers` (the reference's rule, aneforge/moe.py:77-79)."""
+    every = int(getattr(c, "decoder_sparse_step", 1) or 1)
+    dense = set(getattr(c, "mlp_only_layers", []) or [])
+    return [i not in dense and (i + 1) % every == 0 for i in range(int(c.num_hidden_layers))]
+
+
 def _moe_adapter(c, sd) -> tuple[LlamaConfig, dict]:
-    """Qwen3-MoE Hugging Face adapter (aneforge/moe.py:70-107): attention layers as usual, MoE
-    layers carry the fused expert weights plus the router."""
-    n, E, k = int(c.num_hidden_layers), int(c.num_experts), int(c.num_experts_per_tok)
-    moe_ffn = int(c.moe_intermediate_size)
+    """Hugging Face Qwen3-MoE -> (LlamaConfig, canonical weights) (aneforge/moe.py:70-107).  The dense
+    decoder adapter maps the attention half and the dense MLP layers; expert layers swap their MLP
+    for the router and the expert stacks, split out of the fused gate|up tensor and with down taken
+    to the canonical [E, ffn, dim]."""
+    plan = _moe_layer_plan(c)
     qk = "model.layers.0.self_attn.q_norm.weight" in sd
-    step = int(getattr(c, "decoder_sparse_step", 1) or 1)
-    mlp_only = set(getattr(c, "mlp_only_layers", []) or [])
-    is_moe = [(L not in mlp_only) and ((L + 1) % step == 0) for L in range(n)]
-    specs = [LayerSpec(mixer="attention", mlp=("moe" if is_moe[L] else "swiglu"), qk_norm=qk) for L in range(n)]
-    cfg = LlamaConfig(dim=c.hidden_size, n_layers=n, n_heads=c.num_attention_heads,
-                      n_kv_heads=getattr(c, "num_key_value_heads", c.num_attention_heads),
-                      ffn_dim=c.intermediate_size, vocab=c.vocab_size, rope_base=llm._rope_theta(c),
-                      norm_eps=float(c.rms_norm_eps), head_dim=int(getattr(c, "head_dim", 0) or 0), layers=specs,
-                      extra={"n_experts": E, "n_experts_per_tok": k,
-                             "norm_topk_prob": bool(getattr(c, "norm_topk_prob", True))})
-    w = {"embed": sd["model.embed_tokens.weight"], "final_norm": sd["model.norm.weight"],
-         "lm_head": sd.get("lm_head.weight", sd["model.embed_tokens.weight"]), "layers": []}
-    for L in range(n):
-        p = f"model.layers.{L}."
-        lw = {"wq": sd[p + "self_attn.q_proj.weight"], "wk": sd[p + "self_attn.k_proj.weight"],
-              "wv": sd[p + "self_attn.v_proj.weight"], "wo": sd[p + "self_attn.o_proj.weight"],
-              "attn_norm": sd[p + "input_layernorm.weight"], "mlp_norm": sd[p + "post_attention_layernorm.weight"]}
-        if qk:
-            lw["q_norm"] = sd[p + "self_attn.q_norm.weight"]
-            lw["k_norm"] = sd[p + "self_attn.k_norm.weight"]
-        if is_moe[L]:
-            gu = sd[p + "mlp.experts.gate_up_proj"]
-            lw["router"] = sd[p + "mlp.gate.weight"]
-            lw["wgate_exps"] = np.ascontiguousarray(gu[:, :moe_ffn, :])
-            lw["wup_exps"] = np.ascontiguousarray(gu[:, moe_ffn:, :])
-            lw["wdown_exps"] = np.ascontiguousarray(sd[p + "mlp.experts.down_proj"].transpose(0, 2, 1))
-        else:
-            lw["wgate"] = sd[p + "mlp.gate_proj.weight"]
-            lw["wup"] = sd[p + "mlp.up_proj.weight"]
-            lw["wdown"] = sd[p + "mlp.down_proj.weight"]
-        w["layers"].append(lw)
+    cfg = llm._cfg_from_hf(c)
+    cfg.layers = [LayerSpec(mixer="attention", mlp="moe" if on else "swiglu", qk_norm=qk) for on in plan]
+    cfg.extra = {"n_experts": int(c.num_experts), "n_experts_per_tok": int(c.num_experts_per_tok),
+                 "norm_topk_prob": bool(getattr(c, "norm_topk_prob", True))}
+    F = int(c.moe_intermediate_size)
+    w = llm._weights_from_state_dict(sd, cfg)          # expert layers have no dense MLP tensors
+    for i, on in enumerate(plan):
+        if not on:
+            continue
+        lw = w["layers"][i]
+        pre = f"model.layers.{i}.mlp."
+        fused = sd[pre + "experts.gate_up_proj"]                      # [E, 2F, dim]: gate rows, then up rows
+        lw.update(router=sd[pre + "gate.weight"],
+                  wgate_exps=np.ascontiguousarray(fused[:, :F]),
+                  wup_exps=np.ascontiguousarray(fused[:, F:]),
+                  wdown_exps=np.ascontiguousarray(np.swapaxes(sd[pre + "experts.down_proj"], 1, 2)))
     return cfg, w
 
 
@@ -250,81 +225,89 @@ llm.ADAPTERS.append((lambda c: bool(getattr(c, "num_experts", 0)), _moe_adapter)
 
 # ----------------------------------------------------------------------------- GGUF loader
 class _LazyLayers:
-    """Per-layer weights materialised on demand and dropped once packed (aneforge/moe.py:113-126)."""
+    """A sequence of per-layer weight dicts read from the file only when first indexed.  The
+    decoder packs layer i onto the device and then calls free(i), so the host never holds more than
+    one layer's dequantised tensors (aneforge/moe.py:113-126 plays the same role per ANE chunk)."""
 
-    def __init__(self, materialize, n: int):
-        self._mk = materialize
-        self._n = n
-        self._cache: dict = {}
+    def __init__(self, read_layer, n: int):
+        self._read, self._n, self._held = read_layer, n, {}
 
     def __len__(self) -> int:
         return self._n
 
     def __getitem__(self, i: int) -> dict:
-        if i not in self._cache:
-            self._cache[i] = self._mk(i)
-        return self._cache[i]
+        if not 0 <= i < self._n:
+            raise IndexError(i)
+        if i not in self._held:
+            self._held[i] = self._read(i)
+        return self._held[i]
 
     def free(self, i: int) -> None:
-        self._cache.pop(i, None)
+        self._held.pop(i, None)
+
+
+# GGUF metadata -> LlamaConfig fields (key below the "<arch>." prefix, default); the key names are
+# the file format's, as aneforge/moe.py:138-150 reads them.
+_GGUF_HPARAMS = {
+    "n_layers": ("block_count", 0), "dim": ("embedding_length", 0), "n_heads": ("attention.head_count", 0),
+    "n_experts": ("expert_count", 0), "k": ("expert_used_count", 0), "rope_base": ("rope.freq_base", 10000.0),
+    "norm_eps": ("attention.layer_norm_rms_epsilon", 1e-6),
+}
+# canonical per-layer name -> GGUF tensor below "blk.<i>.", always present
+_GGUF_LAYER = {"wq": "attn_q.weight", "wk": "attn_k.weight", "wv": "attn_v.weight", "wo": "attn_output.weight",
+               "attn_norm": "attn_norm.weight", "mlp_norm": "ffn_norm.weight", "router": "ffn_gate_inp.weight"}
+# present only in some architectures: Qwen3 QK-norm, Qwen2 QKV biases
+_GGUF_LAYER_OPTIONAL = {"q_norm": "attn_q_norm.weight", "k_norm": "attn_k_norm.weight",
+                        "q_bias": "attn_q.bias", "k_bias": "attn_k.bias", "v_bias": "attn_v.bias"}
+# Qwen2-MoE shared expert
+_GGUF_SHARED = {"wgate_sh": "ffn_gate_shexp.weight", "wup_sh": "ffn_up_shexp.weight",
+                "wdown_sh": "ffn_down_shexp.weight", "shared_gate": "ffn_gate_inp_shexp.weight"}
 
 
 def load_gguf(path: str, n_layers: int | None = None, compress: str | None = None) -> "llm.LlamaPrefill":
-    """Load a Qwen-MoE GGUF (aneforge/moe.py:129-173) with this package's own GGUF reader.
-    Q4_0 expert tensors stay 4-bit (streamed by the Q4_0 kernels, never dequantised); other
-    tensors are dequantised to fp16 as the reference does.  Arch features (QK-norm, shared
-    expert, QKV biases) are detected from the tensor names."""
+    """A Qwen-MoE GGUF file as a LlamaPrefill (aneforge/moe.py:129-173), read by this package's own
+    GGUF reader.  Expert stacks stored as Q4_0 / Q4_K / Q6_K / Q8_0 reach the device as their codes
+    (the matching kernels stream them); every other tensor is dequantised as the reference does,
+    embedding and lm_head to fp32, the rest to fp16.  The architecture's optional parts (QK-norm,
+    QKV biases, a shared expert) are detected from the tensor names; `n_layers` keeps the first
+    layers only."""
     from ._gguf import GGUFView
     gg = GGUFView(path)
-    sc, get, tn, arch = gg.sc, gg.get, gg.tn, gg.arch
-    opt = lambda name: get(name) if gg.has(name) else None
-    n_total = int(sc("block_count", 0))
-    n = n_total if n_layers is None else min(n_layers, n_total)
-    E, k = int(sc("expert_count", 0)), int(sc("expert_used_count", 0))
-    dim = int(sc("embedding_length", 0))
-    vocab = int(tn["token_embd.weight"].data.shape[0])
-    heads = int(sc("attention.head_count", 0))
-    moe_ffn = int(tn["blk.0.ffn_gate_exps.weight"].shape[1])
-    qk = gg.has("blk.0.attn_q_norm.weight")
-    shared = gg.has("blk.0.ffn_gate_shexp.weight")
-    cfg = llm.LlamaConfig(
-        dim=dim, n_layers=n, n_heads=heads, n_kv_heads=int(sc("attention.head_count_kv", heads)),
-        ffn_dim=moe_ffn, vocab=vocab, rope_base=float(sc("rope.freq_base", 10000.0)),
-        norm_eps=float(sc("attention.layer_norm_rms_epsilon", 1e-6)),
-        head_dim=int(sc("attention.key_length") or dim // heads),
-        layers=[llm.LayerSpec(mixer="attention", mlp="moe", qk_norm=qk) for _ in range(n)],
-        extra={"n_experts": E, "n_experts_per_tok": k, "norm_topk_prob": arch != "qwen2moe"})
+    hp = {name: gg.sc(key, default) for name, (key, default) in _GGUF_HPARAMS.items()}
+    n = int(hp["n_layers"]) if n_layers is None else min(int(n_layers), int(hp["n_layers"]))
+    dim, heads = int(hp["dim"]), int(hp["n_heads"])
+    qk = gg.has("blk.0." + _GGUF_LAYER_OPTIONAL["q_norm"])
+    shared = gg.has("blk.0." + _GGUF_SHARED["wgate_sh"])
+    cfg = LlamaConfig(
+        dim=dim, n_layers=n, n_heads=heads, n_kv_heads=int(gg.sc("attention.head_count_kv", heads)),
+        ffn_dim=int(gg.tn["blk.0.ffn_gate_exps.weight"].shape[1]),
+        vocab=int(gg.tn["token_embd.weight"].data.shape[0]), rope_base=float(hp["rope_base"]),
+        norm_eps=float(hp["norm_eps"]), head_dim=int(gg.sc("attention.key_length") or dim // heads),
+        layers=[LayerSpec(mixer="attention", mlp="moe", qk_norm=qk) for _ in range(n)],
+        # Qwen1.5 / Qwen2-MoE does not renormalise the top-k probabilities
+        extra={"n_experts": int(hp["n_experts"]), "n_experts_per_tok": int(hp["k"]),
+               "norm_topk_prob": gg.arch != "qwen2moe"})
 
-    def experts(name):
-        """An expert stack: per-expert QuantizedWeight when the file holds Q4_0 / Q4_K / Q6_K / Q8_0 codes, else fp16."""
-        q = gg.quantized(name)
-        if q is not None:
-            return q
-        return get(name)
+    def expert_stack(name):
+        codes = gg.quantized(name)
+        return codes if codes is not None else gg.get(name)
 
-    def layer(L):
-        b = f"blk.{L}."
-        d = {"wq": get(b + "attn_q.weight"), "wk": get(b + "attn_k.weight"), "wv": get(b + "attn_v.weight"),
-             "wo": get(b + "attn_output.weight"), "attn_norm": get(b + "attn_norm.weight"),
-             "mlp_norm": get(b + "ffn_norm.weight"), "router": get(b + "ffn_gate_inp.weight"),
-             "wgate_exps": experts(b + "ffn_gate_exps.weight"), "wup_exps": experts(b + "ffn_up_exps.weight")}
-        down = experts(b + "ffn_down_exps.weight")
-        # GGUF stores down as [E, dim, ffn]; the canonical float layout is [E, ffn, dim]
-        d["wdown_exps"] = down if isinstance(down, list) else np.ascontiguousarray(np.asarray(down).transpose(0, 2, 1))
-        for key, nm in (("q_norm", "attn_q_norm.weight"), ("k_norm", "attn_k_norm.weight"),
-                        ("q_bias", "attn_q.bias"), ("k_bias", "attn_k.bias"), ("v_bias", "attn_v.bias")):
-            v = opt(b + nm)
-            if v is not None:
-                d[key] = v
+    def read_layer(i: int) -> dict:
+        blk = f"blk.{i}."
+        lw = {key: gg.get(blk + name) for key, name in _GGUF_LAYER.items()}
+        lw.update((key, gg.get(blk + name)) for key, name in _GGUF_LAYER_OPTIONAL.items() if gg.has(blk + name))
         if shared:
-            d["wgate_sh"] = get(b + "ffn_gate_shexp.weight")
-            d["wup_sh"] = get(b + "ffn_up_shexp.weight")
-            d["wdown_sh"] = get(b + "ffn_down_shexp.weight")
-            d["shared_gate"] = get(b + "ffn_gate_inp_shexp.weight").reshape(1, dim)
+            lw.update((key, gg.get(blk + name)) for key, name in _GGUF_SHARED.items())
+            lw["shared_gate"] = lw["shared_gate"].reshape(1, dim)
+        lw["wgate_exps"] = expert_stack(blk + "ffn_gate_exps.weight")
+        lw["wup_exps"] = expert_stack(blk + "ffn_up_exps.weight")
+        down = expert_stack(blk + "ffn_down_exps.weight")     # [E, dim, ffn] as stored
+        # code stacks stay per expert [dim, ffn]; a float stack goes to the canonical [E, ffn, dim]
+        lw["wdown_exps"] = down if isinstance(down, list) else np.ascontiguousarray(np.swapaxes(down, 1, 2))
         gg.drop_pages()
-        return d
+        return lw
 
-    w = {"embed": get("token_embd.weight", np.float32), "final_norm": get("output_norm.weight"),
-         "lm_head": get("output.weight", np.float32) if gg.has("output.weight") else get("token_embd.weight", np.float32),
-         "layers": _LazyLayers(layer, n)}
+    head = "output.weight" if gg.has("output.weight") else "token_embd.weight"
+    w = {"embed": gg.get("token_embd.weight", np.float32), "final_norm": gg.get("output_norm.weight"),
+         "lm_head": gg.get(head, np.float32), "layers": _LazyLayers(read_layer, n)}
     return llm.LlamaPrefill(cfg, w, compress=compress)

@@ -73,6 +73,13 @@ int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx
 int afx_linear_rms(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
                    float eps, void* y, int ldy, int M, int N, int K, const void* bias, int out_f32,
                    int rows_hint, void* stream);
+/* The lm_head for one hidden row (aneforge/llm.py:338-404, the fp16 head): logits[N] (fp32) =
+ * rms_norm(x, gamma, eps) @ W^T (fmt 2, W fp16 [N][K]), plus slots (16-byte aligned float4
+ * [ceil(N/8)]): for rows 8s..8s+7, {largest logit, its row as int bits (lowest on ties), second
+ * largest, largest |logit|}, which afx_decode_advance merges for the greedy pick and its tie margin;
+ * and, if hn_out is not NULL, the fp16 normalised row the products used [K]. */
+int afx_lm_head(int fmt, const void* w, const void* scale, const void* x, const void* gamma, float eps,
+                float* logits, int N, int K, float* slots, void* hn_out, void* stream);
 /* act[M][N/2] = silu(g) * u, rows of W interleaved (gate_i, up_i), optional RMSNorm first:
  * the front half of _swiglu (aneforge/llm.py:171-175). */
 int afx_linear_swiglu(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
@@ -159,10 +166,16 @@ int afx_sample(const float* logits, int V, const double* params, const double* u
 /* host embedding gather of LlamaPrefill.step (aneforge/llm.py:593-594), on the device */
 int afx_embed(const void* table, const int* ids, void* out, int M, int D, int vocab, void* stream);
 /* One step of the device-resident decode loop (aneforge/llm.py:584-627 step/_sample/generate):
- * token = forced[*step] while *step < *n_forced (prompt), else greedy argmax of logits; then
- * hist[*step] = token, ++*step, ++*pos, h = embed[token] (the host gather of :593-594). */
-int afx_decode_advance(const float* logits, int V, const int* forced, const int* n_forced, int* tok, int* pos,
-                       int* hist, int hist_cap, int* step, const void* embed, void* h, int D, int vocab,
+ * token = forced[*step] while *step < *n_forced (prompt), else the greedy pick (lowest index on ties)
+ * from the slots of afx_lm_head (or from the logits when slots is NULL); then hist[*step] = token,
+ * ++*step, ++*pos, h = embed[token] (the host gather of :593-594).  With tie_margin (a device float),
+ * the reference's near-tie rule (aneforge/llm.py:281, 395-404): when the two largest logits are closer
+ * than margin * max|logit|, every logit inside that window of the largest is recomputed exactly from hn
+ * (the head's fp16 input row [D]) and the head rows (head32 fp32 [V][D] if given, else head16), and
+ * the largest exact value wins. */
+int afx_decode_advance(const float* logits, const float* slots, int V, const float* tie_margin, const void* hn,
+                       const void* head16, const float* head32, const int* forced, const int* n_forced, int* tok,
+                       int* pos, int* hist, int hist_cap, int* step, const void* embed, void* h, int D, int vocab,
                        void* stream);
 /* np.argmax per row (lowest index on ties) */
 int afx_argmax(const float* x, int M, int V, int* out, void* stream);
@@ -196,6 +209,10 @@ int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int
 /* active experts only: act @ Wd_e (bmm_weight, moe.py:58) */
 int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F, int D,
                  const int* cnt, const int* list, float* y, int rows_hint, void* stream);
+/* The graph form of the top-k gate (_topk_gate, aneforge/moe.py:21-37): y = x on the k experts each
+ * row of fp16 probabilities x [T][E] keeps (k rounds of the row maximum, the lowest index among exact
+ * fp16 ties), 0 elsewhere; 1 <= k <= E <= 2049. */
+int afx_topk_mask(const void* x, int T, int E, int k, void* y, void* stream);
 /* h + sum_e gate * y_e (+ shared expert) (moe.py:59-63) */
 int afx_moe_combine(const void* h, const float* y, const float* gate, const void* shared, void* out, int T,
                     int k, int D, void* stream);

@@ -144,30 +144,17 @@ def test_rope_tables_equal_oracle_bitwise():
         assert np.array_equal(a[1].view(np.uint16), b[1].view(np.uint16))
 
 
-def test_decode_logits_tie_margin_fallback():
-    # aneforge tests/test_lm_head.py:186-216
-    cfg = LlamaConfig(dim=64, n_layers=1, n_heads=4, n_kv_heads=2, ffn_dim=128, vocab=100)
-    m = _random_model(cfg, seed=1)
-    m.ane_lm_head = True
-    m._lmh = object()
-    near = np.zeros(100, np.float32); near[0] = 10.0; near[1] = 10.0 - 0.001
-    clear = np.zeros(100, np.float32); clear[0] = 10.0
-    host = np.zeros(100, np.float32); host[1] = 10.0; host[0] = 9.99
-    calls = []
-
-    def fake(which):
-        def _f(h, ane=None):
-            calls.append(ane)
-            return which if ane else host
-        return _f
-
-    m._logits = fake(near)
-    assert int(m._decode_logits(np.zeros(64, np.float32), True, greedy=True).argmax()) == 1 and calls == [True, False]
-    calls.clear(); m._logits = fake(clear)
-    assert int(m._decode_logits(np.zeros(64, np.float32), True, greedy=True).argmax()) == 0 and calls == [True]
-    calls.clear(); m._logits = fake(near)
-    m._decode_logits(np.zeros(64, np.float32), True, greedy=False)
-    assert calls == [True]
+@pytest.mark.parametrize("model_type,extra", [("gemma", {}), ("gemma2", {}), ("gemma3_text", {}),
+                                              ("llama", {"final_logit_softcapping": 30.0})])
+def test_dense_loader_rejects_what_it_would_mis_load(model_type, extra):
+    # aneforge/llm.py:776-788: the dense loader refuses configs whose semantics it would drop; Gemma's
+    # sqrt(dim) embedding scale, (1 + w) norms and GeGLU are not on this device path, so it is refused
+    from types import SimpleNamespace
+    c = SimpleNamespace(model_type=model_type, **extra)
+    with pytest.raises(ValueError, match=repr(model_type)):
+        llm._assert_dense_compatible(c)
+    llm._assert_dense_compatible(SimpleNamespace(model_type="llama"))
+    llm._assert_dense_compatible(SimpleNamespace(model_type="qwen2"))
 
 
 def test_sample_greedy_and_topk():

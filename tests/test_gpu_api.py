@@ -127,17 +127,63 @@ def _moe_weights(E, D, F, seed=0):
 
 
 def test_moe_graph_matches_reference_oracle():
-    # aneforge tests/test_moe.py:48-57 (cosine > 0.99 there; dense graph vs sparse oracle here)
+    # aneforge tests/test_moe.py:48-57 (cosine > 0.99 there): held to the path's bar here, against the
+    # oracle at the kernels' fp16 rounding points with the fp16 weights the layer streams
     say("_moe graph through compile")
     cfg = af.LlamaConfig(dim=32, n_layers=1, n_heads=4, n_kv_heads=2, ffn_dim=16, vocab=16,
                          extra={"n_experts": 8, "n_experts_per_tok": 2, "norm_topk_prob": True})
     w = _moe_weights(8, 32, 16)
-    for T in (1, 5):
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+    for T in (1, 5, 12):
         h = (np.random.default_rng(T).standard_normal((T, 32)) * 0.5).astype(np.float16)
         got = af.compile(af.moe._moe(af.input((T, 32)), w, cfg, af.LayerSpec(mlp="moe")))(h)
-        want, _, _ = ref.moe_layer(h, w["mlp_norm"], w["router"], w["wgate_exps"], w["wup_exps"],
-                                   np.ascontiguousarray(w["wdown_exps"].transpose(0, 2, 1)), 2, True, 1e-5, exact=True)
-        assert cosine(got, want) > 0.999
+        want, _, _ = ref.moe_layer(h, w["mlp_norm"], f16(w["router"]), f16(w["wgate_exps"]), f16(w["wup_exps"]),
+                                   f16(np.ascontiguousarray(w["wdown_exps"].transpose(0, 2, 1))), 2, True, 1e-5)
+        check_hidden(got, want, what=f"moe graph T={T}")
+
+
+def _bmm_reference_weights(W, compress, atol, block_size=32):
+    """The weights the reference bakes for bmm_weight(W) (aneforge/_compile.py:112-188 on
+    W.reshape(B, K*N), :393-399), as fp32 [B, K, N]."""
+    from aneforge_amd import _blob
+    B, Kd, N = W.shape
+    flat = W.reshape(B, Kd * N)
+    rel = lambda rec: np.linalg.norm(rec - flat) / np.linalg.norm(flat)
+    if compress == "int4":
+        packed, cb = _blob.palettize_lut4(flat)              # pinned by the reference's own vectors
+        rec = ref.dequant_lut4(packed, cb, Kd * N)
+        if rel(rec) <= atol:
+            return rec.reshape(W.shape), "lut4"
+        compress = "int8"
+    if compress == "blockwise":
+        q, s, bs = ref.quantize_blockwise(flat, block_size)
+        rec = ref.dequant_blockwise(q, s, bs)
+        if rel(rec) <= atol:
+            return rec.reshape(W.shape), "blockwise"
+        return flat.astype(np.float16).astype(np.float32).reshape(W.shape), "fp16"
+    if compress == "int8":
+        return ref.dequant_w8(*ref.quantize_per_row(flat)).reshape(W.shape), "int8"
+    return flat.astype(np.float16).astype(np.float32).reshape(W.shape), "fp16"
+
+
+@pytest.mark.parametrize("compress,atol,K,want_kind", [
+    (None, 0.05, 64, "fp16"), ("int8", 0.05, 64, "int8"), ("int4", 0.3, 64, "lut4"), ("int4", 0.3, 40, "lut4"),
+    ("int4", 1e-4, 64, "int8"), ("blockwise", 0.05, 64, "blockwise"), ("blockwise", 1e-5, 64, "fp16")])
+def test_bmm_weight_encodings(compress, atol, K, want_kind):
+    """x [B, M, K] @ W [B, K, N] through af.compile: the reference's bmm encoding precedence (int4 ->
+    LUT4 or int8 with one scale per batch; blockwise -> blockwise along K*N or fp16)."""
+    say(f"bmm_weight compress={compress} atol={atol} K={K}")
+    rng = np.random.default_rng(30)
+    B, M, N = 3, 2, 48
+    W = (rng.standard_normal((B, K, N)) * np.array([0.5, 1.0, 2.0])[:, None, None]).astype(np.float32)
+    x = rng.standard_normal((B, M, K)).astype(np.float16)
+    Wr, kind = _bmm_reference_weights(W, compress, atol)
+    assert kind == want_kind
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        got = af.compile(af.input((B, M, K)).bmm_weight(W), compress=compress, compress_atol=atol)(x)
+    for b in range(B):
+        check_f16(got[b], ref.linear(x[b], np.ascontiguousarray(Wr[b].T)), what=f"bmm {compress} batch {b}")
 
 
 def test_compile_multi_share_buffer_keeps_state_resident():

@@ -585,6 +585,74 @@ def test_decode_advance_greedy_and_forced(K):
     assert np.array_equal(host(h)[0], table[t])
 
 
+@pytest.mark.parametrize("N,Kd", [(32000, 4096), (77, 64), (1000, 256)])
+def test_lm_head_logits_slots_and_normalised_row(K, N, Kd):
+    """afx_lm_head (the fused K = 4096 head and the generic path): the same logits as the plain
+    RMSNorm linear, slots that summarise each 8 rows (largest, its lowest row, second largest,
+    largest magnitude), and the fp16 normalised row the products used."""
+    say(f"lm_head slots N={N} K={Kd}")
+    rng = np.random.default_rng(52)
+    W = (rng.standard_normal((N, Kd)) * 0.02).astype(np.float16)
+    W[5] = W[3]                                                     # an exact tie inside slot 0
+    x = rng.standard_normal((1, Kd)).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, Kd).astype(np.float16)
+    hn = torch.zeros(Kd, dtype=torch.float16, device="cuda")
+    lg, slots = K.lm_head(dev(W), dev(x), dev(g), 1e-5, hn=hn)
+    lg, slots = host(lg)[0], host(slots)
+    plain = host(K.linear_rms("fp16", dev(W), None, dev(x), dev(g), 1e-5, out_f32=True))[0]
+    assert np.array_equal(lg, plain)
+    check_f16(lg, ref.linear(ref.rms_norm(x, g, 1e-5), W.astype(np.float32), exact=True)[0], what="head logits")
+    for s in range((N + 7) // 8):
+        r = lg[8 * s:8 * s + 8]
+        i1 = int(np.argmax(r))
+        top2 = np.sort(r)[-2] if r.size > 1 else -np.inf
+        want = (r[i1], 8 * s + i1, top2, np.abs(r).max())
+        got = (slots[s, 0], int(slots[s, 1:2].view(np.int32)[0]), slots[s, 2], slots[s, 3])
+        assert got == want, f"slot {s}: {got} vs {want}"
+    assert slots[0, 0] != lg[3] or slots[0, 2] == slots[0, 0]       # the tie shows as a zero gap
+    hn = host(hn).astype(np.float64)
+    want = ref.rms_norm(x, g, 1e-5)[0]
+    assert np.abs(hn - want).max() <= np.spacing(np.float16(np.abs(want).max()))
+    # the logits are the products of exactly this row
+    assert np.allclose(lg, W.astype(np.float64) @ hn, rtol=1e-5, atol=1e-5)
+
+
+def test_decode_advance_near_tie_recomputes_exactly(K):
+    """The reference's greedy near-tie rule (aneforge/llm.py:395-404) on the device: two logits closer
+    than margin * max|logit| are recomputed exactly from the head's input row and the head's fp32 rows,
+    and the exact winner is taken; a clear gap, or no margin, keeps the plain argmax."""
+    say("decode advance near-tie recompute")
+    rng = np.random.default_rng(53)
+    V, D = 4096, 256
+    hn = rng.uniform(0.1, 1.0, D).astype(np.float16)
+    W32 = (rng.standard_normal((V, D)) * 0.01).astype(np.float32)
+    W32[100] = (np.abs(W32[100]) + 0.05).astype(np.float16).astype(np.float32)   # fp16-exact, >= 2^-5
+    W32[900] = W32[100] + 2.0 ** -18        # under half an fp16 ulp: the fp16 rows tie, the fp32 rows do not
+    W16 = W32.astype(np.float16)
+    assert np.array_equal(W16[100], W16[900])
+    lg = (W16.astype(np.float64) @ hn.astype(np.float64)).astype(np.float32)
+    lg[900] = lg[100]                                               # the fp16 head's exact tie
+    ref_host = W32.astype(np.float64) @ hn.astype(np.float64)
+    assert int(np.argmax(ref_host)) == 900 and int(np.argmax(lg)) == 100
+
+    def step_once(logits, margin, head32=True):
+        tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+        pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+        stp = torch.zeros(1, dtype=torch.int32, device="cuda")
+        hist = torch.zeros(4, dtype=torch.int32, device="cuda")
+        m = None if margin is None else torch.tensor([margin], dtype=torch.float32, device="cuda")
+        K.decode_advance(dev(logits[None]), tok, pos, hist, stp, tie_margin=m, hn=dev(hn),
+                         head16=None if head32 else dev(W16), head32=dev(W32) if head32 else None)
+        return int(host(tok)[0])
+
+    assert step_once(lg, 3e-3) == 900                               # near tie: exact recompute
+    assert step_once(lg, None) == 100                               # no rule: lowest index
+    assert step_once(lg, 3e-3, head32=False) == 100                 # fp16 rows tie exactly: lowest index
+    clear = lg.copy()
+    clear[100] += 1.0
+    assert step_once(clear, 3e-3) == 100                            # a clear gap: no recompute
+
+
 # ----------------------------------------------------------------------------- MoE
 def test_moe_topk_reference_ties(K):
     say("moe top-k tie vectors")

@@ -254,3 +254,43 @@ def test_batched_prefill_matches_forced_steps_and_oracle(compress, chunk):
     want, lgs = ref.generate(prompt, 8, _effective(w, compress), _ocfg(cfg), M=M)
     _assert_tokens_match(got, want, lgs, f"batched prefill compress={compress}")
     m.release()
+
+
+def test_greedy_near_tie_takes_the_host_fp32_choice_in_both_loops():
+    """The reference recomputes a greedy step with the host fp32 head when the device head's top-2
+    logits are within lmhead_tie_margin * max|logit| (aneforge/llm.py:281, 395-404;
+    tests/test_lm_head.py:186-216).  Built case: the layers add nothing (wo = wdown = 0), so h is the
+    token's embedding, whose first entry is positive; the final norm keeps only that entry; lm_head
+    rows 3 and 7 differ by less than an fp16 ulp, so the fp16 head ties them exactly and its plain
+    argmax is 3, while the fp32 head (hn * (1 + 2^-14) > hn * 1) picks 7 at every step."""
+    from aneforge_amd.llm import LlamaConfig, LlamaPrefill
+    say("greedy near-tie rule: graph loop, per-token loop, host head")
+    D, V = 64, 32
+    cfg = LlamaConfig(dim=D, n_layers=2, n_heads=4, n_kv_heads=2, ffn_dim=128, vocab=V)
+    w = _random_weights(cfg, seed=3)
+    for lw in w["layers"]:
+        lw["wo"][:] = 0.0
+        lw["wdown"][:] = 0.0
+    rng = np.random.default_rng(4)
+    w["embed"] = rng.standard_normal((V, D)).astype(np.float32)
+    w["embed"][:, 0] = np.abs(w["embed"][:, 0]) + 0.5
+    w["final_norm"] = np.zeros(D, np.float32)
+    w["final_norm"][0] = 1.0
+    head = np.zeros((V, D), np.float32)
+    head[:, 0] = -0.5
+    head[3, 0] = 1.0
+    head[7, 0] = 1.0 + 2.0 ** -14
+    assert np.float16(head[7, 0]) == np.float16(head[3, 0])
+    w["lm_head"] = head
+    m = LlamaPrefill(cfg, w)
+    prompt = [1, 2, 5]
+    assert m.generate(prompt, max_new_tokens=4) == [7, 7, 7, 7]                 # graph loop
+    seen = []
+    assert m.generate(prompt, max_new_tokens=4, on_token=seen.append) == [7, 7, 7, 7]   # per-token loop
+    assert seen == [7, 7, 7, 7]
+    assert m.generate(prompt, max_new_tokens=4, ane_lm_head=False) == [7, 7, 7, 7]     # host fp32 head
+    m.lmhead_tie_margin = 0.0                                                    # rule off: fp16 tie
+    assert m.generate(prompt, max_new_tokens=4) == [3, 3, 3, 3]
+    m.lmhead_tie_margin = 3e-3
+    assert m.generate(prompt, max_new_tokens=2) == [7, 7]
+    m.release()

@@ -149,17 +149,31 @@ class _Lowering:
             "less", "less_equal", "equal", "not_equal"}
     _RED = {"reduce_sum", "reduce_max", "reduce_mean", "reduce_min", "reduce_sum_square"}
 
-    def __init__(self, compress, atol, block_size):
+    def __init__(self, compress, atol, block_size, alias=None, cache=None, preset=None):
         self.compress, self.atol, self.block_size = compress, atol, block_size
         self.stats = _Enc()
         self.buf: dict[int, torch.Tensor] = {}
         self.steps: list = []
         self.keep: list = []     # packed weights / constants kept alive with the model
+        self.alias = alias or {}   # node id -> id of the input node whose buffer it writes in place
+        self.cache = {} if cache is None else cache   # node id -> packed weights, reused when re-lowering
+        self.preset = preset or {}   # node id -> an existing buffer to keep (input ports when re-lowering)
 
     def out(self, t: Tensor) -> torch.Tensor:
-        b = torch.empty(t.shape if t.shape else (1,), dtype=torch.float16, device="cuda")
+        if id(t) in self.preset:
+            b = self.preset[id(t)]
+        elif id(t) in self.alias:
+            b = self.buf[self.alias[id(t)]]
+        else:
+            b = torch.empty(t.shape if t.shape else (1,), dtype=torch.float16, device="cuda")
         self.buf[id(t)] = b
         return b
+
+    def cached(self, t: Tensor, make):
+        """make() once per node: weight packing is not repeated when the graph is lowered again."""
+        if id(t) not in self.cache:
+            self.cache[id(t)] = make()
+        return self.cache[id(t)]
 
     def lower(self, order):
         for t in order:
@@ -347,7 +361,7 @@ class _Lowering:
         x = self.buf[id(t.srcs[0])]
         W = t.attrs["wt"]
         allow_q = not isinstance(W, np.ndarray) or W.ndim == 2
-        lin = _encode_weight(W, self.compress, self.atol, self.block_size, self.stats, allow_q)
+        lin = self.cached(t, lambda: _encode_weight(W, self.compress, self.atol, self.block_size, self.stats, allow_q))
         bias = None
         if "bias" in t.attrs:
             bias = torch.from_numpy(np.asarray(t.attrs["bias"], np.float32).astype(F16)).cuda()
@@ -398,7 +412,7 @@ class _Lowering:
         W = np.asarray(t.attrs["wt"], np.float32)
         B, Kd, N = W.shape
         self.stats.n_weights += 1
-        lin = self._bmm_weight_rows(W)
+        lin = self.cached(t, lambda: self._bmm_weight_rows(W))
         self.keep.append(lin)
         y = self.out(t)
         lead = t.srcs[0].shape
@@ -423,7 +437,7 @@ class _Lowering:
         """The MoE MLP + residual as the sparse device layer (moe.MoEDecode) over the node's T rows."""
         from .moe import MoEDecode
         x = self.buf[id(t.srcs[0])]
-        layer = MoEDecode(t.attrs["w"], t.attrs["cfg"], t.attrs["ls"], self.compress)
+        layer = self.cached(t, lambda: MoEDecode(t.attrs["w"], t.attrs["cfg"], t.attrs["ls"], self.compress))
         T = t.shape[0]
         bufs = layer._make_bufs(T)
         y = self.out(t)
@@ -467,6 +481,37 @@ class _Lowering:
 
 
 # ----------------------------------------------------------------------------- public API
+_VIEW_OPS = {"reshape"}
+_ELEMENTWISE_OPS = (set(_Lowering._UNARY) | _Lowering._BIN
+                    | {"select", "muls", "adds", "log", "rsqrt", "inverse", "clip"})
+
+
+def _in_place_safe(order, x: Tensor, y: Tensor) -> bool:
+    """Whether output y can be written into input x's buffer (Program.share_buffer aliasing) and still
+    give every op the values it reads: each op that reads x (or a reshape of it) runs before y's op,
+    or is y's own op, elementwise, reading x at y's shape (each element read before it is written)."""
+    if y.op in _VIEW_OPS or y.op == "input" or tuple(x.shape) != tuple(y.shape):
+        return False
+    views, grew = {id(x)}, True
+    while grew:
+        grew = False
+        for t in order:
+            if t.op in _VIEW_OPS and id(t) not in views and id(t.srcs[0]) in views:
+                views.add(id(t))
+                grew = True
+    pos = {id(t): i for i, t in enumerate(order)}
+    for t in order:
+        if t.op in _VIEW_OPS or t.op == "input":
+            continue
+        reads = [s for s in t.srcs if id(s) in views]
+        if not reads or pos[id(t)] < pos[id(y)]:
+            continue
+        if t is y and t.op in _ELEMENTWISE_OPS and all(tuple(s.shape) == tuple(t.shape) for s in reads):
+            continue
+        return False
+    return True
+
+
 def _build(outs, compress, compress_atol, block_size):
     if not torch.cuda.is_available():
         raise RuntimeError("aneforge_amd.compile needs an MI355X GPU (no CPU fallback)")
@@ -474,22 +519,40 @@ def _build(outs, compress, compress_atol, block_size):
     inputs = sorted((t for t in order if t.op == "input"), key=lambda t: t.attrs.get("idx", 0))
     if not inputs:
         raise ValueError("aneforge.compile: graph has no inputs")
+    order = inputs + [t for t in order if t.op != "input"]     # input buffers exist before any op
     for i, t in enumerate(order):
         t._name = f"t{i}"
-    low = _Lowering(compress, compress_atol, block_size)
-    low.lower(order)
+    by_name = {t._name: t for t in order}
+    cache: dict = {}
+
+    def lower(pairs, keep=None):
+        """Lower the graph; `pairs` (output port, input port) share one buffer; `keep` holds input
+        port buffers to reuse (what was already set into them stays)."""
+        alias = {id(by_name[o]): id(by_name[i]) for o, i in pairs}
+        preset = {id(t): keep[t._name] for t in inputs} if keep else None
+        low = _Lowering(compress, compress_atol, block_size, alias, cache, preset)
+        low.lower(order)
+        bufs = {t._name: low.buf[id(t)] for t in inputs}
+        for o in outs:
+            bufs[o._name] = low.buf[id(o)]
+        steps = low.steps
+
+        def plan():
+            for s in steps:
+                s()
+        return plan, bufs, low
+
+    plan, bufs, low = lower([])
     _fallback_signal(compress, compress_atol, low.stats)
-    bufs = {t._name: low.buf[id(t)] for t in inputs}
-    for o in outs:
-        bufs[o._name] = low.buf[id(o)]
-    steps = low.steps
-
-    def plan():
-        for s in steps:
-            s()
-
     prog = Program({t._name: t.shape for t in inputs}, {o._name: o.shape for o in outs}, plan, bufs)
     prog._keep = (low.keep, low.buf)
+
+    def relower(pairs):
+        plan, bufs, lw = lower(pairs, prog._buf)
+        prog._keep = (lw.keep, lw.buf)
+        return plan, bufs
+
+    prog._alias_hooks = (lambda o, i: _in_place_safe(order, by_name[i], by_name[o]), relower)
     return prog, inputs, order
 
 

@@ -5,9 +5,11 @@ over device buffers and a captured kernel sequence instead of an Espresso progra
   execute()              run once, synchronously (the reference's execute is synchronous)
   read_output(name)      a fresh fp16 host copy of an output port
   eval(feed)             set every fed input, execute, read every output
-  share_buffer(...)      alias an output onto an input: after each execute the output is
-                         copied device-to-device into the input port, so resident state
-                         (e.g. a KV cache) never leaves the GPU; must precede the first execute
+  share_buffer(...)      alias an output onto an input (must precede the first execute): the
+                         output is written into the input port's own buffer, so resident state
+                         (e.g. a KV cache) is updated in place and never copied; when an op
+                         would read the input after the output is written, the output is
+                         copied device-to-device into the input after each execute instead
   input_view/output_view the port's device tensor (zero-copy; the reference returns host
                          views of ANE-visible memory)
   release()              drop buffers and the captured graph"""
@@ -29,7 +31,9 @@ class Program:
         self._outputs = dict(outputs)
         self._plan = plan
         self._buf = buffers
-        self._shares: list[tuple[str, str]] = []
+        self._shares: list[tuple[str, str]] = []    # copied after each execute
+        self._aliases: list[tuple[str, str]] = []   # written in place
+        self._alias_hooks = None                    # (in-place check, re-lowering) from the compiler
         self._executed = False
         self._graph = None
         self.stream = torch.cuda.Stream()
@@ -67,7 +71,17 @@ class Program:
         dst = self._port(dst_in_port, self._inputs, "input")
         if tuple(src.shape) != tuple(dst.shape):
             raise RuntimeError(f"share_buffer({src_out_port}->{dst_in_port}): shapes {tuple(src.shape)} vs {tuple(dst.shape)}")
-        self._shares.append((src_out_port, dst_in_port))
+        if any(d == dst_in_port for _, d in self._shares + self._aliases):
+            raise RuntimeError(f"share_buffer: input {dst_in_port!r} is already shared")
+        if self._alias_hooks is not None and self._alias_hooks[0](src_out_port, dst_in_port):
+            self._aliases.append((src_out_port, dst_in_port))
+            self._plan, self._buf = self._alias_hooks[1](self._aliases)
+        else:
+            self._shares.append((src_out_port, dst_in_port))
+
+    def shared_in_place(self, out_port: str) -> bool:
+        """True when share_buffer aliased this output onto its input (no per-execute copy)."""
+        return any(o == out_port for o, _ in self._aliases)
 
     # -- execution --
     def _enqueue(self):

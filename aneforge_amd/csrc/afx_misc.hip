@@ -183,8 +183,30 @@ struct AdvanceArgs {
   int D, vocab;
 };
 
-__device__ __forceinline__ float4 shfl_xor_f4(float4 v, int m) {
-  return float4{__shfl_xor(v.x, m, 64), __shfl_xor(v.y, m, 64), __shfl_xor(v.z, m, 64), __shfl_xor(v.w, m, 64)};
+// One DPP step of a wavefront-wide top2_merge: lanes whose source lane is outside the pattern
+// read the neutral summary, so they keep their own.
+template <int CTRL, int RMASK>
+__device__ __forceinline__ float4 top2_dpp(float4 v) {
+  const int nx = __float_as_int(-INFINITY), ny = 0x7fffffff, nw = __float_as_int(0.0f);
+  float4 o;
+  o.x = __int_as_float(__builtin_amdgcn_update_dpp(nx, __float_as_int(v.x), CTRL, RMASK, 0xf, false));
+  o.y = __int_as_float(__builtin_amdgcn_update_dpp(ny, __float_as_int(v.y), CTRL, RMASK, 0xf, false));
+  o.z = __int_as_float(__builtin_amdgcn_update_dpp(nx, __float_as_int(v.z), CTRL, RMASK, 0xf, false));
+  o.w = __int_as_float(__builtin_amdgcn_update_dpp(nw, __float_as_int(v.w), CTRL, RMASK, 0xf, false));
+  return top2_merge(v, o);
+}
+// The wavefront's merged summary (row shifts, then row broadcasts into lane 63), wave-uniform.
+__device__ __forceinline__ float4 top2_wave(float4 v) {
+  v = top2_dpp<0x111, 0xf>(v);   // row_shr:1
+  v = top2_dpp<0x112, 0xf>(v);   // row_shr:2
+  v = top2_dpp<0x114, 0xf>(v);   // row_shr:4
+  v = top2_dpp<0x118, 0xf>(v);   // row_shr:8: lane 15 of each row holds the row's summary
+  v = top2_dpp<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+  v = top2_dpp<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the total
+  return float4{__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.x), 63)),
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.y), 63)),
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.z), 63)),
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.w), 63))};
 }
 
 __global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
@@ -195,7 +217,11 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
   __shared__ float4 top_all;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
   const float4 none = float4{-INFINITY, __int_as_float(0x7fffffff), -INFINITY, 0.0f};
-  // 1. the greedy summaries, loaded before the step counter is known (they do not depend on it)
+  // 1. every load that does not depend on the pick: the step state, the margin, the summaries
+  const int s = a.step[0];
+  const int p0 = a.pos[0];
+  const int nf = a.n_forced ? a.n_forced[0] : 0;
+  const float margin = a.margin ? a.margin[0] : 0.0f;
   float4 acc = none;
   if (a.slots) {
     const int ns = (a.V + 7) >> 3;
@@ -224,10 +250,8 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
       }
     }
   }
-  const int s = a.step[0];
-  const bool use_forced = a.forced && a.n_forced && s < a.n_forced[0];
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc = top2_merge(acc, shfl_xor_f4(acc, m));
+  const bool use_forced = a.forced && a.n_forced && s < nf;
+  acc = top2_wave(acc);
   if (lane == 0) wpart[wave] = acc;
   __syncthreads();
   if (t == 0) {
@@ -238,7 +262,7 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
     if (!use_forced && (a.logits || a.slots) && a.margin && a.logits && a.hn && (a.head16 || a.head32) &&
         __builtin_isfinite(top.x) && __builtin_isfinite(top.w)) {
       const double gap = (double)top.x - (double)top.z;
-      nt = gap < (double)a.margin[0] * ((double)top.w + 1e-9);
+      nt = gap < (double)margin * ((double)top.w + 1e-9);
     }
     near_tie = nt;
   }
@@ -247,7 +271,7 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
   if (near_tie) {
     // every logit within the window of the largest, recomputed exactly; one wavefront per candidate
     const float4 top = top_all;
-    const double lo = (double)top.x - (double)a.margin[0] * ((double)top.w + 1e-9);
+    const double lo = (double)top.x - (double)margin * ((double)top.w + 1e-9);
     double best = -INFINITY;
     int bi = 0x7fffffff;
     for (int base = wave * 64; base < a.V; base += nw * 64) {
@@ -290,7 +314,7 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
     a.tok[0] = bidx;
     if (s < a.hist_cap) a.hist[s] = bidx;
     a.step[0] = s + 1;
-    a.pos[0] = a.pos[0] + 1;
+    a.pos[0] = p0 + 1;
   }
   __syncthreads();
   if (a.embed) {

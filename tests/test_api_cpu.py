@@ -196,3 +196,15 @@ def test_gguf_roundtrip_and_view(tmp_path):
     assert c[0, 0] == -8.0 and c[1, 31] == 30.0
     assert g.quantized("a.weight") is None
     g.drop_pages()
+
+
+def test_reference_import_name_resolves_to_this_build():
+    # callers of the reference keep `import aneforge as af` and its module paths
+    import aneforge
+    import aneforge_amd
+    from aneforge.llm import LlamaPrefill as LP
+    from aneforge.moe import load_gguf
+    import aneforge._gguf as g
+    assert aneforge.compile is aneforge_amd.compile and aneforge.LlamaPrefill is aneforge_amd.LlamaPrefill
+    assert LP is aneforge_amd.llm.LlamaPrefill and load_gguf is aneforge_amd.moe.load_gguf
+    assert g.GGUFView is aneforge_amd.GGUFView and aneforge.sdpa is aneforge_amd.sdpa

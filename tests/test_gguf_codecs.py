@@ -277,3 +277,25 @@ def test_q8_0_tensors_stream_as_blockwise_codes(tmp_path):
         np.testing.assert_array_equal(w.dequant(), want)
     assert g.quantized("one").fmt == "blockwise"
     assert g.quantized("odd") is None                 # K = 96: not a multiple of 64, dequantised instead
+
+
+def test_q4_k_high_scale_bits_known_answer():
+    # The Q4_K 12-byte scale field written out byte by byte (not through an encoder): sub-blocks 4..7
+    # carry 6-bit scales and mins >= 16, whose top two bits sit in bits 6-7 of bytes 0..3 (scales) and
+    # 4..7 (mins) and whose low nibbles sit in bytes 8..11 (ggml get_scale_min_k4).
+    #   scales 1, 2, 3, 4, 17, 33, 50, 63; mins 5, 6, 7, 8, 48, 20, 31, 60
+    field = bytes([0x41, 0x82, 0xC3, 0xC4,     # scale_j | (scale_{j+4} >> 4) << 6
+                   0xC5, 0x46, 0x47, 0xC8,     # min_j | (min_{j+4} >> 4) << 6
+                   0x01, 0x41, 0xF2, 0xCF])    # (scale_{j+4} & 15) | (min_{j+4} & 15) << 4
+    blk = h16(1.0) + h16(0.5) + field + bytes([0x22] * 128)        # every code 2
+    # w[32j + l] = 1.0 * scale_j * 2 - 0.5 * min_j
+    want = np.repeat(np.array([-0.5, 1.0, 2.5, 4.0, 10.0, 56.0, 84.5, 96.0], F32), 32)
+    np.testing.assert_array_equal(decode("Q4_K", blk), want)
+    from oracle import ref
+    np.testing.assert_array_equal(ref.dequant_q4_k(np.frombuffer(blk, np.uint8).reshape(1, 144))[0], want)
+    # the device layout's unpacked header: per pair p the bytes {sc(2p), sc(2p+1), m(2p), m(2p+1)}
+    from aneforge_amd import _blob
+    _, hdr = _blob.q4_k_repack(np.frombuffer(blk, np.uint8).reshape(1, 144), 1, 256)
+    pairs = hdr.view(np.uint32)[0, 1:5]
+    got = [[int(w >> (8 * i)) & 255 for i in range(4)] for w in pairs]
+    assert got == [[1, 2, 5, 6], [3, 4, 7, 8], [17, 33, 48, 20], [50, 63, 31, 60]]

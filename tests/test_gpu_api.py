@@ -197,11 +197,34 @@ def test_compile_multi_share_buffer_keeps_state_resident():
     mm.prog.share_buffer(0, om[y], 0, inm[id(s)])
     mm.prog.set_input(inm[id(s)], np.zeros((1, 8), np.float16))
     mm.prog.set_input(inm[id(x)], np.full((1, 8), 0.5, np.float16))
+    assert mm.prog.shared_in_place(om[y])                       # y is written into s's buffer
+    assert mm.prog.output_view(om[y]).data_ptr() == mm.prog.input_view(inm[id(s)]).data_ptr()
     for _ in range(3):
         mm.prog.execute()
     assert np.allclose(mm.prog.read_output(om[y]).astype(np.float32), 1.5)
     with pytest.raises(RuntimeError):
         mm.prog.share_buffer(0, om[y], 0, inm[id(s)])      # only before the first execute
+
+
+def test_share_buffer_copies_when_in_place_would_change_a_result():
+    # z reads the state after y (the new state) is computed: an in-place y would hand z the new
+    # value, so the program keeps s and copies y into it after each execute
+    say("share_buffer hazard: copy fallback")
+    x, s = af.input((1, 8)), af.input((1, 8))
+    y = s + x
+    z = (s * 2.0) + y
+    mm = af.compile_multi([y, z])
+    inm = {id(t): n for t, n in mm.input_ports}
+    om = dict(mm.output_ports)
+    mm.prog.share_buffer(0, om[y], 0, inm[id(s)])
+    assert not mm.prog.shared_in_place(om[y])
+    mm.prog.set_input(inm[id(s)], np.full((1, 8), 1.0, np.float16))
+    mm.prog.set_input(inm[id(x)], np.full((1, 8), 0.5, np.float16))
+    for step in range(3):
+        mm.prog.execute()
+        sv = 1.0 + 0.5 * step                                   # the state this execute read
+        assert np.allclose(mm.prog.read_output(om[y]).astype(np.float32), sv + 0.5)
+        assert np.allclose(mm.prog.read_output(om[z]).astype(np.float32), 2 * sv + sv + 0.5)
 
 
 def _moe_model(E=8, k=2, D=128, F=128, layers=2, vocab=64, qk=False, seed=0, dh=32):

@@ -38,8 +38,8 @@ def _effective(w, compress):
             return W.astype(np.float16).astype(np.float32)
         if compress == "int8":
             return ref.dequant_w8(*_blob.quantize_per_row(W))
-        if compress == "q4_0":
-            return ref.dequant_q4_0(_blob.quantize_q4_0(W), *W.shape)
+        if compress == "q4_0":                       # the fp16 weights the kernels multiply with
+            return ref.dequant_q4_0_f16(_blob.quantize_q4_0(W), *W.shape)
         if compress == "blockwise":
             q, sc, bs = _blob.quantize_blockwise(W, 32)
             return ref.dequant_blockwise(q, sc, bs)

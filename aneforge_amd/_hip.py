@@ -35,7 +35,7 @@ SIGNATURES: dict[str, tuple] = {
     "afx_event_elapsed_ms": (_i, [_vp, _vp, _fp]),
     "afx_event_destroy": (_i, [_vp]),
     # weight-streaming linear layers
-    "afx_linear": (_i, [_i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp]),
+    "afx_linear": (_i, [_i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _ll, _vp]),
     "afx_linear_rms": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "afx_lm_head": (_i, [_i, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _vp, _vp, _vp]),
     "afx_linear_swiglu": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _i, _vp, _i, _i, _i, _i, _i, _vp]),
@@ -75,7 +75,7 @@ SIGNATURES: dict[str, tuple] = {
     # mixture of experts
     "afx_moe_topk": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "afx_moe_gateup": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
-    "afx_moe_down": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
+    "afx_moe_down": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _ll, _vp]),
     "afx_topk_mask": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     # batched prefill
     "afx_gemm": (_i, [_i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp]),

@@ -22,6 +22,10 @@ def stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+def _nbytes(t) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
+
+
 def P(t) -> int | None:
     if t is None:
         return None
@@ -42,9 +46,10 @@ def _f16(t, name):
 
 
 # --------------------------------------------------------------------------- linear layers
-def linear(fmt: str, w, scale, x, y=None, bias=None, residual=None, out_f32=False, rows_hint=0):
-    """y[M, N] = x[M, K] @ W^T (+bias) (+residual) for a packed weight (see _blob)."""
-    _dev(w, x, scale, bias, residual)
+def linear(fmt: str, w, scale, x, y=None, bias=None, residual=None, out_f32=False, rows_hint=0, ws=None):
+    """y[M, N] = x[M, K] @ W^T (+bias) (+residual) for a packed weight (see _blob).  ws: an optional
+    fp32 device workspace; 32 * M * N bytes let long rows take the K-split MFMA path."""
+    _dev(w, x, scale, bias, residual, ws)
     M, K = x.shape
     N = w.shape[0]
     if fmt in ("q4_0", "lut4", "q4_k", "q6_k") and w.shape[1] * 2 != K or fmt in ("int8", "blockwise") and w.shape[1] != K:
@@ -52,7 +57,7 @@ def linear(fmt: str, w, scale, x, y=None, bias=None, residual=None, out_f32=Fals
     if y is None:
         y = torch.empty((M, N), dtype=torch.float32 if out_f32 else torch.float16, device=x.device)
     _hip.call("afx_linear", FMT[fmt], P(w), P(scale), P(x), x.stride(0), P(y), y.stride(0), M, N, K,
-              P(bias), P(residual), int(out_f32), rows_hint, stream())
+              P(bias), P(residual), int(out_f32), rows_hint, P(ws), _nbytes(ws), stream())
     return y
 
 
@@ -381,11 +386,12 @@ def moe_gateup(fmt, w, scale, x, k, E, F, cnt, lst, act=None, rows_hint=0):
     return act
 
 
-def moe_down(fmt, w, scale, act, T, k, E, F, D, cnt, lst, y=None, rows_hint=0):
+def moe_down(fmt, w, scale, act, T, k, E, F, D, cnt, lst, y=None, rows_hint=0, ws=None):
+    """ws: optional fp32 workspace; 32 * T * k * D bytes let long expert rows split K."""
     if y is None:
         y = torch.empty((T * k, D), dtype=torch.float32, device=act.device)
     _hip.call("afx_moe_down", FMT[fmt], P(w), P(scale), P(act), T, k, E, F, D, P(cnt), P(lst), P(y),
-              rows_hint, stream())
+              rows_hint, P(ws), _nbytes(ws), stream())
     return y
 
 

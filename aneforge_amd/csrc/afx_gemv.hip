@@ -94,6 +94,7 @@ static int launch(int fmt, GemvArgs& a, int eg, int rows_hint, hipStream_t strea
     MfmaArgs m = {};
     m.w = a.w; m.scale = a.scale; m.x = a.x; m.ldx = a.ldx; m.y = a.y; m.ldy = a.ldy;
     m.bias = a.bias; m.resid = a.resid; m.M = a.M; m.N = a.N; m.K = a.K; m.epi = a.epi;
+    m.ws = a.ws; m.ws_bytes = a.ws_bytes;
     return mfma_launch(fmt, m, 1, stream, what);
   }
   // the vector kernels take up to 8 rows a launch; with a norm prologue, as many as fit the 64 KB of
@@ -190,13 +191,14 @@ extern "C" {
 // out_f32: 0 -> y fp16, 1 -> y fp32.  residual (fp16 [M][ldy], may alias y) adds in place.
 int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                int M, int N, int K, const void* bias, const void* residual, int out_f32,
-               int rows_hint, void* stream) {
+               int rows_hint, void* ws, long long ws_bytes, void* stream) {
   AFX_REQUIRE(fmt >= 0 && fmt <= 6, "afx_linear: unknown weight format %d", fmt);
   AFX_REQUIRE(!(residual && out_f32), "afx_linear: residual add needs an fp16 output");
   AFX_REQUIRE(ldy >= N, "afx_linear: ldy=%d < N=%d", ldy, N);
   GemvArgs a = base_args(w, scale, x, ldx, y, ldy, M, N, K, bias,
                          residual ? EPI_RESID : out_f32 ? EPI_F32 : EPI_F16);
   a.resid = (const half_t*)residual;
+  a.ws = (float*)ws; a.ws_bytes = ws ? ws_bytes : 0;
   return launch(fmt, a, EG_PLAIN, rows_hint, (hipStream_t)stream, "afx_linear");
 }
 

@@ -78,6 +78,8 @@ struct GemvArgs {
   float eps;
   int nq, nk;             // EG_QKV: number of q rows (H*dh) and k rows (KVH*dh); v rows follow
   int dh, rope;           // EG_QKV: head dim; rope on/off
+  float* ws;              // MFMA K-split partials (optional workspace, afx_linear)
+  long long ws_bytes;
   float* slots;           // EG_HEAD: per workgroup {top-1, its row (int bits), top-2, max |y|}
   half_t* hn_out;         // norm prologue: workgroup 0 also writes the fp16 normalised row here
 };

@@ -24,6 +24,9 @@ struct MfmaArgs {
   int epi;                 // EPI_F16 / EPI_RESID / EPI_F32 / EPI_SWIGLU (gemv epilogue codes)
   int xbytes;              // set by mfma_launch: bytes of the activation rows the kernel may read
   int E;                   // set by mfma_launch: experts (1 for a dense linear)
+  float* ws;               // optional fp32 workspace for K-split partials (null: no split)
+  long long ws_bytes;
+  int ks, ws_rows;         // set by mfma_launch: K slices, output rows per slice in ws
 };
 
 // Launch the MFMA kernel over E experts (1 for a dense linear).  Returns 0 or a negative code.

@@ -44,6 +44,7 @@ template <> struct MfmaFmt<FMT_F16> { static constexpr int kK = 32, kMfma = 1; }
 template <> struct MfmaFmt<FMT_BW> { static constexpr int kK = 64, kMfma = 2; };
 
 constexpr int kSPB = 4;            // steps per batch: 16 rows x 256 bytes
+constexpr int kMaxSlices = 8;      // K slices of the split persistent kernel (workspace: 32 B per output)
 constexpr int kPxMaxExperts = 2056; // experts the persistent kernel's LDS list holds (the reference allows 2049)
 constexpr int kWRow = 256 + 16;    // LDS bytes per staged weight row
 constexpr int kSRow = 40;          // LDS bytes per staged Q4_0 scale row (4 superblocks x 8 B, padded)
@@ -293,7 +294,12 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
 // alternate between two LDS buffers: one barrier per tile (wavefront 0 reads tile i's buffer
 // before it reaches the barrier of tile i + 1; the other wavefronts write that buffer again
 // only for tile i + 2, after that barrier).
-template <int FMT, int EG, int NW, int PD, bool MOE>
+// SPLIT: K is cut into a.ks slices (long rows: the x slice of a whole row would not fit the
+// registers), a unit is (expert, slice, tile), and each unit's wavefront-summed tile goes to the
+// fp32 workspace a.ws[slice][row][column] (int8 row scale applied, nothing else); units of one
+// (expert, slice) are contiguous, so x is reloaded only where that pair changes.  A finishing
+// launch sums the slices and applies the epilogue (mfma_finish_kernel).
+template <int FMT, int EG, int NW, int PD, bool MOE, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   constexpr int KS = MfmaFmt<FMT>::kK, NM = MfmaFmt<FMT>::kMfma;
   constexpr int kSPS = FMT == FMT_Q4 ? 4 : 2;     // block scales per step (Q4_0, blockwise)
@@ -309,7 +315,13 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   const size_t rowbytes = Fmt<FMT>::row_bytes(K);
   const unsigned char* wbase = (const unsigned char*)a.w;
   const int nsteps = K / KS;
-  const int s0 = nsteps * wave / NW, nsw = nsteps * (wave + 1) / NW - s0;   // 1 .. kSPB steps
+  const int S = SPLIT ? a.ks : 1;                  // K slices
+  // this wavefront's steps of slice q: [s0, s0 + nsw), 1 .. kSPB of them
+  auto wrange = [&](int q, int& s0, int& nsw) {
+    const int lo = nsteps * q / S, len = nsteps * (q + 1) / S - lo;
+    s0 = lo + len * wave / NW;
+    nsw = lo + len * (wave + 1) / NW - s0;
+  };
   unsigned char* wls = wl[wave];
   unsigned char* sls = sl[wave];
 
@@ -325,6 +337,12 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   __shared__ int act_e[MOE ? kPxMaxExperts : 1];
   __shared__ int wcnt[NW];
   int v = blockIdx.x, vend = ntiles, vstep = G;
+  if constexpr (SPLIT && !MOE) {                   // contiguous ranges of the (slice, tile) units
+    const long long U = (long long)S * ntiles;
+    v = (int)(U * blockIdx.x / G);
+    vend = (int)(U * (blockIdx.x + 1) / G);
+    vstep = 1;
+  }
   if constexpr (MOE) {
     int nact = 0;
     for (int base = 0; base < a.E; base += NW * 64) {
@@ -343,29 +361,27 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
       nact += tot;
       __syncthreads();                             // wcnt is rewritten next round; act_e is complete
     }
-    const long long U = (long long)nact * ntiles;
+    const long long U = (long long)nact * S * ntiles;
     v = (int)(U * blockIdx.x / G);
     vend = (int)(U * (blockIdx.x + 1) / G);
     vstep = 1;
   }
   if (v >= vend) return;                           // whole workgroup, after its last barrier
-  auto unit = [&](int u, int& e, int& tile) {
-    if constexpr (MOE) {
-      e = act_e[u / ntiles];
-      tile = u % ntiles;
-    } else {
-      e = 0;
-      tile = u;
-    }
+  auto unit = [&](int u, int& e, int& q, int& tile) {
+    tile = u % ntiles;
+    q = SPLIT ? (u / ntiles) % S : 0;
+    e = MOE ? act_e[u / (ntiles * S)] : 0;
   };
 
   // this wavefront's slice of x in the B-operand layout (token column r, k slot g), for the
   // expert xe (MoE: column r is entry r of the expert's list; dense: activation row r)
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, a.xbytes);
   bool tok_ok = false;
-  int yr = r, xe = -1;
+  int yr = r, xe = -1;                             // xe: expert * S + slice of the x slice held
   u4 xv[kSPB][NM];
-  auto load_x = [&](int e) {
+  auto load_x = [&](int e, int q) {
+    int s0, nsw;
+    wrange(q, s0, nsw);
     int xr = r;
     tok_ok = r < a.M;
     if constexpr (MOE) {
@@ -388,13 +404,15 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
         xv[t][j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xrs, t < nsw ? xoff + kx * 2 : kOOB, 0, 0));
       }
     }
-    xe = e;
+    xe = e * S + q;
   };
 
   // One tile's weights for this wavefront's steps: 16 rows x 256 bytes, row-contiguous (chunks
   // past this wavefront's range belong to the next one: loaded, never used; clamped at the row
   // end), and the steps' block scales (lane l: row l / 4, step s0 + l % 4).
-  auto load_tile = [&](int e, int tile, u4 (&wq)[4], u2& sq) {
+  auto load_tile = [&](int e, int q, int tile, u4 (&wq)[4], u2& sq) {
+    int s0, nsw;
+    wrange(q, s0, nsw);
     const unsigned char* wb = wbase + (size_t)e * a.w_es;
     const int n0 = tile * 16;
     int c = s0 * 4 + lc;
@@ -413,15 +431,18 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
       else sq = (u2){*(const uint32_t*)sp, 0u};
     }
   };
-  auto compute_tile = [&](int e, int tile, const u4 (&wq)[4], const u2& sq, f4 (&rd)[NW][64]) {
-    if constexpr (MOE) {
-      // the next expert's rows; the full wait keeps these loads from leaving the compiler's
-      // wait counts (in-order, shared with the prefetched tiles) pending past the branch
-      if (e != xe) {
-        load_x(e);
+  auto compute_tile = [&](int e, int q, int tile, const u4 (&wq)[4], const u2& sq, f4 (&rd)[NW][64]) {
+    if constexpr (MOE || SPLIT) {
+      // the next expert's (or slice's) rows; the full wait keeps these loads from leaving the
+      // compiler's wait counts (in-order, shared with the prefetched tiles) pending past the branch
+      if (e * S + q != xe) {
+        load_x(e, q);
         __builtin_amdgcn_s_waitcnt(0);
       }
     }
+    int s0, nsw;
+    wrange(q, s0, nsw);
+    (void)s0;
     wave_sync_lds();                               // the previous tile's staged reads are done
 #pragma unroll
     for (int h = 0; h < 4; ++h) *(u4*)(wls + (4 * h + lr) * kWRow + lc * 16) = wq[h];
@@ -457,7 +478,18 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] += p[i];
       }
-      mfma_store<FMT, EG>(a, a.scale + (size_t)e * a.s_es, v, tile * 16 + 4 * g, tok_ok, yr);
+      const int rb = tile * 16 + 4 * g;
+      if constexpr (SPLIT) {
+        if constexpr (FMT == FMT_I8) {
+          const u2 sv = *(const u2*)(a.scale + (size_t)e * a.s_es + (rb < N ? rb : 0));
+          const h2 s01 = as_h2(sv.x), s23 = as_h2(sv.y);
+          v[0] *= (float)s01.x; v[1] *= (float)s01.y; v[2] *= (float)s23.x; v[3] *= (float)s23.y;
+        }
+        if (tok_ok && rb < N)
+          *(f4*)(a.ws + ((size_t)q * a.ws_rows + yr) * N + rb) = (f4){v[0], v[1], v[2], v[3]};
+      } else {
+        mfma_store<FMT, EG>(a, a.scale + (size_t)e * a.s_es, v, rb, tok_ok, yr);
+      }
     }
   };
 
@@ -468,22 +500,23 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   constexpr int NBUF = PD + 1;
   u4 wq[NBUF][4];
   u2 sq[NBUF];
-  int eu[NBUF], tu[NBUF];
+  int eu[NBUF], qu[NBUF], tu[NBUF];
 #pragma unroll
   for (int b = 0; b < NBUF; ++b) {
     sq[b] = (u2){0u, 0u};
     eu[b] = 0;
+    qu[b] = 0;
     tu[b] = 0;
   }
-  unit(v, eu[0], tu[0]);
-  load_x(eu[0]);
-  load_tile(eu[0], tu[0], wq[0], sq[0]);
+  unit(v, eu[0], qu[0], tu[0]);
+  load_x(eu[0], qu[0]);
+  load_tile(eu[0], qu[0], tu[0], wq[0], sq[0]);
 #pragma unroll
   for (int b = 1; b < PD; ++b) {
     const int vb = v + b * vstep;
     if (vb < vend) {
-      unit(vb, eu[b], tu[b]);
-      load_tile(eu[b], tu[b], wq[b], sq[b]);
+      unit(vb, eu[b], qu[b], tu[b]);
+      load_tile(eu[b], qu[b], tu[b], wq[b], sq[b]);
     }
   }
   int i = 0;                                       // units computed so far
@@ -495,11 +528,12 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
       const int vi = v + i * vstep;
       const int vp = vi + PD * vstep;              // prefetch unit i + PD into buffer (b + PD) % NBUF
       if (vp < vend) {
-        unit(vp, eu[(b + PD) % NBUF], tu[(b + PD) % NBUF]);
-        load_tile(eu[(b + PD) % NBUF], tu[(b + PD) % NBUF], wq[(b + PD) % NBUF], sq[(b + PD) % NBUF]);
+        const int bp = (b + PD) % NBUF;
+        unit(vp, eu[bp], qu[bp], tu[bp]);
+        load_tile(eu[bp], qu[bp], tu[bp], wq[bp], sq[bp]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      compute_tile(eu[b], tu[b], wq[b], sq[b], red[i & 1]);
+      compute_tile(eu[b], qu[b], tu[b], wq[b], sq[b], red[i & 1]);
       ++i;
       more = vi + vstep < vend;
     }
@@ -528,28 +562,50 @@ static mfma_fn pick_mfma(int fmt, bool swiglu, int nw, int nb) {
   return swiglu ? pick_mfma_w<FMT_F16, EG_SWIGLU>(nw, nb) : pick_mfma_w<FMT_F16, EG_PLAIN>(nw, nb);
 }
 
-template <int FMT, int EG, int PD, bool MOE>
+template <int FMT, int EG, int PD, bool MOE, bool SPLIT>
 static mfma_fn pick_mfma_px_w(int nw) {
   if constexpr (FMT == FMT_Q4)   // Q4_0 never takes 16 wavefronts (its x slice would not fit 128 VGPRs)
-    return nw == 4 ? mfma_px_kernel<FMT, EG, 4, PD, MOE> : mfma_px_kernel<FMT, EG, 8, PD, MOE>;
+    return nw == 4 ? mfma_px_kernel<FMT, EG, 4, PD, MOE, SPLIT> : mfma_px_kernel<FMT, EG, 8, PD, MOE, SPLIT>;
+  else if constexpr (SPLIT)      // the split launch takes at most 8 wavefronts
+    return nw == 4 ? mfma_px_kernel<FMT, EG, 4, PD, MOE, SPLIT> : mfma_px_kernel<FMT, EG, 8, PD, MOE, SPLIT>;
   else   // 16 wavefronts keep one unit of prefetch: three would spill at the 128-VGPR cap
-    return nw == 4 ? mfma_px_kernel<FMT, EG, 4, PD, MOE>
-         : nw == 8 ? mfma_px_kernel<FMT, EG, 8, PD, MOE> : mfma_px_kernel<FMT, EG, 16, 1, MOE>;
+    return nw == 4 ? mfma_px_kernel<FMT, EG, 4, PD, MOE, SPLIT>
+         : nw == 8 ? mfma_px_kernel<FMT, EG, 8, PD, MOE, SPLIT> : mfma_px_kernel<FMT, EG, 16, 1, MOE, SPLIT>;
 }
 template <int FMT, bool MOE>
-static mfma_fn pick_mfma_px_f(bool swiglu, int nw, int pd) {
-  if (pd == 3) return swiglu ? pick_mfma_px_w<FMT, EG_SWIGLU, 3, MOE>(nw) : pick_mfma_px_w<FMT, EG_PLAIN, 3, MOE>(nw);
-  return swiglu ? pick_mfma_px_w<FMT, EG_SWIGLU, 1, MOE>(nw) : pick_mfma_px_w<FMT, EG_PLAIN, 1, MOE>(nw);
+static mfma_fn pick_mfma_px_f(bool swiglu, int nw, int pd, bool split) {
+  if (split)                     // the epilogue runs in the finishing launch
+    return pd == 3 ? pick_mfma_px_w<FMT, EG_PLAIN, 3, MOE, true>(nw) : pick_mfma_px_w<FMT, EG_PLAIN, 1, MOE, true>(nw);
+  if (pd == 3)
+    return swiglu ? pick_mfma_px_w<FMT, EG_SWIGLU, 3, MOE, false>(nw) : pick_mfma_px_w<FMT, EG_PLAIN, 3, MOE, false>(nw);
+  return swiglu ? pick_mfma_px_w<FMT, EG_SWIGLU, 1, MOE, false>(nw) : pick_mfma_px_w<FMT, EG_PLAIN, 1, MOE, false>(nw);
 }
 template <bool MOE>
-static mfma_fn pick_mfma_px_m(int fmt, bool swiglu, int nw, int pd) {
-  if (fmt == FMT_I8) return pick_mfma_px_f<FMT_I8, MOE>(swiglu, nw, pd);
-  if (fmt == FMT_BW) return pick_mfma_px_f<FMT_BW, MOE>(swiglu, nw, pd);
-  if (fmt == FMT_Q4) return pick_mfma_px_f<FMT_Q4, MOE>(swiglu, nw, pd);
-  return pick_mfma_px_f<FMT_F16, MOE>(swiglu, nw, pd);
+static mfma_fn pick_mfma_px_m(int fmt, bool swiglu, int nw, int pd, bool split) {
+  if (fmt == FMT_I8) return pick_mfma_px_f<FMT_I8, MOE>(swiglu, nw, pd, split);
+  if (fmt == FMT_BW) return pick_mfma_px_f<FMT_BW, MOE>(swiglu, nw, pd, split);
+  if (fmt == FMT_Q4) return pick_mfma_px_f<FMT_Q4, MOE>(swiglu, nw, pd, split);
+  return pick_mfma_px_f<FMT_F16, MOE>(swiglu, nw, pd, split);
 }
-static mfma_fn pick_mfma_px(int fmt, bool swiglu, int nw, int pd, bool moe) {
-  return moe ? pick_mfma_px_m<true>(fmt, swiglu, nw, pd) : pick_mfma_px_m<false>(fmt, swiglu, nw, pd);
+static mfma_fn pick_mfma_px(int fmt, bool swiglu, int nw, int pd, bool moe, bool split) {
+  return moe ? pick_mfma_px_m<true>(fmt, swiglu, nw, pd, split) : pick_mfma_px_m<false>(fmt, swiglu, nw, pd, split);
+}
+
+// The K-split launch's second half: y[row][n] = epilogue(sum over the slices of ws[slice][row][n])
+// (bias, residual, fp32 or fp16 store; the int8 row scale was applied per slice), four columns per
+// thread.  The SwiGLU epilogue never splits (its gate/up rows are short in every model here).
+__global__ __launch_bounds__(256) void mfma_finish_kernel(MfmaArgs a, int rows) {
+  const int per_row = a.N >> 2;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * per_row) return;
+  const int yr = idx / per_row, rb = 4 * (idx - yr * per_row);
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int q = 0; q < a.ks; ++q) {
+    const f4 p = *(const f4*)(a.ws + ((size_t)q * a.ws_rows + yr) * a.N + rb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] += p[i];
+  }
+  mfma_store<FMT_F16, EG_PLAIN>(a, nullptr, v, rb, true, yr);
 }
 
 static int mfma_cus() {
@@ -599,8 +655,10 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
   // Persistent variant (dense <= 16 rows, MoE <= 16 tokens): the most wavefronts (up to 8 for
   // Q4_0, whose x slice takes 64 VGPRs, else 16) that leave each one a single batch;
   // AFX_MFMA_PX=0 disables it, AFX_MFMA_PX_WAVES=4|8|16 caps the wavefronts.
-  static int px_env = -2, px_waves = 0, px_depth = 0;
+  static int px_env = -2, px_waves = 0, px_depth = 0, px_split = 0;
   if (px_env == -2) {
+    const char* s = getenv("AFX_MFMA_SPLIT");
+    px_split = s ? atoi(s) : 0;
     const char* e = getenv("AFX_MFMA_PX");
     px_env = e ? atoi(e) : 1;
     const char* w = getenv("AFX_MFMA_PX_WAVES");
@@ -614,17 +672,41 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
     int pw = 0;
     for (int w = cap; w >= 4; w >>= 1)
       if (nsteps >= w && (nsteps + w - 1) / w <= kSPB) { pw = w; break; }
+    int S = 1;
+    const long long rows = a.cnt ? (long long)a.T * a.k : a.M;
+    if (!pw && a.ws && !swiglu && (fmt != FMT_Q4 || a.cnt)) {
+      // K slices (2 .. 8) that leave every wavefront one batch, if the workspace holds them; at
+      // most 8 wavefronts (16 would spill at their 128-VGPR cap with the slice bookkeeping).
+      // Measured on MI355X against the tile kernel: int8 / blockwise 4096 x 11008..14336 at 4..16
+      // rows take 17-23 us instead of 21-45, the Q4_0 experts of a 14336-long MoE down ~15%
+      // less; a dense Q4_0 4096 x 11008 takes 15 us instead of 12.4, so it keeps the tile kernel.
+      const int scap = cap < 8 ? cap : 8;
+      for (int s = 2; s <= kMaxSlices && !pw; ++s) {
+        const int lmin = nsteps / s, lmax = (nsteps + s - 1) / s;
+        if ((long long)s * rows * a.N * 4 > a.ws_bytes) break;
+        if (px_split >= 2 && s != px_split) continue;     // AFX_MFMA_SPLIT=2..8: tuning override
+        for (int w = scap; w >= 4; w >>= 1)
+          if (lmin >= w && (lmax + w - 1) / w <= kSPB) { pw = w; S = s; break; }
+      }
+    }
     if (pw) {
+      b.ks = S;
+      b.ws_rows = (int)rows;
       const int ntiles = (a.N + 15) / 16;
-      const long long units = (long long)ntiles * E;   // MoE: units of empty experts are skipped
+      const long long units = (long long)ntiles * E * S;   // MoE: units of empty experts are skipped
       const int grid = units < mfma_cus() ? (int)units : mfma_cus();
       // prefetch depth: three units ahead for long runs of units per workgroup, else one;
       // AFX_MFMA_PX_DEPTH=1|3 overrides
       int pd = (units + grid - 1) / grid >= 6 ? 3 : 1;
       if (px_depth == 1 || px_depth == 3) pd = px_depth;
       if (pw == 16) pd = 1;
-      mfma_fn fn = pick_mfma_px(fmt, swiglu, pw, pd, a.cnt != nullptr);
+      mfma_fn fn = pick_mfma_px(fmt, swiglu, pw, pd, a.cnt != nullptr, S > 1);
       hipLaunchKernelGGL(fn, dim3(grid), dim3(pw * 64), 0, stream, b);
+      if (S == 1) return check_launch(what);
+      int rc = check_launch(what);
+      if (rc) return rc;
+      const long long n = rows * (a.N / 4);
+      hipLaunchKernelGGL(mfma_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, b, (int)rows);
       return check_launch(what);
     }
   }

@@ -337,13 +337,15 @@ int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int
 
 // W: [E][D][F], act: [T*k][F] -> y: [T*k][D] fp32.
 int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F, int D,
-                 const int* cnt, const int* list, float* y, int rows_hint, void* stream) {
+                 const int* cnt, const int* list, float* y, int rows_hint, void* ws, long long ws_bytes,
+                 void* stream) {
   if (rows_hint == 0 && mfma_supported(fmt, F) && D % 4 == 0) {
     MfmaArgs m = {};
     m.w = w; m.scale = (const half_t*)scale; m.x = (const half_t*)act; m.ldx = F; m.y = y; m.ldy = D;
     m.cnt = cnt; m.list = list; m.T = T; m.k = k; m.x_by_token = 0; m.N = D; m.K = F; m.epi = EPI_F32;
     m.w_es = fmt_row_bytes(fmt, F) * D;
     m.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? (long long)D * (F / 32) : fmt == FMT_I8 ? (long long)D : 0;
+    m.ws = (float*)ws; m.ws_bytes = ws ? ws_bytes : 0;
     AFX_REQUIRE(T >= 1 && k >= 1 && E >= 1, "afx_moe_down: bad sizes");
     return mfma_launch(fmt, m, E, (hipStream_t)stream, "afx_moe_down");
   }

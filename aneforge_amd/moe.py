@@ -122,6 +122,8 @@ class MoEDecode:
             "list": torch.empty((E, B), dtype=torch.int32, device=dev),
             "act": torch.empty((B * k, F), dtype=torch.float16, device=dev),
             "y": torch.empty((B * k, D), dtype=torch.float32, device=dev),
+            # K-split partials of the expert down projection (long expert rows)
+            "ws": torch.empty(8 * B * k * D, dtype=torch.float32, device=dev),
         }
         if self.shared:
             Fs = self.sh_gu.N // 2
@@ -148,7 +150,7 @@ class MoEDecode:
         K.moe_gateup(self.gu.fmt, self.gu.w, self.gu.scale, b["hn"][:T], self.k, self.E, self.F, b["cnt"],
                      b["list"], act=b["act"][:T * self.k])
         K.moe_down(self.down.fmt, self.down.w, self.down.scale, b["act"][:T * self.k], T, self.k, self.E,
-                   self.F, self.D, b["cnt"], b["list"], y=b["y"][:T * self.k])
+                   self.F, self.D, b["cnt"], b["list"], y=b["y"][:T * self.k], ws=b["ws"])
         shared = None
         if self.shared:
             K.linear_swiglu(self.sh_gu.fmt, self.sh_gu.w, self.sh_gu.scale, b["hn"][:T], act=b["sh_act"][:T])

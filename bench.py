@@ -194,7 +194,8 @@ def bench_gemv_q4(args, N=11008, Kd=4096):
     ds = [(torch.rand((N, Kd // 32), device="cuda", generator=g) * 0.005).half() for _ in range(copies)]
     x = torch.randn((B, Kd), device="cuda", generator=g).half()
     y = torch.empty((B, N), dtype=torch.float16, device="cuda")
-    gr = Graph(lambda: [K.linear("q4_0", qs[i], ds[i], x, y=y, rows_hint=args.rows_hint) for i in range(copies)])
+    ws = torch.empty(8 * B * N, dtype=torch.float32, device="cuda")    # K-split partials (long rows)
+    gr = Graph(lambda: [K.linear("q4_0", qs[i], ds[i], x, y=y, rows_hint=args.rows_hint, ws=ws) for i in range(copies)])
     for _ in range(3):
         gr.launch()
     ms = gr.time_ms(max(1, args.steps // 8)) / copies
@@ -254,6 +255,7 @@ def bench_moe(args):
     lst = torch.empty((E, T), dtype=torch.int32, device="cuda")
     act = torch.empty((T * k, F), dtype=torch.float16, device="cuda")
     y = torch.empty((T * k, D), dtype=torch.float32, device="cuda")
+    ws = torch.empty(8 * T * k * D, dtype=torch.float32, device="cuda")   # K-split partials of the down
 
     def layer():
         K.rmsnorm(h, gamma, 1e-5, y=hn)
@@ -261,7 +263,7 @@ def bench_moe(args):
             K.linear("fp16", router, None, hn[r0:r0 + 8], y=logits[r0:r0 + 8], out_f32=True)
         K.moe_topk(logits, k, True, gate, sel, cnt, lst)
         K.moe_gateup("q4_0", gu_w, gu_d, hn, k, E, F, cnt, lst, act=act)
-        K.moe_down("q4_0", dn_w, dn_d, act, T, k, E, F, D, cnt, lst, y=y)
+        K.moe_down("q4_0", dn_w, dn_d, act, T, k, E, F, D, cnt, lst, y=y, ws=ws)
         K.moe_combine(h, y, gate, out=hout)
 
     layer()

@@ -53,6 +53,12 @@ int afx_event_destroy(void* ev);
 
 /* y[M][N] = x[M][K] @ W^T (+bias) (+residual, may alias y); out_f32 selects fp32 y.  Any M:
  * 4+ rows without a norm prologue run on MFMA, otherwise the vector kernels take 8 rows a launch.
+ * ws (optional, device, may be NULL): an fp32 workspace of ws_bytes; with up to 32 * M * N bytes,
+ * int8 / blockwise / fp16 rows too long for one pass of the persistent MFMA kernel (K above 4096
+ * int8, 2048 fp16, at 16 or fewer rows) are cut into up to 8 K slices (as many as the workspace
+ * holds at 4 * M * N bytes each) whose partials meet there, then a second launch sums them.  Dense
+ * Q4_0 is measured faster unsplit and ignores ws.  Results differ from the single-pass kernels only
+ * in fp32 summation order.
  * fmt 0: the compress="int8" linear, constexpr_affine_dequantize(axis=0) + matmul
  * (aneforge/_compile.py:171-179, 375-385; aneforge/graph.py:187-195); 1: the GGUF Q4_0 weights
  * the reference dequantises on the host and casts to fp16 (aneforge/_gguf.py:34-39), weight
@@ -67,7 +73,7 @@ int afx_event_destroy(void* ev);
  * 6: GGUF Q6_K after afx_q6_k_repack, weight fp16(d*sc * (q - 32)) (the same reference path). */
 int afx_linear(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy,
                int M, int N, int K, const void* bias, const void* residual, int out_f32,
-               int rows_hint, void* stream);
+               int rows_hint, void* ws, long long ws_bytes, void* stream);
 /* y = rms_norm(x, gamma, eps) @ W^T (+bias): RMSNorm (aneforge/graph.py:293-301,
  * aneforge/_compile.py:738-755) fused as the GEMV prologue. */
 int afx_linear_rms(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
@@ -206,9 +212,12 @@ int afx_moe_topk(const float* logits, int T, int E, int k, int renorm, float* ga
 /* active experts only: silu(x Wg_e^T) * (x Wu_e^T) (_experts_gate, moe.py:40-45, :57) */
 int afx_moe_gateup(int fmt, const void* w, const void* scale, const void* x, int T, int k, int E, int F, int D,
                    const int* cnt, const int* list, void* act, int rows_hint, void* stream);
-/* active experts only: act @ Wd_e (bmm_weight, moe.py:58) */
+/* active experts only: act @ Wd_e (bmm_weight, moe.py:58).  ws (optional, may be NULL): an fp32
+ * workspace; with up to 32 * T * k * D bytes, long expert rows are cut into up to 8 K slices, as for
+ * afx_linear. */
 int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F, int D,
-                 const int* cnt, const int* list, float* y, int rows_hint, void* stream);
+                 const int* cnt, const int* list, float* y, int rows_hint, void* ws, long long ws_bytes,
+                 void* stream);
 /* The graph form of the top-k gate (_topk_gate, aneforge/moe.py:21-37): y = x on the k experts each
  * row of fp16 probabilities x [T][E] keeps (k rounds of the row maximum, the lowest index among exact
  * fp16 ties), 0 elsewhere; 1 <= k <= E <= 2049. */

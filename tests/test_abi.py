@@ -46,7 +46,7 @@ def test_errors_surface_as_runtime_error_without_a_gpu():
     import pytest
     from aneforge_amd import _hip
     with pytest.raises(RuntimeError, match="unknown weight format"):
-        _hip.call("afx_linear", 7, None, None, None, 8, None, 8, 1, 8, 8, None, None, 0, 0, None)
+        _hip.call("afx_linear", 7, None, None, None, 8, None, 8, 1, 8, 8, None, None, 0, 0, None, 0, None)
     with pytest.raises(RuntimeError, match="need 1 <= k <= E"):
         # non-null dummy addresses: validation rejects k before anything is dereferenced
         _hip.call("afx_moe_topk", 256, 1, 8, 9, 1, 256, 256, 256, 256, None)

@@ -115,3 +115,63 @@ def test_moe_skinny_sweep(seed):
                 g, u = ref.linear(x[t:t + 1], G[e]), ref.linear(x[t:t + 1], U[e])
                 assert _bad(a[ent:ent + 1], ref.r16(ref.silu(g) * u)) == 0, f"gate/up token {t} expert {e}"
                 assert _bad(y[ent:ent + 1], ref.linear(a[ent:ent + 1], Dn[e], exact=True)) == 0, f"down token {t} expert {e}"
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4_0", "blockwise"])
+def test_dense_split_k(fmt):
+    """Long rows (K = 11008, 14336: the cfg1 down projection and longer) with a workspace take the
+    K-split persistent kernel (partials in the workspace, a finishing launch for the epilogue);
+    without one they take the tile kernel.  Both meet the oracle bar, for every epilogue."""
+    from aneforge_amd import _kernels as K
+    rng = np.random.default_rng(301)
+    for Kd in (11008, 14336):
+        N = 1044                       # a partial last tile of 16 rows
+        w, s, W = _weights(rng, fmt, N, Kd)
+        wd, sd = dev(w), dev(s)
+        for M in (4, 8, 13, 16):
+            say(f"split-K: dense {fmt} M={M} N={N} K={Kd}")
+            x = rng.standard_normal((M, Kd)).astype(np.float16)
+            b = (rng.standard_normal(N) * 0.1).astype(np.float16)
+            r = rng.standard_normal((M, N)).astype(np.float16)
+            ws = torch.full((8 * M * N,), float("nan"), dtype=torch.float32, device="cuda")   # stale contents
+            want = ref.linear(x, W)
+            assert _bad(host(K.linear(fmt, wd, sd, dev(x), ws=ws)), want) == 0, "plain, split"
+            assert _bad(host(K.linear(fmt, wd, sd, dev(x))), want) == 0, "plain, no workspace"
+            got = host(K.linear(fmt, wd, sd, dev(x), bias=dev(b), residual=dev(r), ws=ws))
+            assert _bad(got, ref.r16(r.astype(np.float64) + ref.linear(x, W, b)), hidden=True) == 0, "bias + residual"
+            got = host(K.linear(fmt, wd, sd, dev(x), out_f32=True, ws=ws))
+            assert _bad(got, ref.linear(x, W, exact=True)) == 0, "fp32 out"
+            small = torch.empty(2 * M * N - 1, dtype=torch.float32, device="cuda")   # too small to split
+            assert _bad(host(K.linear(fmt, wd, sd, dev(x), ws=small)), want) == 0, "workspace too small"
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4_0"])
+def test_moe_down_split_k(fmt):
+    """The expert down projection over long expert rows (F = 14336, the cfg4 experts) with a
+    workspace: K-split units (expert, slice, tile); experts left unrouted; T up to 16 tokens."""
+    from aneforge_amd import _kernels as K
+    rng = np.random.default_rng(302)
+    E, F, D = 6, 14336, 512
+    wdn, sdn, Dn = [], [], []
+    for e in range(E):
+        q, s_, W = _weights(rng, fmt, D, F)
+        wdn.append(q); sdn.append(s_); Dn.append(W)
+    wd, sd = dev(np.stack(wdn)), dev(np.stack(sdn))
+    for T, k in ((1, 2), (4, 2), (16, 2), (9, 3)):
+        say(f"split-K: moe down {fmt} E={E} k={k} T={T} D={D} F={F}")
+        pick = [rng.choice(E - 1, k, replace=False) for _ in range(T)]     # expert E-1 never routed
+        cnt = np.zeros(E, np.int32)
+        lst = np.zeros((E, T), np.int32)
+        for t in range(T):
+            for sl, e in enumerate(pick[t]):
+                lst[e, cnt[e]] = t * k + sl
+                cnt[e] += 1
+        a = (rng.standard_normal((T * k, F)) * 0.5).astype(np.float16)
+        ws = torch.full((8 * T * k * D,), float("nan"), dtype=torch.float32, device="cuda")
+        for w_ in (ws, None):
+            y = host(K.moe_down(fmt, wd, sd, dev(a), T, k, E, F, D, dev(cnt), dev(lst), ws=w_))
+            for t in range(T):
+                for sl, e in enumerate(pick[t]):
+                    ent = t * k + sl
+                    assert _bad(y[ent:ent + 1], ref.linear(a[ent:ent + 1], Dn[e], exact=True)) == 0, \
+                        f"token {t} expert {e} workspace={w_ is not None}"

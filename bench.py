@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--out", default=None, help="also append the JSON line to this file")
     ap.add_argument("--rows-hint", type=int, default=0)
     ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--shape", default="11008x4096", choices=["11008x4096", "4096x11008"],
+                    help="N x K of the cfg1 Q4_0 matrix for --workload gemv_q4")
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--weights", default="int8", choices=["int8", "q4_0", "blockwise", "lut4", "q4_k"],
                     help="linear weight format of the cfg3 model for --workload prefill")
@@ -583,7 +585,8 @@ def main():
             print(json.dumps(r), flush=True)
         return
     if args.workload == "gemv_q4":
-        print(json.dumps(bench_gemv_q4(args)))
+        n, kd = (int(v) for v in args.shape.split("x"))
+        print(json.dumps(bench_gemv_q4(args, n, kd)))
         return
     if args.workload == "attn":
         print(json.dumps(bench_attn(args)))

@@ -43,15 +43,25 @@ __device__ __forceinline__ void i8x4_to_h2(uint32_t w, h2& lo, h2& hi) {
 // e1,e3,e5,e7 (bits 16,20,24,28).  Output: exact fp16 pairs (e0-8,e1-8) .. (e6-8,e7-8).
 // Nibble n in bits 0..3 of a half gives 0x6400|n = 1024+n; in bits 4..7 it gives
 // 1024+16n, and (1024+16n)/16 - 72 = n-8 exactly.
+// The constant in a vector register.  gfx9 VALU instructions read at most one scalar operand and
+// a VOP3 encoding takes no literal, so with both the mask and 0x64006400 as constants the
+// compiler splits (w & mask) | 0x64006400 into v_and + v_or; with 0x64006400 in a vector
+// register (the mask in a scalar one) it is a single v_and_or_b32.
+__device__ __forceinline__ uint32_t vreg_u32(uint32_t c) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "n"(c));
+  return r;
+}
 __device__ __forceinline__ void q4_word_to_h2(uint32_t w, h2 out[4]) {
   const h2 off_lo = {(half_t)-1032.0f, (half_t)-1032.0f};
   const h2 sc_hi = {(half_t)0.0625f, (half_t)0.0625f};
   const h2 off_hi = {(half_t)-72.0f, (half_t)-72.0f};
+  const uint32_t magic = vreg_u32(0x64006400u);
   const uint32_t w8 = w >> 8;
-  out[0] = as_h2((w & 0x000F000Fu) | 0x64006400u) + off_lo;
-  out[1] = as_h2((w & 0x00F000F0u) | 0x64006400u) * sc_hi + off_hi;
-  out[2] = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + off_lo;
-  out[3] = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sc_hi + off_hi;
+  out[0] = as_h2((w & 0x000F000Fu) | magic) + off_lo;
+  out[1] = as_h2((w & 0x00F000F0u) | magic) * sc_hi + off_hi;
+  out[2] = as_h2((w8 & 0x000F000Fu) | magic) + off_lo;
+  out[3] = as_h2((w8 & 0x00F000F0u) | magic) * sc_hi + off_hi;
 }
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }

@@ -410,25 +410,34 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   // One tile's weights for this wavefront's steps: 16 rows x 256 bytes, row-contiguous (chunks
   // past this wavefront's range belong to the next one: loaded, never used; clamped at the row
   // end), and the steps' block scales (lane l: row l / 4, step s0 + l % 4).
-  auto load_tile = [&](int e, int q, int tile, u4 (&wq)[4], u2& sq) {
+  // Buffer loads, so that a unit past the range (ok false) issues the same instructions with an
+  // out-of-range offset (zeros, no memory traffic): every path through the prefetch then has the
+  // same loads in flight, and the compiler's wait counts for a unit's data stay exact (with the
+  // loads of a missing unit skipped by a branch, its merged count waited for the newest prefetch).
+  const __amdgpu_buffer_rsrc_t wrs0 = make_rsrc(wbase, (int)((size_t)N * rowbytes));
+  auto load_tile = [&](int e, int q, int tile, u4 (&wq)[4], u2& sq, bool ok) {
+    // ok as a per-lane value: a select on it stays a v_cndmask (the compiler branches around the
+    // address arithmetic on a uniform condition, and the merged paths cost exact wait counts)
+    const uint32_t okv = vreg_u32(0u) | (uint32_t)ok;
     int s0, nsw;
     wrange(q, s0, nsw);
-    const unsigned char* wb = wbase + (size_t)e * a.w_es;
+    const __amdgpu_buffer_rsrc_t wrs = MOE ? make_rsrc(wbase + (size_t)e * a.w_es, (int)((size_t)N * rowbytes)) : wrs0;
     const int n0 = tile * 16;
     int c = s0 * 4 + lc;
     c = c < nsteps * 4 ? c : nsteps * 4 - 1;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
       const int row = n0 + 4 * h + lr < N ? n0 + 4 * h + lr : N - 1;   // tail rows computed, not stored
-      wq[h] = __builtin_nontemporal_load((const u4*)(wb + (size_t)row * rowbytes + (size_t)c * 16));
+      wq[h] = buf_load16(wrs, okv ? row * (int)rowbytes + c * 16 : kOOB);
     }
     if constexpr (has_block_scales<FMT>()) {
+      const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scale + (size_t)e * a.s_es, N * (K >> 5) * 2);
       const int row = n0 + (lane >> 2) < N ? n0 + (lane >> 2) : N - 1;
       int q = s0 + (lane & 3);
       q = q < nsteps ? q : nsteps - 1;
-      const half_t* sp = a.scale + (size_t)e * a.s_es + (size_t)row * (K >> 5) + (size_t)q * kSPS;
-      if constexpr (FMT == FMT_Q4) sq = *(const u2*)sp;
-      else sq = (u2){*(const uint32_t*)sp, 0u};
+      const int off = okv ? (row * (K >> 5) + q * kSPS) * 2 : kOOB;
+      if constexpr (FMT == FMT_Q4) sq = buf_load8(srs, off);
+      else sq = (u2){buf_load4(srs, off), 0u};
     }
   };
   auto compute_tile = [&](int e, int q, int tile, const u4 (&wq)[4], const u2& sq, f4 (&rd)[NW][64]) {
@@ -510,14 +519,13 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   }
   unit(v, eu[0], qu[0], tu[0]);
   load_x(eu[0], qu[0]);
-  load_tile(eu[0], qu[0], tu[0], wq[0], sq[0]);
+  load_tile(eu[0], qu[0], tu[0], wq[0], sq[0], true);
 #pragma unroll
   for (int b = 1; b < PD; ++b) {
     const int vb = v + b * vstep;
-    if (vb < vend) {
-      unit(vb, eu[b], qu[b], tu[b]);
-      load_tile(eu[b], qu[b], tu[b], wq[b], sq[b]);
-    }
+    const bool ok = vb < vend;
+    unit(ok ? vb : vend - 1, eu[b], qu[b], tu[b]);   // a valid unit's indices either way
+    load_tile(eu[b], qu[b], tu[b], wq[b], sq[b], ok);
   }
   int i = 0;                                       // units computed so far
   bool more = true;
@@ -527,11 +535,10 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
       if (!more) break;
       const int vi = v + i * vstep;
       const int vp = vi + PD * vstep;              // prefetch unit i + PD into buffer (b + PD) % NBUF
-      if (vp < vend) {
-        const int bp = (b + PD) % NBUF;
-        unit(vp, eu[bp], qu[bp], tu[bp]);
-        load_tile(eu[bp], qu[bp], tu[bp], wq[bp], sq[bp]);
-      }
+      const int bp = (b + PD) % NBUF;
+      const bool ok = vp < vend;
+      unit(ok ? vp : vend - 1, eu[bp], qu[bp], tu[bp]);
+      load_tile(eu[bp], qu[bp], tu[bp], wq[bp], sq[bp], ok);
       __builtin_amdgcn_sched_barrier(0);
       compute_tile(eu[b], qu[b], tu[b], wq[b], sq[b], red[i & 1]);
       ++i;
@@ -599,12 +606,19 @@ __global__ __launch_bounds__(256) void mfma_finish_kernel(MfmaArgs a, int rows) 
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= rows * per_row) return;
   const int yr = idx / per_row, rb = 4 * (idx - yr * per_row);
-  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int q = 0; q < a.ks; ++q) {
-    const f4 p = *(const f4*)(a.ws + ((size_t)q * a.ws_rows + yr) * a.N + rb);
+  // every slice's load issued before the first sum (one memory round trip); slots past ks re-read
+  // slice 0 and are not added
+  f4 p[kMaxSlices];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] += p[i];
-  }
+  for (int q = 0; q < kMaxSlices; ++q)
+    p[q] = *(const f4*)(a.ws + ((size_t)(q < a.ks ? q : 0) * a.ws_rows + yr) * a.N + rb);
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int q = 0; q < kMaxSlices; ++q)
+    if (q < a.ks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += p[q][i];
+    }
   mfma_store<FMT_F16, EG_PLAIN>(a, nullptr, v, rb, true, yr);
 }
 

@@ -400,7 +400,10 @@ static attn_fn pick_steps(int nstep) {
   switch (nstep) {
     case 1: return attn_partial_kernel<D, G, 1, kAttnWaves>;
     case 2: return attn_partial_kernel<D, G, 2, kAttnWaves>;
+    case 3: return attn_partial_kernel<D, G, 3, kAttnWaves>;
     case 4: return attn_partial_kernel<D, G, 4, kAttnWaves>;
+    case 5: return attn_partial_kernel<D, G, 5, kAttnWaves>;
+    case 6: return attn_partial_kernel<D, G, 6, kAttnWaves>;
     case 8: return attn_partial_kernel<D, G, 8, kAttnWaves>;
     default: return attn_partial_kernel<D, G, 16, kAttnWaves>;
   }
@@ -426,13 +429,19 @@ static int attn_cus() {
   return cus;
 }
 
-// Steps per wavefront (chunk = nstep * kAttnWaves * (512 / D) positions): the largest chunk that still
-// puts about one workgroup on every CU, and never more than kMaxSplits splits.  Returns 0 if
-// even the largest chunk leaves more than kMaxSplits splits.
+constexpr int kNsteps[] = {1, 2, 3, 4, 5, 6, 8, 16};   // instantiated steps per wavefront
+
+// Steps per wavefront (chunk = nstep * kAttnWaves * (512 / D) positions).  Every partial
+// workgroup streams its chunk at once and the launch ends with its slowest workgroup, so the cost
+// of a split size is the number of dispatch rounds (workgroups / CUs, rounded up) times the chunk;
+// the cheapest wins, the larger chunk (fewer partials to merge) on a tie.  A few workgroups past a
+// whole round share CUs with others and set the launch's end: at the 7B cache bound of 2184 rows,
+// 64-position chunks give 280 workgroups for 256 CUs and an 80-position chunk 224.  Never more
+// than kMaxSplits splits; returns 0 if even the largest chunk leaves more.
 static int choose_nstep(int D, int B, int Hkv, int L, int want) {
   const int pps = 512 / D;
   auto splits = [&](int ns) { const int c = ns * kAttnWaves * pps; return (L + c - 1) / c; };
-  if (want == 0) {                              // tuning override: AFX_ATTN_NSTEP=1|2|4|8|16
+  if (want == 0) {                              // tuning override: AFX_ATTN_NSTEP=1|2|3|4|5|6|8|16
     static int env = -1;
     if (env < 0) {
       const char* e = getenv("AFX_ATTN_NSTEP");
@@ -440,13 +449,18 @@ static int choose_nstep(int D, int B, int Hkv, int L, int want) {
     }
     want = env;
   }
-  if (want == 1 || want == 2 || want == 4 || want == 8 || want == 16) return splits(want) <= kMaxSplits ? want : 0;
-  const int target = attn_cus();
-  for (int ns = 16; ns >= 1; ns >>= 1) {
-    if (splits(ns) > kMaxSplits) return ns == 16 ? 0 : ns * 2;
-    if ((long long)B * Hkv * splits(ns) >= target) return ns;
+  for (int ns : kNsteps)
+    if (want == ns) return splits(want) <= kMaxSplits ? want : 0;
+  const long long cus = attn_cus();
+  int best = 0;
+  long long best_cost = 0;
+  for (int ns : kNsteps) {
+    if (splits(ns) > kMaxSplits) continue;
+    const long long wgs = (long long)B * Hkv * splits(ns);
+    const long long cost = (wgs + cus - 1) / cus * ns;
+    if (!best || cost <= best_cost) { best = ns; best_cost = cost; }
   }
-  return 1;
+  return best;
 }
 
 }  // namespace afx

@@ -65,6 +65,14 @@ def test_attention_workspace_sizes_and_their_errors_without_a_gpu():
         K.attn_ws_bytes(1, 32, 8, 100, 2048)
     with pytest.raises(ValueError, match="128 splits"):
         K.attn_ws_bytes(1, 32, 8, 128, 8192, nstep_hint=1)
+    # the split size: fewest dispatch rounds over 256 CUs times the chunk.  ctx 2048: 64-position
+    # chunks, 32 splits x 8 kv heads = one round; the 7B engine's 2184-row cache: 80-position chunks
+    # (28 splits, 224 workgroups) rather than 64 (35 splits, 280 workgroups, a second round)
+    part = lambda nsp: 32 * nsp * (128 + 2) * 4
+    assert n == part(32)
+    assert K.attn_ws_bytes(1, 32, 8, 128, 2184) == part(28)
+    assert K.attn_ws_bytes(1, 32, 8, 128, 2184, nstep_hint=4) == part(36)   # 35 splits, padded to 4
+    assert K.attn_ws_bytes(16, 32, 8, 128, 8192) == 16 * part(32)
 
 
 def test_noalloc_attention_rejects_shapes_beyond_its_scratch_without_a_gpu():

@@ -438,6 +438,23 @@ def test_decode_attn_device_positions(K, Hq, Hkv, D, Mmax):
     check_f16(got, want, what="attn pos")
 
 
+@pytest.mark.parametrize("nstep", [2, 3, 4, 5, 6, 8, 16])
+def test_decode_attn_every_split_size_at_the_7b_cache_bound(K, nstep):
+    """Each instantiated chunk (16 * nstep positions) at the cfg3 engine's cache bound (2184 rows, 32/8
+    heads, dh 128), positions from the device: a partly filled last split, the final row, and ctx 1.
+    (16-position chunks would need 137 > 128 splits here.)"""
+    say(f"decode attention 7B cache bound nstep={nstep}")
+    rng = np.random.default_rng(41)
+    B, Hq, Hkv, D, Mmax = 3, 32, 8, 128, 2184
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    Kc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
+    Vc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
+    pos = np.array([2048, Mmax - 1, 0], np.int32)
+    got = host(K.decode_attn(dev(q), dev(Kc), dev(Vc), pos=dev(pos), nstep_hint=nstep))
+    want = ref.attention(q[:, :, None, :], Kc, Vc, lengths=pos + 1)[:, :, 0]
+    check_f16(got, want, what=f"attn nstep={nstep}")
+
+
 def test_decode_attn_workspace_reuse_and_graph_replay(K):
     say("decode attention: one workspace reused across calls and graph replays")
     import bench

@@ -370,7 +370,9 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   auto unit = [&](int u, int& e, int& q, int& tile) {
     tile = u % ntiles;
     q = SPLIT ? (u / ntiles) % S : 0;
-    e = MOE ? act_e[u / (ntiles * S)] : 0;
+    // the unit is workgroup-uniform, so its expert is too; said explicitly, or the weight rows'
+    // buffer resource sits in vector registers and every load becomes a per-lane waterfall loop
+    e = MOE ? __builtin_amdgcn_readfirstlane(act_e[u / (ntiles * S)]) : 0;
   };
 
   // this wavefront's slice of x in the B-operand layout (token column r, k slot g), for the

@@ -92,21 +92,44 @@ __device__ __forceinline__ h8 mfma_a_operand(const u4& w, const u2& dv, int g, i
   }
 }
 
+// The epilogue's inputs for a lane's output rows rb .. rb + 3 (N % 4 == 0: all four exist when
+// rb < N), as fp16 pairs, zeros where the epilogue has none: the int8 row scales, the bias, the
+// residual of output row yr.
+struct EpiOps {
+  u2 sc, bi, re;
+};
+__device__ __forceinline__ u2 load_h4(const half_t* p) {
+  h2 lo, hi;
+  lo.x = p[0]; lo.y = p[1]; hi.x = p[2]; hi.y = p[3];
+  return (u2){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+}
+// Loaded where they are used: for the kernels whose epilogue ends the workgroup's work.  The
+// persistent kernel prefetches them with each tile instead (a load issued in its epilogue would
+// wait for every tile in flight before it: the memory counter retires in order).
+template <int FMT>
+__device__ __forceinline__ EpiOps epi_load(const MfmaArgs& a, const half_t* sbase, int rb, bool tok_ok, int yr) {
+  EpiOps o = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
+  if (rb >= a.N) return o;
+  if constexpr (FMT == FMT_I8) o.sc = *(const u2*)(sbase + rb);   // 8-byte aligned: checked at launch
+  if (a.bias) o.bi = load_h4(a.bias + rb);
+  if (a.epi == EPI_RESID && tok_ok) o.re = load_h4(a.resid + (size_t)yr * a.ldy + rb);
+  return o;
+}
+
 // Tile epilogue of wavefront 0: v = this lane's summed tile entries, output rows rb .. rb + 3
 // of one token column, stored to y row yr (tok_ok: the column is a real token) with the int8
-// row scale, the bias and the epilogue.
+// row scale, the bias and the epilogue, whose inputs are in `ops`.
 template <int FMT, int EG>
-__device__ __forceinline__ void mfma_store(const MfmaArgs& a, const half_t* sbase, float (&v)[4], int rb, bool tok_ok,
+__device__ __forceinline__ void mfma_store(const MfmaArgs& a, const EpiOps& ops, float (&v)[4], int rb, bool tok_ok,
                                            int yr) {
   const int N = a.N;
   if constexpr (FMT == FMT_I8) {
-    const u2 sv = *(const u2*)(sbase + (rb < N ? rb : 0));
-    const h2 s01 = as_h2(sv.x), s23 = as_h2(sv.y);
+    const h2 s01 = as_h2(ops.sc.x), s23 = as_h2(ops.sc.y);
     v[0] *= (float)s01.x; v[1] *= (float)s01.y; v[2] *= (float)s23.x; v[3] *= (float)s23.y;
   }
-  if (a.bias) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] += rb + i < N ? (float)a.bias[rb + i] : 0.0f;
+  if (a.bias && rb < N) {
+    const h2 b01 = as_h2(ops.bi.x), b23 = as_h2(ops.bi.y);
+    v[0] += (float)b01.x; v[1] += (float)b01.y; v[2] += (float)b23.x; v[3] += (float)b23.y;
   }
   if (!tok_ok || rb >= N) return;
   if constexpr (EG == EG_SWIGLU) {
@@ -122,11 +145,12 @@ __device__ __forceinline__ void mfma_store(const MfmaArgs& a, const half_t* sbas
       if (rb + i < N) yp[i] = v[i];
   } else {
     half_t* yp = (half_t*)a.y + (size_t)yr * a.ldy + rb;
+    const h2 r01 = as_h2(ops.re.x), r23 = as_h2(ops.re.y);
+    const float res[4] = {(float)r01.x, (float)r01.y, (float)r23.x, (float)r23.y};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (rb + i >= N) break;
       float o = v[i];
-      if (a.epi == EPI_RESID) o = (float)a.resid[(size_t)yr * a.ldy + rb + i] + (float)(half_t)o;
+      if (a.epi == EPI_RESID) o = res[i] + (float)(half_t)o;
       yp[i] = (half_t)o;
     }
   }
@@ -278,7 +302,8 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
         for (int i = 0; i < 4; ++i) v[i] += p[i];
       }
       // output rows n0 + 4g .. + 3 of token ti, to its entry (MoE) or activation row (dense)
-      mfma_store<FMT, EG>(a, sbase, v, n0 + 4 * g, tok_ok, tok_ok ? (lst ? lst[ti] : ti) : 0);
+      const int yr = tok_ok ? (lst ? lst[ti] : ti) : 0;
+      mfma_store<FMT, EG>(a, epi_load<FMT>(a, sbase, n0 + 4 * g, tok_ok, yr), v, n0 + 4 * g, tok_ok, yr);
     }
     __syncthreads();                               // red is reused by the next token group
   }
@@ -307,7 +332,8 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
   __shared__ __align__(16) unsigned char wl[NW][16 * kWRow];
   __shared__ __align__(16) unsigned char sl[NW][has_block_scales<FMT>() ? 16 * kSRow : 16];
   __shared__ f4 red[2][NW][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wavefront index said to be uniform: its step range and the branches on it stay scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;          // MFMA role: A row / B column (token), k slot
   const int lr = lane >> 4, lc = lane & 15;        // load role: row lr + 4h, chunk lc of the batch
   const int N = a.N, K = a.K;
@@ -367,28 +393,48 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
     vstep = 1;
   }
   if (v >= vend) return;                           // whole workgroup, after its last barrier
-  auto unit = [&](int u, int& e, int& q, int& tile) {
-    tile = u % ntiles;
-    q = SPLIT ? (u / ntiles) % S : 0;
-    // the unit is workgroup-uniform, so its expert is too; said explicitly, or the weight rows'
-    // buffer resource sits in vector registers and every load becomes a per-lane waterfall loop
-    e = MOE ? __builtin_amdgcn_readfirstlane(act_e[u / (ntiles * S)]) : 0;
+
+  // A work unit: expert e, K slice q (this wavefront's steps [s0, s0 + nsw) of it), 16-row tile;
+  // every field is workgroup-uniform.  The prefetch cursor walks the units v, v + vstep, ... by
+  // increments, with a division only where the slice changes.
+  struct Unit {
+    int e, q, tile, s0, nsw;
+  };
+  // the expert is read as a uniform value, or the weight rows' buffer resource sits in vector
+  // registers and every load becomes a per-lane waterfall loop
+  auto expert_at = [&](int i) { return MOE ? __builtin_amdgcn_readfirstlane(act_e[i]) : 0; };
+  Unit cur;
+  int cei = MOE ? v / (ntiles * S) : 0;            // MoE: the cursor's expert, as an index into act_e
+  cur.tile = v % ntiles;
+  cur.q = SPLIT ? (v / ntiles) % S : 0;
+  cur.e = expert_at(cei);
+  wrange(cur.q, cur.s0, cur.nsw);
+  auto advance = [&]() {                           // to the next unit of the walk (which exists)
+    if (vstep != 1) {                              // dense, unsplit: tiles blockIdx.x, + G, ...
+      cur.tile += vstep;
+      return;
+    }
+    if (++cur.tile < ntiles) return;
+    cur.tile = 0;
+    if (++cur.q == S) {
+      cur.q = 0;
+      cur.e = expert_at(++cei);
+    }
+    wrange(cur.q, cur.s0, cur.nsw);
   };
 
   // this wavefront's slice of x in the B-operand layout (token column r, k slot g), for the
-  // expert xe (MoE: column r is entry r of the expert's list; dense: activation row r)
+  // expert and slice xe (MoE: column r is entry r of the expert's list; dense: activation row r)
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, a.xbytes);
   bool tok_ok = false;
   int yr = r, xe = -1;                             // xe: expert * S + slice of the x slice held
   u4 xv[kSPB][NM];
-  auto load_x = [&](int e, int q) {
-    int s0, nsw;
-    wrange(q, s0, nsw);
+  auto load_x = [&](const Unit& u) {
     int xr = r;
     tok_ok = r < a.M;
     if constexpr (MOE) {
-      const int* lst = a.list + (size_t)e * a.T;
-      tok_ok = r < a.cnt[e];
+      const int* lst = a.list + (size_t)u.e * a.T;
+      tok_ok = r < a.cnt[u.e];
       const int ent = tok_ok ? lst[r] : 0;
       xr = a.x_by_token ? ent / a.k : ent;
       yr = ent;                                    // output row: the entry
@@ -396,64 +442,73 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
     const int xoff = tok_ok ? xr * a.ldx * 2 : kOOB;   // out of range: reads zeros
 #pragma unroll
     for (int t = 0; t < kSPB; ++t) {
-      const int s = s0 + t;
+      const int s = u.s0 + t;
 #pragma unroll
       for (int j = 0; j < NM; ++j) {
         int kx;
         if constexpr (FMT == FMT_I8 || FMT == FMT_BW) kx = s * KS + 16 * g + 8 * j;
         else if constexpr (FMT == FMT_Q4) kx = 32 * (4 * s + j) + 8 * g;
         else kx = s * KS + 8 * g;
-        xv[t][j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xrs, t < nsw ? xoff + kx * 2 : kOOB, 0, 0));
+        xv[t][j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xrs, t < u.nsw ? xoff + kx * 2 : kOOB, 0, 0));
       }
     }
-    xe = e * S + q;
+    xe = u.e * S + u.q;
   };
 
-  // One tile's weights for this wavefront's steps: 16 rows x 256 bytes, row-contiguous (chunks
-  // past this wavefront's range belong to the next one: loaded, never used; clamped at the row
-  // end), and the steps' block scales (lane l: row l / 4, step s0 + l % 4).
-  // Buffer loads, so that a unit past the range (ok false) issues the same instructions with an
-  // out-of-range offset (zeros, no memory traffic): every path through the prefetch then has the
-  // same loads in flight, and the compiler's wait counts for a unit's data stay exact (with the
-  // loads of a missing unit skipped by a branch, its merged count waited for the newest prefetch).
-  const __amdgpu_buffer_rsrc_t wrs0 = make_rsrc(wbase, (int)((size_t)N * rowbytes));
-  auto load_tile = [&](int e, int q, int tile, u4 (&wq)[4], u2& sq, bool ok) {
-    // ok as a per-lane value: a select on it stays a v_cndmask (the compiler branches around the
-    // address arithmetic on a uniform condition, and the merged paths cost exact wait counts)
-    const uint32_t okv = vreg_u32(0u) | (uint32_t)ok;
-    int s0, nsw;
-    wrange(q, s0, nsw);
-    const __amdgpu_buffer_rsrc_t wrs = MOE ? make_rsrc(wbase + (size_t)e * a.w_es, (int)((size_t)N * rowbytes)) : wrs0;
-    const int n0 = tile * 16;
-    int c = s0 * 4 + lc;
-    c = c < nsteps * 4 ? c : nsteps * 4 - 1;
+  // One tile's weights for this wavefront's steps: 16 rows x 256 bytes, row-contiguous, and the
+  // steps' block scales (lane l: row l / 4, step s0 + l % 4).  Each load is a buffer load at a
+  // fixed per-lane offset from a workgroup-uniform base: the buffer starts at the tile's first
+  // byte of this wavefront's steps and ends with the expert's matrix, so rows past N read zeros
+  // (computed, never stored), and bytes past the wavefront's steps are those of the next steps
+  // or row (loaded, never used).  A unit past the range (ok false) gets an empty buffer: the same
+  // instructions, zeros, no memory traffic, so every path through the prefetch has the same
+  // loads in flight and the compiler's wait counts for a unit's data stay exact.
+  int loff[4];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int row = n0 + 4 * h + lr < N ? n0 + 4 * h + lr : N - 1;   // tail rows computed, not stored
-      wq[h] = buf_load16(wrs, okv ? row * (int)rowbytes + c * 16 : kOOB);
-    }
+  for (int h = 0; h < 4; ++h) loff[h] = (4 * h + lr) * (int)rowbytes + lc * 16;
+  const int soff = ((lane >> 2) * (K >> 5) + (lane & 3) * kSPS) * 2;
+  // The epilogue's inputs (int8 row scales, bias, residual of the lane's output rows
+  // tile * 16 + 4g .. + 3) come with the tile: a load issued in the epilogue would wait for every
+  // tile in flight before it (the memory counter retires in order).  An absent input reads as
+  // an empty buffer (zeros).
+  constexpr bool kEpiIn = !MOE && !SPLIT;         // bias and residual: dense, unsplit launches only
+  const long long res_halves = a.epi == EPI_RESID ? (long long)a.M * a.ldy : 0;
+  auto load_tile = [&](const Unit& u, u4 (&wq)[4], u2& sq, EpiOps& eo, bool ok) {
+    const int n0 = u.tile * 16;
+    const long long wfirst = (long long)n0 * (long long)rowbytes + u.s0 * 64;
+    const __amdgpu_buffer_rsrc_t wrs =
+        make_rsrc(wbase + (size_t)u.e * a.w_es + wfirst, ok ? (int)((long long)N * (long long)rowbytes - wfirst) : 0);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) wq[h] = buf_load16(wrs, loff[h]);
     if constexpr (has_block_scales<FMT>()) {
-      const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scale + (size_t)e * a.s_es, N * (K >> 5) * 2);
-      const int row = n0 + (lane >> 2) < N ? n0 + (lane >> 2) : N - 1;
-      int q = s0 + (lane & 3);
-      q = q < nsteps ? q : nsteps - 1;
-      const int off = okv ? (row * (K >> 5) + q * kSPS) * 2 : kOOB;
-      if constexpr (FMT == FMT_Q4) sq = buf_load8(srs, off);
-      else sq = (u2){buf_load4(srs, off), 0u};
+      const long long sfirst = (long long)n0 * (K >> 5) + u.s0 * kSPS;   // halves
+      const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scale + (size_t)u.e * a.s_es + sfirst,
+                                                   ok ? (int)(((long long)N * (K >> 5) - sfirst) * 2) : 0);
+      if constexpr (FMT == FMT_Q4) sq = buf_load8(srs, soff);
+      else sq = (u2){buf_load4(srs, soff), 0u};
+    }
+    if constexpr (FMT == FMT_I8) {
+      const __amdgpu_buffer_rsrc_t ers = make_rsrc(a.scale + (size_t)u.e * a.s_es + n0, ok ? (N - n0) * 2 : 0);
+      eo.sc = buf_load8(ers, 8 * g);
+    }
+    if constexpr (kEpiIn) {
+      const __amdgpu_buffer_rsrc_t brs =
+          make_rsrc(a.bias ? a.bias + n0 : (const half_t*)a.x, ok && a.bias ? (N - n0) * 2 : 0);
+      eo.bi = buf_load8(brs, 8 * g);
+      const __amdgpu_buffer_rsrc_t rrs =
+          make_rsrc(res_halves ? a.resid + n0 : (const half_t*)a.x, ok && res_halves ? (int)((res_halves - n0) * 2) : 0);
+      eo.re = buf_load8(rrs, (r * a.ldy + 4 * g) * 2);
     }
   };
-  auto compute_tile = [&](int e, int q, int tile, const u4 (&wq)[4], const u2& sq, f4 (&rd)[NW][64]) {
+  auto compute_tile = [&](const Unit& u, const u4 (&wq)[4], const u2& sq, const EpiOps& eo, f4 (&rd)[NW][64]) {
     if constexpr (MOE || SPLIT) {
       // the next expert's (or slice's) rows; the full wait keeps these loads from leaving the
       // compiler's wait counts (in-order, shared with the prefetched tiles) pending past the branch
-      if (e * S + q != xe) {
-        load_x(e, q);
+      if (u.e * S + u.q != xe) {
+        load_x(u);
         __builtin_amdgcn_s_waitcnt(0);
       }
     }
-    int s0, nsw;
-    wrange(q, s0, nsw);
-    (void)s0;
     wave_sync_lds();                               // the previous tile's staged reads are done
 #pragma unroll
     for (int h = 0; h < 4; ++h) *(u4*)(wls + (4 * h + lr) * kWRow + lc * 16) = wq[h];
@@ -468,10 +523,14 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
       if constexpr (FMT == FMT_Q4) dv[t] = *(const u2*)(sls + r * kSRow + t * 8);
       if constexpr (FMT == FMT_BW) dv[t] = (u2){*(const uint32_t*)(sls + r * kSRow + t * 4), 0u};
     }
+    // every step's operands are read before the first is used: one LDS round trip, where the
+    // compiler would otherwise move each step's reads into that step's branch and wait there
+#pragma unroll
+    for (int t = 0; t < kSPB; ++t) asm volatile("" : "+v"(wv[t]), "+v"(dv[t]));
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < kSPB; ++t) {
-      if (t >= nsw) break;                         // wavefront-uniform
+      if (t >= u.nsw) break;                       // wavefront-uniform
 #pragma unroll
       for (int j = 0; j < NM; ++j)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(mfma_a_operand<FMT>(wv[t], dv[t], g, j), as_h8(xv[t][j]), acc,
@@ -489,62 +548,61 @@ __global__ __launch_bounds__(NW * 64) void mfma_px_kernel(MfmaArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] += p[i];
       }
-      const int rb = tile * 16 + 4 * g;
+      const int rb = u.tile * 16 + 4 * g;
       if constexpr (SPLIT) {
         if constexpr (FMT == FMT_I8) {
-          const u2 sv = *(const u2*)(a.scale + (size_t)e * a.s_es + (rb < N ? rb : 0));
-          const h2 s01 = as_h2(sv.x), s23 = as_h2(sv.y);
+          const h2 s01 = as_h2(eo.sc.x), s23 = as_h2(eo.sc.y);
           v[0] *= (float)s01.x; v[1] *= (float)s01.y; v[2] *= (float)s23.x; v[3] *= (float)s23.y;
         }
         if (tok_ok && rb < N)
-          *(f4*)(a.ws + ((size_t)q * a.ws_rows + yr) * N + rb) = (f4){v[0], v[1], v[2], v[3]};
+          *(f4*)(a.ws + ((size_t)u.q * a.ws_rows + yr) * N + rb) = (f4){v[0], v[1], v[2], v[3]};
       } else {
-        mfma_store<FMT, EG>(a, a.scale + (size_t)e * a.s_es, v, rb, tok_ok, yr);
+        mfma_store<FMT, EG>(a, eo, v, rb, tok_ok, yr);
       }
     }
   };
 
-  // PD units in flight ahead of the one being computed: unit j in buffer j % (PD + 1), the
-  // buffers rotated by a fully unrolled inner loop (fixed registers).  PD = 1 for a few units
-  // per workgroup (a deeper prefetch measured slower there: 10.7 against 10.2 us for Q4_0
-  // 11008 x 4096 at 4 rows), PD = 3 for long runs of units (MoE).
+  // PD units in flight ahead of the one being computed: unit j of the walk in buffer j % (PD + 1),
+  // the buffers rotated by a fully unrolled inner loop (fixed registers).  Every pass of the loop
+  // runs all PD + 1 slots (a slot past the walk's end issues out-of-range loads and skips its
+  // tile), so the loop has one entry and one back edge: with early exits from the unrolled slots
+  // the compiler met buffers still in flight on a back edge and waited for all of them there.
+  // PD = 1 for a few units per workgroup (a deeper prefetch measured slower there: 10.7 against
+  // 10.2 us for Q4_0 11008 x 4096 at 4 rows), PD = 3 for long runs of units (MoE).
   constexpr int NBUF = PD + 1;
+  static_assert(NBUF % 2 == 0, "slot b of a pass is unit j0 + b with j0 a multiple of NBUF: red[b & 1] alternates");
   u4 wq[NBUF][4];
   u2 sq[NBUF];
-  int eu[NBUF], qu[NBUF], tu[NBUF];
+  EpiOps eo[NBUF];
+  Unit un[NBUF];
 #pragma unroll
   for (int b = 0; b < NBUF; ++b) {
     sq[b] = (u2){0u, 0u};
-    eu[b] = 0;
-    qu[b] = 0;
-    tu[b] = 0;
+    eo[b] = EpiOps{{0u, 0u}, {0u, 0u}, {0u, 0u}};
+    un[b] = cur;
   }
-  unit(v, eu[0], qu[0], tu[0]);
-  load_x(eu[0], qu[0]);
-  load_tile(eu[0], qu[0], tu[0], wq[0], sq[0], true);
+  const int n = (vend - v + vstep - 1) / vstep;   // units of this workgroup, >= 1
+  // unit j of the walk into buffer b: the cursor moves on while j < n, and a slot past the end
+  // keeps the last unit's indices (its loads are empty either way)
+  auto prefetch = [&](int j, int b) {
+    if (j > 0 && j < n) advance();
+    un[b] = cur;
+    load_tile(un[b], wq[b], sq[b], eo[b], j < n);
+  };
+  load_x(cur);
 #pragma unroll
-  for (int b = 1; b < PD; ++b) {
-    const int vb = v + b * vstep;
-    const bool ok = vb < vend;
-    unit(ok ? vb : vend - 1, eu[b], qu[b], tu[b]);   // a valid unit's indices either way
-    load_tile(eu[b], qu[b], tu[b], wq[b], sq[b], ok);
-  }
-  int i = 0;                                       // units computed so far
-  bool more = true;
-  while (more) {
+  for (int b = 0; b < PD; ++b) prefetch(b, b);
+  // x is complete on every path into the loop (here, and after each reload): otherwise the
+  // compiler's merged wait counts keep the x slice pending and every unit's first MFMA waits for
+  // the tiles prefetched before it
+  __builtin_amdgcn_s_waitcnt(0);
+  for (int j0 = 0; j0 < n; j0 += NBUF) {
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) {
-      if (!more) break;
-      const int vi = v + i * vstep;
-      const int vp = vi + PD * vstep;              // prefetch unit i + PD into buffer (b + PD) % NBUF
-      const int bp = (b + PD) % NBUF;
-      const bool ok = vp < vend;
-      unit(ok ? vp : vend - 1, eu[bp], qu[bp], tu[bp]);
-      load_tile(eu[bp], qu[bp], tu[bp], wq[bp], sq[bp], ok);
+      const int bp = (b + PD) % NBUF;              // unit j0 + b + PD goes to buffer bp
+      prefetch(j0 + b + PD, bp);
       __builtin_amdgcn_sched_barrier(0);
-      compute_tile(eu[b], qu[b], tu[b], wq[b], sq[b], red[i & 1]);
-      ++i;
-      more = vi + vstep < vend;
+      if (j0 + b < n) compute_tile(un[b], wq[b], sq[b], eo[b], red[b & 1]);   // uniform
     }
   }
 }
@@ -621,7 +679,7 @@ __global__ __launch_bounds__(256) void mfma_finish_kernel(MfmaArgs a, int rows) 
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] += p[q][i];
     }
-  mfma_store<FMT_F16, EG_PLAIN>(a, nullptr, v, rb, true, yr);
+  mfma_store<FMT_F16, EG_PLAIN>(a, epi_load<FMT_F16>(a, nullptr, rb, true, yr), v, rb, true, yr);
 }
 
 static int mfma_cus() {
@@ -653,6 +711,7 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
   AFX_REQUIRE(fmt != FMT_BW || (a.scale && ((uintptr_t)a.scale & 3) == 0), "%s: blockwise needs aligned block scales", what);
   AFX_REQUIRE(a.cnt ? (a.list && a.T >= 1 && a.k >= 1) : (a.M >= 1), "%s: bad token description", what);
   AFX_REQUIRE(a.epi != EPI_RESID || a.resid, "%s: residual pointer required", what);
+  AFX_REQUIRE(!a.cnt || (!a.bias && a.epi != EPI_RESID), "%s: expert linears take no bias or residual", what);
   const long long xrows = a.cnt ? (a.x_by_token ? a.T : (long long)a.T * a.k) : a.M;
   const long long xbytes = xrows * a.ldx * 2;
   AFX_REQUIRE(xbytes < 0x7fff0000LL, "%s: activations span %lld bytes (limit 2 GiB)", what, xbytes);
@@ -682,7 +741,11 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
     const char* d = getenv("AFX_MFMA_PX_DEPTH");
     px_depth = d ? atoi(d) : 0;
   }
-  if (px_env != 0 && (a.cnt ? a.T <= 16 && E <= kPxMaxExperts : E == 1 && a.M <= 16)) {
+  // the persistent kernel reads the bias and the residual four fp16 at a time
+  const bool epi_aligned =
+      (!a.bias || ((uintptr_t)a.bias & 7) == 0) &&
+      (a.epi != EPI_RESID || (((uintptr_t)a.resid & 7) == 0 && a.ldy % 4 == 0 && (long long)a.M * a.ldy * 2 < 0x7fff0000LL));
+  if (px_env != 0 && epi_aligned && (a.cnt ? a.T <= 16 && E <= kPxMaxExperts : E == 1 && a.M <= 16)) {
     int cap = fmt == FMT_Q4 ? 8 : 16;
     if (px_waves == 4 || px_waves == 8 || px_waves == 16) cap = px_waves < cap ? px_waves : cap;
     int pw = 0;

@@ -395,6 +395,32 @@ def moe_down(fmt, w, scale, act, T, k, E, F, D, cnt, lst, y=None, rows_hint=0, w
     return y
 
 
+def moe_route_supported(h, router, k):
+    """Whether afx_moe_route takes this batch (one workgroup: T, E <= 16, D <= 4096, aligned rows)."""
+    T, D = h.shape
+    E = router.shape[0]
+    return (1 <= T <= 16 and 1 <= k <= E <= 16 and D % 32 == 0 and 256 <= D <= 4096 and h.stride(0) % 8 == 0
+            and h.data_ptr() % 16 == 0 and router.data_ptr() % 16 == 0)
+
+
+def moe_route(h, gamma, eps, router, k, renorm, hn, gate, sel, cnt, lst, logits=None):
+    """RMSNorm + router logits + top-k + bucketing in one launch (afx_moe_route); hn [T, D] out."""
+    T, D = h.shape
+    E = router.shape[0]
+    _hip.call("afx_moe_route", P(h), h.stride(0), P(gamma), float(eps), P(router), T, E, D, k, int(bool(renorm)),
+              P(hn), hn.stride(0), P(logits), P(gate), P(sel), P(cnt), P(lst), stream())
+    return gate, sel, cnt, lst
+
+
+def moe_down_combine(fmt, w, scale, act, T, k, E, F, D, cnt, lst, y, h, gate, shared=None, out=None, ws=None):
+    """moe_down then moe_combine in one call, the K-split's finishing sum folded into the combine."""
+    if out is None:
+        out = torch.empty_like(h)
+    _hip.call("afx_moe_down_combine", FMT[fmt], P(w), P(scale), P(act), T, k, E, F, D, P(cnt), P(lst), P(y),
+              P(ws), _nbytes(ws), P(h), P(gate), P(shared), P(out), stream())
+    return out
+
+
 def moe_combine(h, y, gate, shared=None, out=None):
     T, D = h.shape
     k = gate.shape[1]

@@ -30,7 +30,9 @@ struct MfmaArgs {
 };
 
 // Launch the MFMA kernel over E experts (1 for a dense linear).  Returns 0 or a negative code.
-int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const char* what);
+// ks_out (optional): a K-split launch then leaves its slices in a.ws without the finishing sum
+// and reports their count there (1: no split, y was written).
+int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const char* what, int* ks_out = nullptr);
 // Whether the MFMA path supports this shape (K divisible into steps, one or more per wavefront).
 bool mfma_supported(int fmt, int K);
 

@@ -699,7 +699,8 @@ bool mfma_supported(int fmt, int K) {
   return K % ks == 0 && K / ks >= 8;                           // at least one step per wavefront
 }
 
-int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const char* what) {
+int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const char* what, int* ks_out) {
+  if (ks_out) *ks_out = 1;
   AFX_REQUIRE(fmt >= 0 && fmt <= 3, "%s: unknown weight format %d", what, fmt);
   AFX_REQUIRE(a.w && a.x && a.y, "%s: null pointer", what);
   AFX_REQUIRE(a.N >= 1 && a.N % 4 == 0, "%s: N=%d must be a multiple of 4", what, a.N);
@@ -784,6 +785,10 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
       if (S == 1) return check_launch(what);
       int rc = check_launch(what);
       if (rc) return rc;
+      if (ks_out) {                                // the caller sums the slices
+        *ks_out = S;
+        return 0;
+      }
       const long long n = rows * (a.N / 4);
       hipLaunchKernelGGL(mfma_finish_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, b, (int)rows);
       return check_launch(what);

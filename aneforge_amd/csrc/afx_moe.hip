@@ -17,6 +17,64 @@
 
 namespace afx {
 
+// One token's routing, by one wavefront: lane l holds the logits of experts l, l + 64, ...
+// (-inf past E).  Softmax in fp32, probabilities rounded to fp16, k rounds of "row max, lowest
+// index among exact fp16 ties" (moe.py:21-37), optional renormalisation (moe.py:55-56).  Lane
+// r < k ends with round r's expert and gate weight.
+template <int J>
+__device__ __forceinline__ void topk_token(const float (&lg)[J], int lane, int E, int k, int renorm, float& gate_r,
+                                           int& sel_r) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < J; ++j) m = fmaxf(m, lg[j]);
+  m = wave_max(m);
+  float ex[J];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    ex[j] = lane + 64 * j < E ? expf(lg[j] - m) : 0.0f;
+    sum += ex[j];
+  }
+  const float inv = 1.0f / wave_sum(sum);
+  // probabilities rounded to fp16 (-1 marks experts this lane does not own)
+  float p[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) p[j] = lane + 64 * j < E ? (float)(half_t)(ex[j] * inv) : -1.0f;
+  // k rounds: max of the fp16 probabilities, lowest index on exact ties; lane r keeps round r
+  float tot = 0.0f, mine = 0.0f;
+  int mine_e = 0;
+  for (int r = 0; r < k; ++r) {
+    float best = -1.0f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (p[j] > best) { best = p[j]; bi = lane + 64 * j; }   // ascending index: first max wins
+    const float wb = wave_max(best);
+    float cand = best == wb ? (float)bi : 3.0e38f;
+    cand = -wave_max(-cand);                     // lowest index holding the maximum
+    const int win = (int)cand;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (lane + 64 * j == win) p[j] = -1.0f;    // taken
+    if (lane == r) { mine = wb; mine_e = win; }
+    tot += wb;
+  }
+  gate_r = renorm ? mine / tot : mine;
+  sel_r = mine_e;
+}
+
+// Device bucketing of the T * k selections s_sel (token-major): cnt[e] and list[e][i] = t*k + slot
+// in token order (deterministic), threads striding over the experts.
+__device__ __forceinline__ void bucket_experts(const int* s_sel, int T, int E, int k, int* __restrict__ cnt,
+                                               int* __restrict__ list) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int c = 0;
+    for (int i = 0; i < T * k; ++i)
+      if (s_sel[i] == e) list[(size_t)e * T + c++] = i;
+    cnt[e] = c;
+  }
+}
+
 // One wavefront per token (tokens w, w + W, ... for the workgroup's W wavefronts); lane l owns
 // experts l, l + 64, ..., l + 64 * (J - 1), J = ceil(E / 64) rounded up to an instantiated count.
 template <int J>
@@ -29,58 +87,156 @@ __global__ __launch_bounds__(1024) void moe_topk_kernel(const float* __restrict_
   for (int tt = wave; tt < T; tt += nw) {
     const float* lr = logits + (size_t)tt * E;
     float lg[J];
-    float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int e = lane + 64 * j;
       lg[j] = e < E ? lr[e] : -INFINITY;
-      m = fmaxf(m, lg[j]);
     }
-    m = wave_max(m);
-    float ex[J];
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      ex[j] = lane + 64 * j < E ? expf(lg[j] - m) : 0.0f;
-      sum += ex[j];
-    }
-    const float inv = 1.0f / wave_sum(sum);
-    // probabilities rounded to fp16 (-1 marks experts this lane does not own)
-    float p[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) p[j] = lane + 64 * j < E ? (float)(half_t)(ex[j] * inv) : -1.0f;
-    // k rounds: max of the fp16 probabilities, lowest index on exact ties; lane r keeps round r
-    float tot = 0.0f, mine = 0.0f;
-    int mine_e = 0;
-    for (int r = 0; r < k; ++r) {
-      float best = -1.0f;
-      int bi = 0x7fffffff;
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-        if (p[j] > best) { best = p[j]; bi = lane + 64 * j; }   // ascending index: first max wins
-      const float wb = wave_max(best);
-      float cand = best == wb ? (float)bi : 3.0e38f;
-      cand = -wave_max(-cand);                   // lowest index holding the maximum
-      const int win = (int)cand;
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-        if (lane + 64 * j == win) p[j] = -1.0f;  // taken
-      if (lane == r) { mine = wb; mine_e = win; }
-      tot += wb;
-    }
+    float g_r;
+    int s_r;
+    topk_token<J>(lg, lane, E, k, renorm, g_r, s_r);
     if (lane < k) {
-      gate[(size_t)tt * k + lane] = renorm ? mine / tot : mine;
-      sel[(size_t)tt * k + lane] = mine_e;
-      s_sel[tt * k + lane] = mine_e;
+      gate[(size_t)tt * k + lane] = g_r;
+      sel[(size_t)tt * k + lane] = s_r;
+      s_sel[tt * k + lane] = s_r;
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int c = 0;
-    for (int i = 0; i < T * k; ++i)
-      if (s_sel[i] == e) list[(size_t)e * T + c++] = i;
-    cnt[e] = c;
+  bucket_experts(s_sel, T, E, k, cnt, list);
+}
+
+// The router in one workgroup for a decode batch (T <= 16 tokens, E <= 16 experts, D <= 4096):
+// RMSNorm of h into hn (global and LDS), the logits hn @ router^T on MFMA, then top-k and
+// bucketing.  Each part repeats the arithmetic of the stand-alone kernels step for step, so the
+// outputs are those of afx_rmsnorm + afx_linear (fp16 router, fp32 logits, from 4 rows up, where
+// afx_linear takes MFMA) + afx_moe_topk, bit for bit: the norm's per-thread partials of a 256-thread row reduction (lane l adds thread
+// l + 64j's chunks into partial j, each partial summed across the wavefront, then the four in
+// order), and the logits' K ranges, MFMA order and cross-wavefront sum of the skinny MFMA kernel
+// with NWR wavefronts (its choice for this K).
+constexpr int kRouteMaxD = 4096;
+constexpr int kRouteRow = kRouteMaxD + 8;          // halves per LDS row of hn (16 bytes of padding)
+template <int NWR>
+__global__ __launch_bounds__(1024) void moe_route_kernel(const half_t* __restrict__ h, int ldh,
+                                                         const half_t* __restrict__ gamma, float eps,
+                                                         const half_t* __restrict__ router, int T, int E, int D,
+                                                         int k, int renorm, half_t* __restrict__ hn, int ldo,
+                                                         float* __restrict__ logits_out, float* __restrict__ gate,
+                                                         int* __restrict__ sel, int* __restrict__ cnt,
+                                                         int* __restrict__ list) {
+  __shared__ __align__(16) half_t hn_l[16][kRouteRow];
+  __shared__ f4 red[NWR][64];
+  __shared__ float lg_l[16][16];                   // [token][expert]
+  __shared__ int s_sel[16 * 64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nv = D >> 3;                           // 16-byte chunks of a row
+  constexpr int kCh = kRouteMaxD / 8 / 64;         // chunks per lane (lane l: chunks l + 64 i)
+  // RMSNorm: wavefront t normalises token t, every load issued before the first sum
+  if (wave < T) {
+    const u4* xr = (const u4*)(h + (size_t)wave * ldh);
+    const u4* gr = (const u4*)gamma;
+    u4 xv[kCh], gv[kCh];
+#pragma unroll
+    for (int i = 0; i < kCh; ++i) {
+      const int f = lane + 64 * i < nv ? lane + 64 * i : 0;
+      xv[i] = xr[f];
+      gv[i] = gr[f];
+    }
+    // thread 64 j + l of the 256-thread reduction holds chunks l + 64 j + 256 m, m = 0, 1, ...
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float part = 0.0f;
+#pragma unroll
+      for (int i = j; i < kCh; i += 4) {
+        float q = dot2(as_h2(xv[i].x), as_h2(xv[i].x), 0.0f);
+        q = dot2(as_h2(xv[i].y), as_h2(xv[i].y), q);
+        q = dot2(as_h2(xv[i].z), as_h2(xv[i].z), q);
+        q = dot2(as_h2(xv[i].w), as_h2(xv[i].w), q);
+        part += lane + 64 * i < nv ? q : 0.0f;
+      }
+      ss += wave_sum(part);
+    }
+    const float rstd = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    u4* yr = (u4*)(hn + (size_t)wave * ldo);
+#pragma unroll
+    for (int i = 0; i < kCh; ++i) {
+      if (lane + 64 * i >= nv) break;
+      uint32_t* xw = (uint32_t*)&xv[i];
+      const uint32_t* gw = (const uint32_t*)&gv[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const h2 xx = as_h2(xw[j]), gg = as_h2(gw[j]);
+        h2 o;
+        o.x = (half_t)(((float)xx.x * rstd) * (float)gg.x);
+        o.y = (half_t)(((float)xx.y * rstd) * (float)gg.y);
+        xw[j] = as_u32(o);
+      }
+      yr[lane + 64 * i] = xv[i];
+      *(u4*)&hn_l[wave][8 * (lane + 64 * i)] = xv[i];
+    }
   }
+  __syncthreads();
+  // logits on MFMA: wavefront w < NWR takes steps [nsteps * w / NWR, nsteps * (w + 1) / NWR) of 32;
+  // all of its router loads are issued before the first product (buffer loads: a step past the
+  // range reads zeros)
+  const int r = lane & 15, g = lane >> 4;
+  const int nsteps = D >> 5;
+  constexpr int kMaxSteps = 16;                    // steps per wavefront for D <= 4096 under route_waves
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (wave < NWR) {
+    const int s0 = nsteps * wave / NWR, s1 = nsteps * (wave + 1) / NWR;
+    const __amdgpu_buffer_rsrc_t rrs = make_rsrc(router, E * D * 2);
+    const int arow = (r < E ? r : E - 1) * D;     // rows past E computed, not kept
+    u4 av[kMaxSteps];
+#pragma unroll
+    for (int i = 0; i < kMaxSteps; ++i)
+      av[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rrs, s0 + i < s1 ? (arow + 32 * (s0 + i) + 8 * g) * 2 : 0x7fff0000, 0, 0));
+#pragma unroll
+    for (int i = 0; i < kMaxSteps; ++i) {
+      if (s0 + i >= s1) break;                     // wavefront-uniform
+      const int s = s0 + i;
+      const u4 bv = r < T ? *(const u4*)&hn_l[r][32 * s + 8 * g] : (u4){0u, 0u, 0u, 0u};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, av[i]), __builtin_bit_cast(h8, bv), acc, 0, 0, 0);
+    }
+    red[wave][lane] = acc;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = acc[i];
+#pragma unroll
+    for (int w = 1; w < NWR; ++w) {
+      const f4 q = red[w][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += q[i];
+    }
+    // lane: token r, experts 4g .. 4g + 3
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * g + i;
+      if (r < T && e < E) {
+        lg_l[r][e] = v[i];
+        if (logits_out) logits_out[(size_t)r * E + e] = v[i];
+      }
+    }
+  }
+  __syncthreads();
+  // top-k: wavefront t routes token t
+  if (wave < T) {
+    float lg[1] = {lane < E ? lg_l[wave][lane] : -INFINITY};
+    float g_r;
+    int s_r;
+    topk_token<1>(lg, lane, E, k, renorm, g_r, s_r);
+    if (lane < k) {
+      gate[(size_t)wave * k + lane] = g_r;
+      sel[(size_t)wave * k + lane] = s_r;
+      s_sel[wave * k + lane] = s_r;
+    }
+  }
+  __syncthreads();
+  bucket_experts(s_sel, T, E, k, cnt, list);
 }
 
 struct MoeArgs {
@@ -199,6 +355,27 @@ __global__ void moe_combine_kernel(const half_t* __restrict__ h, const float* __
   for (int s = 0; s < k; ++s) {
     const float ys = (float)(half_t)y[((size_t)t * k + s) * D + d];
     acc = __builtin_fmaf(gate[(size_t)t * k + s], ys, acc);
+  }
+  float c = (float)(half_t)acc;
+  if (shared) c = (float)(half_t)(c + (float)shared[i]);
+  out[i] = (half_t)((float)h[i] + c);
+}
+
+// The K-split down's finishing sum fused with the combine: y[row][d] = the S slices of ws summed in
+// slice order (the finishing kernel's order), then as moe_combine_kernel; with S = 1, ws is y.
+__global__ void moe_combine_ws_kernel(const half_t* __restrict__ h, const float* __restrict__ ws, int S,
+                                      long long slice, const float* __restrict__ gate,
+                                      const half_t* __restrict__ shared, half_t* __restrict__ out, int T, int k,
+                                      int D) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)T * D) return;
+  const int t = (int)(i / D), d = (int)(i - (long long)t * D);
+  float acc = 0.0f;
+  for (int s = 0; s < k; ++s) {
+    const float* yp = ws + ((size_t)t * k + s) * D + d;
+    float v = 0.0f;
+    for (int q = 0; q < S; ++q) v += yp[(size_t)q * slice];
+    acc = __builtin_fmaf(gate[(size_t)t * k + s], (float)(half_t)v, acc);
   }
   float c = (float)(half_t)acc;
   if (shared) c = (float)(half_t)(c + (float)shared[i]);
@@ -356,6 +533,62 @@ int afx_moe_down(int fmt, const void* w, const void* scale, const void* act, int
   a.s_es = fmt_scale_halves(fmt, D, F);
   const int R = rows_hint == 1 || rows_hint == 2 || rows_hint == 4 ? rows_hint : 4;
   return moe_launch(fmt, a, E, R, (hipStream_t)stream, "afx_moe_down");
+}
+
+// The skinny MFMA kernel's wavefront count for a dense fp16 linear of K = D (the persistent kernel's
+// if each wavefront then has at most one batch, else the tile kernel's), so the fused router
+// splits K as afx_linear would.
+static int route_waves(int D) {
+  const int nsteps = D / 32;
+  for (int w = 16; w >= 4; w >>= 1)
+    if (nsteps >= w && (nsteps + w - 1) / w <= 4) return w;
+  auto batches = [&](int w) { return ((nsteps + w - 1) / w + 3) / 4; };
+  return batches(4) <= 4 ? 4 : batches(8) <= 4 ? 8 : 16;
+}
+
+int afx_moe_route(const void* h, int ldh, const void* gamma, float eps, const void* router, int T, int E, int D,
+                  int k, int renorm, void* hn, int ldo, float* logits, float* gate, int* sel, int* cnt, int* list,
+                  void* stream) {
+  AFX_REQUIRE(h && gamma && router && hn && gate && sel && cnt && list, "afx_moe_route: null pointer");
+  AFX_REQUIRE(T >= 1 && T <= 16 && E >= 1 && E <= 16 && k >= 1 && k <= E,
+              "afx_moe_route: needs 1 <= T <= 16 and 1 <= k <= E <= 16; got T=%d E=%d k=%d", T, E, k);
+  AFX_REQUIRE(D % 32 == 0 && D >= 256 && D <= kRouteMaxD, "afx_moe_route: D=%d must be a multiple of 32 in [256, %d]",
+              D, kRouteMaxD);
+  AFX_REQUIRE(ldh % 8 == 0 && ldo % 8 == 0 && ldh >= D && ldo >= D &&
+                  (((uintptr_t)h | (uintptr_t)gamma | (uintptr_t)router | (uintptr_t)hn) & 15) == 0,
+              "afx_moe_route: rows must be 16-byte aligned (ldh, ldo multiples of 8)");
+  const int nw = route_waves(D);
+  AFX_REQUIRE((D / 32 + nw - 1) / nw <= 16, "afx_moe_route: D=%d splits into more than 16 steps per wavefront", D);
+  auto fn = nw == 4 ? moe_route_kernel<4> : nw == 8 ? moe_route_kernel<8> : moe_route_kernel<16>;
+  hipLaunchKernelGGL(fn, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const half_t*)h, ldh, (const half_t*)gamma,
+                     eps, (const half_t*)router, T, E, D, k, renorm, (half_t*)hn, ldo, logits, gate, sel, cnt, list);
+  return check_launch("afx_moe_route");
+}
+
+int afx_moe_down_combine(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F,
+                         int D, const int* cnt, const int* list, float* y, void* ws, long long ws_bytes,
+                         const void* h, const float* gate, const void* shared, void* out, void* stream) {
+  AFX_REQUIRE(h && gate && out && y, "afx_moe_down_combine: null pointer");
+  int S = 1;
+  if (mfma_supported(fmt, F) && D % 4 == 0) {
+    MfmaArgs m = {};
+    m.w = w; m.scale = (const half_t*)scale; m.x = (const half_t*)act; m.ldx = F; m.y = y; m.ldy = D;
+    m.cnt = cnt; m.list = list; m.T = T; m.k = k; m.x_by_token = 0; m.N = D; m.K = F; m.epi = EPI_F32;
+    m.w_es = fmt_row_bytes(fmt, F) * D;
+    m.s_es = fmt == FMT_Q4 || fmt == FMT_BW ? (long long)D * (F / 32) : fmt == FMT_I8 ? (long long)D : 0;
+    m.ws = (float*)ws; m.ws_bytes = ws ? ws_bytes : 0;
+    AFX_REQUIRE(T >= 1 && k >= 1 && E >= 1, "afx_moe_down_combine: bad sizes");
+    const int rc = mfma_launch(fmt, m, E, (hipStream_t)stream, "afx_moe_down_combine", &S);
+    if (rc) return rc;
+  } else {
+    const int rc = afx_moe_down(fmt, w, scale, act, T, k, E, F, D, cnt, list, y, 0, nullptr, 0, stream);
+    if (rc) return rc;
+  }
+  const long long n = (long long)T * D;
+  hipLaunchKernelGGL(moe_combine_ws_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const half_t*)h, S > 1 ? (const float*)ws : (const float*)y, S, (long long)T * k * D, gate,
+                     (const half_t*)shared, (half_t*)out, T, k, D);
+  return check_launch("afx_moe_down_combine");
 }
 
 int afx_moe_combine(const void* h, const float* y, const float* gate, const void* shared, void* out, int T, int k,

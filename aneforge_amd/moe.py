@@ -144,13 +144,16 @@ class MoEDecode:
         """MoE MLP + residual on h [T, D] in place, with bound buffers b (T <= buffer rows)."""
         from . import _kernels as K
         T = h.shape[0]
-        K.rmsnorm(h, self.norm, self.eps, y=b["hn"][:T])
-        K.linear("fp16", self.router.w, None, b["hn"][:T], y=b["logits"][:T], out_f32=True)
-        K.moe_topk(b["logits"][:T], self.k, self.renorm, b["gate"][:T], b["sel"][:T], b["cnt"], b["list"])
+        if K.moe_route_supported(h, self.router.w, self.k):
+            # norm + router + top-k in one launch (the same bits as the three below)
+            K.moe_route(h, self.norm, self.eps, self.router.w, self.k, self.renorm, b["hn"][:T], b["gate"][:T],
+                        b["sel"][:T], b["cnt"], b["list"])
+        else:
+            K.rmsnorm(h, self.norm, self.eps, y=b["hn"][:T])
+            K.linear("fp16", self.router.w, None, b["hn"][:T], y=b["logits"][:T], out_f32=True)
+            K.moe_topk(b["logits"][:T], self.k, self.renorm, b["gate"][:T], b["sel"][:T], b["cnt"], b["list"])
         K.moe_gateup(self.gu.fmt, self.gu.w, self.gu.scale, b["hn"][:T], self.k, self.E, self.F, b["cnt"],
                      b["list"], act=b["act"][:T * self.k])
-        K.moe_down(self.down.fmt, self.down.w, self.down.scale, b["act"][:T * self.k], T, self.k, self.E,
-                   self.F, self.D, b["cnt"], b["list"], y=b["y"][:T * self.k], ws=b["ws"])
         shared = None
         if self.shared:
             K.linear_swiglu(self.sh_gu.fmt, self.sh_gu.w, self.sh_gu.scale, b["hn"][:T], act=b["sh_act"][:T])
@@ -161,7 +164,10 @@ class MoEDecode:
             K._hip.call("afx_ew_binary", K.EW["mul"], K.P(b["sh_y"]), K._ll([self.D, 1]), K.P(b["sh_gs"]),
                         K._ll([1, 0]), K.P(b["sh"]), 2, K._ii(shape), K.stream())
             shared = b["sh"][:T]
-        K.moe_combine(h, b["y"][:T * self.k], b["gate"][:T], shared=shared, out=h)
+        # the experts' down projection and the gate-weighted combine + residual, in place on h
+        K.moe_down_combine(self.down.fmt, self.down.w, self.down.scale, b["act"][:T * self.k], T, self.k, self.E,
+                           self.F, self.D, b["cnt"], b["list"], b["y"][:T * self.k], h, b["gate"][:T],
+                           shared=shared, out=h, ws=b["ws"])
 
     def enqueue(self, eng):
         self.run(eng.h, self._bufs)

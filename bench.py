@@ -234,8 +234,9 @@ def bench_moe(args):
     renormalisation, 16 tokens, fp16 router ~N(0, 0.02), gamma = 1, h ~N(0, 1).  Expert codes are
     uniform nibbles written straight into the superblock layout on the device (the layout is a
     bit-preserving permutation of GGUF Q4_0), block scales |N(0, 0.02)| / 8.  Timed as a captured
-    graph of the whole layer (norm, router, top-k + bucketing, grouped gate/up + SwiGLU, grouped
-    down, weighted combine + residual); algorithmic bytes = distinct active experts x 99 090 432 B
+    graph of the whole layer as the decode engine runs it: norm + router + top-k + bucketing in one
+    launch, grouped gate/up + SwiGLU, grouped down (K-split) with the weighted combine + residual;
+    algorithmic bytes = distinct active experts x 99 090 432 B
     + router + activations."""
     import torch
     from aneforge_amd import _kernels as K
@@ -259,14 +260,10 @@ def bench_moe(args):
     y = torch.empty((T * k, D), dtype=torch.float32, device="cuda")
     ws = torch.empty(8 * T * k * D, dtype=torch.float32, device="cuda")   # K-split partials of the down
 
-    def layer():
-        K.rmsnorm(h, gamma, 1e-5, y=hn)
-        for r0 in range(0, T, 8):
-            K.linear("fp16", router, None, hn[r0:r0 + 8], y=logits[r0:r0 + 8], out_f32=True)
-        K.moe_topk(logits, k, True, gate, sel, cnt, lst)
+    def layer():                          # the launches of MoEDecode.run (aneforge_amd/moe.py)
+        K.moe_route(h, gamma, 1e-5, router, k, True, hn, gate, sel, cnt, lst)
         K.moe_gateup("q4_0", gu_w, gu_d, hn, k, E, F, cnt, lst, act=act)
-        K.moe_down("q4_0", dn_w, dn_d, act, T, k, E, F, D, cnt, lst, y=y, ws=ws)
-        K.moe_combine(h, y, gate, out=hout)
+        K.moe_down_combine("q4_0", dn_w, dn_d, act, T, k, E, F, D, cnt, lst, y, h, gate, out=hout, ws=ws)
 
     layer()
     torch.cuda.synchronize()

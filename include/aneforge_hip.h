@@ -225,6 +225,21 @@ int afx_topk_mask(const void* x, int T, int E, int k, void* y, void* stream);
 /* h + sum_e gate * y_e (+ shared expert) (moe.py:59-63) */
 int afx_moe_combine(const void* h, const float* y, const float* gate, const void* shared, void* out, int T,
                     int k, int D, void* stream);
+/* The layer's routing for a decode batch in one launch: hn = RMSNorm(h) (the MLP norm before the
+ * router, moe.py:40-63 via llm.py's block), logits = hn @ router^T, then afx_moe_topk's softmax,
+ * top-k, renorm and bucketing (_topk_gate, moe.py:21-37, 55-56); bit for bit the outputs of
+ * afx_rmsnorm + afx_linear (fp16 router, fp32 logits) + afx_moe_topk from T = 4 up (below 4 rows
+ * afx_linear sums on its vector kernels, in another order; these logits are the MFMA ones).  T <= 16, E <= 16,
+ * 256 <= D <= 4096 (D % 32 == 0), 16-byte aligned rows; logits (optional) [T][E] fp32. */
+int afx_moe_route(const void* h, int ldh, const void* gamma, float eps, const void* router, int T, int E, int D,
+                  int k, int renorm, void* hn, int ldo, float* logits, float* gate, int* sel, int* cnt, int* list,
+                  void* stream);
+/* afx_moe_down followed by afx_moe_combine (bmm_weight and the gate-weighted sum, moe.py:58-63), with
+ * the K-split's finishing sum folded into the combine: out is bit for bit that of the two calls. y
+ * [T*k][D] fp32 scratch, ws as for afx_moe_down. */
+int afx_moe_down_combine(int fmt, const void* w, const void* scale, const void* act, int T, int k, int E, int F,
+                         int D, const int* cnt, const int* list, float* y, void* ws, long long ws_bytes,
+                         const void* h, const float* gate, const void* shared, void* out, void* stream);
 
 /* ---- batched prefill --------------------------------------------------------------------- */
 

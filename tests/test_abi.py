@@ -86,3 +86,15 @@ def test_noalloc_attention_rejects_shapes_beyond_its_scratch_without_a_gpu():
     with pytest.raises(RuntimeError, match="head dim"):
         _hip.call("afx_decode_attn_noalloc", 256, 256, 256, 256, 32 * 100, 100, 8 * 64 * 100, 64 * 100,
                   1, 32, 8, 100, 64, None, 64, None, 0, -1, 0.1, 0, None)
+
+
+def test_fused_moe_router_rejects_batches_beyond_one_workgroup_without_a_gpu():
+    # the shape checks are host arithmetic before any launch (non-null dummy addresses)
+    import pytest
+    from aneforge_amd import _hip
+    with pytest.raises(RuntimeError, match="T <= 16"):
+        _hip.call("afx_moe_route", 256, 4096, 256, 1e-5, 256, 17, 8, 4096, 2, 1, 256, 4096, None, 256, 256, 256,
+                  256, None)
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        _hip.call("afx_moe_route", 256, 8192, 256, 1e-5, 256, 4, 8, 8192, 2, 1, 256, 8192, None, 256, 256, 256,
+                  256, None)

@@ -736,6 +736,78 @@ def test_moe_layer_sparse_dispatch(K, fmt):
     check_hidden(out, want, what="moe")           # residual-stream output: fp16-ulp atol
 
 
+@pytest.mark.parametrize("T,E,D,k", [(1, 8, 4096, 2), (5, 4, 256, 1), (16, 8, 4096, 2), (16, 16, 2048, 4),
+                                     (9, 16, 4096, 16), (3, 1, 512, 1)])
+def test_moe_route_is_norm_router_topk_bit_for_bit(K, T, E, D, k):
+    # the one-launch router against the three launches it replaces: hn identical to afx_rmsnorm's,
+    # the logits to afx_linear's from 4 rows up (its MFMA path; below 4 rows it sums on the vector
+    # kernels, in another order), gate, sel and the buckets to afx_moe_topk's on the same logits
+    # (D 2048 takes the 16-wavefront K split, 4096 the 8-wavefront one, 256 / 512 the shortest);
+    # two duplicated router rows give exact logit ties for the tie rule
+    say(f"moe route T={T} E={E} D={D} k={k}")
+    rng = np.random.default_rng(1000 + T * E + k)
+    router = rng.normal(0, 0.05, (E, D)).astype(np.float16)
+    if E >= 4:
+        router[3] = router[1]
+    h = (rng.standard_normal((T, D)) * 2).astype(np.float16)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float16)
+    hd, gd, rd = dev(h), dev(g), dev(router)
+    hn_ref = K.rmsnorm(hd, gd, 1e-5)
+    lg_ref = K.linear("fp16", rd, None, hn_ref, out_f32=True)
+    assert K.moe_route_supported(hd, rd, k)
+    hn = torch.empty_like(hd)
+    lg = torch.empty((T, E), dtype=torch.float32, device="cuda")
+    gate = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    sel = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    cnt = torch.empty((E,), dtype=torch.int32, device="cuda")
+    lst = torch.empty((E, T), dtype=torch.int32, device="cuda")
+    K.moe_route(hd, gd, 1e-5, rd, k, True, hn, gate, sel, cnt, lst, logits=lg)
+    assert np.array_equal(host(hn).view(np.uint16), host(hn_ref).view(np.uint16)), "hn"
+    if T >= 4:
+        assert np.array_equal(host(lg).view(np.uint32), host(lg_ref).view(np.uint32)), "logits"
+    else:
+        np.testing.assert_allclose(host(lg), host(lg_ref), rtol=1e-5, atol=1e-6)
+    gate_ref, sel_ref, cnt_ref, lst_ref = K.moe_topk(lg, k, renorm=True)
+    assert np.array_equal(host(gate).view(np.uint32), host(gate_ref).view(np.uint32)), "gate"
+    assert np.array_equal(host(sel), host(sel_ref)), "sel"
+    c = host(cnt)
+    assert np.array_equal(c, host(cnt_ref)), "cnt"
+    lr, lw = host(lst), host(lst_ref)
+    for e in range(E):
+        assert np.array_equal(lr[e, :c[e]], lw[e, :c[e]]), f"list of expert {e}"
+
+
+@pytest.mark.parametrize("fmt,F,shared", [("q4_0", 14336, False), ("q4_0", 768, True), ("int8", 11008, True)])
+def test_moe_down_combine_is_down_then_combine_bit_for_bit(K, fmt, F, shared):
+    # F = 14336 / 11008 cut the expert rows into K slices whose finishing sum the fused combine does;
+    # F = 768 writes y directly; with a shared expert output added last
+    say(f"moe down+combine fmt={fmt} F={F} shared={shared}")
+    from aneforge_amd import _blob
+    rng = np.random.default_rng(F + len(fmt))
+    E, k, T, D = 8, 2, 16, 512
+    Wd = rng.normal(0, 0.05, (E, D, F)).astype(np.float32)
+    if fmt == "q4_0":
+        dn = [_blob.q4_0_to_superblock(_blob.quantize_q4_0(Wd[e]), D, F) for e in range(E)]
+    else:
+        dn = [_blob.quantize_per_row(Wd[e]) for e in range(E)]
+    wdn, sdn = dev(np.stack([a for a, _ in dn])), dev(np.stack([b for _, b in dn]))
+    lg = dev(rng.standard_normal((T, E)).astype(np.float32))
+    gate, sel, cnt, lst = K.moe_topk(lg, k, renorm=True)
+    act = dev((rng.standard_normal((T * k, F)) * 0.5).astype(np.float16))
+    h = dev(rng.standard_normal((T, D)).astype(np.float16))
+    sh = dev(rng.standard_normal((T, D)).astype(np.float16)) if shared else None
+    ws = torch.empty(8 * T * k * D, dtype=torch.float32, device="cuda")
+    y = K.moe_down(fmt, wdn, sdn, act, T, k, E, F, D, cnt, lst, ws=ws)
+    want = host(K.moe_combine(h, y, gate, shared=sh))
+    y2 = torch.empty((T * k, D), dtype=torch.float32, device="cuda")
+    got = host(K.moe_down_combine(fmt, wdn, sdn, act, T, k, E, F, D, cnt, lst, y2, h, gate, shared=sh, ws=ws))
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    # in place on h, as the decode engine calls it
+    h2 = h.clone()
+    K.moe_down_combine(fmt, wdn, sdn, act, T, k, E, F, D, cnt, lst, y2, h2, gate, shared=sh, out=h2, ws=ws)
+    assert np.array_equal(host(h2).view(np.uint16), want.view(np.uint16))
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "int8"])
 def test_moe_gateup_units_cross_experts_and_skip_empty_ones(K, fmt):
     # 12 tokens top-2 over 5 experts, expert 2 routed no token; 2100 intermediate rows (263

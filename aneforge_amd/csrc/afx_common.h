@@ -139,7 +139,8 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // tie, and the loser's first value competes for second place (an exact tie makes them equal).
 __device__ __forceinline__ float4 top2_merge(float4 a, float4 b) {
   const int ia = __float_as_int(a.y), ib = __float_as_int(b.y);
-  const bool a_first = a.x > b.x || (a.x == b.x && ia < ib);
+  // non-short-circuit operators: three compares combined in lane masks, no branch
+  const bool a_first = (a.x > b.x) | ((a.x == b.x) & (ia < ib));
   const float4 f = a_first ? a : b, o = a_first ? b : a;
   return float4{f.x, f.y, fmaxf(f.z, o.x), fmaxf(a.w, b.w)};
 }

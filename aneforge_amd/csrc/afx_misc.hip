@@ -209,72 +209,91 @@ __device__ __forceinline__ float4 top2_wave(float4 v) {
                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.w), 63))};
 }
 
-__global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
-  __shared__ float4 wpart[16];
-  __shared__ double xbest[16];
-  __shared__ int xidx[16];
-  __shared__ int chosen, near_tie;
-  __shared__ float4 top_all;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
+// The merged summary of the 16 per-wavefront summaries in lanes 0-15 (the other lanes hold the
+// neutral summary), wave-uniform: the row shifts of top2_wave, read from lane 15.
+__device__ __forceinline__ float4 top2_row0(float4 v) {
+  v = top2_dpp<0x111, 0xf>(v);   // row_shr:1
+  v = top2_dpp<0x112, 0xf>(v);   // row_shr:2
+  v = top2_dpp<0x114, 0xf>(v);   // row_shr:4
+  v = top2_dpp<0x118, 0xf>(v);   // row_shr:8: lane 15 holds row 0's summary
+  return float4{__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.x), 15)),
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.y), 15)),
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.z), 15)),
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v.w), 15))};
+}
+
+constexpr int kAdvThreads = 1024;   // the launch's workgroup size (16 wavefronts)
+
+// Every wavefront merges the 16 per-wavefront summaries itself and derives the same pick, so the
+// common step (no near tie) has one barrier: the summary loads go out as soon as the arguments
+// arrive, the step state's loads overlap them, and the token row is gathered by all threads
+// while thread 0 records the token.
+__global__ __launch_bounds__(kAdvThreads) void decode_advance_kernel(AdvanceArgs a) {
+  constexpr int NT = kAdvThreads, NW = NT / 64;
+  __shared__ float4 wpart[NW];
+  __shared__ double xbest[NW];
+  __shared__ int xidx[NW];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const float4 none = float4{-INFINITY, __int_as_float(0x7fffffff), -INFINITY, 0.0f};
-  // 1. every load that does not depend on the pick: the step state, the margin, the summaries
+  // 1. the step state and the margin, with no wait: their values are needed after the summaries
+  // (an absent optional input reads the step word instead, and the value is not used)
   const int s = a.step[0];
   const int p0 = a.pos[0];
-  const int nf = a.n_forced ? a.n_forced[0] : 0;
-  const float margin = a.margin ? a.margin[0] : 0.0f;
+  const int nfr = *(a.n_forced ? a.n_forced : a.step);
+  const float mraw = *(a.margin ? a.margin : (const float*)a.step);
+  // 2. the summaries (or the logits): the long pole
   float4 acc = none;
   if (a.slots) {
     const int ns = (a.V + 7) >> 3;
-    for (int b0 = 0; b0 < ns; b0 += 4 * (int)blockDim.x) {
+    for (int b0 = 0; b0 < ns; b0 += 4 * NT) {
       float4 v[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = b0 + j * (int)blockDim.x + t;
-        v[j] = i < ns ? a.slots[i] : none;
+        const int i = b0 + j * NT + t;
+        v[j] = a.slots[i < ns ? i : ns - 1];   // a clamped duplicate is replaced below
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc = top2_merge(acc, v[j]);
+      for (int j = 0; j < 4; ++j) acc = top2_merge(acc, b0 + j * NT + t < ns ? v[j] : none);
     }
   } else if (a.logits) {
-    for (int b0 = 0; b0 < a.V; b0 += 8 * (int)blockDim.x) {
+    for (int b0 = 0; b0 < a.V; b0 += 8 * NT) {
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int i = b0 + j * (int)blockDim.x + t;
-        v[j] = i < a.V ? a.logits[i] : -INFINITY;
+        const int i = b0 + j * NT + t;
+        v[j] = a.logits[i < a.V ? i : a.V - 1];
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int i = b0 + j * (int)blockDim.x + t;
+        const int i = b0 + j * NT + t;
         if (i < a.V) acc = top2_merge(acc, float4{v[j], __int_as_float(i), -INFINITY, fabsf(v[j])});
       }
     }
   }
+  const int nf = a.n_forced ? nfr : 0;
+  const float margin = a.margin ? mraw : 0.0f;
   const bool use_forced = a.forced && a.n_forced && s < nf;
+  const int fz = use_forced ? a.forced[s] : 0;
   acc = top2_wave(acc);
   if (lane == 0) wpart[wave] = acc;
   __syncthreads();
-  if (t == 0) {
-    float4 top = wpart[0];
-    for (int w = 1; w < nw; ++w) top = top2_merge(top, wpart[w]);
-    top_all = top;
-    int nt = 0;
-    if (!use_forced && (a.logits || a.slots) && a.margin && a.logits && a.hn && (a.head16 || a.head32) &&
-        __builtin_isfinite(top.x) && __builtin_isfinite(top.w)) {
-      const double gap = (double)top.x - (double)top.z;
-      nt = gap < (double)margin * ((double)top.w + 1e-9);
-    }
-    near_tie = nt;
+  // 3. the total, in every wavefront
+  float4 wp = wpart[lane & (NW - 1)];   // one LDS read in every lane; lanes past 15 take the neutral summary
+  asm volatile("" : "+v"(wp.x), "+v"(wp.y), "+v"(wp.z), "+v"(wp.w));
+  const float4 top = top2_row0(lane < NW ? wp : none);
+  bool near_tie = false;
+  if (!use_forced && a.margin && a.logits && a.hn && (a.head16 || a.head32) &&
+      __builtin_isfinite(top.x) && __builtin_isfinite(top.w)) {
+    const double gap = (double)top.x - (double)top.z;
+    near_tie = gap < (double)margin * ((double)top.w + 1e-9);
   }
-  __syncthreads();
-  int pick = __float_as_int(top_all.y);
+  int pick = __float_as_int(top.y);
   if (near_tie) {
     // every logit within the window of the largest, recomputed exactly; one wavefront per candidate
-    const float4 top = top_all;
     const double lo = (double)top.x - (double)margin * ((double)top.w + 1e-9);
     double best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int base = wave * 64; base < a.V; base += nw * 64) {
+    for (int base = wave * 64; base < a.V; base += NT) {
       const int i = base + lane;
       const float lv = i < a.V ? a.logits[i] : -INFINITY;
       unsigned long long m = __ballot((double)lv >= lo);
@@ -296,31 +315,27 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(AdvanceArgs a) {
     }
     if (lane == 0) { xbest[wave] = best; xidx[wave] = bi; }
     __syncthreads();
-    if (t == 0) {
-      double b = xbest[0];
-      int bx = xidx[0];
-      for (int w = 1; w < nw; ++w)
-        if (xbest[w] > b || (xbest[w] == b && xidx[w] < bx)) { b = xbest[w]; bx = xidx[w]; }
-      if (bx != 0x7fffffff) pick = bx;
-    }
+    double b = xbest[0];
+    int bx = xidx[0];
+    for (int w = 1; w < NW; ++w)
+      if (xbest[w] > b || (xbest[w] == b && xidx[w] < bx)) { b = xbest[w]; bx = xidx[w]; }
+    if (bx != 0x7fffffff) pick = bx;
   }
+  int bidx;
+  if (use_forced) bidx = fz;
+  else if (!a.logits && !a.slots) bidx = 0;   // a forced-only step run past its prompt: inert token
+  else bidx = pick >= a.V || pick < 0 ? 0 : pick;   // all-NaN logits: deterministic fallback
+  bidx = bidx < 0 ? 0 : (bidx >= a.vocab ? a.vocab - 1 : bidx);
   if (t == 0) {
-    int bidx;
-    if (use_forced) bidx = a.forced[s];
-    else if (!a.logits && !a.slots) bidx = 0;   // a forced-only step run past its prompt: inert token
-    else bidx = pick >= a.V || pick < 0 ? 0 : pick;   // all-NaN logits: deterministic fallback
-    bidx = bidx < 0 ? 0 : (bidx >= a.vocab ? a.vocab - 1 : bidx);
-    chosen = bidx;
     a.tok[0] = bidx;
     if (s < a.hist_cap) a.hist[s] = bidx;
     a.step[0] = s + 1;
     a.pos[0] = p0 + 1;
   }
-  __syncthreads();
   if (a.embed) {
-    const u4* src = (const u4*)(a.embed + (size_t)chosen * a.D);
+    const u4* src = (const u4*)(a.embed + (size_t)bidx * a.D);
     u4* dst = (u4*)a.h;
-    for (int i = t; i < a.D / 8; i += blockDim.x) dst[i] = src[i];
+    for (int i = t; i < a.D / 8; i += NT) dst[i] = src[i];
   }
 }
 
@@ -854,7 +869,7 @@ int afx_decode_advance(const float* logits, const float* slots, int V, const flo
   a.hn = (const half_t*)hn; a.head16 = (const half_t*)head16; a.head32 = head32;
   a.forced = forced; a.n_forced = n_forced; a.tok = tok; a.pos = pos; a.hist = hist; a.hist_cap = hist_cap;
   a.step = step; a.embed = (const half_t*)embed; a.h = (half_t*)h; a.D = D; a.vocab = vocab > 0 ? vocab : V;
-  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(kAdvThreads), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_advance");
 }
 

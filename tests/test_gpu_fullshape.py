@@ -69,7 +69,7 @@ def test_cfg3_full_model_parity_128_steps():
         mixer.vc[0, :, :P].copy_(torch.from_numpy(v))
     d.reset([tok0], pos0=P, zero_state=False)
     say("cfg3 device: step 0 layer by layer, then per-token steps, then the same steps as graph replays")
-    hs, finals, logits = [], [], []
+    hs, finals, logits, hns = [], [], [], []
     with torch.cuda.stream(d.stream):
         for mixer, mlp in d.layers:
             mixer.enqueue(d)
@@ -78,12 +78,14 @@ def test_cfg3_full_model_parity_128_steps():
         finals.append(d.h.clone())
         d.enqueue_head()
         logits.append(d.logits.clone())
+        hns.append(d.hn.clone())
         d.enqueue_advance(True)
         for _ in range(1, STEPS):
             d.enqueue_layers()
             finals.append(d.h.clone())
             d.enqueue_head()
             logits.append(d.logits.clone())
+            hns.append(d.hn.clone())
             d.enqueue_advance(True)
     toks = d.history(0, STEPS)
     last = d.logits_host().copy()
@@ -94,7 +96,14 @@ def test_cfg3_full_model_parity_128_steps():
     hs = [t.float().cpu().numpy()[0] for t in hs]
     finals = np.stack([t.float().cpu().numpy()[0] for t in finals])
     logits = np.stack([t.cpu().numpy()[0] for t in logits])
+    hns = np.stack([t.cpu().numpy() for t in hns])
     m.release()
+
+    # every greedy token is the exact argmax of the fp16 head over the device's own normalised row
+    # (fp16 x fp16 products are exact in float64): the near-tie rule recomputes exactly, and a clear
+    # gap (>= the margin) is far beyond the fp32 logits' rounding
+    exact = hns.astype(np.float64) @ head.astype(np.float64).T
+    assert [int(np.argmax(r)) for r in exact] == toks, "greedy tokens differ from the exact head argmax"
 
     say("cfg3 oracle: teacher-forced rows, one layer at a time")
     oc = {"n_heads": c["n_heads"], "n_kv_heads": KVH, "dh": dh, "norm_eps": c["norm_eps"]}
@@ -143,7 +152,9 @@ def test_cfg3_full_model_parity_128_steps():
             near_ties.append(s)
     err = np.abs(logits - want).max() / np.abs(want).max()
     say(f"cfg3: {STEPS} steps, tokens equal except near-ties at {near_ties}; free-running logits max rel err {err:.2e}")
-    assert len(near_ties) <= 2
+    # the free-running oracle drifts from the device's fp16 hidden states (err above), so a step whose
+    # top two logits lie closer than that drift can rank them either way: allow a few such steps
+    assert len(near_ties) <= STEPS // 25
 
 
 def test_cfg4_moe_layer_full_shape():

@@ -668,6 +668,64 @@ def test_decode_advance_near_tie_recomputes_exactly(K):
     clear = lg.copy()
     clear[100] += 1.0
     assert step_once(clear, 3e-3) == 100                            # a clear gap: no recompute
+    # the same rule when the pick comes from the lm_head's slot summaries
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    K.decode_advance(dev(lg[None]), tok, torch.zeros(1, dtype=torch.int32, device="cuda"),
+                     torch.zeros(4, dtype=torch.int32, device="cuda"), torch.zeros(1, dtype=torch.int32, device="cuda"),
+                     slots=dev(_host_slots(lg)), tie_margin=torch.tensor([3e-3], dtype=torch.float32, device="cuda"),
+                     hn=dev(hn), head32=dev(W32))
+    assert int(host(tok)[0]) == 900
+
+
+def _host_slots(lg):
+    """The lm_head's greedy-pick summaries of 8 logits each (largest, its lowest index as int32
+    bits, second largest, largest magnitude), built on the host."""
+    V = lg.size
+    ns = (V + 7) // 8
+    r = np.full(ns * 8, -np.inf, np.float32)
+    r[:V] = lg
+    r = r.reshape(ns, 8)
+    i1 = r.argmax(1)
+    rows = np.arange(ns)
+    r2 = r.copy()
+    r2[rows, i1] = -np.inf
+    out = np.zeros((ns, 4), np.float32)
+    out[:, 0] = r[rows, i1]
+    out[:, 1] = (8 * rows + i1).astype(np.int32).view(np.float32)
+    out[:, 2] = r2.max(1)
+    out[:, 3] = np.abs(np.where(np.isfinite(r), r, 0.0)).max(1)
+    return out
+
+
+@pytest.mark.parametrize("V", [32000, 152064, 77, 8])
+def test_decode_advance_from_slots_is_the_argmax(K, V):
+    """The greedy pick from slot summaries (one float4 per 8 logits, several load rounds of the
+    workgroup for a 152k vocabulary) is np.argmax of the logits: the lowest index on a tie across
+    slots and inside one, and the step bookkeeping and embedding gather follow it."""
+    say(f"decode advance from slots V={V}")
+    rng = np.random.default_rng(54 + V)
+    D = 64
+    table = rng.standard_normal((V, D)).astype(np.float16)
+    tb = dev(table)
+    cases = [rng.standard_normal(V).astype(np.float32)]
+    tie = rng.standard_normal(V).astype(np.float32)
+    hi = sorted(rng.choice(V, size=min(V, 3), replace=False).tolist())
+    tie[hi] = tie.max() + 1.0                                       # tie across slots: the lowest index
+    cases.append(tie)
+    last = rng.standard_normal(V).astype(np.float32)
+    last[V - 1] = last.max() + 0.5                                  # the maximum in the last (ragged) slot
+    cases.append(last)
+    for lg in cases:
+        tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+        pos = torch.tensor([5], dtype=torch.int32, device="cuda")
+        step = torch.tensor([1], dtype=torch.int32, device="cuda")
+        hist = torch.full((4,), -1, dtype=torch.int32, device="cuda")
+        h = torch.zeros((1, D), dtype=torch.float16, device="cuda")
+        K.decode_advance(dev(lg[None]), tok, pos, hist, step, tb, h, slots=dev(_host_slots(lg)))
+        want = int(np.argmax(lg))
+        assert int(host(tok)[0]) == want and host(hist)[1] == want
+        assert host(pos)[0] == 6 and host(step)[0] == 2
+        assert np.array_equal(host(h)[0], table[want])
 
 
 # ----------------------------------------------------------------------------- MoE

@@ -476,7 +476,7 @@ class DecodeEngine:
         # sampling: {temperature, top_p, top_k} and one uniform per step, both read on the device
         self.smp_params = torch.zeros(3, dtype=torch.float64, device=dev)
         self.uniforms = torch.zeros(self.M + 8, dtype=torch.float64, device=dev)
-        self.smp_ws = torch.empty(self.V, dtype=torch.float64, device=dev)
+        self.smp_ws = torch.empty(K.sample_ws_elems(self.V), dtype=torch.float64, device=dev)
         if rope_tables is None:
             from .llm import rope_tables as _rt
             rope_tables = _rt(self.M, dh, cfg.rope_base, cfg.rotary_dim, cfg.rope_interleaved, cfg.rope_scaling)

@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple] = {
     # attention
     "afx_decode_attn_ws_bytes": (_ll, [_i, _i, _i, _i, _i, _i]),
     "afx_sample": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _ll, _vp]),
+    "afx_sample_ws_bytes": (_ll, [_i]),
     "afx_decode_attn": (_i, [_vp, _vp, _vp, _vp, _ll, _ll, _ll, _ll, _i, _i, _i, _i, _i, _vp, _i, _vp, _ll,
                              _i, _f, _vp, _ll, _i, _vp]),
     "afx_decode_attn_noalloc": (_i, [_vp, _vp, _vp, _vp, _ll, _ll, _ll, _ll, _i, _i, _i, _i, _i, _vp, _i, _vp,

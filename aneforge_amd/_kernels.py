@@ -228,15 +228,25 @@ def embed(table, ids, out=None):
     return out
 
 
+def sample_ws_elems(V: int) -> int:
+    """float64 elements of the afx_sample workspace for V logits (afx_sample_ws_bytes)."""
+    n = _hip.load().afx_sample_ws_bytes(V)
+    if n < 0:
+        raise ValueError(f"sampling: bad vocabulary size {V}")
+    return (int(n) + 7) // 8
+
+
 def sample(logits, params, uniforms, step=None, forced=None, n_forced=None, out=None, ws=None):
     """Device sampling of the next token from fp32 logits [V] (see afx_sample).  params: float64
-    [3] {temperature, top_p, top_k}; uniforms: float64, u = uniforms[step] (uniforms[0] without step)."""
+    [3] {temperature, top_p, top_k}; uniforms: float64, u = uniforms[step] (uniforms[0] without step);
+    ws: float64 scratch of at least sample_ws_elems(V) elements (allocated when missing or short)."""
     _dev(logits, params, uniforms, step, forced, n_forced, out)
     V = logits.numel()
     if forced is None and out is None:
         out = torch.empty(1, dtype=torch.int32, device=logits.device)
-    if ws is None or ws.numel() < V:
-        ws = torch.empty(V, dtype=torch.float64, device=logits.device)
+    need = sample_ws_elems(V)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.float64, device=logits.device)
     _hip.call("afx_sample", P(logits), V, P(params), P(uniforms), P(step), P(forced), P(n_forced), P(out),
               P(ws), ws.numel() * 8, stream())
     return out

@@ -562,15 +562,81 @@ static int make_shape(Shape5& s, int rank, const int* dim, const long long* sa, 
 
 // ---- temperature / top-k / top-p sampling on the device (the reference's _sample,
 // aneforge/llm.py:406-419, with np.random.choice's inverse-CDF draw) ----
-// One workgroup of 1024 threads.  Logits are ranked by an order-preserving 32-bit key of their
-// fp32 value: logits / T is monotone in the logit and fp32 -> fp64 is exact, so the k-th largest
-// scaled logit and the top-p nucleus are thresholds on that key.  Both thresholds come from a
-// 4-pass radix select (8 bits a pass; counts for top-k, fp64 probability mass for top-p) over
-// per-wavefront LDS histograms.  Ties at the top-p threshold keep the highest indices first (what
-// np.argsort(p)[::-1] gives for tied values in a stably sorted array).  The draw: the first index
-// whose running kept mass (in index order) exceeds u * total, u = uniforms[*step].
-constexpr int kSampleThreads = 1024;
+// Logits are ranked by an order-preserving 32-bit key of their fp32 value: logits / T is monotone
+// in the logit and fp32 -> fp64 is exact, so the k-th largest scaled logit and the top-p nucleus
+// are thresholds on that key.  The selection: the top-k floor (the k-th largest key; ties kept, as
+// lg < kth -> -inf keeps them) and the top-p nucleus edge (the key where the mass from the top
+// first reaches top_p * Z) by 8-bit radix selects over bins of the key.  Ties at the nucleus edge
+// keep the highest indices first (np.argsort(p)[::-1] of a stably sorted array).  The draw: the
+// first index whose running kept mass (in index order) exceeds u * total, u = uniforms[*step].
+// Four launches, so that whole-vocabulary passes run on many CUs:
+// - max, one workgroup per 2048-logit chunk: the chunk's largest key;
+// - prep, one workgroup per chunk: the largest key (from the chunk maxima), e_i = exp(x_i / T -
+//   max / T) in fp64, and per chunk the sum of e and the count and mass of its logits in each of
+//   256 bins of (max - x) / T, T / 8 wide from the top (bin 255 holds the maximum, bin 0 everything
+//   32 T or more below it; masses summed in a fixed order).  The bin is monotone in the key;
+// - gather, one workgroup per chunk: every workgroup merges the bins and derives the same window
+//   of bins that holds what the cut needs: for top-k every bin from the one holding the k-th
+//   largest key up, for top-p alone the one bin holding the nucleus edge (the bins above it are
+//   kept whole).  Each chunk compacts its logits in the window, in index order, into the workspace;
+// - pick, one workgroup of 256 threads: without a cut the draw needs the chunk sums and one chunk;
+//   with a window of at most kSmpCap logits the selection runs on those in LDS (for top-p alone
+//   with the per-chunk mass above the edge for the draw); a larger window runs the selection over
+//   the whole vocabulary.
+constexpr int kSampleThreads = 256;
 constexpr int kSampleWaves = kSampleThreads / 64;
+constexpr int kSmpPrepThreads = 256;
+constexpr int kSmpPer = 8;                                    // logits per prep / gather thread
+constexpr int kSmpChunk = kSmpPrepThreads * kSmpPer;          // logits per chunk
+constexpr int kSmpCap = 6144;                                 // window logits the pick kernel holds in LDS
+constexpr int kSmpMaxChunks = 1024;                           // V <= 2^21
+
+__host__ __device__ inline long long smp_nb(int V) { return ((long long)V + kSmpChunk - 1) / kSmpChunk; }
+__host__ __device__ inline long long smp_stats_off(int V) { return ((long long)V * 8 + 255) / 256 * 256; }
+// The window of bins the cut needs (see the section comment); mode 0: no cut.
+struct SmpWin {
+  int lo, hi, mode;
+  long long ncand;
+  double above;                                      // top-p alone: the mass of the bins above hi
+};
+// Workspace: e[V] (fp64); a 64-byte header (the largest key, the vocabulary's mass, the window);
+// per chunk its sum bsum[NB]; per chunk and bin the mass smass[NB][256] and count scnt[NB][256] of
+// that bin and every bin above it (suffix sums from the top); the window's e ce[cap] (fp64); window
+// offsets coff[NB + 1]; the window's keys ckey[cap] and indices cidx[cap]; chunk maxima cmax[NB].
+struct SmpHdr {
+  unsigned maxkey;
+  int pad;
+  double Z_all;
+  SmpWin win;
+};
+static_assert(sizeof(SmpHdr) <= 64, "sampling workspace header");
+__host__ __device__ inline long long smp_ws_bytes(int V) {
+  const long long nb = smp_nb(V);
+  return smp_stats_off(V) + 64 + nb * 8 + nb * 256 * 8 + (long long)kSmpCap * 8 + nb * 256 * 4 + (nb + 1) * 4 +
+         (long long)kSmpCap * 8 + nb * 4;
+}
+struct SmpWs {
+  SmpHdr* hdr;
+  double *e, *bsum, *smass, *ce;
+  unsigned *scnt, *coff, *ckey, *cmax;
+  int* cidx;
+};
+__device__ __forceinline__ SmpWs smp_ws(double* ws, int V) {
+  unsigned char* s = (unsigned char*)ws + smp_stats_off(V);
+  const long long nb = smp_nb(V);
+  SmpWs w;
+  w.e = ws;
+  w.hdr = (SmpHdr*)s;
+  w.bsum = (double*)(s + 64);
+  w.smass = w.bsum + nb;
+  w.ce = w.smass + nb * 256;
+  w.scnt = (unsigned*)(w.ce + kSmpCap);
+  w.coff = w.scnt + nb * 256;
+  w.ckey = w.coff + nb + 1;
+  w.cidx = (int*)(w.ckey + kSmpCap);
+  w.cmax = (unsigned*)(w.cidx + kSmpCap);
+  return w;
+}
 
 __device__ __forceinline__ uint32_t logit_key(float x) {
   if (x != x) x = -INFINITY;                         // NaN ranks below every number
@@ -585,39 +651,374 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
   return v;
 }
+template <class T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const T o = __shfl_up(v, m, 64);
+    if (lane >= m) v += o;
+  }
+  return v;
+}
+
+// The bin of logit x: 255 - floor((maxv - x) * s) with s = 8 / T, clamped to [0, 255]; NaN and
+// -inf land in bin 0.  Monotone in the key (float subtraction and scaling are monotone).
+__device__ __forceinline__ int smp_bin(float x, float maxv, float s) {
+  if (x != x) return 0;
+  if (!(x < maxv)) return 255;
+  const float d = (maxv - x) * s;
+  return d >= 255.0f ? 0 : 255 - (int)d;
+}
+
+__global__ __launch_bounds__(kSmpPrepThreads) void sample_max_kernel(const float* __restrict__ logits, int V,
+                                                                     const double* __restrict__ params,
+                                                                     double* __restrict__ ws) {
+  __shared__ unsigned s_max[kSmpPrepThreads / 64];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, b = blockIdx.x;
+  if (!(params[0] > 0.0)) return;
+  const SmpWs w = smp_ws(ws, V);
+  const int c0 = b * kSmpChunk + t * kSmpPer;
+  float x[kSmpPer];
+#pragma unroll
+  for (int j = 0; j < kSmpPer; ++j) x[j] = logits[c0 + j < V ? c0 + j : V - 1];   // clamped: a real logit
+  unsigned mk = 0u;
+#pragma unroll
+  for (int j = 0; j < kSmpPer; ++j) mk = max(mk, logit_key(x[j]));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mk = max(mk, (unsigned)__shfl_xor((int)mk, m, 64));
+  if (lane == 0) s_max[wave] = mk;
+  __syncthreads();
+  if (t == 0) w.cmax[b] = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+}
+
+__global__ __launch_bounds__(kSmpPrepThreads) void sample_prep_kernel(const float* __restrict__ logits, int V,
+                                                                      const double* __restrict__ params,
+                                                                      double* __restrict__ ws) {
+  constexpr int NW = kSmpPrepThreads / 64;
+  __shared__ unsigned s_max[NW];
+  __shared__ double s_sum[NW];
+  __shared__ unsigned h_cnt[256];
+  __shared__ double h_mass[NW][256];                 // one copy per wavefront: a fixed summation order
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, b = blockIdx.x;
+  const double temp = params[0];
+  if (!(temp > 0.0)) return;                         // greedy: the pick kernel scans the logits
+  const SmpWs w = smp_ws(ws, V);
+  h_cnt[t] = 0u;
+#pragma unroll
+  for (int j = 0; j < NW; ++j) h_mass[j][t] = 0.0;
+  // 1. the largest key, from the chunk maxima
+  const int nb = (int)smp_nb(V);
+  unsigned mk = 0u;
+  for (int c = t; c < nb; c += kSmpPrepThreads) mk = max(mk, w.cmax[c]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mk = max(mk, (unsigned)__shfl_xor((int)mk, m, 64));
+  if (lane == 0) s_max[wave] = mk;
+  __syncthreads();                                   // also orders the bin clears before the adds
+  mk = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+  if (b == 0 && t == 0) w.hdr->maxkey = mk;
+  const double lgmax = (double)key_logit(mk) / temp;
+  const float maxv = key_logit(mk), sb = (float)(8.0 / temp);
+  // 2. this chunk: e, the chunk sum, and counts and masses per bin
+  const int c0 = b * kSmpChunk + t * kSmpPer;
+  float x[kSmpPer];
+#pragma unroll
+  for (int j = 0; j < kSmpPer; ++j) x[j] = logits[c0 + j < V ? c0 + j : V - 1];
+  double part = 0.0;
+#pragma unroll
+  for (int j = 0; j < kSmpPer; ++j) {
+    if (c0 + j >= V) break;
+    const int bin = smp_bin(x[j], maxv, sb);
+    const double v = x[j] == x[j] ? exp((double)x[j] / temp - lgmax) : 0.0;
+    w.e[c0 + j] = v;
+    part += v;
+    atomicAdd(&h_cnt[bin], 1u);
+    atomicAdd(&h_mass[wave][bin], v);
+  }
+  part = wave_sum_f64(part);
+  if (lane == 0) s_sum[wave] = part;
+  __syncthreads();
+  if (t == 0) w.bsum[b] = ((s_sum[0] + s_sum[1]) + s_sum[2]) + s_sum[3];
+  // suffix sums over the bins (bin t and every bin above it), in a fixed order
+  unsigned sc = h_cnt[t];
+  double sm = ((h_mass[0][t] + h_mass[1][t]) + h_mass[2][t]) + h_mass[3][t];
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const unsigned oc = __shfl_down(sc, m, 64);
+    const double om = __shfl_down(sm, m, 64);
+    if (lane + m < 64) { sc += oc; sm += om; }
+  }
+  __syncthreads();                                   // the bins are read: reuse s_max / s_sum
+  if (lane == 0) { s_max[wave] = sc; s_sum[wave] = sm; }
+  __syncthreads();
+  for (int ww = NW - 1; ww > wave; --ww) { sc += s_max[ww]; sm += s_sum[ww]; }
+  w.scnt[(size_t)b * 256 + t] = sc;
+  w.smass[(size_t)b * 256 + t] = sm;
+}
+
+// The vocabulary's mass from the chunk sums: lane l of a wavefront owns chunks [l * g, l * g + g)
+// (lsum, summed in order), incl is the inclusive scan over the lanes; returns the total.  The
+// gather and pick kernels compute it with the same code, so they agree to the bit.
+__device__ __forceinline__ double smp_total(const double* csum, int nb, double& lsum, double& incl) {
+  const int lane = threadIdx.x & 63, g = (nb + 63) / 64;
+  lsum = 0.0;
+  for (int j = 0; j < g; ++j) {
+    const int c = lane * g + j;
+    lsum += c < nb ? csum[c] : 0.0;
+  }
+  incl = wave_incl_scan(lsum);
+  return __shfl(incl, 63, 64);
+}
+
+// Wavefront 0's walk of 256 bins from the top (lane l holds bins 4l .. 4l + 3): the highest bin
+// b >= 1 whose inclusive sum from the top, started at `start`, reaches `need` (else bin 0), and the
+// sum strictly above it.  Counts are exact in any order; masses add in a fixed tree order.
+template <class T>
+__device__ __forceinline__ int bin_walk(const T (&v)[4], T start, T need, T& above) {
+  const int lane = threadIdx.x & 63;
+  const T lsum = ((v[3] + v[2]) + v[1]) + v[0];
+  T suf = lsum;                                      // sum over the lanes at and above this one
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const T o = __shfl_down(suf, m, 64);
+    if (lane + m < 64) suf += o;
+  }
+  const T sa = suf - lsum;                           // lanes above (exact for counts)
+  const unsigned long long reach = __ballot(start + suf >= need);
+  int b = 0;
+  T acc;
+  if (reach) {
+    const int L = 63 - __clzll((long long)reach);
+    acc = start + __shfl(sa, L, 64);
+    bool found = false;
+    for (int j = 3; j >= (L == 0 ? 1 : 0); --j) {
+      const T c = __shfl(v[j], L, 64);
+      if (acc + c >= need) { b = 4 * L + j; found = true; break; }
+      acc += c;
+    }
+    if (!found) b = 0;                               // only lane 0's bin 0 is left
+  } else {
+    acc = start + __shfl(suf, 0, 64) - __shfl(v[0], 0, 64);   // every bin from 1 up
+  }
+  above = acc;
+  return b;
+}
+
+// Wavefront 0's search of 256 suffix sums S (lane l holds bins 4l .. 4l + 3; non-increasing in
+// the bin): the highest bin b >= 1 with S[b] >= need (else bin 0), and S[b + 1] (0 past the top).
+template <class T>
+__device__ __forceinline__ int suffix_walk(const T (&S)[4], T need, T& next) {
+  const int lane = threadIdx.x & 63;
+  int jb = -1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if ((lane > 0 || j > 0) && S[j] >= need) jb = j;
+  const unsigned long long has = __ballot(jb >= 0);
+  const T up = __shfl_down(S[0], 1, 64);             // the next lane's first bin
+  const T after[4] = {S[1], S[2], S[3], lane < 63 ? up : (T)0};
+  if (!has) {
+    next = __shfl(S[1], 0, 64);
+    return 0;
+  }
+  const int L = 63 - __clzll((long long)has);
+  const int j = __shfl(jb, L, 64);
+  const T a0 = __shfl(after[0], L, 64), a1 = __shfl(after[1], L, 64), a2 = __shfl(after[2], L, 64),
+          a3 = __shfl(after[3], L, 64);
+  next = j == 0 ? a0 : j == 1 ? a1 : j == 2 ? a2 : a3;
+  return 4 * L + j;
+}
+
+// Called by every thread of the workgroup (>= 256 threads); mc / mm: LDS scratch of 256 entries.
+// The merged suffix sums: counts exact, masses added over the chunks in order.
+__device__ void smp_window(const SmpWs& w, int nb, int V, double top_p, long long top_k, double Z_all, unsigned* mc,
+                           double* mm, SmpWin& out) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const bool cut_k = top_k > 0 && top_k < V, cut_p = top_p > 0.0 && top_p < 1.0;
+  if (!cut_k && !cut_p) {
+    if (t == 0) out = SmpWin{0, -1, 0, 0, 0.0};
+    __syncthreads();
+    return;
+  }
+  if (t < 256) {
+    unsigned c = 0;
+    double m = 0.0;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+      unsigned cv[16];
+      double mv[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int b = b0 + j < nb ? b0 + j : nb - 1;
+        cv[j] = w.scnt[(size_t)b * 256 + t];
+        mv[j] = w.smass[(size_t)b * 256 + t];
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (b0 + j < nb) { c += cv[j]; m += mv[j]; }
+    }
+    mc[t] = c;
+    mm[t] = m;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    if (cut_k) {
+      long long v[4], next;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = mc[4 * lane + j];
+      const int b1 = suffix_walk<long long>(v, top_k, next);
+      if (lane == 0) out = SmpWin{b1, 255, 1, (long long)mc[b1], 0.0};
+    } else {
+      double v[4], next;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = mm[4 * lane + j];
+      const int be = suffix_walk<double>(v, top_p * Z_all, next);
+      const long long n = (long long)mc[be] - (be < 255 ? (long long)mc[be + 1] : 0ll);
+      if (lane == 0) out = SmpWin{be, be, 2, n, next};
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ bool smp_use_window(const SmpWin& win, int nb) {
+  return win.mode != 0 && win.ncand >= 1 && win.ncand <= kSmpCap && nb <= kSmpMaxChunks;
+}
+
+__global__ __launch_bounds__(kSmpPrepThreads) void sample_gather_kernel(const float* __restrict__ logits, int V,
+                                                                        const double* __restrict__ params,
+                                                                        double* __restrict__ ws) {
+  constexpr int NW = kSmpPrepThreads / 64;
+  __shared__ unsigned mc[256];
+  __shared__ double mm[256];
+  __shared__ SmpWin win;
+  __shared__ unsigned wc[kSmpMaxChunks];
+  __shared__ unsigned s_u[NW];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, c = blockIdx.x;
+  const double temp = params[0], top_p = params[1];
+  const long long top_k = (long long)params[2];
+  if (!(temp > 0.0)) return;
+  const SmpWs w = smp_ws(ws, V);
+  const int nb = (int)smp_nb(V);
+  double lsum, incl;
+  const double Z_all = smp_total(w.bsum, nb, lsum, incl);
+  smp_window(w, nb, V, top_p, top_k, Z_all, mc, mm, win);
+  if (c == 0 && t == 0) {                            // the pick kernel takes the window from here
+    w.hdr->Z_all = Z_all;
+    w.hdr->win = win;
+  }
+  if (!smp_use_window(win, nb)) return;              // workgroup-uniform
+  const int lo = win.lo, hi = win.hi;
+  const float maxv = key_logit(w.hdr->maxkey), sb = (float)(8.0 / temp);
+  // the window's logits per chunk (suffix counts: [lo, hi] = S[lo] - S[hi + 1]) and this chunk's offset
+  for (int cc = t; cc < nb; cc += kSmpPrepThreads)
+    wc[cc] = w.scnt[(size_t)cc * 256 + lo] - (hi < 255 ? w.scnt[(size_t)cc * 256 + hi + 1] : 0u);
+  __syncthreads();
+  unsigned before = 0;
+  for (int cc = t; cc < c; cc += kSmpPrepThreads) before += wc[cc];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) before += (unsigned)__shfl_xor((int)before, m, 64);
+  if (lane == 0) s_u[wave] = before;
+  __syncthreads();
+  const unsigned off = (s_u[0] + s_u[1]) + (s_u[2] + s_u[3]);
+  if (t == 0) {
+    w.coff[c] = off;
+    if (c == nb - 1) w.coff[nb] = off + wc[c];
+  }
+  // compact the chunk's window logits in index order: thread t owns 8 consecutive logits
+  const int c0 = c * kSmpChunk + t * kSmpPer;
+  float x[kSmpPer];
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < kSmpPer; ++j) x[j] = logits[c0 + j < V ? c0 + j : V - 1];
+#pragma unroll
+  for (int j = 0; j < kSmpPer; ++j) {
+    const int bin = smp_bin(x[j], maxv, sb);
+    n += c0 + j < V && bin >= lo && bin <= hi;
+  }
+  const int inc = wave_incl_scan(n);
+  __syncthreads();
+  if (lane == 63) s_u[wave] = inc;
+  __syncthreads();
+  int pos = (int)off + inc - n;
+  for (int ww = 0; ww < wave; ++ww) pos += s_u[ww];
+#pragma unroll
+  for (int j = 0; j < kSmpPer; ++j) {
+    const int bin = smp_bin(x[j], maxv, sb);
+    if (c0 + j >= V || bin < lo || bin > hi || pos >= kSmpCap) continue;
+    w.ckey[pos] = logit_key(x[j]);
+    w.cidx[pos] = c0 + j;
+    w.ce[pos] = w.e[c0 + j];
+    ++pos;
+  }
+}
 
 struct SampleSmem {
   union {
     unsigned cnt[kSampleWaves][256];
     double mass[kSampleWaves][256];
   } h;
+  unsigned ckey[kSmpCap];                            // the window's logits, in index order
+  int cidx[kSmpCap];
+  double ce[kSmpCap];
+  double km[kSmpMaxChunks];                          // per-chunk kept mass (top-p alone)
   double wsum[kSampleWaves];
-  unsigned wmax[kSampleWaves];
+  unsigned wmax[kSampleWaves], wmin[kSampleWaves];
   unsigned prefix, mask;
   long long remaining;
   double above, target;
   long long wtie[kSampleWaves];
-  int token, last;
+  int token, last, tie_cut;
 };
 
-// Radix select over keys matching the current prefix.  COUNT: the key holding the remaining-th
-// largest element; otherwise the key at which the mass from the top first reaches target.
-template <bool COUNT>
-__device__ void radix_select(const float* logits, const double* e, int V, unsigned floor_key, SampleSmem& sm) {
-  const int t = threadIdx.x, wave = t >> 6;
-  for (int shift = 24; shift >= 0; shift -= 8) {
+// The whole vocabulary (keys from the logits, e from the workspace) or the window in LDS.
+struct SmpAll {
+  const float* logits;
+  const double* e;
+  int n;
+  __device__ unsigned key(int i) const { return logit_key(logits[i]); }
+  __device__ double mass(int i) const { return e[i]; }
+  __device__ int index(int i) const { return i; }
+};
+struct SmpCand {
+  const unsigned* k;
+  const int* idx;
+  const double* e;
+  int n;
+  __device__ unsigned key(int i) const { return k[i]; }
+  __device__ double mass(int i) const { return e[i]; }
+  __device__ int index(int i) const { return idx[i]; }
+};
+
+constexpr int kSmpBatch = 8;   // loads in flight per thread in the passes
+
+// Radix select over keys >= floor_key matching the current prefix, from bit `top` down.  COUNT: the
+// key holding the remaining-th largest element; otherwise the key at which the mass from the top
+// first reaches target.
+template <bool COUNT, class Acc>
+__device__ void radix_select(const Acc& A, unsigned floor_key, SampleSmem& sm, int top = 24) {
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  for (int shift = top; shift >= 0; shift -= 8) {
     for (int i = t; i < kSampleWaves * 256; i += kSampleThreads) {
       if (COUNT) (&sm.h.cnt[0][0])[i] = 0u;
       else (&sm.h.mass[0][0])[i] = 0.0;
     }
     __syncthreads();
     const unsigned prefix = sm.prefix, mask = sm.mask;
-    for (int i = t; i < V; i += kSampleThreads) {
-      const unsigned k = logit_key(logits[i]);
-      if (k < floor_key || (k & mask) != prefix) continue;
-      const int bin = (k >> shift) & 255;
-      if (COUNT) atomicAdd(&sm.h.cnt[wave][bin], 1u);
-      else atomicAdd(&sm.h.mass[wave][bin], e[i]);
+    for (int b0 = 0; b0 < A.n; b0 += kSmpBatch * kSampleThreads) {
+      unsigned k[kSmpBatch];
+      double m[kSmpBatch];
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) {
+        const int i = b0 + j * kSampleThreads + t;
+        const int ic = i < A.n ? i : A.n - 1;
+        k[j] = A.key(ic);
+        m[j] = COUNT ? 0.0 : A.mass(ic);
+      }
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) {
+        if (b0 + j * kSampleThreads + t >= A.n || k[j] < floor_key || (k[j] & mask) != prefix) continue;
+        const int bin = (k[j] >> shift) & 255;
+        if (COUNT) atomicAdd(&sm.h.cnt[wave][bin], 1u);
+        else atomicAdd(&sm.h.mass[wave][bin], m[j]);
+      }
     }
     __syncthreads();
     if (t < 256) {                                   // merge the wavefront copies in a fixed order
@@ -626,175 +1027,435 @@ __device__ void radix_select(const float* logits, const double* e, int V, unsign
         for (int w = 0; w < kSampleWaves; ++w) c += sm.h.cnt[w][t];
         sm.h.cnt[0][t] = c;
       } else {
-        double m = 0.0;
-        for (int w = 0; w < kSampleWaves; ++w) m += sm.h.mass[w][t];
-        sm.h.mass[0][t] = m;
+        double ms = 0.0;
+        for (int w = 0; w < kSampleWaves; ++w) ms += sm.h.mass[w][t];
+        sm.h.mass[0][t] = ms;
       }
     }
     __syncthreads();
-    if (t == 0) {
-      int b = 255;
+    if (wave == 0) {
+      int b;
       if (COUNT) {
-        long long acc = 0;
-        for (; b > 0 && acc + (long long)sm.h.cnt[0][b] < sm.remaining; --b) acc += sm.h.cnt[0][b];
-        sm.remaining -= acc;
+        long long v[4], above;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = sm.h.cnt[0][4 * lane + j];
+        b = bin_walk<long long>(v, 0ll, sm.remaining, above);
+        if (lane == 0) sm.remaining -= above;
       } else {
-        double acc = sm.above;
-        for (; b > 0 && acc + sm.h.mass[0][b] < sm.target; --b) acc += sm.h.mass[0][b];
-        sm.above = acc;
+        double v[4], above;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = sm.h.mass[0][4 * lane + j];
+        b = bin_walk<double>(v, sm.above, sm.target, above);
+        if (lane == 0) sm.above = above;
       }
-      sm.prefix |= (unsigned)b << shift;
-      sm.mask |= 255u << shift;
+      if (lane == 0) {
+        sm.prefix |= (unsigned)b << shift;
+        sm.mask |= 255u << shift;
+      }
     }
     __syncthreads();
   }
 }
 
+// The two-level draw: the chunk whose running kept mass first exceeds u * total (chunk masses
+// cm(c), inclusive scan over the lanes in a fixed order), then the position inside it (two logits
+// per thread, kept(i, key) selects; e from the workspace).  Rounding that leaves no crossing takes
+// the chunk's last kept logit.
+template <class CM, class KEPT>
+__device__ int smp_chunk_draw(const float* logits, const double* e, int V, int nb, double u, CM cm, KEPT kept,
+                              SampleSmem& sm) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = (nb + 63) / 64;
+  double lsum = 0.0;
+  for (int j = 0; j < g; ++j) {
+    const int c = lane * g + j;
+    lsum += c < nb ? cm(c) : 0.0;
+  }
+  const double incl = wave_incl_scan(lsum);
+  const double total = __shfl(incl, 63, 64);
+  const double target = u * total;
+  const unsigned long long over = __ballot(incl > target);
+  int cb = -1;
+  double base = 0.0;
+  if (over) {
+    const int L = __ffsll((long long)over) - 1;
+    double run = __shfl(incl - lsum, L, 64);
+    int lastc = -1;
+    double lastbase = 0.0;
+    for (int j = 0; j < g; ++j) {
+      const int c = L * g + j;
+      if (c >= nb) break;
+      const double m = cm(c);
+      if (m > 0.0) { lastc = c; lastbase = run; }
+      if (run + m > target) { cb = c; base = run; break; }
+      run += m;
+    }
+    if (cb < 0) { cb = lastc; base = lastbase; }     // rounding inside the lane's chunks
+  }
+  if (cb < 0) {                                      // target at the very end: the last chunk with mass
+    cb = nb - 1;
+    while (cb > 0 && !(cm(cb) > 0.0)) --cb;
+    base = -INFINITY;                                // no crossing inside: its last kept logit
+  }
+  constexpr int PT = kSmpChunk / kSampleThreads;     // consecutive logits per thread
+  const int e0 = cb * kSmpChunk + PT * t;
+  float x[PT];
+  double a[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    x[j] = logits[e0 + j < V ? e0 + j : V - 1];
+    a[j] = e[e0 + j < V ? e0 + j : V - 1];
+  }
+  double loc = 0.0;
+  int lastp = -1;
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    a[j] = e0 + j < V && kept(e0 + j, logit_key(x[j])) ? a[j] : 0.0;
+    loc += a[j];
+    if (a[j] > 0.0) lastp = e0 + j;
+  }
+  const double inc = wave_incl_scan(loc);
+  __syncthreads();
+  if (lane == 63) sm.wsum[wave] = inc;
+  if (t == 0) { sm.token = 0x7fffffff; sm.last = -1; }
+  __syncthreads();
+  double ex = inc - loc;
+  for (int ww = 0; ww < wave; ++ww) ex += sm.wsum[ww];
+  const double tg = target - base;
+  if (loc > 0.0 && ex <= tg && tg < ex + loc) {
+    double run = ex;
+    int pk = -1;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      if (pk >= 0 || a[j] == 0.0) continue;
+      run += a[j];
+      if (run > tg) pk = e0 + j;
+    }
+    atomicMin(&sm.token, pk >= 0 ? pk : lastp);     // rounding inside the range: its last kept logit
+  }
+  atomicMax(&sm.last, lastp);
+  __syncthreads();
+  return sm.token != 0x7fffffff ? sm.token : (sm.last >= 0 ? sm.last : 0);
+}
+
+// Top-k floor, top-p edge, the kept set and the draw over A (positions in index order); returns
+// the vocabulary index.  Z_all: the vocabulary's mass (used without a top-k cut).
+// The radix passes start below the key bytes that every element of A shares (cp_prefix under
+// cp_mask, first pass at bit cp_top).
+template <class Acc>
+__device__ int smp_select_draw(const Acc& A, int V, double temp, double lgmax, double top_p, long long top_k,
+                               double u, double Z_all, unsigned cp_prefix, unsigned cp_mask, int cp_top,
+                               SampleSmem& sm) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if (t == 0) { sm.prefix = cp_prefix; sm.mask = cp_mask; sm.above = 0.0; sm.token = 0x7fffffff; sm.last = -1; }
+  __syncthreads();
+  // top-k: keep the logits >= the k-th largest (ties included)
+  unsigned kfloor = 0u;
+  const bool cut_k = top_k > 0 && top_k < V;
+  if (cut_k) {
+    if (t == 0) sm.remaining = top_k;
+    __syncthreads();
+    radix_select<true>(A, 0u, sm, cp_top);
+    kfloor = sm.prefix;
+    __syncthreads();
+    if (t == 0) { sm.prefix = cp_prefix; sm.mask = cp_mask; }
+  }
+  // Z: the kept mass after top-k
+  double Z = Z_all;
+  if (cut_k) {
+    double part = 0.0;
+    for (int b0 = 0; b0 < A.n; b0 += kSmpBatch * kSampleThreads) {
+      unsigned k[kSmpBatch];
+      double m[kSmpBatch];
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) {
+        const int i = b0 + j * kSampleThreads + t;
+        const int ic = i < A.n ? i : A.n - 1;
+        k[j] = A.key(ic);
+        m[j] = A.mass(ic);
+      }
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j)
+        if (b0 + j * kSampleThreads + t < A.n && k[j] >= kfloor) part += m[j];
+    }
+    part = wave_sum_f64(part);
+    __syncthreads();
+    if (lane == 0) sm.wsum[wave] = part;
+    __syncthreads();
+    Z = 0.0;
+    for (int w = 0; w < kSampleWaves; ++w) Z += sm.wsum[w];
+  }
+  // top-p: the smallest top set whose mass reaches top_p * Z
+  unsigned pkey = kfloor;
+  long long ntie = 0;                                // tied logits kept at pkey (0: no top-p cut)
+  if (top_p > 0.0 && top_p < 1.0) {
+    __syncthreads();
+    if (t == 0) sm.target = top_p * Z;
+    __syncthreads();
+    radix_select<false>(A, kfloor, sm, cp_top);
+    pkey = sm.prefix;
+    const double q = exp((double)key_logit(pkey) / temp - lgmax);
+    const double need = sm.target - sm.above;
+    ntie = need > 0.0 ? (long long)ceil(need / q) : 1;
+    if (ntie < 1) ntie = 1;
+  }
+  __syncthreads();
+  // the kept set: keys above pkey, and at pkey the first ntie ties counted from the highest index
+  // down (all of them without a top-p cut).  Thread t owns positions [i0, i1), read kSmpBatch at a time.
+  const int per = (A.n + kSampleThreads - 1) / kSampleThreads;
+  const int i0 = min(A.n, t * per), i1 = min(A.n, i0 + per);
+  auto load = [&](int base, unsigned (&k)[kSmpBatch], double (&m)[kSmpBatch], bool with_mass) {
+#pragma unroll
+    for (int j = 0; j < kSmpBatch; ++j) {
+      const int i = base + j < i1 ? base + j : i1 - 1;
+      k[j] = A.key(i);
+      m[j] = with_mass ? A.mass(i) : 0.0;
+    }
+  };
+  long long rties = 0;                               // ties at pkey in this thread's range
+  if (ntie)
+    for (int b = i0; b < i1; b += kSmpBatch) {
+      unsigned k[kSmpBatch];
+      double m[kSmpBatch];
+      load(b, k, m, false);
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) rties += b + j < i1 && k[j] == pkey;
+    }
+  long long ties_after = 0;                          // ties at pkey in higher threads' ranges
+  if (ntie) {
+    long long suf = rties;                           // inclusive suffix sum within the wavefront
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const long long o = __shfl_down(suf, m, 64);
+      if (lane + m < 64) suf += o;
+    }
+    if (lane == 0) sm.wtie[wave] = suf;
+    __syncthreads();
+    ties_after = suf - rties;
+    for (int w = wave + 1; w < kSampleWaves; ++w) ties_after += sm.wtie[w];
+  }
+  double local = 0.0;                                // kept mass of the range, in index order
+  {
+    long long higher = ties_after + rties;           // ties at positions >= i (before visiting i)
+    for (int b = i0; b < i1; b += kSmpBatch) {
+      unsigned k[kSmpBatch];
+      double m[kSmpBatch];
+      load(b, k, m, true);
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) {
+        if (b + j >= i1) break;
+        const bool tie = ntie && k[j] == pkey;
+        if (tie) --higher;                           // now: ties at positions > i
+        if (k[j] >= pkey && (!tie || higher < ntie)) local += m[j];
+      }
+    }
+  }
+  const double incl = wave_incl_scan(local);         // exclusive prefix over threads, fixed order
+  __syncthreads();
+  if (lane == 63) sm.wsum[wave] = incl;
+  __syncthreads();
+  double excl = incl - local, total = 0.0;
+  for (int w = 0; w < kSampleWaves; ++w) {
+    if (w < wave) excl += sm.wsum[w];
+    total += sm.wsum[w];
+  }
+  // np.random.choice: the first position whose cumulative probability exceeds u
+  const double target = u * total;
+  int pick = 0x7fffffff, last = -1;
+  if (local > 0.0 && target < excl + local) {
+    double run = excl;
+    long long higher = ties_after + rties;
+    bool done = false;
+    for (int b = i0; b < i1 && !done; b += kSmpBatch) {
+      unsigned k[kSmpBatch];
+      double m[kSmpBatch];
+      load(b, k, m, true);
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) {
+        if (done || b + j >= i1) continue;
+        const bool tie = ntie && k[j] == pkey;
+        if (tie) --higher;
+        if (!(k[j] >= pkey && (!tie || higher < ntie)) || m[j] == 0.0) continue;
+        last = b + j;
+        run += m[j];
+        if (run > target) { pick = b + j; done = true; }
+      }
+    }
+    if (pick == 0x7fffffff && excl <= target) pick = last;   // rounding inside the range
+  }
+  if (excl <= target || local > 0.0) atomicMin(&sm.token, pick);
+  __syncthreads();
+  if (sm.token == 0x7fffffff) {                      // target at the very end: the highest kept position
+    int hi = -1;
+    long long higher = ties_after + rties;
+    for (int b = i0; b < i1; b += kSmpBatch) {
+      unsigned k[kSmpBatch];
+      double m[kSmpBatch];
+      load(b, k, m, true);
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) {
+        if (b + j >= i1) break;
+        const bool tie = ntie && k[j] == pkey;
+        if (tie) --higher;
+        if (k[j] >= pkey && (!tie || higher < ntie) && m[j] > 0.0) hi = b + j;
+      }
+    }
+    atomicMax(&sm.last, hi);
+    __syncthreads();
+    if (t == 0) sm.token = sm.last < 0 ? 0 : sm.last;
+  }
+  __syncthreads();
+  const int p = sm.token;
+  return p >= 0 && p < A.n ? A.index(p) : 0;
+}
+
+// The key bytes every window logit shares: their prefix, its mask, and the first radix pass below them.
+__device__ void smp_common_prefix(const SmpCand& A, SampleSmem& sm, unsigned& prefix, unsigned& mask, int& top) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  unsigned mn = 0xffffffffu, mx = 0u;
+  for (int i = t; i < A.n; i += kSampleThreads) {
+    mn = min(mn, A.k[i]);
+    mx = max(mx, A.k[i]);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    mn = min(mn, (unsigned)__shfl_xor((int)mn, m, 64));
+    mx = max(mx, (unsigned)__shfl_xor((int)mx, m, 64));
+  }
+  __syncthreads();
+  if (lane == 0) { sm.wmax[wave] = mx; sm.wmin[wave] = mn; }
+  __syncthreads();
+  for (int w = 0; w < kSampleWaves; ++w) {
+    mn = min(mn, sm.wmin[w]);
+    mx = max(mx, sm.wmax[w]);
+  }
+  const unsigned diff = mn ^ mx;
+  const int nbytes = diff == 0u ? 4 : __clz(diff) / 8;
+  mask = nbytes == 0 ? 0u : nbytes == 4 ? 0xffffffffu : ~(0xffffffffu >> (8 * nbytes));
+  prefix = mx & mask;
+  top = 24 - 8 * nbytes;
+}
+
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
     const float* __restrict__ logits, int V, const double* __restrict__ params, const double* __restrict__ uniforms,
     const int* __restrict__ step, int* __restrict__ forced, int* __restrict__ n_forced, int* __restrict__ out,
-    double* __restrict__ e) {
+    double* __restrict__ ws) {
   __shared__ SampleSmem sm;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const double temp = params[0], top_p = params[1];
   const long long top_k = (long long)params[2];
   const int s = step ? step[0] : 0;
   const double u = uniforms[s];
-
-  // 1. the largest key (greedy: the lowest index holding it, like np.argmax)
-  unsigned mk = 0;
-  for (int i = t; i < V; i += kSampleThreads) mk = max(mk, logit_key(logits[i]));
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) mk = max(mk, (unsigned)__shfl_xor((int)mk, m, 64));
-  if (lane == 0) sm.wmax[wave] = mk;
-  if (t == 0) { sm.token = 0x7fffffff; sm.last = -1; sm.prefix = 0u; sm.mask = 0u; sm.above = 0.0; }
-  __syncthreads();
-  mk = sm.wmax[0];
-  for (int w = 1; w < kSampleWaves; ++w) mk = max(mk, sm.wmax[w]);
+  int tok = 0;
   if (!(temp > 0.0)) {
+    // greedy: the lowest index holding the largest key, like np.argmax
+    unsigned mk = 0;
+#pragma unroll 8
+    for (int i = t; i < V; i += kSampleThreads) mk = max(mk, logit_key(logits[i]));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mk = max(mk, (unsigned)__shfl_xor((int)mk, m, 64));
+    if (lane == 0) sm.wmax[wave] = mk;
+    if (t == 0) sm.token = 0x7fffffff;
+    __syncthreads();
+    mk = sm.wmax[0];
+    for (int w = 1; w < kSampleWaves; ++w) mk = max(mk, sm.wmax[w]);
     for (int i = t; i < V; i += kSampleThreads)
       if (logit_key(logits[i]) == mk) { atomicMin(&sm.token, i); break; }
     __syncthreads();
+    tok = sm.token;
   } else {
-    const double lgmax = (double)key_logit(mk) / temp;
-    // 2. top-k: keep the logits >= the k-th largest (ties included, as lg < kth -> -inf)
-    unsigned kfloor = 0u;
-    if (top_k > 0 && top_k < V) {
-      if (t == 0) sm.remaining = top_k;
-      __syncthreads();
-      radix_select<true>(logits, e, V, 0u, sm);
-      kfloor = sm.prefix;
-      __syncthreads();
-      if (t == 0) { sm.prefix = 0u; sm.mask = 0u; }
-    }
-    // 3. e_i = exp(lg_i - lg_max) for the kept logits, and their sum
-    double part = 0.0;
-    for (int i = t; i < V; i += kSampleThreads) {
-      const float x = logits[i];
-      const double v = logit_key(x) >= kfloor && x == x ? exp((double)x / temp - lgmax) : 0.0;
-      e[i] = v;
-      part += v;
-    }
-    part = wave_sum_f64(part);
-    if (lane == 0) sm.wsum[wave] = part;
-    __syncthreads();
-    double Z = 0.0;
-    for (int w = 0; w < kSampleWaves; ++w) Z += sm.wsum[w];
-    // 4. top-p: the smallest top set whose mass reaches top_p * Z
-    unsigned pkey = kfloor;
-    long long ntie = 0;                              // tied logits kept at pkey (0: no top-p cut)
-    if (top_p > 0.0 && top_p < 1.0) {
-      if (t == 0) sm.target = top_p * Z;
-      __syncthreads();
-      radix_select<false>(logits, e, V, kfloor, sm);
-      pkey = sm.prefix;
-      const double q = exp((double)key_logit(pkey) / temp - lgmax);
-      const double need = sm.target - sm.above;
-      ntie = need > 0.0 ? (long long)ceil(need / q) : 1;
-      if (ntie < 1) ntie = 1;
-    }
-    __syncthreads();
-    // 5. the kept set: keys above pkey, and at pkey the first ntie ties counted from the highest
-    // index down (all of them without a top-p cut).  Thread t owns indices [i0, i1).
-    const int per = (V + kSampleThreads - 1) / kSampleThreads;
-    const int i0 = min(V, t * per), i1 = min(V, i0 + per);
-    long long rties = 0;                             // ties at pkey in this thread's range
-    if (ntie)
-      for (int i = i0; i < i1; ++i) rties += logit_key(logits[i]) == pkey;
-    long long ties_after = 0;                        // ties at pkey in higher threads' ranges
-    if (ntie) {
-      long long suf = rties;                         // inclusive suffix sum within the wavefront
+    const SmpWs w = smp_ws(ws, V);
+    const int nb = (int)smp_nb(V);
+    const SmpHdr hdr = *w.hdr;                       // the largest key, the mass and the window (gather)
+    const double lgmax = (double)key_logit(hdr.maxkey) / temp;
+    const double Z_all = hdr.Z_all;
+    const SmpWin win = hdr.win;
+    if (win.mode == 0) {
+      tok = smp_chunk_draw(logits, w.e, V, nb, u, [&](int c) { return w.bsum[c]; },
+                           [](int, unsigned) { return true; }, sm);
+    } else if (!smp_use_window(win, nb)) {
+      SmpAll A{logits, w.e, V};
+      tok = smp_select_draw(A, V, temp, lgmax, top_p, top_k, u, Z_all, 0u, 0u, 24, sm);
+    } else {
+      const int n = (int)win.ncand;
+      for (int b0 = 0; b0 < n; b0 += 4 * kSampleThreads) {
+        unsigned kk[4];
+        int ii[4];
+        double ee[4];
 #pragma unroll
-      for (int m = 1; m < 64; m <<= 1) {
-        const long long o = __shfl_down(suf, m, 64);
-        if (lane + m < 64) suf += o;
-      }
-      if (lane == 0) sm.wtie[wave] = suf;
-      __syncthreads();
-      ties_after = suf - rties;
-      for (int w = wave + 1; w < kSampleWaves; ++w) ties_after += sm.wtie[w];
-    }
-    // kept mass of the range, in index order
-    double local = 0.0;
-    {
-      long long higher = ties_after + rties;         // ties at indices >= i (before visiting i)
-      for (int i = i0; i < i1; ++i) {
-        const unsigned k = logit_key(logits[i]);
-        const bool tie = ntie && k == pkey;
-        if (tie) --higher;                           // now: ties at indices > i
-        if (k >= pkey && (!tie || higher < ntie)) local += e[i];
-      }
-    }
-    // exclusive prefix of the kept mass over threads, summed in a fixed order
-    double incl = local;
+        for (int j = 0; j < 4; ++j) {
+          const int i = b0 + j * kSampleThreads + t < n ? b0 + j * kSampleThreads + t : n - 1;
+          kk[j] = w.ckey[i];
+          ii[j] = w.cidx[i];
+          ee[j] = w.ce[i];
+        }
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-      const double o = __shfl_up(incl, m, 64);
-      if (lane >= m) incl += o;
-    }
-    if (lane == 63) sm.wsum[wave] = incl;
-    __syncthreads();
-    double excl = incl - local, total = 0.0;
-    for (int w = 0; w < kSampleWaves; ++w) {
-      if (w < wave) excl += sm.wsum[w];
-      total += sm.wsum[w];
-    }
-    // np.random.choice: the first index whose cumulative probability exceeds u
-    const double target = u * total;
-    int pick = 0x7fffffff, last = -1;
-    if (local > 0.0 && target < excl + local) {
-      double run = excl;
-      long long higher = ties_after + rties;
-      for (int i = i0; i < i1; ++i) {
-        const unsigned k = logit_key(logits[i]);
-        const bool tie = ntie && k == pkey;
-        if (tie) --higher;
-        if (!(k >= pkey && (!tie || higher < ntie)) || e[i] == 0.0) continue;
-        last = i;
-        run += e[i];
-        if (run > target) { pick = i; break; }
+        for (int j = 0; j < 4; ++j) {
+          const int i = b0 + j * kSampleThreads + t;
+          if (i >= n) continue;
+          sm.ckey[i] = kk[j];
+          sm.cidx[i] = ii[j];
+          sm.ce[i] = ee[j];
+        }
       }
-      if (pick == 0x7fffffff && excl <= target) pick = last;   // rounding inside the range
-    }
-    if (excl <= target || local > 0.0) atomicMin(&sm.token, pick);
-    __syncthreads();
-    if (sm.token == 0x7fffffff) {                    // target at the very end: the highest kept index
-      int hi = -1;
-      long long higher = ties_after + rties;
-      for (int i = i0; i < i1; ++i) {
-        const unsigned k = logit_key(logits[i]);
-        const bool tie = ntie && k == pkey;
-        if (tie) --higher;
-        if (k >= pkey && (!tie || higher < ntie) && e[i] > 0.0) hi = i;
-      }
-      atomicMax(&sm.last, hi);
       __syncthreads();
-      if (t == 0) sm.token = sm.last < 0 ? 0 : sm.last;
+      SmpCand A{sm.ckey, sm.cidx, sm.ce, n};
+      unsigned cp, cm;
+      int ctop;
+      smp_common_prefix(A, sm, cp, cm, ctop);
+      if (win.mode == 1) {
+        tok = smp_select_draw(A, V, temp, lgmax, top_p, top_k, u, Z_all, cp, cm, ctop, sm);
+      } else {
+        // top-p alone: the radix select over the edge bin's logits, the mass above it from the bins
+        if (t == 0) {
+          sm.prefix = cp;
+          sm.mask = cm;
+          sm.above = win.above;
+          sm.target = top_p * Z_all;
+        }
+        __syncthreads();
+        radix_select<false>(A, 0u, sm, ctop);
+        const unsigned pkey = sm.prefix;
+        const double q = exp((double)key_logit(pkey) / temp - lgmax);
+        const double need = sm.target - sm.above;
+        long long ntie = need > 0.0 ? (long long)ceil(need / q) : 1;
+        if (ntie < 1) ntie = 1;
+        // ties at pkey are window logits; the kept ones are the ntie of highest index
+        const int per = (n + kSampleThreads - 1) / kSampleThreads;
+        const int i0 = min(n, t * per), i1 = min(n, i0 + per);
+        int nt = 0;
+        for (int i = i0; i < i1; ++i) nt += sm.ckey[i] == pkey;
+        const int inc = wave_incl_scan(nt);
+        if (lane == 63) sm.wmax[wave] = (unsigned)inc;
+        if (t == 0) sm.tie_cut = -1;
+        __syncthreads();
+        int ex = inc - nt, tot = 0;
+        for (int ww = 0; ww < kSampleWaves; ++ww) {
+          if (ww < wave) ex += (int)sm.wmax[ww];
+          tot += (int)sm.wmax[ww];
+        }
+        const long long skip = (long long)tot - ntie;   // ties below the kept ones
+        if (skip > 0 && ex <= skip && skip < ex + nt) {
+          int r = ex;
+          for (int i = i0; i < i1; ++i)
+            if (sm.ckey[i] == pkey && r++ == skip) { sm.tie_cut = sm.cidx[i]; break; }
+        }
+        __syncthreads();
+        const int tie_cut = sm.tie_cut;
+        auto kept = [&](int i, unsigned k) { return k > pkey || (k == pkey && i >= tie_cut); };
+        // per-chunk kept mass: the bins above the edge (suffix sum), plus the chunk's kept window logits
+        for (int c = t; c < nb; c += kSampleThreads) {
+          double m = win.lo < 255 ? w.smass[(size_t)c * 256 + win.lo + 1] : 0.0;
+          const int a = (int)w.coff[c], b = (int)w.coff[c + 1];
+          for (int i = a; i < b; ++i)
+            if (kept(sm.cidx[i], sm.ckey[i])) m += sm.ce[i];
+          sm.km[c] = m;
+        }
+        __syncthreads();
+        tok = smp_chunk_draw(logits, w.e, V, nb, u, [&](int c) { return sm.km[c]; }, kept, sm);
+      }
     }
   }
-  __syncthreads();
   if (t == 0) {
-    int tok = sm.token;
     if (tok < 0 || tok >= V) tok = 0;
     if (forced) forced[s] = tok;
     if (n_forced) n_forced[0] = s + 1;
@@ -873,14 +1534,26 @@ int afx_decode_advance(const float* logits, const float* slots, int V, const flo
   return check_launch("afx_decode_advance");
 }
 
+// Workspace bytes afx_sample needs for V logits.
+long long afx_sample_ws_bytes(int V) { return V >= 1 ? smp_ws_bytes(V) : -1; }
+
 // params: device {temperature, top_p, top_k} as doubles; u = uniforms[*step] (uniforms[0] without
 // step).  The token goes to forced[*step] (and n_forced = *step + 1, so afx_decode_advance takes
-// it) and/or out[0].  ws: V doubles.
+// it) and/or out[0].  ws: afx_sample_ws_bytes(V) bytes.
 int afx_sample(const float* logits, int V, const double* params, const double* uniforms, const int* step,
                int* forced, int* n_forced, int* out, double* ws, long long ws_bytes, void* stream) {
   AFX_REQUIRE(logits && params && uniforms && ws && V >= 1, "afx_sample: bad arguments");
+  AFX_REQUIRE(smp_nb(V) <= kSmpMaxChunks, "afx_sample: V = %d exceeds %d", V, kSmpMaxChunks * kSmpChunk);
   AFX_REQUIRE(forced || out, "afx_sample: no output");
-  AFX_REQUIRE(ws_bytes >= 8LL * V, "afx_sample: workspace %lld B < %lld B", ws_bytes, 8LL * V);
+  AFX_REQUIRE(((uintptr_t)ws & 7) == 0, "afx_sample: the workspace must be 8-byte aligned");
+  AFX_REQUIRE(ws_bytes >= smp_ws_bytes(V), "afx_sample: workspace %lld B < %lld B (afx_sample_ws_bytes)", ws_bytes,
+              smp_ws_bytes(V));
+  hipLaunchKernelGGL(sample_max_kernel, dim3((unsigned)smp_nb(V)), dim3(kSmpPrepThreads), 0, (hipStream_t)stream,
+                     logits, V, params, ws);
+  hipLaunchKernelGGL(sample_prep_kernel, dim3((unsigned)smp_nb(V)), dim3(kSmpPrepThreads), 0, (hipStream_t)stream,
+                     logits, V, params, ws);
+  hipLaunchKernelGGL(sample_gather_kernel, dim3((unsigned)smp_nb(V)), dim3(kSmpPrepThreads), 0,
+                     (hipStream_t)stream, logits, V, params, ws);
   hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kSampleThreads), 0, (hipStream_t)stream, logits, V, params,
                      uniforms, step, forced, n_forced, out, ws);
   return check_launch("afx_sample");

@@ -12,6 +12,8 @@ rotating weight copies inside a captured graph (working set > 2x the 256 MB MALL
 --workload copy streams a plain 1 GiB copy: the calibration run for the FETCH_SIZE /
 WRITE_SIZE counters behind roofline.traffic, and a measured copy ceiling.
 --workload prefill times the batched MFMA prefill of a --ctx-token prompt on the cfg3 model.
+--workload sample times the device sampler per parameter set, then cfg3 decode with device sampling
+against greedy decode in the same run.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode]
 """
@@ -35,7 +37,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "gemv_w8", "gemv_q4", "gemv_formats", "attn", "moe", "kernels", "copy",
-                             "prefill"])
+                             "prefill", "sample"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--out", default=None, help="also append the JSON line to this file")
     ap.add_argument("--rows-hint", type=int, default=0)
@@ -227,6 +229,61 @@ def bench_attn(args, ctx=None, B=None):
     byts = per + 2 * 2 * B * Hq * D
     return {"workload": f"cfg2 decode attention ctx={ctx}", "batch": B, "us": ms * 1e3, "bytes": byts,
             "GBps": byts / (ms * 1e-3) / 1e9, "frac": byts / (ms * 1e-3) / HBM_PEAK, "copies": copies}
+
+
+def bench_sample(args):
+    """Device sampling: afx_sample (prep + pick launches) per parameter set at the cfg3 vocabulary and
+    Qwen's 151936, N(0, 2.5^2) logits; then cfg3 decode with the sampler in the step graph against
+    greedy decode in the same run."""
+    import ctypes
+    import torch
+    from aneforge_amd import _hip, _kernels as K
+    rows = []
+    sets = [(0.8, 1.0, 0), (0.8, 0.9, 40), (0.7, 0.9, 0), (1.0, 0.95, 0), (0.6, 0.9, 50)]
+    for V in (CFG3["vocab"], 151936):
+        g = torch.Generator(device="cuda").manual_seed(7)
+        lg = torch.randn(V, device="cuda", generator=g) * 2.5
+        uni = torch.rand(64, dtype=torch.float64, device="cuda", generator=g)
+        step = torch.zeros(1, dtype=torch.int32, device="cuda")
+        out = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ws = torch.empty(K.sample_ws_elems(V), dtype=torch.float64, device="cuda")
+        for T, top_p, top_k in sets:
+            params = torch.tensor([T, top_p, float(top_k)], dtype=torch.float64, device="cuda")
+            gr = Graph(lambda: [K.sample(lg, params, uni, step=step, out=out, ws=ws) for _ in range(8)])
+            for _ in range(3):
+                gr.launch()
+            ms = gr.time_ms(8) / 8
+            rows.append({"workload": f"afx_sample V={V} T={T} top_p={top_p} top_k={top_k}", "us": ms * 1e3})
+    # sampled cfg3 decode against greedy, same engine and positions
+    K_steps, W_steps = args.steps, args.warmup
+    cfg, eng, layers = build_cfg3_engine(K_steps, W_steps)
+    P = CFG3["prefill"]
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    _hip.call("afx_event_create", ctypes.byref(e0))
+    _hip.call("afx_event_create", ctypes.byref(e1))
+
+    def timed(run):
+        eng.reset([1], pos0=P, zero_state=False)
+        run(W_steps)
+        eng.sync()
+        eng.reset([1], pos0=P, zero_state=False)
+        eng.sync()
+        _hip.call("afx_event_record", e0, eng.stream.cuda_stream)
+        run(K_steps)
+        _hip.call("afx_event_record", e1, eng.stream.cuda_stream)
+        ms = ctypes.c_float()
+        _hip.call("afx_event_elapsed_ms", e0, e1, ctypes.byref(ms))
+        eng.sync()
+        return K_steps / (ms.value / 1e3)
+
+    greedy = timed(lambda n: eng.run(0, n))
+    rng = np.random.default_rng(8)
+    T, top_p, top_k = 0.8, 0.9, 40
+    eng.set_sampling(T, top_p, top_k, rng.random(max(K_steps, W_steps) + 8), 0)
+    sampled = timed(lambda n: eng.run_sampled(n))
+    rows.append({"workload": f"cfg3 decode, device sampling T={T} top_p={top_p} top_k={top_k}",
+                 "tokens_per_s": sampled, "greedy_tokens_per_s": greedy})
+    return rows
 
 
 def bench_moe(args):
@@ -596,6 +653,10 @@ def main():
         return
     if args.workload == "prefill":
         print(json.dumps(bench_prefill(args)))
+        return
+    if args.workload == "sample":
+        for r in bench_sample(args):
+            print(json.dumps(r), flush=True)
         return
     if args.workload == "decode":
         res = bench_decode(args)

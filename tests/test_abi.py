@@ -75,6 +75,25 @@ def test_attention_workspace_sizes_and_their_errors_without_a_gpu():
     assert K.attn_ws_bytes(16, 32, 8, 128, 8192) == 16 * part(32)
 
 
+def test_sampler_workspace_size_and_its_check_without_a_gpu():
+    # fp64 terms for V logits (padded to 256 bytes), a 64-byte header (largest key, total mass,
+    # window), then per 2048-logit chunk: its sum (fp64), 256 suffix masses (fp64), 256 suffix counts
+    # (u32), its window offset (u32, one more) and its largest key (u32); and a 6144-logit window
+    # (key, index, fp64 term)
+    import pytest
+    from aneforge_amd import _hip, _kernels as K
+    lib = _hip.load()
+    for V in (1, 8, 2048, 2049, 32000, 151936):
+        nb = -(-V // 2048)
+        assert lib.afx_sample_ws_bytes(V) == (-(-V * 8 // 256) * 256 + 64 + nb * (8 + 256 * 8 + 256 * 4)
+                                              + (nb + 1) * 4 + 6144 * (8 + 4 + 4) + nb * 4)
+    assert lib.afx_sample_ws_bytes(0) == -1
+    assert K.sample_ws_elems(32000) * 8 >= lib.afx_sample_ws_bytes(32000)
+    # a workspace of V doubles (the old contract) is now too small: rejected before any launch
+    with pytest.raises(RuntimeError, match="afx_sample_ws_bytes"):
+        _hip.call("afx_sample", 256, 32000, 256, 256, None, None, None, 256, 256, 32000 * 8, None)
+
+
 def test_noalloc_attention_rejects_shapes_beyond_its_scratch_without_a_gpu():
     # the size check is host arithmetic before any device call: 64 sequences of 32 heads at 8192
     # positions need 34 MB of split partials, more than the 16 MiB array

@@ -536,13 +536,15 @@ def test_norm_prologue_linears_split_rows_to_fit_lds(K, fmt, M, N, Kd):
 
 
 # ----------------------------------------------------------------------------- sampling
-@pytest.mark.parametrize("V,grid", [(32000, 0.0), (1000, 0.25), (151936, 0.0)])
-def test_sample_matches_oracle(K, V, grid):
+@pytest.mark.parametrize("V,grid,sd", [(32000, 0.0, 2.5), (1000, 0.25, 2.5), (151936, 0.0, 2.5), (32000, 0.0, 0.05)])
+def test_sample_matches_oracle(K, V, grid, sd):
     # temperature / top-k / top-p / the inverse-CDF draw against the oracle's restatement of the
-    # reference's _sample; grid > 0 rounds the logits so ties are common (top-k and nucleus edges)
-    say(f"device sampling V={V} ties={grid > 0}")
+    # reference's _sample; grid > 0 rounds the logits so ties are common (top-k and nucleus edges);
+    # sd = 0.05 makes the distribution nearly flat, so a top-p nucleus holds most of the vocabulary
+    # (more than the pick kernel's LDS window: the selection runs over the whole vocabulary)
+    say(f"device sampling V={V} ties={grid > 0} sd={sd}")
     rng = np.random.default_rng(V)
-    logits = (rng.standard_normal(V) * 2.5).astype(np.float32)
+    logits = (rng.standard_normal(V) * sd).astype(np.float32)
     if grid:
         logits = (np.round(logits / grid) * grid).astype(np.float32)
     lg = dev(logits)

@@ -561,6 +561,31 @@ def test_sample_matches_oracle(K, V, grid, sd):
             assert got == want, f"T={T} top_p={top_p} top_k={top_k} u={u}: {got} vs {want}"
 
 
+@pytest.mark.parametrize("V", [1, 8, 2049, 40000])
+def test_sample_edge_cases_match_oracle(K, V):
+    """Masked (-inf) logits, a vocabulary one past a 2048-logit chunk, a single logit, ties, a nucleus
+    holding only the maximum (top_p 1e-9), top_k = 1, a very sharp (T = 0.05) and a nearly flat
+    (T = 10) distribution, each token for token against the oracle's _sample."""
+    say(f"device sampling edge cases V={V}")
+    rng = np.random.default_rng(100 + V)
+    logits = (rng.standard_normal(V) * 2.0).astype(np.float32)
+    if V >= 8:
+        logits[rng.random(V) < 0.1] = -np.inf                      # banned tokens
+        logits[3] = logits[5] = np.float32(np.max(logits[np.isfinite(logits)]) + 0.5)   # a tie at the top
+    lg = dev(logits)
+    ws = torch.empty(K.sample_ws_elems(V), dtype=torch.float64, device="cuda")
+    us = np.concatenate([[0.0, 0.5, 1.0 - 1e-12], rng.random(9)])
+    uni = torch.from_numpy(us).cuda()
+    for T, top_p, top_k in [(0.5, 1.0, 0), (1.0, 0.9, 0), (1.0, 1e-9, 0), (0.05, 0.9, 5), (10.0, 0.95, 0),
+                            (1.0, 0.5, 1), (0.8, 0.9, 3)]:
+        params = torch.tensor([T, top_p, float(top_k)], dtype=torch.float64, device="cuda")
+        for j, u in enumerate(us):
+            step = torch.tensor([j], dtype=torch.int32, device="cuda")
+            got = int(host(K.sample(lg, params, uni, step=step, ws=ws))[0])
+            want = ref.sample(logits, T, top_p, top_k, float(u))
+            assert got == want, f"V={V} T={T} top_p={top_p} top_k={top_k} u={u}: {got} vs {want}"
+
+
 # ----------------------------------------------------------------------------- small ops
 def test_rmsnorm_rope_embed_argmax(K):
     say("rmsnorm / rope / embed / argmax")

@@ -51,7 +51,35 @@ struct AttnArgs {
   long long mask_bs;
   int B, Hq, Hkv, L, Mmax, chunk, nsplit, nsp, causal_off;  // causal_off < 0: no causal masking
   float scale_log2;    // scale * log2(e)
+  int xcd;             // 1: one-dimensional grids placed by XCD (see partial_coords)
 };
+
+// Workgroup b of a launch runs on XCD b % 8.  With a.xcd set (Hkv * B a multiple of 8), both
+// launches use one-dimensional grids in which every workgroup of one (kv head, sequence) group g =
+// kvh + Hkv * b runs on XCD g % 8: the partial workgroups of all its splits, and the combine
+// workgroups of its query heads, which then read the partials from that XCD's L2 instead of HBM.
+__device__ __forceinline__ void partial_coords(const AttnArgs& a, int& split, int& kvh, int& b) {
+  if (!a.xcd) {
+    split = blockIdx.x; kvh = blockIdx.y; b = blockIdx.z;
+    return;
+  }
+  const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int g = x + 8 * (slot / a.nsplit);
+  split = slot % a.nsplit;
+  kvh = g % a.Hkv;
+  b = g / a.Hkv;
+}
+__device__ __forceinline__ void combine_coords(const AttnArgs& a, int& h, int& b) {
+  if (!a.xcd) {
+    h = blockIdx.x; b = blockIdx.y;
+    return;
+  }
+  const int gq = a.Hq / a.Hkv;
+  const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int g = x + 8 * (slot / gq);
+  h = (g % a.Hkv) * gq + slot % gq;
+  b = g / a.Hkv;
+}
 
 __device__ __forceinline__ int seq_len(const AttnArgs& a, int b) {
   int L = a.pos ? a.pos[b] + 1 : a.L;
@@ -170,7 +198,8 @@ __global__ __launch_bounds__(NW * 64) void attn_partial_kernel(AttnArgs a) {
   __shared__ float red_l[Q][G];
   __shared__ float red_o[Q][HB][D];
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  int split, kvh, b;
+  partial_coords(a, split, kvh, b);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p0 = split * C;
   const int dl = lane % LPP;       // which 8-dim slice
@@ -335,7 +364,8 @@ template <int D, int NV4>
 __global__ __launch_bounds__(D < 64 ? 64 : D) void attn_combine_kernel(AttnArgs a) {
   constexpr int NT = D < 64 ? 64 : D;
   static_assert(kMaxSplits == 128 && NV4 * 4 <= kMaxSplits, "two split statistics per lane");
-  const int h = blockIdx.x, b = blockIdx.y;
+  int h, b;
+  combine_coords(a, h, b);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int NSP = a.nsp;                        // multiple of 4, <= kMaxSplits
   const size_t bh = (size_t)b * a.Hq + h;
@@ -515,12 +545,20 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
   a.ws_ml = a.ws_o + (size_t)B * Hq * D * a.nsp;
   const attn_fn fn = D == 8 ? pick_g<8>(G, ns) : D == 16 ? pick_g<16>(G, ns) : D == 32 ? pick_g<32>(G, ns)
                    : D == 64 ? pick_g<64>(G, ns) : D == 128 ? pick_g<128>(G, ns) : pick_g<256>(G, ns);
-  hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(kAttnWaves * 64), 0, (hipStream_t)stream, a);
+  static int xcd_env = -1;                         // tuning override: AFX_ATTN_XCD=0 keeps the 3-D grids
+  if (xcd_env < 0) {
+    const char* e = getenv("AFX_ATTN_XCD");
+    xcd_env = e ? atoi(e) != 0 : 1;
+  }
+  a.xcd = xcd_env && (Hkv * B) % 8 == 0;
+  if (a.xcd) hipLaunchKernelGGL(fn, dim3(a.nsplit * Hkv * B), dim3(kAttnWaves * 64), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL(fn, dim3(a.nsplit, Hkv, B), dim3(kAttnWaves * 64), 0, (hipStream_t)stream, a);
   int rc = check_launch("afx_decode_attn");
   if (rc) return rc;
   const attn_fn cf = D == 8 ? pick_combine<8>(a.nsp) : D == 16 ? pick_combine<16>(a.nsp) : D == 32 ? pick_combine<32>(a.nsp)
                    : D == 64 ? pick_combine<64>(a.nsp) : D == 128 ? pick_combine<128>(a.nsp) : pick_combine<256>(a.nsp);
-  hipLaunchKernelGGL(cf, dim3(Hq, B), dim3(D < 64 ? 64 : D), 0, (hipStream_t)stream, a);
+  if (a.xcd) hipLaunchKernelGGL(cf, dim3(Hq * B), dim3(D < 64 ? 64 : D), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL(cf, dim3(Hq, B), dim3(D < 64 ? 64 : D), 0, (hipStream_t)stream, a);
   return check_launch("afx_decode_attn(combine)");
 }
 

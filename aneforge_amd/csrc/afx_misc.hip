@@ -1057,6 +1057,63 @@ __device__ void radix_select(const Acc& A, unsigned floor_key, SampleSmem& sm, i
   }
 }
 
+// The same radix select run by wavefront 0 alone on one LDS histogram (no workgroup barrier per
+// pass), for windows of at most kSmpWaveSel logits; the caller follows it with a barrier.  LDS
+// operations of one wavefront complete in order, so a fence and wave barrier order each pass.
+constexpr int kSmpWaveSel = 1024;
+__device__ __forceinline__ void smp_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+template <bool COUNT, class Acc>
+__device__ void radix_select_wave(const Acc& A, unsigned floor_key, SampleSmem& sm, int top = 24) {
+  const int lane = threadIdx.x & 63;
+  unsigned prefix = sm.prefix, mask = sm.mask;
+  long long remaining = sm.remaining;
+  double above = sm.above;
+  const double target = sm.target;
+  for (int shift = top; shift >= 0; shift -= 8) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (COUNT) sm.h.cnt[0][4 * lane + j] = 0u;
+      else sm.h.mass[0][4 * lane + j] = 0.0;
+    }
+    smp_wave_sync();
+    for (int i = lane; i < A.n; i += 64) {
+      const unsigned k = A.key(i);
+      if (k < floor_key || (k & mask) != prefix) continue;
+      const int bin = (k >> shift) & 255;
+      if (COUNT) atomicAdd(&sm.h.cnt[0][bin], 1u);
+      else atomicAdd(&sm.h.mass[0][bin], A.mass(i));
+    }
+    smp_wave_sync();
+    int b;
+    if (COUNT) {
+      long long v[4], ab;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = sm.h.cnt[0][4 * lane + j];
+      b = bin_walk<long long>(v, 0ll, remaining, ab);
+      remaining -= ab;
+    } else {
+      double v[4], ab;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = sm.h.mass[0][4 * lane + j];
+      b = bin_walk<double>(v, above, target, ab);
+      above = ab;
+    }
+    prefix |= (unsigned)b << shift;
+    mask |= 255u << shift;
+    smp_wave_sync();                                 // the bins are read before the next pass clears them
+  }
+  if (lane == 0) {
+    sm.prefix = prefix;
+    sm.mask = mask;
+    sm.remaining = remaining;
+    sm.above = above;
+  }
+}
+
 // The two-level draw: the chunk whose running kept mass first exceeds u * total (chunk masses
 // cm(c), inclusive scan over the lanes in a fixed order), then the position inside it (two logits
 // per thread, kept(i, key) selects; e from the workspace).  Rounding that leaves no crossing takes
@@ -1151,10 +1208,16 @@ __device__ int smp_select_draw(const Acc& A, int V, double temp, double lgmax, d
   // top-k: keep the logits >= the k-th largest (ties included)
   unsigned kfloor = 0u;
   const bool cut_k = top_k > 0 && top_k < V;
+  const bool small = A.n <= kSmpWaveSel;
   if (cut_k) {
     if (t == 0) sm.remaining = top_k;
     __syncthreads();
-    radix_select<true>(A, 0u, sm, cp_top);
+    if (small) {
+      if (wave == 0) radix_select_wave<true>(A, 0u, sm, cp_top);
+      __syncthreads();
+    } else {
+      radix_select<true>(A, 0u, sm, cp_top);
+    }
     kfloor = sm.prefix;
     __syncthreads();
     if (t == 0) { sm.prefix = cp_prefix; sm.mask = cp_mask; }
@@ -1191,7 +1254,12 @@ __device__ int smp_select_draw(const Acc& A, int V, double temp, double lgmax, d
     __syncthreads();
     if (t == 0) sm.target = top_p * Z;
     __syncthreads();
-    radix_select<false>(A, kfloor, sm, cp_top);
+    if (small) {
+      if (wave == 0) radix_select_wave<false>(A, kfloor, sm, cp_top);
+      __syncthreads();
+    } else {
+      radix_select<false>(A, kfloor, sm, cp_top);
+    }
     pkey = sm.prefix;
     const double q = exp((double)key_logit(pkey) / temp - lgmax);
     const double need = sm.target - sm.above;
@@ -1413,7 +1481,12 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
           sm.target = top_p * Z_all;
         }
         __syncthreads();
-        radix_select<false>(A, 0u, sm, ctop);
+        if (n <= kSmpWaveSel) {
+          if (wave == 0) radix_select_wave<false>(A, 0u, sm, ctop);
+          __syncthreads();
+        } else {
+          radix_select<false>(A, 0u, sm, ctop);
+        }
         const unsigned pkey = sm.prefix;
         const double q = exp((double)key_logit(pkey) / temp - lgmax);
         const double need = sm.target - sm.above;

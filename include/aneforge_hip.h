@@ -139,8 +139,8 @@ int afx_decode_attn(const void* q, const void* k, const void* v, void* o, long l
                     float scale, void* ws, long long ws_bytes, int nstep_hint, void* stream);
 /* No counterpart in the reference.  afx_decode_attn without a workspace, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
- * the split partials go to a 16 MiB device array inside the library, one per device, held until the
- * process ends.  Calls whose partials (afx_decode_attn_ws_bytes) exceed 16 MiB fail with an error.
+ * the split partials go to a 32 MiB device array inside the library, one per device, held until the
+ * process ends.  Calls whose partials (afx_decode_attn_ws_bytes) exceed 32 MiB fail with an error.
  * The stream must belong to the calling thread's current device.  Calls that overlap on one device
  * share the array and race. */
 int afx_decode_attn_noalloc(const void* q, const void* k, const void* v, void* o, long long q_bs,

@@ -67,12 +67,13 @@ def test_attention_workspace_sizes_and_their_errors_without_a_gpu():
         K.attn_ws_bytes(1, 32, 8, 128, 8192, nstep_hint=1)
     # the split size: fewest dispatch rounds over 256 CUs times the chunk.  ctx 2048: 64-position
     # chunks, 32 splits x 8 kv heads = one round; the 7B engine's 2184-row cache: 80-position chunks
-    # (28 splits, 224 workgroups) rather than 64 (35 splits, 280 workgroups, a second round)
+    # (28 splits, 224 workgroups) rather than 64 (35 splits, 280 workgroups, a second round); B=16 at
+    # ctx 8192 ties every chunk of 4..16 steps and takes 8 steps (128 positions, 64 splits), not 16
     part = lambda nsp: 32 * nsp * (128 + 2) * 4
     assert n == part(32)
     assert K.attn_ws_bytes(1, 32, 8, 128, 2184) == part(28)
     assert K.attn_ws_bytes(1, 32, 8, 128, 2184, nstep_hint=4) == part(36)   # 35 splits, padded to 4
-    assert K.attn_ws_bytes(16, 32, 8, 128, 8192) == 16 * part(32)
+    assert K.attn_ws_bytes(16, 32, 8, 128, 8192) == 16 * part(64)
 
 
 def test_sampler_workspace_size_and_its_check_without_a_gpu():
@@ -96,7 +97,7 @@ def test_sampler_workspace_size_and_its_check_without_a_gpu():
 
 def test_noalloc_attention_rejects_shapes_beyond_its_scratch_without_a_gpu():
     # the size check is host arithmetic before any device call: 64 sequences of 32 heads at 8192
-    # positions need 34 MB of split partials, more than the 16 MiB array
+    # positions (16-step chunks: 32 splits) need 34 MB of split partials, more than the 32 MiB array
     import pytest
     from aneforge_amd import _hip
     with pytest.raises(RuntimeError, match="scratch array"):

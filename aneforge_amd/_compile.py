@@ -350,12 +350,28 @@ class _Lowering:
                                                K.stream()))
 
     # -- matmuls --
+    _GEMM_MIN_ROWS = 17
+
     def _gemv_rows(self, lin: "E.Linear", x2, y2, bias=None):
-        """y2[M, N] = x2[M, K] @ W^T (+bias), in row blocks of up to 8 (the GEMV's M limit)."""
+        """y2[M, N] = x2[M, K] @ W^T (+bias) as one contraction over all M rows, as the reference emits
+        one matmul for any M (aneforge/_compile.py:375-385).  Up to 16 rows: one afx_linear (vector GEMV
+        to 3 rows, the skinny MFMA kernel from 4).  From 17 rows: the MFMA GEMM, which streams the weight
+        once per 128-row tile; formats it does not read packed are expanded to fp16 first (once per
+        call, into a buffer of this program), as the batched prefill does."""
         M = x2.shape[0]
-        for r0 in range(0, M, 8):
-            xs, ys = x2[r0:r0 + 8], y2[r0:r0 + 8]
-            self.steps.append(lambda xs=xs, ys=ys: K.linear(lin.fmt, lin.w, lin.scale, xs, y=ys, bias=bias))
+        if M >= self._GEMM_MIN_ROWS and lin.K % 64 == 0 and lin.N % 16 == 0:
+            if lin.fmt in E._GEMM_FMTS:
+                self.steps.append(lambda: K.gemm(lin.fmt, lin.w, lin.scale, x2, y=y2, bias=bias))
+                return
+            w16 = torch.empty((lin.N, lin.K), dtype=torch.float16, device="cuda")
+            self.keep.append(w16)
+
+            def run():
+                K.dequant_f16(lin.fmt, lin.w, lin.scale, lin.N, lin.K, out=w16)
+                K.gemm("fp16", w16, None, x2, y=y2, bias=bias)
+            self.steps.append(run)
+            return
+        self.steps.append(lambda: K.linear(lin.fmt, lin.w, lin.scale, x2, y=y2, bias=bias))
 
     def _op_matmul(self, t):
         x = self.buf[id(t.srcs[0])]

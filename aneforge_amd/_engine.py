@@ -372,6 +372,7 @@ class AttentionDecode:
 
 class SwiGLUDecode:
     """SwiGLU MLP with residual (aneforge/llm.py:171-175): h + down(silu(gate(n)) * up(n)), n = rms(h)."""
+    GELU = False                   # the gate's activation: silu (SwiGLU) or tanh-GELU (GeGLU)
 
     def __init__(self, lw: dict, cfg, ls, compress):
         D = cfg.dim
@@ -399,7 +400,7 @@ class SwiGLUDecode:
 
     def enqueue(self, eng):
         act = eng.act[:, :self.F]
-        K.linear_swiglu(self.gu.fmt, self.gu.w, self.gu.scale, eng.h, self.norm, self.eps, act=act)
+        K.linear_swiglu(self.gu.fmt, self.gu.w, self.gu.scale, eng.h, self.norm, self.eps, act=act, gelu=self.GELU)
         K.linear(self.down.fmt, self.down.w, self.down.scale, act, y=eng.h, residual=eng.h)
 
     def prefill_supported(self) -> bool:
@@ -411,12 +412,18 @@ class SwiGLUDecode:
         hn = bufs["hn"][:m]
         K.rmsnorm(X, self.norm, self.eps, y=hn)
         act = bufs["act"][:m, :self.F]
-        prefill_gemm(eng, self.gu, hn, act, epi="swiglu")
+        prefill_gemm(eng, self.gu, hn, act, epi="geglu" if self.GELU else "swiglu")
         prefill_gemm(eng, self.down, act, X, residual=X, epi="resid")
 
     @property
     def nbytes(self):
         return self.gu.nbytes + self.down.nbytes + self.norm.numel() * 2
+
+
+class GeGLUDecode(SwiGLUDecode):
+    """GeGLU MLP with residual, Gemma's (aneforge/llm.py:191-196): h + down(gelu_tanh(gate(n)) * up(n)),
+    on the SwiGLU kernels with the tanh-GELU activation in the same epilogue."""
+    GELU = True
 
 
 # ----------------------------------------------------------------------------- the engine
@@ -513,14 +520,21 @@ class DecodeEngine:
         if was_on != self._tie_on:                    # the captured steps change shape: capture again
             self.close()
 
-    def enqueue_advance(self, with_logits: bool):
+    def enqueue_advance(self, with_logits: bool, gather: bool = True):
+        """The step's token (forced, or the greedy pick) and bookkeeping; `gather` also writes the
+        token's embedding row into h (otherwise enqueue_embed does it as a launch of its own)."""
         fused = with_logits and self.head.fmt == "fp16" and self.head.bias is None
         tie = fused and self._tie_on
         K.decode_advance(self.logits if with_logits else None, self.tok, self.pos, self.hist, self.step,
-                         self.embed, self.h, self.forced, self.n_forced, slots=self.slots if fused else None,
+                         self.embed if gather else None, self.h, self.forced, self.n_forced,
+                         slots=self.slots if fused else None,
                          tie_margin=self.tie_margin if tie else None, hn=self.hn if tie else None,
                          head16=self.head.w if tie and self.head32 is None else None,
                          head32=self.head32 if tie else None)
+
+    def enqueue_embed(self, ids):
+        """h = embed[ids[0]] (ids: a one-element int32 device tensor)."""
+        K.embed(self.embed, ids, out=self.h)
 
     def enqueue_sample(self):
         """The step's token from the logits by the device sampler, queued as forced[step]."""

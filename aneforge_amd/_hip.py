@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple] = {
     "afx_linear_rms": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "afx_lm_head": (_i, [_i, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _vp, _vp, _vp]),
     "afx_linear_swiglu": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _i, _vp, _i, _i, _i, _i, _i, _vp]),
+    "afx_linear_geglu": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "afx_qkv_rope_kv": (_i, [_i, _vp, _vp, _vp, _i, _vp, _f, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _vp,
                              _vp, _i, _vp, _vp, _ll, _ll, _i, _i, _i, _i, _vp]),
     # codecs

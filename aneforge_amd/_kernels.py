@@ -72,15 +72,16 @@ def linear_rms(fmt, w, scale, x, gamma, eps, y=None, bias=None, out_f32=False, r
     return y
 
 
-def linear_swiglu(fmt, w, scale, x, gamma=None, eps=0.0, act=None, rows_hint=0):
-    """act[M, F] = silu(g) * u with rows of W interleaved (gate_i, up_i); RMSNorm first if gamma."""
+def linear_swiglu(fmt, w, scale, x, gamma=None, eps=0.0, act=None, rows_hint=0, gelu=False):
+    """act[M, F] = silu(g) * u (gelu: gelu_tanh(g) * u, GeGLU) with rows of W interleaved
+    (gate_i, up_i); RMSNorm first if gamma."""
     _dev(w, x)
     M, K = x.shape
     N = w.shape[0]
     if act is None:
         act = torch.empty((M, N // 2), dtype=torch.float16, device=x.device)
-    _hip.call("afx_linear_swiglu", FMT[fmt], P(w), P(scale), P(x), x.stride(0), P(gamma), float(eps),
-              int(gamma is not None), P(act), act.stride(0), M, N, K, rows_hint, stream())
+    _hip.call("afx_linear_geglu" if gelu else "afx_linear_swiglu", FMT[fmt], P(w), P(scale), P(x), x.stride(0),
+              P(gamma), float(eps), int(gamma is not None), P(act), act.stride(0), M, N, K, rows_hint, stream())
     return act
 
 
@@ -441,16 +442,16 @@ def moe_combine(h, y, gate, shared=None, out=None):
 
 
 # ----------------------------------------------------------------------------- batched prefill
-GEMM_EPI = {"f16": 0, "resid": 1, "f32": 2, "swiglu": 3}
+GEMM_EPI = {"f16": 0, "resid": 1, "f32": 2, "swiglu": 3, "geglu": 5}
 
 
 def gemm(fmt, w, scale, x, y=None, bias=None, residual=None, epi="f16"):
-    """MFMA GEMM for many rows: y = epi(x @ W^T); epi "swiglu" writes [M, N/2]."""
+    """MFMA GEMM for many rows: y = epi(x @ W^T); epi "swiglu" / "geglu" writes [M, N/2]."""
     _dev(w, x)
     M, Kd = x.shape
     N = w.shape[0]
     if y is None:
-        cols = N // 2 if epi == "swiglu" else N
+        cols = N // 2 if epi in ("swiglu", "geglu") else N
         y = torch.empty((M, cols), dtype=torch.float32 if epi == "f32" else torch.float16, device=x.device)
     if epi == "resid" and residual is None:
         residual = y

@@ -587,8 +587,14 @@ int scratch_ptr(void* stream, void** out) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_dev[dev]) {
+    // The first call on a device may come while the caller captures a graph: the symbol lookup is no
+    // stream work, so this thread's capture mode is relaxed around it (and restored) so that a
+    // capture in the global mode does not reject it.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const hipError_t em = hipThreadExchangeStreamCaptureMode(&mode);
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (em == hipSuccess) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || !p)
       return set_error("afx_decode_attn_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
     g_scratch_dev[dev] = p;

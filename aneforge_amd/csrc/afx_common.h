@@ -133,6 +133,16 @@ __device__ __forceinline__ int reduced_row_of_lane(int lane) {
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// tanh-approximated GELU (the "gelu_pytorch_tanh" of Gemma's GeGLU), 0.5 g (1 + tanh(z)) with
+// z = sqrt(2/pi) (g + 0.044715 g^3); since 0.5 (1 + tanh(z)) = 1 / (1 + exp(-2z)), this is
+// g / (1 + exp(-2z)): the same form as silu with a different argument.
+__device__ __forceinline__ float gelu_tanh(float g) {
+  const float two_z = 1.5957691216057308f * (g + 0.044715f * g * g * g);   // 2 * sqrt(2/pi) * (...)
+  return g / (1.0f + __expf(-two_z));
+}
+// The gated MLP activation of an interleaved (gate, up) row pair: silu for SwiGLU, tanh-GELU for
+// GeGLU (gelu = 1; a uniform flag, so the two share every kernel instance).
+__device__ __forceinline__ float glu_act(bool gelu, float g) { return gelu ? gelu_tanh(g) : silu(g); }
 
 // Greedy-pick summaries {largest value, its index (int bits), second largest, largest magnitude}
 // of two disjoint index ranges, merged: the larger first value wins, the lower index on an exact

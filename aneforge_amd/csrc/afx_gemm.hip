@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
           const float pv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
           if ((fr & 1) == 0 && m < M && n < N) {
             const float g = (float)(half_t)v, u = (float)(half_t)pv;
-            ((half_t*)a.y)[(size_t)m * a.ldy + (n >> 1)] = (half_t)(silu(g) * u);
+            ((half_t*)a.y)[(size_t)m * a.ldy + (n >> 1)] = (half_t)(glu_act(a.epi == EPI_GEGLU, g) * u);
           }
         } else {
           if (m < M && n < N) {
@@ -210,7 +210,7 @@ extern "C" {
 
 // Y = epilogue(X @ W^T) for M activation rows (batched prefill).  fmt: 0 = int8 + row scale,
 // 2 = fp16, 3 = int8 + fp16 scale per 32-weight block.  epi: 0 fp16, 1 fp16 + residual (resid [M][ldy], may alias y), 2 fp32, 3 SwiGLU
-// over interleaved gate/up rows (y[m][n/2] = silu(g) * u, ldy >= N/2).
+// over interleaved gate/up rows (y[m][n/2] = silu(g) * u, ldy >= N/2), 5 GeGLU (the same with gelu_tanh(g)).
 int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, void* y, int ldy, int M, int N,
              int K, const void* bias, const void* residual, int epi, void* stream) {
   AFX_REQUIRE(fmt == FMT_I8 || fmt == FMT_F16 || fmt == FMT_BW,
@@ -220,11 +220,12 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
               "afx_gemm: need M >= 1, N %% 16 == 0, K %% 64 == 0 (M=%d N=%d K=%d)", M, N, K);
   AFX_REQUIRE(ldx >= K && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0,
               "afx_gemm: x and weights must be 16-byte aligned rows (ldx %% 8 == 0)");
-  AFX_REQUIRE(epi >= 0 && epi <= 3, "afx_gemm: unknown epilogue %d", epi);
+  AFX_REQUIRE((epi >= 0 && epi <= 3) || epi == EPI_GEGLU, "afx_gemm: unknown epilogue %d", epi);
+  const bool glu = epi == EPI_SWIGLU || epi == EPI_GEGLU;
   AFX_REQUIRE(fmt != FMT_I8 || scale, "afx_gemm: int8 weights need row scales");
   AFX_REQUIRE(fmt != FMT_BW || (scale && ((uintptr_t)scale & 3) == 0), "afx_gemm: blockwise weights need aligned block scales");
   AFX_REQUIRE(epi != EPI_RESID || residual, "afx_gemm: residual pointer required");
-  AFX_REQUIRE(epi == EPI_SWIGLU ? ldy >= N / 2 : ldy >= N, "afx_gemm: ldy=%d too small", ldy);
+  AFX_REQUIRE(glu ? ldy >= N / 2 : ldy >= N, "afx_gemm: ldy=%d too small", ldy);
   GemmArgs a = {};
   a.w = w; a.scale = (const half_t*)scale; a.bias = (const half_t*)bias; a.x = (const half_t*)x; a.y = y;
   a.resid = (const half_t*)residual; a.ldx = ldx; a.ldy = ldy; a.M = M; a.N = N; a.K = K; a.epi = epi;
@@ -232,9 +233,9 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   a.tiles = a.tiles_m * ((N + kGBN - 1) / kGBN);
   a.per_xcd = (a.tiles + 7) / 8;
   gemm_fn fn;
-  if (fmt == FMT_I8) fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_I8, EG_SWIGLU> : gemm_kernel<FMT_I8, EG_PLAIN>;
-  else if (fmt == FMT_BW) fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_BW, EG_SWIGLU> : gemm_kernel<FMT_BW, EG_PLAIN>;
-  else fn = epi == EPI_SWIGLU ? gemm_kernel<FMT_F16, EG_SWIGLU> : gemm_kernel<FMT_F16, EG_PLAIN>;
+  if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU> : gemm_kernel<FMT_I8, EG_PLAIN>;
+  else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU> : gemm_kernel<FMT_BW, EG_PLAIN>;
+  else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU> : gemm_kernel<FMT_F16, EG_PLAIN>;
   hipLaunchKernelGGL(fn, dim3(8 * a.per_xcd), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("afx_gemm");
 }

@@ -257,6 +257,19 @@ int afx_linear_swiglu(int fmt, const void* w, const void* scale, const void* x, 
   return launch(fmt, a, EG_SWIGLU, rows_hint, (hipStream_t)stream, "afx_linear_swiglu");
 }
 
+// GeGLU MLP front half (Gemma, aneforge/llm.py:185-196): act[m][i] = gelu_tanh(g_i) * u_i, otherwise
+// exactly afx_linear_swiglu (same arguments, kernels and row interleaving).
+int afx_linear_geglu(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
+                     float eps, int norm, void* act, int ld_act, int M, int N, int K, int rows_hint,
+                     void* stream) {
+  AFX_REQUIRE(fmt >= 0 && fmt <= 6, "afx_linear_geglu: unknown weight format %d", fmt);
+  AFX_REQUIRE(!norm || gamma, "afx_linear_geglu: RMSNorm prologue needs gamma");
+  AFX_REQUIRE(ld_act >= N / 2, "afx_linear_geglu: ld_act=%d < N/2=%d", ld_act, N / 2);
+  GemvArgs a = base_args(w, scale, x, ldx, act, ld_act, M, N, K, nullptr, EPI_GEGLU);
+  a.gamma = norm ? (const half_t*)gamma : nullptr; a.eps = eps;
+  return launch(fmt, a, EG_SWIGLU, rows_hint, (hipStream_t)stream, "afx_linear_geglu");
+}
+
 // Fused attention input projection for decode: [q|k|v] = rms_norm(h) @ Wqkv^T (+bias), RoPE on
 // q and k (rows interleaved per head as (d, d+dh/2)), q -> qout[M][nq], k/v -> the caches at
 // row pos[m]:  cache[m*seq_stride + kvh*head_stride + pos*dh + d]; pos outside [0, kv_len) is skipped.

@@ -41,7 +41,8 @@
 //   EG_PLAIN   runtime-selected store: EPI_F16  y = fp16(acc*s + bias)
 //                                      EPI_RESID y = fp16(resid + fp16(acc*s + bias))  (llm.py:237)
 //                                      EPI_F32  y = acc*s + bias as fp32 (logits)
-//   EG_SWIGLU  rows interleaved (gate_i, up_i): act[i] = fp16(silu(g16) * u16)   (llm.py:171-175)
+//   EG_SWIGLU  rows interleaved (gate_i, up_i): act[i] = fp16(silu(g16) * u16)   (llm.py:171-175),
+//              or fp16(gelu_tanh(g16) * u16) when epi is EPI_GEGLU (Gemma, llm.py:185-196)
 //   EG_QKV     fused q|k|v rows; q and k rows are interleaved per head as (d, d+dh/2) pairs so
 //              RoPE (llm.py:96-105) is applied to the pair; k and v are written straight into
 //              the resident cache at row pos (replaces the masked O(M) rewrite, llm.py:233).
@@ -53,7 +54,7 @@
 
 namespace afx {
 
-enum { EPI_F16 = 0, EPI_RESID = 1, EPI_F32 = 2, EPI_SWIGLU = 3, EPI_QKV = 4 };
+enum { EPI_F16 = 0, EPI_RESID = 1, EPI_F32 = 2, EPI_SWIGLU = 3, EPI_QKV = 4, EPI_GEGLU = 5 };
 enum { EG_PLAIN = 0, EG_SWIGLU = 1, EG_QKV = 2, EG_HEAD = 3 };
 
 struct GemvArgs {
@@ -144,7 +145,7 @@ __device__ __forceinline__ void gemv_store(const GemvArgs& a, const float (&v)[M
       }
     } else if constexpr (EG == EG_SWIGLU) {
       const float g16 = (float)(half_t)v[m][0], u16 = (float)(half_t)v[m][1];
-      ((half_t*)a.y)[(size_t)m * a.ldy + (row0 >> 1)] = (half_t)(silu(g16) * u16);
+      ((half_t*)a.y)[(size_t)m * a.ldy + (row0 >> 1)] = (half_t)(glu_act(a.epi == EPI_GEGLU, g16) * u16);
     } else {
       const int p = e_pos[m];
       if (p < 0 || p >= a.kv_len) continue;

@@ -21,7 +21,7 @@ struct MfmaArgs {
   int x_by_token;          // MoE: x row of an entry = entry / k (1) or the entry itself (0)
   int M;                   // dense: activation rows (<= 16 per token group; any count, in groups)
   int N, K;
-  int epi;                 // EPI_F16 / EPI_RESID / EPI_F32 / EPI_SWIGLU (gemv epilogue codes)
+  int epi;                 // EPI_F16 / EPI_RESID / EPI_F32 / EPI_SWIGLU / EPI_GEGLU (gemv epilogue codes)
   int xbytes;              // set by mfma_launch: bytes of the activation rows the kernel may read
   int E;                   // set by mfma_launch: experts (1 for a dense linear)
   float* ws;               // optional fp32 workspace for K-split partials (null: no split)

@@ -136,8 +136,9 @@ __device__ __forceinline__ void mfma_store(const MfmaArgs& a, const EpiOps& ops,
     half_t* yp = (half_t*)a.y + (size_t)yr * a.ldy + (rb >> 1);
     const float g0 = (float)(half_t)v[0], u0 = (float)(half_t)v[1];
     const float g1 = (float)(half_t)v[2], u1 = (float)(half_t)v[3];
-    yp[0] = (half_t)(silu(g0) * u0);
-    yp[1] = (half_t)(silu(g1) * u1);
+    const bool gelu = a.epi == EPI_GEGLU;
+    yp[0] = (half_t)(glu_act(gelu, g0) * u0);
+    yp[1] = (half_t)(glu_act(gelu, g1) * u1);
   } else if (a.epi == EPI_F32) {
     float* yp = (float*)a.y + (size_t)yr * a.ldy + rb;
 #pragma unroll
@@ -722,7 +723,7 @@ int mfma_launch(int fmt, const MfmaArgs& a, int E, hipStream_t stream, const cha
   MfmaArgs b = a;
   b.xbytes = (int)xbytes;
   b.E = E;
-  const bool swiglu = a.epi == EPI_SWIGLU;
+  const bool swiglu = a.epi == EPI_SWIGLU || a.epi == EPI_GEGLU;   // gated pair epilogue
   // wavefronts per workgroup: the fewest of 4, 8, 16 that leave each wavefront at most four
   // batches; batches per round = batches per wavefront, capped at 4 (measured on MI355X);
   // AFX_MFMA_WAVES=4|8|16 overrides when that count also leaves at most four batches

@@ -27,9 +27,9 @@ class ModelType(str, Enum):
     QWEN = "qwen"
 
 
-# Architectures whose semantics the dense Llama path would drop (Gemma's sqrt(dim) embedding scale,
-# (1 + w) norms and GeGLU; Gemma-2/3 softcapping and sliding attention): rejected, never mis-loaded.
-_DENSE_INCOMPATIBLE = {ModelType.GEMMA, ModelType.GEMMA2, ModelType.GEMMA3, ModelType.GEMMA3_TEXT}
+# Architectures whose semantics the dense Llama path would drop (Gemma-2/3 softcapping and sliding
+# attention; aneforge/llm.py:30-32): rejected, never mis-loaded.  Gemma has its own adapter.
+_DENSE_INCOMPATIBLE = {ModelType.GEMMA2, ModelType.GEMMA3, ModelType.GEMMA3_TEXT}
 
 
 @dataclass
@@ -118,7 +118,7 @@ def rope(x, cos, sin):
 from . import _engine as _eng  # noqa: E402
 
 DECODE_MIXERS: dict = {"attention": _eng.AttentionDecode}
-DECODE_MLPS: dict = {"swiglu": _eng.SwiGLUDecode}
+DECODE_MLPS: dict = {"swiglu": _eng.SwiGLUDecode, "geglu": _eng.GeGLUDecode}
 PREFILL_MIXERS: dict = DECODE_MIXERS
 PREFILL_MLPS: dict = DECODE_MLPS
 
@@ -314,7 +314,6 @@ class LlamaPrefill:
         eos = {int(eos_id)} if isinstance(eos_id, int) else {int(e) for e in (eos_id or ())}
         use_dev = self.ane_lm_head if ane_lm_head is None else bool(ane_lm_head)
         d = self._decoder(M)
-        t0 = time.perf_counter()
         if batched_prefill:
             d.prefill(prompt)                  # batched MFMA prefill (forced steps where unsupported)
             n_run = 0
@@ -334,44 +333,89 @@ class LlamaPrefill:
                 d.set_sampling(temperature, top_p, top_k, np.random.random_sample(n_gen), n_pre)
                 d.run_sampled(n_gen)
             return d.history(n_pre, n_gen)
-        d.run(n_run, 0)
-        if on_stage is not None:
-            d.sync()
-            on_stage("prefill", time.perf_counter() - t0)
-        out = []
         import torch
-        for i in range(n_gen):
-            t1 = time.perf_counter()
-            if greedy and use_dev:
-                d.run(0, 1)
-                nxt = d.history(n_pre + i, 1)[0]
-            elif use_dev:
-                d.set_sampling(temperature, top_p, top_k, [np.random.random_sample()], n_pre + i)
-                d.run_sampled(1)
-                nxt = d.history(n_pre + i, 1)[0]
-            else:                                    # host lm_head (ane_lm_head=False)
+        profiling = on_stage is not None
+        if profiling and n_run:
+            # token-by-token prefill, staged as the reference's step() is (aneforge/llm.py:583-597)
+            for p in range(n_run):
+                self._profiled_step(d, p - 1, prompt[0], on_stage)
                 with torch.cuda.stream(d.stream):
-                    d.enqueue_layers()
-                d.sync()
+                    d.enqueue_advance(False, gather=False)
+        else:
+            d.run(n_run, 0)
+        out = []
+        for i in range(n_gen):
+            k = n_pre + i
+            if profiling:
+                # the reference's per-token stages (aneforge/llm.py:568-628): embedding and layers are
+                # the two halves of `step`, then lm_head and sample; each stage is its own launches,
+                # timed to the end of its device work
+                t1 = time.perf_counter()
+                self._profiled_step(d, k - 1, prompt[0], on_stage)
+                on_stage("step", time.perf_counter() - t1)
+            t1 = time.perf_counter()
+            if use_dev:
+                with torch.cuda.stream(d.stream):
+                    if profiling:
+                        d.enqueue_head()
+                        d.sync()
+                        on_stage("lm_head", time.perf_counter() - t1)
+                        t1 = time.perf_counter()
+                        if not greedy:
+                            d.set_sampling(temperature, top_p, top_k, [np.random.random_sample()], k)
+                            d.enqueue_sample()
+                        d.enqueue_advance(greedy, gather=False)
+                    elif greedy:
+                        d.run(0, 1)
+                    else:
+                        d.set_sampling(temperature, top_p, top_k, [np.random.random_sample()], k)
+                        d.run_sampled(1)
+                nxt = d.history(k, 1)[0]
+            else:                                    # host lm_head (ane_lm_head=False)
+                if not profiling:
+                    with torch.cuda.stream(d.stream):
+                        d.enqueue_layers()
+                    d.sync()
                 hn = d.h.float().cpu().numpy()[0]
                 g = np.asarray(self.w["final_norm"], np.float64)
                 hn = hn / np.sqrt((hn.astype(np.float64) ** 2).mean() + self.cfg.norm_eps) * g
                 logits = self._host_logits(hn.astype(np.float16).astype(np.float32))
+                if profiling:
+                    on_stage("lm_head", time.perf_counter() - t1)
+                    t1 = time.perf_counter()
                 nxt = self._sample(logits, temperature, top_p, top_k)
-                k = n_pre + i
                 with torch.cuda.stream(d.stream):
                     d.forced[k].fill_(nxt)
                     d.n_forced.fill_(k + 1)
-                    d.enqueue_advance(False)
-            if on_stage is not None:
+                    d.enqueue_advance(False, gather=not profiling)
                 d.sync()
-                on_stage("step", time.perf_counter() - t1)
+            if profiling:
+                on_stage("sample", time.perf_counter() - t1)
             out.append(int(nxt))
             if nxt in eos:
                 break
             if on_token is not None:
                 on_token(int(nxt))
         return out
+
+    @staticmethod
+    def _profiled_step(d, hist_idx: int, first_tok: int, on_stage):
+        """One decode step's layers with the pending token's embedding gathered as a launch of its
+        own (the token is hist[hist_idx], or first_tok before any step): emits `embedding` and
+        `layers`, each timed to the end of its device work."""
+        import torch
+        t0 = time.perf_counter()
+        with torch.cuda.stream(d.stream):
+            ids = (d.hist[hist_idx:hist_idx + 1] if hist_idx >= 0
+                   else torch.tensor([int(first_tok)], dtype=torch.int32, device="cuda"))
+            d.enqueue_embed(ids)
+        d.sync()
+        on_stage("embedding", time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        with torch.cuda.stream(d.stream):
+            d.enqueue_layers()
+        d.sync()
+        on_stage("layers", time.perf_counter() - t0)
 
 
 # ----------------------------------------------------------------------------- HF adapters
@@ -443,16 +487,54 @@ def _cfg_from_hf(c) -> LlamaConfig:
                        rope_scaling=_rope_scaling(c))
 
 
+def _gemma_adapter(c, sd) -> tuple[LlamaConfig, dict]:
+    """Gemma (aneforge/llm.py:685-700): a Llama-shaped decoder whose differences go into the weights at
+    load time: the embedding rows scaled by sqrt(dim) (HF scales the looked-up embeddings; the tied
+    head keeps the unscaled table), the RMSNorm gains in the (1 + w) convention, and the GeGLU MLP
+    (`LayerSpec(mlp="geglu")`, tanh-GELU on the gate)."""
+    n = int(c.num_hidden_layers)
+    cfg = LlamaConfig(dim=c.hidden_size, n_layers=n, n_heads=c.num_attention_heads,
+                      n_kv_heads=int(getattr(c, "num_key_value_heads", c.num_attention_heads)),
+                      ffn_dim=c.intermediate_size, vocab=c.vocab_size, rope_base=_rope_theta(c),
+                      norm_eps=float(c.rms_norm_eps), head_dim=int(getattr(c, "head_dim", 0) or 0),
+                      layers=[LayerSpec(mixer="attention", mlp="geglu") for _ in range(n)])
+    w = _weights_from_state_dict(sd, cfg)
+    w["embed"] = np.asarray(w["embed"], np.float32) * np.float32(np.sqrt(c.hidden_size))
+    for lw in w["layers"]:
+        lw["attn_norm"] = np.asarray(lw["attn_norm"], np.float32) + 1.0
+        lw["mlp_norm"] = np.asarray(lw["mlp_norm"], np.float32) + 1.0
+    w["final_norm"] = np.asarray(w["final_norm"], np.float32) + 1.0
+    return cfg, w
+
+
+def _gpt2_adapter(c, sd):
+    """GPT-2 (the reference's adapter, aneforge/llm.py:730-763) needs LayerNorm with a bias, learned
+    position embeddings and a non-gated GELU MLP with biases; none of these is on this device decode
+    path, so the architecture is refused by name rather than mis-loaded as a Llama."""
+    raise ValueError("load_llm: 'gpt2' (LayerNorm, learned position embeddings, GELU MLP) is not on this "
+                     "decode path; supported: dense Llama / Qwen / Mistral, Gemma and Qwen-MoE")
+
+
 ADAPTERS: list = [
+    (lambda c: getattr(c, "model_type", None) == ModelType.GPT2, _gpt2_adapter),
+    (lambda c: getattr(c, "model_type", None) == ModelType.GEMMA, _gemma_adapter),
     (lambda c: getattr(c, "model_type", None) == ModelType.MISTRAL, _mistral_adapter),
 ]
+
+
+def adapter_for(c):
+    """The adapter from_pretrained uses for a Hugging Face config (first registered match, else the
+    dense Llama adapter after its compatibility check)."""
+    adapt = next((fn for pred, fn in ADAPTERS if pred(c)), _dense_adapter)
+    if adapt is _dense_adapter:
+        _assert_dense_compatible(c)
+    return adapt
 
 
 def _assert_dense_compatible(c) -> None:
     """A config headed for the dense Llama adapter must not carry semantics that adapter ignores: logit
     softcapping (checked first, so a Llama-shaped finetune with an unusual model_type still loads) or
-    one of the architectures listed above.  The reference draws the same line (aneforge/llm.py:776-788);
-    its Gemma adapter is not built here, so Gemma is refused too."""
+    one of the architectures listed above.  The reference draws the same line (aneforge/llm.py:776-788)."""
     model_type = getattr(c, "model_type", "?")
     softcap = getattr(c, "attn_logit_softcapping", None) or getattr(c, "final_logit_softcapping", None)
     if softcap:
@@ -460,7 +542,7 @@ def _assert_dense_compatible(c) -> None:
                          f"implement; loading it would give wrong logits")
     if model_type in _DENSE_INCOMPATIBLE:
         raise ValueError(f"load_llm: {model_type!r} has architecture-specific semantics the dense decoder does "
-                         f"not implement (supported: dense Llama / Qwen / Mistral and Qwen-MoE)")
+                         f"not implement (supported: dense Llama / Qwen / Mistral, Gemma and Qwen-MoE)")
 
 
 def from_pretrained(name: str, compress: str | None = None, ane_lm_head: bool = True) -> LlamaPrefill:
@@ -469,9 +551,7 @@ def from_pretrained(name: str, compress: str | None = None, ane_lm_head: bool = 
     import torch
     from transformers import AutoModelForCausalLM
     hf = AutoModelForCausalLM.from_pretrained(name)
-    adapt = next((fn for pred, fn in ADAPTERS if pred(hf.config)), _dense_adapter)
-    if adapt is _dense_adapter:
-        _assert_dense_compatible(hf.config)
+    adapt = adapter_for(hf.config)
     sd = {k: v.detach().to(torch.float16).numpy() for k, v in hf.state_dict().items()}
     cfg, weights = adapt(hf.config, sd)
     return LlamaPrefill(cfg, weights, compress=compress, ane_lm_head=ane_lm_head)

@@ -91,6 +91,11 @@ int afx_lm_head(int fmt, const void* w, const void* scale, const void* x, const 
 int afx_linear_swiglu(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
                       float eps, int norm, void* act, int ld_act, int M, int N, int K, int rows_hint,
                       void* stream);
+/* act[M][N/2] = gelu_tanh(g) * u, otherwise as afx_linear_swiglu: the front half of _geglu, Gemma's
+ * MLP (aneforge/llm.py:185-196; gelu_tanh is the reference's _gelu_tanh, llm.py:185-189). */
+int afx_linear_geglu(int fmt, const void* w, const void* scale, const void* x, int ldx, const void* gamma,
+                     float eps, int norm, void* act, int ld_act, int M, int N, int K, int rows_hint,
+                     void* stream);
 /* [q|k|v] = rms_norm(h) @ Wqkv^T (+bias), RoPE on q and k, k/v written into the resident cache
  * at row pos[m]: the projection half of _attn_decode (aneforge/llm.py:214-233) including the
  * masked positional cache write Kin*inv + k*oh, done here as one O(1) row store. */

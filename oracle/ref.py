@@ -25,7 +25,10 @@ Pinning status (see tests/test_oracle.py):
   rope_tables / rope / llama3 scaling    pinned: transformers' rope utilities + HF formula
   attention (sdpa / GQA decode)         pinned: torch SDPA, ctx=1 and equal-key cases
   topk_gate / moe_layer                 pinned: reference tie KAT + HF Qwen3-MoE block
-  decoder step / generate               pinned: HF LlamaForCausalLM (tiny, fp32)
+  decoder step / generate               pinned: HF LlamaForCausalLM (tiny, fp32); with cfg mlp="geglu"
+                                        and Gemma-baked weights, HF GemmaForCausalLM (tiny, fp64)
+  gelu_tanh                             pinned: torch's gelu(approximate="tanh")
+  cpu_decode_layer_f32 (timed baseline) pinned: decode_layer(exact=True) at a reduced GQA layer
   decode_rows                           pinned: n sequential decode_layer calls (dense and MoE layers)
   palettize_lut4 (aneforge_amd._blob)   pinned: vectors recorded from the reference function
                                         (tests/golden/make_lut4_vectors.py, lut4_vectors.npz)
@@ -305,6 +308,19 @@ def silu(x):
     return x / (1.0 + np.exp(-x))
 
 
+def gelu_tanh(x):
+    """The tanh-approximated GELU, 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))): the reference's
+    _gelu_tanh (aneforge/llm.py:185-189), Gemma's gelu_pytorch_tanh."""
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def glu_act(cfg):
+    """The gated MLP's gate activation: silu for SwiGLU (aneforge/llm.py:171-175), tanh-GELU for the
+    GeGLU of Gemma (cfg["mlp"] == "geglu", aneforge/llm.py:191-196)."""
+    return gelu_tanh if cfg.get("mlp", "swiglu") == "geglu" else silu
+
+
 # ----------------------------------------------------------------------------- MoE
 def topk_gate(probs16, k):
     """aneforge/moe.py:21-37: k rounds of row max with the LOWEST index among exact ties;
@@ -401,7 +417,7 @@ def decode_layer(h16, w, cfg, K, V, pos, cos_row, sin_row, exact=False, trace=No
     hn = rms_norm(h1, w["mlp_norm"], eps, exact)
     g = linear(hn, w["wgate"], None, exact)
     u = linear(hn, w["wup"], None, exact)
-    act = r16(silu(g) * u, exact)
+    act = r16(glu_act(cfg)(g) * u, exact)
     out = r16(h1 + linear(act, w["wdown"], None, exact), exact)
     if trace is not None:
         trace.append(out.copy())
@@ -443,7 +459,7 @@ def decode_rows(h16, w, cfg, K, V, pos0, cos, sin, exact=False):
     hn = rms_norm(h1, w["mlp_norm"], eps, exact)
     g = linear(hn, w["wgate"], None, exact)
     u = linear(hn, w["wup"], None, exact)
-    act = r16(silu(g) * u, exact)
+    act = r16(glu_act(cfg)(g) * u, exact)
     return r16(h1 + linear(act, w["wdown"], None, exact), exact)
 
 

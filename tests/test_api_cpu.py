@@ -144,17 +144,59 @@ def test_rope_tables_equal_oracle_bitwise():
         assert np.array_equal(a[1].view(np.uint16), b[1].view(np.uint16))
 
 
-@pytest.mark.parametrize("model_type,extra", [("gemma", {}), ("gemma2", {}), ("gemma3_text", {}),
+@pytest.mark.parametrize("model_type,extra", [("gemma2", {}), ("gemma3_text", {}),
                                               ("llama", {"final_logit_softcapping": 30.0})])
 def test_dense_loader_rejects_what_it_would_mis_load(model_type, extra):
-    # aneforge/llm.py:776-788: the dense loader refuses configs whose semantics it would drop; Gemma's
-    # sqrt(dim) embedding scale, (1 + w) norms and GeGLU are not on this device path, so it is refused
+    # aneforge/llm.py:776-788: the dense loader refuses configs whose semantics it would drop
     from types import SimpleNamespace
     c = SimpleNamespace(model_type=model_type, **extra)
     with pytest.raises(ValueError, match=repr(model_type)):
         llm._assert_dense_compatible(c)
+    with pytest.raises(ValueError, match=repr(model_type)):
+        llm.adapter_for(c)
     llm._assert_dense_compatible(SimpleNamespace(model_type="llama"))
     llm._assert_dense_compatible(SimpleNamespace(model_type="qwen2"))
+
+
+def test_adapter_registry_routes_gemma_mistral_and_refuses_gpt2():
+    # aneforge/llm.py:766-773: GPT-2 and Gemma have adapters of their own ahead of the dense fallback;
+    # GPT-2 is refused by name here (LayerNorm, learned positions and a GELU MLP are not on this path)
+    from types import SimpleNamespace
+    from transformers import GPT2Config
+    with pytest.raises(ValueError, match="'gpt2'"):
+        llm.adapter_for(GPT2Config(n_layer=1, n_embd=32, n_head=2, vocab_size=64))(GPT2Config(), {})
+    assert llm.adapter_for(SimpleNamespace(model_type="gemma")) is llm._gemma_adapter
+    assert llm.adapter_for(SimpleNamespace(model_type="mistral")) is llm._mistral_adapter
+    assert llm.adapter_for(SimpleNamespace(model_type="llama")) is llm._dense_adapter
+
+
+def test_gemma_adapter_bakes_embed_scale_and_unit_offset_norms():
+    # aneforge/llm.py:685-700 against HF's GemmaForCausalLM pieces: the scaled embedding rows are what
+    # GemmaModel feeds layer 0, (1 + w) is GemmaRMSNorm's gain, the tied head keeps the raw table
+    import torch
+    from transformers import GemmaConfig, GemmaForCausalLM
+    hf_cfg = GemmaConfig(hidden_size=64, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=1,
+                         head_dim=16, intermediate_size=128, vocab_size=64, rms_norm_eps=1e-6,
+                         max_position_embeddings=64, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    m = GemmaForCausalLM(hf_cfg).eval()
+    with torch.no_grad():
+        for p in m.parameters():
+            if p.dim() == 1:
+                p.uniform_(-0.5, 0.5)                      # norms start at zero in HF: make (1 + w) visible
+    sd = {k: v.detach().float().numpy() for k, v in m.state_dict().items()}
+    cfg, w = llm._gemma_adapter(m.config, sd)
+    assert [ls.mlp for ls in cfg.layers] == ["geglu", "geglu"] and cfg.dh == 16 and cfg.n_kv_heads == 1
+    ids = torch.tensor([[3, 9, 27]])
+    with torch.no_grad():
+        x = m.model.embed_tokens(ids)                      # GemmaScaledWordEmbedding: table row * sqrt(dim)
+        nrm = m.model.layers[0].input_layernorm(x)
+    assert float(m.model.embed_tokens.embed_scale) == np.float32(np.sqrt(64))
+    assert np.allclose(w["embed"][[3, 9, 27]], x[0].numpy(), rtol=1e-6, atol=1e-7)
+    xn = x[0].numpy().astype(np.float64)
+    mine = xn / np.sqrt((xn ** 2).mean(-1, keepdims=True) + cfg.norm_eps) * w["layers"][0]["attn_norm"]
+    assert np.allclose(mine, nrm[0].numpy(), rtol=1e-5, atol=1e-6)
+    assert np.array_equal(w["lm_head"], sd["model.embed_tokens.weight"])
 
 
 def test_sample_greedy_and_topk():

@@ -8,7 +8,7 @@ import warnings
 import numpy as np
 import pytest
 
-from _util import check_f16, check_hidden, cosine, say
+from _util import check_f16, check_hidden, cosine, dev, host, say
 from oracle import ref
 
 pytestmark = pytest.mark.gpu
@@ -28,6 +28,78 @@ def test_compile_int8_linear_cfg0():
     check_f16(got, want, what="compile int8")
     assert got.dtype == np.float32 and m.n_ops == 1
     m.release()
+
+
+def test_compile_many_row_linear_is_one_contraction():
+    """af.compile(af.input((2048, 4096)).linear(W), compress="int8"): the reference emits one matmul for
+    any M (aneforge/_compile.py:375-385); here the 2048 rows run as one MFMA GEMM that streams the weight
+    once per 128-row tile, checked against the oracle and timed against the same rows as 8-row GEMV
+    launches (each re-streaming the whole weight), both as captured graphs."""
+    import time
+    from aneforge_amd import _kernels as K
+    say("af.compile int8 linear [2048 x 4096] x [4096 x 4096]: one contraction")
+    rng = np.random.default_rng(5)
+    M, N, Kd = 2048, 4096, 4096
+    W = rng.standard_normal((N, Kd)).astype(np.float32) * 0.02
+    x = rng.standard_normal((M, Kd)).astype(np.float16)
+    m = af.compile(af.input((M, Kd)).linear(W), compress="int8")
+    got = m(x)
+    q, s = ref.quantize_per_row(W)
+    rows = rng.choice(M, 96, replace=False)                       # oracle rows (float64 on the host)
+    check_f16(got[rows], ref.linear(x[rows], ref.dequant_w8(q, s)), what="compile int8 M=2048")
+
+    def best(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        out = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            out.append(time.perf_counter() - t0)
+        return min(out)
+    t_one = best(m.execute)
+    wq, ws_ = dev(q), dev(s)
+    xd = m.input_view().reshape(M, Kd)
+    yd = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for r0 in range(0, M, 8):
+            K.linear("int8", wq, ws_, xd[r0:r0 + 8], y=yd[r0:r0 + 8])
+    t_rows = best(g.replay)
+    say(f"one contraction {t_one * 1e3:.3f} ms, 8-row launches {t_rows * 1e3:.3f} ms ({t_rows / t_one:.1f}x)")
+    check_f16(host(yd)[rows], got[rows], what="8-row form")
+    assert t_rows >= 10 * t_one
+    m.release()
+
+
+@pytest.mark.parametrize("compress", [None, "q4_0", "blockwise", "int4", "int8"])
+@pytest.mark.parametrize("M", [5, 40])
+def test_compile_multi_row_linear_formats(compress, M):
+    """Up to 16 rows one afx_linear launch (skinny MFMA), more rows the GEMM (packed int8 / fp16, or
+    the fp16 expansion of the other encodings), each with a bias, against the oracle."""
+    say(f"af.compile multi-row linear compress={compress} M={M}")
+    rng = np.random.default_rng(6)
+    W = rng.standard_normal((256, 512)).astype(np.float32) * 0.05
+    b = rng.standard_normal(256).astype(np.float32)
+    x = rng.standard_normal((M, 512)).astype(np.float16)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        got = af.compile(af.input((M, 512)).linear(W, b), compress=compress, compress_atol=0.5)(x)
+    if compress is None:
+        Wf = W.astype(np.float16).astype(np.float32)
+    elif compress == "q4_0":
+        Wf = ref.dequant_q4_0_f16(ref.quantize_q4_0(W), 256, 512)
+    elif compress == "blockwise":
+        q, s, bs = ref.quantize_blockwise(W, 32)
+        Wf = (q.reshape(256, 16, 32) * s.astype(np.float32)[:, :, None]).reshape(256, 512).astype(np.float16).astype(np.float32)
+    elif compress == "int4":
+        from aneforge_amd import _blob
+        packed, cb = _blob.palettize_lut4(W)
+        Wf = ref.dequant_lut4(packed, cb, 512)
+    else:
+        Wf = ref.dequant_w8(*ref.quantize_per_row(W))
+    check_f16(got, ref.linear(x, Wf, b.astype(np.float16)), what=f"{compress} M={M}")
 
 
 @pytest.mark.parametrize("compress", [None, "q4_0", "blockwise", "int4", "sparse", "auto"])
@@ -102,6 +174,28 @@ def test_sdpa(H, Hkv, Sq, Skv, D, mode):
     else:
         want = ref.attention(q, k, v, mask=None if mask is None else mask[0, 0])
     check_f16(got, want, what=f"sdpa {mode}")
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_sdpa_long_query(masked):
+    """The reference's query-tiled case (tests/test_sdpa_causal.py:72-91): H 4, S 1500, D 64, plain and
+    with a [1, 1, S, S] additive mask, here one decode-kernel row per query (the mask row is that
+    query's), against the oracle at the fp16 bar."""
+    H, S, D = 4, 1500, 64
+    say(f"af.sdpa long query H={H} S={S} D={D} masked={masked}")
+    rng = np.random.default_rng(7)
+    q, k, v = (rng.standard_normal((1, H, S, D)).astype(np.float16) for _ in range(3))
+    ins = [af.input((1, H, S, D)) for _ in range(3)]
+    feed = [q, k, v]
+    mask = None
+    if masked:
+        mask = rng.standard_normal((1, 1, S, S)).astype(np.float16)
+        ins.append(af.input((1, 1, S, S)))
+        feed.append(mask)
+    got = af.compile(af.sdpa(*ins[:3], attn_mask=ins[3] if masked else None))(*feed)
+    assert tuple(np.asarray(got).shape) == (1, H, S, D)
+    want = ref.attention(q, k, v, mask=None if mask is None else mask[0, 0])
+    check_f16(got, want, what=f"sdpa S={S} masked={masked}")
 
 
 def test_topk_gate_exact_ties_select_exactly_k():

@@ -121,6 +121,34 @@ def test_generate_streams_and_stops_on_eos():
     assert len(m.generate([3, 4], max_new_tokens=50, max_len=6)) == 4      # cache-full stop (pos >= M-1)
 
 
+@pytest.mark.parametrize("mode", ["greedy", "sampled", "host_head", "stepwise_prefill"])
+def test_generate_on_stage_reports_the_reference_stages(mode):
+    # aneforge/llm.py:568-628: per token `embedding` and `layers` (the halves of `step`), `step`,
+    # `lm_head`, `sample`; a token-by-token prefill reports embedding / layers per prompt token.
+    # The staged loop gives the same tokens as the unstaged one.
+    from aneforge_amd.llm import LlamaConfig, LlamaPrefill
+    say(f"generate(on_stage=...) {mode}")
+    cfg = LlamaConfig(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, ffn_dim=512, vocab=128)
+    m = LlamaPrefill(cfg, _random_weights(cfg, seed=5), compress="int8")
+    prompt, n = [4, 9, 21, 3], 6
+    kw = {"temperature": 0.9, "top_k": 20} if mode == "sampled" else {}
+    if mode == "host_head":
+        kw["ane_lm_head"] = False
+    if mode == "stepwise_prefill":
+        kw["batched_prefill"] = False
+    np.random.seed(5)
+    plain = m.generate(prompt, max_new_tokens=n, **kw)
+    stages = []
+    np.random.seed(5)
+    staged = m.generate(prompt, max_new_tokens=n, on_stage=lambda name, dt: stages.append((name, dt)), **kw)
+    assert staged == plain and len(plain) == n
+    per_token = ["embedding", "layers", "step", "lm_head", "sample"]
+    pre = ["embedding", "layers"] * (len(prompt) - 1) if mode == "stepwise_prefill" else []
+    assert [s for s, _ in stages] == pre + per_token * n
+    assert all(dt >= 0.0 for _, dt in stages)
+    m.release()
+
+
 def test_device_sampling_steps_match_oracle_and_generate_paths():
     # each sampled step: the token the device sampler queued equals the oracle's _sample on the
     # same step's logits and uniform; generate's graph loop and its per-token loop agree
@@ -294,3 +322,74 @@ def test_greedy_near_tie_takes_the_host_fp32_choice_in_both_loops():
     m.lmhead_tie_margin = 3e-3
     assert m.generate(prompt, max_new_tokens=2) == [7, 7]
     m.release()
+
+
+def _hf_tiny_gemma(head_dim=16, hidden=64, heads=4, kv=1, ffn=128, vocab=64):
+    from transformers import GemmaConfig, GemmaForCausalLM
+    hf_cfg = GemmaConfig(hidden_size=hidden, num_hidden_layers=2, num_attention_heads=heads, num_key_value_heads=kv,
+                         head_dim=head_dim, intermediate_size=ffn, vocab_size=vocab, rms_norm_eps=1e-6,
+                         max_position_embeddings=256, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    m = GemmaForCausalLM(hf_cfg).eval()
+    with torch.no_grad():
+        for p in m.parameters():
+            if p.dim() == 1:
+                p.uniform_(-0.5, 0.5)                      # non-zero (1 + w) gains
+            else:
+                p.normal_(0.0, p.shape[1] ** -0.5)        # O(1) gate pre-activations: GeGLU != SwiGLU
+    return m
+
+
+def test_prefill_matches_huggingface_gemma():
+    """The Gemma adapter on the device (aneforge tests/test_llm.py:120-135): the sqrt(dim) embedding,
+    (1 + w) norms and the GeGLU MLP reproduce HF GemmaForCausalLM: cosine > 0.999 and the same argmax;
+    greedy generation equals the oracle's (its GeGLU decoder is pinned to HF Gemma on the CPU)."""
+    from aneforge_amd.llm import LlamaPrefill, _gemma_adapter
+    say("prefill + generate vs Hugging Face Gemma")
+    m = _hf_tiny_gemma()
+    toks = [int(t) for t in np.random.default_rng(0).integers(0, 64, 10)]
+    with torch.no_grad():
+        want = m(torch.tensor(toks)[None]).logits[0, -1].numpy()
+    sd = {k: v.detach().float().numpy() for k, v in m.state_dict().items()}
+    cfg, w = _gemma_adapter(m.config, sd)
+    lp = LlamaPrefill(cfg, w)
+    got = lp.prefill(toks)[0]
+    assert cosine(got, want) > 0.999 and int(np.argmax(got)) == int(np.argmax(want))
+    gen = lp.generate(toks, max_new_tokens=8)
+    oc = dict(_ocfg(cfg), mlp="geglu")
+    ow = _effective(w, None)                            # the fp16 tables and weights the device holds
+    ref_toks, lgs = ref.generate(toks, 8, ow, oc, M=len(toks) + 8)
+    _assert_tokens_match(gen, ref_toks, lgs, "gemma generate")
+    lp.release()
+
+
+@pytest.mark.parametrize("compress", [None, "int8"])
+def test_gemma_batched_prefill_geglu_matches_forced_steps(compress):
+    """Head dim 128, so the batched prefill runs (the GEMM's GeGLU epilogue): the same cache and the
+    same greedy continuation as the token-by-token forced steps."""
+    from aneforge_amd.llm import LlamaPrefill, _gemma_adapter
+    say(f"gemma batched prefill (GeGLU GEMM) compress={compress}")
+    m = _hf_tiny_gemma(head_dim=128, hidden=256, heads=2, kv=1, ffn=512, vocab=128)
+    sd = {k: v.detach().float().numpy() for k, v in m.state_dict().items()}
+    cfg, w = _gemma_adapter(m.config, sd)
+    lp = LlamaPrefill(cfg, w, compress=compress)
+    prompt = [int(t) for t in np.random.default_rng(12).integers(0, 128, 40)]
+    d = lp._decoder(len(prompt) + 8)
+    assert d.prefill_supported()
+    d.prefill(prompt)
+    d.sync()
+    batched = [mx.kc.float().cpu().numpy()[0, :, :len(prompt) - 1] for mx, _ in d.layers]
+    d.reset(prompt)
+    d.run(len(prompt) - 1, 0)
+    d.sync()
+    stepped = [mx.kc.float().cpu().numpy()[0, :, :len(prompt) - 1] for mx, _ in d.layers]
+    for a, b in zip(batched, stepped):
+        check_f16(a, b, what="gemma cache rows: batched prefill vs forced steps")
+    a = lp.generate(prompt, max_new_tokens=6, batched_prefill=True)
+    b = lp.generate(prompt, max_new_tokens=6, batched_prefill=False)
+    oc = dict(_ocfg(cfg), mlp="geglu")
+    ow = _effective(w, compress)
+    want, lgs = ref.generate(prompt, 6, ow, oc, M=len(prompt) + 6)
+    _assert_tokens_match(a, want, lgs, "gemma batched prefill generate")
+    _assert_tokens_match(b, want, lgs, "gemma stepped generate")
+    lp.release()

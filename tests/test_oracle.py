@@ -495,3 +495,79 @@ def test_dequant_q6_k_kat_and_encoder():
         want = np.array([np.float32(np.float32(d) * np.float32(sc[i // 16])) * np.float32(q[i]) for i in range(256)],
                         np.float32)
         np.testing.assert_array_equal(ref.dequant_q6_k(blk)[0], want)
+
+
+def test_cpu_baseline_layer_matches_the_exact_decode_layer():
+    """The timed CPU baseline (ref.cpu_decode_layer_f32, fp32 numpy) computes the same layer as the
+    pinned decode_layer(exact=True): GQA 4:1 at a populated cache position, non-unit norm gains, the
+    new K/V row written in place.  A wrong kv-head mapping, RoPE sign or a skipped residual moves the
+    output far outside the fp32-vs-fp64 tolerance used here."""
+    rng = np.random.default_rng(11)
+    D, H, KV, dh, F, M, pos = 256, 8, 2, 32, 512, 96, 70
+    cfg = {"n_heads": H, "n_kv_heads": KV, "dh": dh, "norm_eps": 1e-5}
+    sd = lambda *s: rng.standard_normal(s) / np.sqrt(s[-1])
+    w = {"wq": sd(H * dh, D), "wk": sd(KV * dh, D), "wv": sd(KV * dh, D), "wo": sd(D, H * dh),
+         "wgate": sd(F, D), "wup": sd(F, D), "wdown": sd(D, F),
+         "attn_norm": rng.uniform(0.5, 1.5, D), "mlp_norm": rng.uniform(0.5, 1.5, D)}
+    cos, sin = ref.rope_tables(M, dh)
+    h = rng.standard_normal((1, D))
+    K0, V0 = rng.standard_normal((KV, M, dh)), rng.standard_normal((KV, M, dh))
+    K64, V64 = K0.copy(), V0.copy()
+    want = ref.decode_layer(h, w, cfg, K64, V64, pos, cos[pos], sin[pos], exact=True)
+    f32 = {k: np.asarray(v, np.float32) for k, v in w.items()}
+    K32, V32 = K0.astype(np.float32), V0.astype(np.float32)
+    got = ref.cpu_decode_layer_f32(h.astype(np.float32), f32, cfg, K32, V32, pos,
+                                   cos[pos].astype(np.float32), sin[pos].astype(np.float32))
+    assert got.dtype == np.float32 and got.shape == (1, D)
+    scale = np.abs(want).max()
+    assert np.abs(got - want).max() <= 1e-4 * scale, np.abs(got - want).max() / scale
+    assert np.abs(K32[:, pos] - K64[:, pos]).max() <= 1e-4 and np.abs(V32[:, pos] - V64[:, pos]).max() <= 1e-4
+    assert np.array_equal(K32[:, :pos], K0[:, :pos].astype(np.float32))     # only row pos is written
+    # a plausible slip fails: the interleaved kv-head mapping (query head j reading kv head j % KV
+    # instead of j // G) is emulated by reordering the q rows and o-proj columns so that head j lands
+    # where the baseline's h // G mapping gives it kv head j % KV
+    perm = [j for r in range(KV) for j in range(H) if j % KV == r]
+    wq, wo = f32["wq"].reshape(H, dh, D), f32["wo"].reshape(D, H, dh)
+    slip = dict(f32, wq=wq[perm].reshape(H * dh, D), wo=wo[:, perm].reshape(D, H * dh))
+    bad = ref.cpu_decode_layer_f32(h.astype(np.float32), slip, cfg, K0.astype(np.float32), V0.astype(np.float32),
+                                   pos, cos[pos].astype(np.float32), sin[pos].astype(np.float32))
+    assert np.abs(bad - want).max() > 1e-2 * scale
+
+
+def test_gelu_tanh_matches_torch():
+    x = np.linspace(-12, 12, 4001)
+    want = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    assert np.abs(ref.gelu_tanh(x) - want).max() < 1e-14
+    assert np.abs(ref.gelu_tanh(x) - ref.silu(x)).max() > 0.1          # the two gates differ
+
+
+def test_decoder_geglu_matches_hf_gemma_logits():
+    # the Gemma adapter's baked weights (sqrt(dim) embedding rows, (1 + w) norms) through the oracle's
+    # decoder with the GeGLU gate reproduce HF GemmaForCausalLM (aneforge tests/test_llm.py:120-135)
+    from transformers import GemmaConfig, GemmaForCausalLM
+    from aneforge_amd import llm
+    hf_cfg = GemmaConfig(hidden_size=64, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=1,
+                         head_dim=16, intermediate_size=128, vocab_size=64, rms_norm_eps=1e-6,
+                         max_position_embeddings=64, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    m = GemmaForCausalLM(hf_cfg).eval().double()
+    with torch.no_grad():
+        for p in m.parameters():
+            if p.dim() == 1:
+                p.uniform_(-0.5, 0.5)                      # non-zero (1 + w) gains
+            else:
+                p.normal_(0.0, p.shape[1] ** -0.5)        # O(1) gate pre-activations
+    prompt = [3, 17, 5, 42, 9, 60]
+    with torch.no_grad():
+        want = m(torch.tensor(prompt)[None]).logits[0].numpy()
+        hf = m.generate(torch.tensor(prompt)[None], max_new_tokens=3, do_sample=False)[0, len(prompt):].tolist()
+    sd = {k: v.detach().numpy() for k, v in m.state_dict().items()}
+    cfg, W = llm._gemma_adapter(m.config, sd)
+    oc = {"n_heads": 4, "n_kv_heads": 1, "dh": 16, "norm_eps": 1e-6, "rope_base": 10000.0, "mlp": "geglu"}
+    toks, lg = ref.generate(prompt, 3, W, oc, M=16, exact=True)
+    # GemmaRMSNorm computes in float32 (x.float(), weight.float()) even in a float64 model
+    assert np.abs(lg[0] - want[-1]).max() <= 2e-4 * np.abs(want[-1]).max()
+    assert toks == hf
+    # the SwiGLU gate on the same weights is far off: the activation is what the test pins
+    _, bad = ref.generate(prompt, 1, W, dict(oc, mlp="swiglu"), M=16, exact=True)
+    assert np.abs(bad[0] - want[-1]).max() > 1e-2 * np.abs(want[-1]).max()

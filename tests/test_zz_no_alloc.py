@@ -24,16 +24,47 @@ def _call(name, q, k, v, o, B, Hq, Hkv, D, ctx, ws=None):
     return o
 
 
-@pytest.mark.parametrize("cases", [[(2, 2048, 2048), (1, 300, 512)], [(16, 512, 512), (3, 77, 100)]])
+def _inputs(B, Hq, Hkv, D, Mmax, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    kc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
+    vc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
+    return q, kc, vc
+
+
+def test_noalloc_first_call_inside_a_graph_capture():
+    """The process's first noalloc call (which resolves the scratch array's device address) made while
+    torch captures a graph: the replays equal the workspace entry point, bit for bit, at a shape whose
+    B * Hkv is not a multiple of 8 (the three-dimensional grids)."""
+    from aneforge_amd import _kernels as K
+    B, Hq, Hkv, D, ctx, Mmax = 3, 16, 2, 128, 700, 768
+    say(f"decode attention noalloc: first call under graph capture, B={B} Hq={Hq} Hkv={Hkv} ctx={ctx}")
+    q, kc, vc = _inputs(B, Hq, Hkv, D, Mmax, 690)
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    o = torch.empty_like(qd)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _call("afx_decode_attn_noalloc", qd, kd, vd, o, B, Hq, Hkv, D, ctx)
+    ws = torch.empty(K.attn_ws_bytes(B, Hq, Hkv, D, Mmax) // 4 + 1, dtype=torch.float32, device="cuda")
+    want_ws = host(_call("afx_decode_attn", qd, kd, vd, torch.empty_like(qd), B, Hq, Hkv, D, ctx, ws=ws))
+    for r in range(3):                                     # eager work and a sync between the replays
+        o.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(o).view(np.uint16), want_ws.view(np.uint16)), f"replay {r} differs"
+    want = ref.attention(q[:, :, None, :], kc[:, :, :ctx], vc[:, :, :ctx])[:, :, 0]
+    check_f16(host(o), want, what="noalloc under capture vs oracle")
+
+
+@pytest.mark.parametrize("cases", [[(2, 32, 8, 2048, 2048), (1, 32, 8, 300, 512)],
+                                   [(16, 32, 8, 512, 512), (3, 32, 8, 77, 100)],
+                                   [(3, 16, 2, 1000, 1024), (1, 8, 1, 64, 64)]])
 def test_noalloc_matches_workspace_entry_point(cases):
     from aneforge_amd import _kernels as K
-    Hq, Hkv, D = 32, 8, 128
-    for i, (B, ctx, Mmax) in enumerate(cases):
-        say(f"decode attention noalloc call {i}: B={B} ctx={ctx} Mmax={Mmax}")
-        rng = np.random.default_rng(700 + i)
-        q = rng.standard_normal((B, Hq, D)).astype(np.float16)
-        kc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
-        vc = rng.standard_normal((B, Hkv, Mmax, D)).astype(np.float16)
+    D = 128
+    for i, (B, Hq, Hkv, ctx, Mmax) in enumerate(cases):
+        say(f"decode attention noalloc call {i}: B={B} Hq={Hq} Hkv={Hkv} ctx={ctx} Mmax={Mmax}")
+        q, kc, vc = _inputs(B, Hq, Hkv, D, Mmax, 700 + i)
         qd, kd, vd = dev(q), dev(kc), dev(vc)
         ws = torch.empty(K.attn_ws_bytes(B, Hq, Hkv, D, Mmax) // 4 + 1, dtype=torch.float32, device="cuda")
         want_ws = host(_call("afx_decode_attn", qd, kd, vd, torch.empty_like(qd), B, Hq, Hkv, D, ctx, ws=ws))

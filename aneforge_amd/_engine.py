@@ -527,7 +527,7 @@ class DecodeEngine:
         tie = fused and self._tie_on
         K.decode_advance(self.logits if with_logits else None, self.tok, self.pos, self.hist, self.step,
                          self.embed if gather else None, self.h, self.forced, self.n_forced,
-                         slots=self.slots if fused else None,
+                         slots=self.slots if fused else None, vocab=self.embed.shape[0],
                          tie_margin=self.tie_margin if tie else None, hn=self.hn if tie else None,
                          head16=self.head.w if tie and self.head32 is None else None,
                          head32=self.head32 if tie else None)

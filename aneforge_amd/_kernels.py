@@ -254,11 +254,13 @@ def sample(logits, params, uniforms, step=None, forced=None, n_forced=None, out=
 
 
 def decode_advance(logits, tok, pos, hist, step, embed_table=None, h=None, forced=None, n_forced=None,
-                   slots=None, tie_margin=None, hn=None, head16=None, head32=None):
+                   slots=None, tie_margin=None, hn=None, head16=None, head32=None, vocab=None):
     """Next token (forced prompt token, or the greedy pick with the lm_head tie rule when tie_margin
-    is given) + bookkeeping + embedding gather (see afx_decode_advance)."""
+    is given) + bookkeeping + embedding gather (see afx_decode_advance).  Token ids are clamped to
+    [0, vocab): the embedding table's rows, else `vocab`, else the logits' width."""
     V = logits.shape[-1] if logits is not None else 0
-    vocab, D = (embed_table.shape if embed_table is not None else (V, 0))
+    D = embed_table.shape[1] if embed_table is not None else 0
+    vocab = embed_table.shape[0] if embed_table is not None else (vocab if vocab is not None else V)
     if tie_margin is not None:
         D = hn.numel()
     _hip.call("afx_decode_advance", P(logits), P(slots), V, P(tie_margin), P(hn), P(head16), P(head32),

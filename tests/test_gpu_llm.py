@@ -383,8 +383,14 @@ def test_gemma_batched_prefill_geglu_matches_forced_steps(compress):
     d.run(len(prompt) - 1, 0)
     d.sync()
     stepped = [mx.kc.float().cpu().numpy()[0, :, :len(prompt) - 1] for mx, _ in d.layers]
-    for a, b in zip(batched, stepped):
-        check_f16(a, b, what="gemma cache rows: batched prefill vs forced steps")
+    for li, (g_, w_) in enumerate(zip(batched, stepped)):
+        if li == 0:         # same fp16 embeddings: the paths differ in accumulation order (standalone norm +
+                            # GEMM vs the GEMV's fused norm), so an fp16 rounding may land one ulp apart
+            check_hidden(g_, w_, what="gemma layer 0 k cache: batched prefill vs forced steps")
+        else:               # inputs already differ by fp16 ulps (the GeGLU GEMM vs GEMV order)
+            assert cosine(g_, w_) >= 0.9999, f"gemma layer {li}: cosine {cosine(g_, w_):.6f}"
+            tol = 2 * float(np.spacing(np.float16(np.abs(w_).max())))
+            assert np.abs(g_ - w_).max() <= tol, f"gemma layer {li}: max err {np.abs(g_ - w_).max():.3e} > {tol:.3e}"
     a = lp.generate(prompt, max_new_tokens=6, batched_prefill=True)
     b = lp.generate(prompt, max_new_tokens=6, batched_prefill=False)
     oc = dict(_ocfg(cfg), mlp="geglu")

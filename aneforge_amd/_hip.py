@@ -84,7 +84,8 @@ SIGNATURES: dict[str, tuple] = {
     "afx_qkv_split_rope": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i, _vp, _vp, _ll, _i, _vp]),
     "afx_prefill_attn": (_i, [_vp, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _vp]),
     "afx_moe_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
-    "afx_moe_route": (_i, [_vp, _i, _vp, _f, _vp, _i, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "afx_moe_route": (_i, [_vp, _i, _vp, _f, _vp, _i, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "afx_moe_route_sync_words": (_i, []),
     "afx_moe_down_combine": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp,
                                   _vp, _vp]),
 }

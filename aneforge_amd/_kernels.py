@@ -416,12 +416,19 @@ def moe_route_supported(h, router, k):
             and h.data_ptr() % 16 == 0 and router.data_ptr() % 16 == 0)
 
 
-def moe_route(h, gamma, eps, router, k, renorm, hn, gate, sel, cnt, lst, logits=None):
-    """RMSNorm + router logits + top-k + bucketing in one launch (afx_moe_route); hn [T, D] out."""
+def moe_route_sync(device="cuda"):
+    """A zeroed sync buffer for moe_route's one-workgroup-per-token form (one per MoE layer state)."""
+    return torch.zeros(_hip.load().afx_moe_route_sync_words(), dtype=torch.int32, device=device)
+
+
+def moe_route(h, gamma, eps, router, k, renorm, hn, gate, sel, cnt, lst, logits=None, sync=None):
+    """RMSNorm + router logits + top-k + bucketing in one launch (afx_moe_route); hn [T, D] out.
+    With `sync` (moe_route_sync()) one workgroup per token, else one workgroup for the batch."""
     T, D = h.shape
     E = router.shape[0]
+    _dev(sync)
     _hip.call("afx_moe_route", P(h), h.stride(0), P(gamma), float(eps), P(router), T, E, D, k, int(bool(renorm)),
-              P(hn), hn.stride(0), P(logits), P(gate), P(sel), P(cnt), P(lst), stream())
+              P(hn), hn.stride(0), P(logits), P(gate), P(sel), P(cnt), P(lst), P(sync), stream())
     return gate, sel, cnt, lst
 
 

@@ -32,7 +32,7 @@ extern "C" {
 
 const char* afx_last_error(void) { return g_err; }
 
-int afx_abi_version(void) { return 1; }
+int afx_abi_version(void) { return 2; }
 
 // Device facts the host planner uses (CU count for grid sizing, LDS and L2 sizes).
 int afx_device_info(int device, int* cu_count, int* lds_bytes, int* l2_bytes, int* gcn_arch) {

@@ -77,6 +77,29 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Reductions over the 16 lanes of each DPP row (xor 1, xor 2, then the half-row and row mirrors,
+// which pair the two halves of an 8 / 16 lane group): every lane of a row gets its row's result.
+// Four dependent VALU operations instead of six LDS-routed shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);     // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);     // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);    // row_half_mirror
+  return v + dpp_f<0x140>(v);   // row_mirror
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  return fmaxf(v, dpp_f<0x140>(v));
+}
+__device__ __forceinline__ float lane0(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+}
+
 // Transposed butterfly: each lane holds v[R] (R row partials); afterwards lane l holds the
 // full 64-lane sum of row (l >> (6 - log2 R)) in v[0].  Costs R-1 + log2(64/R) shuffles
 // instead of R*6.

@@ -24,6 +24,28 @@ namespace afx {
 template <int J>
 __device__ __forceinline__ void topk_token(const float (&lg)[J], int lane, int E, int k, int renorm, float& gate_r,
                                            int& sel_r) {
+  if (J == 1 && E <= 16) {
+    // up to 16 experts, all in lanes 0..15 (DPP row 0): the same steps with row reductions, whose
+    // results lane 0 broadcasts
+    const bool own = lane < E;
+    const float m = lane0(row16_max(own ? lg[0] : -INFINITY));
+    const float ex = own ? expf(lg[0] - m) : 0.0f;
+    const float inv = 1.0f / lane0(row16_sum(ex));
+    float p = own ? (float)(half_t)(ex * inv) : -1.0f;
+    float tot = 0.0f, mine = 0.0f;
+    int mine_e = 0;
+    for (int r = 0; r < k; ++r) {
+      const float wb = lane0(row16_max(p));
+      const float cand = p == wb ? (float)lane : 3.0e38f;
+      const int win = (int)lane0(-row16_max(-cand));   // lowest lane holding the maximum
+      if (lane == win) p = -1.0f;                        // taken
+      if (lane == r) { mine = wb; mine_e = win; }
+      tot += wb;
+    }
+    gate_r = renorm ? mine / tot : mine;
+    sel_r = mine_e;
+    return;
+  }
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < J; ++j) m = fmaxf(m, lg[j]);
@@ -72,6 +94,18 @@ __device__ __forceinline__ void bucket_experts(const int* s_sel, int T, int E, i
     for (int i = 0; i < T * k; ++i)
       if (s_sel[i] == e) list[(size_t)e * T + c++] = i;
     cnt[e] = c;
+  }
+}
+
+// The same buckets from one wavefront for at most 64 selections (lane i holds entry i, -1 for none):
+// per expert one ballot, each entry's place is the count of earlier entries with its expert.
+__device__ __forceinline__ void bucket_experts_wave(int s, int lane, int T, int E, int* __restrict__ cnt,
+                                                    int* __restrict__ list) {
+  const unsigned long long below = (1ull << lane) - 1ull;
+  for (int e = 0; e < E; ++e) {
+    const unsigned long long m = __ballot(s == e);
+    if (s == e) list[(size_t)e * T + __popcll(m & below)] = lane;
+    if (lane == 0) cnt[e] = __popcll(m);
   }
 }
 
@@ -237,6 +271,173 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const half_t* __restric
   }
   __syncthreads();
   bucket_experts(s_sel, T, E, k, cnt, list);
+}
+
+// The same routing with one workgroup per token (grid T, NWR wavefronts), so the loads and the
+// normalisation of the T rows run on T CUs instead of one.  Workgroup t repeats the single-workgroup
+// kernel's arithmetic for its token: wavefront 0 normalises row t (the 256-thread reduction order),
+// the NWR wavefronts compute the router MFMA over their K ranges with row t in B column t (the
+// column it has in the batched product, other columns zero), and wavefront 0 sums the partials in
+// the same order and routes the token; so hn, the logits, gate and sel are bit for bit those of
+// moe_route_kernel.  The bucketing needs every token's choice: each workgroup takes a ticket from
+// the caller's counter sync[0] (agent-scope atomic), publishes its k choices as tagged words
+// sync[1 + t * k + slot] = (tag << 8) | expert (agent-scope stores, one word each, so a word is
+// either old or whole), and the workgroup holding the call's last ticket reads all T * k words,
+// waiting (bounded) until each carries the call's tag, then buckets.  Tickets of one call are
+// base .. base + T - 1 with base a multiple of 16 (the last workgroup pads the counter to the next
+// multiple), so tag = ticket / 16 + 1 names the call (never 0, the words' initial value).
+constexpr int kRouteSyncWords = 1 + 16 * 16;
+constexpr unsigned kRouteSpin = 1u << 20;        // polls per word before giving up (no arrival)
+template <int NWR>
+__global__ __launch_bounds__(NWR * 64) void moe_route_tok_kernel(const half_t* __restrict__ h, int ldh,
+                                                                 const half_t* __restrict__ gamma, float eps,
+                                                                 const half_t* __restrict__ router, int T, int E,
+                                                                 int D, int k, int renorm, half_t* __restrict__ hn,
+                                                                 int ldo, float* __restrict__ logits_out,
+                                                                 float* __restrict__ gate, int* __restrict__ sel,
+                                                                 int* __restrict__ cnt, int* __restrict__ list,
+                                                                 unsigned* __restrict__ sync) {
+  __shared__ __align__(16) half_t hn_l[kRouteRow];
+  __shared__ f4 red[NWR][64];
+  __shared__ float lg_l[16];
+  __shared__ int s_sel[16 * 16];
+  __shared__ unsigned s_ticket;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tok = blockIdx.x;
+  const int nv = D >> 3;
+  constexpr int kCh = kRouteMaxD / 8 / 64;
+  // wavefront 0 requests its row and gamma before its router slice: the norm needs them first
+  u4 xv[kCh], gv[kCh];
+  if (wave == 0) {
+    const u4* xr = (const u4*)(h + (size_t)tok * ldh);
+    const u4* gr = (const u4*)gamma;
+#pragma unroll
+    for (int i = 0; i < kCh; ++i) {
+      const int f = lane + 64 * i < nv ? lane + 64 * i : 0;
+      xv[i] = xr[f];
+      gv[i] = gr[f];
+    }
+  }
+  // router loads of this wavefront's K range (rows past E, whose products are never kept, and steps
+  // past the range read zeros without traffic)
+  const int r = lane & 15, g = lane >> 4;
+  const int nsteps = D >> 5;
+  constexpr int kMaxSteps = NWR >= 16 ? 8 : 16;     // steps per wavefront (D <= 4096 under route_waves)
+  const int s0 = nsteps * wave / NWR, s1 = nsteps * (wave + 1) / NWR;
+  const __amdgpu_buffer_rsrc_t rrs = make_rsrc(router, E * D * 2);
+  u4 av[kMaxSteps];
+#pragma unroll
+  for (int i = 0; i < kMaxSteps; ++i)
+    av[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(
+                                       rrs, s0 + i < s1 && r < E ? (r * D + 32 * (s0 + i) + 8 * g) * 2 : 0x7fff0000,
+                                       0, 0));
+  // RMSNorm of row tok by wavefront 0, in moe_route_kernel's order
+  if (wave == 0) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float part = 0.0f;
+#pragma unroll
+      for (int i = j; i < kCh; i += 4) {
+        float q = dot2(as_h2(xv[i].x), as_h2(xv[i].x), 0.0f);
+        q = dot2(as_h2(xv[i].y), as_h2(xv[i].y), q);
+        q = dot2(as_h2(xv[i].z), as_h2(xv[i].z), q);
+        q = dot2(as_h2(xv[i].w), as_h2(xv[i].w), q);
+        part += lane + 64 * i < nv ? q : 0.0f;
+      }
+      ss += wave_sum(part);
+    }
+    const float rstd = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    u4* yr = (u4*)(hn + (size_t)tok * ldo);
+    auto nrm = [&](uint32_t xw, uint32_t gw) {
+      const h2 xx = as_h2(xw), gg = as_h2(gw);
+      h2 o;
+      o.x = (half_t)(((float)xx.x * rstd) * (float)gg.x);
+      o.y = (half_t)(((float)xx.y * rstd) * (float)gg.y);
+      return as_u32(o);
+    };
+#pragma unroll
+    for (int i = 0; i < kCh; ++i) {
+      if (lane + 64 * i >= nv) break;
+      const u4 o = {nrm(xv[i].x, gv[i].x), nrm(xv[i].y, gv[i].y), nrm(xv[i].z, gv[i].z), nrm(xv[i].w, gv[i].w)};
+      yr[lane + 64 * i] = o;
+      *(u4*)&hn_l[8 * (lane + 64 * i)] = o;
+    }
+  }
+  __syncthreads();
+  // logits of token tok: B column tok holds its row, the other columns zero (every LDS read issued
+  // before the first product; steps past the wavefront's range are skipped, uniformly)
+  u4 bvs[kMaxSteps];
+#pragma unroll
+  for (int i = 0; i < kMaxSteps; ++i) {
+    const int s = s0 + i < s1 ? s0 + i : s0;
+    bvs[i] = r == tok ? *(const u4*)&hn_l[32 * s + 8 * g] : (u4){0u, 0u, 0u, 0u};
+  }
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < kMaxSteps; ++i)
+    if (s0 + i < s1)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, av[i]), __builtin_bit_cast(h8, bvs[i]), acc,
+                                                   0, 0, 0);
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = acc[i];
+#pragma unroll
+    for (int w = 1; w < NWR; ++w) {
+      const f4 q = red[w][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += q[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * g + i;
+      if (r == tok && e < E) {
+        lg_l[e] = v[i];
+        if (logits_out) logits_out[(size_t)tok * E + e] = v[i];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float lg[1] = {lane < E ? lg_l[lane] : -INFINITY};
+    float g_r;
+    int s_r;
+    topk_token<1>(lg, lane, E, k, renorm, g_r, s_r);
+    unsigned ticket = 0;
+    if (lane == 0) ticket = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __builtin_amdgcn_readfirstlane(ticket);
+    const unsigned tag = ((ticket >> 4) + 1u) & 0xffffffu;
+    if (lane < k) {
+      gate[(size_t)tok * k + lane] = g_r;
+      sel[(size_t)tok * k + lane] = s_r;
+      __hip_atomic_store(sync + 1 + tok * k + lane, (tag << 8) | (unsigned)s_r, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) s_ticket = ticket;
+  }
+  __syncthreads();
+  const unsigned ticket = s_ticket;
+  if ((int)(ticket & 15u) != T - 1) return;        // not the call's last workgroup (uniform)
+  // the last workgroup: every token's tagged choices, then the buckets
+  const unsigned tag = ((ticket >> 4) + 1u) & 0xffffffu;
+  for (int i = threadIdx.x; i < T * k; i += NWR * 64) {
+    unsigned w = 0;
+    for (unsigned it = 0; it < kRouteSpin; ++it) {
+      w = __hip_atomic_load(sync + 1 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((w >> 8) == tag) break;
+    }
+    s_sel[i] = (w >> 8) == tag ? (int)(w & 0xffu) : -1;   // -1 (never arrived): routed nowhere
+  }
+  __syncthreads();
+  if (T * k <= 64) {
+    if (wave == 0) bucket_experts_wave(lane < T * k ? s_sel[lane] : -1, lane, T, E, cnt, list);
+  } else {
+    bucket_experts(s_sel, T, E, k, cnt, list);
+  }
+  if (threadIdx.x == 0 && T < 16) __hip_atomic_fetch_add(sync, (unsigned)(16 - T), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct MoeArgs {
@@ -548,7 +749,7 @@ static int route_waves(int D) {
 
 int afx_moe_route(const void* h, int ldh, const void* gamma, float eps, const void* router, int T, int E, int D,
                   int k, int renorm, void* hn, int ldo, float* logits, float* gate, int* sel, int* cnt, int* list,
-                  void* stream) {
+                  unsigned* sync, void* stream) {
   AFX_REQUIRE(h && gamma && router && hn && gate && sel && cnt && list, "afx_moe_route: null pointer");
   AFX_REQUIRE(T >= 1 && T <= 16 && E >= 1 && E <= 16 && k >= 1 && k <= E,
               "afx_moe_route: needs 1 <= T <= 16 and 1 <= k <= E <= 16; got T=%d E=%d k=%d", T, E, k);
@@ -559,6 +760,14 @@ int afx_moe_route(const void* h, int ldh, const void* gamma, float eps, const vo
               "afx_moe_route: rows must be 16-byte aligned (ldh, ldo multiples of 8)");
   const int nw = route_waves(D);
   AFX_REQUIRE((D / 32 + nw - 1) / nw <= 16, "afx_moe_route: D=%d splits into more than 16 steps per wavefront", D);
+  if (sync) {                                    // one workgroup per token
+    AFX_REQUIRE(((uintptr_t)sync & 3) == 0, "afx_moe_route: sync must be 4-byte aligned");
+    auto fn = nw == 4 ? moe_route_tok_kernel<4> : nw == 8 ? moe_route_tok_kernel<8> : moe_route_tok_kernel<16>;
+    hipLaunchKernelGGL(fn, dim3(T), dim3(nw * 64), 0, (hipStream_t)stream, (const half_t*)h, ldh,
+                       (const half_t*)gamma, eps, (const half_t*)router, T, E, D, k, renorm, (half_t*)hn, ldo, logits,
+                       gate, sel, cnt, list, sync);
+    return check_launch("afx_moe_route");
+  }
   auto fn = nw == 4 ? moe_route_kernel<4> : nw == 8 ? moe_route_kernel<8> : moe_route_kernel<16>;
   hipLaunchKernelGGL(fn, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const half_t*)h, ldh, (const half_t*)gamma,
                      eps, (const half_t*)router, T, E, D, k, renorm, (half_t*)hn, ldo, logits, gate, sel, cnt, list);
@@ -599,5 +808,8 @@ int afx_moe_combine(const void* h, const float* y, const float* gate, const void
                      (const half_t*)h, y, gate, (const half_t*)shared, (half_t*)out, T, k, D);
   return check_launch("afx_moe_combine");
 }
+
+// 32-bit words of the afx_moe_route `sync` buffer (zeroed once by the caller).
+int afx_moe_route_sync_words(void) { return kRouteSyncWords; }
 
 }  // extern "C"

@@ -111,6 +111,7 @@ class MoEDecode:
 
     def _make_bufs(self, B):
         import torch
+        from . import _kernels as K
         D, E, k, F = self.D, self.E, self.k, self.F
         dev = "cuda"
         bufs = {
@@ -124,6 +125,8 @@ class MoEDecode:
             "y": torch.empty((B * k, D), dtype=torch.float32, device=dev),
             # K-split partials of the expert down projection (long expert rows)
             "ws": torch.empty(8 * B * k * D, dtype=torch.float32, device=dev),
+            # the router's per-token form: arrival counter + tagged choices (zeroed once)
+            "sync": K.moe_route_sync(dev),
         }
         if self.shared:
             Fs = self.sh_gu.N // 2
@@ -147,7 +150,7 @@ class MoEDecode:
         if K.moe_route_supported(h, self.router.w, self.k):
             # norm + router + top-k in one launch (the same bits as the three below)
             K.moe_route(h, self.norm, self.eps, self.router.w, self.k, self.renorm, b["hn"][:T], b["gate"][:T],
-                        b["sel"][:T], b["cnt"], b["list"])
+                        b["sel"][:T], b["cnt"], b["list"], sync=b["sync"])
         else:
             K.rmsnorm(h, self.norm, self.eps, y=b["hn"][:T])
             K.linear("fp16", self.router.w, None, b["hn"][:T], y=b["logits"][:T], out_f32=True)

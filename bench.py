@@ -316,9 +316,10 @@ def bench_moe(args):
     act = torch.empty((T * k, F), dtype=torch.float16, device="cuda")
     y = torch.empty((T * k, D), dtype=torch.float32, device="cuda")
     ws = torch.empty(8 * T * k * D, dtype=torch.float32, device="cuda")   # K-split partials of the down
+    sync = K.moe_route_sync()                                              # the router's per-token form
 
     def layer():                          # the launches of MoEDecode.run (aneforge_amd/moe.py)
-        K.moe_route(h, gamma, 1e-5, router, k, True, hn, gate, sel, cnt, lst)
+        K.moe_route(h, gamma, 1e-5, router, k, True, hn, gate, sel, cnt, lst, sync=sync)
         K.moe_gateup("q4_0", gu_w, gu_d, hn, k, E, F, cnt, lst, act=act)
         K.moe_down_combine("q4_0", dn_w, dn_d, act, T, k, E, F, D, cnt, lst, y, h, gate, out=hout, ws=ws)
 

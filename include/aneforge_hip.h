@@ -237,10 +237,15 @@ int afx_moe_combine(const void* h, const float* y, const float* gate, const void
  * top-k, renorm and bucketing (_topk_gate, moe.py:21-37, 55-56); bit for bit the outputs of
  * afx_rmsnorm + afx_linear (fp16 router, fp32 logits) + afx_moe_topk from T = 4 up (below 4 rows
  * afx_linear sums on its vector kernels, in another order; these logits are the MFMA ones).  T <= 16, E <= 16,
- * 256 <= D <= 4096 (D % 32 == 0), 16-byte aligned rows; logits (optional) [T][E] fp32. */
+ * 256 <= D <= 4096 (D % 32 == 0), 16-byte aligned rows; logits (optional) [T][E] fp32.
+ * sync (optional): afx_moe_route_sync_words() zeroed 32-bit words owned by the caller; with it the
+ * router runs one workgroup per token (same outputs, bit for bit) and the last one buckets.  Calls
+ * sharing one sync buffer must not overlap; without it, one workgroup does everything. */
 int afx_moe_route(const void* h, int ldh, const void* gamma, float eps, const void* router, int T, int E, int D,
                   int k, int renorm, void* hn, int ldo, float* logits, float* gate, int* sel, int* cnt, int* list,
-                  void* stream);
+                  unsigned* sync, void* stream);
+/* 32-bit words of afx_moe_route's sync buffer. */
+int afx_moe_route_sync_words(void);
 /* afx_moe_down followed by afx_moe_combine (bmm_weight and the gate-weighted sum, moe.py:58-63), with
  * the K-split's finishing sum folded into the combine: out is bit for bit that of the two calls. y
  * [T*k][D] fp32 scratch, ws as for afx_moe_down. */

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(_hip.lib_path())], capture_output=True, text=True).stdout
     exported = set(re.findall(r"\bT (afx_\w+)", out))
     assert set(_declared()) <= exported
-    assert lib.afx_abi_version() == 1
+    assert lib.afx_abi_version() == 2
 
 
 def test_argument_counts_match_header():
@@ -114,7 +114,7 @@ def test_fused_moe_router_rejects_batches_beyond_one_workgroup_without_a_gpu():
     from aneforge_amd import _hip
     with pytest.raises(RuntimeError, match="T <= 16"):
         _hip.call("afx_moe_route", 256, 4096, 256, 1e-5, 256, 17, 8, 4096, 2, 1, 256, 4096, None, 256, 256, 256,
-                  256, None)
+                  256, None, None)
     with pytest.raises(RuntimeError, match="multiple of 32"):
         _hip.call("afx_moe_route", 256, 8192, 256, 1e-5, 256, 4, 8, 8192, 2, 1, 256, 8192, None, 256, 256, 256,
-                  256, None)
+                  256, None, None)

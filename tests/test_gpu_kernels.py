@@ -889,6 +889,38 @@ def test_moe_route_is_norm_router_topk_bit_for_bit(K, T, E, D, k):
     lr, lw = host(lst), host(lst_ref)
     for e in range(E):
         assert np.array_equal(lr[e, :c[e]], lw[e, :c[e]]), f"list of expert {e}"
+    # one workgroup per token (the sync buffer): the same bits, on repeated calls that share the buffer
+    # (a smaller batch in between re-aligns its counter) and as graph replays
+    sync = K.moe_route_sync()
+    outs = [torch.full_like(t, -7) for t in (hn, lg, gate, sel, cnt, lst)]
+
+    def per_token(rows):
+        K.moe_route(hd[:rows], gd, 1e-5, rd, k, True, outs[0][:rows], outs[2][:rows], outs[3][:rows], outs[4],
+                    outs[5], logits=outs[1][:rows], sync=sync)
+
+    def same(what):
+        torch.cuda.synchronize()
+        for name, a, b in zip(("hn", "logits", "gate", "sel", "cnt"), outs[:5], (hn, lg, gate, sel, cnt)):
+            assert np.array_equal(host(a).view(np.uint8), host(b).view(np.uint8)), f"{what}: {name}"
+        lp = host(outs[5])
+        for e in range(E):
+            assert np.array_equal(lp[e, :c[e]], lr[e, :c[e]]), f"{what}: list of expert {e}"
+    per_token(T)
+    same("per-token call 1")
+    per_token(max(1, T - 2))
+    for t_ in outs:
+        t_.fill_(-7)
+    per_token(T)
+    same("per-token call 3 (after a smaller batch)")
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        per_token(T)
+    for rep in range(3):
+        for t_ in outs:
+            t_.fill_(-7)
+        gph.replay()
+        same(f"per-token graph replay {rep}")
+    assert int(host(sync)[0]) % 16 == 0
 
 
 @pytest.mark.parametrize("fmt,F,shared", [("q4_0", 14336, False), ("q4_0", 768, True), ("int8", 11008, True)])

@@ -51,6 +51,43 @@ __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
   return r;
 }
 
+// Epilogue of a 64 x 64 wavefront tile: lane holds rows 4 * fg + i of column fr in every 16 x 16 tile.
+template <int FMT, int EG>
+__device__ __forceinline__ void gemm_store(const GemmArgs& a, const f4 (&acc)[4][4], int m0, int n0, int wm, int wn,
+                                           int fr, int fg) {
+  const int M = a.M, N = a.N;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 64 + j * 16 + fr;
+    const int nc = n < N ? n : N - 1;
+    const float sc = FMT == FMT_I8 ? (float)a.scale[nc] : 1.0f;
+    const float bi = a.bias ? (float)a.bias[nc] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
+        const float v = acc[i][j][r] * sc + bi;
+        if constexpr (EG == EG_SWIGLU) {
+          // gate row n (even) and up row n + 1 sit in lanes l and l ^ 1
+          const float pv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
+          if ((fr & 1) == 0 && m < M && n < N) {
+            const float g = (float)(half_t)v, u = (float)(half_t)pv;
+            ((half_t*)a.y)[(size_t)m * a.ldy + (n >> 1)] = (half_t)(glu_act(a.epi == EPI_GEGLU, g) * u);
+          }
+        } else {
+          if (m < M && n < N) {
+            if (a.epi == EPI_F32) ((float*)a.y)[(size_t)m * a.ldy + n] = v;
+            else if (a.epi == EPI_RESID)
+              ((half_t*)a.y)[(size_t)m * a.ldy + n] = (half_t)((float)a.resid[(size_t)m * a.ldy + n] + (float)(half_t)v);
+            else ((half_t*)a.y)[(size_t)m * a.ldy + n] = (half_t)v;
+          }
+        }
+      }
+    }
+  }
+}
+
 template <int FMT, int EG>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   constexpr int WS = GemmW<FMT>::kStride, WR = GemmW<FMT>::kRow, WC = GemmW<FMT>::kChunks;
@@ -167,37 +204,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     __syncthreads();
   }
 
-  // epilogue: lane holds rows 4 * fg + i of column fr in every 16 x 16 tile
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 64 + j * 16 + fr;
-    const int nc = n < N ? n : N - 1;
-    const float sc = FMT == FMT_I8 ? (float)a.scale[nc] : 1.0f;
-    const float bi = a.bias ? (float)a.bias[nc] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
-        const float v = acc[i][j][r] * sc + bi;
-        if constexpr (EG == EG_SWIGLU) {
-          // gate row n (even) and up row n + 1 sit in lanes l and l ^ 1
-          const float pv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
-          if ((fr & 1) == 0 && m < M && n < N) {
-            const float g = (float)(half_t)v, u = (float)(half_t)pv;
-            ((half_t*)a.y)[(size_t)m * a.ldy + (n >> 1)] = (half_t)(glu_act(a.epi == EPI_GEGLU, g) * u);
-          }
-        } else {
-          if (m < M && n < N) {
-            if (a.epi == EPI_F32) ((float*)a.y)[(size_t)m * a.ldy + n] = v;
-            else if (a.epi == EPI_RESID)
-              ((half_t*)a.y)[(size_t)m * a.ldy + n] = (half_t)((float)a.resid[(size_t)m * a.ldy + n] + (float)(half_t)v);
-            else ((half_t*)a.y)[(size_t)m * a.ldy + n] = (half_t)v;
-          }
-        }
-      }
-    }
-  }
+  gemm_store<FMT, EG>(a, acc, m0, n0, wm, wn, fr, fg);
 }
 
 typedef void (*gemm_fn)(GemmArgs);

@@ -10,8 +10,8 @@
 // workgroup computes a 128 x 128 tile of Y; its four wavefronts own 64 x 64 quarters, each as
 // 4 x 4 MFMA tiles (16 fp32 accumulators per lane).  K advances 64 at a time through two LDS
 // stages: the next stage's global loads are issued before the current stage's MFMAs and land in
-// the other stage afterwards, one barrier per step.  LDS rows are padded (144 bytes for fp16,
-// 72 for int8) so the 16-byte / 8-byte fragment reads of 16 rows hit distinct banks.
+// the other stage afterwards, one barrier per step.  LDS rows are unpadded and XOR-swizzled (below)
+// so the 16-byte / 8-byte fragment reads of 16 rows hit distinct banks.
 // Fragments: A lane l = row l % 16, k 8 * (l / 16) .. + 7 (activations); B lane l = column
 // l % 16 (output feature), same k (weights; int8 codes converted exactly to fp16 in
 // registers, the row scale applied to the fp32 result); D lane l = rows 4 * (l / 16) + i,
@@ -25,12 +25,21 @@ namespace afx {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kGBM = 128, kGBN = 128, kGBK = 64;
-constexpr int kGAStride = kGBK * 2 + 16;            // bytes per staged activation row
+constexpr int kGAStride = kGBK * 2;                 // bytes per staged activation row (unpadded, swizzled)
 
 template <int FMT> struct GemmW;
-template <> struct GemmW<FMT_I8> { static constexpr int kRow = kGBK, kStride = kGBK + 8, kChunks = 2; };
-template <> struct GemmW<FMT_F16> { static constexpr int kRow = kGBK * 2, kStride = kGBK * 2 + 16, kChunks = 4; };
-template <> struct GemmW<FMT_BW> { static constexpr int kRow = kGBK, kStride = kGBK + 8, kChunks = 2; };
+template <> struct GemmW<FMT_I8> { static constexpr int kRow = kGBK, kStride = kGBK, kChunks = 2; };
+template <> struct GemmW<FMT_F16> { static constexpr int kRow = kGBK * 2, kStride = kGBK * 2, kChunks = 4; };
+template <> struct GemmW<FMT_BW> { static constexpr int kRow = kGBK, kStride = kGBK, kChunks = 2; };
+
+// LDS rows are stored unpadded with their 16-byte chunks (128-byte rows: activations, fp16 weights) or
+// 8-byte units (64-byte rows: int8 codes) permuted by an XOR of the row, so that the fragment reads
+// of 8 (16-byte) or 16 (8-byte) consecutive rows at one logical offset, and the staging writes, hit
+// distinct banks.  Logical chunk c of row r sits at chunk c ^ (r & 7); logical unit u of a code row
+// at unit u ^ ((r >> 2) & 7).  (Padding did the same with 144 / 72-byte rows, at 55 KB of LDS per
+// workgroup for int8 against 48 KB here, which leaves room for a third workgroup per CU.)
+__device__ __forceinline__ int swz16(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+__device__ __forceinline__ int swz8(int r, int u) { return r * 64 + ((u ^ ((r >> 2) & 7)) << 3); }
 
 struct GemmArgs {
   const void* w;          // [N][K] codes (int8) or values (fp16)
@@ -113,17 +122,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const int c = tid + 256 * i, r = c >> 3, ch = c & 7;
     const int m = m0 + r < M ? m0 + r : M - 1;     // clamped rows are computed, not stored
     xp[i] = a.x + (size_t)m * a.ldx + ch * 8;
-    aoff[i] = r * kGAStride + ch * 16;
+    aoff[i] = swz16(r, ch);
   }
   const unsigned char* wp[WC];
-  int boff[WC];
+  int boff[WC], boff2[WC];
 #pragma unroll
   for (int i = 0; i < WC; ++i) {
     const int c = tid + 256 * i;
     const int r = kCodes ? c >> 2 : c >> 3, ch = kCodes ? c & 3 : c & 7;
     const int n = n0 + r < N ? n0 + r : N - 1;
     wp[i] = (const unsigned char*)a.w + (size_t)n * (kCodes ? K : 2 * K) + ch * 16;
-    boff[i] = r * WS + ch * 16;
+    boff[i] = kCodes ? swz8(r, 2 * ch) : swz16(r, ch);   // codes: the chunk's two 8-byte units
+    boff2[i] = kCodes ? swz8(r, 2 * ch + 1) : 0;
   }
   const half_t* sp = nullptr;                       // blockwise: thread t < 128 carries row n0 + t's scales
   if constexpr (FMT == FMT_BW) {
@@ -147,9 +157,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     for (int i = 0; i < 4; ++i) *(u4*)(As[s] + aoff[i]) = ra[i];
 #pragma unroll
     for (int i = 0; i < WC; ++i) {
-      if constexpr (kCodes) {                      // 72-byte rows: two 8-byte stores keep alignment
+      if constexpr (kCodes) {                      // the two 8-byte units land apart after the swizzle
         *(u2*)(Bs[s] + boff[i]) = (u2){rb[i].x, rb[i].y};
-        *(u2*)(Bs[s] + boff[i] + 8) = (u2){rb[i].z, rb[i].w};
+        *(u2*)(Bs[s] + boff2[i]) = (u2){rb[i].z, rb[i].w};
       } else {
         *(u4*)(Bs[s] + boff[i]) = rb[i];
       }
@@ -174,19 +184,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
       h8 af[4], bf[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        af[i] = __builtin_bit_cast(h8, *(const u4*)(As[s] + (wm * 64 + i * 16 + fr) * kGAStride + (kk * 32 + 8 * fg) * 2));
+        af[i] = __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(wm * 64 + i * 16 + fr, kk * 4 + fg)));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const unsigned char* bp = Bs[s] + (wn * 64 + j * 16 + fr) * WS;
+        const int br = wn * 64 + j * 16 + fr;
         if constexpr (FMT == FMT_I8) {
-          bf[j] = i8x8_to_h8(*(const u2*)(bp + kk * 32 + 8 * fg));
+          bf[j] = i8x8_to_h8(*(const u2*)(Bs[s] + swz8(br, kk * 4 + fg)));
         } else if constexpr (FMT == FMT_BW) {       // k 32kk .. 32kk + 31 is block kk of the step
-          const h2 sp2 = as_h2(Ss[s][wn * 64 + j * 16 + fr]);
+          const h2 sp2 = as_h2(Ss[s][br]);
           const half_t sc = kk ? sp2.y : sp2.x;
           const h8 s8 = {sc, sc, sc, sc, sc, sc, sc, sc};
-          bf[j] = i8x8_to_h8(*(const u2*)(bp + kk * 32 + 8 * fg)) * s8;   // fp16(q * s)
+          bf[j] = i8x8_to_h8(*(const u2*)(Bs[s] + swz8(br, kk * 4 + fg))) * s8;   // fp16(q * s)
         } else {
-          bf[j] = __builtin_bit_cast(h8, *(const u4*)(bp + (kk * 32 + 8 * fg) * 2));
+          bf[j] = __builtin_bit_cast(h8, *(const u4*)(Bs[s] + swz16(br, kk * 4 + fg)));
         }
       }
       // raised wave priority over the MFMA cluster: a wavefront that has its fragments keeps the matrix

@@ -578,17 +578,19 @@ static int make_shape(Shape5& s, int rank, const int* dim, const long long* sa, 
 // - gather, one workgroup per chunk: every workgroup merges the bins and derives the same window
 //   of bins that holds what the cut needs: for top-k every bin from the one holding the k-th
 //   largest key up, for top-p alone the one bin holding the nucleus edge (the bins above it are
-//   kept whole).  Each chunk compacts its logits in the window, in index order, into the workspace;
+//   kept whole).  Each chunk compacts its logits in the window, in index order, into the workspace
+//   (up to kSmpWin logits);
 // - pick, one workgroup of 256 threads: without a cut the draw needs the chunk sums and one chunk;
-//   with a window of at most kSmpCap logits the selection runs on those in LDS (for top-p alone
-//   with the per-chunk mass above the edge for the draw); a larger window runs the selection over
-//   the whole vocabulary.
+//   with a window the selection runs on its logits (for top-p alone with the per-chunk mass above
+//   the edge for the draw), copied to LDS when at most kSmpCap, else read from the workspace; a
+//   window above kSmpWin runs the selection over the whole vocabulary.
 constexpr int kSampleThreads = 256;
 constexpr int kSampleWaves = kSampleThreads / 64;
 constexpr int kSmpPrepThreads = 256;
 constexpr int kSmpPer = 8;                                    // logits per prep / gather thread
 constexpr int kSmpChunk = kSmpPrepThreads * kSmpPer;          // logits per chunk
 constexpr int kSmpCap = 6144;                                 // window logits the pick kernel holds in LDS
+constexpr int kSmpWin = 1 << 16;                              // window logits gather compacts into the workspace
 constexpr int kSmpMaxChunks = 1024;                           // V <= 2^21
 
 __host__ __device__ inline long long smp_nb(int V) { return ((long long)V + kSmpChunk - 1) / kSmpChunk; }
@@ -601,8 +603,9 @@ struct SmpWin {
 };
 // Workspace: e[V] (fp64); a 64-byte header (the largest key, the vocabulary's mass, the window);
 // per chunk its sum bsum[NB]; per chunk and bin the mass smass[NB][256] and count scnt[NB][256] of
-// that bin and every bin above it (suffix sums from the top); the window's e ce[cap] (fp64); window
-// offsets coff[NB + 1]; the window's keys ckey[cap] and indices cidx[cap]; chunk maxima cmax[NB].
+// that bin and every bin above it (suffix sums from the top); the window's e ce[kSmpWin] (fp64);
+// window offsets coff[NB + 1]; the window's keys ckey[kSmpWin] and indices cidx[kSmpWin]; chunk
+// maxima cmax[NB].
 struct SmpHdr {
   unsigned maxkey;
   int pad;
@@ -612,8 +615,8 @@ struct SmpHdr {
 static_assert(sizeof(SmpHdr) <= 64, "sampling workspace header");
 __host__ __device__ inline long long smp_ws_bytes(int V) {
   const long long nb = smp_nb(V);
-  return smp_stats_off(V) + 64 + nb * 8 + nb * 256 * 8 + (long long)kSmpCap * 8 + nb * 256 * 4 + (nb + 1) * 4 +
-         (long long)kSmpCap * 8 + nb * 4;
+  return smp_stats_off(V) + 64 + nb * 8 + nb * 256 * 8 + (long long)kSmpWin * 8 + nb * 256 * 4 + (nb + 1) * 4 +
+         (long long)kSmpWin * 8 + nb * 4;
 }
 struct SmpWs {
   SmpHdr* hdr;
@@ -630,11 +633,11 @@ __device__ __forceinline__ SmpWs smp_ws(double* ws, int V) {
   w.bsum = (double*)(s + 64);
   w.smass = w.bsum + nb;
   w.ce = w.smass + nb * 256;
-  w.scnt = (unsigned*)(w.ce + kSmpCap);
+  w.scnt = (unsigned*)(w.ce + kSmpWin);
   w.coff = w.scnt + nb * 256;
   w.ckey = w.coff + nb + 1;
-  w.cidx = (int*)(w.ckey + kSmpCap);
-  w.cmax = (unsigned*)(w.cidx + kSmpCap);
+  w.cidx = (int*)(w.ckey + kSmpWin);
+  w.cmax = (unsigned*)(w.cidx + kSmpWin);
   return w;
 }
 
@@ -829,7 +832,9 @@ __device__ __forceinline__ int suffix_walk(const T (&S)[4], T need, T& next) {
 }
 
 // Called by every thread of the workgroup (>= 256 threads); mc / mm: LDS scratch of 256 entries.
-// The merged suffix sums: counts exact, masses added over the chunks in order.
+// The merged suffix sums: counts exact, masses added over the chunks in order; the top-k window
+// needs the counts only.  Every gather workgroup merges for itself: a merge by one workgroup needs
+// a device-scope fence per chunk, which measured slower at every vocabulary size up to 2^21.
 __device__ void smp_window(const SmpWs& w, int nb, int V, double top_p, long long top_k, double Z_all, unsigned* mc,
                            double* mm, SmpWin& out) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -839,7 +844,18 @@ __device__ void smp_window(const SmpWs& w, int nb, int V, double top_p, long lon
     __syncthreads();
     return;
   }
-  if (t < 256) {
+  if (t < 256 && cut_k) {
+    unsigned c = 0;
+    for (int b0 = 0; b0 < nb; b0 += 32) {
+      unsigned cv[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) cv[j] = w.scnt[(size_t)(b0 + j < nb ? b0 + j : nb - 1) * 256 + t];
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        if (b0 + j < nb) c += cv[j];
+    }
+    mc[t] = c;
+  } else if (t < 256) {
     unsigned c = 0;
     double m = 0.0;
     for (int b0 = 0; b0 < nb; b0 += 16) {
@@ -879,7 +895,7 @@ __device__ void smp_window(const SmpWs& w, int nb, int V, double top_p, long lon
 }
 
 __device__ __forceinline__ bool smp_use_window(const SmpWin& win, int nb) {
-  return win.mode != 0 && win.ncand >= 1 && win.ncand <= kSmpCap && nb <= kSmpMaxChunks;
+  return win.mode != 0 && win.ncand >= 1 && win.ncand <= kSmpWin && nb <= kSmpMaxChunks;
 }
 
 __global__ __launch_bounds__(kSmpPrepThreads) void sample_gather_kernel(const float* __restrict__ logits, int V,
@@ -942,7 +958,7 @@ __global__ __launch_bounds__(kSmpPrepThreads) void sample_gather_kernel(const fl
 #pragma unroll
   for (int j = 0; j < kSmpPer; ++j) {
     const int bin = smp_bin(x[j], maxv, sb);
-    if (c0 + j >= V || bin < lo || bin > hi || pos >= kSmpCap) continue;
+    if (c0 + j >= V || bin < lo || bin > hi || pos >= kSmpWin) continue;
     w.ckey[pos] = logit_key(x[j]);
     w.cidx[pos] = c0 + j;
     w.ce[pos] = w.e[c0 + j];
@@ -1380,6 +1396,7 @@ __device__ int smp_select_draw(const Acc& A, int V, double temp, double lgmax, d
 __device__ void smp_common_prefix(const SmpCand& A, SampleSmem& sm, unsigned& prefix, unsigned& mask, int& top) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   unsigned mn = 0xffffffffu, mx = 0u;
+#pragma unroll 8
   for (int i = t; i < A.n; i += kSampleThreads) {
     mn = min(mn, A.k[i]);
     mx = max(mx, A.k[i]);
@@ -1401,6 +1418,91 @@ __device__ void smp_common_prefix(const SmpCand& A, SampleSmem& sm, unsigned& pr
   mask = nbytes == 0 ? 0u : nbytes == 4 ? 0xffffffffu : ~(0xffffffffu >> (8 * nbytes));
   prefix = mx & mask;
   top = 24 - 8 * nbytes;
+}
+
+// The draw over the window's n logits A (in LDS, or in the workspace above the LDS cap), in index
+// order.  A top-k cut (mode 1) runs the whole selection over the window; top-p alone (mode 2) runs
+// the radix select over the edge bin's logits with the mass of the bins above it, then the two-level
+// draw with each chunk's kept mass (its bins above the edge plus its kept window logits).
+__device__ __forceinline__ int smp_pick_window(const SmpCand& A, const float* logits, const SmpWs& w,
+                                               const SmpWin& win, int V, int nb, double temp, double lgmax,
+                                               double top_p, long long top_k, double u, double Z_all,
+                                               SampleSmem& sm) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, n = A.n;
+  unsigned cp, cm;
+  int ctop;
+  smp_common_prefix(A, sm, cp, cm, ctop);
+  if (win.mode == 1) return smp_select_draw(A, V, temp, lgmax, top_p, top_k, u, Z_all, cp, cm, ctop, sm);
+  if (t == 0) {
+    sm.prefix = cp;
+    sm.mask = cm;
+    sm.above = win.above;
+    sm.target = top_p * Z_all;
+  }
+  __syncthreads();
+  if (n <= kSmpWaveSel) {
+    if (wave == 0) radix_select_wave<false>(A, 0u, sm, ctop);
+    __syncthreads();
+  } else {
+    radix_select<false>(A, 0u, sm, ctop);
+  }
+  const unsigned pkey = sm.prefix;
+  const double q = exp((double)key_logit(pkey) / temp - lgmax);
+  const double need = sm.target - sm.above;
+  long long ntie = need > 0.0 ? (long long)ceil(need / q) : 1;
+  if (ntie < 1) ntie = 1;
+  // ties at pkey are window logits; the kept ones are the ntie of highest index
+  const int per = (n + kSampleThreads - 1) / kSampleThreads;
+  const int i0 = min(n, t * per), i1 = min(n, i0 + per);
+  int nt = 0;
+  for (int b = i0; b < i1; b += kSmpBatch) {
+    unsigned k[kSmpBatch];
+#pragma unroll
+    for (int j = 0; j < kSmpBatch; ++j) k[j] = A.k[b + j < i1 ? b + j : i1 - 1];
+#pragma unroll
+    for (int j = 0; j < kSmpBatch; ++j) nt += b + j < i1 && k[j] == pkey;
+  }
+  const int inc = wave_incl_scan(nt);
+  if (lane == 63) sm.wmax[wave] = (unsigned)inc;
+  if (t == 0) sm.tie_cut = -1;
+  __syncthreads();
+  int ex = inc - nt, tot = 0;
+  for (int ww = 0; ww < kSampleWaves; ++ww) {
+    if (ww < wave) ex += (int)sm.wmax[ww];
+    tot += (int)sm.wmax[ww];
+  }
+  const long long skip = (long long)tot - ntie;     // ties below the kept ones
+  if (skip > 0 && ex <= skip && skip < ex + nt) {
+    int r = ex;
+    for (int i = i0; i < i1; ++i)
+      if (A.k[i] == pkey && r++ == skip) { sm.tie_cut = A.idx[i]; break; }
+  }
+  __syncthreads();
+  const int tie_cut = sm.tie_cut;
+  auto kept = [&](int i, unsigned k) { return k > pkey || (k == pkey && i >= tie_cut); };
+  // per-chunk kept mass, the chunk's window logits added in index order
+  for (int c = t; c < nb; c += kSampleThreads) {
+    double m = win.lo < 255 ? w.smass[(size_t)c * 256 + win.lo + 1] : 0.0;
+    const int a = (int)w.coff[c], b = (int)w.coff[c + 1];
+    for (int b0 = a; b0 < b; b0 += kSmpBatch) {
+      unsigned k[kSmpBatch];
+      int ix[kSmpBatch];
+      double e[kSmpBatch];
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j) {
+        const int i = b0 + j < b ? b0 + j : b - 1;
+        k[j] = A.k[i];
+        ix[j] = A.idx[i];
+        e[j] = A.e[i];
+      }
+#pragma unroll
+      for (int j = 0; j < kSmpBatch; ++j)
+        if (b0 + j < b && kept(ix[j], k[j])) m += e[j];
+    }
+    sm.km[c] = m;
+  }
+  __syncthreads();
+  return smp_chunk_draw(logits, w.e, V, nb, u, [&](int c) { return sm.km[c]; }, kept, sm);
 }
 
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
@@ -1445,86 +1547,33 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(
       tok = smp_select_draw(A, V, temp, lgmax, top_p, top_k, u, Z_all, 0u, 0u, 24, sm);
     } else {
       const int n = (int)win.ncand;
-      for (int b0 = 0; b0 < n; b0 += 4 * kSampleThreads) {
-        unsigned kk[4];
-        int ii[4];
-        double ee[4];
+      if (n <= kSmpCap) {                            // the window into LDS
+        for (int b0 = 0; b0 < n; b0 += 4 * kSampleThreads) {
+          unsigned kk[4];
+          int ii[4];
+          double ee[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = b0 + j * kSampleThreads + t < n ? b0 + j * kSampleThreads + t : n - 1;
-          kk[j] = w.ckey[i];
-          ii[j] = w.cidx[i];
-          ee[j] = w.ce[i];
-        }
+          for (int j = 0; j < 4; ++j) {
+            const int i = b0 + j * kSampleThreads + t < n ? b0 + j * kSampleThreads + t : n - 1;
+            kk[j] = w.ckey[i];
+            ii[j] = w.cidx[i];
+            ee[j] = w.ce[i];
+          }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = b0 + j * kSampleThreads + t;
-          if (i >= n) continue;
-          sm.ckey[i] = kk[j];
-          sm.cidx[i] = ii[j];
-          sm.ce[i] = ee[j];
-        }
-      }
-      __syncthreads();
-      SmpCand A{sm.ckey, sm.cidx, sm.ce, n};
-      unsigned cp, cm;
-      int ctop;
-      smp_common_prefix(A, sm, cp, cm, ctop);
-      if (win.mode == 1) {
-        tok = smp_select_draw(A, V, temp, lgmax, top_p, top_k, u, Z_all, cp, cm, ctop, sm);
-      } else {
-        // top-p alone: the radix select over the edge bin's logits, the mass above it from the bins
-        if (t == 0) {
-          sm.prefix = cp;
-          sm.mask = cm;
-          sm.above = win.above;
-          sm.target = top_p * Z_all;
+          for (int j = 0; j < 4; ++j) {
+            const int i = b0 + j * kSampleThreads + t;
+            if (i >= n) continue;
+            sm.ckey[i] = kk[j];
+            sm.cidx[i] = ii[j];
+            sm.ce[i] = ee[j];
+          }
         }
         __syncthreads();
-        if (n <= kSmpWaveSel) {
-          if (wave == 0) radix_select_wave<false>(A, 0u, sm, ctop);
-          __syncthreads();
-        } else {
-          radix_select<false>(A, 0u, sm, ctop);
-        }
-        const unsigned pkey = sm.prefix;
-        const double q = exp((double)key_logit(pkey) / temp - lgmax);
-        const double need = sm.target - sm.above;
-        long long ntie = need > 0.0 ? (long long)ceil(need / q) : 1;
-        if (ntie < 1) ntie = 1;
-        // ties at pkey are window logits; the kept ones are the ntie of highest index
-        const int per = (n + kSampleThreads - 1) / kSampleThreads;
-        const int i0 = min(n, t * per), i1 = min(n, i0 + per);
-        int nt = 0;
-        for (int i = i0; i < i1; ++i) nt += sm.ckey[i] == pkey;
-        const int inc = wave_incl_scan(nt);
-        if (lane == 63) sm.wmax[wave] = (unsigned)inc;
-        if (t == 0) sm.tie_cut = -1;
-        __syncthreads();
-        int ex = inc - nt, tot = 0;
-        for (int ww = 0; ww < kSampleWaves; ++ww) {
-          if (ww < wave) ex += (int)sm.wmax[ww];
-          tot += (int)sm.wmax[ww];
-        }
-        const long long skip = (long long)tot - ntie;   // ties below the kept ones
-        if (skip > 0 && ex <= skip && skip < ex + nt) {
-          int r = ex;
-          for (int i = i0; i < i1; ++i)
-            if (sm.ckey[i] == pkey && r++ == skip) { sm.tie_cut = sm.cidx[i]; break; }
-        }
-        __syncthreads();
-        const int tie_cut = sm.tie_cut;
-        auto kept = [&](int i, unsigned k) { return k > pkey || (k == pkey && i >= tie_cut); };
-        // per-chunk kept mass: the bins above the edge (suffix sum), plus the chunk's kept window logits
-        for (int c = t; c < nb; c += kSampleThreads) {
-          double m = win.lo < 255 ? w.smass[(size_t)c * 256 + win.lo + 1] : 0.0;
-          const int a = (int)w.coff[c], b = (int)w.coff[c + 1];
-          for (int i = a; i < b; ++i)
-            if (kept(sm.cidx[i], sm.ckey[i])) m += sm.ce[i];
-          sm.km[c] = m;
-        }
-        __syncthreads();
-        tok = smp_chunk_draw(logits, w.e, V, nb, u, [&](int c) { return sm.km[c]; }, kept, sm);
+        tok = smp_pick_window(SmpCand{sm.ckey, sm.cidx, sm.ce, n}, logits, w, win, V, nb, temp, lgmax, top_p,
+                              top_k, u, Z_all, sm);
+      } else {                                       // a larger window is read where gather left it
+        tok = smp_pick_window(SmpCand{w.ckey, w.cidx, w.ce, n}, logits, w, win, V, nb, temp, lgmax, top_p, top_k,
+                              u, Z_all, sm);
       }
     }
   }

@@ -79,7 +79,7 @@ def test_attention_workspace_sizes_and_their_errors_without_a_gpu():
 def test_sampler_workspace_size_and_its_check_without_a_gpu():
     # fp64 terms for V logits (padded to 256 bytes), a 64-byte header (largest key, total mass,
     # window), then per 2048-logit chunk: its sum (fp64), 256 suffix masses (fp64), 256 suffix counts
-    # (u32), its window offset (u32, one more) and its largest key (u32); and a 6144-logit window
+    # (u32), its window offset (u32, one more) and its largest key (u32); and a 65536-logit window
     # (key, index, fp64 term)
     import pytest
     from aneforge_amd import _hip, _kernels as K
@@ -87,7 +87,7 @@ def test_sampler_workspace_size_and_its_check_without_a_gpu():
     for V in (1, 8, 2048, 2049, 32000, 151936):
         nb = -(-V // 2048)
         assert lib.afx_sample_ws_bytes(V) == (-(-V * 8 // 256) * 256 + 64 + nb * (8 + 256 * 8 + 256 * 4)
-                                              + (nb + 1) * 4 + 6144 * (8 + 4 + 4) + nb * 4)
+                                              + (nb + 1) * 4 + 65536 * (8 + 4 + 4) + nb * 4)
     assert lib.afx_sample_ws_bytes(0) == -1
     assert K.sample_ws_elems(32000) * 8 >= lib.afx_sample_ws_bytes(32000)
     # a workspace of V doubles (the old contract) is now too small: rejected before any launch

@@ -565,12 +565,16 @@ def test_norm_prologue_linears_split_rows_to_fit_lds(K, fmt, M, N, Kd):
 
 
 # ----------------------------------------------------------------------------- sampling
-@pytest.mark.parametrize("V,grid,sd", [(32000, 0.0, 2.5), (1000, 0.25, 2.5), (151936, 0.0, 2.5), (32000, 0.0, 0.05)])
+@pytest.mark.parametrize("V,grid,sd", [(32000, 0.0, 2.5), (1000, 0.25, 2.5), (151936, 0.0, 2.5), (32000, 0.0, 0.05),
+                                       (262144, 0.0, 2.5), (151936, 0.0, 0.01)])
 def test_sample_matches_oracle(K, V, grid, sd):
     # temperature / top-k / top-p / the inverse-CDF draw against the oracle's restatement of the
-    # reference's _sample; grid > 0 rounds the logits so ties are common (top-k and nucleus edges);
-    # sd = 0.05 makes the distribution nearly flat, so a top-p nucleus holds most of the vocabulary
-    # (more than the pick kernel's LDS window: the selection runs over the whole vocabulary)
+    # reference's _sample; grid > 0 rounds the logits so ties are common (top-k and nucleus edges).
+    # The window of candidate logits takes every size: sd = 0.05 makes the distribution nearly flat,
+    # so a top-p nucleus holds most of the vocabulary (a window above the pick kernel's LDS cap, read
+    # from the workspace); at V = 262144 a top-k of 7000 and T = 2 top-p edges land there too; and
+    # sd = 0.01 at V = 151936 puts every logit in one bin (above the workspace window: the selection
+    # runs over the whole vocabulary)
     say(f"device sampling V={V} ties={grid > 0} sd={sd}")
     rng = np.random.default_rng(V)
     logits = (rng.standard_normal(V) * sd).astype(np.float32)
@@ -580,7 +584,8 @@ def test_sample_matches_oracle(K, V, grid, sd):
     ws = torch.empty(V, dtype=torch.float64, device="cuda")
     us = np.concatenate([[0.0, 0.5, 1.0 - 1e-12], rng.random(21)])
     for T, top_p, top_k in [(0.0, 1.0, 0), (1.0, 1.0, 0), (0.7, 1.0, 0), (0.8, 1.0, 40), (1.0, 0.9, 0),
-                            (0.8, 0.9, 40), (1.3, 0.5, 5), (1.0, 0.999, 0), (0.6, 0.95, 1), (2.0, 0.3, V + 5)]:
+                            (0.8, 0.9, 40), (1.3, 0.5, 5), (1.0, 0.999, 0), (0.6, 0.95, 1), (2.0, 0.3, V + 5),
+                            (2.0, 0.95, 0), (0.9, 1.0, 7000)]:
         params = torch.tensor([T, top_p, float(top_k)], dtype=torch.float64, device="cuda")
         uni = torch.from_numpy(us).cuda()
         for j, u in enumerate(us):

@@ -22,6 +22,7 @@ CFLAGS = [
     # keep hipcc from forming packed-fp32 VALU ops (v_pk_fma_f32 and friends)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
+    "-Wno-pass-failed",   # an occupancy target that LDS, not registers, already limits
 ]
 
 

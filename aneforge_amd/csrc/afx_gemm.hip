@@ -7,8 +7,9 @@
 //
 // Prefill multiplies the same weights by hundreds or thousands of token rows, so unlike the
 // decode GEMV this is a dense contraction that v_mfma_f32_16x16x32_f16 bounds.  A 256-thread
-// workgroup computes a 128 x 128 tile of Y; its four wavefronts own 64 x 64 quarters, each as
-// 4 x 4 MFMA tiles (16 fp32 accumulators per lane).  K advances 64 at a time through two LDS
+// workgroup computes a 128 x 128 tile of Y; its four wavefronts own 64 x 64 quarters (fp16
+// weights) or 128 x 32 column strips (int8 codes), 16 MFMA tiles of 16 x 16 each (16 fp32
+// accumulators per lane; the kernel forms below).  K advances 64 at a time through two LDS
 // stages: the next stage's global loads are issued before the current stage's MFMAs and land in
 // the other stage afterwards, one barrier per step.  LDS rows are unpadded and XOR-swizzled (below)
 // so the 16-byte / 8-byte fragment reads of 16 rows hit distinct banks.
@@ -49,6 +50,7 @@ struct GemmArgs {
   void* y;                // output rows, stride ldy (fp16, or fp32 for EPI_F32)
   const half_t* resid;    // EPI_RESID: [M][ldy] fp16 (may alias y)
   int ldx, ldy, M, N, K, epi, tiles_m, tiles, per_xcd;
+  int x_bytes, w_bytes;   // WL 2: bytes of X and W the buffer loads may read (< 2^31)
 };
 
 __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
@@ -60,22 +62,31 @@ __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
   return r;
 }
 
-// Epilogue of a 64 x 64 wavefront tile: lane holds rows 4 * fg + i of column fr in every 16 x 16 tile.
-template <int FMT, int EG>
-__device__ __forceinline__ void gemm_store(const GemmArgs& a, const f4 (&acc)[4][4], int m0, int n0, int wm, int wn,
+// Kernel forms (WL).  0: 2 x 2 wavefronts of 64 x 64 (4 x 4 tiles of 16 x 16), pointer loads.
+// 2: 1 x 4 wavefronts of 128 x 32 (8 x 2 tiles), so each weight column is read from LDS and
+// converted by one wavefront only (half the int8 conversion work of form 0, more activation
+// fragment reads); buffer loads with the step's K offset in a scalar register; the K loop unrolled
+// by two so the LDS stage offsets are constants.  Together they cut the int8 loop's VALU from about
+// 115 to 41 instructions per K step and wavefront.  (1: form 2's layout with form 0's loads.)
+template <int WL> struct WaveLayout { static constexpr int MT = WL ? 8 : 4, NT = WL ? 2 : 4; };
+template <int V> struct Stage { static constexpr int value = V; };
+
+// Epilogue of a wavefront tile: lane holds rows 4 * fg + i of column fr in every 16 x 16 tile.
+template <int FMT, int EG, int MT, int NT>
+__device__ __forceinline__ void gemm_store(const GemmArgs& a, const f4 (&acc)[MT][NT], int m0, int n0, int wm, int wn,
                                            int fr, int fg) {
   const int M = a.M, N = a.N;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 64 + j * 16 + fr;
+  for (int j = 0; j < NT; ++j) {
+    const int n = n0 + wn * NT * 16 + j * 16 + fr;
     const int nc = n < N ? n : N - 1;
     const float sc = FMT == FMT_I8 ? (float)a.scale[nc] : 1.0f;
     const float bi = a.bias ? (float)a.bias[nc] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MT; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * fg + r;
+        const int m = m0 + wm * MT * 16 + i * 16 + 4 * fg + r;
         const float v = acc[i][j][r] * sc + bi;
         if constexpr (EG == EG_SWIGLU) {
           // gate row n (even) and up row n + 1 sit in lanes l and l ^ 1
@@ -97,8 +108,9 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, const f4 (&acc)[4]
   }
 }
 
-template <int FMT, int EG>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+template <int FMT, int EG, int WL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_kernel(GemmArgs a) {
+  constexpr int MT = WaveLayout<WL>::MT, NT = WaveLayout<WL>::NT;
   constexpr int WS = GemmW<FMT>::kStride, WR = GemmW<FMT>::kRow, WC = GemmW<FMT>::kChunks;
   constexpr bool kCodes = FMT == FMT_I8 || FMT == FMT_BW;   // one byte per weight
   __shared__ __align__(16) unsigned char As[2][kGBM * kGAStride];
@@ -110,7 +122,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   if (logical >= a.tiles) return;                   // whole workgroup: no barrier reached
   const int n0 = (logical / a.tiles_m) * kGBN, m0 = (logical % a.tiles_m) * kGBM;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = WL ? 0 : wave >> 1, wn = WL ? wave : wave & 1;
   const int M = a.M, N = a.N, K = a.K;
   const int nk = K / kGBK;
 
@@ -142,11 +154,30 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   }
   u4 ra[4], rb[WC];
   uint32_t rs = 0;
+  // WL 2: buffer loads over the whole X and W (byte offsets fit 31 bits, checked by the host), the
+  // per-lane offset fixed and the step's K offset a scalar, so a step's loads take no address VALU
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes), wr = make_rsrc(a.w, a.w_bytes);
+  int xo[4], wo[WC];
+  if constexpr (WL == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xo[i] = (int)((const unsigned char*)xp[i] - (const unsigned char*)a.x);
+#pragma unroll
+    for (int i = 0; i < WC; ++i) wo[i] = (int)(wp[i] - (const unsigned char*)a.w);
+  }
   auto load = [&](int kt) {
+    if constexpr (WL == 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ra[i] = *(const u4*)(xp[i] + (size_t)kt * kGBK);
+      for (int i = 0; i < 4; ++i)
+        ra[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], kt * (kGBK * 2), 0));
 #pragma unroll
-    for (int i = 0; i < WC; ++i) rb[i] = __builtin_nontemporal_load((const u4*)(wp[i] + (size_t)kt * WR));
+      for (int i = 0; i < WC; ++i)
+        rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[i], kt * WR, 2));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ra[i] = *(const u4*)(xp[i] + (size_t)kt * kGBK);
+#pragma unroll
+      for (int i = 0; i < WC; ++i) rb[i] = __builtin_nontemporal_load((const u4*)(wp[i] + (size_t)kt * WR));
+    }
     if constexpr (FMT == FMT_BW) rs = *(const uint32_t*)(sp + 2 * kt);
   };
   auto stage = [&](int s) {
@@ -166,28 +197,29 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     }
   };
 
-  f4 acc[4][4];
+  f4 acc[MT][NT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NT; ++j) acc[i][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
   load(0);
   stage(0);
   __syncthreads();
   const int fr = lane & 15, fg = lane >> 4;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int s = kt & 1;
+  // one K step on stage s: the next stage's loads, this stage's MFMAs, then the next stage staged
+  auto kstep = [&](int kt, auto st) {
+    const int s = decltype(st)::value >= 0 ? decltype(st)::value : (kt & 1);
     if (kt + 1 < nk) load(kt + 1);                 // next stage streams during this stage's MFMAs
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      h8 af[4], bf[4];
+      h8 af[MT], bf[NT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(wm * 64 + i * 16 + fr, kk * 4 + fg)));
+      for (int i = 0; i < MT; ++i)
+        af[i] = __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(wm * MT * 16 + i * 16 + fr, kk * 4 + fg)));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int br = wn * 64 + j * 16 + fr;
+      for (int j = 0; j < NT; ++j) {
+        const int br = wn * NT * 16 + j * 16 + fr;
         if constexpr (FMT == FMT_I8) {
           bf[j] = i8x8_to_h8(*(const u2*)(Bs[s] + swz8(br, kk * 4 + fg)));
         } else if constexpr (FMT == FMT_BW) {       // k 32kk .. 32kk + 31 is block kk of the step
@@ -205,16 +237,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
       // each, measured 0.5% slower with it and keeps the default priority
       if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
       if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
     }
     if (kt + 1 < nk) stage(s ^ 1);                 // the other stage was last read before the previous barrier
     __syncthreads();
+  };
+  if constexpr (WL == 2) {                         // unrolled by two: the stage offsets are constants
+    for (int kt = 0; kt < nk; kt += 2) {
+      kstep(kt, Stage<0>{});
+      if (kt + 1 < nk) kstep(kt + 1, Stage<1>{});
+    }
+  } else {
+    for (int kt = 0; kt < nk; ++kt) kstep(kt, Stage<-1>{});
   }
 
-  gemm_store<FMT, EG>(a, acc, m0, n0, wm, wn, fr, fg);
+  gemm_store<FMT, EG, MT, NT>(a, acc, m0, n0, wm, wn, fr, fg);
 }
 
 typedef void (*gemm_fn)(GemmArgs);
@@ -249,10 +289,29 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   a.tiles_m = (M + kGBM - 1) / kGBM;
   a.tiles = a.tiles_m * ((N + kGBN - 1) / kGBN);
   a.per_xcd = (a.tiles + 7) / 8;
+  // kernel form: 2 for int8 codes, 0 for fp16 weights (the faster of the two on each format at the
+  // 7B prefill shapes; outputs are bit-identical); AFX_GEMM_WL=0|2 overrides.  Form 2 addresses X and
+  // W with 31-bit buffer offsets, so larger operands take form 0.
+  static int wl_env = -2;
+  if (wl_env == -2) {
+    const char* e = getenv("AFX_GEMM_WL");
+    wl_env = e ? atoi(e) : -1;
+  }
+  const long long xb = ((long long)(M - 1) * ldx + K) * 2;
+  const long long wb = (long long)N * K * (fmt == FMT_F16 ? 2 : 1);
+  const bool form2 = (wl_env == 2 || (wl_env != 0 && fmt != FMT_F16)) && xb < (1ll << 31) && wb < (1ll << 31);
   gemm_fn fn;
-  if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU> : gemm_kernel<FMT_I8, EG_PLAIN>;
-  else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU> : gemm_kernel<FMT_BW, EG_PLAIN>;
-  else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU> : gemm_kernel<FMT_F16, EG_PLAIN>;
+  if (form2) {
+    a.x_bytes = (int)xb;
+    a.w_bytes = (int)wb;
+    if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU, 2> : gemm_kernel<FMT_I8, EG_PLAIN, 2>;
+    else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU, 2> : gemm_kernel<FMT_BW, EG_PLAIN, 2>;
+    else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU, 2> : gemm_kernel<FMT_F16, EG_PLAIN, 2>;
+  } else {
+    if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU, 0> : gemm_kernel<FMT_I8, EG_PLAIN, 0>;
+    else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU, 0> : gemm_kernel<FMT_BW, EG_PLAIN, 0>;
+    else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU, 0> : gemm_kernel<FMT_F16, EG_PLAIN, 0>;
+  }
   hipLaunchKernelGGL(fn, dim3(8 * a.per_xcd), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("afx_gemm");
 }

@@ -64,13 +64,18 @@ int afx_graph_begin(void* stream) {
 }
 
 int afx_graph_end(void* stream, void** exec_out) {
+  AFX_REQUIRE(exec_out, "afx_graph_end: null exec_out");
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
   if (e != hipSuccess) return afx::set_error("hipStreamEndCapture: %s", hipGetErrorString(e));
   hipGraphExec_t ex = nullptr;
   e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
+  const hipError_t d = hipGraphDestroy(g);       // the executable graph keeps what it needs
   if (e != hipSuccess) return afx::set_error("hipGraphInstantiate: %s", hipGetErrorString(e));
+  if (d != hipSuccess) {
+    (void)hipGraphExecDestroy(ex);
+    return afx::set_error("hipGraphDestroy: %s", hipGetErrorString(d));
+  }
   *exec_out = (void*)ex;
   return 0;
 }
@@ -90,6 +95,7 @@ int afx_graph_destroy(void* exec) {
 
 // ---- events on the caller's stream (timing the stream the kernels actually run on) ----
 int afx_event_create(void** ev) {
+  AFX_REQUIRE(ev, "afx_event_create: null output pointer");
   hipEvent_t e;
   hipError_t r = hipEventCreate(&e);
   if (r != hipSuccess) return afx::set_error("hipEventCreate: %s", hipGetErrorString(r));
@@ -102,6 +108,7 @@ int afx_event_record(void* ev, void* stream) {
   return 0;
 }
 int afx_event_elapsed_ms(void* start, void* stop, float* ms) {
+  AFX_REQUIRE(start && stop && ms, "afx_event_elapsed_ms: null argument");
   hipError_t r = hipEventSynchronize((hipEvent_t)stop);
   if (r != hipSuccess) return afx::set_error("hipEventSynchronize: %s", hipGetErrorString(r));
   r = hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop);
@@ -109,7 +116,9 @@ int afx_event_elapsed_ms(void* start, void* stop, float* ms) {
   return 0;
 }
 int afx_event_destroy(void* ev) {
-  if (ev) hipEventDestroy((hipEvent_t)ev);
+  if (!ev) return 0;
+  const hipError_t r = hipEventDestroy((hipEvent_t)ev);
+  if (r != hipSuccess) return afx::set_error("hipEventDestroy: %s", hipGetErrorString(r));
   return 0;
 }
 

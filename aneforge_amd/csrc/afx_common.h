@@ -183,7 +183,7 @@ __device__ __forceinline__ float4 top2_merge(float4 a, float4 b) {
 // ---- host-side error plumbing shared by all entry points (defined in afx_capi.hip) ----
 extern "C" const char* afx_last_error(void);
 namespace afx {
-int set_error(const char* fmt, ...);
+int set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));   // the compiler checks every message
 int check_launch(const char* what);
 }  // namespace afx
 

@@ -1642,7 +1642,7 @@ int afx_decode_advance(const float* logits, const float* slots, int V, const flo
                        void* stream) {
   AFX_REQUIRE(tok && pos && step && (logits || slots || forced), "afx_decode_advance: bad arguments");
   AFX_REQUIRE(!(logits || slots) || V >= 1, "afx_decode_advance: V must be positive");
-  AFX_REQUIRE(!embed || (h && D % 8 == 0 && vocab >= 1), "afx_decode_advance: embed gather needs h, D % 8 == 0");
+  AFX_REQUIRE(!embed || (h && D % 8 == 0 && vocab >= 1), "afx_decode_advance: embed gather needs h, D %% 8 == 0");
   AFX_REQUIRE(logits || slots || n_forced, "afx_decode_advance: a forced-only step needs n_forced");
   AFX_REQUIRE(!slots || ((uintptr_t)slots & 15) == 0, "afx_decode_advance: slots must be 16-byte aligned");
   AFX_REQUIRE(!tie_margin || (logits && hn && (head16 || head32) && D >= 1),
@@ -1657,7 +1657,7 @@ int afx_decode_advance(const float* logits, const float* slots, int V, const flo
 }
 
 // Workspace bytes afx_sample needs for V logits.
-long long afx_sample_ws_bytes(int V) { return V >= 1 ? smp_ws_bytes(V) : -1; }
+long long afx_sample_ws_bytes(int V) { return V >= 1 && smp_nb(V) <= kSmpMaxChunks ? smp_ws_bytes(V) : -1; }
 
 // params: device {temperature, top_p, top_k} as doubles; u = uniforms[*step] (uniforms[0] without
 // step).  The token goes to forced[*step] (and n_forced = *step + 1, so afx_decode_advance takes

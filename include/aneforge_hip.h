@@ -172,7 +172,8 @@ int afx_head_norm_rope(void* x, long long seq_stride, long long head_stride, int
  * whose cumulative kept probability exceeds u.  params: device doubles {temperature, top_p, top_k};
  * u = uniforms[*step] (uniforms[0] when step is NULL).  The token goes to forced[*step] with
  * n_forced = *step + 1 (afx_decode_advance then takes it) and/or out[0].  ws: afx_sample_ws_bytes(V)
- * bytes, 8-byte aligned (the fp64 terms exp(x/T - max/T) and per-chunk sums and key histograms). */
+ * bytes, 8-byte aligned (the fp64 terms exp(x/T - max/T) and per-chunk sums and key histograms);
+ * -1 for V outside [1, 2^21], which afx_sample rejects. */
 long long afx_sample_ws_bytes(int V);
 int afx_sample(const float* logits, int V, const double* params, const double* uniforms, const int* step,
                int* forced, int* n_forced, int* out, double* ws, long long ws_bytes, void* stream);

@@ -27,7 +27,7 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-from . import _blob
+from . import _blob, _cache
 from . import _engine as E
 from . import _kernels as K
 from ._runtime import Program
@@ -74,7 +74,7 @@ def _encode_weight(W, compress, atol, block_size, stats: _Enc, allow_q=True):
             stats.rejected["sparse"] = stats.rejected.get("sparse", 0) + 1
         return E.pack_linear(W, None)
     if compress == "int4":
-        packed, cb = _blob.palettize_lut4(W)
+        packed, cb = _cache.cached("palettize_lut4", _blob.palettize_lut4, W)
         idx = np.empty((W.shape[0], packed.shape[1] * 2), np.uint8)
         idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
         rec = cb.astype(np.float32)[idx[:, :W.shape[1]]]
@@ -83,7 +83,7 @@ def _encode_weight(W, compress, atol, block_size, stats: _Enc, allow_q=True):
         stats.rejected["int4"] = stats.rejected.get("int4", 0) + 1
         return E.pack_linear(W, "int8")
     if compress == "blockwise":
-        q, s, bs = _blob.quantize_blockwise(W, block_size)
+        q, s, bs = _cache.cached("quantize_blockwise", _blob.quantize_blockwise, W, block_size)
         N, Kd = W.shape
         rec = (q.reshape(N, Kd // bs, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(N, Kd)
         if _rel_err(rec, W) <= atol:
@@ -400,7 +400,7 @@ class _Lowering:
         to_rows = lambda a: np.ascontiguousarray(a.reshape(B, Kd, N).transpose(0, 2, 1)).reshape(B * N, Kd)
         mode = self.compress
         if mode == "int4" and (Kd * N) % 2 == 0:
-            packed, cb = _blob.palettize_lut4(flat)
+            packed, cb = _cache.cached("palettize_lut4", _blob.palettize_lut4, flat)
             idx = np.empty((B, Kd * N), np.uint8)
             idx[:, 0::2], idx[:, 1::2] = packed & 15, packed >> 4
             if _rel_err(cb.astype(np.float32)[idx], flat) <= self.atol:
@@ -411,14 +411,14 @@ class _Lowering:
                 return E.pack_encoded("fp16", cb[rows], None)
             self.stats.rejected["int4"] = self.stats.rejected.get("int4", 0) + 1
         if mode == "blockwise":
-            q, s, bs = _blob.quantize_blockwise(flat, self.block_size)
+            q, s, bs = _cache.cached("quantize_blockwise", _blob.quantize_blockwise, flat, self.block_size)
             rec = (q.reshape(B, -1, bs).astype(np.float32) * s.astype(np.float32)[:, :, None]).reshape(B, -1)
             if _rel_err(rec, flat) <= self.atol:
                 return E.pack_encoded("fp16", to_rows(rec.astype(F16)), None)
             self.stats.rejected["blockwise"] = self.stats.rejected.get("blockwise", 0) + 1
             mode = None
         if mode in ("int8", "auto", "int4", "q4_0"):
-            q, s = _blob.quantize_per_row(flat)                      # one scale per batch
+            q, s = _cache.cached("quantize_per_row", _blob.quantize_per_row, flat)   # one scale per batch
             return E.pack_encoded("int8", to_rows(q), np.repeat(s, N))
         return E.pack_encoded("fp16", to_rows(flat.astype(F16)), None)
 

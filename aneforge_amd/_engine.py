@@ -27,7 +27,7 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-from . import _blob, _hip
+from . import _blob, _cache, _hip
 from . import _kernels as K
 
 F16 = np.float16
@@ -174,18 +174,18 @@ def encode(W: np.ndarray, compress: str | None):
     if compress in (None, "fp16", "sparse"):
         return "fp16", W.astype(F16), None
     if compress in ("int8", "auto"):
-        q, s = _blob.quantize_per_row(W)
+        q, s = _cache.cached("quantize_per_row", _blob.quantize_per_row, W)
         return "int8", q, s
     if compress in ("q4_0", "gguf_q4_0"):
         N, Kd = W.shape
         if Kd % 128:
             raise ValueError(f"q4_0 needs in_features % 128 == 0 (got {Kd})")
-        qs, d = _blob.q4_0_to_superblock(_blob.quantize_q4_0(W), N, Kd)
+        qs, d = _blob.q4_0_to_superblock(_cache.cached("quantize_q4_0", _blob.quantize_q4_0, W), N, Kd)
         return "q4_0", qs, d
     if compress == "blockwise":
-        return blockwise_encoding(*_blob.quantize_blockwise(W, 32))
+        return blockwise_encoding(*_cache.cached("quantize_blockwise", _blob.quantize_blockwise, W, 32))
     if compress == "int4":
-        return lut4_encoding(*_blob.palettize_lut4(W), W.shape[1])
+        return lut4_encoding(*_cache.cached("palettize_lut4", _blob.palettize_lut4, W), W.shape[1])
     raise ValueError(f"unknown compress={compress!r}")
 
 
@@ -209,7 +209,7 @@ def per_tensor(W, compress):
     W = np.asarray(W, np.float32)
     if W.shape[1] % 32:
         return W                                    # no lut4 kernel for this width: encoded after fusing
-    packed, cb = _blob.palettize_lut4(W)
+    packed, cb = _cache.cached("palettize_lut4", _blob.palettize_lut4, W)
     fmt, codes, scale = lut4_encoding(packed, cb, W.shape[1])
     return QuantizedWeight(fmt, codes, scale, W.shape)
 

@@ -175,3 +175,75 @@ def test_moe_down_split_k(fmt):
                     ent = t * k + sl
                     assert _bad(y[ent:ent + 1], ref.linear(a[ent:ent + 1], Dn[e], exact=True)) == 0, \
                         f"token {t} expert {e} workspace={w_ is not None}"
+
+
+@pytest.mark.parametrize("seed", [301, 302])
+def test_prefill_gemm_sweep(seed):
+    """The prefill GEMM at random shapes: ragged row and column tiles, odd numbers of 64-deep K steps
+    (the K loop runs two steps per iteration), activations read through a row stride wider than K,
+    every epilogue, int8 / blockwise / fp16 weights, against the oracle's float64 product."""
+    from aneforge_amd import _kernels as K
+    rng = np.random.default_rng(seed)
+    epis = ["f16", "resid", "f32", "swiglu", "geglu"]
+    for trial in range(15):
+        fmt = ["int8", "blockwise", "fp16"][trial % 3]
+        epi = epis[trial % 5]
+        M = int(rng.integers(1, 600))
+        N = int(rng.integers(1, 48)) * 16 * (2 if epi in ("swiglu", "geglu") else 1)
+        Kd = int(rng.integers(1, 24)) * 64
+        pad = int(rng.integers(0, 3)) * 8
+        say(f"sweep {seed}/{trial}: prefill gemm {fmt} {epi} M={M} N={N} K={Kd} ldx={Kd + pad}")
+        w, s, W = _weights(rng, fmt, N, Kd)
+        xbuf = rng.standard_normal((M, Kd + pad)).astype(np.float16)
+        x = xbuf[:, :Kd]
+        xd = dev(xbuf)[:, :Kd]                         # a row stride of K + pad
+        lin = np.asarray(x, np.float64) @ np.asarray(W, np.float64).T
+        wd, sd = dev(w), (dev(s) if s is not None else None)
+        if epi == "resid":
+            r = rng.standard_normal((M, N)).astype(np.float16)
+            y = dev(r)
+            K.gemm(fmt, wd, sd, xd, y=y, residual=y, epi="resid")
+            assert _bad(host(y), ref.r16(r.astype(np.float64) + ref.r16(lin)), hidden=True) == 0, "resid"
+            continue
+        got = host(K.gemm(fmt, wd, sd, xd, epi=epi))
+        if epi in ("swiglu", "geglu"):
+            g, u = ref.r16(lin[:, 0::2]), ref.r16(lin[:, 1::2])
+            act = ref.silu(g) if epi == "swiglu" else ref.gelu_tanh(g)
+            assert _bad(got, ref.r16(act * u)) == 0, epi
+        elif epi == "f32":
+            assert _bad(got, lin) == 0, "f32"
+        else:
+            assert _bad(got, ref.r16(lin)) == 0, "f16"
+
+
+@pytest.mark.parametrize("seed", [401, 402])
+def test_sampling_sweep(seed):
+    """Device sampling against the oracle's restatement of the reference's _sample, token for token, at
+    random vocabularies (1 .. 300000), logit spreads (nearly flat to very sharp), masked (-inf) and
+    rounded (tied) logits, and random temperature / top-k / top-p, so the candidate window takes every
+    size: none, in LDS, in the workspace, and past it (the whole-vocabulary selection)."""
+    from aneforge_amd import _kernels as K
+    rng = np.random.default_rng(seed)
+    for trial in range(24):
+        V = int(np.exp(rng.uniform(0, np.log(300000)))) + 1
+        sd = float(np.exp(rng.uniform(np.log(0.01), np.log(8.0))))
+        logits = (rng.standard_normal(V) * sd).astype(np.float32)
+        if rng.random() < 0.3:
+            logits = (np.round(logits / (sd / 4)) * (sd / 4)).astype(np.float32)
+        if rng.random() < 0.3 and V > 2:
+            logits[rng.random(V) < rng.uniform(0.0, 0.5)] = -np.inf
+            logits[int(rng.integers(0, V))] = 0.0                # at least one finite logit
+        T = 0.0 if rng.random() < 0.1 else float(np.exp(rng.uniform(np.log(0.05), np.log(3.0))))
+        top_p = 1.0 if rng.random() < 0.3 else float(rng.uniform(0.01, 0.999))
+        top_k = 0 if rng.random() < 0.4 else int(np.exp(rng.uniform(0, np.log(V + 6))))
+        us = rng.random(4)
+        say(f"sweep {seed}/{trial}: sample V={V} sd={sd:.3g} T={T:.3g} top_p={top_p:.3g} top_k={top_k}")
+        lg = dev(logits)
+        params = torch.tensor([T, top_p, float(top_k)], dtype=torch.float64, device="cuda")
+        uni = torch.from_numpy(us).cuda()
+        ws = torch.empty(K.sample_ws_elems(V), dtype=torch.float64, device="cuda")
+        for j, u in enumerate(us):
+            step = torch.tensor([j], dtype=torch.int32, device="cuda")
+            got = int(host(K.sample(lg, params, uni, step=step, ws=ws))[0])
+            want = ref.sample(logits, T, top_p, top_k, float(u))
+            assert got == want, f"V={V} T={T} top_p={top_p} top_k={top_k} u={u}: {got} vs {want}"

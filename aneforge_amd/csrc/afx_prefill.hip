@@ -145,35 +145,43 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
         s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[ks], kf, s[j], 0, 0, 0);
       }
     }
-    // online softmax (log2 domain); lane holds rows 4 * fg + i, key j * 16 + fr
+    // online softmax (log2 domain); lane holds rows 4 * fg + i, key j * 16 + fr.  Only a block with a key
+    // past the wavefront's first query position needs the causal mask (wavefront-uniform); the scale
+    // (positive) is applied to the block maximum and inside the exponent's FMA.
+    if (key0 + kPK - 1 > a.pos0 + m0 + wave * 16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j][i] = key0 + j * 16 + fr <= qpos[i] ? s[j][i] : -INFINITY;
+    }
     float alpha[4];
+    bool grew = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float bm = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = key0 + j * 16 + fr;
-        const float x = key <= qpos[i] ? s[j][i] * a.scale_log2 : -INFINITY;
-        s[j][i] = x;
-        bm = fmaxf(bm, x);
-      }
-      bm = row16<true>(bm);
+      for (int j = 0; j < 4; ++j) bm = fmaxf(bm, s[j][i]);
+      bm = row16<true>(bm) * a.scale_log2;
       const float mn = fmaxf(mrow[i], bm);         // finite: every row sees key 0 in block 0
+      grew = grew || mn > mrow[i];
       alpha[i] = __builtin_amdgcn_exp2f(mrow[i] - mn);
       mrow[i] = mn;
       float rs = 0.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p = __builtin_amdgcn_exp2f(s[j][i] - mn);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][i], a.scale_log2, -mn));
         s[j][i] = p;
         rs += p;
       }
       lrow[i] = lrow[i] * alpha[i] + row16<false>(rs);
     }
+    // rescale only when some row's maximum grew (otherwise every alpha is exactly 1)
+    if (__builtin_amdgcn_ballot_w64(grew)) {
 #pragma unroll
-    for (int d = 0; d < 8; ++d)
+      for (int d = 0; d < 8; ++d)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[d][i] *= alpha[i];
+        for (int i = 0; i < 4; ++i) acc[d][i] *= alpha[i];
+    }
     // P (fp16) through the wavefront's LDS tile into the A-operand layout
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -240,6 +248,7 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
                      void* o, int ldo, int M, int pos0, int Hq, int Hkv, int D, float scale, void* stream) {
   AFX_REQUIRE(q && kcache && vcache && o, "afx_prefill_attn: null pointer");
   AFX_REQUIRE(D == kPD, "afx_prefill_attn: head dim %d not supported (128)", D);
+  AFX_REQUIRE(scale > 0.0f, "afx_prefill_attn: scale %g must be positive", (double)scale);
   AFX_REQUIRE(Hkv >= 1 && Hq % Hkv == 0, "afx_prefill_attn: bad heads Hq=%d Hkv=%d", Hq, Hkv);
   AFX_REQUIRE(M >= 1 && pos0 >= 0 && pos0 + M <= Mmax && kv_hs >= (long long)Mmax * D,
               "afx_prefill_attn: positions %d..%d outside the %d-row cache", pos0, pos0 + M - 1, Mmax);

@@ -171,12 +171,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         ra[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], kt * (kGBK * 2), 0));
 #pragma unroll
       for (int i = 0; i < WC; ++i)
-        rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[i], kt * WR, 2));
+        rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[i], kt * WR, 0));
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) ra[i] = *(const u4*)(xp[i] + (size_t)kt * kGBK);
 #pragma unroll
-      for (int i = 0; i < WC; ++i) rb[i] = __builtin_nontemporal_load((const u4*)(wp[i] + (size_t)kt * WR));
+      for (int i = 0; i < WC; ++i) rb[i] = *(const u4*)(wp[i] + (size_t)kt * WR);
     }
     if constexpr (FMT == FMT_BW) rs = *(const uint32_t*)(sp + 2 * kt);
   };

@@ -16,6 +16,7 @@
 // consecutive keys of one dim).  S stays in registers for an online softmax (row max and sum
 // by DPP rotations inside the 16-lane rows that hold one query row's scores); P goes through a
 // wavefront-private LDS tile to change from the MFMA result layout to the operand layout.
+#include <stdlib.h>
 #include "afx_common.h"
 
 namespace afx {
@@ -67,6 +68,8 @@ struct PrefillAttnArgs {
   long long kv_hs;
   int ldq, ldo, M, pos0, Hq, Hkv, Mmax;
   float scale_log2;
+  int tiles;              // query tiles (the pipelined form's grid is tiles * Hq workgroups)
+  int xcd_map;            // pipelined form: kv head k on XCD k % 8 (Hkv % 8 == 0)
 };
 
 // max / sum over the 16 lanes of each DPP row (every lane receives the result)
@@ -80,141 +83,229 @@ __device__ __forceinline__ float row16(float v) {
   return v;
 }
 
+// One 64-key block of a wavefront's 16 queries: S = Q K^T from the staged K, the online softmax
+// update (log2 domain), P through the wavefront's LDS tile, O += P V from the staged V^T.
+__device__ __forceinline__ void attn_block(const PrefillAttnArgs& a, const unsigned char* Ks, const unsigned char* Vt,
+                                           unsigned char* pw, const h8 (&qf)[4], const int (&qpos)[4], int key0,
+                                           int mwave, int fr, int fg, f4 (&acc)[8], float (&mrow)[4],
+                                           float (&lrow)[4]) {
+  // S = Q K^T for 16 queries x 64 keys (four 16-key tiles)
+  f4 s[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    s[j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const h8 kf = __builtin_bit_cast(h8, *(const u4*)(Ks + (j * 16 + fr) * kKStride + (ks * 32 + 8 * fg) * 2));
+      s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[ks], kf, s[j], 0, 0, 0);
+    }
+  }
+  // online softmax (log2 domain); lane holds rows 4 * fg + i, key j * 16 + fr.  Only a block with a key
+  // past the wavefront's first query position needs the causal mask (wavefront-uniform); the scale
+  // (positive) is applied to the block maximum and inside the exponent's FMA.
+  if (key0 + kPK - 1 > mwave) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[j][i] = key0 + j * 16 + fr <= qpos[i] ? s[j][i] : -INFINITY;
+  }
+  float alpha[4];
+  bool grew = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float bm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bm = fmaxf(bm, s[j][i]);
+    bm = row16<true>(bm) * a.scale_log2;
+    const float mn = fmaxf(mrow[i], bm);         // finite: every row sees key 0 in block 0
+    grew = grew || mn > mrow[i];
+    alpha[i] = __builtin_amdgcn_exp2f(mrow[i] - mn);
+    mrow[i] = mn;
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][i], a.scale_log2, -mn));
+      s[j][i] = p;
+      rs += p;
+    }
+    lrow[i] = lrow[i] * alpha[i] + row16<false>(rs);
+  }
+  // rescale only when some row's maximum grew (otherwise every alpha is exactly 1)
+  if (__builtin_amdgcn_ballot_w64(grew)) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[d][i] *= alpha[i];
+  }
+  // P (fp16) through the wavefront's LDS tile into the A-operand layout
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *(half_t*)(pw + (4 * fg + i) * kPStride + (j * 16 + fr) * 2) = (half_t)s[j][i];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  h8 pf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) pf[ks] = __builtin_bit_cast(h8, *(const u4*)(pw + fr * kPStride + (ks * 32 + 8 * fg) * 2));
+  // O += P V over eight 16-dim tiles
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const h8 vf = __builtin_bit_cast(h8, *(const u4*)(Vt + (d * 16 + fr) * kVStride + (ks * 32 + 8 * fg) * 2));
+      acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vf, acc[d], 0, 0, 0);
+    }
+}
+
+// K (row-major, 4 x 16 B per thread) and V (transposed while staged: one key per lane, four
+// 16-byte dim groups per wavefront) of the 64-key block at key0 into LDS.
+struct KvRegs { u4 k[4], v[4]; };
+__device__ __forceinline__ void kv_load(const PrefillAttnArgs& a, const half_t* kbase, const half_t* vbase, int key0,
+                                        int tid, int lane, int wave, KvRegs& r) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    const int key = key0 + row < a.Mmax ? key0 + row : a.Mmax - 1;   // past the cache: masked in attn_block
+    r.k[i] = *(const u4*)(kbase + (size_t)key * kPD + ch * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ch = wave * 4 + i;                 // dims ch * 8 .. + 7 of key `lane`
+    const int key = key0 + lane < a.Mmax ? key0 + lane : a.Mmax - 1;
+    r.v[i] = *(const u4*)(vbase + (size_t)key * kPD + ch * 8);
+  }
+}
+__device__ __forceinline__ void kv_stage(const KvRegs& r, unsigned char* Ks, unsigned char* Vt, int tid, int lane,
+                                         int wave) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    *(u4*)(Ks + row * kKStride + ch * 16) = r.k[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ch = wave * 4 + i;
+    const uint32_t w4[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *(uint16_t*)(Vt + (ch * 8 + 2 * j) * kVStride + lane * 2) = (uint16_t)(w4[j] & 0xffffu);
+      *(uint16_t*)(Vt + (ch * 8 + 2 * j + 1) * kVStride + lane * 2) = (uint16_t)(w4[j] >> 16);
+    }
+  }
+}
+
+// The workgroup's query tile and head, and the lane's query fragments / positions.
+struct AttnTile { int h, kvh, m0, nkb; };
+__device__ __forceinline__ void attn_prologue(const PrefillAttnArgs& a, const AttnTile& tl, int wave, int fr, int fg,
+                                              h8 (&qf)[4], int (&qpos)[4]) {
+  const int mq = tl.m0 + wave * 16 + fr;
+  const half_t* qrow = a.q + (size_t)(mq < a.M ? mq : a.M - 1) * a.ldq + (size_t)tl.h * kPD;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = __builtin_bit_cast(h8, *(const u4*)(qrow + ks * 32 + 8 * fg));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qpos[i] = a.pos0 + tl.m0 + wave * 16 + 4 * fg + i;
+}
+// o = acc / l: lane holds rows 4 * fg + i of dim d * 16 + fr
+__device__ __forceinline__ void attn_store(const PrefillAttnArgs& a, const AttnTile& tl, int wave, int fr, int fg,
+                                           const f4 (&acc)[8], const float (&lrow)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = tl.m0 + wave * 16 + 4 * fg + i;
+    if (m >= a.M) continue;
+    const float inv = 1.0f / lrow[i];
+    half_t* orow = a.o + (size_t)m * a.ldo + (size_t)tl.h * kPD;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) orow[d * 16 + fr] = (half_t)(acc[d][i] * inv);
+  }
+}
+__device__ __forceinline__ AttnTile attn_tile(const PrefillAttnArgs& a, int h, int m0) {
+  AttnTile t;
+  t.h = h;
+  t.kvh = h / (a.Hq / a.Hkv);
+  t.m0 = m0;
+  const int mlast = m0 + kPQ - 1 < a.M - 1 ? m0 + kPQ - 1 : a.M - 1;
+  t.nkb = (a.pos0 + mlast) / kPK + 1;            // through the last key any query of the tile sees
+  return t;
+}
+
+// Single-buffered form: grid (query tiles, heads), K/V of each block loaded, staged, then used.
 __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   __shared__ __align__(16) unsigned char Ks[kPK * kKStride];
   __shared__ __align__(16) unsigned char Vt[kPD * kVStride];
   __shared__ __align__(16) unsigned char Ps[4][16 * kPStride];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fg = lane >> 4;
-  const int h = blockIdx.y, kvh = h / (a.Hq / a.Hkv);
-  const int m0 = blockIdx.x * kPQ;
-  const int mlast = m0 + kPQ - 1 < a.M - 1 ? m0 + kPQ - 1 : a.M - 1;
-  const int kend = a.pos0 + mlast;               // last key any query of this workgroup sees
-  const int nkb = kend / kPK + 1;
-  const half_t* kbase = a.k + (size_t)kvh * a.kv_hs;
-  const half_t* vbase = a.v + (size_t)kvh * a.kv_hs;
-
-  // this lane's query fragments (row fr of the wavefront's 16, dims ks * 32 + 8 * fg ..)
-  const int mq = m0 + wave * 16 + fr;
-  const half_t* qrow = a.q + (size_t)(mq < a.M ? mq : a.M - 1) * a.ldq + (size_t)h * kPD;
+  const AttnTile tl = attn_tile(a, blockIdx.y, blockIdx.x * kPQ);
+  const half_t* kbase = a.k + (size_t)tl.kvh * a.kv_hs;
+  const half_t* vbase = a.v + (size_t)tl.kvh * a.kv_hs;
   h8 qf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) qf[ks] = __builtin_bit_cast(h8, *(const u4*)(qrow + ks * 32 + 8 * fg));
-  // positions of the four query rows this lane's results belong to
   int qpos[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) qpos[i] = a.pos0 + m0 + wave * 16 + 4 * fg + i;
-
+  attn_prologue(a, tl, wave, fr, fg, qf, qpos);
   f4 acc[8];
 #pragma unroll
   for (int d = 0; d < 8; ++d) acc[d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
   float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, lrow[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  unsigned char* pw = Ps[wave];
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int key0 = kb * kPK;
-    // stage K (row-major) and V (transposed): K as 4 x 16 B per thread, V one key per lane
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i, r = c >> 4, ch = c & 15;
-      const int key = key0 + r < a.Mmax ? key0 + r : a.Mmax - 1;   // past the cache: masked below
-      *(u4*)(Ks + r * kKStride + ch * 16) = *(const u4*)(kbase + (size_t)key * kPD + ch * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ch = wave * 4 + i;                 // dims ch * 8 .. + 7 of key `lane`
-      const int key = key0 + lane < a.Mmax ? key0 + lane : a.Mmax - 1;
-      const u4 vv = *(const u4*)(vbase + (size_t)key * kPD + ch * 8);
-      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        *(uint16_t*)(Vt + (ch * 8 + 2 * j) * kVStride + lane * 2) = (uint16_t)(w4[j] & 0xffffu);
-        *(uint16_t*)(Vt + (ch * 8 + 2 * j + 1) * kVStride + lane * 2) = (uint16_t)(w4[j] >> 16);
-      }
-    }
+  for (int kb = 0; kb < tl.nkb; ++kb) {
+    KvRegs r;
+    kv_load(a, kbase, vbase, kb * kPK, tid, lane, wave, r);
+    kv_stage(r, Ks, Vt, tid, lane, wave);
     __syncthreads();
-
-    // S = Q K^T for 16 queries x 64 keys (four 16-key tiles)
-    f4 s[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s[j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const h8 kf = __builtin_bit_cast(h8, *(const u4*)(Ks + (j * 16 + fr) * kKStride + (ks * 32 + 8 * fg) * 2));
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[ks], kf, s[j], 0, 0, 0);
-      }
-    }
-    // online softmax (log2 domain); lane holds rows 4 * fg + i, key j * 16 + fr.  Only a block with a key
-    // past the wavefront's first query position needs the causal mask (wavefront-uniform); the scale
-    // (positive) is applied to the block maximum and inside the exponent's FMA.
-    if (key0 + kPK - 1 > a.pos0 + m0 + wave * 16) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) s[j][i] = key0 + j * 16 + fr <= qpos[i] ? s[j][i] : -INFINITY;
-    }
-    float alpha[4];
-    bool grew = false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float bm = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bm = fmaxf(bm, s[j][i]);
-      bm = row16<true>(bm) * a.scale_log2;
-      const float mn = fmaxf(mrow[i], bm);         // finite: every row sees key 0 in block 0
-      grew = grew || mn > mrow[i];
-      alpha[i] = __builtin_amdgcn_exp2f(mrow[i] - mn);
-      mrow[i] = mn;
-      float rs = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][i], a.scale_log2, -mn));
-        s[j][i] = p;
-        rs += p;
-      }
-      lrow[i] = lrow[i] * alpha[i] + row16<false>(rs);
-    }
-    // rescale only when some row's maximum grew (otherwise every alpha is exactly 1)
-    if (__builtin_amdgcn_ballot_w64(grew)) {
-#pragma unroll
-      for (int d = 0; d < 8; ++d)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[d][i] *= alpha[i];
-    }
-    // P (fp16) through the wavefront's LDS tile into the A-operand layout
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *(half_t*)(pw + (4 * fg + i) * kPStride + (j * 16 + fr) * 2) = (half_t)s[j][i];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    h8 pf[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) pf[ks] = __builtin_bit_cast(h8, *(const u4*)(pw + fr * kPStride + (ks * 32 + 8 * fg) * 2));
-    // O += P V over eight 16-dim tiles
-#pragma unroll
-    for (int d = 0; d < 8; ++d)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const h8 vf = __builtin_bit_cast(h8, *(const u4*)(Vt + (d * 16 + fr) * kVStride + (ks * 32 + 8 * fg) * 2));
-        acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[ks], vf, acc[d], 0, 0, 0);
-      }
+    attn_block(a, Ks, Vt, Ps[wave], qf, qpos, kb * kPK, a.pos0 + tl.m0 + wave * 16, fr, fg, acc, mrow, lrow);
     __syncthreads();                               // Ks, Vt and this wavefront's P are reused next block
   }
+  attn_store(a, tl, wave, fr, fg, acc, lrow);
+}
 
-  // o = acc / l: lane holds rows 4 * fg + i of dim d * 16 + fr
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + wave * 16 + 4 * fg + i;
-    if (m >= a.M) continue;
-    const float inv = 1.0f / lrow[i];
-    half_t* orow = a.o + (size_t)m * a.ldo + (size_t)h * kPD;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) orow[d * 16 + fr] = (half_t)(acc[d][i] * inv);
+// Pipelined form (the default): the same per-block math, with
+//  * the next block's K/V loaded into registers while the current block's MFMAs run, and staged into
+//    the other of two LDS buffers afterwards (one barrier per block);
+//  * the heaviest query tiles (the most causal key blocks) dispatched first, so the launch does not
+//    end on a few long tiles;
+//  * with Hkv % 8 == 0, every tile of kv head k on XCD k % 8 (workgroup b runs on XCD b % 8), so a
+//    head's K/V rows are fetched into one L2 and reused there by its G query heads.
+// Outputs are bit-identical to the single-buffered form.
+__global__ __launch_bounds__(256) void prefill_attn_kernel2(PrefillAttnArgs a) {
+  __shared__ __align__(16) unsigned char Ks[2][kPK * kKStride];
+  __shared__ __align__(16) unsigned char Vt[2][kPD * kVStride];
+  __shared__ __align__(16) unsigned char Ps[4][16 * kPStride];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int id = blockIdx.x, G = a.Hq / a.Hkv;
+  int t, h;
+  if (a.xcd_map) {
+    const int x = id & 7, l = id >> 3, per_t = (a.Hkv >> 3) * G;
+    t = a.tiles - 1 - l / per_t;
+    const int r = l - (l / per_t) * per_t;
+    h = (x + 8 * (r / G)) * G + r % G;
+  } else {
+    t = a.tiles - 1 - id / a.Hq;
+    h = id % a.Hq;
   }
+  const AttnTile tl = attn_tile(a, h, t * kPQ);
+  const half_t* kbase = a.k + (size_t)tl.kvh * a.kv_hs;
+  const half_t* vbase = a.v + (size_t)tl.kvh * a.kv_hs;
+  KvRegs r;
+  kv_load(a, kbase, vbase, 0, tid, lane, wave, r);
+  h8 qf[4];
+  int qpos[4];
+  attn_prologue(a, tl, wave, fr, fg, qf, qpos);
+  f4 acc[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) acc[d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+  float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, lrow[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  kv_stage(r, Ks[0], Vt[0], tid, lane, wave);
+  __syncthreads();
+  const int mwave = a.pos0 + tl.m0 + wave * 16;
+  for (int kb = 0; kb < tl.nkb; ++kb) {
+    const int s = kb & 1;
+    if (kb + 1 < tl.nkb) kv_load(a, kbase, vbase, (kb + 1) * kPK, tid, lane, wave, r);
+    attn_block(a, Ks[s], Vt[s], Ps[wave], qf, qpos, kb * kPK, mwave, fr, fg, acc, mrow, lrow);
+    if (kb + 1 < tl.nkb) kv_stage(r, Ks[s ^ 1], Vt[s ^ 1], tid, lane, wave);   // last read before the previous barrier
+    __syncthreads();
+  }
+  attn_store(a, tl, wave, fr, fg, acc, lrow);
 }
 
 }  // namespace afx
@@ -259,7 +350,17 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
   a.q = (const half_t*)q; a.k = (const half_t*)kcache; a.v = (const half_t*)vcache; a.o = (half_t*)o;
   a.kv_hs = kv_hs; a.ldq = ldq; a.ldo = ldo; a.M = M; a.pos0 = pos0; a.Hq = Hq; a.Hkv = Hkv; a.Mmax = Mmax;
   a.scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(prefill_attn_kernel, dim3((M + kPQ - 1) / kPQ, Hq), dim3(256), 0, (hipStream_t)stream, a);
+  a.tiles = (M + kPQ - 1) / kPQ;
+  a.xcd_map = Hkv % 8 == 0;
+  static int v1_env = -1;
+  if (v1_env < 0) {
+    const char* e = getenv("AFX_PREFILL_ATTN_V1");
+    v1_env = e && atoi(e) == 1 ? 1 : 0;
+  }
+  if (v1_env)                                      // the single-buffered form (same outputs)
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.tiles, Hq), dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(prefill_attn_kernel2, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("afx_prefill_attn");
 }
 

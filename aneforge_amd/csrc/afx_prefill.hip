@@ -308,6 +308,195 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel2(PrefillAttnArgs a) {
   attn_store(a, tl, wave, fr, fg, acc, lrow);
 }
 
+// ---- transposed-score form: S^T = K Q^T, 32 queries per wavefront, P never leaves the registers ----
+// With K as the A operand and Q^T as B, a lane's MFMA result holds keys 4 * fg .. + 3 (of a 16-key
+// tile) for query fr, so every score of one query sits in the four lanes fr, fr + 16, fr + 32, fr + 48:
+//  * row maxima and sums are a lane-local reduction over 16 values plus two cross-lane exchanges;
+//  * the fp16 probabilities of key tiles 2ks and 2ks + 1 are exactly the B operand P^T of the
+//    32-key slot ks of O^T = V^T P^T, under the k order (4 fg .. + 3, 16 + 4 fg .. + 3), which V^T
+//    is staged in (vt_pos), so a lane's 8 keys of one dim are one 16-byte LDS read;
+//  * O^T's result holds dims 4 * fg .. + 3 of query fr: the softmax rescale is lane-local.
+// Two query tiles per wavefront share every K and V fragment read (half the LDS reads per MFMA of
+// the forms above).  Summation orders differ from them: results agree to fp16 rounding.
+constexpr int kPQ3 = 128;                // queries per workgroup (4 wavefronts x 32)
+
+__device__ __forceinline__ int vt_pos(int key) {   // staged position of key (0..63) in a V^T row
+  const int k = key & 31;
+  return (key & 32) + 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3);
+}
+__device__ __forceinline__ float xor_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float xor_sum(float v) {
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+__device__ __forceinline__ void kv_stage3(const KvRegs& r, unsigned char* Ks, unsigned char* Vt, int tid, int lane,
+                                          int wave) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    *(u4*)(Ks + row * kKStride + ch * 16) = r.k[i];
+  }
+  const int vp = vt_pos(lane) * 2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ch = wave * 4 + i;
+    const uint32_t w4[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *(uint16_t*)(Vt + (ch * 8 + 2 * j) * kVStride + vp) = (uint16_t)(w4[j] & 0xffffu);
+      *(uint16_t*)(Vt + (ch * 8 + 2 * j + 1) * kVStride + vp) = (uint16_t)(w4[j] >> 16);
+    }
+  }
+}
+
+__device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsigned char* Ks, const unsigned char* Vt,
+                                            const h8 (&qf)[2][4], const int (&qp)[2], int key0, int mwpos, int fr,
+                                            int fg, f4 (&acc)[2][8], float (&mrow)[2], float (&lrow)[2]) {
+  f4 st[2][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h8 kf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      kf[ks] = __builtin_bit_cast(h8, *(const u4*)(Ks + (j * 16 + fr) * kKStride + (ks * 32 + 8 * fg) * 2));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      st[u][j] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) st[u][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[ks], qf[u][ks], st[u][j], 0, 0, 0);
+    }
+  }
+  // causal mask only in a block holding a key past the wavefront's first query position (uniform)
+  if (key0 + kPK - 1 > mwpos) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[u][j][i] = key0 + j * 16 + 4 * fg + i <= qp[u] ? st[u][j][i] : -INFINITY;
+  }
+  float alpha[2];
+  bool grew = false;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    float bm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bm = fmaxf(bm, st[u][j][i]);
+    bm = xor_max(bm) * a.scale_log2;
+    const float mn = fmaxf(mrow[u], bm);         // finite: every query sees key 0 in block 0
+    grew = grew || mn > mrow[u];
+    alpha[u] = __builtin_amdgcn_exp2f(mrow[u] - mn);
+    mrow[u] = mn;
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[u][j][i], a.scale_log2, -mn));
+        st[u][j][i] = p;
+        rs += p;
+      }
+    lrow[u] = lrow[u] * alpha[u] + xor_sum(rs);
+  }
+  if (__builtin_amdgcn_ballot_w64(grew)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[u][d][i] *= alpha[u];
+  }
+  h8 pf[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const f4 lo = st[u][2 * ks], hi = st[u][2 * ks + 1];
+      pf[u][ks] = (h8){(half_t)lo[0], (half_t)lo[1], (half_t)lo[2], (half_t)lo[3],
+                       (half_t)hi[0], (half_t)hi[1], (half_t)hi[2], (half_t)hi[3]};
+    }
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const h8 vf = __builtin_bit_cast(h8, *(const u4*)(Vt + (d * 16 + fr) * kVStride + (ks * 32 + 8 * fg) * 2));
+#pragma unroll
+      for (int u = 0; u < 2; ++u) acc[u][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[u][ks], acc[u][d], 0, 0, 0);
+    }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel3(PrefillAttnArgs a) {
+  __shared__ __align__(16) unsigned char Ks[2][kPK * kKStride];
+  __shared__ __align__(16) unsigned char Vt[2][kPD * kVStride];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int id = blockIdx.x, G = a.Hq / a.Hkv;
+  int t, h;                                      // heaviest tiles first; kv head k on XCD k % 8
+  if (a.xcd_map) {
+    const int x = id & 7, l = id >> 3, per_t = (a.Hkv >> 3) * G;
+    t = a.tiles - 1 - l / per_t;
+    const int r = l - (l / per_t) * per_t;
+    h = (x + 8 * (r / G)) * G + r % G;
+  } else {
+    t = a.tiles - 1 - id / a.Hq;
+    h = id % a.Hq;
+  }
+  const int m0 = t * kPQ3, kvh = h / G;
+  const int mlast = m0 + kPQ3 - 1 < a.M - 1 ? m0 + kPQ3 - 1 : a.M - 1;
+  const int nkb = (a.pos0 + mlast) / kPK + 1;
+  const int mw = m0 + 32 * wave;                 // the wavefront's first query
+  const int wlast = mw < a.M ? a.pos0 + (mw + 31 < a.M - 1 ? mw + 31 : a.M - 1) : -1;   // its last visible key
+  const half_t* kbase = a.k + (size_t)kvh * a.kv_hs;
+  const half_t* vbase = a.v + (size_t)kvh * a.kv_hs;
+  KvRegs r;
+  kv_load(a, kbase, vbase, 0, tid, lane, wave, r);
+  h8 qf[2][4];
+  int qp[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int mq = mw + 16 * u + fr;
+    const half_t* qrow = a.q + (size_t)(mq < a.M ? mq : a.M - 1) * a.ldq + (size_t)h * kPD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[u][ks] = __builtin_bit_cast(h8, *(const u4*)(qrow + ks * 32 + 8 * fg));
+    qp[u] = a.pos0 + mq;
+  }
+  f4 acc[2][8];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[u][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+  float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.0f, 0.0f};
+  kv_stage3(r, Ks[0], Vt[0], tid, lane, wave);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int s = kb & 1;
+    if (kb + 1 < nkb) kv_load(a, kbase, vbase, (kb + 1) * kPK, tid, lane, wave, r);
+    if (kb * kPK <= wlast)                       // blocks wholly past the wavefront's queries are skipped
+      attn_block3(a, Ks[s], Vt[s], qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow);
+    if (kb + 1 < nkb) kv_stage3(r, Ks[s ^ 1], Vt[s ^ 1], tid, lane, wave);
+    __syncthreads();
+  }
+  // o = O^T / l: lane holds dims 16 d + 4 fg .. + 3 of query mw + 16 u + fr
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int m = mw + 16 * u + fr;
+    if (m >= a.M) continue;
+    const float inv = 1.0f / lrow[u];
+    half_t* orow = a.o + (size_t)m * a.ldo + (size_t)h * kPD + 4 * fg;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const h2 lo = {(half_t)(acc[u][d][0] * inv), (half_t)(acc[u][d][1] * inv)};
+      const h2 hi = {(half_t)(acc[u][d][2] * inv), (half_t)(acc[u][d][3] * inv)};
+      *(u2*)(orow + d * 16) = (u2){as_u32(lo), as_u32(hi)};
+    }
+  }
+}
+
 }  // namespace afx
 
 using namespace afx;
@@ -352,15 +541,19 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
   a.scale_log2 = scale * 1.4426950408889634f;
   a.tiles = (M + kPQ - 1) / kPQ;
   a.xcd_map = Hkv % 8 == 0;
-  static int v1_env = -1;
-  if (v1_env < 0) {
-    const char* e = getenv("AFX_PREFILL_ATTN_V1");
-    v1_env = e && atoi(e) == 1 ? 1 : 0;
+  static int form_env = -1;
+  if (form_env < 0) {
+    const char* e = getenv("AFX_PREFILL_ATTN_FORM");
+    form_env = e ? atoi(e) : 3;
   }
-  if (v1_env)                                      // the single-buffered form (same outputs)
+  if (form_env == 1) {                             // single-buffered
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.tiles, Hq), dim3(256), 0, (hipStream_t)stream, a);
-  else
+  } else if (form_env == 2 || ldo % 4 != 0 || ((uintptr_t)o & 7) != 0) {   // pipelined, bit-identical to form 1
     hipLaunchKernelGGL(prefill_attn_kernel2, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
+  } else {                                         // transposed scores, 128 queries per workgroup (8-byte stores)
+    a.tiles = (M + kPQ3 - 1) / kPQ3;
+    hipLaunchKernelGGL(prefill_attn_kernel3, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
+  }
   return check_launch("afx_prefill_attn");
 }
 

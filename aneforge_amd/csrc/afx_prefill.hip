@@ -70,6 +70,7 @@ struct PrefillAttnArgs {
   float scale_log2;
   int tiles;              // query tiles (the pipelined form's grid is tiles * Hq workgroups)
   int xcd_map;            // pipelined form: kv head k on XCD k % 8 (Hkv % 8 == 0)
+  int order;              // form 3 tile order: 1 paired heavy / light, 0 heaviest first
 };
 
 // max / sum over the 16 lanes of each DPP row (every lane receives the result)
@@ -436,16 +437,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fg = lane >> 4;
   const int id = blockIdx.x, G = a.Hq / a.Hkv;
-  int t, h;                                      // heaviest tiles first; kv head k on XCD k % 8
+  int k, h;                                      // k-th tile slot of the order below; kv head k on XCD k % 8
   if (a.xcd_map) {
     const int x = id & 7, l = id >> 3, per_t = (a.Hkv >> 3) * G;
-    t = a.tiles - 1 - l / per_t;
-    const int r = l - (l / per_t) * per_t;
+    k = l / per_t;
+    const int r = l - k * per_t;
     h = (x + 8 * (r / G)) * G + r % G;
   } else {
-    t = a.tiles - 1 - id / a.Hq;
+    k = id / a.Hq;
     h = id % a.Hq;
   }
+  // Tile order: the first half of the slots heaviest first (the most causal key blocks), the second
+  // half lightest first.  When the grid fits the CUs in two workgroups each, a CU's second
+  // workgroup then pairs tile T - 1 - j with tile j: every CU gets about the same number of blocks.
+  // a.order == 0: heaviest first throughout.
+  const int half = (a.tiles + 1) >> 1;
+  const int t = a.order == 0 || k < half ? a.tiles - 1 - k : k - half;
   const int m0 = t * kPQ3, kvh = h / G;
   const int mlast = m0 + kPQ3 - 1 < a.M - 1 ? m0 + kPQ3 - 1 : a.M - 1;
   const int nkb = (a.pos0 + mlast) / kPK + 1;
@@ -552,6 +559,12 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
     hipLaunchKernelGGL(prefill_attn_kernel2, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
   } else {                                         // transposed scores, 128 queries per workgroup (8-byte stores)
     a.tiles = (M + kPQ3 - 1) / kPQ3;
+    static int order_env = -1;
+    if (order_env < 0) {
+      const char* e = getenv("AFX_PREFILL_ATTN_ORDER");
+      order_env = e ? atoi(e) : 1;
+    }
+    a.order = order_env;
     hipLaunchKernelGGL(prefill_attn_kernel3, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
   }
   return check_launch("afx_prefill_attn");

@@ -312,11 +312,8 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   // tile order: groups of 8 weight tiles per XCD (AFX_GEMM_GN overrides; 0 = the row-tiles-fastest
   // contiguous order).  At M = 2048 on the 7B shapes, against the contiguous order: gate/up 900 -> 947,
   // down 798 -> 815 TFLOP/s, o-proj and QKV within noise; outputs bit-identical.
-  static int gn_env = -2;
-  if (gn_env == -2) {
-    const char* e = getenv("AFX_GEMM_GN");
-    gn_env = e ? atoi(e) : 8;
-  }
+  const char* ge = getenv("AFX_GEMM_GN");            // read per call: tests compare the orders in one process
+  const int gn_env = ge ? atoi(ge) : 8;
   a.gn = gn_env > 0 ? gn_env : 0;
   if (a.gn > 0) a.per_xcd = ((a.tiles_n + 7) / 8) * a.tiles_m;   // the largest XCD range
   // kernel form: 2 for int8 codes, 0 for fp16 weights (the faster of the two on each format at the

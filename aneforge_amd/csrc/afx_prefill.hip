@@ -548,23 +548,16 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
   a.scale_log2 = scale * 1.4426950408889634f;
   a.tiles = (M + kPQ - 1) / kPQ;
   a.xcd_map = Hkv % 8 == 0;
-  static int form_env = -1;
-  if (form_env < 0) {
-    const char* e = getenv("AFX_PREFILL_ATTN_FORM");
-    form_env = e ? atoi(e) : 3;
-  }
+  const char* fe = getenv("AFX_PREFILL_ATTN_FORM");   // read per call: tests compare the forms in one process
+  const int form_env = fe ? atoi(fe) : 3;
   if (form_env == 1) {                             // single-buffered
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.tiles, Hq), dim3(256), 0, (hipStream_t)stream, a);
   } else if (form_env == 2 || ldo % 4 != 0 || ((uintptr_t)o & 7) != 0) {   // pipelined, bit-identical to form 1
     hipLaunchKernelGGL(prefill_attn_kernel2, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
   } else {                                         // transposed scores, 128 queries per workgroup (8-byte stores)
     a.tiles = (M + kPQ3 - 1) / kPQ3;
-    static int order_env = -1;
-    if (order_env < 0) {
-      const char* e = getenv("AFX_PREFILL_ATTN_ORDER");
-      order_env = e ? atoi(e) : 1;
-    }
-    a.order = order_env;
+    const char* oe = getenv("AFX_PREFILL_ATTN_ORDER");
+    a.order = oe ? atoi(oe) : 1;
     hipLaunchKernelGGL(prefill_attn_kernel3, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
   }
   return check_launch("afx_prefill_attn");

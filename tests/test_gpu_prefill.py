@@ -111,3 +111,76 @@ def test_prefill_attention_matches_oracle(M, pos0, Hq, Hkv):
     mask = np.where(np.arange(L)[None, :] <= pos0 + np.arange(M)[:, None], 0.0, -np.inf)
     want = ref.attention(q.reshape(M, Hq, D).transpose(1, 0, 2)[None], Kc[None, :, :L], Vc[None, :, :L], mask=mask)
     check_f16(host(o), want[0].transpose(1, 0, 2).reshape(M, Hq * D), what="prefill attention")
+
+
+def _env(name, value):
+    """Set (or clear, value None) one of the kernel-form environment switches; returns the old value."""
+    import os
+    old = os.environ.get(name)
+    if value is None:
+        os.environ.pop(name, None)
+    else:
+        os.environ[name] = str(value)
+    return old
+
+
+@pytest.mark.parametrize("M,pos0,Hq,Hkv,Mmax", [(300, 0, 16, 8, 320), (257, 40, 8, 8, 300), (130, 0, 8, 2, 256),
+                                                (1, 5, 4, 2, 64), (640, 100, 16, 8, 800)])
+def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
+    """Every prefill-attention form against the oracle: single-buffered (1), pipelined (2, the same
+    arithmetic: bit-identical to 1), transposed scores (3, the default) with both tile orders, on
+    grids with several workgroup rounds, the XCD mapping (Hkv = 8) and without it (Hkv = 2)."""
+    import torch
+    from aneforge_amd import _kernels as Kn
+    D = 128
+    rng = np.random.default_rng(M * 7 + pos0 + Hq + Hkv)
+    L = pos0 + M
+    Kc = np.zeros((Hkv, Mmax, D), np.float16)
+    Vc = np.zeros((Hkv, Mmax, D), np.float16)
+    Kc[:, :L] = rng.standard_normal((Hkv, L, D)).astype(np.float16)
+    Vc[:, :L] = rng.standard_normal((Hkv, L, D)).astype(np.float16)
+    q = rng.standard_normal((M, Hq * D)).astype(np.float16)
+    mask = np.where(np.arange(L)[None, :] <= pos0 + np.arange(M)[:, None], 0.0, -np.inf)
+    want = ref.attention(q.reshape(M, Hq, D).transpose(1, 0, 2)[None], Kc[None, :, :L], Vc[None, :, :L], mask=mask)
+    want = want[0].transpose(1, 0, 2).reshape(M, Hq * D)
+    outs = {}
+    old_f, old_o = _env("AFX_PREFILL_ATTN_FORM", None), _env("AFX_PREFILL_ATTN_ORDER", None)
+    try:
+        for form, order in ((1, None), (2, None), (3, 0), (3, 1)):
+            _env("AFX_PREFILL_ATTN_FORM", form)
+            _env("AFX_PREFILL_ATTN_ORDER", order)
+            say(f"prefill_attn form={form} order={order} M={M} pos0={pos0} Hq={Hq} Hkv={Hkv}")
+            o = torch.zeros((M, Hq * D), dtype=torch.float16, device="cuda")
+            Kn.prefill_attn(dev(q), dev(Kc), dev(Vc), o, pos0, Hq, Hkv)
+            outs[(form, order)] = host(o)
+            check_f16(outs[(form, order)], want, what=f"prefill attention form {form} order {order}")
+    finally:
+        _env("AFX_PREFILL_ATTN_FORM", old_f)
+        _env("AFX_PREFILL_ATTN_ORDER", old_o)
+    np.testing.assert_array_equal(outs[(1, None)], outs[(2, None)])
+    np.testing.assert_array_equal(outs[(3, 0)], outs[(3, 1)])
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp16"])
+@pytest.mark.parametrize("M,N,K", [(300, 2304, 256), (1000, 1280, 512), (2048, 4096, 128)])
+def test_gemm_tile_orders_bit_identical(fmt, M, N, K):
+    """The grouped tile order (default), other group sizes and the contiguous order (AFX_GEMM_GN=0)
+    compute every output tile the same way: bit-identical, and to the oracle's bar."""
+    import torch
+    from aneforge_amd import _kernels as Kn
+    rng = np.random.default_rng(M + N + K)
+    w, s, Wf = _weights(fmt, N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    want = ref.r16(np.asarray(x, np.float64) @ np.asarray(Wf, np.float64).T)
+    outs = []
+    old = _env("AFX_GEMM_GN", None)
+    try:
+        for gn in (None, 0, 3, 16):
+            _env("AFX_GEMM_GN", gn)
+            say(f"gemm tile order GN={gn} {fmt} M={M} N={N} K={K}")
+            outs.append(host(Kn.gemm(fmt, w, s, dev(x), epi="f16")))
+    finally:
+        _env("AFX_GEMM_GN", old)
+    check_f16(outs[0], want, what=f"gemm {fmt} grouped order")
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])

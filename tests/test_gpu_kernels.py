@@ -640,10 +640,12 @@ def test_rmsnorm_rope_embed_argmax(K):
     assert host(K.argmax(dev(lg))).tolist() == [int(np.argmax(lg[0])), 7]
 
 
-def test_decode_advance_greedy_and_forced(K):
-    say("decode advance (argmax / forced + hist + pos + embed)")
+@pytest.mark.parametrize("V,D", [(32000, 4096), (1000, 4088), (1000, 4104), (300, 8)])
+def test_decode_advance_greedy_and_forced(K, V, D):
+    """A forced step, then a greedy one, with the embedding row gathered into h, at row widths that
+    do and do not fill the workgroup's 16-byte pieces evenly (4088, 4104, 8)."""
+    say(f"decode advance (argmax / forced + hist + pos + embed) V={V} D={D}")
     rng = np.random.default_rng(51)
-    V, D = 32000, 4096
     lg = rng.standard_normal(V).astype(np.float32)
     table = rng.standard_normal((V, D)).astype(np.float16)
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -713,15 +715,21 @@ def test_decode_advance_near_tie_recomputes_exactly(K):
     ref_host = W32.astype(np.float64) @ hn.astype(np.float64)
     assert int(np.argmax(ref_host)) == 900 and int(np.argmax(lg)) == 100
 
+    table = rng.standard_normal((V, D)).astype(np.float16)        # embedding rows: h follows the pick
+    tb = dev(table)
+
     def step_once(logits, margin, head32=True):
         tok = torch.zeros(1, dtype=torch.int32, device="cuda")
         pos = torch.zeros(1, dtype=torch.int32, device="cuda")
         stp = torch.zeros(1, dtype=torch.int32, device="cuda")
         hist = torch.zeros(4, dtype=torch.int32, device="cuda")
+        h = torch.zeros((1, D), dtype=torch.float16, device="cuda")
         m = None if margin is None else torch.tensor([margin], dtype=torch.float32, device="cuda")
-        K.decode_advance(dev(logits[None]), tok, pos, hist, stp, tie_margin=m, hn=dev(hn),
+        K.decode_advance(dev(logits[None]), tok, pos, hist, stp, tb, h, tie_margin=m, hn=dev(hn),
                          head16=None if head32 else dev(W16), head32=dev(W32) if head32 else None)
-        return int(host(tok)[0])
+        t = int(host(tok)[0])
+        assert np.array_equal(host(h)[0], table[t])
+        return t
 
     assert step_once(lg, 3e-3) == 900                               # near tie: exact recompute
     assert step_once(lg, None) == 100                               # no rule: lowest index
@@ -731,11 +739,13 @@ def test_decode_advance_near_tie_recomputes_exactly(K):
     assert step_once(clear, 3e-3) == 100                            # a clear gap: no recompute
     # the same rule when the pick comes from the lm_head's slot summaries
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    h = torch.zeros((1, D), dtype=torch.float16, device="cuda")
     K.decode_advance(dev(lg[None]), tok, torch.zeros(1, dtype=torch.int32, device="cuda"),
                      torch.zeros(4, dtype=torch.int32, device="cuda"), torch.zeros(1, dtype=torch.int32, device="cuda"),
-                     slots=dev(_host_slots(lg)), tie_margin=torch.tensor([3e-3], dtype=torch.float32, device="cuda"),
+                     tb, h, slots=dev(_host_slots(lg)), tie_margin=torch.tensor([3e-3], dtype=torch.float32, device="cuda"),
                      hn=dev(hn), head32=dev(W32))
     assert int(host(tok)[0]) == 900
+    assert np.array_equal(host(h)[0], table[900])                   # not the top-1's row (100)
 
 
 def _host_slots(lg):

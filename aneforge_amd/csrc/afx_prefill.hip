@@ -353,6 +353,9 @@ __device__ __forceinline__ void kv_stage3(const KvRegs& r, unsigned char* Ks, un
   }
 }
 
+// EMPTY: a query may have seen no key yet (a block range that starts past its position); its
+// running maximum is then -inf and the exponents take 0 in its place, so its probabilities are 0.
+template <bool EMPTY = false>
 __device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsigned char* Ks, const unsigned char* Vt,
                                             const h8 (&qf)[2][4], const int (&qp)[2], int key0, int mwpos, int fr,
                                             int fg, f4 (&acc)[2][8], float (&mrow)[2], float (&lrow)[2]) {
@@ -389,16 +392,17 @@ __device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsi
 #pragma unroll
       for (int i = 0; i < 4; ++i) bm = fmaxf(bm, st[u][j][i]);
     bm = xor_max(bm) * a.scale_log2;
-    const float mn = fmaxf(mrow[u], bm);         // finite: every query sees key 0 in block 0
+    const float mn = fmaxf(mrow[u], bm);         // finite unless EMPTY: every query sees key 0 in block 0
+    const float me = EMPTY && mn == -INFINITY ? 0.0f : mn;
     grew = grew || mn > mrow[u];
-    alpha[u] = __builtin_amdgcn_exp2f(mrow[u] - mn);
+    alpha[u] = __builtin_amdgcn_exp2f(mrow[u] - me);
     mrow[u] = mn;
     float rs = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[u][j][i], a.scale_log2, -mn));
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[u][j][i], a.scale_log2, -me));
         st[u][j][i] = p;
         rs += p;
       }
@@ -504,6 +508,121 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ---- form 3 with each tile's key range split over two halves of one workgroup ----
+// A causal prompt's query tiles differ in work by up to the tile count (tile t has 2t + 2 key
+// blocks), and one 4-wavefront workgroup per tile leaves a CU with a heavy tile running alone long
+// after its light neighbour is done.  Here an 8-wavefront workgroup takes one 128-query tile: waves
+// 0-3 run form 3 over the first half of its key blocks, waves 4-7 over the second half, each half
+// with its own double-buffered K / V^T stages (140 KB of LDS: one workgroup per CU, two wavefronts
+// per SIMD as in form 3), and the second half's running maxima, sums and accumulators are merged
+// into the first's through LDS.  No tile costs more than half the longest key range, and with the
+// tiles dispatched heaviest first over two rounds of workgroups the CUs finish together.
+constexpr int kKB4 = kPK * kKStride, kVB4 = kPD * kVStride;   // bytes of one K stage, one V^T stage
+constexpr int kX4 = 68;                  // floats per lane handed over: 2 x 8 accumulator f4s + 2 maxima + 2 sums
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel4(PrefillAttnArgs a) {
+  __shared__ __align__(16) unsigned char lds[4 * kKB4 + 4 * kVB4];   // K stages [half][2], then V^T stages [half][2]
+  static_assert(4 * 64 * kX4 * 4 <= 4 * kKB4, "the handover fits in the K stages");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hf = wave >> 2, w4 = wave & 3, htid = tid & 255;   // half, wavefront and thread within it
+  const int fr = lane & 15, fg = lane >> 4;
+  unsigned char* const Kh = lds + hf * 2 * kKB4;
+  unsigned char* const Vh = lds + 4 * kKB4 + hf * 2 * kVB4;
+  const int id = blockIdx.x, G = a.Hq / a.Hkv;
+  int k, h;                                      // k-th tile slot, heaviest first; kv head k on XCD k % 8
+  if (a.xcd_map) {
+    const int x = id & 7, l = id >> 3, per_t = (a.Hkv >> 3) * G;
+    k = l / per_t;
+    const int r = l - k * per_t;
+    h = (x + 8 * (r / G)) * G + r % G;
+  } else {
+    k = id / a.Hq;
+    h = id % a.Hq;
+  }
+  const int t = a.tiles - 1 - k;
+  const int m0 = t * kPQ3, kvh = h / G;
+  const int mlast = m0 + kPQ3 - 1 < a.M - 1 ? m0 + kPQ3 - 1 : a.M - 1;
+  const int nkb = (a.pos0 + mlast) / kPK + 1;
+  const int nb0 = nkb >> 1;                      // the first half takes blocks [0, nb0), the second [nb0, nkb)
+  const int kb0 = hf ? nb0 : 0, kb1 = hf ? nkb : nb0;
+  const int trips = nkb - nb0;                   // the longer half's count: both halves meet every barrier
+  const int mw = m0 + 32 * w4;                   // the wavefront's first query
+  const int wlast = mw < a.M ? a.pos0 + (mw + 31 < a.M - 1 ? mw + 31 : a.M - 1) : -1;   // its last visible key
+  const half_t* kbase = a.k + (size_t)kvh * a.kv_hs;
+  const half_t* vbase = a.v + (size_t)kvh * a.kv_hs;
+  KvRegs r;
+  if (kb0 < kb1) kv_load(a, kbase, vbase, kb0 * kPK, htid, lane, w4, r);
+  h8 qf[2][4];
+  int qp[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int mq = mw + 16 * u + fr;
+    const half_t* qrow = a.q + (size_t)(mq < a.M ? mq : a.M - 1) * a.ldq + (size_t)h * kPD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[u][ks] = __builtin_bit_cast(h8, *(const u4*)(qrow + ks * 32 + 8 * fg));
+    qp[u] = a.pos0 + mq;
+  }
+  f4 acc[2][8];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[u][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+  float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.0f, 0.0f};
+  if (kb0 < kb1) kv_stage3(r, Kh, Vh, htid, lane, w4);
+  __syncthreads();
+  for (int i = 0; i < trips; ++i) {
+    const int kb = kb0 + i, s = i & 1;
+    const bool more = kb + 1 < kb1;              // uniform over the half
+    if (more) kv_load(a, kbase, vbase, (kb + 1) * kPK, htid, lane, w4, r);
+    if (kb < kb1 && kb * kPK <= wlast)           // blocks wholly past the wavefront's queries are skipped
+      attn_block3<true>(a, Kh + s * kKB4, Vh + s * kVB4, qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow);
+    if (more) kv_stage3(r, Kh + (s ^ 1) * kKB4, Vh + (s ^ 1) * kVB4, htid, lane, w4);
+    __syncthreads();
+  }
+  // the second half hands over through the (now idle) K stages: lane-major, so the accesses are
+  // consecutive words; wavefront w4 of each half holds the same queries in the same lanes
+  float* const xw = (float*)lds + w4 * kX4 * 64 + lane;
+  if (hf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xw[((u * 8 + d) * 4 + i) * 64] = acc[u][d][i];
+      xw[(64 + u) * 64] = mrow[u];
+      xw[(66 + u) * 64] = lrow[u];
+    }
+  }
+  __syncthreads();
+  if (hf) return;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const float mb = xw[(64 + u) * 64], lb = xw[(66 + u) * 64];
+    const float mn = fmaxf(mrow[u], mb);         // finite for every stored query: the half holding block 0 saw key 0
+    const float sa = __builtin_amdgcn_exp2f(mrow[u] - mn);
+    const float sb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - mn);
+    lrow[u] = lrow[u] * sa + lb * sb;
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[u][d][i] = acc[u][d][i] * sa + xw[((u * 8 + d) * 4 + i) * 64] * sb;
+  }
+  // o = O^T / l: lane holds dims 16 d + 4 fg .. + 3 of query mw + 16 u + fr
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int m = mw + 16 * u + fr;
+    if (m >= a.M) continue;
+    const float inv = 1.0f / lrow[u];
+    half_t* orow = a.o + (size_t)m * a.ldo + (size_t)h * kPD + 4 * fg;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const h2 lo = {(half_t)(acc[u][d][0] * inv), (half_t)(acc[u][d][1] * inv)};
+      const h2 hi = {(half_t)(acc[u][d][2] * inv), (half_t)(acc[u][d][3] * inv)};
+      *(u2*)(orow + d * 16) = (u2){as_u32(lo), as_u32(hi)};
+    }
+  }
+}
+
 }  // namespace afx
 
 using namespace afx;
@@ -548,12 +667,18 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
   a.scale_log2 = scale * 1.4426950408889634f;
   a.tiles = (M + kPQ - 1) / kPQ;
   a.xcd_map = Hkv % 8 == 0;
+  // Default: form 4 while the causal part dominates (pos0 < M: tile work grows with the tile index, and
+  // splitting each tile's keys evens the CUs out), form 3 once the cached prefix does (a later chunk,
+  // whose tiles differ little and which form 4's single barrier domain per CU slows by ~6%).
   const char* fe = getenv("AFX_PREFILL_ATTN_FORM");   // read per call: tests compare the forms in one process
-  const int form_env = fe ? atoi(fe) : 3;
+  const int form_env = fe ? atoi(fe) : (pos0 < M ? 4 : 3);
   if (form_env == 1) {                             // single-buffered
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.tiles, Hq), dim3(256), 0, (hipStream_t)stream, a);
   } else if (form_env == 2 || ldo % 4 != 0 || ((uintptr_t)o & 7) != 0) {   // pipelined, bit-identical to form 1
     hipLaunchKernelGGL(prefill_attn_kernel2, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
+  } else if (form_env == 4) {                      // form 3 with each tile's keys split over two halves
+    a.tiles = (M + kPQ3 - 1) / kPQ3;
+    hipLaunchKernelGGL(prefill_attn_kernel4, dim3(a.tiles * Hq), dim3(512), 0, (hipStream_t)stream, a);
   } else {                                         // transposed scores, 128 queries per workgroup (8-byte stores)
     a.tiles = (M + kPQ3 - 1) / kPQ3;
     const char* oe = getenv("AFX_PREFILL_ATTN_ORDER");

@@ -128,8 +128,10 @@ def _env(name, value):
                                                 (1, 5, 4, 2, 64), (640, 100, 16, 8, 800)])
 def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     """Every prefill-attention form against the oracle: single-buffered (1), pipelined (2, the same
-    arithmetic: bit-identical to 1), transposed scores (3, the default) with both tile orders, on
-    grids with several workgroup rounds, the XCD mapping (Hkv = 8) and without it (Hkv = 2)."""
+    arithmetic: bit-identical to 1), transposed scores (3, the default) with both tile orders, and 3
+    with each tile's keys split over two halves of the workgroup (4: a single-block tile whose first
+    half is empty, and queries that see no key of the second half), on grids with several workgroup
+    rounds, the XCD mapping (Hkv = 8) and without it (Hkv = 2)."""
     import torch
     from aneforge_amd import _kernels as Kn
     D = 128
@@ -146,7 +148,7 @@ def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     outs = {}
     old_f, old_o = _env("AFX_PREFILL_ATTN_FORM", None), _env("AFX_PREFILL_ATTN_ORDER", None)
     try:
-        for form, order in ((1, None), (2, None), (3, 0), (3, 1)):
+        for form, order in ((1, None), (2, None), (3, 0), (3, 1), (4, None)):
             _env("AFX_PREFILL_ATTN_FORM", form)
             _env("AFX_PREFILL_ATTN_ORDER", order)
             say(f"prefill_attn form={form} order={order} M={M} pos0={pos0} Hq={Hq} Hkv={Hkv}")

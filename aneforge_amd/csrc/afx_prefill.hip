@@ -353,9 +353,48 @@ __device__ __forceinline__ void kv_stage3(const KvRegs& r, unsigned char* Ks, un
   }
 }
 
+// Row-major V stages for the transposing LDS reads (ds_read_b64_tr_b16): V rows of 256 bytes,
+// unpadded, their 16-byte chunks permuted by an even XOR of the row (chunk c of row r at
+// c ^ 2 (r & 7)).  One operand read takes 32 bytes from each of 16 rows; the XOR puts rows with
+// r & 7 = 0..7 on 8 distinct 32-byte bank ranges, and spreads the 16-byte staging stores of 8
+// consecutive rows at one logical chunk over 8 distinct chunks.
+constexpr int kVRow = kPD * 2;
+__device__ __forceinline__ int vsw(int row, int ch) { return row * kVRow + ((ch ^ ((row & 7) << 1)) << 4); }
+
+// K and V rows alike: 16 lanes per key row, consecutive 16-byte chunks; K first, so the scores
+// can start while V is in flight.
+__device__ __forceinline__ void kv_load_rm(const PrefillAttnArgs& a, const half_t* kbase, const half_t* vbase,
+                                           int key0, int tid, KvRegs& r) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    const int key = key0 + row < a.Mmax ? key0 + row : a.Mmax - 1;   // past the cache: masked in attn_block3
+    r.k[i] = *(const u4*)(kbase + (size_t)key * kPD + ch * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    const int key = key0 + row < a.Mmax ? key0 + row : a.Mmax - 1;
+    r.v[i] = *(const u4*)(vbase + (size_t)key * kPD + ch * 8);
+  }
+}
+__device__ __forceinline__ void kv_stage_rm(const KvRegs& r, unsigned char* Ks, unsigned char* Vs, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 256 * i, row = c >> 4, ch = c & 15;
+    *(u4*)(Ks + row * kKStride + ch * 16) = r.k[i];
+    *(u4*)(Vs + vsw(row, ch)) = r.v[i];
+  }
+}
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
 // EMPTY: a query may have seen no key yet (a block range that starts past its position); its
 // running maximum is then -inf and the exponents take 0 in its place, so its probabilities are 0.
-template <bool EMPTY = false>
+// VTR: V staged row-major (kv_stage_rm) and read through ds_read_b64_tr_b16, else V^T (kv_stage3).
+template <bool EMPTY = false, bool VTR = false>
 __device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsigned char* Ks, const unsigned char* Vt,
                                             const h8 (&qf)[2][4], const int (&qp)[2], int key0, int mwpos, int fr,
                                             int fg, f4 (&acc)[2][8], float (&mrow)[2], float (&lrow)[2]) {
@@ -429,15 +468,29 @@ __device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsi
   for (int d = 0; d < 8; ++d)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const h8 vf = __builtin_bit_cast(h8, *(const u4*)(Vt + (d * 16 + fr) * kVStride + (ks * 32 + 8 * fg) * 2));
+      h8 vf;
+      if constexpr (VTR) {
+        // within each 16-lane group the read hands lane i element j of lane i / 4 + 4 j's 8 bytes:
+        // lane (fr, fg) asks for dims 16 d + 4 (fr & 3) .. + 3 of key 32 ks + 4 fg + fr / 4 and
+        // receives dim 16 d + fr of keys 32 ks + 4 fg + 0..3; the second read takes keys + 16
+        const int row = ks * 32 + 4 * fg + (fr >> 2);
+        unsigned char* const vp = (unsigned char*)Vt + vsw(row, 2 * d + ((fr >> 1) & 1)) + (fr & 1) * 8;
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)vp);
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vp + 16 * kVRow));
+        vf = __builtin_bit_cast(h8, (v8s){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+      } else {
+        vf = __builtin_bit_cast(h8, *(const u4*)(Vt + (d * 16 + fr) * kVStride + (ks * 32 + 8 * fg) * 2));
+      }
 #pragma unroll
       for (int u = 0; u < 2; ++u) acc[u][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[u][ks], acc[u][d], 0, 0, 0);
     }
 }
 
+template <bool VTR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel3(PrefillAttnArgs a) {
+  constexpr int VB = VTR ? kPK * kVRow : kPD * kVStride;   // bytes of one V stage
   __shared__ __align__(16) unsigned char Ks[2][kPK * kKStride];
-  __shared__ __align__(16) unsigned char Vt[2][kPD * kVStride];
+  __shared__ __align__(16) unsigned char Vt[2][VB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fg = lane >> 4;
   const int id = blockIdx.x, G = a.Hq / a.Hkv;
@@ -465,7 +518,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const half_t* kbase = a.k + (size_t)kvh * a.kv_hs;
   const half_t* vbase = a.v + (size_t)kvh * a.kv_hs;
   KvRegs r;
-  kv_load(a, kbase, vbase, 0, tid, lane, wave, r);
+  auto load = [&](int key0) {
+    if constexpr (VTR) kv_load_rm(a, kbase, vbase, key0, tid, r);
+    else kv_load(a, kbase, vbase, key0, tid, lane, wave, r);
+  };
+  auto stage = [&](unsigned char* K, unsigned char* V) {
+    if constexpr (VTR) kv_stage_rm(r, K, V, tid);
+    else kv_stage3(r, K, V, tid, lane, wave);
+  };
+  load(0);
   h8 qf[2][4];
   int qp[2];
 #pragma unroll
@@ -482,14 +543,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[u][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
   float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.0f, 0.0f};
-  kv_stage3(r, Ks[0], Vt[0], tid, lane, wave);
+  stage(Ks[0], Vt[0]);
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int s = kb & 1;
-    if (kb + 1 < nkb) kv_load(a, kbase, vbase, (kb + 1) * kPK, tid, lane, wave, r);
+    if (kb + 1 < nkb) load((kb + 1) * kPK);
     if (kb * kPK <= wlast)                       // blocks wholly past the wavefront's queries are skipped
-      attn_block3(a, Ks[s], Vt[s], qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow);
-    if (kb + 1 < nkb) kv_stage3(r, Ks[s ^ 1], Vt[s ^ 1], tid, lane, wave);
+      attn_block3<false, VTR>(a, Ks[s], Vt[s], qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow);
+    if (kb + 1 < nkb) stage(Ks[s ^ 1], Vt[s ^ 1]);
     __syncthreads();
   }
   // o = O^T / l: lane holds dims 16 d + 4 fg .. + 3 of query mw + 16 u + fr
@@ -517,11 +578,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // per SIMD as in form 3), and the second half's running maxima, sums and accumulators are merged
 // into the first's through LDS.  No tile costs more than half the longest key range, and with the
 // tiles dispatched heaviest first over two rounds of workgroups the CUs finish together.
-constexpr int kKB4 = kPK * kKStride, kVB4 = kPD * kVStride;   // bytes of one K stage, one V^T stage
+constexpr int kKB4 = kPK * kKStride;     // bytes of one K stage
 constexpr int kX4 = 68;                  // floats per lane handed over: 2 x 8 accumulator f4s + 2 maxima + 2 sums
 
+template <bool VTR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel4(PrefillAttnArgs a) {
-  __shared__ __align__(16) unsigned char lds[4 * kKB4 + 4 * kVB4];   // K stages [half][2], then V^T stages [half][2]
+  constexpr int kVB4 = VTR ? kPK * kVRow : kPD * kVStride;   // bytes of one V stage
+  __shared__ __align__(16) unsigned char lds[4 * kKB4 + 4 * kVB4];   // K stages [half][2], then V stages [half][2]
   static_assert(4 * 64 * kX4 * 4 <= 4 * kKB4, "the handover fits in the K stages");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hf = wave >> 2, w4 = wave & 3, htid = tid & 255;   // half, wavefront and thread within it
@@ -551,7 +614,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const half_t* kbase = a.k + (size_t)kvh * a.kv_hs;
   const half_t* vbase = a.v + (size_t)kvh * a.kv_hs;
   KvRegs r;
-  if (kb0 < kb1) kv_load(a, kbase, vbase, kb0 * kPK, htid, lane, w4, r);
+  auto load = [&](int key0) {
+    if constexpr (VTR) kv_load_rm(a, kbase, vbase, key0, htid, r);
+    else kv_load(a, kbase, vbase, key0, htid, lane, w4, r);
+  };
+  auto stage = [&](unsigned char* K, unsigned char* V) {
+    if constexpr (VTR) kv_stage_rm(r, K, V, htid);
+    else kv_stage3(r, K, V, htid, lane, w4);
+  };
+  if (kb0 < kb1) load(kb0 * kPK);
   h8 qf[2][4];
   int qp[2];
 #pragma unroll
@@ -568,15 +639,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[u][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
   float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.0f, 0.0f};
-  if (kb0 < kb1) kv_stage3(r, Kh, Vh, htid, lane, w4);
+  if (kb0 < kb1) stage(Kh, Vh);
   __syncthreads();
   for (int i = 0; i < trips; ++i) {
     const int kb = kb0 + i, s = i & 1;
     const bool more = kb + 1 < kb1;              // uniform over the half
-    if (more) kv_load(a, kbase, vbase, (kb + 1) * kPK, htid, lane, w4, r);
+    if (more) load((kb + 1) * kPK);
     if (kb < kb1 && kb * kPK <= wlast)           // blocks wholly past the wavefront's queries are skipped
-      attn_block3<true>(a, Kh + s * kKB4, Vh + s * kVB4, qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow);
-    if (more) kv_stage3(r, Kh + (s ^ 1) * kKB4, Vh + (s ^ 1) * kVB4, htid, lane, w4);
+      attn_block3<true, VTR>(a, Kh + s * kKB4, Vh + s * kVB4, qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow);
+    if (more) stage(Kh + (s ^ 1) * kKB4, Vh + (s ^ 1) * kVB4);
     __syncthreads();
   }
   // the second half hands over through the (now idle) K stages: lane-major, so the accesses are
@@ -676,14 +747,19 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.tiles, Hq), dim3(256), 0, (hipStream_t)stream, a);
   } else if (form_env == 2 || ldo % 4 != 0 || ((uintptr_t)o & 7) != 0) {   // pipelined, bit-identical to form 1
     hipLaunchKernelGGL(prefill_attn_kernel2, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
-  } else if (form_env == 4) {                      // form 3 with each tile's keys split over two halves
+  } else {
     a.tiles = (M + kPQ3 - 1) / kPQ3;
-    hipLaunchKernelGGL(prefill_attn_kernel4, dim3(a.tiles * Hq), dim3(512), 0, (hipStream_t)stream, a);
-  } else {                                         // transposed scores, 128 queries per workgroup (8-byte stores)
-    a.tiles = (M + kPQ3 - 1) / kPQ3;
-    const char* oe = getenv("AFX_PREFILL_ATTN_ORDER");
-    a.order = oe ? atoi(oe) : 1;
-    hipLaunchKernelGGL(prefill_attn_kernel3, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
+    const char* ve = getenv("AFX_PREFILL_ATTN_VTR");   // V staged row-major + transposing reads (1) or V^T (0)
+    const bool vtr = ve ? atoi(ve) != 0 : true;
+    if (form_env == 4) {                           // form 3 with each tile's keys split over two halves
+      auto kfn = vtr ? prefill_attn_kernel4<true> : prefill_attn_kernel4<false>;
+      hipLaunchKernelGGL(kfn, dim3(a.tiles * Hq), dim3(512), 0, (hipStream_t)stream, a);
+    } else {                                       // transposed scores, 128 queries per workgroup (8-byte stores)
+      const char* oe = getenv("AFX_PREFILL_ATTN_ORDER");
+      a.order = oe ? atoi(oe) : 1;
+      auto kfn = vtr ? prefill_attn_kernel3<true> : prefill_attn_kernel3<false>;
+      hipLaunchKernelGGL(kfn, dim3(a.tiles * Hq), dim3(256), 0, (hipStream_t)stream, a);
+    }
   }
   return check_launch("afx_prefill_attn");
 }

@@ -128,7 +128,7 @@ def _env(name, value):
                                                 (1, 5, 4, 2, 64), (640, 100, 16, 8, 800)])
 def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     """Every prefill-attention form against the oracle: single-buffered (1), pipelined (2, the same
-    arithmetic: bit-identical to 1), transposed scores (3, the default) with both tile orders, and 3
+    arithmetic: bit-identical to 1), transposed scores (3) with both tile orders and both V stagings, and 3
     with each tile's keys split over two halves of the workgroup (4: a single-block tile whose first
     half is empty, and queries that see no key of the second half), on grids with several workgroup
     rounds, the XCD mapping (Hkv = 8) and without it (Hkv = 2)."""
@@ -147,20 +147,27 @@ def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     want = want[0].transpose(1, 0, 2).reshape(M, Hq * D)
     outs = {}
     old_f, old_o = _env("AFX_PREFILL_ATTN_FORM", None), _env("AFX_PREFILL_ATTN_ORDER", None)
+    old_v = _env("AFX_PREFILL_ATTN_VTR", None)
     try:
-        for form, order in ((1, None), (2, None), (3, 0), (3, 1), (4, None)):
+        for form, order, vtr in ((1, None, None), (2, None, None), (3, 0, None), (3, 1, None), (3, 1, 0),
+                                 (4, None, None), (4, None, 0)):
             _env("AFX_PREFILL_ATTN_FORM", form)
             _env("AFX_PREFILL_ATTN_ORDER", order)
-            say(f"prefill_attn form={form} order={order} M={M} pos0={pos0} Hq={Hq} Hkv={Hkv}")
+            _env("AFX_PREFILL_ATTN_VTR", vtr)
+            say(f"prefill_attn form={form} order={order} vtr={vtr} M={M} pos0={pos0} Hq={Hq} Hkv={Hkv}")
             o = torch.zeros((M, Hq * D), dtype=torch.float16, device="cuda")
             Kn.prefill_attn(dev(q), dev(Kc), dev(Vc), o, pos0, Hq, Hkv)
-            outs[(form, order)] = host(o)
-            check_f16(outs[(form, order)], want, what=f"prefill attention form {form} order {order}")
+            outs[(form, order, vtr)] = host(o)
+            check_f16(outs[(form, order, vtr)], want, what=f"prefill attention form {form} order {order} vtr {vtr}")
     finally:
         _env("AFX_PREFILL_ATTN_FORM", old_f)
         _env("AFX_PREFILL_ATTN_ORDER", old_o)
-    np.testing.assert_array_equal(outs[(1, None)], outs[(2, None)])
-    np.testing.assert_array_equal(outs[(3, 0)], outs[(3, 1)])
+        _env("AFX_PREFILL_ATTN_VTR", old_v)
+    np.testing.assert_array_equal(outs[(1, None, None)], outs[(2, None, None)])
+    np.testing.assert_array_equal(outs[(3, 0, None)], outs[(3, 1, None)])
+    # the V operand's staging layout (row-major + transposing reads, or V^T) changes no arithmetic
+    np.testing.assert_array_equal(outs[(3, 1, None)], outs[(3, 1, 0)])
+    np.testing.assert_array_equal(outs[(4, None, None)], outs[(4, None, 0)])
 
 
 @pytest.mark.parametrize("fmt", ["int8", "fp16"])

@@ -71,6 +71,9 @@ __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
 // fragment reads); buffer loads with the step's K offset in a scalar register; the K loop unrolled
 // by two so the LDS stage offsets are constants.  Together they cut the int8 loop's VALU from about
 // 115 to 41 instructions per K step and wavefront.  (1: form 2's layout with form 0's loads.)
+// 3: form 2 with the second half-step's fragments read from LDS between the first half-step's
+// MFMAs (each A fragment once its two products are issued), so a K step waits on LDS once, not
+// twice, at the same register count (three wavefronts per SIMD).
 template <int WL> struct WaveLayout { static constexpr int MT = WL ? 8 : 4, NT = WL ? 2 : 4; };
 template <int V> struct Stage { static constexpr int value = V; };
 
@@ -177,14 +180,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   // per-lane offset fixed and the step's K offset a scalar, so a step's loads take no address VALU
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes), wr = make_rsrc(a.w, a.w_bytes);
   int xo[4], wo[WC];
-  if constexpr (WL == 2) {
+  if constexpr (WL >= 2) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) xo[i] = (int)((const unsigned char*)xp[i] - (const unsigned char*)a.x);
 #pragma unroll
     for (int i = 0; i < WC; ++i) wo[i] = (int)(wp[i] - (const unsigned char*)a.w);
   }
   auto load = [&](int kt) {
-    if constexpr (WL == 2) {
+    if constexpr (WL >= 2) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         ra[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], kt * (kGBK * 2), 0));
@@ -230,6 +233,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   auto kstep = [&](int kt, auto st) {
     const int s = decltype(st)::value >= 0 ? decltype(st)::value : (kt & 1);
     if (kt + 1 < nk) load(kt + 1);                 // next stage streams during this stage's MFMAs
+    if constexpr (WL == 3) {
+      // the second half-step's fragments are read between the first half-step's MFMAs, each A fragment
+      // as soon as its two products have been issued, so only the first half-step waits on LDS
+      typedef typename std::conditional<kCodes, u2, u4>::type Raw;
+      auto read_a = [&](int kk, int i) {
+        return __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(i * 16 + fr, kk * 4 + fg)));
+      };
+      auto read_b = [&](int kk, int j) -> Raw {
+        const int br = wn * NT * 16 + j * 16 + fr;
+        if constexpr (kCodes) return *(const u2*)(Bs[s] + swz8(br, kk * 4 + fg));
+        else return *(const u4*)(Bs[s] + swz16(br, kk * 4 + fg));
+      };
+      auto conv_b = [&](int kk, int j, Raw r) -> h8 {
+        if constexpr (FMT == FMT_I8) {
+          return i8x8_to_h8(r);
+        } else if constexpr (FMT == FMT_BW) {
+          const h2 sp2 = as_h2(Ss[s][wn * NT * 16 + j * 16 + fr]);
+          const half_t sc = kk ? sp2.y : sp2.x;
+          const h8 s8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+          return i8x8_to_h8(r) * s8;
+        } else {
+          return __builtin_bit_cast(h8, r);
+        }
+      };
+      h8 af[MT];
+      Raw bq[NT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) af[i] = read_a(0, i);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) bq[j] = read_b(0, j);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        h8 bf[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) bf[j] = conv_b(kk, j, bq[j]);
+        if (kk == 0)
+#pragma unroll
+          for (int j = 0; j < NT; ++j) bq[j] = read_b(1, j);
+        if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          if (kk == 0) af[i] = read_a(1, i);
+        }
+        if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
+      }
+    } else {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       h8 af[MT], bf[NT];
@@ -261,10 +312,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
       if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
     }
+    }
     if (kt + 1 < nk) stage(s ^ 1);                 // the other stage was last read before the previous barrier
     __syncthreads();
   };
-  if constexpr (WL == 2) {                         // unrolled by two: the stage offsets are constants
+  if constexpr (WL >= 2) {                         // unrolled by two: the stage offsets are constants
     for (int kt = 0; kt < nk; kt += 2) {
       kstep(kt, Stage<0>{});
       if (kt + 1 < nk) kstep(kt + 1, Stage<1>{});
@@ -316,19 +368,25 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   const int gn_env = ge ? atoi(ge) : 8;
   a.gn = gn_env > 0 ? gn_env : 0;
   if (a.gn > 0) a.per_xcd = ((a.tiles_n + 7) / 8) * a.tiles_m;   // the largest XCD range
-  // kernel form: 2 for int8 codes, 0 for fp16 weights (the faster of the two on each format at the
-  // 7B prefill shapes; outputs are bit-identical); AFX_GEMM_WL=0|2 overrides.  Form 2 addresses X and
-  // W with 31-bit buffer offsets, so larger operands take form 0.
-  static int wl_env = -2;
-  if (wl_env == -2) {
-    const char* e = getenv("AFX_GEMM_WL");
-    wl_env = e ? atoi(e) : -1;
-  }
+  // kernel form: 3 for int8 codes, 2 for blockwise, 0 for fp16 weights (the fastest on each format at
+  // the 7B prefill shapes; outputs are bit-identical): int8 at M = 2048 form 2 -> 3 QKV 874 -> 930, o-proj
+  // 728 -> 769, gate/up 966 -> 994, down 850 -> 922 TFLOP/s; blockwise even; fp16 form 3 ~25% slower.
+  // AFX_GEMM_WL=0|2|3 overrides.  Forms 2 and 3 address X and W with 31-bit buffer offsets, so larger
+  // operands take form 0.
+  const char* we = getenv("AFX_GEMM_WL");           // read per call, like AFX_GEMM_GN
+  const int wl_env = we ? atoi(we) : -1;
+  const int wl = wl_env >= 0 ? wl_env : (fmt == FMT_I8 ? 3 : fmt == FMT_BW ? 2 : 0);
   const long long xb = ((long long)(M - 1) * ldx + K) * 2;
   const long long wb = (long long)N * K * (fmt == FMT_F16 ? 2 : 1);
-  const bool form2 = (wl_env == 2 || (wl_env != 0 && fmt != FMT_F16)) && xb < (1ll << 31) && wb < (1ll << 31);
+  const bool form2 = (wl == 2 || wl == 3) && xb < (1ll << 31) && wb < (1ll << 31);
   gemm_fn fn;
-  if (form2) {
+  if (form2 && wl == 3) {
+    a.x_bytes = (int)xb;
+    a.w_bytes = (int)wb;
+    if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU, 3> : gemm_kernel<FMT_I8, EG_PLAIN, 3>;
+    else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU, 3> : gemm_kernel<FMT_BW, EG_PLAIN, 3>;
+    else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU, 3> : gemm_kernel<FMT_F16, EG_PLAIN, 3>;
+  } else if (form2) {
     a.x_bytes = (int)xb;
     a.w_bytes = (int)wb;
     if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU, 2> : gemm_kernel<FMT_I8, EG_PLAIN, 2>;

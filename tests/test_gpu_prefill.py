@@ -170,11 +170,13 @@ def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     np.testing.assert_array_equal(outs[(4, None, None)], outs[(4, None, 0)])
 
 
-@pytest.mark.parametrize("fmt", ["int8", "fp16"])
+@pytest.mark.parametrize("fmt", ["int8", "fp16", "blockwise"])
 @pytest.mark.parametrize("M,N,K", [(300, 2304, 256), (1000, 1280, 512), (2048, 4096, 128)])
 def test_gemm_tile_orders_bit_identical(fmt, M, N, K):
-    """The grouped tile order (default), other group sizes and the contiguous order (AFX_GEMM_GN=0)
-    compute every output tile the same way: bit-identical, and to the oracle's bar."""
+    """The grouped tile order (default), other group sizes and the contiguous order (AFX_GEMM_GN=0),
+    and every kernel form (AFX_GEMM_WL: 0 the 2 x 2 layout, 2 the 1 x 4 layout, 3 the 1 x 4 layout
+    with the second half-step's fragments read during the first's products) compute every output
+    tile the same way: bit-identical, and to the oracle's bar."""
     import torch
     from aneforge_amd import _kernels as Kn
     rng = np.random.default_rng(M + N + K)
@@ -182,14 +184,16 @@ def test_gemm_tile_orders_bit_identical(fmt, M, N, K):
     x = rng.standard_normal((M, K)).astype(np.float16)
     want = ref.r16(np.asarray(x, np.float64) @ np.asarray(Wf, np.float64).T)
     outs = []
-    old = _env("AFX_GEMM_GN", None)
+    old, old_wl = _env("AFX_GEMM_GN", None), _env("AFX_GEMM_WL", None)
     try:
-        for gn in (None, 0, 3, 16):
+        for gn, wl in ((None, None), (0, None), (3, None), (16, None), (None, 0), (None, 2), (None, 3)):
             _env("AFX_GEMM_GN", gn)
-            say(f"gemm tile order GN={gn} {fmt} M={M} N={N} K={K}")
+            _env("AFX_GEMM_WL", wl)
+            say(f"gemm tile order GN={gn} WL={wl} {fmt} M={M} N={N} K={K}")
             outs.append(host(Kn.gemm(fmt, w, s, dev(x), epi="f16")))
     finally:
         _env("AFX_GEMM_GN", old)
+        _env("AFX_GEMM_WL", old_wl)
     check_f16(outs[0], want, what=f"gemm {fmt} grouped order")
     for o in outs[1:]:
         np.testing.assert_array_equal(o, outs[0])

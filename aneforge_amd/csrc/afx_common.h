@@ -167,6 +167,29 @@ __device__ __forceinline__ float gelu_tanh(float g) {
 // GeGLU (gelu = 1; a uniform flag, so the two share every kernel instance).
 __device__ __forceinline__ float glu_act(bool gelu, float g) { return gelu ? gelu_tanh(g) : silu(g); }
 
+// v_permlane16_swap(a, b) exchanges the odd 16-lane rows of a with the even rows of b, and
+// v_permlane32_swap the upper 32 lanes of a with the lower 32 lanes of b.  With b a copy of a,
+// afterwards a and b hold each row (half) and its partner row (half), so op(a, b) reduces over
+// lane pairs 16 (32) apart in every lane.  Issued as inline assembly on two distinct registers
+// (the s_nop covers the VALU-write-then-permlane hazard): this compiler's builtin returns the
+// same half twice when its two results are combined.
+__device__ __forceinline__ void swap16(float v, float& r0, float& r1) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b;
+  asm volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "=&v"(b));
+  r0 = __builtin_bit_cast(float, a);
+  r1 = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ void swap32(float v, float& r0, float& r1) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b;
+  asm volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "=&v"(b));
+  r0 = __builtin_bit_cast(float, a);
+  r1 = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float swap16_sum(float v) { float a, b; swap16(v, a, b); return a + b; }
+__device__ __forceinline__ float swap32_sum(float v) { float a, b; swap32(v, a, b); return a + b; }
+__device__ __forceinline__ float swap16_max(float v) { float a, b; swap16(v, a, b); return fmaxf(a, b); }
+__device__ __forceinline__ float swap32_max(float v) { float a, b; swap32(v, a, b); return fmaxf(a, b); }
+
 // Greedy-pick summaries {largest value, its index (int bits), second largest, largest magnitude}
 // of two disjoint index ranges, merged: the larger first value wins, the lower index on an exact
 // tie, and the loser's first value competes for second place (an exact tie makes them equal).

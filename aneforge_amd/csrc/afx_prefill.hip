@@ -325,14 +325,10 @@ __device__ __forceinline__ int vt_pos(int key) {   // staged position of key (0.
   const int k = key & 31;
   return (key & 32) + 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3);
 }
-__device__ __forceinline__ float xor_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
-}
-__device__ __forceinline__ float xor_sum(float v) {
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
-}
+// over the lanes l, l ^ 16, l ^ 32, l ^ 48 (one query's four lanes), through the permlane swaps rather
+// than LDS permutes: (v_l op v_l^16) op (v_l^32 op v_l^48) in every lane
+__device__ __forceinline__ float xor_max(float v) { return swap32_max(swap16_max(v)); }
+__device__ __forceinline__ float xor_sum(float v) { return swap32_sum(swap16_sum(v)); }
 __device__ __forceinline__ void kv_stage3(const KvRegs& r, unsigned char* Ks, unsigned char* Vt, int tid, int lane,
                                           int wave) {
 #pragma unroll

@@ -42,8 +42,8 @@ __global__ void qkv_split_rope_kernel(const half_t* __restrict__ qkv, int ldqkv,
     if (rope) {
       const float c0 = (float)cos_t[(size_t)p * dh + d], s0 = (float)sin_t[(size_t)p * dh + d];
       const float c1 = (float)cos_t[(size_t)p * dh + d + half], s1 = (float)sin_t[(size_t)p * dh + d + half];
-      o0 = v0 * c0 - v1 * s0;
-      o1 = v1 * c1 + v0 * s1;
+      o0 = __builtin_fmaf(v0, c0, -(v1 * s0));   // the contraction spelled out: both kernels round alike
+      o1 = __builtin_fmaf(v1, c1, v0 * s1);
     }
     half_t* dst = isk ? kc + (size_t)head * kv_hs + (size_t)p * dh : q + (size_t)m * ldq + (size_t)head * dh;
     dst[d] = (half_t)o0;
@@ -54,6 +54,54 @@ __global__ void qkv_split_rope_kernel(const half_t* __restrict__ qkv, int ldqkv,
     half_t* dst = vc + (size_t)head * kv_hs + (size_t)p * dh + d;
     dst[0] = (half_t)v0;
     dst[1] = (half_t)v1;
+  }
+}
+
+// The same split with 8 packed rows (4 RoPE pairs, or 8 V dims) per thread: one 16-byte load, two
+// 8-byte stores (dims d .. d + 3 and d + dh/2 .. + 3) or one 16-byte store, and 8-byte table loads;
+// the per-element arithmetic is the scalar kernel's.  Needs dh % 8 == 0 and 16 / 8-byte aligned rows.
+__global__ void qkv_split_rope_kernel8(const half_t* __restrict__ qkv, int ldqkv, int M, int nq, int nk, int dh,
+                                       const half_t* __restrict__ cos_t, const half_t* __restrict__ sin_t,
+                                       int pos0, int rope, half_t* __restrict__ q, int ldq,
+                                       half_t* __restrict__ kc, half_t* __restrict__ vc, long long kv_hs) {
+  const int chunks = (nq + 2 * nk) >> 3;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * chunks) return;
+  const int m = (int)(i / chunks), c = (int)(i - (long long)m * chunks);
+  const int col0 = 8 * c, p = pos0 + m;
+  const u4 raw = *(const u4*)(qkv + (size_t)m * ldqkv + col0);
+  if (col0 < nq + nk) {
+    const bool isk = col0 >= nq;
+    const int rl = isk ? col0 - nq : col0;
+    const int head = rl / dh, d = (rl - head * dh) >> 1, half = dh >> 1;   // pairs d .. d + 3
+    const h2 pr[4] = {as_h2(raw.x), as_h2(raw.y), as_h2(raw.z), as_h2(raw.w)};
+    half_t r0[4], r1[4];                         // dims d + j and d + dh/2 + j
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { r0[j] = pr[j].x; r1[j] = pr[j].y; }
+    if (rope) {
+      const u2 c0 = *(const u2*)(cos_t + (size_t)p * dh + d), c1 = *(const u2*)(cos_t + (size_t)p * dh + d + half);
+      const u2 s0 = *(const u2*)(sin_t + (size_t)p * dh + d), s1 = *(const u2*)(sin_t + (size_t)p * dh + d + half);
+      const h2 cc0[2] = {as_h2(c0.x), as_h2(c0.y)}, cc1[2] = {as_h2(c1.x), as_h2(c1.y)};
+      const h2 ss0[2] = {as_h2(s0.x), as_h2(s0.y)}, ss1[2] = {as_h2(s1.x), as_h2(s1.y)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v0 = (float)r0[j], v1 = (float)r1[j];
+        const float a0 = (float)(j & 1 ? cc0[j >> 1].y : cc0[j >> 1].x), b0 = (float)(j & 1 ? ss0[j >> 1].y : ss0[j >> 1].x);
+        const float a1 = (float)(j & 1 ? cc1[j >> 1].y : cc1[j >> 1].x), b1 = (float)(j & 1 ? ss1[j >> 1].y : ss1[j >> 1].x);
+        // each result rounded straight from the fma to fp16, as in the one-pair kernel and the decode
+        // epilogue (the fp16 conversion fused into the fma: not the fp32 result rounded again)
+        r0[j] = (half_t)__builtin_fmaf(v0, a0, -(v1 * b0));
+        r1[j] = (half_t)__builtin_fmaf(v1, a1, v0 * b1);
+      }
+    }
+    half_t* dst = isk ? kc + (size_t)head * kv_hs + (size_t)p * dh : q + (size_t)m * ldq + (size_t)head * dh;
+    const h2 l0 = {r0[0], r0[1]}, l1 = {r0[2], r0[3]}, u0 = {r1[0], r1[1]}, u1 = {r1[2], r1[3]};
+    *(u2*)(dst + d) = (u2){as_u32(l0), as_u32(l1)};
+    *(u2*)(dst + d + half) = (u2){as_u32(u0), as_u32(u1)};
+  } else {
+    const int rl = col0 - nq - nk;
+    const int head = rl / dh, d = rl - head * dh;
+    *(u4*)(vc + (size_t)head * kv_hs + (size_t)p * dh + d) = raw;
   }
 }
 
@@ -707,10 +755,16 @@ int afx_qkv_split_rope(const void* qkv, int ldqkv, int M, int nq, int nk, int dh
               "afx_qkv_split_rope: bad sizes");
   AFX_REQUIRE(pos0 >= 0 && pos0 + M <= kv_len && kv_hs >= (long long)kv_len * dh,
               "afx_qkv_split_rope: positions %d..%d outside the %d-row cache", pos0, pos0 + M - 1, kv_len);
-  const long long n = (long long)M * ((nq + 2 * nk) / 2);
-  hipLaunchKernelGGL(qkv_split_rope_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     (const half_t*)qkv, ldqkv, M, nq, nk, dh, (const half_t*)cos_tab, (const half_t*)sin_tab, pos0,
-                     rope, (half_t*)q, ldq, (half_t*)kcache, (half_t*)vcache, kv_hs);
+  // 8 packed rows per thread where every row, table and cache row is 16-byte aligned (AFX_QKV_SPLIT_VEC=0
+  // forces one pair per thread; the outputs are the same bits)
+  const char* ve = getenv("AFX_QKV_SPLIT_VEC");
+  const bool vec = (ve ? atoi(ve) != 0 : true) && dh % 8 == 0 && ldqkv % 8 == 0 && ldq % 8 == 0 && kv_hs % 8 == 0 &&
+                   (((uintptr_t)qkv | (uintptr_t)q | (uintptr_t)kcache | (uintptr_t)vcache) & 15) == 0 &&
+                   (!rope || (((uintptr_t)cos_tab | (uintptr_t)sin_tab) & 7) == 0);
+  const long long n = (long long)M * ((nq + 2 * nk) / (vec ? 8 : 2));
+  hipLaunchKernelGGL(vec ? qkv_split_rope_kernel8 : qkv_split_rope_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, (hipStream_t)stream, (const half_t*)qkv, ldqkv, M, nq, nk, dh, (const half_t*)cos_tab,
+                     (const half_t*)sin_tab, pos0, rope, (half_t*)q, ldq, (half_t*)kcache, (half_t*)vcache, kv_hs);
   return check_launch("afx_qkv_split_rope");
 }
 

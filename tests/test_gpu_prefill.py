@@ -65,28 +65,41 @@ def test_gemm_rejects_bad_shapes():
         Kn.gemm("fp16", w, None, x)
 
 
-@pytest.mark.parametrize("M,pos0", [(1, 0), (5, 3), (40, 17)])
-def test_qkv_split_rope_matches_oracle(M, pos0):
+@pytest.mark.parametrize("M,pos0,H,KV,dh", [(1, 0, 2, 1, 64), (5, 3, 2, 1, 64), (40, 17, 2, 1, 64),
+                                            (33, 20, 4, 2, 128), (7, 0, 3, 1, 8)])
+def test_qkv_split_rope_matches_oracle(M, pos0, H, KV, dh):
+    """The split against the oracle; 8 packed rows per thread (default) and one pair per thread
+    (AFX_QKV_SPLIT_VEC=0) write the same bits."""
     import torch
     from aneforge_amd import _blob
     from aneforge_amd import _kernels as Kn
-    H, KV, dh, Mmax = 2, 1, 64, 64
+    Mmax = 64
     rng = np.random.default_rng(M + 31 * pos0)
     nq, nk = H * dh, KV * dh
     nat = rng.standard_normal((M, nq + 2 * nk)).astype(np.float16)     # natural [q | k | v]
     pq, pk = _blob.rope_pair_order(H, dh), _blob.rope_pair_order(KV, dh)
     packed = np.concatenate([nat[:, :nq][:, pq], nat[:, nq:nq + nk][:, pk], nat[:, nq + nk:]], 1)
     cos, sin = ref.rope_tables(Mmax, dh)
-    q = torch.zeros((M, nq), dtype=torch.float16, device="cuda")
-    kc = torch.zeros((KV, Mmax, dh), dtype=torch.float16, device="cuda")
-    vc = torch.zeros((KV, Mmax, dh), dtype=torch.float16, device="cuda")
-    say(f"qkv_split_rope M={M} pos0={pos0}")
-    Kn.qkv_split_rope(dev(packed), nq, nk, dh, dev(cos), dev(sin), pos0, q, kc, vc)
+    outs = []
+    old = _env("AFX_QKV_SPLIT_VEC", None)
+    try:
+        for vec in (None, 0):
+            _env("AFX_QKV_SPLIT_VEC", vec)
+            q = torch.zeros((M, nq), dtype=torch.float16, device="cuda")
+            kc = torch.zeros((KV, Mmax, dh), dtype=torch.float16, device="cuda")
+            vc = torch.zeros((KV, Mmax, dh), dtype=torch.float16, device="cuda")
+            say(f"qkv_split_rope M={M} pos0={pos0} H={H} KV={KV} dh={dh} vec={vec}")
+            Kn.qkv_split_rope(dev(packed), nq, nk, dh, dev(cos), dev(sin), pos0, q, kc, vc)
+            outs.append((host(q), host(kc), host(vc)))
+    finally:
+        _env("AFX_QKV_SPLIT_VEC", old)
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a, b)
     p = np.arange(pos0, pos0 + M)
     want_q = ref.rope(nat[:, :nq].reshape(M, H, dh), cos[p][:, None], sin[p][:, None]).reshape(M, nq)
     want_k = ref.rope(nat[:, nq:nq + nk].reshape(M, KV, dh), cos[p][:, None], sin[p][:, None])
-    check_f16(host(q), want_q, what="q")
-    got_k, got_v = host(kc), host(vc)
+    got_q, got_k, got_v = outs[0]
+    check_f16(got_q, want_q, what="q")
     check_f16(got_k[:, pos0:pos0 + M].transpose(1, 0, 2), want_k, what="k rows")
     np.testing.assert_array_equal(got_v[:, pos0:pos0 + M].transpose(1, 0, 2),
                                   nat[:, nq + nk:].reshape(M, KV, dh))

@@ -74,7 +74,13 @@ __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
 // 3: form 2 with the second half-step's fragments read from LDS between the first half-step's
 // MFMAs (each A fragment once its two products are issued), so a K step waits on LDS once, not
 // twice, at the same register count (three wavefronts per SIMD).
-template <int WL> struct WaveLayout { static constexpr int MT = WL ? 8 : 4, NT = WL ? 2 : 4; };
+// 4: form 3's loop with eight wavefronts per workgroup (512 threads) in 2 x 4 tiles of 64 x 32, so a
+// CU holding two workgroups (the N = 4096 shapes: 512 tiles) runs four wavefronts per SIMD, not two.
+template <int WL> struct WaveLayout {
+  static constexpr int MT = WL == 4 ? 4 : (WL ? 8 : 4), NT = WL == 4 ? 2 : (WL ? 2 : 4);
+  static constexpr int NTH = WL == 4 ? 512 : 256;   // threads per workgroup
+  static constexpr int WPE = WL == 4 ? 4 : 3;        // wavefronts per SIMD the register budget is sized for
+};
 template <int V> struct Stage { static constexpr int value = V; };
 
 // Epilogue of a wavefront tile: lane holds rows 4 * fg + i of column fr in every 16 x 16 tile.
@@ -115,9 +121,11 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, const f4 (&acc)[MT
 }
 
 template <int FMT, int EG, int WL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_kernel(GemmArgs a) {
-  constexpr int MT = WaveLayout<WL>::MT, NT = WaveLayout<WL>::NT;
-  constexpr int WS = GemmW<FMT>::kStride, WR = GemmW<FMT>::kRow, WC = GemmW<FMT>::kChunks;
+__global__ __launch_bounds__(WaveLayout<WL>::NTH)
+__attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) void gemm_kernel(GemmArgs a) {
+  constexpr int MT = WaveLayout<WL>::MT, NT = WaveLayout<WL>::NT, NTH = WaveLayout<WL>::NTH;
+  constexpr int WS = GemmW<FMT>::kStride, WR = GemmW<FMT>::kRow, WC = GemmW<FMT>::kChunks * 256 / NTH;
+  constexpr int AC = 4 * 256 / NTH;                 // 16-byte activation chunks per thread and stage
   constexpr bool kCodes = FMT == FMT_I8 || FMT == FMT_BW;   // one byte per weight
   __shared__ __align__(16) unsigned char As[2][kGBM * kGAStride];
   __shared__ __align__(16) unsigned char Bs[2][kGBN * WS];
@@ -144,16 +152,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     m0 = (logical % a.tiles_m) * kGBM;
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = WL ? 0 : wave >> 1, wn = WL ? wave : wave & 1;
+  const int wm = WL == 4 ? wave >> 2 : (WL ? 0 : wave >> 1), wn = WL == 4 ? wave & 3 : (WL ? wave : wave & 1);
   const int M = a.M, N = a.N, K = a.K;
   const int nk = K / kGBK;
 
   // global-load roles: activations 4 x 16 B per thread (row c / 8, chunk c % 8), weights WC x 16 B
-  const half_t* xp[4];
-  int aoff[4];
+  const half_t* xp[AC];
+  int aoff[AC];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + 256 * i, r = c >> 3, ch = c & 7;
+  for (int i = 0; i < AC; ++i) {
+    const int c = tid + NTH * i, r = c >> 3, ch = c & 7;
     const int m = m0 + r < M ? m0 + r : M - 1;     // clamped rows are computed, not stored
     xp[i] = a.x + (size_t)m * a.ldx + ch * 8;
     aoff[i] = swz16(r, ch);
@@ -162,7 +170,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   int boff[WC], boff2[WC];
 #pragma unroll
   for (int i = 0; i < WC; ++i) {
-    const int c = tid + 256 * i;
+    const int c = tid + NTH * i;
     const int r = kCodes ? c >> 2 : c >> 3, ch = kCodes ? c & 3 : c & 7;
     const int n = n0 + r < N ? n0 + r : N - 1;
     wp[i] = (const unsigned char*)a.w + (size_t)n * (kCodes ? K : 2 * K) + ch * 16;
@@ -174,29 +182,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int n = n0 + (tid & 127) < N ? n0 + (tid & 127) : N - 1;
     sp = a.scale + (size_t)n * (K >> 5);
   }
-  u4 ra[4], rb[WC];
+  u4 ra[AC], rb[WC];
   uint32_t rs = 0;
   // WL 2: buffer loads over the whole X and W (byte offsets fit 31 bits, checked by the host), the
   // per-lane offset fixed and the step's K offset a scalar, so a step's loads take no address VALU
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes), wr = make_rsrc(a.w, a.w_bytes);
-  int xo[4], wo[WC];
+  int xo[AC], wo[WC];
   if constexpr (WL >= 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xo[i] = (int)((const unsigned char*)xp[i] - (const unsigned char*)a.x);
+    for (int i = 0; i < AC; ++i) xo[i] = (int)((const unsigned char*)xp[i] - (const unsigned char*)a.x);
 #pragma unroll
     for (int i = 0; i < WC; ++i) wo[i] = (int)(wp[i] - (const unsigned char*)a.w);
   }
   auto load = [&](int kt) {
     if constexpr (WL >= 2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < AC; ++i)
         ra[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], kt * (kGBK * 2), 0));
 #pragma unroll
       for (int i = 0; i < WC; ++i)
         rb[i] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[i], kt * WR, 0));
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ra[i] = *(const u4*)(xp[i] + (size_t)kt * kGBK);
+      for (int i = 0; i < AC; ++i) ra[i] = *(const u4*)(xp[i] + (size_t)kt * kGBK);
 #pragma unroll
       for (int i = 0; i < WC; ++i) rb[i] = *(const u4*)(wp[i] + (size_t)kt * WR);
     }
@@ -207,7 +215,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       if (tid < kGBN) Ss[s][tid] = rs;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(u4*)(As[s] + aoff[i]) = ra[i];
+    for (int i = 0; i < AC; ++i) *(u4*)(As[s] + aoff[i]) = ra[i];
 #pragma unroll
     for (int i = 0; i < WC; ++i) {
       if constexpr (kCodes) {                      // the two 8-byte units land apart after the swizzle
@@ -233,12 +241,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   auto kstep = [&](int kt, auto st) {
     const int s = decltype(st)::value >= 0 ? decltype(st)::value : (kt & 1);
     if (kt + 1 < nk) load(kt + 1);                 // next stage streams during this stage's MFMAs
-    if constexpr (WL == 3) {
+    if constexpr (WL >= 3) {
       // the second half-step's fragments are read between the first half-step's MFMAs, each A fragment
       // as soon as its two products have been issued, so only the first half-step waits on LDS
       typedef typename std::conditional<kCodes, u2, u4>::type Raw;
       auto read_a = [&](int kk, int i) {
-        return __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(i * 16 + fr, kk * 4 + fg)));
+        return __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(wm * MT * 16 + i * 16 + fr, kk * 4 + fg)));
       };
       auto read_b = [&](int kk, int j) -> Raw {
         const int br = wn * NT * 16 + j * 16 + fr;
@@ -368,19 +376,34 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   const int gn_env = ge ? atoi(ge) : 8;
   a.gn = gn_env > 0 ? gn_env : 0;
   if (a.gn > 0) a.per_xcd = ((a.tiles_n + 7) / 8) * a.tiles_m;   // the largest XCD range
-  // kernel form: 3 for int8 codes, 2 for blockwise, 0 for fp16 weights (the fastest on each format at
-  // the 7B prefill shapes; outputs are bit-identical): int8 at M = 2048 form 2 -> 3 QKV 874 -> 930, o-proj
-  // 728 -> 769, gate/up 966 -> 994, down 850 -> 922 TFLOP/s; blockwise even; fp16 form 3 ~25% slower.
-  // AFX_GEMM_WL=0|2|3 overrides.  Forms 2 and 3 address X and W with 31-bit buffer offsets, so larger
-  // operands take form 0.
+  // kernel form (outputs are bit-identical across forms): int8 codes take form 4 when the tiles fit two
+  // workgroups per CU (the N = 4096 shapes at M = 2048: o-proj 95.5 -> 85.9 us, down 208.6 -> 201.2 us
+  // against form 3) and form 3 otherwise (gate/up, QKV at M = 2048; form 2 -> 3 there: QKV 874 -> 930,
+  // gate/up 966 -> 994 TFLOP/s); blockwise takes form 2 (form 3 even, form 4 slower); fp16 weights form 0
+  // (forms 3 and 4 ~25% slower).  AFX_GEMM_WL=0|2|3|4 overrides.  Forms 2-4 address X and W with 31-bit
+  // buffer offsets, so larger operands take form 0.
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
   const char* we = getenv("AFX_GEMM_WL");           // read per call, like AFX_GEMM_GN
   const int wl_env = we ? atoi(we) : -1;
-  const int wl = wl_env >= 0 ? wl_env : (fmt == FMT_I8 ? 3 : fmt == FMT_BW ? 2 : 0);
+  const int wl = wl_env >= 0 ? wl_env : (fmt == FMT_I8 ? (a.tiles <= 2 * cus ? 4 : 3) : fmt == FMT_BW ? 2 : 0);
   const long long xb = ((long long)(M - 1) * ldx + K) * 2;
   const long long wb = (long long)N * K * (fmt == FMT_F16 ? 2 : 1);
-  const bool form2 = (wl == 2 || wl == 3) && xb < (1ll << 31) && wb < (1ll << 31);
+  const bool form2 = wl >= 2 && wl <= 4 && xb < (1ll << 31) && wb < (1ll << 31);
   gemm_fn fn;
-  if (form2 && wl == 3) {
+  int nth = 256;
+  if (form2 && wl == 4) {
+    a.x_bytes = (int)xb;
+    a.w_bytes = (int)wb;
+    nth = 512;
+    if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU, 4> : gemm_kernel<FMT_I8, EG_PLAIN, 4>;
+    else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU, 4> : gemm_kernel<FMT_BW, EG_PLAIN, 4>;
+    else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU, 4> : gemm_kernel<FMT_F16, EG_PLAIN, 4>;
+  } else if (form2 && wl == 3) {
     a.x_bytes = (int)xb;
     a.w_bytes = (int)wb;
     if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU, 3> : gemm_kernel<FMT_I8, EG_PLAIN, 3>;
@@ -397,7 +420,7 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
     else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU, 0> : gemm_kernel<FMT_BW, EG_PLAIN, 0>;
     else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU, 0> : gemm_kernel<FMT_F16, EG_PLAIN, 0>;
   }
-  hipLaunchKernelGGL(fn, dim3(8 * a.per_xcd), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(fn, dim3(8 * a.per_xcd), dim3(nth), 0, (hipStream_t)stream, a);
   return check_launch("afx_gemm");
 }
 

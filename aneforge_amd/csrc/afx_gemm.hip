@@ -76,10 +76,18 @@ __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
 // twice, at the same register count (three wavefronts per SIMD).
 // 4: form 3's loop with eight wavefronts per workgroup (512 threads) in 2 x 4 tiles of 64 x 32, so a
 // CU holding two workgroups (the N = 4096 shapes: 512 tiles) runs four wavefronts per SIMD, not two.
+// 6: form 4 with the barrier in the middle of the K step.  The first half-step's products run; the
+// next step's tiles are staged into the other stage and the step after next starts loading into the
+// freed staging registers (so global loads still get a full step); one barrier publishes the stage;
+// and the next step's first fragments are read between the second half-step's products.  No LDS read
+// then waits at the top of a step, which pays where a CU holds a single workgroup (tiles <= CUs).
+// (The same order over form 3's layout, "form 5", needed 168 VGPRs with spills and measured even with
+// form 3; it is not instantiated.)
 template <int WL> struct WaveLayout {
-  static constexpr int MT = WL == 4 ? 4 : (WL ? 8 : 4), NT = WL == 4 ? 2 : (WL ? 2 : 4);
-  static constexpr int NTH = WL == 4 ? 512 : 256;   // threads per workgroup
-  static constexpr int WPE = WL == 4 ? 4 : 3;        // wavefronts per SIMD the register budget is sized for
+  static constexpr bool W8 = WL == 4 || WL == 6;     // eight wavefronts in 2 x 4
+  static constexpr int MT = W8 ? 4 : (WL ? 8 : 4), NT = W8 ? 2 : (WL ? 2 : 4);
+  static constexpr int NTH = W8 ? 512 : 256;        // threads per workgroup
+  static constexpr int WPE = W8 ? 4 : 3;            // wavefronts per SIMD the register budget is sized for
 };
 template <int V> struct Stage { static constexpr int value = V; };
 
@@ -152,7 +160,8 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
     m0 = (logical % a.tiles_m) * kGBM;
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = WL == 4 ? wave >> 2 : (WL ? 0 : wave >> 1), wn = WL == 4 ? wave & 3 : (WL ? wave : wave & 1);
+  constexpr bool W8 = WaveLayout<WL>::W8;
+  const int wm = W8 ? wave >> 2 : (WL ? 0 : wave >> 1), wn = W8 ? wave & 3 : (WL ? wave : wave & 1);
   const int M = a.M, N = a.N, K = a.K;
   const int nk = K / kGBK;
 
@@ -235,6 +244,9 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
 
   load(0);
   stage(0);
+  if constexpr (WL == 6) {
+    if (nk > 1) load(1);                           // the mid-step form keeps one step of loads in flight
+  }
   __syncthreads();
   const int fr = lane & 15, fg = lane >> 4;
   // one K step on stage s: the next stage's loads, this stage's MFMAs, then the next stage staged
@@ -324,7 +336,76 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
     if (kt + 1 < nk) stage(s ^ 1);                 // the other stage was last read before the previous barrier
     __syncthreads();
   };
-  if constexpr (WL >= 2) {                         // unrolled by two: the stage offsets are constants
+  if constexpr (WL == 6) {
+    typedef typename std::conditional<kCodes, u2, u4>::type Raw;
+    auto read_a = [&](int s, int kk, int i) {
+      return __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(wm * MT * 16 + i * 16 + fr, kk * 4 + fg)));
+    };
+    auto read_b = [&](int s, int kk, int j) -> Raw {
+      const int br = wn * NT * 16 + j * 16 + fr;
+      if constexpr (kCodes) return *(const u2*)(Bs[s] + swz8(br, kk * 4 + fg));
+      else return *(const u4*)(Bs[s] + swz16(br, kk * 4 + fg));
+    };
+    auto conv_b = [&](int s, int kk, int j, Raw r) -> h8 {
+      if constexpr (FMT == FMT_I8) {
+        return i8x8_to_h8(r);
+      } else if constexpr (FMT == FMT_BW) {
+        const h2 sp2 = as_h2(Ss[s][wn * NT * 16 + j * 16 + fr]);
+        const half_t sc = kk ? sp2.y : sp2.x;
+        const h8 s8 = {sc, sc, sc, sc, sc, sc, sc, sc};
+        return i8x8_to_h8(r) * s8;
+      } else {
+        return __builtin_bit_cast(h8, r);
+      }
+    };
+    h8 af[MT];
+    Raw bq[NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) af[i] = read_a(0, 0, i);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) bq[j] = read_b(0, 0, j);
+    auto mstep = [&](int kt, auto st) {
+      constexpr int s = decltype(st)::value;
+      const bool more = kt + 1 < nk;               // uniform over the workgroup
+      h8 bf[NT];
+      // first half-step: kk 0's products, kk 1's fragments read between them
+#pragma unroll
+      for (int j = 0; j < NT; ++j) bf[j] = conv_b(s, 0, j, bq[j]);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) bq[j] = read_b(s, 1, j);
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        af[i] = read_a(s, 1, i);
+      }
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
+      // the next step's tiles into the other stage (last read before the previous barrier), the step
+      // after next loading into the freed registers, one barrier
+      if (more) stage(s ^ 1);
+      if (kt + 2 < nk) load(kt + 2);
+      if (more) __syncthreads();
+      // second half-step: kk 1's products, the next step's kk 0 fragments read between them
+#pragma unroll
+      for (int j = 0; j < NT; ++j) bf[j] = conv_b(s, 1, j, bq[j]);
+      if (more)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) bq[j] = read_b(s ^ 1, 0, j);
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        if (more) af[i] = read_a(s ^ 1, 0, i);
+      }
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
+    };
+    for (int kt = 0; kt < nk; kt += 2) {           // unrolled by two: the stage offsets are constants
+      mstep(kt, Stage<0>{});
+      if (kt + 1 < nk) mstep(kt + 1, Stage<1>{});
+    }
+  } else if constexpr (WL >= 2) {                  // unrolled by two: the stage offsets are constants
     for (int kt = 0; kt < nk; kt += 2) {
       kstep(kt, Stage<0>{});
       if (kt + 1 < nk) kstep(kt + 1, Stage<1>{});
@@ -376,12 +457,13 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   const int gn_env = ge ? atoi(ge) : 8;
   a.gn = gn_env > 0 ? gn_env : 0;
   if (a.gn > 0) a.per_xcd = ((a.tiles_n + 7) / 8) * a.tiles_m;   // the largest XCD range
-  // kernel form (outputs are bit-identical across forms): int8 codes take form 4 when the tiles fit two
-  // workgroups per CU (the N = 4096 shapes at M = 2048: o-proj 95.5 -> 85.9 us, down 208.6 -> 201.2 us
-  // against form 3) and form 3 otherwise (gate/up, QKV at M = 2048; form 2 -> 3 there: QKV 874 -> 930,
-  // gate/up 966 -> 994 TFLOP/s); blockwise takes form 2 (form 3 even, form 4 slower); fp16 weights form 0
-  // (forms 3 and 4 ~25% slower).  AFX_GEMM_WL=0|2|3|4 overrides.  Forms 2-4 address X and W with 31-bit
-  // buffer offsets, so larger operands take form 0.
+  // kernel form (outputs are bit-identical across forms): int8 codes take form 6 when the tiles fit one
+  // workgroup per CU (N = 4096 at M = 1000: o-proj 57.2 -> 53.3 us, down 130.3 -> 120.9 us against form
+  // 4), form 4 when they fit two (the N = 4096 shapes at M = 2048: o-proj 95.5 -> 85.9 us, down 208.6 ->
+  // 201.2 us against form 3) and form 3 otherwise (gate/up, QKV at M = 2048; form 2 -> 3 there: QKV 874 ->
+  // 930, gate/up 966 -> 994 TFLOP/s); blockwise takes form 2 (form 3 even, form 4 slower); fp16 weights
+  // form 0 (forms 3 and 4 ~25% slower).  AFX_GEMM_WL=0|2|3|4|6 overrides.  Forms 2-6 address X and W with
+  // 31-bit buffer offsets, so larger operands take form 0.
   static int cus = 0;
   if (cus == 0) {
     int dev = 0;
@@ -390,13 +472,20 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   }
   const char* we = getenv("AFX_GEMM_WL");           // read per call, like AFX_GEMM_GN
   const int wl_env = we ? atoi(we) : -1;
-  const int wl = wl_env >= 0 ? wl_env : (fmt == FMT_I8 ? (a.tiles <= 2 * cus ? 4 : 3) : fmt == FMT_BW ? 2 : 0);
+  const int wl = wl_env >= 0 ? wl_env : (fmt == FMT_I8 ? (a.tiles <= cus ? 6 : a.tiles <= 2 * cus ? 4 : 3) : fmt == FMT_BW ? 2 : 0);
   const long long xb = ((long long)(M - 1) * ldx + K) * 2;
   const long long wb = (long long)N * K * (fmt == FMT_F16 ? 2 : 1);
-  const bool form2 = wl >= 2 && wl <= 4 && xb < (1ll << 31) && wb < (1ll << 31);
+  const bool form2 = (wl == 2 || wl == 3 || wl == 4 || wl == 6) && xb < (1ll << 31) && wb < (1ll << 31);
   gemm_fn fn;
   int nth = 256;
-  if (form2 && wl == 4) {
+  if (form2 && wl == 6) {
+    a.x_bytes = (int)xb;
+    a.w_bytes = (int)wb;
+    nth = 512;
+    if (fmt == FMT_I8) fn = glu ? gemm_kernel<FMT_I8, EG_SWIGLU, 6> : gemm_kernel<FMT_I8, EG_PLAIN, 6>;
+    else if (fmt == FMT_BW) fn = glu ? gemm_kernel<FMT_BW, EG_SWIGLU, 6> : gemm_kernel<FMT_BW, EG_PLAIN, 6>;
+    else fn = glu ? gemm_kernel<FMT_F16, EG_SWIGLU, 6> : gemm_kernel<FMT_F16, EG_PLAIN, 6>;
+  } else if (form2 && wl == 4) {
     a.x_bytes = (int)xb;
     a.w_bytes = (int)wb;
     nth = 512;

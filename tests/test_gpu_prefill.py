@@ -189,8 +189,8 @@ def test_gemm_tile_orders_bit_identical(fmt, M, N, K):
     """The grouped tile order (default), other group sizes and the contiguous order (AFX_GEMM_GN=0),
     and every kernel form (AFX_GEMM_WL: 0 the 2 x 2 layout, 2 the 1 x 4 layout, 3 the 1 x 4 layout
     with the second half-step's fragments read during the first's products, 4 form 3's loop over
-    eight wavefronts in 2 x 4) compute every output tile the same way: bit-identical, and to the
-    oracle's bar."""
+    eight wavefronts in 2 x 4, 6 form 4 with the barrier in the middle of the K step)
+    compute every output tile the same way: bit-identical, and to the oracle's bar."""
     import torch
     from aneforge_amd import _kernels as Kn
     rng = np.random.default_rng(M + N + K)
@@ -200,7 +200,8 @@ def test_gemm_tile_orders_bit_identical(fmt, M, N, K):
     outs = []
     old, old_wl = _env("AFX_GEMM_GN", None), _env("AFX_GEMM_WL", None)
     try:
-        for gn, wl in ((None, None), (0, None), (3, None), (16, None), (None, 0), (None, 2), (None, 3), (None, 4)):
+        for gn, wl in ((None, None), (0, None), (3, None), (16, None), (None, 0), (None, 2), (None, 3), (None, 4),
+                       (None, 6)):
             _env("AFX_GEMM_GN", gn)
             _env("AFX_GEMM_WL", wl)
             say(f"gemm tile order GN={gn} WL={wl} {fmt} M={M} N={N} K={K}")

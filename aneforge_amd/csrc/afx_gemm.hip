@@ -6,10 +6,10 @@
 //   (compress="blockwise": W^ = fp16(q * s[n][k / 32]), the reference's reconstruction) or fp16 [N][K].
 //
 // Prefill multiplies the same weights by hundreds or thousands of token rows, so unlike the
-// decode GEMV this is a dense contraction that v_mfma_f32_16x16x32_f16 bounds.  A 256-thread
-// workgroup computes a 128 x 128 tile of Y; its four wavefronts own 64 x 64 quarters (fp16
-// weights) or 128 x 32 column strips (int8 codes), 16 MFMA tiles of 16 x 16 each (16 fp32
-// accumulators per lane; the kernel forms below).  K advances 64 at a time through two LDS
+// decode GEMV this is a dense contraction that v_mfma_f32_16x16x32_f16 bounds.  A workgroup
+// computes a 128 x 128 tile of Y: four wavefronts owning 64 x 64 quarters (fp16 weights) or
+// 128 x 32 column strips (int8 codes), 16 MFMA tiles of 16 x 16 each, or, for grids of at most two
+// tiles per CU, eight wavefronts owning 64 x 32 (the kernel forms below).  K advances 64 at a time through two LDS
 // stages: the next stage's global loads are issued before the current stage's MFMAs and land in
 // the other stage afterwards, one barrier per step.  LDS rows are unpadded and XOR-swizzled (below)
 // so the 16-byte / 8-byte fragment reads of 16 rows hit distinct banks.

@@ -618,8 +618,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // blocks), and one 4-wavefront workgroup per tile leaves a CU with a heavy tile running alone long
 // after its light neighbour is done.  Here an 8-wavefront workgroup takes one 128-query tile: waves
 // 0-3 run form 3 over the first half of its key blocks, waves 4-7 over the second half, each half
-// with its own double-buffered K / V^T stages (140 KB of LDS: one workgroup per CU, two wavefronts
-// per SIMD as in form 3), and the second half's running maxima, sums and accumulators are merged
+// with its own double-buffered K and V stages (132 KB of LDS with row-major V, 140 KB with V^T: one
+// workgroup per CU, two wavefronts per SIMD as in form 3), and the second half's running maxima, sums
+// and accumulators are merged
 // into the first's through LDS.  No tile costs more than half the longest key range, and with the
 // tiles dispatched heaviest first over two rounds of workgroups the CUs finish together.
 constexpr int kKB4 = kPK * kKStride;     // bytes of one K stage

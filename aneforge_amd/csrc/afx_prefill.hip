@@ -438,10 +438,12 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 // EMPTY: a query may have seen no key yet (a block range that starts past its position); its
 // running maximum is then -inf and the exponents take 0 in its place, so its probabilities are 0.
 // VTR: V staged row-major (kv_stage_rm) and read through ds_read_b64_tr_b16, else V^T (kv_stage3).
-template <bool EMPTY = false, bool VTR = false>
-__device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsigned char* Ks, const unsigned char* Vt,
-                                            const h8 (&qf)[2][4], const int (&qp)[2], int key0, int mwpos, int fr,
-                                            int fg, f4 (&acc)[2][8], float (&mrow)[2], float (&lrow)[2]) {
+// The block in two phases: attn_s3 (S^T, mask, online softmax, the accumulators rescaled, P^T packed
+// into pf) and attn_pv3 (O^T += V^T P^T); attn_block3 runs both.
+template <bool EMPTY = false>
+__device__ __forceinline__ void attn_s3(const PrefillAttnArgs& a, const unsigned char* Ks, const h8 (&qf)[2][4],
+                                        const int (&qp)[2], int key0, int mwpos, int fr, int fg, f4 (&acc)[2][8],
+                                        float (&mrow)[2], float (&lrow)[2], h8 (&pf)[2][2]) {
   f4 st[2][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -499,7 +501,6 @@ __device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsi
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[u][d][i] *= alpha[u];
   }
-  h8 pf[2][2];
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -508,6 +509,10 @@ __device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsi
       pf[u][ks] = (h8){(half_t)lo[0], (half_t)lo[1], (half_t)lo[2], (half_t)lo[3],
                        (half_t)hi[0], (half_t)hi[1], (half_t)hi[2], (half_t)hi[3]};
     }
+}
+template <bool VTR = false>
+__device__ __forceinline__ void attn_pv3(const unsigned char* Vt, const h8 (&pf)[2][2], int fr, int fg,
+                                         f4 (&acc)[2][8]) {
 #pragma unroll
   for (int d = 0; d < 8; ++d)
 #pragma unroll
@@ -528,6 +533,14 @@ __device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsi
 #pragma unroll
       for (int u = 0; u < 2; ++u) acc[u][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[u][ks], acc[u][d], 0, 0, 0);
     }
+}
+template <bool EMPTY = false, bool VTR = false>
+__device__ __forceinline__ void attn_block3(const PrefillAttnArgs& a, const unsigned char* Ks, const unsigned char* Vt,
+                                            const h8 (&qf)[2][4], const int (&qp)[2], int key0, int mwpos, int fr,
+                                            int fg, f4 (&acc)[2][8], float (&mrow)[2], float (&lrow)[2]) {
+  h8 pf[2][2];
+  attn_s3<EMPTY>(a, Ks, qf, qp, key0, mwpos, fr, fg, acc, mrow, lrow, pf);
+  attn_pv3<VTR>(Vt, pf, fr, fg, acc);
 }
 
 template <bool VTR>
@@ -739,6 +752,139 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ---- form 4 with the second half one phase behind ----
+// In form 4 both halves pass the block barrier together and run the same code, so the two wavefronts
+// of a SIMD (one per half) issue their S^T products, then their softmax, then their P.V products at the
+// same time.  Here the second half runs block i - 1's P.V before block i's S^T and softmax, so across a
+// SIMD one wavefront's softmax (VALU) meets the other's products (MFMA).  The second half then reads
+// block i - 1's V during block i, while block i + 1 is staged: its V takes three stages (the K stages
+// stay two).  LDS: 148 KB with row-major V.  The arithmetic of every block is form 4's.
+template <bool VTR>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel5(PrefillAttnArgs a) {
+  constexpr int kVB5 = VTR ? kPK * kVRow : kPD * kVStride;   // bytes of one V stage
+  // K stages [half][2], then V stages: the first half's two, the second half's three
+  __shared__ __align__(16) unsigned char lds[4 * kKB4 + 5 * kVB5];
+  static_assert(4 * 64 * kX4 * 4 <= 4 * kKB4, "the handover fits in the K stages");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hf = wave >> 2, w4 = wave & 3, htid = tid & 255;
+  const int fr = lane & 15, fg = lane >> 4;
+  unsigned char* const Kh = lds + hf * 2 * kKB4;
+  unsigned char* const Vh = lds + 4 * kKB4 + hf * 2 * kVB5;
+  const int id = blockIdx.x, G = a.Hq / a.Hkv;
+  int k, h;                                      // k-th tile slot, heaviest first; kv head k on XCD k % 8
+  if (a.xcd_map) {
+    const int x = id & 7, l = id >> 3, per_t = (a.Hkv >> 3) * G;
+    k = l / per_t;
+    const int r = l - k * per_t;
+    h = (x + 8 * (r / G)) * G + r % G;
+  } else {
+    k = id / a.Hq;
+    h = id % a.Hq;
+  }
+  const int t = a.tiles - 1 - k;
+  const int m0 = t * kPQ3, kvh = h / G;
+  const int mlast = m0 + kPQ3 - 1 < a.M - 1 ? m0 + kPQ3 - 1 : a.M - 1;
+  const int nkb = (a.pos0 + mlast) / kPK + 1;
+  const int nb0 = nkb >> 1;
+  const int kb0 = hf ? nb0 : 0, kb1 = hf ? nkb : nb0;
+  const int trips = nkb - nb0;
+  const int mw = m0 + 32 * w4;
+  const int wlast = mw < a.M ? a.pos0 + (mw + 31 < a.M - 1 ? mw + 31 : a.M - 1) : -1;
+  const half_t* kbase = a.k + (size_t)kvh * a.kv_hs;
+  const half_t* vbase = a.v + (size_t)kvh * a.kv_hs;
+  KvRegs r;
+  auto load = [&](int key0) {
+    if constexpr (VTR) kv_load_rm(a, kbase, vbase, key0, htid, r);
+    else kv_load(a, kbase, vbase, key0, htid, lane, w4, r);
+  };
+  auto stage = [&](unsigned char* K, unsigned char* V) {
+    if constexpr (VTR) kv_stage_rm(r, K, V, htid);
+    else kv_stage3(r, K, V, htid, lane, w4);
+  };
+  // the half's V stage of its i-th block: two alternating for the first half, three for the second
+  auto vstage = [&](int i) { return Vh + (hf ? i % 3 : i & 1) * kVB5; };
+  if (kb0 < kb1) load(kb0 * kPK);
+  h8 qf[2][4];
+  int qp[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int mq = mw + 16 * u + fr;
+    const half_t* qrow = a.q + (size_t)(mq < a.M ? mq : a.M - 1) * a.ldq + (size_t)h * kPD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[u][ks] = __builtin_bit_cast(h8, *(const u4*)(qrow + ks * 32 + 8 * fg));
+    qp[u] = a.pos0 + mq;
+  }
+  f4 acc[2][8];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[u][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+  float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.0f, 0.0f};
+  h8 pf[2][2];                                   // the second half: the previous block's P^T
+  if (kb0 < kb1) stage(Kh, vstage(0));
+  __syncthreads();
+  for (int i = 0; i < trips; ++i) {
+    const int kb = kb0 + i;
+    const bool mine = kb < kb1, more = kb + 1 < kb1;   // uniform over the half
+    if (more) load((kb + 1) * kPK);
+    if (hf == 0) {
+      if (mine && kb * kPK <= wlast) {
+        h8 p0[2][2];
+        attn_s3<false>(a, Kh + (i & 1) * kKB4, qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow, p0);
+        attn_pv3<VTR>(vstage(i), p0, fr, fg, acc);
+      }
+    } else {
+      // block i - 1's P.V (its V stays in its stage until block i + 2 is staged), then block i's S^T
+      if (i > 0 && (kb - 1) * kPK <= wlast) attn_pv3<VTR>(vstage(i - 1), pf, fr, fg, acc);
+      if (kb * kPK <= wlast)
+        attn_s3<true>(a, Kh + (i & 1) * kKB4, qf, qp, kb * kPK, a.pos0 + mw, fr, fg, acc, mrow, lrow, pf);
+    }
+    if (more) stage(Kh + ((i + 1) & 1) * kKB4, vstage(i + 1));
+    __syncthreads();
+  }
+  // the second half's last P.V: its V was staged before the last barrier and is not written again
+  if (hf && trips > 0 && (kb1 - 1) * kPK <= wlast) attn_pv3<VTR>(vstage(trips - 1), pf, fr, fg, acc);
+  float* const xw = (float*)lds + w4 * kX4 * 64 + lane;
+  if (hf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xw[((u * 8 + d) * 4 + i) * 64] = acc[u][d][i];
+      xw[(64 + u) * 64] = mrow[u];
+      xw[(66 + u) * 64] = lrow[u];
+    }
+  }
+  __syncthreads();
+  if (hf) return;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const float mb = xw[(64 + u) * 64], lb = xw[(66 + u) * 64];
+    const float mn = fmaxf(mrow[u], mb);         // finite for every stored query: the half holding block 0 saw key 0
+    const float sa = __builtin_amdgcn_exp2f(mrow[u] - mn);
+    const float sb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - mn);
+    lrow[u] = lrow[u] * sa + lb * sb;
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[u][d][i] = acc[u][d][i] * sa + xw[((u * 8 + d) * 4 + i) * 64] * sb;
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int m = mw + 16 * u + fr;
+    if (m >= a.M) continue;
+    const float inv = 1.0f / lrow[u];
+    half_t* orow = a.o + (size_t)m * a.ldo + (size_t)h * kPD + 4 * fg;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const h2 lo = {(half_t)(acc[u][d][0] * inv), (half_t)(acc[u][d][1] * inv)};
+      const h2 hi = {(half_t)(acc[u][d][2] * inv), (half_t)(acc[u][d][3] * inv)};
+      *(u2*)(orow + d * 16) = (u2){as_u32(lo), as_u32(hi)};
+    }
+  }
+}
+
 }  // namespace afx
 
 using namespace afx;
@@ -789,11 +935,12 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
   a.scale_log2 = scale * 1.4426950408889634f;
   a.tiles = (M + kPQ - 1) / kPQ;
   a.xcd_map = Hkv % 8 == 0;
-  // Default: form 4 while the causal part dominates (pos0 < M: tile work grows with the tile index, and
-  // splitting each tile's keys evens the CUs out), form 3 once the cached prefix does (a later chunk,
-  // whose tiles differ little and which form 4's single barrier domain per CU slows by ~6%).
+  // Default: form 5 (form 4's arithmetic, bit for bit) while the causal part dominates (pos0 < M: tile
+  // work grows with the tile index, and splitting each tile's keys evens the CUs out), form 3 once the
+  // cached prefix does (a later chunk, whose tiles differ little and which the split forms' single
+  // barrier domain per CU slows by 3-6%).
   const char* fe = getenv("AFX_PREFILL_ATTN_FORM");   // read per call: tests compare the forms in one process
-  const int form_env = fe ? atoi(fe) : (pos0 < M ? 4 : 3);
+  const int form_env = fe ? atoi(fe) : (pos0 < M ? 5 : 3);
   if (form_env == 1) {                             // single-buffered
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(a.tiles, Hq), dim3(256), 0, (hipStream_t)stream, a);
   } else if (form_env == 2 || ldo % 4 != 0 || ((uintptr_t)o & 7) != 0) {   // pipelined, bit-identical to form 1
@@ -804,6 +951,9 @@ int afx_prefill_attn(const void* q, int ldq, const void* kcache, const void* vca
     const bool vtr = ve ? atoi(ve) != 0 : true;
     if (form_env == 4) {                           // form 3 with each tile's keys split over two halves
       auto kfn = vtr ? prefill_attn_kernel4<true> : prefill_attn_kernel4<false>;
+      hipLaunchKernelGGL(kfn, dim3(a.tiles * Hq), dim3(512), 0, (hipStream_t)stream, a);
+    } else if (form_env == 5) {                    // form 4 with the second half one phase behind
+      auto kfn = vtr ? prefill_attn_kernel5<true> : prefill_attn_kernel5<false>;
       hipLaunchKernelGGL(kfn, dim3(a.tiles * Hq), dim3(512), 0, (hipStream_t)stream, a);
     } else {                                       // transposed scores, 128 queries per workgroup (8-byte stores)
       const char* oe = getenv("AFX_PREFILL_ATTN_ORDER");

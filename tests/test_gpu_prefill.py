@@ -144,7 +144,8 @@ def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     arithmetic: bit-identical to 1), transposed scores (3) with both tile orders and both V stagings, and 3
     with each tile's keys split over two halves of the workgroup (4: a single-block tile whose first
     half is empty, and queries that see no key of the second half), on grids with several workgroup
-    rounds, the XCD mapping (Hkv = 8) and without it (Hkv = 2)."""
+    rounds, the XCD mapping (Hkv = 8) and without it (Hkv = 2); 5 is form 4 with the second half one
+    phase behind (bit-identical to 4)."""
     import torch
     from aneforge_amd import _kernels as Kn
     D = 128
@@ -163,7 +164,7 @@ def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     old_v = _env("AFX_PREFILL_ATTN_VTR", None)
     try:
         for form, order, vtr in ((1, None, None), (2, None, None), (3, 0, None), (3, 1, None), (3, 1, 0),
-                                 (4, None, None), (4, None, 0)):
+                                 (4, None, None), (4, None, 0), (5, None, None), (5, None, 0)):
             _env("AFX_PREFILL_ATTN_FORM", form)
             _env("AFX_PREFILL_ATTN_ORDER", order)
             _env("AFX_PREFILL_ATTN_VTR", vtr)
@@ -181,6 +182,9 @@ def test_prefill_attention_forms(M, pos0, Hq, Hkv, Mmax):
     # the V operand's staging layout (row-major + transposing reads, or V^T) changes no arithmetic
     np.testing.assert_array_equal(outs[(3, 1, None)], outs[(3, 1, 0)])
     np.testing.assert_array_equal(outs[(4, None, None)], outs[(4, None, 0)])
+    # form 5 reorders form 4's phases across the two halves, not its arithmetic
+    np.testing.assert_array_equal(outs[(5, None, None)], outs[(4, None, None)])
+    np.testing.assert_array_equal(outs[(5, None, 0)], outs[(4, None, None)])
 
 
 @pytest.mark.parametrize("fmt", ["int8", "fp16", "blockwise"])

@@ -85,7 +85,8 @@ __device__ __forceinline__ h8 i8x8_to_h8(u2 v) {
 // form 3; it is not instantiated.)
 template <int WL> struct WaveLayout {
   static constexpr bool W8 = WL == 4 || WL == 6;     // eight wavefronts in 2 x 4
-  static constexpr int MT = W8 ? 4 : (WL ? 8 : 4), NT = W8 ? 2 : (WL ? 2 : 4);
+  static constexpr bool Q4 = WL == 0;                // four wavefronts in 2 x 2
+  static constexpr int MT = W8 ? 4 : (Q4 ? 4 : 8), NT = W8 ? 2 : (Q4 ? 4 : 2);
   static constexpr int NTH = W8 ? 512 : 256;        // threads per workgroup
   static constexpr int WPE = W8 ? 4 : 3;            // wavefronts per SIMD the register budget is sized for
 };
@@ -160,8 +161,8 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
     m0 = (logical % a.tiles_m) * kGBM;
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  constexpr bool W8 = WaveLayout<WL>::W8;
-  const int wm = W8 ? wave >> 2 : (WL ? 0 : wave >> 1), wn = W8 ? wave & 3 : (WL ? wave : wave & 1);
+  constexpr bool W8 = WaveLayout<WL>::W8, Q4 = WaveLayout<WL>::Q4;
+  const int wm = W8 ? wave >> 2 : (Q4 ? wave >> 1 : 0), wn = W8 ? wave & 3 : (Q4 ? wave & 1 : wave);
   const int M = a.M, N = a.N, K = a.K;
   const int nk = K / kGBK;
 
@@ -462,8 +463,10 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   // 4), form 4 when they fit two (the N = 4096 shapes at M = 2048: o-proj 95.5 -> 85.9 us, down 208.6 ->
   // 201.2 us against form 3) and form 3 otherwise (gate/up, QKV at M = 2048; form 2 -> 3 there: QKV 874 ->
   // 930, gate/up 966 -> 994 TFLOP/s); blockwise takes form 2 (form 3 even, form 4 slower); fp16 weights
-  // form 0 (forms 3 and 4 ~25% slower).  AFX_GEMM_WL=0|2|3|4|6 overrides.  Forms 2-6 address X and W with
-  // 31-bit buffer offsets, so larger operands take form 0.
+  // take form 6 (eight wavefronts without the AGPR spill-over of the four-wavefront fp16 forms, which
+  // leaves them at one or two wavefronts per SIMD: at M = 2048 against form 0, QKV 137.7 -> 125.3,
+  // gate/up 470.0 -> 422.6, down 234.8 -> 214.1 us).  AFX_GEMM_WL=0|2|3|4|6 overrides.  Forms 2-6 address
+  // X and W with 31-bit buffer offsets, so larger operands take form 0.
   static int cus = 0;
   if (cus == 0) {
     int dev = 0;
@@ -472,7 +475,7 @@ int afx_gemm(int fmt, const void* w, const void* scale, const void* x, int ldx, 
   }
   const char* we = getenv("AFX_GEMM_WL");           // read per call, like AFX_GEMM_GN
   const int wl_env = we ? atoi(we) : -1;
-  const int wl = wl_env >= 0 ? wl_env : (fmt == FMT_I8 ? (a.tiles <= cus ? 6 : a.tiles <= 2 * cus ? 4 : 3) : fmt == FMT_BW ? 2 : 0);
+  const int wl = wl_env >= 0 ? wl_env : (fmt == FMT_I8 ? (a.tiles <= cus ? 6 : a.tiles <= 2 * cus ? 4 : 3) : fmt == FMT_BW ? 2 : 6);
   const long long xb = ((long long)(M - 1) * ldx + K) * 2;
   const long long wb = (long long)N * K * (fmt == FMT_F16 ? 2 : 1);
   const bool form2 = (wl == 2 || wl == 3 || wl == 4 || wl == 6) && xb < (1ll << 31) && wb < (1ll << 31);

@@ -256,10 +256,7 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
     if (kt + 1 < nk) load(kt + 1);                 // next stage streams during this stage's MFMAs
     if constexpr (WL >= 3) {
       // the second half-step's fragments are read between the first half-step's MFMAs, each A fragment
-      // as soon as its two products have been issued, so only the first half-step waits on LDS.  The
-      // raised priority over the MFMA clusters (form 2's, below) helps only the eight-wavefront form 4:
-      // without it form 3 ran 1-3% faster on the four int8 7B shapes, form 4 1-2% slower, and form 6
-      // (fp16) 1-2% faster on three of them
+      // as soon as its two products have been issued, so only the first half-step waits on LDS
       typedef typename std::conditional<kCodes, u2, u4>::type Raw;
       auto read_a = [&](int kk, int i) {
         return __builtin_bit_cast(h8, *(const u4*)(As[s] + swz16(wm * MT * 16 + i * 16 + fr, kk * 4 + fg)));
@@ -295,14 +292,14 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
         if (kk == 0)
 #pragma unroll
           for (int j = 0; j < NT; ++j) bq[j] = read_b(1, j);
-        if constexpr (FMT != FMT_BW && WL == 4) __builtin_amdgcn_s_setprio(1);
+        if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
           for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
           if (kk == 0) af[i] = read_a(1, i);
         }
-        if constexpr (FMT != FMT_BW && WL == 4) __builtin_amdgcn_s_setprio(0);
+        if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
       }
     } else {
 #pragma unroll
@@ -377,12 +374,14 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
       for (int j = 0; j < NT; ++j) bf[j] = conv_b(s, 0, j, bq[j]);
 #pragma unroll
       for (int j = 0; j < NT; ++j) bq[j] = read_b(s, 1, j);
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         af[i] = read_a(s, 1, i);
       }
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
       // the next step's tiles into the other stage (last read before the previous barrier), the step
       // after next loading into the freed registers, one barrier
       if (more) stage(s ^ 1);
@@ -394,12 +393,14 @@ __attribute__((amdgpu_waves_per_eu(WaveLayout<WL>::WPE, WaveLayout<WL>::WPE))) v
       if (more)
 #pragma unroll
         for (int j = 0; j < NT; ++j) bq[j] = read_b(s ^ 1, 0, j);
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         if (more) af[i] = read_a(s ^ 1, 0, i);
       }
+      if constexpr (FMT != FMT_BW) __builtin_amdgcn_s_setprio(0);
     };
     for (int kt = 0; kt < nk; kt += 2) {           // unrolled by two: the stage offsets are constants
       mstep(kt, Stage<0>{});

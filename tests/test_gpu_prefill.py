@@ -216,3 +216,42 @@ def test_gemm_tile_orders_bit_identical(fmt, M, N, K):
     check_f16(outs[0], want, what=f"gemm {fmt} grouped order")
     for o in outs[1:]:
         np.testing.assert_array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp16"])
+@pytest.mark.parametrize("M,N,K", [(2048, 6144, 64), (600, 4096, 128)])
+@pytest.mark.parametrize("epi", ["resid", "swiglu", "f32"])
+def test_gemm_epilogues_every_form(fmt, M, N, K, epi):
+    """Each epilogue under every kernel form, at a grid whose default is form 3 (768 int8 tiles: three
+    workgroups per CU) and one whose default is form 6 (160 tiles): bit-identical across the forms, and
+    the default to the oracle's bar."""
+    import torch
+    from aneforge_amd import _kernels as Kn
+    rng = np.random.default_rng(M + N + K + len(epi))
+    w, s, Wf = _weights(fmt, N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    lin = np.asarray(x, np.float64) @ np.asarray(Wf, np.float64).T
+    r = rng.standard_normal((M, N)).astype(np.float16) if epi == "resid" else None
+    outs = []
+    old = _env("AFX_GEMM_WL", None)
+    try:
+        for wl in (None, 0, 2, 3, 4, 6):
+            _env("AFX_GEMM_WL", wl)
+            say(f"gemm epilogue {epi} WL={wl} {fmt} M={M} N={N} K={K}")
+            if epi == "resid":
+                y = dev(r)
+                Kn.gemm(fmt, w, s, dev(x), y=y, residual=y, epi="resid")
+                outs.append(host(y))
+            else:
+                outs.append(host(Kn.gemm(fmt, w, s, dev(x), epi=epi)))
+    finally:
+        _env("AFX_GEMM_WL", old)
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+    if epi == "resid":
+        check_hidden(outs[0], ref.r16(r.astype(np.float64) + ref.r16(lin)), what=f"gemm {fmt} resid")
+    elif epi == "swiglu":
+        g, u = ref.r16(lin[:, 0::2]), ref.r16(lin[:, 1::2])
+        check_f16(outs[0], ref.r16(ref.silu(g) * u), what=f"gemm {fmt} swiglu")
+    else:
+        check_f16(outs[0], lin, what=f"gemm {fmt} f32")

@@ -219,12 +219,13 @@ def test_gemm_tile_orders_bit_identical(fmt, M, N, K):
 
 
 @pytest.mark.parametrize("fmt", ["int8", "fp16"])
-@pytest.mark.parametrize("M,N,K", [(2048, 6144, 64), (600, 4096, 128)])
+@pytest.mark.parametrize("M,N,K", [(2048, 6144, 64), (600, 4096, 128), (333, 400, 192)])
 @pytest.mark.parametrize("epi", ["resid", "swiglu", "f32"])
 def test_gemm_epilogues_every_form(fmt, M, N, K, epi):
     """Each epilogue under every kernel form, at a grid whose default is form 3 (768 int8 tiles: three
-    workgroups per CU) and one whose default is form 6 (160 tiles): bit-identical across the forms, and
-    the default to the oracle's bar."""
+    workgroups per CU), one whose default is form 6 (160 tiles), and ragged rows and columns (333 x 400:
+    partial tiles in both directions): bit-identical across the forms, and the default to the oracle's
+    bar."""
     import torch
     from aneforge_amd import _kernels as Kn
     rng = np.random.default_rng(M + N + K + len(epi))

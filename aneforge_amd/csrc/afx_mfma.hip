@@ -216,25 +216,11 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
     // rounds of NB batches (NB = this shape's batches per wavefront when that is at most 4):
     // all of a round's weight loads are issued at once
     for (int b0 = 0; b0 < nb; b0 += NB) {
-      u4 wq[NB][4];
-      u2 sq[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        // batch b0 + b, clamped per lane to the row (a clamped chunk is loaded but never used)
-        const int sb = s0 + (b0 + b) * kSPB;
-        int c = sb * 4 + lc;
-        c = c < nsteps * 4 ? c : nsteps * 4 - 1;
-#pragma unroll
-        for (int h = 0; h < 4; ++h) wq[b][h] = __builtin_nontemporal_load((const u4*)(lrow[h] + (size_t)(c - lc) * 16));
-        if constexpr (has_block_scales<FMT>()) {
-          int q = sb + (lane & 3);
-          q = q < nsteps ? q : nsteps - 1;
-          if constexpr (FMT == FMT_Q4) sq[b] = *(const u2*)(srow + (size_t)(q - (lane & 3)) * 4);
-          else sq[b] = (u2){*(const uint32_t*)(srow + (size_t)(q - (lane & 3)) * 2), 0u};
-        }
-      }
       // activations: one batch (4 steps) per load group; int8/fp16 keep two groups in flight
-      // (the next batch's loads go out before this batch's math), Q4_0 one (its group is 4x larger)
+      // (the next batch's loads go out before this batch's math), Q4_0 one (its group is 4x larger).
+      // The round's first group is issued before its weight loads: the memory counter retires in
+      // order, so the first batch's math then waits only for the first batch's weights, and runs
+      // while the later batches' weights are still arriving.
       constexpr int XG = NM <= 2 ? 2 : 1;
       auto load_x = [&](u4 (&xv)[kSPB][NM], int b) {
 #pragma unroll
@@ -253,13 +239,30 @@ __global__ __launch_bounds__(NW * 64) void mfma_kernel(MfmaArgs a) {
         }
       };
       u4 xv[XG][kSPB][NM];
-      if constexpr (XG == 2) load_x(xv[0], 0);
+      load_x(xv[0], 0);
+      u4 wq[NB][4];
+      u2 sq[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        // batch b0 + b, clamped per lane to the row (a clamped chunk is loaded but never used)
+        const int sb = s0 + (b0 + b) * kSPB;
+        int c = sb * 4 + lc;
+        c = c < nsteps * 4 ? c : nsteps * 4 - 1;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) wq[b][h] = __builtin_nontemporal_load((const u4*)(lrow[h] + (size_t)(c - lc) * 16));
+        if constexpr (has_block_scales<FMT>()) {
+          int q = sb + (lane & 3);
+          q = q < nsteps ? q : nsteps - 1;
+          if constexpr (FMT == FMT_Q4) sq[b] = *(const u2*)(srow + (size_t)(q - (lane & 3)) * 4);
+          else sq[b] = (u2){*(const uint32_t*)(srow + (size_t)(q - (lane & 3)) * 2), 0u};
+        }
+      }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         if (b0 + b >= nb) break;                   // wavefront-uniform
         if constexpr (XG == 2) {
           if (b + 1 < NB) load_x(xv[(b + 1) & 1], b + 1);
-        } else {
+        } else if (b) {
           load_x(xv[0], b);
         }
         u4 (&xb)[kSPB][NM] = xv[XG == 2 ? (b & 1) : 0];

@@ -23,6 +23,23 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 
+// RMSNorm output of an fp16 pair: fp16((x * rstd) * g), each product rounded to fp32 as written.
+// Each product is one v_fma_mix_f32 reading its fp16 operand in place, with a -0 addend:
+// a*b + (-0) rounds exactly as a*b, signed zeros included, so the result is the plain
+// convert-and-multiply form's bit for bit at half its instructions.
+__device__ __forceinline__ uint32_t rms_pair(uint32_t x2, uint32_t g2, float rstd) {
+  const float mz = -0.0f;
+  float a0, a1, b0, b1;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(a0) : "v"(x2), "v"(rstd), "v"(mz));
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(a1) : "v"(x2), "v"(rstd), "v"(mz));
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(b0) : "v"(a0), "v"(g2), "v"(mz));
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(b1) : "v"(a1), "v"(g2), "v"(mz));
+  h2 o;
+  o.x = (half_t)b0;
+  o.y = (half_t)b1;
+  return as_u32(o);
+}
+
 // c + a.x*b.x + a.y*b.y in fp32 (v_dot2_f32_f16).
 __device__ __forceinline__ float dot2(h2 a, h2 b, float c) {
   return __builtin_amdgcn_fdot2(a, b, c, false);

@@ -501,13 +501,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
       uint32_t* xw = (uint32_t*)&xq[i];
       const uint32_t* gw = (const uint32_t*)&gq[i];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const h2 xx = as_h2(xw[jj]), gg = as_h2(gw[jj]);
-        h2 r;
-        r.x = (half_t)(((float)xx.x * rstd) * (float)gg.x);
-        r.y = (half_t)(((float)xx.y * rstd) * (float)gg.y);
-        xw[jj] = as_u32(r);
-      }
+      for (int jj = 0; jj < 4; ++jj) xw[jj] = rms_pair(xw[jj], gw[jj], rstd);
     }
     if constexpr (EG == EG_HEAD) {
       if (a.hn_out && blockIdx.x == 0) {

@@ -45,6 +45,17 @@ template <> struct Fmt<FMT_I8> {
     for (int i = 0; i < 8; ++i) acc = dot2(q[i], x[i], acc);
     return acc;
   }
+  // The same chunk with every code offset by +1152 (the conversion's magic value left in place):
+  // sum (q + 1152) x; the caller subtracts 1152 * sum(x) once per row.
+  __device__ static float dot_biased(const u4& w, const h2 (&x)[kXH2], float acc) {
+    const uint32_t wd[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc = dot2(as_h2(__builtin_amdgcn_perm(0x64646464u, wd[i], 0x04010400u)), x[2 * i], acc);
+      acc = dot2(as_h2(__builtin_amdgcn_perm(0x64646464u, wd[i], 0x04030402u)), x[2 * i + 1], acc);
+    }
+    return acc;
+  }
 };
 
 template <> struct Fmt<FMT_Q4> {

@@ -429,6 +429,11 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
   static_assert(EG != EG_HEAD || NORM == 1, "the lm_head variant has the norm prologue");
   __shared__ __align__(16) half_t xs[NORM ? KMAX : 8];
   __shared__ float red[4];
+  __shared__ float xsum[4];
+  // int8 with the norm prologue: the codes enter the dot products as q + 1152 (no subtraction per
+  // pair) and each row's sum is corrected by 1152 * sum(x) once; sum(x) comes from the staging
+  // pass.  Only there: with one row per wavefront the sum costs about what the subtractions do.
+  constexpr bool kBiased = FMT == FMT_I8 && NORM == 1;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int N = a.N, K = a.K;
   const int nchunks = K / Fmt<FMT>::kWeightsPerChunk;
@@ -511,14 +516,29 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
       }
     }
   }
+  float sx = 0.0f;
   if constexpr (NORM) {
+    float xp = 0.0f;
 #pragma unroll
     for (int i = 0; i < NVT; ++i) {
       int f = t + 256 * i;
+      if constexpr (kBiased) {
+        const h2 one = {(half_t)1.0f, (half_t)1.0f};
+        float q = dot2(as_h2(xq[i].x), one, 0.0f);
+        q = dot2(as_h2(xq[i].y), one, q);
+        q = dot2(as_h2(xq[i].z), one, q);
+        q = dot2(as_h2(xq[i].w), one, q);
+        xp += f < nv ? q : 0.0f;
+      }
       f = f < nv ? f : nv - 1;                       // a clamped duplicate rewrites its own value
       *(u4*)(xs + 8 * f) = xq[i];
     }
+    if constexpr (kBiased) {
+      xp = wave_sum_uniform(xp);
+      if (lane == 0) xsum[wave] = xp;
+    }
     __syncthreads();
+    if constexpr (kBiased) sx = (xsum[0] + xsum[1]) + (xsum[2] + xsum[3]);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int c = 64 * u + lane;
@@ -549,20 +569,31 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(GemvArgs a) {
           dv.x = ok ? dv.x : 0u;                     // d = dmin = 0: weight 0 for any code
         } else if constexpr (FMT == FMT_Q6K) {
           dv.z = ok ? dv.z : 0u;                     // d = 0: weight 0 for any code
-        } else if constexpr (FMT != FMT_L4) {
+        } else if constexpr (FMT != FMT_L4 && !kBiased) {
           wv.x = ok ? wv.x : 0u; wv.y = ok ? wv.y : 0u; wv.z = ok ? wv.z : 0u; wv.w = ok ? wv.w : 0u;
         }
       }
-      const float t = Fmt<FMT>::dot(wv, xv[u], dv, fctx[r], acc[r]);
-      // LUT4: index 0 still looks up an entry, so a chunk past K drops its whole sum
-      acc[r] = FMT == FMT_L4 && u == U - 1 && !ok ? acc[r] : t;
+      if constexpr (kBiased) {
+        // a chunk past K: its biased codes are not zero, so its x is (clamped duplicates)
+        h2 xz[Fmt<FMT>::kXH2];
+#pragma unroll
+        for (int j = 0; j < Fmt<FMT>::kXH2; ++j) xz[j] = u == U - 1 && !ok ? (h2){(half_t)0.0f, (half_t)0.0f} : xv[u][j];
+        acc[r] = Fmt<FMT_I8>::dot_biased(wv, xz, acc[r]);
+      } else {
+        const float t = Fmt<FMT>::dot(wv, xv[u], dv, fctx[r], acc[r]);
+        // LUT4: index 0 still looks up an entry, so a chunk past K drops its whole sum
+        acc[r] = FMT == FMT_L4 && u == U - 1 && !ok ? acc[r] : t;
+      }
     }
   }
 
   float v[1][R];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-    v[0][r] = wave_sum_uniform(acc[r]) * (float)h_scale[r] + (a.bias ? (float)h_bias[r] : 0.0f);
+  for (int r = 0; r < R; ++r) {
+    float d = wave_sum_uniform(acc[r]);
+    if constexpr (kBiased) d -= 1152.0f * sx;
+    v[0][r] = d * (float)h_scale[r] + (a.bias ? (float)h_bias[r] : 0.0f);
+  }
   if constexpr (EG == EG_HEAD) {
     __shared__ float4 part[4];
     float t1 = -INFINITY, t2 = -INFINITY, ma = 0.0f;

@@ -354,6 +354,31 @@ def test_linear_rms_prologue(K, fmt):
     check_f16(got, want, what=f"rms+{fmt}")
 
 
+@pytest.mark.parametrize("Kd", [4096, 4000, 2048])
+def test_linear_int8_norm_row_kernel_positive_mean(K, Kd):
+    """One activation row through the int8 norm-prologue row kernel (plain and SwiGLU), whose dot
+    products run on the codes offset by +1152 and subtract 1152 * sum(x) per row: a row with a large
+    positive mean makes that correction as large as it gets, and K = 4000 / 2048 leave part or all of
+    the last units past K (their x must add nothing)."""
+    from aneforge_amd import _blob
+    say(f"int8 norm row kernel, positive-mean row, K={Kd}")
+    rng = np.random.default_rng(31)
+    N = 1536
+    h = rng.uniform(0.5, 1.5, (1, Kd)).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, Kd).astype(np.float16)
+    hn = ref.rms_norm(h, g, 1e-5)
+    q, s = _w8(N, Kd, 32)
+    got = host(K.linear_rms("int8", dev(q), dev(s), dev(h), dev(g), 1e-5))
+    check_f16(got, ref.linear(hn, ref.dequant_w8(q, s)), what=f"rms int8 K={Kd}")
+    qg, sg = _w8(N // 2, Kd, 33)
+    qu, su = _w8(N // 2, Kd, 34)
+    act = host(K.linear_swiglu("int8", dev(_blob.interleave_rows(qg, qu)), dev(_blob.interleave_rows(sg, su)), dev(h),
+                               gamma=dev(g), eps=1e-5))
+    gg = ref.linear(hn, ref.dequant_w8(qg, sg))
+    uu = ref.linear(hn, ref.dequant_w8(qu, su))
+    check_f16(act, ref.r16(ref.silu(gg) * uu), what=f"rms swiglu int8 K={Kd}")
+
+
 def test_linear_swiglu(K):
     say("linear swiglu (gate/up interleaved) with norm")
     from aneforge_amd import _blob
